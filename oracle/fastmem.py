@@ -1,0 +1,279 @@
+"""Float64 CPU restatement of the UnifiedLM fast-memory path (ORACLE, test infrastructure).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this
+module, as the checker. Nothing in the product imports it.
+
+Every function works on plain tensors (or a dict of parameters named like the
+reference's ``UnifiedLM.state_dict()``), so the oracle does not depend on the
+product's ``model.py``. The maths restated here, for one batch row and time t:
+
+    k_t    = r_{t-1},  k_0 = 0                         kernel.py:6, test_all.py:71
+    c_t    = w + sum_{s<=t} lam^(t-s) k_s              kernel.py:7
+    q_t    = r_t / c_t                                 kernel.py:8
+    fast_t = sum_{s<=t} lam^(t-s) (q_t . k_s) v_s      kernel.py:9
+    lam    = exp(g),  g = -exp(log_rate)               model.py:84
+
+and the block around it (model.py:70-85): RMSNorm, causal depthwise conv,
+relu^2 address normalised by eps + row sum, value projection, mu read-out.
+
+How each function is pinned (tests/test_oracle.py):
+  dense_fast_memory     closed form; brute-force double loop on tiny shapes;
+                        special cases lam -> 0, lam = 1, T = 1, zero rows.
+  chunked_fast_memory   equals dense for chunk 1, 7, 16, 64 (test_all.py:100-107).
+  address               row sums z/(eps+z) < 1, zero where pre <= 0,
+                        gradcheck of its backward formula.
+  fast_memory_grads     torch.autograd.gradcheck at tiny shapes and the
+                        reference's dg identity (kernel.py:173-175).
+  lm_forward            parallel == forward_recurrent (test_all.py:110-116),
+                        causality (test_all.py:119-128), finite grads.
+  forward_recurrent     logits of the reference's own run.c (compiled under
+                        oracle/_ref) and the committed run.c golden fixture.
+"""
+import math
+
+import torch
+import torch.nn.functional as F
+
+
+# ---------------------------------------------------------------------------
+# fast-memory operator (kernel.py:1-15, test_all.py:28-61)
+
+def shift_keys(r):
+    """Write addresses k_t = r_{t-1}, k_0 = 0 (test_all.py:71, kernel.py:126)."""
+    return F.pad(r, (0, 0, 1, 0))[:, :-1]
+
+
+def decay_mask(T, lam, dtype=torch.float64):
+    """M[t, s] = lam^(t-s) for s <= t, else 0 (test_all.py:58)."""
+    t = torch.arange(T, dtype=dtype)
+    lag = (t[:, None] - t[None, :])
+    return (lag >= 0).to(dtype) * lam ** lag.clamp(min=0)
+
+
+def dense_fast_memory(r, v, lam, w):
+    """Quadratic form (test_all.py:54-61): returns (q, fast).
+
+    r (B,T,A), v (B,T,D), lam 0-d tensor, w (A,)."""
+    T = r.shape[1]
+    k = shift_keys(r)
+    M = decay_mask(T, lam, r.dtype)
+    c = w + M @ k
+    q = r / c
+    fast = ((q @ k.transpose(1, 2)) * M) @ v.to(r.dtype)
+    return q, fast
+
+
+def chunked_fast_memory(r, v, lam, w, chunk=64):
+    """Chunkwise form (test_all.py:28-51): quadratic inside chunks of length
+    ``chunk``, the A x D state and the A-vector evidence carried between them."""
+    B, T, A = r.shape
+    D = v.shape[-1]
+    k = shift_keys(r)
+    v = v.to(r.dtype)
+    state = r.new_zeros(B, A, D)          # sum_s lam^(t0-1-s) k_s v_s^T
+    mass = r.new_zeros(B, 1, A)           # sum_s lam^(t0-1-s) k_s
+    qs, fs = [], []
+    for t0 in range(0, T, chunk):
+        L = min(chunk, T - t0)
+        i = torch.arange(L, dtype=r.dtype)
+        M = decay_mask(L, lam, r.dtype)
+        into = (lam ** (i + 1))[None, :, None]          # carried state -> row i
+        tail = (lam ** (L - 1 - i))[None, :, None]      # row i -> chunk end
+        kc, rc, vc = k[:, t0:t0 + L], r[:, t0:t0 + L], v[:, t0:t0 + L]
+        q = rc / (w + into * mass + M @ kc)
+        inter = (q * into) @ state
+        intra = ((q @ kc.transpose(1, 2)) * M) @ vc
+        fs.append(inter + intra)
+        qs.append(q)
+        state = lam ** L * state + (kc * tail).transpose(1, 2) @ vc
+        mass = lam ** L * mass + (kc * tail).sum(1, keepdim=True)
+    return torch.cat(qs, 1), torch.cat(fs, 1)
+
+
+def fast_memory(r, v, g, w, form="chunked", chunk=64):
+    """unified_memory(r, v, g, w) -> (q, fast) (kernel.py:236-238) in the
+    dtype of r; lam = exp(g). Differentiable in r, v, g, w."""
+    lam = torch.exp(g)
+    if form == "dense":
+        return dense_fast_memory(r, v, lam, w)
+    return chunked_fast_memory(r, v, lam, w, chunk)
+
+
+def fast_memory_grads(r, v, g, w, dq, dfast, form="chunked"):
+    """Float64 gradients (dr, dv, dg, dw) of <q, dq> + <fast, dfast> by autograd."""
+    r = r.detach().double().requires_grad_(True)
+    v = v.detach().double().requires_grad_(True)
+    g = g.detach().double().requires_grad_(True)
+    w = w.detach().double().requires_grad_(True)
+    q, fast = fast_memory(r, v, g, w, form)
+    loss = (fast * dfast.double()).sum()
+    if dq is not None:
+        loss = loss + (q * dq.double()).sum()
+    dr, dv, dg, dw = torch.autograd.grad(loss, (r, v, g, w))
+    return dr, dv, dg, dw
+
+
+def dg_identity(r, v, g, w, dq_out, dfast):
+    """The reference's closed form of d loss / d g (kernel.py:155-175):
+
+        dg = sum_t t [q.dq_f + dc.(c - w)]_t - sum_s s [k.(dk_f + dk_c)]_s
+
+    computed here from float64 autograd pieces; used to pin that identity."""
+    r, v, w, g = r.double(), v.double(), w.double(), g.double()
+    lam = torch.exp(g)
+    B, T, A = r.shape
+    k = shift_keys(r)
+    M = decay_mask(T, lam)
+    c = w + M @ k
+    q = r / c
+    do = dfast.double()
+    S = (do @ v.transpose(1, 2)) * M                 # (dfast_t . v_s) lam^(t-s)
+    P = (q @ k.transpose(1, 2)) * M                  # (q_t . k_s) lam^(t-s)
+    dq_f = S @ k
+    dk_f = S.transpose(1, 2) @ q
+    dq = dq_f + (dq_out.double() if dq_out is not None else 0.0)
+    dc = -dq * q / c
+    dk_c = M.transpose(0, 1) @ dc
+    pos = torch.arange(T, dtype=torch.float64)[None, :, None]
+    return ((pos * (q * dq_f + dc * (c - w))).sum() - (pos * k * (dk_f + dk_c)).sum()), P
+
+
+# ---------------------------------------------------------------------------
+# relu^2 slot address (model.py:70-72) and the block (model.py:31-42, 77-85)
+
+def address(pre, log_eps):
+    """r = z / (exp(clamp(log_eps, -10, 10)) + sum_a z), z = relu(pre)^2 where
+    ``pre`` already includes the key bias (model.py:70-72)."""
+    z = F.relu(pre).square()
+    return z / (log_eps.clamp(-10, 10).exp() + z.sum(-1, keepdim=True))
+
+
+def rmsnorm(x, weight, eps):
+    """x * rsqrt(mean(x^2) + eps) * weight (model.py:37-42)."""
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * weight
+
+
+def causal_conv(h, weight):
+    """Depthwise causal conv: weight (D, 1, K), taps oldest -> newest (model.py:61, 79)."""
+    Kc = weight.shape[-1]
+    T = h.shape[1]
+    return F.conv1d(h.transpose(1, 2), weight, padding=Kc - 1, groups=h.shape[-1])[..., :T].transpose(1, 2)
+
+
+def prior_mass(log_w):
+    """w = exp(clamp(log_w, -7, 12)) (model.py:74-75)."""
+    return log_w.clamp(-7.0, 12.0).exp()
+
+
+def decay_log(log_rate):
+    """g = -exp(log_rate), so lam = exp(g) (model.py:84, 104)."""
+    return -log_rate.exp()
+
+
+def block_forward(p, prefix, x, norm_eps=1e-5, form="chunked", chunk=64):
+    """UnifiedBlock.forward with the fast read replaced by a reference form
+    (model.py:77-85, test_all.py:64-72). ``p`` maps state_dict names to tensors."""
+    g = lambda n: p[prefix + n]
+    h = rmsnorm(x, g("norm.weight"), norm_eps)
+    u = causal_conv(h, g("conv.weight"))
+    r = address(F.linear(u, g("key.weight"), g("key.bias")), g("log_eps"))
+    v = F.linear(h, g("val.weight"))
+    w = prior_mass(g("log_w"))
+    q, fast = fast_memory(r, v, decay_log(g("log_rate")), w, form, chunk)
+    return x + F.linear(q * w, g("mu.weight")) + fast
+
+
+def n_layers_of(p):
+    return 1 + max(int(k.split(".")[1]) for k in p if k.startswith("layers."))
+
+
+def lm_forward(p, tokens, targets=None, norm_eps=1e-5, form="chunked", chunk=64):
+    """UnifiedLM.forward in a reference form (test_all.py:64-75, model.py:149-162).
+    Returns (logits, loss); the classifier is tied to the embedding (model.py:127)."""
+    emb = p["tok_embeddings.weight"]
+    h = emb[tokens]
+    for i in range(n_layers_of(p)):
+        h = block_forward(p, f"layers.{i}.", h, norm_eps, form, chunk)
+    logits = F.linear(rmsnorm(h, p["norm.weight"], norm_eps), p.get("output.weight", emb))
+    loss = None
+    if targets is not None:
+        loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), targets.reshape(-1), ignore_index=-1)
+    return logits, loss
+
+
+# ---------------------------------------------------------------------------
+# token-by-token decode (model.py:87-111, 164-175; run.c:193-265)
+
+def init_state(p, prefix, batch):
+    """Decode state at the prior (model.py:88-94, run.c:121-138):
+    U = mu * w, c = w, r_prev = 0, empty conv buffer."""
+    mu = p[prefix + "mu.weight"]
+    w = prior_mass(p[prefix + "log_w"])
+    D, A = mu.shape
+    Kc = p[prefix + "conv.weight"].shape[-1]
+    return {"buf": mu.new_zeros(batch, D, Kc - 1),
+            "U": (mu * w).expand(batch, D, A).clone(),
+            "c": w.expand(batch, A).clone(),
+            "r_prev": mu.new_zeros(batch, A)}
+
+
+def block_step(p, prefix, x, s, norm_eps=1e-5):
+    """One position of UnifiedBlock.step (model.py:96-111): write under the
+    previous address with decay toward the prior, then read with q = r / c."""
+    g = lambda n: p[prefix + n]
+    h = rmsnorm(x, g("norm.weight"), norm_eps)
+    win = torch.cat([s["buf"], h[:, :, None]], dim=-1)
+    u = (win * g("conv.weight")[:, 0, :]).sum(-1)
+    s["buf"] = win[:, :, 1:]
+    r = address(F.linear(u, g("key.weight"), g("key.bias")), g("log_eps"))
+    lam = torch.exp(decay_log(g("log_rate")))
+    v = F.linear(h, g("val.weight"))
+    w = prior_mass(g("log_w"))
+    mu = g("mu.weight")
+    s["U"] = lam * s["U"] + (1 - lam) * mu * w + v[:, :, None] * s["r_prev"][:, None, :]
+    s["c"] = lam * s["c"] + (1 - lam) * w + s["r_prev"]
+    y = (s["U"] @ (r / s["c"])[:, :, None]).squeeze(-1)
+    s["r_prev"] = r
+    return x + y
+
+
+def forward_recurrent(p, tokens, norm_eps=1e-5):
+    """UnifiedLM.forward_recurrent (model.py:164-175): logits (B, T, V)."""
+    B, T = tokens.shape
+    L = n_layers_of(p)
+    emb = p["tok_embeddings.weight"]
+    states = [init_state(p, f"layers.{i}.", B) for i in range(L)]
+    out = []
+    for t in range(T):
+        h = emb[tokens[:, t]]
+        for i in range(L):
+            h = block_step(p, f"layers.{i}.", h, states[i], norm_eps)
+        out.append(F.linear(rmsnorm(h, p["norm.weight"], norm_eps), p.get("output.weight", emb)))
+    return torch.stack(out, 1)
+
+
+# ---------------------------------------------------------------------------
+# seeded parameters
+
+def tiny_params(seed=0, dim=32, n_layers=3, hidden_dim=48, vocab_size=97, max_seq_len=40,
+                conv_size=4, prior=4.0, dtype=torch.float64):
+    """Parameters with every path non-trivial, distributed like the reference's
+    ``tiny_model`` fixture (test_all.py:78-90) on top of the UnifiedLM init
+    (model.py:129-147): conv ~ N(0, .5^2), key bias ~ N(0, .5^2), val ~ N(0, .2^2),
+    log_rate = log 0.05, log_w ~ N(0, 1). Values are this generator's own draws."""
+    gen = torch.Generator().manual_seed(seed)
+    n = lambda *shape, std=1.0: torch.randn(*shape, generator=gen, dtype=dtype) * std
+    p = {"tok_embeddings.weight": n(vocab_size, dim, std=0.02)}
+    for i in range(n_layers):
+        pre = f"layers.{i}."
+        p[pre + "norm.weight"] = torch.ones(dim, dtype=dtype)
+        p[pre + "conv.weight"] = n(dim, 1, conv_size, std=0.5)
+        p[pre + "key.weight"] = n(hidden_dim, dim, std=0.02)
+        p[pre + "key.bias"] = n(hidden_dim, std=0.5)
+        p[pre + "mu.weight"] = n(dim, hidden_dim, std=0.02 / math.sqrt(n_layers))
+        p[pre + "log_eps"] = torch.zeros((), dtype=dtype)
+        p[pre + "val.weight"] = n(dim, dim, std=0.2)
+        p[pre + "log_rate"] = torch.tensor(math.log(0.05), dtype=dtype)
+        p[pre + "log_w"] = n(hidden_dim, std=1.0)
+    p["norm.weight"] = torch.ones(dim, dtype=dtype)
+    return p

@@ -1,0 +1,260 @@
+"""Pins the float64 oracle (CPU only).
+
+Each oracle function is checked against something other than its own formula:
+a brute-force scalar loop, the recurrent (U, c) form, closed-form special
+cases, finite differences, the reference's invariant tests (test_all.py:100-137)
+and the logits of the reference's own run.c (golden fixture + live build).
+"""
+import math
+import os
+import tempfile
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fastmem as fm
+from oracle import runc, ulme
+
+TOL = 1e-8  # test_all.py:22
+
+
+def _inputs(B=2, T=11, A=5, D=3, seed=0, lam=0.8):
+    g = torch.Generator().manual_seed(seed)
+    r = torch.rand(B, T, A, generator=g, dtype=torch.float64)
+    r = r / (1 + r.sum(-1, keepdim=True))
+    v = torch.randn(B, T, D, generator=g, dtype=torch.float64)
+    w = torch.rand(A, generator=g, dtype=torch.float64) * 3 + 0.1
+    return r, v, torch.tensor(math.log(lam), dtype=torch.float64), w
+
+
+def _brute(r, v, lam, w):
+    """Scalar double loop straight from the definitions (kernel.py:4-9)."""
+    B, T, A = r.shape
+    D = v.shape[-1]
+    r, v, w, lam = r.tolist(), v.tolist(), w.tolist(), float(lam)
+    key = lambda b, s, a: r[b][s - 1][a] if s > 0 else 0.0
+    q = [[[0.0] * A for _ in range(T)] for _ in range(B)]
+    f = [[[0.0] * D for _ in range(T)] for _ in range(B)]
+    for b in range(B):
+        for t in range(T):
+            for a in range(A):
+                c = w[a] + sum(lam ** (t - s) * key(b, s, a) for s in range(t + 1))
+                q[b][t][a] = r[b][t][a] / c
+            for s in range(t + 1):
+                dot = sum(q[b][t][a] * key(b, s, a) for a in range(A))
+                for d in range(D):
+                    f[b][t][d] += lam ** (t - s) * dot * v[b][s][d]
+    return torch.tensor(q, dtype=torch.float64), torch.tensor(f, dtype=torch.float64)
+
+
+def _recurrent(r, v, lam, w):
+    """Token-by-token U/c recursion with the prior folded in (model.py:107-109)."""
+    B, T, A = r.shape
+    U = torch.zeros(B, v.shape[-1], A, dtype=torch.float64)  # mu = 0: U holds S only
+    c = w.expand(B, A).clone()
+    rp = torch.zeros(B, A, dtype=torch.float64)
+    qs, fs = [], []
+    for t in range(T):
+        U = lam * U + v[:, t, :, None] * rp[:, None, :]
+        c = lam * c + (1 - lam) * w + rp
+        q = r[:, t] / c
+        qs.append(q)
+        fs.append((U @ q[:, :, None]).squeeze(-1))
+        rp = r[:, t]
+    return torch.stack(qs, 1), torch.stack(fs, 1)
+
+
+def test_dense_matches_bruteforce():
+    r, v, g, w = _inputs(B=2, T=7, A=3, D=2)
+    q, f = fm.dense_fast_memory(r, v, g.exp(), w)
+    qb, fb = _brute(r, v, g.exp(), w)
+    assert (q - qb).abs().max() < 1e-12
+    assert (f - fb).abs().max() < 1e-12
+
+
+@pytest.mark.parametrize("mistake", ["no_shift", "reversed_decay", "no_prior", "transposed_scores"])
+def test_bruteforce_detects_planted_mistakes(mistake):
+    """A mistake planted in a copy of the dense form is caught by the brute force."""
+    r, v, g, w = _inputs(B=1, T=6, A=3, D=2)
+    lam = g.exp()
+    T = r.shape[1]
+    k = r if mistake == "no_shift" else fm.shift_keys(r)
+    M = fm.decay_mask(T, lam)
+    if mistake == "reversed_decay":
+        M = M.transpose(0, 1)
+    c = (0.0 if mistake == "no_prior" else w) + M @ k
+    q = r / (c + (1.0 if mistake == "no_prior" else 0.0))
+    S = q @ k.transpose(1, 2)
+    if mistake == "transposed_scores":
+        S = S.transpose(1, 2)
+    f = (S * M) @ v
+    qb, fb = _brute(r, v, lam, w)
+    assert max((q - qb).abs().max().item(), (f - fb).abs().max().item()) > 1e-6
+
+
+def test_recurrent_form_matches_dense():
+    r, v, g, w = _inputs(B=3, T=20, A=6, D=4)
+    q, f = fm.dense_fast_memory(r, v, g.exp(), w)
+    qr, fr = _recurrent(r, v, g.exp(), w)
+    assert (q - qr).abs().max() < 1e-12
+    assert (f - fr).abs().max() < 1e-12
+
+
+@pytest.mark.parametrize("chunk", [1, 7, 16, 64])
+def test_chunked_equals_dense(chunk):
+    r, v, g, w = _inputs(B=2, T=150, A=9, D=5)
+    q, f = fm.fast_memory(r, v, g, w, "dense")
+    qc, fc = fm.fast_memory(r, v, g, w, "chunked", chunk)
+    assert (q - qc).abs().max() < TOL
+    assert (f - fc).abs().max() < TOL
+
+
+def test_special_case_lam_to_zero():
+    """lam -> 0: c_t = w + k_t and fast_t = (q_t . k_t) v_t."""
+    r, v, _, w = _inputs(T=9)
+    g = torch.tensor(-60.0, dtype=torch.float64)
+    q, f = fm.fast_memory(r, v, g, w, "chunked", 4)
+    k = fm.shift_keys(r)
+    assert (q - r / (w + k)).abs().max() < 1e-14
+    assert (f - (q * k).sum(-1, keepdim=True) * v).abs().max() < 1e-14
+
+
+def test_special_case_lam_one():
+    """lam = 1: prefix sums."""
+    r, v, _, w = _inputs(T=13)
+    g = torch.tensor(0.0, dtype=torch.float64)
+    q, f = fm.fast_memory(r, v, g, w, "chunked", 5)
+    k = fm.shift_keys(r)
+    qe = r / (w + k.cumsum(1))
+    fe = torch.stack([(qe[:, t:t + 1] @ k[:, :t + 1].transpose(1, 2)) @ v[:, :t + 1] for t in range(13)], 1)[:, :, 0]
+    assert (q - qe).abs().max() < 1e-13
+    assert (f - fe).abs().max() < 1e-13
+
+
+def test_special_case_single_step_and_zero_rows():
+    r, v, g, w = _inputs(T=1)
+    q, f = fm.fast_memory(r, v, g, w)
+    assert (q - r / w).abs().max() < 1e-15 and f.abs().max() == 0
+    r, v, g, w = _inputs(T=10)
+    r[:, 4] = 0
+    q, f = fm.fast_memory(r, v, g, w)
+    assert q[:, 4].abs().max() == 0 and f[:, 4].abs().max() == 0
+
+
+def test_address_invariants():
+    g = torch.Generator().manual_seed(3)
+    pre = torch.randn(4, 7, 50, generator=g, dtype=torch.float64)
+    r = fm.address(pre, torch.tensor(0.0, dtype=torch.float64))
+    assert (r >= 0).all() and (r[pre <= 0] == 0).all()
+    assert (r.sum(-1) < 1).all()
+    z = pre.clamp(min=0) ** 2
+    assert (r.sum(-1) - z.sum(-1) / (1 + z.sum(-1))).abs().max() < 1e-14
+    r_lo = fm.address(pre, torch.tensor(-10.0, dtype=torch.float64))   # eps = e^-10
+    assert (r_lo.sum(-1) - 1).abs().max() < 1e-3
+    assert torch.allclose(fm.address(pre, torch.tensor(-30.0, dtype=torch.float64)), r_lo)  # clamp
+
+
+def test_gradcheck_fast_memory():
+    r, v, g, w = _inputs(B=1, T=7, A=3, D=2)
+    args = tuple(x.clone().requires_grad_(True) for x in (r, v, g, w))
+    assert torch.autograd.gradcheck(lambda *a: fm.fast_memory(*a, "chunked", 3), args)
+
+
+def test_gradcheck_address():
+    g = torch.Generator().manual_seed(5)
+    pre = torch.randn(3, 6, generator=g, dtype=torch.float64).requires_grad_(True)
+    le = torch.tensor(0.3, dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(fm.address, (pre, le))
+
+
+def test_dg_identity_matches_autograd():
+    """The reference's positional form of d/dg (kernel.py:173-175) equals autograd."""
+    r, v, g, w = _inputs(B=2, T=40, A=6, D=4)
+    gen = torch.Generator().manual_seed(9)
+    dq = torch.randn(r.shape, generator=gen, dtype=torch.float64)
+    df = torch.randn(v.shape, generator=gen, dtype=torch.float64)
+    _, _, dg, _ = fm.fast_memory_grads(r, v, g, w, dq, df, "dense")
+    dg_id, _ = fm.dg_identity(r, v, g, w, dq, df)
+    assert abs(dg.item() - dg_id.item()) < 1e-10 * max(1.0, abs(dg.item()))
+
+
+# ----- model level (test_all.py:100-137)
+
+def _tokens(B=3, T=40, V=97, seed=0):
+    return torch.randint(0, V, (B, T), generator=torch.Generator().manual_seed(seed))
+
+
+def test_model_chunked_equals_dense():
+    p = fm.tiny_params()
+    x = _tokens()
+    a, _ = fm.lm_forward(p, x, form="chunked", chunk=7)
+    b, _ = fm.lm_forward(p, x, form="dense")
+    assert (a - b).abs().max() < TOL
+
+
+def test_parallel_equals_recurrent():
+    p = fm.tiny_params()
+    x = _tokens()
+    a, _ = fm.lm_forward(p, x, form="chunked", chunk=16)
+    assert (a - fm.forward_recurrent(p, x)).abs().max() < TOL
+
+
+def test_causality():
+    p = fm.tiny_params()
+    x = _tokens()
+    x2 = x.clone()
+    x2[:, 25:] = _tokens(3, 15, seed=1)
+    a, _ = fm.lm_forward(p, x, form="chunked", chunk=7)
+    b, _ = fm.lm_forward(p, x2, form="chunked", chunk=7)
+    assert (a[:, :25] - b[:, :25]).abs().max() < TOL
+
+
+def test_gradients_finite():
+    p = {k: v.clone().requires_grad_(True) for k, v in fm.tiny_params().items()}
+    x = _tokens()
+    _, loss = fm.lm_forward(p, x, x, form="chunked", chunk=7)
+    loss.backward()
+    for name, t in p.items():
+        assert t.grad is not None and torch.isfinite(t.grad).all(), name
+
+
+# ----- the reference's own C decoder
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "runc_decode.npz")
+
+
+def _golden():
+    z = np.load(GOLDEN)
+    p = {k[len("param/"):]: torch.from_numpy(z[k]).double() for k in z.files if k.startswith("param/")}
+    return p, torch.from_numpy(z["tokens"]), z["logits"]
+
+
+def test_recurrent_matches_runc_golden():
+    """forward_recurrent of the oracle against logits written by run.c itself."""
+    p, tokens, logits = _golden()
+    got = fm.forward_recurrent(p, tokens[None])[0].numpy()
+    scale = np.abs(logits).max()
+    assert np.abs(got - logits).max() < 1e-5 * scale
+
+
+def test_parallel_matches_runc_golden():
+    p, tokens, logits = _golden()
+    got, _ = fm.lm_forward(p, tokens[None], form="chunked", chunk=64)
+    assert np.abs(got[0].numpy() - logits).max() < 1e-5 * np.abs(logits).max()
+
+
+@pytest.mark.skipif(not runc.available(), reason="oracle/_ref/librunc_ref.so not built")
+def test_recurrent_matches_runc_live():
+    """A fresh seeded model with an untied classifier, through run.c."""
+    p = fm.tiny_params(seed=11, dim=16, n_layers=2, hidden_dim=20, vocab_size=41, dtype=torch.float32)
+    p["output.weight"] = torch.randn(41, 16, generator=torch.Generator().manual_seed(2)) * 0.1
+    tokens = _tokens(1, 30, 41, seed=4)[0]
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "m.bin")
+        ulme.write_ulme_v1(p, path, max_seq_len=30)
+        magic, version, cfg = ulme.read_header(path)
+        assert (magic, version, cfg[-1]) == (ulme.MAGIC, 1, 0)
+        ref = runc.RuncReference(path).logits(tokens.tolist())
+    got = fm.forward_recurrent({k: v.double() for k, v in p.items()}, tokens[None])[0].numpy()
+    assert np.abs(got - ref).max() < 1e-5 * np.abs(ref).max()

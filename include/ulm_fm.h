@@ -1,0 +1,154 @@
+/*
+ * ulm_fm.h - C ABI of libulm_fm.so, the MI355X (gfx950) implementation of
+ * UnifiedLM's fast-memory path.
+ *
+ * The reference has no C ABI for this path: its boundary is the Python
+ * autograd Function `unified_memory(r, v, g, w) -> (q, fast)`
+ * (kernel.py:199-238) called from UnifiedBlock.forward (model.py:84), and the
+ * token-by-token UnifiedBlock.step / forward_recurrent (model.py:87-111,
+ * 164-175) mirrored in C by run.c:193-265. Each entry point below names the
+ * reference code it replaces.
+ *
+ * Conventions:
+ *   - all pointers are device pointers (HBM of the current HIP device);
+ *   - `stream` is a hipStream_t; every kernel is enqueued on it and the call
+ *     returns without synchronising;
+ *   - nothing is allocated inside; temporaries live in a caller-provided
+ *     workspace whose size the matching *_workspace_bytes function returns;
+ *   - tensors are dense row-major: (B,T,A) means A fastest;
+ *   - `g` is a device pointer to one fp32 scalar g = -exp(log_rate), so
+ *     lam = exp(g) is read on the device and no host sync happens
+ *     (kernel.py:31, model.py:84);
+ *   - return 0 (ULM_OK) or a nonzero ulm_status; ulm_last_error() gives the
+ *     calling thread's last message. Arguments are validated before any HIP
+ *     call, so an invalid call never touches the GPU.
+ */
+#ifndef ULM_FM_H
+#define ULM_FM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum ulm_status { ULM_OK = 0, ULM_ERR_INVALID = 1, ULM_ERR_UNSUPPORTED = 2, ULM_ERR_LAUNCH = 3 };
+
+/* Element types for arguments whose dtype follows the caller's tensor. */
+enum ulm_dtype { ULM_F32 = 0, ULM_BF16 = 1, ULM_F16 = 2 };
+
+/* Chunk length of the chunked kernels (kernel.py:20, CHUNK = 64). */
+#define ULM_CHUNK 64
+
+int ulm_abi_version(void);
+const char *ulm_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * Training: fused fast memory. Replaces UnifiedMemory.forward
+ * (kernel.py:202-213): q = r / c with c = w + decayed cumsum of k = shift(r),
+ * fast = causal scalar-decay linear attention of (q, k, v).
+ *
+ *   r      (B,T,A) fp32          read addresses
+ *   v16    (B,T,D) bf16          values, already cast to bf16 (kernel.py:205)
+ *   w      (A,)    fp32          prior mass
+ *   q      (B,T,A) fp32   out    returned and saved
+ *   fast   (B,T,D) fast_dtype out  (v.dtype in the reference, kernel.py:211)
+ *   q16, k16 (B,T,A) bf16 out    saved for backward (kernel.py:212)
+ *   n_ckpt (B,ceil(T/64),A) fp32 out  evidence n = c - w at the end of each
+ *                                 chunk's predecessor, saved for backward in
+ *                                 place of the full c tensor
+ */
+size_t ulm_fm_fwd_workspace_bytes(int B, int T, int A, int D, int fast_dtype);
+int ulm_fm_fwd(const float *r, const uint16_t *v16, const float *g, const float *w,
+               float *q, void *fast, int fast_dtype, uint16_t *q16, uint16_t *k16, float *n_ckpt,
+               void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream);
+
+/* Replaces UnifiedMemory.backward (kernel.py:216-233): the three chunked
+ * products dq, dk (reverse), dv (reverse) and the denominator chain rule.
+ *
+ *   dfast  (B,T,D) dfast_dtype   upstream gradient of fast
+ *   dq_out (B,T,A) fp32 or NULL  upstream gradient of the returned q
+ *                                 (HAS_DQO, kernel.py:166-167, 228)
+ *   dr     (B,T,A) fp32  out
+ *   dv     (B,T,D) dv_dtype out  (dfast.dtype in the reference, kernel.py:223)
+ *   dg     (1,)    fp32  out     d loss / d g
+ *   dw     (A,)    fp32  out
+ * dg and dw are reduced deterministically (no atomics). */
+size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D);
+int ulm_fm_bwd(const float *r, const uint16_t *v16, const float *g, const float *w,
+               const float *q, const uint16_t *q16, const uint16_t *k16, const float *n_ckpt,
+               const void *dfast, int dfast_dtype, const float *dq_out,
+               float *dr, void *dv, int dv_dtype, float *dg, float *dw,
+               void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream);
+
+/* Building block of both: out += o, o_t = sum_{s<=t} lam^(t-s) (a_t . b_s) c_s
+ * (s >= t and time read backwards when reverse != 0). Replaces `_la`
+ * (kernel.py:183-196) with the chunk state kept in fp32 on chip.
+ * a, b (B,T,K) bf16; c (B,T,V) bf16; out (B,T,V) fp32 accumulated with
+ * atomic adds, so the caller zeroes it first. */
+int ulm_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out,
+           int B, int T, int K, int V, int reverse, void *stream);
+
+/* ------------------------------------------------------------------------
+ * relu^2 slot address. Replaces UnifiedBlock.code (model.py:70-72) after
+ * the key GEMM: r = z / (exp(clamp(log_eps,-10,10)) + sum_a z),
+ * z = relu(pre + bias)^2, one row per token.
+ *
+ *   pre   (M,A) pre_dtype        K u without the bias
+ *   bias  (A,)  fp32 or NULL
+ *   log_eps (1,) fp32 device scalar
+ *   r     (M,A) fp32 out
+ *   denom (M,)  fp32 out         exp(clamp(log_eps)) + sum_a z, saved for backward
+ */
+int ulm_addr_fwd(const void *pre, int pre_dtype, const float *bias, const float *log_eps,
+                 float *r, float *denom, int M, int A, void *stream);
+
+/* Backward of ulm_addr_fwd: dpre (M,A) pre_dtype, dbias (A,) fp32 (may be
+ * NULL when bias is NULL), dlog_eps (1,) fp32. */
+size_t ulm_addr_bwd_workspace_bytes(int M, int A);
+int ulm_addr_bwd(const void *pre, int pre_dtype, const float *bias, const float *log_eps,
+                 const float *r, const float *denom, const float *dr,
+                 void *dpre, float *dbias, float *dlog_eps,
+                 void *workspace, size_t workspace_bytes, int M, int A, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Batched recurrent decode, N sequences, one block, one position. Together
+ * these replace UnifiedBlock.step (model.py:96-111) / run.c:193-265. The
+ * slot contents are held as S = U - mu*w, so the stored state is exactly the
+ * north-star S_t = lam S_{t-1} + v_t r_{t-1}^T and y = S q + mu (w*q).
+ *
+ * ulm_decode_pre: h = RMSNorm(x) (model.py:31-42), u = causal depthwise conv
+ *   over [conv_buf, h] (model.py:100-102), conv_buf shifted in place.
+ *   x (N,D), norm_w (D,), conv_w (D,Kc) oldest->newest, conv_buf (N,D,Kc-1),
+ *   h (N,D) out, u (N,D) out.
+ */
+int ulm_decode_pre(const float *x, const float *norm_w, const float *conv_w, float *conv_buf,
+                   float *h, float *u, int N, int D, int Kc, float norm_eps, void *stream);
+
+/* ulm_decode_addr: r = relu^2 address of pre + bias (model.py:103);
+ *   c <- lam c + (1-lam) w + r_prev (model.py:108); q = r / c; wq = w * q.
+ *   pre (N,A) fp32 (K u), c (N,A) in/out, r_prev (N,A), r/q/wq (N,A) out. */
+int ulm_decode_addr(const float *pre, const float *bias, const float *log_eps, const float *w,
+                    const float *g, const float *r_prev, float *c, float *r, float *q, float *wq,
+                    int N, int A, void *stream);
+
+/* ulm_decode_state: S <- lam S + v r_prev^T (model.py:107 minus its constant
+ *   prior term), y = S q (model.py:109), out = x + y + ymu where
+ *   ymu = mu (w*q) is computed by the caller's GEMM.
+ *   S (N,D,A) fp32 in/out, v/x/ymu/out (N,D), r_prev/q (N,A). */
+int ulm_decode_state(float *S, const float *v, const float *r_prev, const float *q,
+                     const float *g, const float *x, const float *ymu, float *out,
+                     int N, int D, int A, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Diagnostics. Writes, for lane l of one wave, the operand/result layout of
+ * one v_mfma_f32_32x32x16_bf16 on A = a (32x16 row-major), B = b (16x32
+ * row-major): d (32x32 row-major) = A B computed through the kernels' own
+ * operand-loading helpers. No counterpart in the reference. */
+int ulm_probe_mfma(const uint16_t *a, const uint16_t *b, float *d, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ULM_FM_H */

@@ -45,7 +45,8 @@ def shift_keys(r):
 
 def decay_mask(T, lam, dtype=torch.float64):
     """M[t, s] = lam^(t-s) for s <= t, else 0 (test_all.py:58)."""
-    t = torch.arange(T, dtype=dtype)
+    dev = lam.device if isinstance(lam, torch.Tensor) else None
+    t = torch.arange(T, dtype=dtype, device=dev)
     lag = (t[:, None] - t[None, :])
     return (lag >= 0).to(dtype) * lam ** lag.clamp(min=0)
 
@@ -75,7 +76,7 @@ def chunked_fast_memory(r, v, lam, w, chunk=64):
     qs, fs = [], []
     for t0 in range(0, T, chunk):
         L = min(chunk, T - t0)
-        i = torch.arange(L, dtype=r.dtype)
+        i = torch.arange(L, dtype=r.dtype, device=r.device)
         M = decay_mask(L, lam, r.dtype)
         into = (lam ** (i + 1))[None, :, None]          # carried state -> row i
         tail = (lam ** (L - 1 - i))[None, :, None]      # row i -> chunk end
@@ -88,6 +89,17 @@ def chunked_fast_memory(r, v, lam, w, chunk=64):
         state = lam ** L * state + (kc * tail).transpose(1, 2) @ vc
         mass = lam ** L * mass + (kc * tail).sum(1, keepdim=True)
     return torch.cat(qs, 1), torch.cat(fs, 1)
+
+
+def la_dense(a, b, c, lam, reverse=False):
+    """The chunked kernel's building block in quadratic form (kernel.py:183-184):
+    o_t = sum_{s<=t} lam^(t-s) (a_t . b_s) c_s, or s >= t when ``reverse``."""
+    a, b, c = a.double(), b.double(), c.double()
+    if reverse:
+        a, b, c = a.flip(1), b.flip(1), c.flip(1)
+    M = decay_mask(a.shape[1], torch.as_tensor(lam, dtype=torch.float64)).to(a.device)
+    o = ((a @ b.transpose(1, 2)) * M) @ c
+    return o.flip(1) if reverse else o
 
 
 def fast_memory(r, v, g, w, form="chunked", chunk=64):
@@ -134,7 +146,7 @@ def dg_identity(r, v, g, w, dq_out, dfast):
     dq = dq_f + (dq_out.double() if dq_out is not None else 0.0)
     dc = -dq * q / c
     dk_c = M.transpose(0, 1) @ dc
-    pos = torch.arange(T, dtype=torch.float64)[None, :, None]
+    pos = torch.arange(T, dtype=torch.float64, device=r.device)[None, :, None]
     return ((pos * (q * dq_f + dc * (c - w))).sum() - (pos * k * (dk_f + dk_c)).sum()), P
 
 

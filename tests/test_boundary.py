@@ -1,0 +1,114 @@
+"""The C-ABI boundary and the host-side checks (CPU only: no compute call
+reaches the GPU; invalid calls must fail before any HIP call)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ulm_fm.h")
+
+import ulm_native as nat  # noqa: E402
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ulm_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = nat.lib()
+    declared = header_functions()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert sorted(nat.SIGNATURES) == declared
+    assert lib.ulm_abi_version() == 1
+
+
+def test_c_side_rejects_bad_sizes_without_touching_the_gpu():
+    lib = nat.lib()
+    st = lib.ulm_la(None, None, None, None, None, 0, 10, 8, 8, 0, None)
+    assert st == nat.ULM_ERR_INVALID
+    assert b"bad sizes" in lib.ulm_last_error()
+    st = lib.ulm_fm_fwd(*([None] * 6), 0, None, None, None, None, 0, 2, 64, 8, 8, None)
+    assert st == nat.ULM_ERR_INVALID and b"null pointer" in lib.ulm_last_error()
+    st = lib.ulm_decode_state(*([None] * 8), 4, 8, 100000, None)
+    assert st == nat.ULM_ERR_INVALID and b"LDS" in lib.ulm_last_error()
+
+
+def test_nonzero_status_surfaces_as_runtime_error():
+    with pytest.raises(RuntimeError, match="status 1"):
+        nat.call("ulm_la", None, None, None, None, None, 1, 0, 8, 8, 0, None)
+
+
+def test_workspace_sizes():
+    lib = nat.lib()
+    B, T, A, D = 16, 1024, 3072, 768
+    assert lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_F32) == 0
+    assert lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * D * 4
+    assert lib.ulm_fm_bwd_workspace_bytes(B, T, A, D) >= B * T * (2 * A * 4 + D * 6)
+    assert lib.ulm_addr_bwd_workspace_bytes(B * T, A) >= A * 4
+    assert lib.ulm_fm_bwd_workspace_bytes(0, T, A, D) == 0
+
+
+def _fm_args(B=2, T=70, A=12, D=8, dtype=torch.float32):
+    return (torch.rand(B, T, A, dtype=dtype), torch.randn(B, T, D, dtype=dtype),
+            torch.tensor(-0.05), torch.full((A,), 4.0))
+
+
+def test_unified_memory_input_checks():
+    from kernel import unified_memory
+    r, v, g, w = _fm_args()
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        unified_memory(r, v, g, w)                       # CPU tensors: no fallback
+    with pytest.raises(ValueError, match="disagree"):
+        unified_memory(r, v[:, :5], g, w)
+    with pytest.raises(ValueError, match="w must have shape"):
+        unified_memory(r, v, g, w[:5])
+    with pytest.raises(ValueError, match="empty"):
+        unified_memory(r[:0], v[:0], g, w)
+    with pytest.raises(ValueError, match="one scalar"):
+        unified_memory(r, v, torch.zeros(2), w)
+    with pytest.raises(TypeError, match="floating"):
+        unified_memory(r.long(), v, g, w)
+    with pytest.raises(ValueError, match=r"\(B, T, A\)"):
+        unified_memory(r[0], v[0], g, w)
+
+
+def test_address_input_checks():
+    from kernel import relu2_address
+    pre = torch.randn(4, 10)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        relu2_address(pre, torch.zeros(10), torch.zeros(()))
+    with pytest.raises(ValueError, match="bias"):
+        relu2_address(pre, torch.zeros(9), torch.zeros(()))
+    with pytest.raises(TypeError, match="floating"):
+        relu2_address(pre.int(), None, torch.zeros(()))
+
+
+def test_decode_rejects_non_fp32():
+    from kernel import decode_state
+    S = torch.zeros(2, 4, 8, dtype=torch.float64)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        decode_state(S, torch.zeros(2, 4), torch.zeros(2, 8), torch.zeros(2, 8), torch.zeros(1), torch.zeros(2, 4),
+                     torch.zeros(2, 4))
+
+
+def test_model_parameters_match_reference_layout():
+    """The module tree and parameter names of the reference (model.py:45-147)."""
+    from model import ModelArgs, UnifiedLM
+    m = UnifiedLM(ModelArgs(dim=16, n_layers=2, hidden_dim=24, vocab_size=50, max_seq_len=32))
+    names = [n for n, _ in m.named_parameters()]
+    expect = ["tok_embeddings.weight"]
+    for i in range(2):
+        # a module's own parameters come before its submodules' in named_parameters()
+        expect += [f"layers.{i}.{n}" for n in ("log_eps", "log_rate", "log_w", "norm.weight", "conv.weight",
+                                               "key.weight", "key.bias", "mu.weight", "val.weight")]
+    expect += ["norm.weight"]
+    assert names == expect
+    assert m.output.weight is m.tok_embeddings.weight
+    assert torch.all(m.layers[0].val.weight == 0) and torch.all(m.layers[0].conv.weight[:, 0, -1] == 1)

@@ -1,0 +1,185 @@
+"""Parity of the HIP kernels with the float64 oracle (needs an MI355X).
+
+Tolerances: training path 1e-2 norm-wise relative error on outputs and every
+gradient (test_all.py:166); fp32 decode 1e-5 relative to forward_recurrent.
+Every case prints its name before touching the GPU.
+"""
+import math
+
+import pytest
+import torch
+
+from helpers import fm_inputs, oracle_params, rel, say, tiny_model
+from oracle import fastmem as fm
+
+pytestmark = pytest.mark.gpu
+
+import kernel  # noqa: E402
+
+
+def test_mfma_operand_layout():
+    say("mfma layout probe 32x32x16 bf16")
+    gen = torch.Generator().manual_seed(0)
+    a = torch.randn(32, 16, generator=gen).to(torch.bfloat16)
+    b = torch.randn(16, 32, generator=gen).to(torch.bfloat16)
+    d = kernel.probe_mfma(a.cuda(), b.cuda()).cpu()
+    ref = a.double() @ b.double()
+    assert (d.double() - ref).abs().max() < 1e-4
+
+
+LA_CASES = [
+    # B, T, K, V, reverse
+    (1, 64, 128, 256, False),
+    (1, 64, 128, 256, True),
+    (2, 200, 140, 64, False),
+    (2, 200, 140, 64, True),
+    (1, 1, 16, 8, False),
+    (2, 130, 48, 32, True),
+    (1, 300, 300, 520, False),
+    (2, 256, 256, 512, True),
+]
+
+
+@pytest.mark.parametrize("B,T,K,V,reverse", LA_CASES)
+def test_la_matches_dense(B, T, K, V, reverse):
+    say(f"la B={B} T={T} K={K} V={V} reverse={reverse}")
+    gen = torch.Generator().manual_seed(B * 1000 + T + K + V)
+    a = (torch.randn(B, T, K, generator=gen) / math.sqrt(K)).to(torch.bfloat16)
+    b = torch.randn(B, T, K, generator=gen).to(torch.bfloat16)
+    c = torch.randn(B, T, V, generator=gen).to(torch.bfloat16)
+    lam = 0.93
+    g = torch.tensor([math.log(lam)], dtype=torch.float32)
+    out = kernel.la(a.cuda(), b.cuda(), c.cuda(), g.cuda(), reverse).cpu()
+    ref = fm.la_dense(a, b, c, lam, reverse)
+    assert torch.isfinite(out).all()
+    assert rel(out, ref) < 1e-2
+
+
+OP_CASES = [
+    # B, T, A, D, dtype of v
+    (2, 200, 140, 64, torch.float32),
+    (2, 64, 128, 32, torch.float32),
+    (3, 77, 48, 40, torch.bfloat16),
+    (1, 1, 64, 64, torch.float32),
+    (4, 256, 1152, 288, torch.bfloat16),   # 15M-shape block, fewer rows
+]
+
+
+@pytest.mark.parametrize("B,T,A,D,vdt", OP_CASES)
+def test_unified_memory_matches_oracle(B, T, A, D, vdt):
+    say(f"unified_memory B={B} T={T} A={A} D={D} v={vdt}")
+    r, v, g, w = fm_inputs(B, T, A, D, seed=T + A, device="cpu")
+    gen = torch.Generator().manual_seed(7)
+    dq = torch.randn(B, T, A, generator=gen, dtype=torch.float64) * 0.1
+    df = torch.randn(B, T, D, generator=gen, dtype=torch.float64)
+    # GPU: fp32 inputs (v in vdt), grads for all four
+    rg = r.float().cuda().requires_grad_(True)
+    vg = v.to(vdt).cuda().requires_grad_(True)
+    gg = g.float().cuda().requires_grad_(True)
+    wg = w.float().cuda().requires_grad_(True)
+    q, fast = kernel.unified_memory(rg, vg, gg, wg)
+    assert q.dtype == torch.float32 and fast.dtype == vdt
+    ((q * dq.float().cuda()).sum() + (fast.float() * df.float().cuda()).sum()).backward()
+    torch.cuda.synchronize()
+    # oracle: float64 on the same (rounded) inputs
+    vr = v.to(vdt).double()
+    qr, fr = fm.fast_memory(r, vr, g, w, "chunked")
+    dr, dv, dgr, dw = fm.fast_memory_grads(r, vr, g, w, dq, df)
+    assert rel(q, qr) < 1e-5
+    assert rel(fast, fr) < 1e-2
+    errs = {"dr": rel(rg.grad, dr), "dv": rel(vg.grad, dv), "dg": rel(gg.grad, dgr), "dw": rel(wg.grad, dw)}
+    say(f"  rel errors {errs}")
+    assert max(errs.values()) < 1e-2, errs
+
+
+@pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
+def test_address_matches_oracle(pdt):
+    say(f"relu2 address {pdt}")
+    gen = torch.Generator().manual_seed(3)
+    M, A = 300, 700
+    pre = torch.randn(M, A, generator=gen).to(pdt)
+    bias = torch.randn(A, generator=gen) * 0.5
+    le = torch.tensor(0.3)
+    dr = torch.randn(M, A, generator=gen)
+    pg = pre.cuda().requires_grad_(True)
+    bg = bias.cuda().requires_grad_(True)
+    lg = le.cuda().requires_grad_(True)
+    r = kernel.relu2_address(pg, bg, lg)
+    (r * dr.cuda()).sum().backward()
+    p64 = pre.double().requires_grad_(True)
+    b64 = bias.double().requires_grad_(True)
+    l64 = le.double().requires_grad_(True)
+    rr = fm.address(p64 + b64, l64)
+    (rr * dr.double()).sum().backward()
+    assert rel(r, rr) < 1e-5
+    tol = 1e-5 if pdt == torch.float32 else 1e-2
+    assert rel(pg.grad, p64.grad) < tol
+    assert rel(bg.grad, b64.grad) < 1e-5
+    assert rel(lg.grad, l64.grad) < 1e-5
+
+
+def _decode_model(seed=0, **kw):
+    return tiny_model(seed, **kw).cuda()
+
+
+def test_decode_matches_oracle_recurrent():
+    say("decode: forward_recurrent vs oracle, tiny model, B=3 T=40")
+    model = _decode_model()
+    x = torch.randint(0, 97, (3, 40), generator=torch.Generator().manual_seed(0))
+    got = model.forward_recurrent(x.cuda()).cpu()
+    ref = fm.forward_recurrent(oracle_params(model), x)
+    assert rel(got, ref) < 1e-5
+    assert (got.double() - ref).abs().max() < 1e-5 * ref.abs().max()
+
+
+def test_decode_matches_runc_golden():
+    """GPU decode against logits written by the reference's run.c."""
+    import os
+    import numpy as np
+    say("decode: run.c golden fixture")
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "runc_decode.npz"))
+    from model import ModelArgs, UnifiedLM
+    p = {k[len("param/"):]: torch.from_numpy(z[k]) for k in z.files if k.startswith("param/")}
+    D = p["layers.0.norm.weight"].shape[0]
+    A = p["layers.0.key.weight"].shape[0]
+    L = fm.n_layers_of(p)
+    model = UnifiedLM(ModelArgs(dim=D, n_layers=L, hidden_dim=A, vocab_size=p["tok_embeddings.weight"].shape[0],
+                                conv_size=p["layers.0.conv.weight"].shape[-1]))
+    model.load_state_dict({**p, "output.weight": p["tok_embeddings.weight"]})
+    model = model.cuda()
+    tokens = torch.from_numpy(z["tokens"])[None].cuda()
+    got = model.forward_recurrent(tokens)[0].cpu().numpy()
+    ref = z["logits"]
+    assert np.abs(got - ref).max() < 1e-5 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+def test_model_kernel_vs_reference(autocast):
+    """test_all.py:140-166: loss and every parameter gradient of UnifiedLM.forward
+    against the float64 reference, T and A not multiples of the tiles."""
+    say(f"model kernel vs float64 reference, autocast={autocast}")
+    kw = dict(dim=64, n_layers=2, hidden_dim=140, vocab_size=512, max_seq_len=200)
+    model = tiny_model(**kw).cuda().train()
+    params = oracle_params(model, requires_grad=True)
+    x = torch.randint(0, 512, (2, 200), generator=torch.Generator().manual_seed(1))
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        model(x.cuda(), x.cuda())
+    model.last_loss.backward()
+    torch.cuda.synchronize()
+    _, loss = fm.lm_forward(params, x, x, form="chunked", chunk=64)
+    loss.backward()
+    out = {"loss": abs(model.last_loss.item() - loss.item()) / abs(loss.item())}
+    for name, p in model.named_parameters():
+        out[name] = rel(p.grad, params[name].grad)
+    say(f"  worst {max(out.values()):.3e}")
+    assert max(out.values()) < 1e-2, out
+
+
+def test_parallel_matches_recurrent_on_gpu():
+    say("model: training kernels vs decode kernels")
+    model = tiny_model().cuda()
+    x = torch.randint(0, 97, (3, 40), generator=torch.Generator().manual_seed(0)).cuda()
+    with torch.no_grad():
+        a = model(x, x)   # logits (B, T, V) with targets
+    b = model.forward_recurrent(x)
+    assert rel(a, b) < 1e-2

@@ -110,6 +110,22 @@ def test_chunked_equals_dense(chunk):
     assert (f - fc).abs().max() < TOL
 
 
+def test_la_dense_and_role_table():
+    """la_dense(q, k, v) is fast, and the three backward products of the role
+    table (docs/kernel.md:22-27) are the autograd gradients of it."""
+    r, v, g, w = _inputs(B=2, T=30, A=6, D=4)
+    lam = g.exp()
+    q, f = fm.dense_fast_memory(r, v, lam, w)
+    k = fm.shift_keys(r)
+    assert (fm.la_dense(q, k, v, lam) - f).abs().max() < 1e-13
+    do = torch.randn(f.shape, generator=torch.Generator().manual_seed(1), dtype=torch.float64)
+    q_, k_, v_ = (x.clone().requires_grad_(True) for x in (q, k, v))
+    (fm.la_dense(q_, k_, v_, lam) * do).sum().backward()
+    assert (fm.la_dense(do, v, k, lam) - q_.grad).abs().max() < 1e-12
+    assert (fm.la_dense(v, do, q, lam, reverse=True) - k_.grad).abs().max() < 1e-12
+    assert (fm.la_dense(k, q, do, lam, reverse=True) - v_.grad).abs().max() < 1e-12
+
+
 def test_special_case_lam_to_zero():
     """lam -> 0: c_t = w + k_t and fast_t = (q_t . k_t) v_t."""
     r, v, _, w = _inputs(T=9)

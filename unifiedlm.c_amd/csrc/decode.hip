@@ -1,0 +1,179 @@
+// Batched recurrent decode of one UnifiedBlock for N sequences and one position.
+//
+// Replaces UnifiedBlock.step (model.py:96-111) and its C mirror run.c:193-265.
+// Per block and position the caller runs:
+//   ulm_decode_pre   RMSNorm + causal depthwise conv window       (model.py:99-102)
+//   pre = u K^T, v = h Wv^T                                        (library GEMMs)
+//   ulm_decode_addr  relu^2 address, c update, q = r / c, w*q      (model.py:103-108)
+//   ymu = (w*q) mu^T                                               (library GEMM)
+//   ulm_decode_state S <- lam S + v r_prev^T, y = S q, out         (model.py:107-111)
+//
+// HBM layout: S is (N, D, A) fp32 with the slot index fastest, one row of A
+// floats per (sequence, feature), like run.c's U[l][i][a] (run.c:38-41). The
+// state kernel streams every row exactly once per token (read + write), which
+// is the whole of the path's HBM traffic at large N: 8*A*D bytes per sequence.
+#include "ulm_common.h"
+
+namespace ulm {
+
+// Sum over a 256-thread block; every thread gets the result.
+__device__ __forceinline__ float block_sum_256(float v, float *red) {
+    v = wave_sum(v);
+    int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+}
+
+__global__ __launch_bounds__(256) void decode_pre_kernel(const float *__restrict__ x, const float *__restrict__ nw,
+                                                         const float *__restrict__ cw, float *__restrict__ buf,
+                                                         float *__restrict__ h, float *__restrict__ u, int D, int Kc,
+                                                         float eps) {
+    __shared__ float red[4];
+    const size_t n = blockIdx.x;
+    const float *xr = x + n * D;
+    float ss = 0.f;
+    for (int d = threadIdx.x; d < D; d += 256) ss += xr[d] * xr[d];
+    ss = block_sum_256(ss, red);
+    const float inv = rsqrtf(ss / static_cast<float>(D) + eps);
+    const int kw = Kc - 1;
+    for (int d = threadIdx.x; d < D; d += 256) {
+        const float hd = (xr[d] * inv) * nw[d];
+        float *st = buf + (n * D + d) * kw;
+        const float *w = cw + static_cast<size_t>(d) * Kc;
+        float ud = 0.f;
+        for (int j = 0; j < kw; ++j) ud += w[j] * st[j];
+        ud += w[kw] * hd;
+        for (int j = 0; j + 1 < kw; ++j) st[j] = st[j + 1];
+        if (kw > 0) st[kw - 1] = hd;
+        h[n * D + d] = hd;
+        u[n * D + d] = ud;
+    }
+}
+
+__global__ __launch_bounds__(256) void decode_addr_kernel(const float *__restrict__ pre, const float *__restrict__ bias,
+                                                          const float *__restrict__ log_eps, const float *__restrict__ w,
+                                                          const float *__restrict__ g, const float *__restrict__ r_prev,
+                                                          float *__restrict__ c, float *__restrict__ r,
+                                                          float *__restrict__ q, float *__restrict__ wq, int A) {
+    __shared__ float red[4];
+    const size_t row = static_cast<size_t>(blockIdx.x) * A;
+    float s = 0.f;
+    for (int a = threadIdx.x; a < A; a += 256) {
+        float p = pre[row + a] + (bias ? bias[a] : 0.f);
+        p = p > 0.f ? p : 0.f;
+        s += p * p;
+    }
+    s = block_sum_256(s, red);
+    const float denom = __expf(fminf(fmaxf(log_eps[0], -10.f), 10.f)) + s;
+    const float lam = __expf(g[0]);
+    for (int a = threadIdx.x; a < A; a += 256) {
+        float p = pre[row + a] + (bias ? bias[a] : 0.f);
+        p = p > 0.f ? p : 0.f;
+        const float ra = (p * p) / denom;
+        const float cn = lam * c[row + a] + (1.f - lam) * w[a] + r_prev[row + a];
+        const float qa = ra / cn;
+        c[row + a] = cn;
+        r[row + a] = ra;
+        q[row + a] = qa;
+        wq[row + a] = w[a] * qa;
+    }
+}
+
+constexpr int kStateRows = 16;   // rows (features) per block, 4 per wave
+
+// S[n, d, :] <- lam S + v[n, d] r_prev[n, :];  out[n, d] = x + S[n, d, :] . q[n, :] + ymu.
+// q and r_prev of the block's sequence are staged once in LDS; each wave
+// streams whole rows with 16-byte accesses and reduces its dot product with
+// cross-lane shuffles.
+template <bool VEC4>
+__global__ __launch_bounds__(256) void decode_state_kernel(float *__restrict__ S, const float *__restrict__ v,
+                                                           const float *__restrict__ r_prev, const float *__restrict__ q,
+                                                           const float *__restrict__ g, const float *__restrict__ x,
+                                                           const float *__restrict__ ymu, float *__restrict__ out, int D,
+                                                           int A) {
+    extern __shared__ float smem[];
+    float *sq = smem;
+    float *srp = smem + A;
+    const size_t n = blockIdx.x;
+    for (int a = threadIdx.x; a < A; a += 256) {
+        sq[a] = q[n * A + a];
+        srp[a] = r_prev[n * A + a];
+    }
+    __syncthreads();
+    const float lam = __expf(g[0]);
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int d0 = blockIdx.y * kStateRows;
+    for (int i = wave; i < kStateRows; i += 4) {
+        const int d = d0 + i;
+        if (d >= D) break;
+        float *Sr = S + (n * D + d) * static_cast<size_t>(A);
+        const float vd = v[n * D + d];
+        float acc = 0.f;
+        if (VEC4) {
+            const int A4 = A / 4;
+            float4 *S4 = reinterpret_cast<float4 *>(Sr);
+            const float4 *q4 = reinterpret_cast<const float4 *>(sq);
+            const float4 *p4 = reinterpret_cast<const float4 *>(srp);
+#pragma unroll 4
+            for (int j = lane; j < A4; j += kWave) {
+                float4 s = S4[j];
+                const float4 rp = p4[j], qq = q4[j];
+                s.x = lam * s.x + vd * rp.x;
+                s.y = lam * s.y + vd * rp.y;
+                s.z = lam * s.z + vd * rp.z;
+                s.w = lam * s.w + vd * rp.w;
+                S4[j] = s;
+                acc += s.x * qq.x + s.y * qq.y + s.z * qq.z + s.w * qq.w;
+            }
+        } else {
+            for (int a = lane; a < A; a += kWave) {
+                const float s = lam * Sr[a] + vd * srp[a];
+                Sr[a] = s;
+                acc += s * sq[a];
+            }
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) out[n * D + d] = x[n * D + d] + acc + ymu[n * D + d];
+    }
+}
+
+}  // namespace ulm
+
+using namespace ulm;
+
+extern "C" int ulm_decode_pre(const float *x, const float *norm_w, const float *conv_w, float *conv_buf, float *h,
+                              float *u, int N, int D, int Kc, float norm_eps, void *stream) {
+    ULM_REQUIRE(N > 0 && D > 0 && Kc >= 1, "ulm_decode_pre: bad sizes N=%d D=%d Kc=%d", N, D, Kc);
+    ULM_REQUIRE(x && norm_w && conv_w && h && u && (Kc == 1 || conv_buf), "ulm_decode_pre: null pointer");
+    decode_pre_kernel<<<dim3(N), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(x, norm_w, conv_w, conv_buf, h, u,
+                                                                                   D, Kc, norm_eps);
+    return check_launch("decode_pre_kernel");
+}
+
+extern "C" int ulm_decode_addr(const float *pre, const float *bias, const float *log_eps, const float *w,
+                               const float *g, const float *r_prev, float *c, float *r, float *q, float *wq, int N,
+                               int A, void *stream) {
+    ULM_REQUIRE(N > 0 && A > 0, "ulm_decode_addr: bad sizes N=%d A=%d", N, A);
+    ULM_REQUIRE(pre && log_eps && w && g && r_prev && c && r && q && wq, "ulm_decode_addr: null pointer");
+    decode_addr_kernel<<<dim3(N), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(pre, bias, log_eps, w, g, r_prev,
+                                                                                    c, r, q, wq, A);
+    return check_launch("decode_addr_kernel");
+}
+
+extern "C" int ulm_decode_state(float *S, const float *v, const float *r_prev, const float *q, const float *g,
+                                const float *x, const float *ymu, float *out, int N, int D, int A, void *stream) {
+    ULM_REQUIRE(N > 0 && D > 0 && A > 0, "ulm_decode_state: bad sizes N=%d D=%d A=%d", N, D, A);
+    ULM_REQUIRE(A <= 8192, "ulm_decode_state: A=%d exceeds the LDS staging limit 8192", A);
+    ULM_REQUIRE(S && v && r_prev && q && g && x && ymu && out, "ulm_decode_state: null pointer");
+    const dim3 grid(N, (D + kStateRows - 1) / kStateRows);
+    const size_t lds = 2 * static_cast<size_t>(A) * sizeof(float);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool vec = (A % 4 == 0) && (reinterpret_cast<uintptr_t>(S) % 16 == 0);
+    if (vec)
+        decode_state_kernel<true><<<grid, dim3(256), lds, s>>>(S, v, r_prev, q, g, x, ymu, out, D, A);
+    else
+        decode_state_kernel<false><<<grid, dim3(256), lds, s>>>(S, v, r_prev, q, g, x, ymu, out, D, A);
+    return check_launch("decode_state_kernel");
+}

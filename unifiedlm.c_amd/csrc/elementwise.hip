@@ -1,0 +1,41 @@
+// Zero fill and dtype conversion used between the chunked kernels. A fill
+// kernel rather than hipMemsetAsync keeps the calls safe to capture in a
+// HIP graph.
+#include "ulm_common.h"
+
+namespace ulm {
+
+__global__ void fill_zero_kernel(uint4 *p, size_t n16, uint8_t *tail, size_t ntail) {
+    size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t k = i; k < n16; k += stride) p[k] = make_uint4(0, 0, 0, 0);
+    if (i < ntail) tail[i] = 0;
+}
+
+int launch_fill_zero(void *p, size_t bytes, hipStream_t s) {
+    if (bytes == 0) return ULM_OK;
+    size_t n16 = bytes / 16;
+    size_t ntail = bytes - n16 * 16;
+    size_t blocks = (n16 + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    if (blocks == 0) blocks = 1;
+    fill_zero_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(
+        static_cast<uint4 *>(p), n16, static_cast<uint8_t *>(p) + n16 * 16, ntail);
+    return check_launch("fill_zero_kernel");
+}
+
+__global__ void convert_kernel(const void *src, int sdt, void *dst, int ddt, size_t n) {
+    size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t k = i; k < n; k += stride) store_from_f32(dst, k, ddt, load_as_f32(src, k, sdt));
+}
+
+int launch_convert(const void *src, int src_dt, void *dst, int dst_dt, size_t n, hipStream_t s) {
+    if (n == 0) return ULM_OK;
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    convert_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(src, src_dt, dst, dst_dt, n);
+    return check_launch("convert_kernel");
+}
+
+}  // namespace ulm

@@ -1,0 +1,240 @@
+// Per-slot statistics of the fast memory: the decayed evidence scan and its
+// backward. Replaces _fwd_stats_kernel / _bwd_stats_kernel (kernel.py:104-180).
+//
+// Forward, per batch row and slot a:
+//   k_t = r_{t-1} (k_0 = 0),  n_t = lam n_{t-1} + k_t,  c_t = w_a + n_t,  q_t = r_t / c_t
+// Backward (kernel.py:142-178), walking time in reverse:
+//   dq = dq_f + dq_out, dr_t = dq_t / c_t + dkt_{t+1}, dc = -dq q / c,
+//   dkc_t = dc_t + lam dkc_{t+1}, dkt = dk_f + dkc, dw = sum_t dc,
+//   dg = sum_t (t - tau) [q dq_f + dc (c - w) - k dkt]_t     (any tau; tau = (T-1)/2)
+//
+// Thread layout: a 256-thread block owns 64 slots of one batch row; thread
+// (slot s, segment j) holds 16 consecutive positions of each 64-position chunk,
+// so every global access is a 256-byte row segment. A chunk is scanned in
+// registers per segment and the four segments are joined through LDS
+// (carry_j = lam^16 carry_{j-1} + total_{j-1}). Instead of the full c tensor
+// the forward saves n at every chunk start (B x ceil(T/64) x A); the backward
+// rebuilds c inside each chunk from it.
+#include "ulm_common.h"
+
+namespace ulm {
+
+constexpr int kSeg = 16;      // positions per thread segment
+constexpr int kSlots = 64;    // slots per block
+
+__device__ __forceinline__ float pow_int(float x, int e) {
+    float r = 1.f;
+    for (int i = 0; i < e; ++i) r *= x;
+    return r;
+}
+
+__global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict__ r, const float *__restrict__ w,
+                                                        const float *__restrict__ g, float *__restrict__ q,
+                                                        uint16_t *__restrict__ q16, uint16_t *__restrict__ k16,
+                                                        float *__restrict__ nck, int T, int A, int NT) {
+    __shared__ float tot[4][kSlots];
+    const int s = threadIdx.x % kSlots, j = threadIdx.x / kSlots;
+    const int a = blockIdx.x * kSlots + s;
+    const bool va = a < A;
+    const size_t b = blockIdx.y;
+    const float lam = __expf(g[0]);
+    const float lam16 = pow_int(lam, kSeg);
+    const float wa = va ? w[a] : 1.f;
+    float carry = 0.f;   // n at the position before the chunk
+    for (int n = 0; n < NT; ++n) {
+        const int t0 = n * ULM_CHUNK + j * kSeg;
+        float rv[kSeg], kv[kSeg], nl[kSeg];
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) {
+            const int t = t0 + i;
+            rv[i] = (va && t < T) ? r[(b * T + t) * A + a] : 0.f;
+        }
+        kv[0] = (va && t0 >= 1 && t0 - 1 < T) ? r[(b * T + t0 - 1) * A + a] : 0.f;
+#pragma unroll
+        for (int i = 1; i < kSeg; ++i) kv[i] = rv[i - 1];
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) {
+            acc = lam * acc + kv[i];
+            nl[i] = acc;
+        }
+        tot[j][s] = acc;
+        __syncthreads();
+        float cj = carry;
+        for (int m = 0; m < j; ++m) cj = lam16 * cj + tot[m][s];
+        float pw = lam;
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) {
+            const int t = t0 + i;
+            const float ct = wa + (pw * cj + nl[i]);
+            pw *= lam;
+            if (va && t < T) {
+                const size_t o = (b * T + t) * A + a;
+                const float qt = rv[i] / ct;
+                q[o] = qt;
+                q16[o] = f32_to_bf16_bits(qt);
+                k16[o] = f32_to_bf16_bits(kv[i]);
+            }
+        }
+        if (j == 0 && va) nck[(b * NT + n) * A + a] = carry;
+        float nc = carry;
+        for (int m = 0; m < 4; ++m) nc = lam16 * nc + tot[m][s];
+        carry = nc;
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict__ dqf, const float *__restrict__ dqo,
+                                                        const float *__restrict__ q, const float *__restrict__ r,
+                                                        const float *__restrict__ nck, const float *__restrict__ w,
+                                                        const float *__restrict__ g, const float *__restrict__ dkf,
+                                                        float *__restrict__ dr, float *__restrict__ dw_part,
+                                                        double *__restrict__ dg_part, int T, int A, int NT) {
+    __shared__ float tot[4][kSlots];
+    __shared__ float first_dkt[4][kSlots];
+    __shared__ float dw_sh[4][kSlots];
+    __shared__ double dg_sh[4];
+    const int s = threadIdx.x % kSlots, j = threadIdx.x / kSlots;
+    const int a = blockIdx.x * kSlots + s;
+    const bool va = a < A;
+    const size_t b = blockIdx.y;
+    const float lam = __expf(g[0]);
+    const float lam16 = pow_int(lam, kSeg);
+    const float wa = va ? w[a] : 1.f;
+    const double tau = 0.5 * (T - 1);
+    float dkc_next = 0.f;   // dkc at the first position after the chunk
+    float dkt_next = 0.f;   // dkt at the first position after the chunk
+    float dw_acc = 0.f;
+    double dg_acc = 0.0;
+    for (int n = NT - 1; n >= 0; --n) {
+        const int t0 = n * ULM_CHUNK + j * kSeg;
+        float rv[kSeg], kv[kSeg], cv[kSeg], dq[kSeg], dc[kSeg], dqfv[kSeg];
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) {
+            const int t = t0 + i;
+            const bool ok = va && t < T;
+            const size_t o = (b * T + t) * A + a;
+            rv[i] = ok ? r[o] : 0.f;
+            dqfv[i] = ok ? dqf[o] : 0.f;
+            dq[i] = dqfv[i] + ((ok && dqo) ? dqo[o] : 0.f);
+        }
+        kv[0] = (va && t0 >= 1 && t0 - 1 < T) ? r[(b * T + t0 - 1) * A + a] : 0.f;
+#pragma unroll
+        for (int i = 1; i < kSeg; ++i) kv[i] = rv[i - 1];
+        // rebuild n (hence c) inside the chunk from its checkpoint
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) {
+            acc = lam * acc + kv[i];
+            cv[i] = acc;
+        }
+        tot[j][s] = acc;
+        __syncthreads();
+        float cj = va ? nck[(b * NT + n) * A + a] : 0.f;
+        for (int m = 0; m < j; ++m) cj = lam16 * cj + tot[m][s];
+        __syncthreads();
+        float pw = lam;
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) {
+            cv[i] = wa + (pw * cj + cv[i]);
+            pw *= lam;
+        }
+        // dc and its reverse decayed scan
+        float rl[kSeg];
+        float racc = 0.f;
+#pragma unroll
+        for (int i = kSeg - 1; i >= 0; --i) {
+            const int t = t0 + i;
+            const float qt = (va && t < T) ? q[(b * T + t) * A + a] : 0.f;
+            dc[i] = -dq[i] * qt / cv[i];
+            racc = dc[i] + lam * racc;
+            rl[i] = racc;
+            rv[i] = qt;   // rv now holds q
+        }
+        tot[j][s] = racc;
+        __syncthreads();
+        float rj = dkc_next;
+        for (int m = 3; m > j; --m) rj = tot[m][s] + lam16 * rj;
+        float dkt[kSeg];
+        float pr = lam;   // lam^(16-i) for i = 15 .. 0
+#pragma unroll
+        for (int i = kSeg - 1; i >= 0; --i) {
+            const int t = t0 + i;
+            const float dkft = (va && t < T) ? dkf[(b * T + t) * A + a] : 0.f;
+            const float dkc = rl[i] + pr * rj;
+            pr *= lam;
+            dkt[i] = dkft + dkc;
+        }
+        first_dkt[j][s] = dkt[0];
+        if (j == 0) tot[0][s] = rl[0] + pow_int(lam, kSeg) * rj;   // dkc at chunk start (rl[0] + lam^16 r_0)
+        __syncthreads();
+        const float after = (j == 3) ? dkt_next : first_dkt[j + 1][s];
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) {
+            const int t = t0 + i;
+            if (va && t < T) {
+                const float nxt = (i + 1 < kSeg) ? dkt[i + 1] : after;
+                dr[(b * T + t) * A + a] = dq[i] / cv[i] + nxt;
+                dw_acc += dc[i];
+                const double pos = static_cast<double>(t) - tau;
+                dg_acc += pos * (static_cast<double>(rv[i] * dqfv[i] + dc[i] * (cv[i] - wa)) -
+                                 static_cast<double>(kv[i] * dkt[i]));
+            }
+        }
+        dkc_next = tot[0][s];
+        dkt_next = first_dkt[0][s];
+        __syncthreads();
+    }
+    dw_sh[j][s] = dw_acc;
+    dg_acc = wave_sum(dg_acc);
+    if (threadIdx.x % kWave == 0) dg_sh[threadIdx.x / kWave] = dg_acc;
+    __syncthreads();
+    if (j == 0 && va) dw_part[b * A + a] = dw_sh[0][s] + dw_sh[1][s] + dw_sh[2][s] + dw_sh[3][s];
+    if (threadIdx.x == 0) dg_part[b * gridDim.x + blockIdx.x] = dg_sh[0] + dg_sh[1] + dg_sh[2] + dg_sh[3];
+}
+
+// dw[a] = sum_b dw_part[b, a]; dg = sum of all dg partials, in a fixed order.
+__global__ __launch_bounds__(256) void stats_reduce_kernel(const float *__restrict__ dw_part,
+                                                           const double *__restrict__ dg_part, float *__restrict__ dw,
+                                                           float *__restrict__ dg, int B, int A, int ndg) {
+    const int a = blockIdx.x * 256 + threadIdx.x;
+    if (a < A) {
+        float s = 0.f;
+        for (int b = 0; b < B; ++b) s += dw_part[static_cast<size_t>(b) * A + a];
+        dw[a] = s;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        double s = 0.0;
+        for (int k = 0; k < ndg; ++k) s += dg_part[k];
+        dg[0] = static_cast<float>(s);
+    }
+}
+
+int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16, uint16_t *k16,
+                     float *nck, int B, int T, int A, hipStream_t s) {
+    const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
+    fwd_stats_kernel<<<dim3((A + kSlots - 1) / kSlots, B), 256, 0, s>>>(r, w, g, q, q16, k16, nck, T, A, NT);
+    return check_launch("fwd_stats_kernel");
+}
+
+size_t bwd_stats_partial_bytes(int B, int A) {
+    const size_t nb = (A + kSlots - 1) / kSlots;
+    return align_up(static_cast<size_t>(B) * A * sizeof(float), 256) + align_up(B * nb * sizeof(double), 256);
+}
+
+int launch_bwd_stats(const float *dqf, const float *dqo, const float *q, const float *r, const float *nck,
+                     const float *w, const float *g, const float *dkf, float *dr, float *dw, float *dg, void *part,
+                     int B, int T, int A, hipStream_t s) {
+    const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
+    const int nb = (A + kSlots - 1) / kSlots;
+    float *dw_part = static_cast<float *>(part);
+    double *dg_part = reinterpret_cast<double *>(static_cast<char *>(part) +
+                                                 align_up(static_cast<size_t>(B) * A * sizeof(float), 256));
+    bwd_stats_kernel<<<dim3(nb, B), 256, 0, s>>>(dqf, dqo, q, r, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT);
+    int st = check_launch("bwd_stats_kernel");
+    if (st) return st;
+    stats_reduce_kernel<<<(A + 255) / 256, 256, 0, s>>>(dw_part, dg_part, dw, dg, B, A, B * nb);
+    return check_launch("stats_reduce_kernel");
+}
+
+}  // namespace ulm

@@ -1,0 +1,224 @@
+"""UnifiedBlock's fast memory on MI355X: the operator surface of the reference's
+kernel.py (kernel.py:1-15, 199-238), computed by hand-written gfx950 HIP
+kernels in libulm_fm.so.
+
+unified_memory(r, v, g, w) -> (q, fast), for every batch row and position t:
+
+    k_t    = r_{t-1}                                     (k_0 = 0, write address)
+    c_t    = w + sum_{s<=t} lam^(t-s) k_s                (slot evidence mass, lam = exp(g))
+    q_t    = r_t / c_t
+    fast_t = sum_{s<=t} lam^(t-s) (q_t . k_s) v_s
+
+Matmul operands are bf16 with fp32 accumulation and an fp32 chunk state kept
+on chip; c, q and all their gradients are fp32, as in the reference.
+
+Besides the operator this module exposes the relu^2 slot address
+(model.py:70-72) as an autograd Function and the three per-token decode
+kernels used by UnifiedBlock.step.
+"""
+import torch
+
+import ulm_native as nat
+from ulm_native import call, ptr
+
+CHUNK = 64          # kernel.py:20
+
+
+def _check_float(name, t):
+    if not torch.is_floating_point(t):
+        raise TypeError(f"{name} must be a floating tensor, got {t.dtype}")
+
+
+def _check_fm(r, v, g, w):
+    for name, t in (("r", r), ("v", v), ("g", g), ("w", w)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a tensor")
+        _check_float(name, t)
+    if r.dim() != 3 or v.dim() != 3:
+        raise ValueError(f"r and v must be (B, T, A) and (B, T, D); got {tuple(r.shape)} and {tuple(v.shape)}")
+    B, T, A = r.shape
+    if v.shape[:2] != r.shape[:2]:
+        raise ValueError(f"r {tuple(r.shape)} and v {tuple(v.shape)} disagree on (B, T)")
+    if B == 0 or T == 0 or A == 0 or v.shape[2] == 0:
+        raise ValueError(f"empty input: r {tuple(r.shape)}, v {tuple(v.shape)}")
+    if w.shape != (A,):
+        raise ValueError(f"w must have shape ({A},), got {tuple(w.shape)}")
+    if g.numel() != 1:
+        raise ValueError(f"g must hold one scalar, got shape {tuple(g.shape)}")
+    nat.dtype_code(v.dtype)
+    nat.require_device(r, v, g, w)
+
+
+class UnifiedMemory(torch.autograd.Function):
+    """Replaces kernel.py:199-233. Saves r, v16, g, w, q, q16, k16 and the
+    per-chunk evidence checkpoints (instead of the full c tensor)."""
+
+    @staticmethod
+    def forward(ctx, r, v, g, w):
+        _check_fm(r, v, g, w)
+        B, T, A = r.shape
+        D = v.shape[-1]
+        r32 = r.float().contiguous()
+        v16 = v.to(torch.bfloat16).contiguous()
+        g1 = g.float().reshape(1).contiguous()
+        w32 = w.float().contiguous()
+        nt = (T + CHUNK - 1) // CHUNK
+        q = torch.empty_like(r32)
+        fast = torch.empty(B, T, D, device=r.device, dtype=v.dtype)
+        q16 = torch.empty(B, T, A, device=r.device, dtype=torch.bfloat16)
+        k16 = torch.empty_like(q16)
+        nck = torch.empty(B, nt, A, device=r.device, dtype=torch.float32)
+        fdt = nat.dtype_code(v.dtype)
+        ws_bytes = nat.lib().ulm_fm_fwd_workspace_bytes(B, T, A, D, fdt)
+        ws = torch.empty(max(ws_bytes, 1), device=r.device, dtype=torch.uint8)
+        call("ulm_fm_fwd", ptr(r32), ptr(v16), ptr(g1), ptr(w32), ptr(q), ptr(fast), fdt, ptr(q16), ptr(k16),
+             ptr(nck), ptr(ws), ws_bytes, B, T, A, D, nat.stream_of(r))
+        ctx.save_for_backward(r32, v16, g1, w32, q, q16, k16, nck)
+        ctx.g_shape = g.shape
+        return q, fast
+
+    @staticmethod
+    def backward(ctx, dq_out, dfast):
+        r, v16, g1, w, q, q16, k16, nck = ctx.saved_tensors
+        B, T, A = r.shape
+        D = v16.shape[-1]
+        if dfast is None:
+            dfast = torch.zeros(B, T, D, device=r.device, dtype=torch.float32)
+        nat.dtype_code(dfast.dtype)
+        dfast = dfast.contiguous()
+        dqo = dq_out.float().contiguous() if dq_out is not None else None
+        dr = torch.empty_like(r)
+        dv = torch.empty(B, T, D, device=r.device, dtype=dfast.dtype)
+        dg = torch.empty(1, device=r.device, dtype=torch.float32)
+        dw = torch.empty(A, device=r.device, dtype=torch.float32)
+        ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D)
+        ws = torch.empty(ws_bytes, device=r.device, dtype=torch.uint8)
+        ddt = nat.dtype_code(dfast.dtype)
+        call("ulm_fm_bwd", ptr(r), ptr(v16), ptr(g1), ptr(w), ptr(q), ptr(q16), ptr(k16), ptr(nck), ptr(dfast), ddt,
+             ptr(dqo), ptr(dr), ptr(dv), ddt, ptr(dg), ptr(dw), ptr(ws), ws_bytes, B, T, A, D, nat.stream_of(r))
+        return dr, dv, dg.reshape(ctx.g_shape), dw
+
+
+def unified_memory(r, v, g, w):
+    """r: (B,T,M) read addresses, v: (B,T,D) values, g: scalar log decay, w: (M,) prior mass."""
+    return UnifiedMemory.apply(r, v, g, w)
+
+
+def la(a, b, c, g, reverse=False):
+    """o_t = sum_{s<=t} lam^(t-s) (a_t . b_s) c_s (s>=t when reverse), fp32 output.
+    The chunked building block (kernel.py:183-196); a, b (B,T,K), c (B,T,V)."""
+    nat.require_device(a, b, c, g)
+    a16, b16, c16 = (x.to(torch.bfloat16).contiguous() for x in (a, b, c))
+    B, T, K = a16.shape
+    V = c16.shape[-1]
+    if b16.shape != a16.shape or c16.shape[:2] != a16.shape[:2]:
+        raise ValueError("la: a, b must be (B,T,K) and c (B,T,V)")
+    g1 = g.float().reshape(1).contiguous()
+    out = torch.zeros(B, T, V, device=a.device, dtype=torch.float32)
+    call("ulm_la", ptr(a16), ptr(b16), ptr(c16), ptr(g1), ptr(out), B, T, K, V, int(reverse), nat.stream_of(a))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# relu^2 slot address (model.py:70-72)
+
+class Relu2Address(torch.autograd.Function):
+    """r = z / (exp(clamp(log_eps,-10,10)) + sum_a z), z = relu(pre + bias)^2."""
+
+    @staticmethod
+    def forward(ctx, pre, bias, log_eps):
+        _check_float("pre", pre)
+        if pre.dim() < 1 or pre.numel() == 0:
+            raise ValueError(f"pre must be non-empty (..., A), got {tuple(pre.shape)}")
+        A = pre.shape[-1]
+        if bias is not None and bias.shape != (A,):
+            raise ValueError(f"bias must have shape ({A},), got {tuple(bias.shape)}")
+        if log_eps.numel() != 1:
+            raise ValueError("log_eps must hold one scalar")
+        nat.require_device(pre, bias, log_eps)
+        pdt = nat.dtype_code(pre.dtype)
+        pre_c = pre.contiguous()
+        b32 = bias.float().contiguous() if bias is not None else None
+        le = log_eps.float().reshape(1).contiguous()
+        M = pre_c.numel() // A
+        r = torch.empty(pre.shape, device=pre.device, dtype=torch.float32)
+        denom = torch.empty(M, device=pre.device, dtype=torch.float32)
+        call("ulm_addr_fwd", ptr(pre_c), pdt, ptr(b32), ptr(le), ptr(r), ptr(denom), M, A, nat.stream_of(pre))
+        ctx.save_for_backward(pre_c, b32, le, r, denom)
+        ctx.has_bias = bias is not None
+        ctx.le_shape = log_eps.shape
+        return r
+
+    @staticmethod
+    def backward(ctx, dr):
+        pre, b32, le, r, denom = ctx.saved_tensors
+        A = pre.shape[-1]
+        M = pre.numel() // A
+        dr = dr.float().contiguous()
+        dpre = torch.empty_like(pre)
+        dbias = torch.empty(A, device=pre.device, dtype=torch.float32) if ctx.has_bias else None
+        dle = torch.empty(1, device=pre.device, dtype=torch.float32)
+        ws_bytes = nat.lib().ulm_addr_bwd_workspace_bytes(M, A)
+        ws = torch.empty(ws_bytes, device=pre.device, dtype=torch.uint8)
+        call("ulm_addr_bwd", ptr(pre), nat.dtype_code(pre.dtype), ptr(b32), ptr(le), ptr(r), ptr(denom), ptr(dr),
+             ptr(dpre), ptr(dbias), ptr(dle), ptr(ws), ws_bytes, M, A, nat.stream_of(pre))
+        return dpre, dbias, dle.reshape(ctx.le_shape)
+
+
+def relu2_address(pre, bias, log_eps):
+    """The slot address of model.py:70-72 from pre = K u (bias added in fp32 inside)."""
+    return Relu2Address.apply(pre, bias, log_eps)
+
+
+# ---------------------------------------------------------------------------
+# per-token decode (model.py:96-111), N sequences at once, fp32
+
+def _f32c(t):
+    if t.dtype != torch.float32 or not t.is_contiguous():
+        raise ValueError("decode tensors must be contiguous float32")
+    return t
+
+
+def decode_pre(x, norm_w, conv_w, conv_buf, norm_eps):
+    """h = RMSNorm(x), u = causal conv over [conv_buf, h]; conv_buf shifted in place."""
+    N, D = x.shape
+    Kc = conv_w.shape[-1]
+    nat.require_device(x, norm_w, conv_w, conv_buf)
+    h = torch.empty_like(x)
+    u = torch.empty_like(x)
+    call("ulm_decode_pre", ptr(_f32c(x)), ptr(_f32c(norm_w)), ptr(_f32c(conv_w)), ptr(_f32c(conv_buf)), ptr(h), ptr(u),
+         N, D, Kc, float(norm_eps), nat.stream_of(x))
+    return h, u
+
+
+def decode_addr(pre, bias, log_eps, w, g, r_prev, c):
+    """r = relu^2 address, c <- lam c + (1-lam) w + r_prev (in place), q = r / c.
+    Returns (r, q, w*q)."""
+    N, A = pre.shape
+    nat.require_device(pre, bias, log_eps, w, g, r_prev, c)
+    r = torch.empty_like(pre)
+    q = torch.empty_like(pre)
+    wq = torch.empty_like(pre)
+    call("ulm_decode_addr", ptr(_f32c(pre)), ptr(None if bias is None else _f32c(bias)), ptr(_f32c(log_eps)),
+         ptr(_f32c(w)), ptr(_f32c(g)), ptr(_f32c(r_prev)), ptr(_f32c(c)), ptr(r), ptr(q), ptr(wq), N, A,
+         nat.stream_of(pre))
+    return r, q, wq
+
+
+def decode_state(S, v, r_prev, q, g, x, ymu, out=None):
+    """S <- lam S + v r_prev^T (in place); returns x + S q + ymu."""
+    N, D, A = S.shape
+    nat.require_device(S, v, r_prev, q, g, x, ymu)
+    out = torch.empty_like(x) if out is None else out
+    call("ulm_decode_state", ptr(_f32c(S)), ptr(_f32c(v)), ptr(_f32c(r_prev)), ptr(_f32c(q)), ptr(_f32c(g)),
+         ptr(_f32c(x)), ptr(_f32c(ymu)), ptr(out), N, D, A, nat.stream_of(S))
+    return out
+
+
+def probe_mfma(a, b):
+    """D = A B (A 32x16, B 16x32, bf16) through the kernels' MFMA operand layout."""
+    a16 = a.to(torch.bfloat16).contiguous()
+    b16 = b.to(torch.bfloat16).contiguous()
+    d = torch.empty(32, 32, device=a.device, dtype=torch.float32)
+    call("ulm_probe_mfma", ptr(a16), ptr(b16), ptr(d), nat.stream_of(a))
+    return d

@@ -1,0 +1,94 @@
+"""ctypes binding of libulm_fm.so, the HIP/CDNA4 fast-memory library.
+
+The library is built in place by ``build.py`` (hipcc, gfx950). There is no
+fallback: if the library is missing, loading raises, and every operator
+requires its tensors on a ROCm device.
+"""
+import ctypes
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libulm_fm.so")
+
+ULM_OK, ULM_ERR_INVALID, ULM_ERR_UNSUPPORTED, ULM_ERR_LAUNCH = 0, 1, 2, 3
+ULM_F32, ULM_BF16, ULM_F16 = 0, 1, 2
+DTYPE_CODE = {torch.float32: ULM_F32, torch.bfloat16: ULM_BF16, torch.float16: ULM_F16}
+
+P, I, SZ, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_float
+
+# name -> (restype, argtypes); must match include/ulm_fm.h
+SIGNATURES = {
+    "ulm_abi_version": (I, []),
+    "ulm_last_error": (ctypes.c_char_p, []),
+    "ulm_fm_fwd_workspace_bytes": (SZ, [I, I, I, I, I]),
+    "ulm_fm_fwd": (I, [P, P, P, P, P, P, I, P, P, P, P, SZ, I, I, I, I, P]),
+    "ulm_fm_bwd_workspace_bytes": (SZ, [I, I, I, I]),
+    "ulm_fm_bwd": (I, [P, P, P, P, P, P, P, P, P, I, P, P, P, I, P, P, P, SZ, I, I, I, I, P]),
+    "ulm_la": (I, [P, P, P, P, P, I, I, I, I, I, P]),
+    "ulm_addr_fwd": (I, [P, I, P, P, P, P, I, I, P]),
+    "ulm_addr_bwd_workspace_bytes": (SZ, [I, I]),
+    "ulm_addr_bwd": (I, [P, I, P, P, P, P, P, P, P, P, P, SZ, I, I, P]),
+    "ulm_decode_pre": (I, [P, P, P, P, P, P, I, I, I, F, P]),
+    "ulm_decode_addr": (I, [P, P, P, P, P, P, P, P, P, P, I, I, P]),
+    "ulm_decode_state": (I, [P, P, P, P, P, P, P, P, I, I, I, P]),
+    "ulm_probe_mfma": (I, [P, P, P, P]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises if it was never built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python unifiedlm.c_amd/build.py` "
+                               "(the fast-memory operators have no CPU or PyTorch fallback)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def call(name, *args):
+    """Calls an entry point and raises RuntimeError on a nonzero status."""
+    status = getattr(lib(), name)(*args)
+    if status != ULM_OK:
+        msg = lib().ulm_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed with status {status}: {msg}")
+
+
+def ptr(t):
+    """Device pointer of a tensor, or NULL for None."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def require_device(*tensors):
+    """All tensors on one ROCm device; raises otherwise (no CPU fallback)."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError("the fast-memory operators run only on a ROCm GPU; got a tensor on "
+                               f"{t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def dtype_code(dtype):
+    if dtype not in DTYPE_CODE:
+        raise TypeError(f"unsupported dtype {dtype}; expected float32, bfloat16 or float16")
+    return DTYPE_CODE[dtype]

@@ -1,0 +1,233 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X fast-memory path.
+
+One step = the fast-memory forward + backward (unified_memory and its
+backward) of all 12 UnifiedBlocks of the 110M shape on one synthetic batch:
+B=16, T=1024, D=768, A=3072 slots, chunk 64, v/dfast in bf16, r/q/stats fp32.
+Inputs are resident in HBM before the timed region. Prints one JSON line:
+
+  value      Mtok/s = B*T / step time
+  roofline   the chunked MFMA kernel (la_kernel): algorithmic flops per launch
+             (B*T*(4*K*V + 2*64*(K+V))) over its average launch time, measured
+             with HIP events on its own stream over the timed steps, against
+             the 2516.6 TFLOP/s dense bf16 peak
+  cpu_baseline  the oracle's chunked PyTorch form on the host cores (fp32,
+             fwd+bwd of one block at B=1, T=1024), scaled to the 12-block step
+  decode     batched recurrent decode at the 110M shape: 256 sequences, 12
+             blocks, fp32 state (29 GB); 512 prefill positions then greedy
+             steps; GB/s of the algorithmic bytes per step against 8 TB/s
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--decode-steps N]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "unifiedlm.c_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "fast-memory fwd+bwd Mtokens/s at 110M shape (% bf16 MFMA peak); decode GB/s"
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_HBM_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "la_kernel_traffic.json")
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=5)
+    p.add_argument("--warmup", type=int, default=2)
+    p.add_argument("--shape", default="110M")
+    p.add_argument("--decode-steps", type=int, default=256)
+    p.add_argument("--prefill", type=int, default=512)
+    p.add_argument("--decode-seqs", type=int, default=256)
+    p.add_argument("--no-decode", action="store_true")
+    p.add_argument("--no-cpu", action="store_true")
+    return p.parse_args()
+
+
+def bench_training(torch, args):
+    import kernel
+    import ulm_native
+    import workloads
+    cfg = workloads.SHAPES[args.shape]
+    B, T, D, A, L = cfg["B"], cfg["T"], cfg["D"], cfg["A"], cfg["blocks"]
+    dev = torch.device("cuda:0")
+    log(f"training workload {args.shape}: B={B} T={T} D={D} A={A} blocks={L}")
+    blocks = []
+    for l in range(L):
+        r, v, g, w = workloads.block_inputs(B, T, D, A, seed=1000 + l, device=dev, v_dtype=torch.bfloat16)
+        blocks.append([t.requires_grad_(True) for t in (r, v, g, w)])
+    gen = torch.Generator(device=dev).manual_seed(5)
+    dq_up = (torch.randn(B, T, A, device=dev, generator=gen) * 0.01).contiguous()
+    df_up = torch.randn(B, T, D, device=dev, generator=gen).to(torch.bfloat16)
+
+    def step():
+        outs = [kernel.unified_memory(*blk) for blk in blocks]
+        for blk, (q, fast) in zip(reversed(blocks), reversed(outs)):
+            torch.autograd.grad((q, fast), blk, (dq_up, df_up))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    with ulm_native.LaTimer(max_launches=4 * L * args.steps + 16) as timer:
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    la_ms = timer.total_ms / max(timer.launches, 1)
+    la_flops = workloads.la_flops(B, T, A, D)
+    achieved = la_flops / (la_ms * 1e-3) / 1e12
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+    ftok = 4 * la_flops / (B * T)
+    path_tflops = ftok * L * B * T / (ms_step * 1e-3) / 1e12
+    log(f"step {ms_step:.2f} ms, la_kernel {la_ms:.3f} ms x {timer.launches} launches, {achieved:.1f} TFLOP/s")
+    return dict(B=B, T=T, D=D, A=A, L=L, ms_step=ms_step, value=B * T / (ms_step * 1e-3) / 1e6,
+                roofline={"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                          "kernel": "la_kernel", "flops_per_launch": la_flops,
+                          "avg_launch_ms": round(la_ms, 4), "launches_timed": timer.launches},
+                path_tflops=path_tflops)
+
+
+def bench_cpu_baseline(torch, train):
+    """The oracle's chunked PyTorch form, fwd+bwd of one block at B=1, fp32."""
+    from oracle import fastmem as fm
+    import workloads
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    T, D, A, L = train["T"], train["D"], train["A"], train["L"]
+    r, v, g, w = workloads.block_inputs(1, T, D, A, seed=1000, device="cpu", v_dtype=torch.float32)
+    leaves = [t.detach().requires_grad_(True) for t in (r, v, g, w)]
+    dq = torch.randn(1, T, A) * 0.01
+    df = torch.randn(1, T, D)
+
+    def run():
+        q, fast = fm.fast_memory(*leaves, form="chunked", chunk=64)
+        torch.autograd.grad((q, fast), leaves, (dq, df))
+
+    run()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t_block = sorted(times)[1]
+    value = T / (t_block * L) / 1e6   # Mtok/s of the 12-block fwd+bwd
+    cpu = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
+    log(f"cpu baseline: {t_block * 1e3:.1f} ms per block (B=1), {threads} threads, {cpu}")
+    return {"value": round(value, 6), "unit": "Mtok/s", "cores": threads, "kind": "port",
+            "sample": f"oracle chunked_fast_memory fp32 fwd+bwd, one block at B=1 T={T} D={D} A={A}, "
+                      f"median of 3 after 1 warm-up ({t_block * 1e3:.1f} ms), scaled to {L} blocks per token",
+            "cpu_model": cpu}
+
+
+def bench_decode(torch, args):
+    from model import ModelArgs, UnifiedLM
+    import workloads
+    c = workloads.DECODE_110M
+    N, D, A, L, V = args.decode_seqs, c["D"], c["A"], c["blocks"], c["vocab"]
+    dev = torch.device("cuda:0")
+    log(f"decode workload: N={N} D={D} A={A} blocks={L} vocab={V} prefill={args.prefill} steps={args.decode_steps}")
+    torch.manual_seed(0)
+    model = UnifiedLM(ModelArgs(dim=D, n_layers=L, hidden_dim=A, vocab_size=V, max_seq_len=1024))
+    workloads.init_decode_model(model, seed=42)
+    model = model.to(dev).eval()
+    gen = torch.Generator(device=dev).manual_seed(3)
+    prompt = torch.randint(0, V, (N, args.prefill), device=dev, generator=gen)
+    states = model.init_states(N, dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits = None
+    for t in range(args.prefill):
+        logits = model.step(prompt[:, t], states)
+        if t % 128 == 127:
+            torch.cuda.synchronize()
+            log(f"  prefill {t + 1}/{args.prefill}")
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    nxt = logits.argmax(-1)
+    for i in range(args.decode_steps):
+        logits = model.step(nxt, states)
+        nxt = logits.argmax(-1)
+        if i % 64 == 63:
+            torch.cuda.synchronize()
+            log(f"  decode {i + 1}/{args.decode_steps}")
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    bytes_step = workloads.decode_bytes_per_step(N, L, A, D, V)
+    step_ms = (t2 - t1) * 1e3 / max(args.decode_steps, 1)
+    pre_ms = (t1 - t0) * 1e3 / max(args.prefill, 1)
+    gbps = bytes_step / (step_ms * 1e-3) / 1e9
+    log(f"decode {step_ms:.2f} ms/step, {gbps:.0f} GB/s; prefill {pre_ms:.2f} ms/position")
+    return {"metric": "decode GB/s", "value": round(gbps, 1), "unit": "GB/s", "ms_per_step": round(step_ms, 3),
+            "tok_per_s": round(N / (step_ms * 1e-3), 1), "prefill_ms_per_position": round(pre_ms, 3),
+            "prefill_GBps": round(bytes_step / (pre_ms * 1e-3) / 1e9, 1), "bytes_per_step": bytes_step,
+            "state_GB": round(N * L * D * A * 4 / 1e9, 2),
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None},
+            "config": {"N": N, "D": D, "A": A, "blocks": L, "vocab": V, "prefill": args.prefill,
+                       "steps": args.decode_steps}}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "the fast-memory path shards by sequence with no communication for decode and a DDP "
+              "all-reduce for training, which is not built here.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    train = bench_training(torch, args)
+    cpu = None if args.no_cpu else bench_cpu_baseline(torch, train)
+    decode = None if args.no_decode else bench_decode(torch, args)
+    out = {
+        "metric": METRIC,
+        "value": round(train["value"], 4),
+        "unit": "Mtok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(train["ms_step"], 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"fast-memory fwd+bwd, {train['L']} blocks of the {args.shape} shape",
+                   "global_batch": train["B"], "seq_len": train["T"], "dim": train["D"], "slots": train["A"],
+                   "blocks": train["L"], "chunk": 64, "parallelism": "single GPU"},
+        "path_tflops": round(train["path_tflops"], 2),
+        "path_frac_bf16_peak": round(train["path_tflops"] / PEAK_BF16_TFLOPS, 4),
+        "roofline": train["roofline"],
+        "cpu_baseline": cpu,
+        "decode": decode,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -142,7 +142,16 @@ int ulm_decode_state(float *S, const float *v, const float *r_prev, const float 
                      int N, int D, int A, void *stream);
 
 /* ------------------------------------------------------------------------
- * Diagnostics. Writes, for lane l of one wave, the operand/result layout of
+ * Diagnostics: HIP-event timing of every chunked-kernel launch (ulm_la and
+ * the launches inside ulm_fm_fwd / ulm_fm_bwd) between start and stop, on
+ * the stream each launch uses. stop() synchronises on the recorded events
+ * and returns the summed kernel time and the number of launches timed.
+ * Process-wide and not thread-safe; no counterpart in the reference
+ * (its timings come from external scripts, docs/kernel.md:55-70). */
+int ulm_la_timer_start(int max_launches);
+int ulm_la_timer_stop(double *total_ms, int *launches);
+
+/* Writes, for lane l of one wave, the operand/result layout of
  * one v_mfma_f32_32x32x16_bf16 on A = a (32x16 row-major), B = b (16x32
  * row-major): d (32x32 row-major) = A B computed through the kernels' own
  * operand-loading helpers. No counterpart in the reference. */

@@ -318,8 +318,36 @@ __global__ __launch_bounds__(kThreads, 1) void la_kernel(const uint16_t *__restr
     }
 }
 
+// ---- launch timer (diagnostics): HIP events around every la_kernel launch
+// while enabled, so a benchmark can read the kernel's own average duration on
+// the stream it runs on. Process-wide and not thread-safe.
+namespace {
+struct LaTimer {
+    bool on = false;
+    int cap = 0, used = 0;
+    hipEvent_t *ev = nullptr;
+};
+LaTimer g_la_timer;
+}  // namespace
+
+static int launch_la_kernel(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B,
+                            int T, int K, int V, bool reverse, hipStream_t s);
+
 int launch_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B, int T, int K,
               int V, bool reverse, hipStream_t s) {
+    const bool timed = g_la_timer.on && g_la_timer.used < g_la_timer.cap;
+    if (timed && hipEventRecord(g_la_timer.ev[2 * g_la_timer.used], s) != hipSuccess) return check_launch("timer");
+    int st = launch_la_kernel(a, b, c, g, out, B, T, K, V, reverse, s);
+    if (st) return st;
+    if (timed) {
+        if (hipEventRecord(g_la_timer.ev[2 * g_la_timer.used + 1], s) != hipSuccess) return check_launch("timer");
+        ++g_la_timer.used;
+    }
+    return ULM_OK;
+}
+
+static int launch_la_kernel(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B,
+                            int T, int K, int V, bool reverse, hipStream_t s) {
     const int NT = (T + C - 1) / C;
     const int nK = (K + KT - 1) / KT, nV = (V + VT - 1) / VT;
     const long long total = static_cast<long long>(B) * nK * nV;
@@ -474,6 +502,42 @@ extern "C" int ulm_fm_bwd(const float *r, const uint16_t *v16, const float *g, c
     ULM_TRY(launch_la(k16, q16, do16, g, dv_acc, B, T, A, D, true, s));
     ULM_TRY(launch_bwd_stats(ws.dqf, dq_out, q, r, n_ckpt, w, g, ws.dkf, dr, dw, dg, ws.part, B, T, A, s));
     if (dv_dtype != ULM_F32) ULM_TRY(launch_convert(dv_acc, ULM_F32, dv, dv_dtype, nd, s));
+    return ULM_OK;
+}
+
+extern "C" int ulm_la_timer_start(int max_launches) {
+    ULM_REQUIRE(max_launches > 0 && max_launches <= 1 << 16, "ulm_la_timer_start: bad capacity %d", max_launches);
+    if (g_la_timer.cap < max_launches) {
+        hipEvent_t *ev = new hipEvent_t[2 * max_launches];
+        for (int i = 0; i < 2 * g_la_timer.cap; ++i) ev[i] = g_la_timer.ev[i];
+        for (int i = 2 * g_la_timer.cap; i < 2 * max_launches; ++i)
+            if (hipEventCreate(&ev[i]) != hipSuccess) {
+                delete[] ev;
+                return check_launch("hipEventCreate");
+            }
+        delete[] g_la_timer.ev;
+        g_la_timer.ev = ev;
+        g_la_timer.cap = max_launches;
+    }
+    g_la_timer.used = 0;
+    g_la_timer.on = true;
+    return ULM_OK;
+}
+
+extern "C" int ulm_la_timer_stop(double *total_ms, int *launches) {
+    ULM_REQUIRE(total_ms && launches, "ulm_la_timer_stop: null pointer");
+    g_la_timer.on = false;
+    double tot = 0.0;
+    for (int i = 0; i < g_la_timer.used; ++i) {
+        if (hipEventSynchronize(g_la_timer.ev[2 * i + 1]) != hipSuccess) return check_launch("hipEventSynchronize");
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, g_la_timer.ev[2 * i], g_la_timer.ev[2 * i + 1]) != hipSuccess)
+            return check_launch("hipEventElapsedTime");
+        tot += ms;
+    }
+    *total_ms = tot;
+    *launches = g_la_timer.used;
+    g_la_timer.used = 0;
     return ULM_OK;
 }
 

@@ -33,8 +33,29 @@ SIGNATURES = {
     "ulm_decode_pre": (I, [P, P, P, P, P, P, I, I, I, F, P]),
     "ulm_decode_addr": (I, [P, P, P, P, P, P, P, P, P, P, I, I, P]),
     "ulm_decode_state": (I, [P, P, P, P, P, P, P, P, I, I, I, P]),
+    "ulm_la_timer_start": (I, [I]),
+    "ulm_la_timer_stop": (I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]),
     "ulm_probe_mfma": (I, [P, P, P, P]),
 }
+
+
+class LaTimer:
+    """Context manager: HIP-event time of every chunked-kernel launch inside it.
+    After exit, ``total_ms`` and ``launches`` hold the sums."""
+
+    def __init__(self, max_launches=4096):
+        self.max_launches = max_launches
+        self.total_ms, self.launches = 0.0, 0
+
+    def __enter__(self):
+        call("ulm_la_timer_start", self.max_launches)
+        return self
+
+    def __exit__(self, *exc):
+        ms, n = ctypes.c_double(), ctypes.c_int()
+        call("ulm_la_timer_stop", ctypes.byref(ms), ctypes.byref(n))
+        self.total_ms, self.launches = ms.value, n.value
+        return False
 
 _lib = None
 

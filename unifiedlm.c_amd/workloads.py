@@ -1,0 +1,81 @@
+"""Seeded synthetic workloads at the benchmark shapes of the fast-memory path.
+
+Block inputs follow one distribution at every shape: h ~ N(0,1) as the block
+input (RMSNorm weight 1 and the identity conv make u = h), key weight
+K ~ N(0, 1/D), key bias 0, eps = 1 (log_eps = 0), value weight ~ N(0, 1/D),
+prior w = 4, one decay lam = sigmoid(N(3, 0.5)) per block, mu ~ N(0, 0.02^2)
+(0.02 read as a standard deviation). The relu^2 addresses then come out
+about half zero with row sums below 1.
+"""
+import math
+
+import torch
+
+SHAPES = {
+    "260K": dict(B=8, T=512, D=64, A=128, blocks=5),
+    "15M": dict(B=32, T=256, D=288, A=1152, blocks=1),
+    "42M": dict(B=16, T=1024, D=512, A=2048, blocks=1),
+    "110M": dict(B=16, T=1024, D=768, A=3072, blocks=12),
+}
+DECODE_110M = dict(N=256, D=768, A=3072, blocks=12, vocab=32000, prefill=512, steps=256)
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def block_decay(seed):
+    """lam = sigmoid(x), x ~ N(3, 0.5)."""
+    return torch.sigmoid(3.0 + 0.5 * torch.randn((), generator=_gen(seed), dtype=torch.float64)).item()
+
+
+def block_inputs(B, T, D, A, seed, device="cuda", v_dtype=torch.float32):
+    """(r, v, g, w) of one block: r fp32 (B,T,A), v (B,T,D) in v_dtype, g 0-d fp32, w (A,) fp32."""
+    gen = _gen(seed)
+    h = torch.randn(B, T, D, generator=gen)
+    K = torch.randn(A, D, generator=gen) / math.sqrt(D)
+    Wv = torch.randn(D, D, generator=gen) / math.sqrt(D)
+    h, K, Wv = h.to(device), K.to(device), Wv.to(device)
+    z = torch.relu(h @ K.t()).square()
+    r = z / (1.0 + z.sum(-1, keepdim=True))
+    v = (h @ Wv.t()).to(v_dtype)
+    lam = block_decay(seed + 7919)
+    g = torch.tensor(math.log(lam), dtype=torch.float32, device=device)
+    w = torch.full((A,), 4.0, dtype=torch.float32, device=device)
+    return r.contiguous(), v.contiguous(), g, w
+
+
+def init_decode_model(model, seed):
+    """Re-draws every block of a UnifiedLM with the benchmark distribution
+    (the default init zeroes the value weight, which would leave S = 0)."""
+    gen = _gen(seed)
+    D = model.params.dim
+    with torch.no_grad():
+        for i, layer in enumerate(model.layers):
+            layer.key.weight.copy_(torch.randn(layer.key.weight.shape, generator=gen) / math.sqrt(D))
+            layer.key.bias.zero_()
+            layer.val.weight.copy_(torch.randn(layer.val.weight.shape, generator=gen) / math.sqrt(D))
+            layer.mu.weight.copy_(torch.randn(layer.mu.weight.shape, generator=gen) * 0.02)
+            layer.log_eps.zero_()
+            layer.log_w.fill_(math.log(4.0))
+            lam = block_decay(seed + 31 * i)
+            layer.log_rate.fill_(math.log(-math.log(lam)))
+    return model
+
+
+def decode_bytes_per_step(N, L, A, D, V, conv_size=4):
+    """Algorithmic HBM bytes of one decode position for N sequences and L blocks, fp32:
+    S read+write, c and r_prev read+write, the conv window read+write, every block's
+    weights once and the tied classifier."""
+    kw = conv_size - 1
+    per_seq_block = 8 * A * D + 16 * A + 8 * kw * D
+    # norm D, conv D*Kc, key A*D + bias A, mu D*A, val D*D, w A, lam, eps
+    weights = 4 * (2 * A * D + D * D + 2 * A + (1 + conv_size) * D + 2)
+    return N * L * per_seq_block + L * weights + 4 * V * D
+
+
+def la_flops(B, T, K, V, chunk=64):
+    """Algorithmic flops of one chunked product o = LA(a, b, c) with keys K and
+    values V: state update 2KV, state read-out 2KV, intra scores 2CK and intra
+    apply 2CV per token, intra tiles counted dense."""
+    return B * T * (4 * K * V + 2 * chunk * (K + V))

@@ -157,6 +157,16 @@ int ulm_la_timer_stop(double *total_ms, int *launches);
  * operand-loading helpers. No counterpart in the reference. */
 int ulm_probe_mfma(const uint16_t *a, const uint16_t *b, float *d, void *stream);
 
+/* LDS transpose read: lane L of one wave addresses elements 4L..4L+3 of the
+ * 256 16-bit values in src (staged in LDS) with ds_read_b64_tr_b16 and writes
+ * the 4 values it receives to dst[4L..4L+3]. */
+int ulm_probe_lds_tr(const uint16_t *src, uint16_t *dst, void *stream);
+
+/* Buffer-to-LDS DMA: lane L loads 16 bytes at byte offset offsets[L] of src
+ * (n floats; offsets past the end read as zero) with buffer_load_dwordx4
+ * ... lds; the 256-float LDS image is copied to dst. */
+int ulm_probe_lds_dma(const float *src, int n, const int *offsets, float *dst, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

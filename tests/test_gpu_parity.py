@@ -183,3 +183,35 @@ def test_parallel_matches_recurrent_on_gpu():
         a = model(x, x)   # logits (B, T, V) with targets
     b = model.forward_recurrent(x)
     assert rel(a, b) < 1e-2
+
+
+def test_lds_transpose_read_layout():
+    """ds_read_b64_tr_b16: lane L of each 16-lane group g receives column L%16
+    of the group's 4 x 16 block: src[64 g + 16 e + L%16], e = 0..3."""
+    import ulm_native as nat
+    say("probe ds_read_b64_tr_b16")
+    src = torch.arange(256, dtype=torch.int32).to(torch.int16).cuda()
+    dst = torch.zeros(256, dtype=torch.int16, device="cuda")
+    nat.call("ulm_probe_lds_tr", nat.ptr(src), nat.ptr(dst), nat.stream_of(src))
+    got = dst.cpu().view(64, 4).long()
+    L = torch.arange(64)[:, None]
+    e = torch.arange(4)[None, :]
+    assert torch.equal(got, 64 * (L // 16) + 16 * e + L % 16)
+
+
+def test_buffer_lds_dma_layout():
+    """buffer_load_dwordx4 ... lds: lane L's 16 bytes land at LDS 16 L; an
+    offset past the buffer end delivers zeros."""
+    import ulm_native as nat
+    say("probe buffer->LDS DMA")
+    n = 256
+    src = torch.arange(n, dtype=torch.float32).cuda()
+    offs = [16 * (63 - L) for L in range(60)] + [4 * n + 1000] * 4
+    offsets = torch.tensor(offs, dtype=torch.int32).cuda()
+    dst = torch.zeros(256, device="cuda")
+    nat.call("ulm_probe_lds_dma", nat.ptr(src), n, nat.ptr(offsets), nat.ptr(dst), nat.stream_of(src))
+    got = dst.cpu().view(64, 4)
+    exp = torch.zeros(64, 4)
+    for L in range(60):
+        exp[L] = torch.arange(4) + 4 * (63 - L)
+    assert torch.equal(got, exp)

@@ -333,11 +333,19 @@ LaTimer g_la_timer;
 static int launch_la_kernel(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B,
                             int T, int K, int V, bool reverse, hipStream_t s);
 
+// la_pipe.hip: the pipelined kernel for aligned shapes
+int launch_la_pipelined(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B,
+                        int T, int K, int V, bool reverse, bool split, hipStream_t s);
+
+// `split` carries the decayed state-update operand as a bf16 hi + lo pair
+// (pipelined kernel only); the backward uses it for dq and dk, the inputs of
+// the positional d/dg identity, whose cancellation amplifies rounding.
 int launch_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B, int T, int K,
-              int V, bool reverse, hipStream_t s) {
+              int V, bool reverse, hipStream_t s, bool split = false) {
     const bool timed = g_la_timer.on && g_la_timer.used < g_la_timer.cap;
     if (timed && hipEventRecord(g_la_timer.ev[2 * g_la_timer.used], s) != hipSuccess) return check_launch("timer");
-    int st = launch_la_kernel(a, b, c, g, out, B, T, K, V, reverse, s);
+    int st = launch_la_pipelined(a, b, c, g, out, B, T, K, V, reverse, split, s);
+    if (st == ULM_ERR_UNSUPPORTED) st = launch_la_kernel(a, b, c, g, out, B, T, K, V, reverse, s);
     if (st) return st;
     if (timed) {
         if (hipEventRecord(g_la_timer.ev[2 * g_la_timer.used + 1], s) != hipSuccess) return check_launch("timer");
@@ -492,10 +500,10 @@ extern "C" int ulm_fm_bwd(const float *r, const uint16_t *v16, const float *g, c
     }
     // dq_f = LA(dfast, v, k): keys = D, values = A
     ULM_TRY(launch_fill_zero(ws.dqf, na * 4, s));
-    ULM_TRY(launch_la(do16, v16, k16, g, ws.dqf, B, T, D, A, false, s));
+    ULM_TRY(launch_la(do16, v16, k16, g, ws.dqf, B, T, D, A, false, s, true));
     // dk_f = LA_rev(v, dfast, q)
     ULM_TRY(launch_fill_zero(ws.dkf, na * 4, s));
-    ULM_TRY(launch_la(v16, do16, q16, g, ws.dkf, B, T, D, A, true, s));
+    ULM_TRY(launch_la(v16, do16, q16, g, ws.dkf, B, T, D, A, true, s, true));
     // dv = LA_rev(k, q, dfast): keys = A, values = D
     float *dv_acc = dv_dtype == ULM_F32 ? static_cast<float *>(dv) : ws.dv32;
     ULM_TRY(launch_fill_zero(dv_acc, nd * 4, s));

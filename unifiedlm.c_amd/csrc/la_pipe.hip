@@ -1,0 +1,366 @@
+// Pipelined chunked linear attention for aligned shapes (K and V multiples of
+// 8): the same product and work split as la_kernel in fm_chunk.hip,
+//
+//   o_t = sum_{s<=t} lam^(t-s) (a_t . b_s) c_s          (time reversed if REV)
+//
+// with each workgroup holding an fp32 state tile H[k0:k0+KT, v0:v0+256] in
+// registers while it walks the chunks of one batch row, and partial outputs
+// over its KT keys added to `out` with fp32 atomics. What differs:
+//
+//  * tiles arrive by buffer -> LDS DMA (buffer_load_dwordx4 ... lds, 16 bytes
+//    per lane), double buffered: chunk n+1 streams into the other stage while
+//    chunk n is computed; rows past T and keys past K read as zero through the
+//    buffer range check, so the loads are branch free;
+//  * a, b and c stay in their natural [time][feature] layout in LDS; the
+//    operands that contract over time (b^T and c for the state update, c for
+//    the intra-chunk product) are read with ds_read_b64_tr_b16, which returns
+//    the transposed 4 x 16 block of each 16-lane group;
+//  * the tail decay lam^(63-j) of the state update is applied to the c
+//    operand in registers (once per chunk) instead of to a transposed b copy;
+//    with SPLIT the decayed c is carried as a bf16 hi + lo pair, so the state
+//    update is exact to fp32 accumulation for the given bf16 inputs;
+//  * synchronisation is explicit: one vmcnt+barrier per chunk for the DMA and
+//    one lgkm+barrier for the shared P tile.
+//
+// LDS rows carry one 16-byte pad so MFMA operand reads of 32 consecutive rows
+// hit distinct banks.
+#include "ulm_common.h"
+
+namespace ulm {
+
+namespace pipe {
+
+constexpr int C = ULM_CHUNK;
+constexpr int VT = 256;          // state columns per workgroup (4 waves x 64)
+constexpr int kThreads = 256;
+constexpr int PITCH_P = C + 8;   // P row pitch in elements
+
+template <int KT>
+struct Cfg {
+    static constexpr int KCH = KT / 8;             // 16-byte chunks per a/b row
+    static constexpr int APITCH = KCH + 1;         // chunk slots per LDS row (one pad)
+    static constexpr int VCH = VT / 8;
+    static constexpr int CPITCH = VCH + 1;
+    static constexpr int A_BYTES = C * APITCH * 16;
+    static constexpr int C_BYTES = C * CPITCH * 16;
+    static constexpr int STAGE = 2 * A_BYTES + C_BYTES;
+    static constexpr int LDS_BYTES = 2 * STAGE;     // dynamic LDS: the two DMA stages
+    // DMA wave-instructions per stage (64 slots of 16 bytes each)
+    static constexpr int A_INSTR = APITCH, C_INSTR = CPITCH;
+    static constexpr int TOTAL_INSTR = 2 * A_INSTR + C_INSTR;
+};
+
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ bf16x8 cat4(bf16x4 lo, bf16x4 hi) {
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+__device__ __forceinline__ bf16x8 ld8(const unsigned char *p) { return *reinterpret_cast<const bf16x8 *>(p); }
+__device__ __forceinline__ bf16x4 ld4(const unsigned char *p) { return *reinterpret_cast<const bf16x4 *>(p); }
+__device__ __forceinline__ bf16x4 ldtr(const unsigned char *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)(p));
+}
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    return static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor words (gfx9 layout: base, stride 0, byte range, dword3).
+__device__ __forceinline__ u32x4 buffer_words(const void *base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+// buffer_load_dwordx4 ... lds: this lane's 16 bytes at byte offset `voff` land in
+// LDS at lds_base + 16 * lane; offsets past the range deliver zeros. Issued as
+// inline asm so the compiler does not track it as a pending LDS write (it would
+// otherwise wait for it before unrelated LDS reads); the kernel orders it
+// itself with vmcnt(0) + barrier before the stage is read. M0 is restored.
+__device__ __forceinline__ void dma16(const void *lds_base, uint32_t voff, u32x4 rs) {
+    const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uint64_t>((lds_void *)lds_base));
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds_addr), "v"(voff), "s"(rs)
+        : "memory");
+}
+
+// wait for this wave's DMA and LDS traffic, then meet the other waves
+__device__ __forceinline__ void sync_all() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void sync_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <bool REV>
+__device__ __forceinline__ int time_pos(int t, int T) { return REV ? T - 1 - t : t; }
+
+template <int KT, bool REV, bool SPLIT>
+__global__ __launch_bounds__(kThreads, 1) void la_pipe_kernel(const uint16_t *__restrict__ A_,
+                                                              const uint16_t *__restrict__ B_,
+                                                              const uint16_t *__restrict__ C_,
+                                                              const float *__restrict__ g, float *__restrict__ out,
+                                                              int T, int K, int V, int NT, int nK, int nV, int total,
+                                                              int Btot) {
+    using G = Cfg<KT>;
+    // The DMA stages live in dynamic LDS; the shared score tile P is a separate object.
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ __align__(16) unsigned char sP[C * PITCH_P * 2];
+
+    int tile = blockIdx.x;
+    if (total % 8 == 0) tile = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;   // XCD-local tiles
+    const int vt = tile % nV;
+    const int kt = (tile / nV) % nK;
+    const int bb = tile / (nV * nK);
+    const int k0 = kt * KT, v0 = vt * VT;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform, kept in an SGPR
+    const int lane = tid % kWave;
+    const int lr = lane % 32, lh = lane / 32;
+    const int p16 = lane % 16, g16 = lane / 16;
+
+    const float gl = g[0];   // lam^k = exp(g k), k >= 0 only
+
+    const uint32_t rowA32 = static_cast<uint32_t>(bb) * static_cast<uint32_t>(T);
+    const u32x4 rsA = buffer_words(A_, static_cast<uint32_t>(static_cast<size_t>(Btot) * T * K * 2));
+    const u32x4 rsB = buffer_words(B_, static_cast<uint32_t>(static_cast<size_t>(Btot) * T * K * 2));
+    const u32x4 rsC = buffer_words(C_, static_cast<uint32_t>(static_cast<size_t>(Btot) * T * V * 2));
+    const __amdgpu_buffer_rsrc_t rsO =
+        __builtin_amdgcn_make_buffer_rsrc(out, 0, static_cast<int>(static_cast<size_t>(Btot) * T * V * 4), 0x00020000);
+    constexpr int OOB = 0x7fffffff;   // DMA slots outside the tensor: the range check delivers zeros
+
+    // ---- DMA of chunk n into stage s. A tile of `pitch` 16-byte slots per row
+    // takes `pitch` wave instructions of 64 slots; wave w issues w, w+4, ...
+    // One loop per tile keeps each buffer descriptor in fixed registers.
+    auto issue_tile = [&](const u32x4 rs, unsigned char *dst0, int pitch, int nch, int col0,
+                          int ncols, int n) {
+        for (int idx = wave; idx < pitch; idx += 4) {
+            const int slot = 64 * idx + lane;
+            const int row = slot / pitch, cc = slot - row * pitch;
+            const int t = n * C + row;
+            const int col = col0 + 8 * cc;
+            const bool ok = (cc < nch) & (t < T) & (col < ncols);
+            // 32-bit unsigned offsets: every tensor is below 2 GB (checked at launch)
+            const uint32_t off = (rowA32 + static_cast<uint32_t>(time_pos<REV>(t, T))) * static_cast<uint32_t>(ncols) * 2u +
+                                 static_cast<uint32_t>(col) * 2u;
+            dma16(dst0 + 1024 * idx, ok ? off : static_cast<uint32_t>(OOB), rs);
+        }
+    };
+    auto issue_chunk = [&](int n, int s) {
+        unsigned char *stage = smem + s * G::STAGE;
+        issue_tile(rsA, stage, G::APITCH, G::KCH, k0, K, n);
+        issue_tile(rsB, stage + G::A_BYTES, G::APITCH, G::KCH, k0, K, n);
+        issue_tile(rsC, stage + 2 * G::A_BYTES, G::CPITCH, G::VCH, v0, V, n);
+    };
+
+    f32x16 H[KT / 32][2];
+#pragma unroll
+    for (int m = 0; m < KT / 32; ++m)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) H[m][nt][r] = 0.f;
+
+    const int wcol = 64 * wave;
+    const int jt = wave >> 1, it = wave & 1;
+    constexpr int AROW = G::APITCH * 16, CROW = G::CPITCH * 16, PROW = PITCH_P * 2;
+    // transposed-read supplier coordinates of this lane (see ds_read_b64_tr_b16)
+    const int tr_row = 8 * (g16 / 2) + p16 / 4;
+    const int tr_col = 16 * (g16 % 2) + 4 * (p16 % 4);
+
+    issue_chunk(0, 0);
+    for (int n = 0; n < NT; ++n) {
+        sync_all();   // chunk n landed in stage n&1; everyone is done with stage (n+1)&1
+        if (n + 1 < NT) issue_chunk(n + 1, (n + 1) & 1);
+        const unsigned char *sa = smem + (n & 1) * G::STAGE;
+        const unsigned char *sb = sa + G::A_BYTES;
+        const unsigned char *sc = sa + 2 * G::A_BYTES;
+
+        // ---- partial scores S^T[j][i] = b_j . a_i over this tile's keys -> P[i][j]
+        {
+            f32x16 s = {};
+#pragma unroll
+            for (int ks = 0; ks < KT / 16; ++ks)
+                s = mfma(ld8(sb + (32 * jt + lr) * AROW + (16 * ks + 8 * lh) * 2),
+                         ld8(sa + (32 * it + lr) * AROW + (16 * ks + 8 * lh) * 2), s);
+            const int i = 32 * it + lr;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int j0 = 32 * jt + 8 * rr + 4 * lh;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int lag = i - (j0 + e);
+                    const float dk = __expf(gl * static_cast<float>(lag));
+                    v[e] = lag >= 0 ? s[4 * rr + e] * dk : 0.f;
+                }
+                uint2 pk;
+                pk.x = pack2(v[0], v[1]);
+                pk.y = pack2(v[2], v[3]);
+                *reinterpret_cast<uint2 *>(sP + i * PROW + j0 * 2) = pk;
+            }
+        }
+
+        // ---- read-out of the carried state: O = diag(lam^(i+1)) a H
+        f32x16 O[2][2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) O[mt][nt][r] = 0.f;
+        if (n > 0) {
+#pragma unroll
+            for (int mh = 0; mh < KT / 32; ++mh) {
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) {
+                    bf16x8 hop[2];
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) hop[nt][e] = static_cast<bf16>(H[mh][nt][8 * hb + e]);
+                    const int kc = 32 * mh + 16 * hb + 4 * lh;
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt) {
+                        const unsigned char *row = sa + (32 * mt + lr) * AROW;
+                        const bf16x8 x = cat4(ld4(row + kc * 2), ld4(row + (kc + 8) * 2));
+#pragma unroll
+                        for (int nt = 0; nt < 2; ++nt) O[mt][nt] = mfma(x, hop[nt], O[mt][nt]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float sc = __expf(gl * static_cast<float>(32 * mt + 8 * (r / 4) + 4 * lh + (r % 4) + 1));
+                    O[mt][0][r] *= sc;
+                    O[mt][1][r] *= sc;
+                }
+        }
+        sync_lds();   // P complete
+
+        // ---- c operand for this wave's columns, contracted over time (transposed reads)
+        bf16x8 cop[2][4];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const unsigned char *p = sc + (16 * ks + tr_row) * CROW + (wcol + 32 * nt + tr_col) * 2;
+                cop[nt][ks] = cat4(ldtr(p), ldtr(p + 4 * CROW));
+            }
+
+        // ---- intra-chunk part: O += P c
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const bf16x8 pp = ld8(sP + (32 * mt + lr) * PROW + (16 * ks + 8 * lh) * 2);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) O[mt][nt] = mfma(pp, cop[nt][ks], O[mt][nt]);
+            }
+
+        // ---- partial output: fp32 buffer atomics. Lanes outside (T, V) are
+        // skipped by an exec mask, never by an out-of-range offset; chunks that
+        // lie wholly inside take the unguarded path (a wave-uniform branch).
+        const bool interior = (n + 1) * C <= T && v0 + VT <= V;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const int col = v0 + wcol + 32 * nt + lr;
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int t = n * C + 32 * mt + 8 * (r / 4) + 4 * lh + (r % 4);
+                    const uint32_t off = ((rowA32 + static_cast<uint32_t>(time_pos<REV>(t, T))) * static_cast<uint32_t>(V) +
+                                          static_cast<uint32_t>(col)) * 4u;
+                    if (interior || ((t < T) & (col < V)))
+                        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(O[mt][nt][r], rsO, static_cast<int>(off), 0, 0);
+                }
+        }
+
+        // ---- state update: H = lam^64 H + b^T (lam^(63-j) c_j)
+        if (n + 1 < NT) {
+            bf16x8 chi[2][4], clo[2][4];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const uint4 x = __builtin_bit_cast(uint4, cop[nt][ks]);
+                    const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+                    uint32_t hi[4], lo[4];
+#pragma unroll
+                    for (int h = 0; h < 4; ++h) {
+                        const int j = 16 * ks + 8 * lh + 2 * h;
+                        const float f0 = __uint_as_float(xs[h] << 16) * __expf(gl * static_cast<float>(C - 1 - j));
+                        const float f1 = __uint_as_float(xs[h] & 0xffff0000u) * __expf(gl * static_cast<float>(C - 2 - j));
+                        hi[h] = pack2(f0, f1);
+                        if (SPLIT)
+                            lo[h] = pack2(f0 - __uint_as_float(hi[h] << 16), f1 - __uint_as_float(hi[h] & 0xffff0000u));
+                    }
+                    chi[nt][ks] = __builtin_bit_cast(bf16x8, make_uint4(hi[0], hi[1], hi[2], hi[3]));
+                    if (SPLIT) clo[nt][ks] = __builtin_bit_cast(bf16x8, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+                }
+            const float dC = __expf(gl * static_cast<float>(C));
+#pragma unroll
+            for (int mh = 0; mh < KT / 32; ++mh) {
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) H[mh][nt][r] *= dC;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const unsigned char *p = sb + (16 * ks + tr_row) * AROW + (32 * mh + tr_col) * 2;
+                    const bf16x8 x = cat4(ldtr(p), ldtr(p + 4 * AROW));
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) {
+                        H[mh][nt] = mfma(x, chi[nt][ks], H[mh][nt]);
+                        if (SPLIT) H[mh][nt] = mfma(x, clo[nt][ks], H[mh][nt]);
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int KT, bool REV, bool SPLIT>
+int launch(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B, int T, int K,
+           int V, hipStream_t s) {
+    using G = Cfg<KT>;
+    const int NT = (T + C - 1) / C;
+    const int nK = (K + KT - 1) / KT, nV = (V + VT - 1) / VT;
+    const long long total = static_cast<long long>(B) * nK * nV;
+    const void *fn = reinterpret_cast<const void *>(&la_pipe_kernel<KT, REV, SPLIT>);
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES) != hipSuccess)
+        return check_launch("la_pipe_kernel attribute");
+    la_pipe_kernel<KT, REV, SPLIT><<<dim3(static_cast<unsigned>(total)), kThreads, G::LDS_BYTES, s>>>(
+        a, b, c, g, out, T, K, V, NT, nK, nV, static_cast<int>(total), B);
+    return check_launch("la_pipe_kernel");
+}
+
+}  // namespace pipe
+
+// Pipelined kernel for K % 8 == 0 and V % 8 == 0 with every tensor below 2 GB
+// (32-bit buffer offsets); returns ULM_ERR_UNSUPPORTED otherwise.
+int launch_la_pipelined(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B,
+                        int T, int K, int V, bool reverse, bool split, hipStream_t s) {
+    const size_t bytes_out = static_cast<size_t>(B) * T * V * 4;
+    const size_t bytes_in = static_cast<size_t>(B) * T * (K > V ? K : V) * 2;
+    if (K % 8 || V % 8 || bytes_out >= (1ull << 31) || bytes_in >= (1ull << 31)) return ULM_ERR_UNSUPPORTED;
+    const long long total = static_cast<long long>(B) * ((K + 127) / 128) * ((V + pipe::VT - 1) / pipe::VT);
+    if (total > 0x7fffffffLL) return ULM_ERR_UNSUPPORTED;
+    if (reverse)
+        return split ? pipe::launch<128, true, true>(a, b, c, g, out, B, T, K, V, s)
+                     : pipe::launch<128, true, false>(a, b, c, g, out, B, T, K, V, s);
+    return split ? pipe::launch<128, false, true>(a, b, c, g, out, B, T, K, V, s)
+                 : pipe::launch<128, false, false>(a, b, c, g, out, B, T, K, V, s);
+}
+
+}  // namespace ulm

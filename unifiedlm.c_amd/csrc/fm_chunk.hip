@@ -366,8 +366,16 @@ static int launch_la_kernel(const uint16_t *a, const uint16_t *b, const uint16_t
                                     : reinterpret_cast<const void *>(&la_kernel<true, false>))
                              : (vec ? reinterpret_cast<const void *>(&la_kernel<false, true>)
                                     : reinterpret_cast<const void *>(&la_kernel<false, false>));
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
-        return check_launch("la_kernel attribute");
+    // the LDS opt-in is a host call of its own; make it once per kernel and device
+    static bool attr_done[4][64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return check_launch("hipGetDevice");
+    bool &done = attr_done[(reverse ? 2 : 0) + (vec ? 1 : 0)][dev];
+    if (!done) {
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
+            return check_launch("la_kernel attribute");
+        done = true;
+    }
     const dim3 grid(static_cast<unsigned>(total));
     const int tot = static_cast<int>(total);
     if (reverse) {

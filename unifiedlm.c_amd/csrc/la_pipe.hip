@@ -160,13 +160,17 @@ __global__ __launch_bounds__(kThreads, 1) void la_pipe_kernel(const uint16_t *__
         issue_tile(rsC, stage + 2 * G::A_BYTES, G::CPITCH, G::VCH, v0, V, n);
     };
 
-    f32x16 H[KT / 32][2];
+    // State: H = s * G with a wave-uniform scalar s, so the per-chunk decay
+    // lam^64 of the state folds into s instead of a pass over G; G is rescaled
+    // (s reset to 1) only when s would drop below 2^-40.
+    f32x16 Gs[KT / 32][2];
 #pragma unroll
     for (int m = 0; m < KT / 32; ++m)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) H[m][nt][r] = 0.f;
+            for (int r = 0; r < 16; ++r) Gs[m][nt][r] = 0.f;
+    float s_state = 1.f;
 
     const int wcol = 64 * wave;
     const int jt = wave >> 1, it = wave & 1;
@@ -174,6 +178,27 @@ __global__ __launch_bounds__(kThreads, 1) void la_pipe_kernel(const uint16_t *__
     // transposed-read supplier coordinates of this lane (see ds_read_b64_tr_b16)
     const int tr_row = 8 * (g16 / 2) + p16 / 4;
     const int tr_col = 16 * (g16 % 2) + 4 * (p16 % 4);
+
+    // ---- decay factors, fixed per lane for the whole walk (lam^k = exp(g k), k >= 0)
+    float smask[16];   // score tile: lam^(i-j) for j <= i, else 0
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int lag = (32 * it + lr) - (32 * jt + 8 * rr + 4 * lh + e);
+            smask[4 * rr + e] = lag >= 0 ? __expf(gl * static_cast<float>(lag)) : 0.f;
+        }
+    float rrow[4];     // read-out rows i = 32 mt + 8 q + 4 lh + e: lam^(1 + 4 lh + e) * lam^(8 q + 32 mt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rrow[e] = __expf(gl * static_cast<float>(1 + 4 * lh + e));
+    float cks[4];      // state-update rows j = 16 ks + 8 lh + e: lam^(56 - 8 lh - 16 ks) * lam^(7 - e)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) cks[ks] = __expf(gl * static_cast<float>(56 - 8 * lh - 16 * ks));
+    const float lam8 = __expf(gl * 8.f), lam64 = __expf(gl * 64.f);
+    const bool lam64_tiny = lam64 < 0x1p-40f;
+
+    // atomics of interior chunks: per-lane voffset, uniform soffset per row
+    const uint32_t V4 = static_cast<uint32_t>(V) * 4u;
 
     issue_chunk(0, 0);
     for (int n = 0; n < NT; ++n) {
@@ -185,30 +210,28 @@ __global__ __launch_bounds__(kThreads, 1) void la_pipe_kernel(const uint16_t *__
 
         // ---- partial scores S^T[j][i] = b_j . a_i over this tile's keys -> P[i][j]
         {
-            f32x16 s = {};
+            f32x16 s0 = {}, s1 = {};
 #pragma unroll
-            for (int ks = 0; ks < KT / 16; ++ks)
-                s = mfma(ld8(sb + (32 * jt + lr) * AROW + (16 * ks + 8 * lh) * 2),
-                         ld8(sa + (32 * it + lr) * AROW + (16 * ks + 8 * lh) * 2), s);
+            for (int ks = 0; ks < KT / 16; ks += 2) {
+                s0 = mfma(ld8(sb + (32 * jt + lr) * AROW + (16 * ks + 8 * lh) * 2),
+                          ld8(sa + (32 * it + lr) * AROW + (16 * ks + 8 * lh) * 2), s0);
+                s1 = mfma(ld8(sb + (32 * jt + lr) * AROW + (16 * ks + 16 + 8 * lh) * 2),
+                          ld8(sa + (32 * it + lr) * AROW + (16 * ks + 16 + 8 * lh) * 2), s1);
+            }
             const int i = 32 * it + lr;
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
                 const int j0 = 32 * jt + 8 * rr + 4 * lh;
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int lag = i - (j0 + e);
-                    const float dk = __expf(gl * static_cast<float>(lag));
-                    v[e] = lag >= 0 ? s[4 * rr + e] * dk : 0.f;
-                }
                 uint2 pk;
-                pk.x = pack2(v[0], v[1]);
-                pk.y = pack2(v[2], v[3]);
+                pk.x = pack2((s0[4 * rr + 0] + s1[4 * rr + 0]) * smask[4 * rr + 0],
+                             (s0[4 * rr + 1] + s1[4 * rr + 1]) * smask[4 * rr + 1]);
+                pk.y = pack2((s0[4 * rr + 2] + s1[4 * rr + 2]) * smask[4 * rr + 2],
+                             (s0[4 * rr + 3] + s1[4 * rr + 3]) * smask[4 * rr + 3]);
                 *reinterpret_cast<uint2 *>(sP + i * PROW + j0 * 2) = pk;
             }
         }
 
-        // ---- read-out of the carried state: O = diag(lam^(i+1)) a H
+        // ---- read-out of the carried state: O = diag(lam^(i+1)) s a G
         f32x16 O[2][2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
@@ -225,7 +248,7 @@ __global__ __launch_bounds__(kThreads, 1) void la_pipe_kernel(const uint16_t *__
 #pragma unroll
                     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) hop[nt][e] = static_cast<bf16>(H[mh][nt][8 * hb + e]);
+                        for (int e = 0; e < 8; ++e) hop[nt][e] = static_cast<bf16>(Gs[mh][nt][8 * hb + e]);
                     const int kc = 32 * mh + 16 * hb + 4 * lh;
 #pragma unroll
                     for (int mt = 0; mt < 2; ++mt) {
@@ -236,14 +259,18 @@ __global__ __launch_bounds__(kThreads, 1) void la_pipe_kernel(const uint16_t *__
                     }
                 }
             }
+            float rq = s_state;          // lam^(8 q + 32 mt) * s, q + 4 mt = 0 .. 7
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
+            for (int k = 0; k < 8; ++k) {
+                const int mt = k / 4, q = k % 4;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float sc = __expf(gl * static_cast<float>(32 * mt + 8 * (r / 4) + 4 * lh + (r % 4) + 1));
-                    O[mt][0][r] *= sc;
-                    O[mt][1][r] *= sc;
+                for (int e = 0; e < 4; ++e) {
+                    const float sc = rrow[e] * rq;
+                    O[mt][0][4 * q + e] *= sc;
+                    O[mt][1][4 * q + e] *= sc;
                 }
+                rq *= lam8;
+            }
         }
         sync_lds();   // P complete
 
@@ -267,40 +294,78 @@ __global__ __launch_bounds__(kThreads, 1) void la_pipe_kernel(const uint16_t *__
                 for (int nt = 0; nt < 2; ++nt) O[mt][nt] = mfma(pp, cop[nt][ks], O[mt][nt]);
             }
 
-        // ---- partial output: fp32 buffer atomics. Lanes outside (T, V) are
-        // skipped by an exec mask, never by an out-of-range offset; chunks that
-        // lie wholly inside take the unguarded path (a wave-uniform branch).
-        const bool interior = (n + 1) * C <= T && v0 + VT <= V;
+        // ---- partial output: fp32 buffer atomics. Interior chunks address rows
+        // with a uniform soffset; edge chunks skip lanes outside (T, V) by an
+        // exec mask (never by an out-of-range offset).
+        if ((n + 1) * C <= T && v0 + VT <= V) {
+            const uint32_t row0 = REV ? rowA32 + static_cast<uint32_t>(T - 1 - n * C - 4 * lh - 59)
+                                      : rowA32 + static_cast<uint32_t>(n * C + 4 * lh);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            const int col = v0 + wcol + 32 * nt + lr;
+            for (int nt = 0; nt < 2; ++nt) {
+                const uint32_t voff = row0 * V4 + static_cast<uint32_t>(v0 + wcol + 32 * nt + lr) * 4u;
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
+                for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int t = n * C + 32 * mt + 8 * (r / 4) + 4 * lh + (r % 4);
-                    const uint32_t off = ((rowA32 + static_cast<uint32_t>(time_pos<REV>(t, T))) * static_cast<uint32_t>(V) +
-                                          static_cast<uint32_t>(col)) * 4u;
-                    if (interior || ((t < T) & (col < V)))
-                        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(O[mt][nt][r], rsO, static_cast<int>(off), 0, 0);
-                }
+                    for (int r = 0; r < 16; ++r) {
+                        const int u = 32 * mt + 8 * (r / 4) + (r % 4);
+                        const uint32_t soff = static_cast<uint32_t>(REV ? 59 - u : u) * V4;
+                        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(O[mt][nt][r], rsO, static_cast<int>(voff),
+                                                                        static_cast<int>(soff), 0);
+                    }
+            }
+        } else {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const int col = v0 + wcol + 32 * nt + lr;
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int t = n * C + 32 * mt + 8 * (r / 4) + 4 * lh + (r % 4);
+                        const uint32_t off = ((rowA32 + static_cast<uint32_t>(time_pos<REV>(t, T))) *
+                                                  static_cast<uint32_t>(V) + static_cast<uint32_t>(col)) * 4u;
+                        if ((t < T) & (col < V))
+                            __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(O[mt][nt][r], rsO, static_cast<int>(off), 0, 0);
+                    }
+            }
         }
 
-        // ---- state update: H = lam^64 H + b^T (lam^(63-j) c_j)
+        // ---- state update: H' = lam^64 H + b^T (lam^(63-j) c_j), as s' G'
         if (n + 1 < NT) {
+            // next scale: s' = lam^64 s (G unchanged), or s' = 1 with G rescaled by lam^64 s
+            const bool renorm = lam64_tiny || lam64 * s_state < 0x1p-40f;
+            const float s_next = renorm ? 1.f : lam64 * s_state;
+            const float inv_s = 1.f / s_next;
+            if (renorm) {
+                const float f = lam64 * s_state;
+#pragma unroll
+                for (int mh = 0; mh < KT / 32; ++mh)
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) Gs[mh][nt][r] *= f;
+            }
+            s_state = s_next;
+            // decayed value operand lam^(63-j) c_j / s', as bf16 (hi [+ lo])
             bf16x8 chi[2][4], clo[2][4];
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
+            for (int ks = 0; ks < 4; ++ks) {
+                float fe = cks[ks] * inv_s;   // lam^(63 - j) / s' for e = 7, times lam per step down
+                float fac[8];
 #pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
+                for (int e = 7; e >= 0; --e) {
+                    fac[e] = fe;
+                    fe *= __expf(gl);
+                }
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
                     const uint4 x = __builtin_bit_cast(uint4, cop[nt][ks]);
                     const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
                     uint32_t hi[4], lo[4];
 #pragma unroll
                     for (int h = 0; h < 4; ++h) {
-                        const int j = 16 * ks + 8 * lh + 2 * h;
-                        const float f0 = __uint_as_float(xs[h] << 16) * __expf(gl * static_cast<float>(C - 1 - j));
-                        const float f1 = __uint_as_float(xs[h] & 0xffff0000u) * __expf(gl * static_cast<float>(C - 2 - j));
+                        const float f0 = __uint_as_float(xs[h] << 16) * fac[2 * h];
+                        const float f1 = __uint_as_float(xs[h] & 0xffff0000u) * fac[2 * h + 1];
                         hi[h] = pack2(f0, f1);
                         if (SPLIT)
                             lo[h] = pack2(f0 - __uint_as_float(hi[h] << 16), f1 - __uint_as_float(hi[h] & 0xffff0000u));
@@ -308,24 +373,19 @@ __global__ __launch_bounds__(kThreads, 1) void la_pipe_kernel(const uint16_t *__
                     chi[nt][ks] = __builtin_bit_cast(bf16x8, make_uint4(hi[0], hi[1], hi[2], hi[3]));
                     if (SPLIT) clo[nt][ks] = __builtin_bit_cast(bf16x8, make_uint4(lo[0], lo[1], lo[2], lo[3]));
                 }
-            const float dC = __expf(gl * static_cast<float>(C));
+            }
 #pragma unroll
-            for (int mh = 0; mh < KT / 32; ++mh) {
+            for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) H[mh][nt][r] *= dC;
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
+                for (int mh = 0; mh < KT / 32; ++mh) {
                     const unsigned char *p = sb + (16 * ks + tr_row) * AROW + (32 * mh + tr_col) * 2;
                     const bf16x8 x = cat4(ldtr(p), ldtr(p + 4 * AROW));
 #pragma unroll
                     for (int nt = 0; nt < 2; ++nt) {
-                        H[mh][nt] = mfma(x, chi[nt][ks], H[mh][nt]);
-                        if (SPLIT) H[mh][nt] = mfma(x, clo[nt][ks], H[mh][nt]);
+                        Gs[mh][nt] = mfma(x, chi[nt][ks], Gs[mh][nt]);
+                        if (SPLIT) Gs[mh][nt] = mfma(x, clo[nt][ks], Gs[mh][nt]);
                     }
                 }
-            }
         }
     }
 }
@@ -337,9 +397,16 @@ int launch(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float 
     const int NT = (T + C - 1) / C;
     const int nK = (K + KT - 1) / KT, nV = (V + VT - 1) / VT;
     const long long total = static_cast<long long>(B) * nK * nV;
-    const void *fn = reinterpret_cast<const void *>(&la_pipe_kernel<KT, REV, SPLIT>);
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES) != hipSuccess)
-        return check_launch("la_pipe_kernel attribute");
+    // the LDS opt-in is a host call of its own; make it once per device
+    static bool attr_done[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return check_launch("hipGetDevice");
+    if (!attr_done[dev]) {
+        const void *fn = reinterpret_cast<const void *>(&la_pipe_kernel<KT, REV, SPLIT>);
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES) != hipSuccess)
+            return check_launch("la_pipe_kernel attribute");
+        attr_done[dev] = true;
+    }
     la_pipe_kernel<KT, REV, SPLIT><<<dim3(static_cast<unsigned>(total)), kThreads, G::LDS_BYTES, s>>>(
         a, b, c, g, out, T, K, V, NT, nK, nV, static_cast<int>(total), B);
     return check_launch("la_pipe_kernel");

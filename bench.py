@@ -7,8 +7,8 @@ B=16, T=1024, D=768, A=3072 slots, chunk 64, v/dfast in bf16, r/q/stats fp32.
 Inputs are resident in HBM before the timed region. Prints one JSON line:
 
   value      Mtok/s = B*T / step time
-  roofline   the chunked MFMA kernel (la_kernel): algorithmic flops per launch
-             (B*T*(4*K*V + 2*64*(K+V))) over its average launch time, measured
+  roofline   the chunked MFMA kernel (la_kgroup_kernel): algorithmic flops per
+             launch (B*T*(4*K*V + 2*64*V)) over its average launch time, measured
              with HIP events on its own stream over the timed steps, against
              the 2516.6 TFLOP/s dense bf16 peak
   cpu_baseline  the oracle's chunked PyTorch form on the host cores (fp32,
@@ -35,7 +35,7 @@ for _p in (ROOT, PKG):
 METRIC = "fast-memory fwd+bwd Mtokens/s at 110M shape (% bf16 MFMA peak); decode GB/s"
 PEAK_BF16_TFLOPS = 2516.6
 PEAK_HBM_GBPS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "la_kernel_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "la_kgroup_kernel_traffic.json")
 
 
 def log(msg):
@@ -88,19 +88,19 @@ def bench_training(torch, args):
         t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / args.steps
     la_ms = timer.total_ms / max(timer.launches, 1)
-    la_flops = workloads.la_flops(B, T, A, D)
+    la_flops = workloads.la_kernel_flops(B, T, A, D)
     achieved = la_flops / (la_ms * 1e-3) / 1e12
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             traffic = json.load(f).get("bytes_per_launch")
-    ftok = 4 * la_flops / (B * T)
+    ftok = 4 * workloads.la_flops(B, T, A, D) / (B * T)
     path_tflops = ftok * L * B * T / (ms_step * 1e-3) / 1e12
-    log(f"step {ms_step:.2f} ms, la_kernel {la_ms:.3f} ms x {timer.launches} launches, {achieved:.1f} TFLOP/s")
+    log(f"step {ms_step:.2f} ms, la_kgroup_kernel {la_ms:.3f} ms x {timer.launches} launches, {achieved:.1f} TFLOP/s")
     return dict(B=B, T=T, D=D, A=A, L=L, ms_step=ms_step, value=B * T / (ms_step * 1e-3) / 1e6,
                 roofline={"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
-                          "kernel": "la_kernel", "flops_per_launch": la_flops,
+                          "kernel": "la_kgroup_kernel", "flops_per_launch": la_flops,
                           "avg_launch_ms": round(la_ms, 4), "launches_timed": timer.launches},
                 path_tflops=path_tflops)
 

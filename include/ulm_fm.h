@@ -54,19 +54,23 @@ const char *ulm_last_error(void);
  *   w      (A,)    fp32          prior mass
  *   q      (B,T,A) fp32   out    returned and saved
  *   fast   (B,T,D) fast_dtype out  (v.dtype in the reference, kernel.py:211)
- *   q16, k16 (B,T,A) bf16 out    saved for backward (kernel.py:212)
- *   n_ckpt (B,ceil(T/64),A) fp32 out  evidence n = c - w at the end of each
- *                                 chunk's predecessor, saved for backward in
- *                                 place of the full c tensor
+ *   saved  ulm_fm_saved_bytes() bytes, out: what the backward needs besides
+ *          r, v16, g, w and q (the reference saves c, q16, k16, kernel.py:212;
+ *          this holds bf16 copies of q and k in natural and chunk-transposed
+ *          layouts, the transposed values, the score tiles of the dv product
+ *          and the evidence n at every chunk start in place of c). Opaque to
+ *          the caller; pass it unchanged to ulm_fm_bwd.
  */
+size_t ulm_fm_saved_bytes(int B, int T, int A, int D);
 size_t ulm_fm_fwd_workspace_bytes(int B, int T, int A, int D, int fast_dtype);
 int ulm_fm_fwd(const float *r, const uint16_t *v16, const float *g, const float *w,
-               float *q, void *fast, int fast_dtype, uint16_t *q16, uint16_t *k16, float *n_ckpt,
+               float *q, void *fast, int fast_dtype, void *saved, size_t saved_bytes,
                void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream);
 
 /* Replaces UnifiedMemory.backward (kernel.py:216-233): the three chunked
  * products dq, dk (reverse), dv (reverse) and the denominator chain rule.
  *
+ *   saved  the buffer ulm_fm_fwd filled for the same r, v16, g, w, q
  *   dfast  (B,T,D) dfast_dtype   upstream gradient of fast
  *   dq_out (B,T,A) fp32 or NULL  upstream gradient of the returned q
  *                                 (HAS_DQO, kernel.py:166-167, 228)
@@ -77,18 +81,20 @@ int ulm_fm_fwd(const float *r, const uint16_t *v16, const float *g, const float 
  * dg and dw are reduced deterministically (no atomics). */
 size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D);
 int ulm_fm_bwd(const float *r, const uint16_t *v16, const float *g, const float *w,
-               const float *q, const uint16_t *q16, const uint16_t *k16, const float *n_ckpt,
+               const float *q, const void *saved, size_t saved_bytes,
                const void *dfast, int dfast_dtype, const float *dq_out,
                float *dr, void *dv, int dv_dtype, float *dg, float *dw,
                void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream);
 
-/* Building block of both: out += o, o_t = sum_{s<=t} lam^(t-s) (a_t . b_s) c_s
- * (s >= t and time read backwards when reverse != 0). Replaces `_la`
- * (kernel.py:183-196) with the chunk state kept in fp32 on chip.
- * a, b (B,T,K) bf16; c (B,T,V) bf16; out (B,T,V) fp32 accumulated with
- * atomic adds, so the caller zeroes it first. */
+/* Building block of both: out = o, o_t = sum_{s<=t} lam^(t-s) (a_t . b_s) c_s
+ * (s >= t when reverse != 0). Replaces `_la` (kernel.py:183-196) with the
+ * chunk state kept in fp32 on chip. a, b (B,T,K) bf16; c (B,T,V) bf16;
+ * out (B,T,V) fp32, overwritten. split != 0 carries the decayed state-update
+ * operand as a bf16 hi + lo pair (used by the backward's dq and dk). */
+size_t ulm_la_workspace_bytes(int B, int T, int K, int V);
 int ulm_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out,
-           int B, int T, int K, int V, int reverse, void *stream);
+           int B, int T, int K, int V, int reverse, int split,
+           void *workspace, size_t workspace_bytes, void *stream);
 
 /* ------------------------------------------------------------------------
  * relu^2 slot address. Replaces UnifiedBlock.code (model.py:70-72) after

@@ -26,15 +26,15 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert sorted(nat.SIGNATURES) == declared
-    assert lib.ulm_abi_version() == 1
+    assert lib.ulm_abi_version() == 2
 
 
 def test_c_side_rejects_bad_sizes_without_touching_the_gpu():
     lib = nat.lib()
-    st = lib.ulm_la(None, None, None, None, None, 0, 10, 8, 8, 0, None)
+    st = lib.ulm_la(None, None, None, None, None, 0, 10, 8, 8, 0, 0, None, 0, None)
     assert st == nat.ULM_ERR_INVALID
     assert b"bad sizes" in lib.ulm_last_error()
-    st = lib.ulm_fm_fwd(*([None] * 6), 0, None, None, None, None, 0, 2, 64, 8, 8, None)
+    st = lib.ulm_fm_fwd(*([None] * 6), 0, None, 0, None, 0, 2, 64, 8, 8, None)
     assert st == nat.ULM_ERR_INVALID and b"null pointer" in lib.ulm_last_error()
     st = lib.ulm_decode_state(*([None] * 8), 4, 8, 100000, None)
     assert st == nat.ULM_ERR_INVALID and b"LDS" in lib.ulm_last_error()
@@ -42,15 +42,23 @@ def test_c_side_rejects_bad_sizes_without_touching_the_gpu():
 
 def test_nonzero_status_surfaces_as_runtime_error():
     with pytest.raises(RuntimeError, match="status 1"):
-        nat.call("ulm_la", None, None, None, None, None, 1, 0, 8, 8, 0, None)
+        nat.call("ulm_la", None, None, None, None, None, 1, 0, 8, 8, 0, 0, None, 0, None)
 
 
 def test_workspace_sizes():
     lib = nat.lib()
     B, T, A, D = 16, 1024, 3072, 768
-    assert lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_F32) == 0
+    NT = (T + 63) // 64
+    # 4 key groups of 768 slots: fp32 partial outputs, plus the forward score tiles
+    assert lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_F32) >= 4 * B * T * D * 4 + B * NT * 64 * 64 * 2
     assert lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * D * 4
     assert lib.ulm_fm_bwd_workspace_bytes(B, T, A, D) >= B * T * (2 * A * 4 + D * 6)
+    # saved: bf16 q, k in natural and transposed layouts, three v copies, n checkpoints
+    assert lib.ulm_fm_saved_bytes(B, T, A, D) >= B * T * (8 * A + 6 * D) + B * NT * A * 4
+    # unaligned sizes keep only the natural copies and the checkpoints
+    assert lib.ulm_fm_saved_bytes(2, 70, 12, 8) >= 2 * 70 * 12 * 4 + 2 * 2 * 12 * 4
+    assert lib.ulm_la_workspace_bytes(2, 70, 12, 8) == 0
+    assert lib.ulm_la_workspace_bytes(B, T, A, D) >= 2 * B * NT * A * 64 * 2 + 4 * B * T * D * 4
     assert lib.ulm_addr_bwd_workspace_bytes(B * T, A) >= A * 4
     assert lib.ulm_fm_bwd_workspace_bytes(0, T, A, D) == 0
 

@@ -28,31 +28,42 @@ def test_mfma_operand_layout():
 
 
 LA_CASES = [
-    # B, T, K, V, reverse
-    (1, 64, 128, 256, False),
-    (1, 64, 128, 256, True),
-    (2, 200, 140, 64, False),
-    (2, 200, 140, 64, True),
-    (1, 1, 16, 8, False),
-    (2, 130, 48, 32, True),
-    (1, 300, 300, 520, False),
-    (2, 256, 256, 512, True),
+    # B, T, K, V, reverse, lam, split
+    # generic kernel (K or V not a multiple of 32)
+    (2, 200, 140, 64, False, 0.93, False),
+    (2, 200, 140, 64, True, 0.93, False),
+    (1, 1, 16, 8, False, 0.93, False),
+    (2, 130, 48, 32, True, 0.93, False),
+    (1, 300, 300, 520, False, 0.93, False),
+    # K-group kernel
+    (1, 64, 128, 256, False, 0.93, False),
+    (1, 64, 128, 256, True, 0.93, True),
+    (2, 256, 256, 512, True, 0.93, False),
+    (2, 200, 96, 96, False, 0.93, False),      # ragged T, a half-empty value tile, a keyless wave
+    (2, 200, 96, 96, True, 0.93, True),
+    (1, 600, 1600, 64, False, 0.93, False),    # 3 key groups; the state scale renormalises
+    (1, 600, 1600, 64, True, 0.93, True),
+    (2, 300, 64, 128, False, 0.5, False),      # lam^64 below 2^-40: explicit per-chunk decay
+    (2, 300, 64, 128, True, 0.5, True),
+    (1, 128, 32, 32, False, 0.99, False),
+    (1, 1024, 768, 192, True, 0.953, True),
 ]
 
 
-@pytest.mark.parametrize("B,T,K,V,reverse", LA_CASES)
-def test_la_matches_dense(B, T, K, V, reverse):
-    say(f"la B={B} T={T} K={K} V={V} reverse={reverse}")
+@pytest.mark.parametrize("B,T,K,V,reverse,lam,split", LA_CASES)
+def test_la_matches_dense(B, T, K, V, reverse, lam, split):
+    say(f"la B={B} T={T} K={K} V={V} reverse={reverse} lam={lam} split={split}")
     gen = torch.Generator().manual_seed(B * 1000 + T + K + V)
     a = (torch.randn(B, T, K, generator=gen) / math.sqrt(K)).to(torch.bfloat16)
     b = torch.randn(B, T, K, generator=gen).to(torch.bfloat16)
     c = torch.randn(B, T, V, generator=gen).to(torch.bfloat16)
-    lam = 0.93
     g = torch.tensor([math.log(lam)], dtype=torch.float32)
-    out = kernel.la(a.cuda(), b.cuda(), c.cuda(), g.cuda(), reverse).cpu()
-    ref = fm.la_dense(a, b, c, lam, reverse)
+    out = kernel.la(a.cuda(), b.cuda(), c.cuda(), g.cuda(), reverse, split).cpu()
+    ref = fm.la_dense(a, b, c, float(torch.exp(g.double())), reverse)
     assert torch.isfinite(out).all()
-    assert rel(out, ref) < 1e-2
+    err = rel(out, ref)
+    say(f"  rel error {err:.3e}")
+    assert err < 1e-2
 
 
 OP_CASES = [
@@ -62,6 +73,8 @@ OP_CASES = [
     (3, 77, 48, 40, torch.bfloat16),
     (1, 1, 64, 64, torch.float32),
     (4, 256, 1152, 288, torch.bfloat16),   # 15M-shape block, fewer rows
+    (2, 200, 128, 64, torch.float32),      # K-group kernels with a ragged last chunk
+    (1, 512, 3072, 768, torch.bfloat16),   # 110M-shape block, one row of 512 positions
 ]
 
 

@@ -19,7 +19,8 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libulm_fm.so")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 
-SOURCES = ["status.hip", "elementwise.hip", "decode.hip", "address.hip", "fm_stats.hip", "fm_chunk.hip", "la_pipe.hip", "probe.hip"]
+SOURCES = ["status.hip", "elementwise.hip", "decode.hip", "address.hip", "fm_stats.hip", "fm_chunk.hip",
+           "fm_chunks.hip", "la_kgroup.hip", "fm_ops.hip", "probe.hip"]
 ARCH = "gfx950"
 FLAGS = [f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-munsafe-fp-atomics",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -33,9 +34,13 @@ def hipcc():
     return path
 
 
+# per-source extra flags
+EXTRA = {}
+
+
 def _compile(src):
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc()] + FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc()] + FLAGS + EXTRA.get(src, []) + ["-c", os.path.join(CSRC, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature; drop that line
     err = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l and l.strip())

@@ -318,9 +318,9 @@ __global__ __launch_bounds__(kThreads, 1) void la_kernel(const uint16_t *__restr
     }
 }
 
-// ---- launch timer (diagnostics): HIP events around every la_kernel launch
-// while enabled, so a benchmark can read the kernel's own average duration on
-// the stream it runs on. Process-wide and not thread-safe.
+// ---- launch timer (diagnostics): HIP events around every chunked-kernel
+// launch while enabled, so a benchmark can read the kernel's own average
+// duration on the stream it runs on. Process-wide and not thread-safe.
 namespace {
 struct LaTimer {
     bool on = false;
@@ -328,38 +328,31 @@ struct LaTimer {
     hipEvent_t *ev = nullptr;
 };
 LaTimer g_la_timer;
+bool g_la_timer_open = false;   // a begin without its end
 }  // namespace
 
-static int launch_la_kernel(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B,
-                            int T, int K, int V, bool reverse, hipStream_t s);
-
-// la_pipe.hip: the pipelined kernel for aligned shapes
-int launch_la_pipelined(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B,
-                        int T, int K, int V, bool reverse, bool split, hipStream_t s);
-
-// `split` carries the decayed state-update operand as a bf16 hi + lo pair
-// (pipelined kernel only); the backward uses it for dq and dk, the inputs of
-// the positional d/dg identity, whose cancellation amplifies rounding.
-int launch_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B, int T, int K,
-              int V, bool reverse, hipStream_t s, bool split = false) {
-    const bool timed = g_la_timer.on && g_la_timer.used < g_la_timer.cap;
-    if (timed && hipEventRecord(g_la_timer.ev[2 * g_la_timer.used], s) != hipSuccess) return check_launch("timer");
-    int st = launch_la_pipelined(a, b, c, g, out, B, T, K, V, reverse, split, s);
-    if (st == ULM_ERR_UNSUPPORTED) st = launch_la_kernel(a, b, c, g, out, B, T, K, V, reverse, s);
-    if (st) return st;
-    if (timed) {
-        if (hipEventRecord(g_la_timer.ev[2 * g_la_timer.used + 1], s) != hipSuccess) return check_launch("timer");
-        ++g_la_timer.used;
-    }
+int la_timer_begin(hipStream_t s) {
+    g_la_timer_open = g_la_timer.on && g_la_timer.used < g_la_timer.cap;
+    if (g_la_timer_open && hipEventRecord(g_la_timer.ev[2 * g_la_timer.used], s) != hipSuccess)
+        return check_launch("timer");
     return ULM_OK;
 }
 
-static int launch_la_kernel(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B,
-                            int T, int K, int V, bool reverse, hipStream_t s) {
+int la_timer_end(hipStream_t s) {
+    if (!g_la_timer_open) return ULM_OK;
+    g_la_timer_open = false;
+    if (hipEventRecord(g_la_timer.ev[2 * g_la_timer.used + 1], s) != hipSuccess) return check_launch("timer");
+    ++g_la_timer.used;
+    return ULM_OK;
+}
+
+// Generic chunked kernel, any K and V: out += o (fp32 atomics; the caller zeroes out).
+int launch_la_generic(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B,
+                      int T, int K, int V, bool reverse, hipStream_t s) {
     const int NT = (T + C - 1) / C;
     const int nK = (K + KT - 1) / KT, nV = (V + VT - 1) / VT;
     const long long total = static_cast<long long>(B) * nK * nV;
-    if (total > 0x7fffffffLL) return fail(ULM_ERR_UNSUPPORTED, "ulm_la: grid of %lld workgroups", total);
+    if (total > 0x7fffffffLL) return fail(ULM_ERR_UNSUPPORTED, "chunked kernel: grid of %lld workgroups", total);
     const bool vec = (K % 8 == 0) && (V % 8 == 0);
     const size_t lds = sizeof(LaSmem);
     const void *fn = reverse ? (vec ? reinterpret_cast<const void *>(&la_kernel<true, true>)
@@ -378,6 +371,8 @@ static int launch_la_kernel(const uint16_t *a, const uint16_t *b, const uint16_t
     }
     const dim3 grid(static_cast<unsigned>(total));
     const int tot = static_cast<int>(total);
+    int st = la_timer_begin(s);
+    if (st) return st;
     if (reverse) {
         if (vec) la_kernel<true, true><<<grid, kThreads, lds, s>>>(a, b, c, g, out, T, K, V, NT, nK, nV, tot);
         else la_kernel<true, false><<<grid, kThreads, lds, s>>>(a, b, c, g, out, T, K, V, NT, nK, nV, tot);
@@ -385,7 +380,9 @@ static int launch_la_kernel(const uint16_t *a, const uint16_t *b, const uint16_t
         if (vec) la_kernel<false, true><<<grid, kThreads, lds, s>>>(a, b, c, g, out, T, K, V, NT, nK, nV, tot);
         else la_kernel<false, false><<<grid, kThreads, lds, s>>>(a, b, c, g, out, T, K, V, NT, nK, nV, tot);
     }
-    return check_launch("la_kernel");
+    st = check_launch("la_kernel");
+    if (st) return st;
+    return la_timer_end(s);
 }
 
 // ---- layout probe: one wave, D (32x32) = A (32x16) B (16x32) through the
@@ -404,122 +401,9 @@ __global__ void probe_mfma_kernel(const uint16_t *__restrict__ a, const uint16_t
     for (int r = 0; r < 16; ++r) d[(8 * (r / 4) + 4 * lh + (r % 4)) * 32 + lr] = acc[r];
 }
 
-// from fm_stats.hip
-int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16, uint16_t *k16,
-                     float *nck, int B, int T, int A, hipStream_t s);
-size_t bwd_stats_partial_bytes(int B, int A);
-int launch_bwd_stats(const float *dqf, const float *dqo, const float *q, const float *r, const float *nck,
-                     const float *w, const float *g, const float *dkf, float *dr, float *dw, float *dg, void *part,
-                     int B, int T, int A, hipStream_t s);
-
 }  // namespace ulm
 
 using namespace ulm;
-
-#define ULM_TRY(x)              \
-    do {                        \
-        int _st = (x);          \
-        if (_st) return _st;    \
-    } while (0)
-
-extern "C" int ulm_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B,
-                      int T, int K, int V, int reverse, void *stream) {
-    ULM_REQUIRE(B > 0 && T > 0 && K > 0 && V > 0, "ulm_la: bad sizes B=%d T=%d K=%d V=%d", B, T, K, V);
-    ULM_REQUIRE(a && b && c && g && out, "ulm_la: null pointer");
-    return launch_la(a, b, c, g, out, B, T, K, V, reverse != 0, static_cast<hipStream_t>(stream));
-}
-
-extern "C" size_t ulm_fm_fwd_workspace_bytes(int B, int T, int A, int D, int fast_dtype) {
-    (void)A;
-    if (B <= 0 || T <= 0 || D <= 0) return 0;
-    return fast_dtype == ULM_F32 ? 0 : align_up(static_cast<size_t>(B) * T * D * sizeof(float), 256);
-}
-
-extern "C" int ulm_fm_fwd(const float *r, const uint16_t *v16, const float *g, const float *w, float *q, void *fast,
-                          int fast_dtype, uint16_t *q16, uint16_t *k16, float *n_ckpt, void *workspace,
-                          size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
-    ULM_REQUIRE(B > 0 && T > 0 && A > 0 && D > 0, "ulm_fm_fwd: bad sizes B=%d T=%d A=%d D=%d", B, T, A, D);
-    ULM_REQUIRE(valid_dtype(fast_dtype), "ulm_fm_fwd: bad fast dtype %d", fast_dtype);
-    ULM_REQUIRE(r && v16 && g && w && q && fast && q16 && k16 && n_ckpt, "ulm_fm_fwd: null pointer");
-    const size_t need = ulm_fm_fwd_workspace_bytes(B, T, A, D, fast_dtype);
-    ULM_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), "ulm_fm_fwd: workspace of %zu bytes, need %zu",
-                workspace_bytes, need);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const size_t nf = static_cast<size_t>(B) * T * D;
-    float *acc = fast_dtype == ULM_F32 ? static_cast<float *>(fast) : static_cast<float *>(workspace);
-    ULM_TRY(launch_fwd_stats(r, w, g, q, q16, k16, n_ckpt, B, T, A, s));
-    ULM_TRY(launch_fill_zero(acc, nf * sizeof(float), s));
-    ULM_TRY(launch_la(q16, k16, v16, g, acc, B, T, A, D, false, s));
-    if (fast_dtype != ULM_F32) ULM_TRY(launch_convert(acc, ULM_F32, fast, fast_dtype, nf, s));
-    return ULM_OK;
-}
-
-namespace {
-struct BwdWs {
-    uint16_t *do16;
-    float *dqf, *dkf, *dv32;
-    void *part;
-    size_t bytes;
-};
-BwdWs bwd_layout(void *base, int B, int T, int A, int D) {
-    const size_t nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
-    size_t off = 0;
-    BwdWs w;
-    char *p = static_cast<char *>(base);
-    w.do16 = reinterpret_cast<uint16_t *>(p + off);
-    off += align_up(nd * 2, 256);
-    w.dqf = reinterpret_cast<float *>(p + off);
-    off += align_up(na * 4, 256);
-    w.dkf = reinterpret_cast<float *>(p + off);
-    off += align_up(na * 4, 256);
-    w.dv32 = reinterpret_cast<float *>(p + off);
-    off += align_up(nd * 4, 256);
-    w.part = p + off;
-    off += bwd_stats_partial_bytes(B, A);
-    w.bytes = off;
-    return w;
-}
-}  // namespace
-
-extern "C" size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D) {
-    if (B <= 0 || T <= 0 || A <= 0 || D <= 0) return 0;
-    return bwd_layout(nullptr, B, T, A, D).bytes;
-}
-
-extern "C" int ulm_fm_bwd(const float *r, const uint16_t *v16, const float *g, const float *w, const float *q,
-                          const uint16_t *q16, const uint16_t *k16, const float *n_ckpt, const void *dfast,
-                          int dfast_dtype, const float *dq_out, float *dr, void *dv, int dv_dtype, float *dg, float *dw,
-                          void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
-    ULM_REQUIRE(B > 0 && T > 0 && A > 0 && D > 0, "ulm_fm_bwd: bad sizes B=%d T=%d A=%d D=%d", B, T, A, D);
-    ULM_REQUIRE(valid_dtype(dfast_dtype) && valid_dtype(dv_dtype), "ulm_fm_bwd: bad dtype %d/%d", dfast_dtype,
-                dv_dtype);
-    ULM_REQUIRE(r && v16 && g && w && q && q16 && k16 && n_ckpt && dfast && dr && dv && dg && dw,
-                "ulm_fm_bwd: null pointer");
-    const size_t need = ulm_fm_bwd_workspace_bytes(B, T, A, D);
-    ULM_REQUIRE(workspace && workspace_bytes >= need, "ulm_fm_bwd: workspace of %zu bytes, need %zu",
-                workspace_bytes, need);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    BwdWs ws = bwd_layout(workspace, B, T, A, D);
-    const size_t nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
-    const uint16_t *do16 = static_cast<const uint16_t *>(dfast);
-    if (dfast_dtype != ULM_BF16) {
-        ULM_TRY(launch_convert(dfast, dfast_dtype, ws.do16, ULM_BF16, nd, s));
-        do16 = ws.do16;
-    }
-    // dq_f = LA(dfast, v, k): keys = D, values = A
-    ULM_TRY(launch_fill_zero(ws.dqf, na * 4, s));
-    ULM_TRY(launch_la(do16, v16, k16, g, ws.dqf, B, T, D, A, false, s, true));
-    // dk_f = LA_rev(v, dfast, q)
-    ULM_TRY(launch_fill_zero(ws.dkf, na * 4, s));
-    ULM_TRY(launch_la(v16, do16, q16, g, ws.dkf, B, T, D, A, true, s, true));
-    // dv = LA_rev(k, q, dfast): keys = A, values = D
-    float *dv_acc = dv_dtype == ULM_F32 ? static_cast<float *>(dv) : ws.dv32;
-    ULM_TRY(launch_fill_zero(dv_acc, nd * 4, s));
-    ULM_TRY(launch_la(k16, q16, do16, g, dv_acc, B, T, A, D, true, s));
-    ULM_TRY(launch_bwd_stats(ws.dqf, dq_out, q, r, n_ckpt, w, g, ws.dkf, dr, dw, dg, ws.part, B, T, A, s));
-    if (dv_dtype != ULM_F32) ULM_TRY(launch_convert(dv_acc, ULM_F32, dv, dv_dtype, nd, s));
-    return ULM_OK;
-}
 
 extern "C" int ulm_la_timer_start(int max_launches) {
     ULM_REQUIRE(max_launches > 0 && max_launches <= 1 << 16, "ulm_la_timer_start: bad capacity %d", max_launches);

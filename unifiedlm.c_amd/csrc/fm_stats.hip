@@ -6,7 +6,9 @@
 // Backward (kernel.py:142-178), walking time in reverse:
 //   dq = dq_f + dq_out, dr_t = dq_t / c_t + dkt_{t+1}, dc = -dq q / c,
 //   dkc_t = dc_t + lam dkc_{t+1}, dkt = dk_f + dkc, dw = sum_t dc,
-//   dg = sum_t (t - tau) [q dq_f + dc (c - w) - k dkt]_t     (any tau; tau = (T-1)/2)
+//   dg = sum_t (t - tau) [q dq_f + dc (c - w) - k dk_f - k dkc]_t   (any tau; tau = (T-1)/2)
+//   with the bf16 copies of q and k in the dq_f and dk_f terms (the values the
+//   chunked products used), so the pair terms cancel exactly between the sums.
 //
 // Thread layout: a 256-thread block owns 64 slots of one batch row; thread
 // (slot s, segment j) holds 16 consecutive positions of each 64-position chunk,
@@ -31,6 +33,7 @@ __device__ __forceinline__ float pow_int(float x, int e) {
 __global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict__ r, const float *__restrict__ w,
                                                         const float *__restrict__ g, float *__restrict__ q,
                                                         uint16_t *__restrict__ q16, uint16_t *__restrict__ k16,
+                                                        uint16_t *__restrict__ qT, uint16_t *__restrict__ kT,
                                                         float *__restrict__ nck, int T, int A, int NT) {
     __shared__ float tot[4][kSlots];
     const int s = threadIdx.x % kSlots, j = threadIdx.x / kSlots;
@@ -63,18 +66,39 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict_
         float cj = carry;
         for (int m = 0; m < j; ++m) cj = lam16 * cj + tot[m][s];
         float pw = lam;
+        uint32_t qpk[kSeg / 2], kpk[kSeg / 2];   // bf16 pairs for the chunk-transposed copies
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
             const int t = t0 + i;
             const float ct = wa + (pw * cj + nl[i]);
             pw *= lam;
+            uint16_t qb = 0, kb = 0;   // positions past T are zero in the transposed copies
             if (va && t < T) {
                 const size_t o = (b * T + t) * A + a;
                 const float qt = rv[i] / ct;
+                qb = f32_to_bf16_bits(qt);
+                kb = f32_to_bf16_bits(kv[i]);
                 q[o] = qt;
-                q16[o] = f32_to_bf16_bits(qt);
-                k16[o] = f32_to_bf16_bits(kv[i]);
+                q16[o] = qb;
+                k16[o] = kb;
             }
+            if (i % 2 == 0) {
+                qpk[i / 2] = qb;
+                kpk[i / 2] = kb;
+            } else {
+                qpk[i / 2] |= static_cast<uint32_t>(qb) << 16;
+                kpk[i / 2] |= static_cast<uint32_t>(kb) << 16;
+            }
+        }
+        if (kT && va) {
+            // (B, NT, A, 64): this thread's 16 positions of slot a are 32 contiguous bytes
+            const size_t o = ((b * NT + n) * A + a) * ULM_CHUNK + j * kSeg;
+            uint4 *dq = reinterpret_cast<uint4 *>(qT + o);
+            uint4 *dk = reinterpret_cast<uint4 *>(kT + o);
+            dq[0] = make_uint4(qpk[0], qpk[1], qpk[2], qpk[3]);
+            dq[1] = make_uint4(qpk[4], qpk[5], qpk[6], qpk[7]);
+            dk[0] = make_uint4(kpk[0], kpk[1], kpk[2], kpk[3]);
+            dk[1] = make_uint4(kpk[4], kpk[5], kpk[6], kpk[7]);
         }
         if (j == 0 && va) nck[(b * NT + n) * A + a] = carry;
         float nc = carry;
@@ -155,15 +179,15 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
         __syncthreads();
         float rj = dkc_next;
         for (int m = 3; m > j; --m) rj = tot[m][s] + lam16 * rj;
-        float dkt[kSeg];
+        float dkt[kSeg], dkfv[kSeg], dkcv[kSeg];
         float pr = lam;   // lam^(16-i) for i = 15 .. 0
 #pragma unroll
         for (int i = kSeg - 1; i >= 0; --i) {
             const int t = t0 + i;
-            const float dkft = (va && t < T) ? dkf[(b * T + t) * A + a] : 0.f;
-            const float dkc = rl[i] + pr * rj;
+            dkfv[i] = (va && t < T) ? dkf[(b * T + t) * A + a] : 0.f;
+            dkcv[i] = rl[i] + pr * rj;
             pr *= lam;
-            dkt[i] = dkft + dkc;
+            dkt[i] = dkfv[i] + dkcv[i];
         }
         first_dkt[j][s] = dkt[0];
         if (j == 0) tot[0][s] = rl[0] + pow_int(lam, kSeg) * rj;   // dkc at chunk start (rl[0] + lam^16 r_0)
@@ -176,9 +200,14 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
                 const float nxt = (i + 1 < kSeg) ? dkt[i + 1] : after;
                 dr[(b * T + t) * A + a] = dq[i] / cv[i] + nxt;
                 dw_acc += dc[i];
+                // The fast-read terms take the bf16 q and k that the dq and dk
+                // products contracted with, so each (t, s) pair enters both sums
+                // with the same value and the position weights cancel to t - s.
+                const float q16 = bf16_to_f32(f32_to_bf16_bits(rv[i]));
+                const float k16 = bf16_to_f32(f32_to_bf16_bits(kv[i]));
                 const double pos = static_cast<double>(t) - tau;
-                dg_acc += pos * (static_cast<double>(rv[i] * dqfv[i] + dc[i] * (cv[i] - wa)) -
-                                 static_cast<double>(kv[i] * dkt[i]));
+                dg_acc += pos * (static_cast<double>(q16 * dqfv[i] + dc[i] * (cv[i] - wa)) -
+                                 static_cast<double>(k16 * dkfv[i] + kv[i] * dkcv[i]));
             }
         }
         dkc_next = tot[0][s];
@@ -210,10 +239,13 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(const float *__restri
     }
 }
 
+// qT, kT: (B, NT, A, 64) chunk-transposed bf16 copies of q and k (both or neither)
 int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16, uint16_t *k16,
-                     float *nck, int B, int T, int A, hipStream_t s) {
+                     uint16_t *qT, uint16_t *kT, float *nck, int B, int T, int A, hipStream_t s) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
-    fwd_stats_kernel<<<dim3((A + kSlots - 1) / kSlots, B), 256, 0, s>>>(r, w, g, q, q16, k16, nck, T, A, NT);
+    if ((qT == nullptr) != (kT == nullptr)) return fail(ULM_ERR_INVALID, "fwd stats: qT and kT go together");
+    fwd_stats_kernel<<<dim3((A + kSlots - 1) / kSlots, B), 256, 0, s>>>(r, w, g, q, q16, k16, qT, kT, nck, T, A,
+                                                                         NT);
     return check_launch("fwd_stats_kernel");
 }
 

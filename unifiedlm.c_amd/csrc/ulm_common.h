@@ -74,6 +74,27 @@ __device__ __forceinline__ void store_from_f32(void *p, size_t i, int dtype, flo
     else static_cast<_Float16 *>(p)[i] = static_cast<_Float16>(v);
 }
 
+// ---- scale schedule of the chunked state H = s G. The K-group kernel and the
+// producer of its pre-decayed update operand both follow it with the same
+// float operations, so the divisor folded into the operand is the one the
+// kernel assumes. Walk step k: read-out (k >= 1) renormalises s to 1 when it
+// fell below kRenorm; the update then sets s_{k+1} = lam^64 s (or keeps s = 1
+// when lam^64 itself is below kRenorm and G is decayed explicitly instead).
+constexpr float kRenorm = 0x1p-40f;
+
+__device__ __forceinline__ float state_lam64(float g) { return __expf(g * 64.f); }
+
+// 1 / s_{k+1}, the divisor folded into the update operand of walk step k
+__device__ inline float state_inv_scale(float lam64, int k) {
+    const bool tiny = lam64 < kRenorm;
+    float s = 1.f;
+    for (int i = 0; i <= k; ++i) {
+        if (i > 0 && !tiny && s < kRenorm) s = 1.f;
+        s = tiny ? 1.f : lam64 * s;
+    }
+    return 1.f / s;
+}
+
 inline bool valid_dtype(int dt) { return dt == ULM_F32 || dt == ULM_BF16 || dt == ULM_F16; }
 
 // Generic elementwise helpers (elementwise.hip).

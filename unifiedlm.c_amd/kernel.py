@@ -50,8 +50,10 @@ def _check_fm(r, v, g, w):
 
 
 class UnifiedMemory(torch.autograd.Function):
-    """Replaces kernel.py:199-233. Saves r, v16, g, w, q, q16, k16 and the
-    per-chunk evidence checkpoints (instead of the full c tensor)."""
+    """Replaces kernel.py:199-233. Saves r, v16, g, w, q and one opaque buffer
+    that the forward fills with what the backward needs (bf16 copies of q and
+    k, chunk-transposed operands, score tiles and the per-chunk evidence
+    checkpoints that stand in for the full c tensor)."""
 
     @staticmethod
     def forward(ctx, r, v, g, w):
@@ -62,24 +64,22 @@ class UnifiedMemory(torch.autograd.Function):
         v16 = v.to(torch.bfloat16).contiguous()
         g1 = g.float().reshape(1).contiguous()
         w32 = w.float().contiguous()
-        nt = (T + CHUNK - 1) // CHUNK
         q = torch.empty_like(r32)
         fast = torch.empty(B, T, D, device=r.device, dtype=v.dtype)
-        q16 = torch.empty(B, T, A, device=r.device, dtype=torch.bfloat16)
-        k16 = torch.empty_like(q16)
-        nck = torch.empty(B, nt, A, device=r.device, dtype=torch.float32)
+        saved_bytes = nat.lib().ulm_fm_saved_bytes(B, T, A, D)
+        saved = torch.empty(saved_bytes, device=r.device, dtype=torch.uint8)
         fdt = nat.dtype_code(v.dtype)
         ws_bytes = nat.lib().ulm_fm_fwd_workspace_bytes(B, T, A, D, fdt)
         ws = torch.empty(max(ws_bytes, 1), device=r.device, dtype=torch.uint8)
-        call("ulm_fm_fwd", ptr(r32), ptr(v16), ptr(g1), ptr(w32), ptr(q), ptr(fast), fdt, ptr(q16), ptr(k16),
-             ptr(nck), ptr(ws), ws_bytes, B, T, A, D, nat.stream_of(r))
-        ctx.save_for_backward(r32, v16, g1, w32, q, q16, k16, nck)
+        call("ulm_fm_fwd", ptr(r32), ptr(v16), ptr(g1), ptr(w32), ptr(q), ptr(fast), fdt, ptr(saved), saved_bytes,
+             ptr(ws), ws_bytes, B, T, A, D, nat.stream_of(r))
+        ctx.save_for_backward(r32, v16, g1, w32, q, saved)
         ctx.g_shape = g.shape
         return q, fast
 
     @staticmethod
     def backward(ctx, dq_out, dfast):
-        r, v16, g1, w, q, q16, k16, nck = ctx.saved_tensors
+        r, v16, g1, w, q, saved = ctx.saved_tensors
         B, T, A = r.shape
         D = v16.shape[-1]
         if dfast is None:
@@ -94,7 +94,7 @@ class UnifiedMemory(torch.autograd.Function):
         ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D)
         ws = torch.empty(ws_bytes, device=r.device, dtype=torch.uint8)
         ddt = nat.dtype_code(dfast.dtype)
-        call("ulm_fm_bwd", ptr(r), ptr(v16), ptr(g1), ptr(w), ptr(q), ptr(q16), ptr(k16), ptr(nck), ptr(dfast), ddt,
+        call("ulm_fm_bwd", ptr(r), ptr(v16), ptr(g1), ptr(w), ptr(q), ptr(saved), saved.numel(), ptr(dfast), ddt,
              ptr(dqo), ptr(dr), ptr(dv), ddt, ptr(dg), ptr(dw), ptr(ws), ws_bytes, B, T, A, D, nat.stream_of(r))
         return dr, dv, dg.reshape(ctx.g_shape), dw
 
@@ -104,9 +104,10 @@ def unified_memory(r, v, g, w):
     return UnifiedMemory.apply(r, v, g, w)
 
 
-def la(a, b, c, g, reverse=False):
+def la(a, b, c, g, reverse=False, split=False):
     """o_t = sum_{s<=t} lam^(t-s) (a_t . b_s) c_s (s>=t when reverse), fp32 output.
-    The chunked building block (kernel.py:183-196); a, b (B,T,K), c (B,T,V)."""
+    The chunked building block (kernel.py:183-196); a, b (B,T,K), c (B,T,V).
+    split carries the decayed state-update operand as a bf16 hi + lo pair."""
     nat.require_device(a, b, c, g)
     a16, b16, c16 = (x.to(torch.bfloat16).contiguous() for x in (a, b, c))
     B, T, K = a16.shape
@@ -114,8 +115,11 @@ def la(a, b, c, g, reverse=False):
     if b16.shape != a16.shape or c16.shape[:2] != a16.shape[:2]:
         raise ValueError("la: a, b must be (B,T,K) and c (B,T,V)")
     g1 = g.float().reshape(1).contiguous()
-    out = torch.zeros(B, T, V, device=a.device, dtype=torch.float32)
-    call("ulm_la", ptr(a16), ptr(b16), ptr(c16), ptr(g1), ptr(out), B, T, K, V, int(reverse), nat.stream_of(a))
+    out = torch.empty(B, T, V, device=a.device, dtype=torch.float32)
+    ws_bytes = nat.lib().ulm_la_workspace_bytes(B, T, K, V)
+    ws = torch.empty(max(ws_bytes, 1), device=a.device, dtype=torch.uint8)
+    call("ulm_la", ptr(a16), ptr(b16), ptr(c16), ptr(g1), ptr(out), B, T, K, V, int(reverse), int(split), ptr(ws),
+         ws_bytes, nat.stream_of(a))
     return out
 
 

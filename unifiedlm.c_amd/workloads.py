@@ -79,3 +79,10 @@ def la_flops(B, T, K, V, chunk=64):
     values V: state update 2KV, state read-out 2KV, intra scores 2CK and intra
     apply 2CV per token, intra tiles counted dense."""
     return B * T * (4 * K * V + 2 * chunk * (K + V))
+
+
+def la_kernel_flops(B, T, K, V, chunk=64):
+    """Algorithmic flops of one launch of the K-group chunked kernel: state
+    update 2KV, read-out 2KV and intra apply 2CV per token. The intra scores
+    (2CK per token) are computed once per chunk by the scores kernel."""
+    return B * T * (4 * K * V + 2 * chunk * V)

@@ -1,10 +1,8 @@
 // Per-chunk layouts consumed by the K-group chunked kernel (la_kgroup.hip).
 //
-//  * chunk_transpose: dst[b][n][x][i] = src[b][64n + i][x] as bf16, zero for
-//    64n + i >= T: the feature-major copy of each 64-position chunk, so the
-//    operands that contract over time load as 16 contiguous bytes (8
-//    positions of one feature); optionally also the pre-decayed copy that
-//    the chunked kernel's state update consumes.
+//  * chunk_transpose: the tiled copies of a (B, T, X) tensor that the chunked
+//    kernel loads (R and Q layouts of ulm_common.h; positions past T are zero),
+//    optionally with the pre-decayed copy its state update consumes.
 //  * chunk_scores: per chunk n, with S[i][j] = a_{64n+i} . b_{64n+j},
 //      P_lo[i][j] = S[i][j] lam^(i-j)  (j <= i, else 0)   forward walk
 //      P_up[i][j] = S[j][i] lam^(j-i)  (j >= i, else 0)   = P_lo^T
@@ -22,17 +20,20 @@ namespace chunks {
 
 constexpr int C = ULM_CHUNK;
 
-// grid (ceil(X/64), NT, B), 256 threads: one 64-position x 64-feature tile.
-// DEC = 0: raw copy only. DEC = 1 / 2: also the pre-decayed update operand of
-// the forward / reversed walk, bf16 hi (+ lo = the rounding remainder):
+// grid (ceil(X/64), NT, B), 256 threads: one 64-position x 64-feature block of
+// X (B, T, X) in any float dtype, rounded to bf16 (X % 32 == 0). Outputs, each
+// optional: raw (Q layout), the pre-decayed update operand hi (+ lo, the
+// rounding remainder) in the Q layout, and xr (R layout). DEC = 1 / 2 decays
+// for the forward / reversed walk:
 //   forward  lam^(63-i) x / s_{n+1}          at walk step n
 //   reversed lam^i      x / s_{NT-n}         at walk step NT-1-n
 // with s the state scale schedule of the chunked kernel (state_inv_scale).
 template <int DEC>
 __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__ src, int sdt, uint16_t *__restrict__ raw,
                                                         uint16_t *__restrict__ hi, uint16_t *__restrict__ lo,
-                                                        const float *__restrict__ g, int T, int X, int NT) {
-    __shared__ uint16_t tile[C][C + 2];
+                                                        uint16_t *__restrict__ xr, const float *__restrict__ g, int T,
+                                                        int X, int NT) {
+    __shared__ __align__(16) uint16_t tile[C][C + 8];   // [position][feature]
     const int x0 = blockIdx.x * C, n = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
     {
@@ -47,18 +48,32 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__
         }
     }
     __syncthreads();
-    const int xl = tid / 4, i0 = (tid % 4) * 16;   // feature row xl, 16 positions
+    if (xr) {
+        // R layout: 64 positions x 64 features are 8 tiles; thread -> 2 lanes of one tile
+        const int tl = tid / 32, mt = tl / 4, tf4 = tl % 4;
+        if (x0 + 16 * tf4 < X) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int l = 2 * (tid % 32) + u, row = 32 * mt + l % 32, col = 16 * tf4 + 8 * (l / 32);
+                *reinterpret_cast<uint4 *>(xr + r_index(b, n * C + row, x0 + col, NT, X)) =
+                    *reinterpret_cast<const uint4 *>(&tile[row][col]);
+            }
+        }
+    }
+    // Q layouts: feature xl, positions i0 .. i0+15 = two lanes' 16 bytes
+    const int xl = tid / 4, i0 = (tid % 4) * 16;
     const int x = x0 + xl;
     if (x >= X) return;
-    const size_t o = ((static_cast<size_t>(b) * NT + n) * X + x) * C + i0;
     if (raw) {
-        uint32_t w[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            w[e] = static_cast<uint32_t>(tile[i0 + 2 * e][xl]) | (static_cast<uint32_t>(tile[i0 + 2 * e + 1][xl]) << 16);
-        uint4 *d = reinterpret_cast<uint4 *>(raw + o);
-        d[0] = make_uint4(w[0], w[1], w[2], w[3]);
-        d[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        for (int h = 0; h < 2; ++h) {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                w[e] = static_cast<uint32_t>(tile[i0 + 8 * h + 2 * e][xl]) |
+                       (static_cast<uint32_t>(tile[i0 + 8 * h + 2 * e + 1][xl]) << 16);
+            *reinterpret_cast<uint4 *>(raw + q_index(b, n * C + i0 + 8 * h, x, NT, X)) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
     }
     if (DEC) {
         const float gl = g[0];
@@ -80,13 +95,11 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__
                 wl[e / 2] |= static_cast<uint32_t>(l) << 16;
             }
         }
-        uint4 *dh = reinterpret_cast<uint4 *>(hi + o);
-        dh[0] = make_uint4(wh[0], wh[1], wh[2], wh[3]);
-        dh[1] = make_uint4(wh[4], wh[5], wh[6], wh[7]);
-        if (lo) {
-            uint4 *dl = reinterpret_cast<uint4 *>(lo + o);
-            dl[0] = make_uint4(wl[0], wl[1], wl[2], wl[3]);
-            dl[1] = make_uint4(wl[4], wl[5], wl[6], wl[7]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const size_t o = q_index(b, n * C + i0 + 8 * h, x, NT, X);
+            *reinterpret_cast<uint4 *>(hi + o) = make_uint4(wh[4 * h], wh[4 * h + 1], wh[4 * h + 2], wh[4 * h + 3]);
+            if (lo) *reinterpret_cast<uint4 *>(lo + o) = make_uint4(wl[4 * h], wl[4 * h + 1], wl[4 * h + 2], wl[4 * h + 3]);
         }
     }
 }
@@ -95,75 +108,54 @@ __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// grid (NT, B), 256 threads. Wave w owns score tile (mt, nt) = (w/2, w%2) of the
-// 64 x 64 chunk, 32 x 32, contracted over all K (K % 8 == 0). Tile (0, 1) is
-// strictly above the diagonal: that wave only writes the zero tiles.
-__global__ __launch_bounds__(256) void scores_kernel(const uint16_t *__restrict__ A_, const uint16_t *__restrict__ B_,
+// grid (NT, B), 256 threads. From a and b in the R layout (K % 16 == 0), wave w
+// computes the score tile (mt, nt) = (w/2, w%2) of the 64 x 64 chunk over all K
+// (tile (0, 1) lies strictly above the diagonal and is zero in both outputs);
+// P_lo and P_up go out in the tile layout (p_index) through an LDS transpose.
+__global__ __launch_bounds__(256) void scores_kernel(const uint16_t *__restrict__ aR, const uint16_t *__restrict__ bR,
                                                      const float *__restrict__ g, uint16_t *__restrict__ Plo,
-                                                     uint16_t *__restrict__ Pup, int T, int K, int NT) {
+                                                     uint16_t *__restrict__ Pup, int K, int NT) {
+    __shared__ __align__(16) uint16_t slo[C][C + 8], sup[C][C + 8];   // [i][j]
     const int n = blockIdx.x, b = blockIdx.y;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int lr = lane % 32, lh = lane / 32;
     const int mt = wave >> 1, nt = wave & 1;
-    const size_t tile_off = (static_cast<size_t>(b) * NT + n) * C * C;
-    uint16_t *lo = Plo + tile_off, *up = Pup + tile_off;
-    if (mt == 0 && nt == 1) {
-        // P_lo rows 0..31 x cols 32..63 and P_up rows 32..63 x cols 0..31 are zero
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = 8 * (r / 4) + 4 * lh + (r % 4);
-            lo[row * C + 32 + lr] = 0;
-            up[(32 + row) * C + lr] = 0;
-        }
-        return;
-    }
-    const int ti = n * C + 32 * mt + lr, tj = n * C + 32 * nt + lr;
-    const bool oki = ti < T, okj = tj < T;
-    const uint16_t *pa = A_ + (static_cast<size_t>(b) * T + (oki ? ti : 0)) * K + 8 * lh;
-    const uint16_t *pb = B_ + (static_cast<size_t>(b) * T + (okj ? tj : 0)) * K + 8 * lh;
-    const int nks = K / 16;   // full 16-key steps; a trailing 8 keys (K % 16 == 8) taken by lh == 0
+    const int KT = K / 16;   // tiles per R row block
     f32x16 acc[4] = {};
-    int ks = 0;
-    for (; ks + 4 <= nks; ks += 4) {
+    if (!(mt == 0 && nt == 1)) {
+        const uint16_t *pa = aR + ((static_cast<size_t>(b) * (2 * NT) + 2 * n + mt) * KT) * kTileElems + 8 * lane;
+        const uint16_t *pb = bR + ((static_cast<size_t>(b) * (2 * NT) + 2 * n + nt) * KT) * kTileElems + 8 * lane;
+        int ks = 0;
+        for (; ks + 4 <= KT; ks += 4) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const bf16x8 x = oki ? *reinterpret_cast<const bf16x8 *>(pa + 16 * (ks + u)) : bf16x8{};
-            const bf16x8 y = okj ? *reinterpret_cast<const bf16x8 *>(pb + 16 * (ks + u)) : bf16x8{};
-            acc[u] = mfma(x, y, acc[u]);
+            for (int u = 0; u < 4; ++u)
+                acc[u] = mfma(*reinterpret_cast<const bf16x8 *>(pa + (ks + u) * kTileElems),
+                              *reinterpret_cast<const bf16x8 *>(pb + (ks + u) * kTileElems), acc[u]);
         }
-    }
-    for (; ks < nks; ++ks) {
-        const bf16x8 x = oki ? *reinterpret_cast<const bf16x8 *>(pa + 16 * ks) : bf16x8{};
-        const bf16x8 y = okj ? *reinterpret_cast<const bf16x8 *>(pb + 16 * ks) : bf16x8{};
-        acc[0] = mfma(x, y, acc[0]);
-    }
-    if (K % 16) {
-        const bool tail = lh == 0;
-        const bf16x8 x = (oki && tail) ? *reinterpret_cast<const bf16x8 *>(pa + 16 * nks) : bf16x8{};
-        const bf16x8 y = (okj && tail) ? *reinterpret_cast<const bf16x8 *>(pb + 16 * nks) : bf16x8{};
-        acc[1] = mfma(x, y, acc[1]);
+        for (; ks < KT; ++ks)
+            acc[0] = mfma(*reinterpret_cast<const bf16x8 *>(pa + ks * kTileElems),
+                          *reinterpret_cast<const bf16x8 *>(pb + ks * kTileElems), acc[0]);
     }
     const float gl = g[0];
     const int j = 32 * nt + lr;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        uint16_t vals[4];
+    for (int r = 0; r < 16; ++r) {
+        const int i = 32 * mt + 8 * (r / 4) + 4 * lh + (r % 4);
+        const float sv = acc[0][r] + acc[1][r] + acc[2][r] + acc[3][r];
+        const int lag = i - j;
+        const uint16_t v = f32_to_bf16_bits(lag >= 0 ? sv * __expf(gl * static_cast<float>(lag)) : 0.f);
+        slo[i][j] = v;   // P_lo[i][j]
+        sup[j][i] = v;   // P_up[j][i] = P_lo[i][j]
+    }
+    __syncthreads();
+    // 2 x 8 tiles of 1 KB: thread -> 2 lanes of one tile of each
+    const int tl = threadIdx.x / 32, tm = tl / 4, tq = tl % 4;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int r = 4 * q + m;
-            const int i = 32 * mt + 8 * q + 4 * lh + m;
-            const float s = acc[0][r] + acc[1][r] + acc[2][r] + acc[3][r];
-            const int lag = i - j;
-            const float v = lag >= 0 ? s * __expf(gl * static_cast<float>(lag)) : 0.f;
-            vals[m] = f32_to_bf16_bits(v);
-            lo[i * C + j] = vals[m];
-        }
-        // P_up[j][i .. i+3] = P_lo[i .. i+3][j]
-        const int i0 = 32 * mt + 8 * q + 4 * lh;
-        uint2 pk;
-        pk.x = static_cast<uint32_t>(vals[0]) | (static_cast<uint32_t>(vals[1]) << 16);
-        pk.y = static_cast<uint32_t>(vals[2]) | (static_cast<uint32_t>(vals[3]) << 16);
-        *reinterpret_cast<uint2 *>(up + j * C + i0) = pk;
+    for (int u = 0; u < 2; ++u) {
+        const int l = 2 * (threadIdx.x % 32) + u, i = 32 * tm + l % 32, j0 = 16 * tq + 8 * (l / 32);
+        const size_t o = p_index(b, n, i, j0, NT);
+        *reinterpret_cast<uint4 *>(Plo + o) = *reinterpret_cast<const uint4 *>(&slo[i][j0]);
+        *reinterpret_cast<uint4 *>(Pup + o) = *reinterpret_cast<const uint4 *>(&sup[i][j0]);
     }
 }
 
@@ -200,24 +192,27 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(const float *__rest
 
 }  // namespace chunks
 
-// raw, hi, lo: (B, NT, X, 64) bf16 or null. decay 0: raw only; 1 / 2: hi (+ lo)
+// Tiled copies of X (B, T, X): raw, hi, lo in the Q layout and xr in the R
+// layout, each bf16 or null (X % 32 == 0). decay 0: no hi / lo; 1 / 2: hi (+ lo)
 // hold the pre-decayed update operand of the forward / reversed walk.
-int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t *hi, uint16_t *lo, const float *g,
-                           int decay, int B, int T, int X, hipStream_t s) {
+int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t *hi, uint16_t *lo, uint16_t *xr,
+                           const float *g, int decay, int B, int T, int X, hipStream_t s) {
+    if (X % 32) return fail(ULM_ERR_INVALID, "chunk transpose: X=%d is not a multiple of 32", X);
     if (decay && !(hi && g)) return fail(ULM_ERR_INVALID, "chunk transpose: decayed output needs hi and g");
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
     const dim3 grid((X + ULM_CHUNK - 1) / ULM_CHUNK, NT, B);
-    if (decay == 1) chunks::transpose_kernel<1><<<grid, 256, 0, s>>>(src, src_dt, raw, hi, lo, g, T, X, NT);
-    else if (decay == 2) chunks::transpose_kernel<2><<<grid, 256, 0, s>>>(src, src_dt, raw, hi, lo, g, T, X, NT);
-    else chunks::transpose_kernel<0><<<grid, 256, 0, s>>>(src, src_dt, raw, nullptr, nullptr, g, T, X, NT);
+    if (decay == 1) chunks::transpose_kernel<1><<<grid, 256, 0, s>>>(src, src_dt, raw, hi, lo, xr, g, T, X, NT);
+    else if (decay == 2) chunks::transpose_kernel<2><<<grid, 256, 0, s>>>(src, src_dt, raw, hi, lo, xr, g, T, X, NT);
+    else chunks::transpose_kernel<0><<<grid, 256, 0, s>>>(src, src_dt, raw, nullptr, nullptr, xr, g, T, X, NT);
     return check_launch("chunk transpose_kernel");
 }
 
-int launch_chunk_scores(const uint16_t *a, const uint16_t *b, const float *g, uint16_t *Plo, uint16_t *Pup, int B,
+// a, b in the R layout (K % 16 == 0); P_lo, P_up in the tile layout of p_index.
+int launch_chunk_scores(const uint16_t *aR, const uint16_t *bR, const float *g, uint16_t *Plo, uint16_t *Pup, int B,
                         int T, int K, hipStream_t s) {
-    if (K % 8) return fail(ULM_ERR_UNSUPPORTED, "chunk scores: K=%d is not a multiple of 8", K);
+    if (K % 16) return fail(ULM_ERR_UNSUPPORTED, "chunk scores: K=%d is not a multiple of 16", K);
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
-    chunks::scores_kernel<<<dim3(NT, B), 256, 0, s>>>(a, b, g, Plo, Pup, T, K, NT);
+    chunks::scores_kernel<<<dim3(NT, B), 256, 0, s>>>(aR, bR, g, Plo, Pup, K, NT);
     return check_launch("chunk scores_kernel");
 }
 

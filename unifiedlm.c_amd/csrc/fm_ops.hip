@@ -6,18 +6,19 @@
 //   fast = LA(q, k, v)          dq_f = LA(dfast, v, k)
 //   dk_f = LA_rev(v, dfast, q)  dv   = LA_rev(k, q, dfast)
 // For aligned shapes (A and D multiples of 32) they run on the K-group kernel
-// (la_kgroup.hip), which reads a in natural layout, b and c chunk-transposed
-// and the intra-chunk matrix P from chunk_scores. The reversed products walk
-// the forward chunks backwards, so one transposed copy per tensor serves both
-// directions and the score tiles pair up: P_dv = P_fwd^T, P_dk = P_dq^T. The
-// decay of the state update always rides on the D-sized tensor of the
-// product (v or dfast), pre-multiplied into a bf16 hi + lo copy by
-// chunk_transpose: v forward for fast and dq, dfast reversed for dk and dv.
+// (la_kgroup.hip), whose operands are the tiled copies of ulm_common.h: the
+// read-out operand a in the R layout, the update operands and the raw c of the
+// intra-chunk product in the Q layout, the intra-chunk matrices from
+// chunk_scores. The reversed products walk the forward chunks backwards, so one
+// tiled copy per tensor serves both directions and the score tiles pair up:
+// P_dv = P_fwd^T, P_dk = P_dq^T. The decay of the state update always rides on
+// the D-sized tensor of the product (v or dfast), pre-multiplied into a bf16
+// hi + lo copy: v forward for fast and dq, dfast reversed for dk and dv.
 // The forward keeps what the backward needs in one "saved" buffer:
-//   q16, k16 (B,T,A) bf16; qT, kT (B,NT,A,64) bf16; vT, vT~hi, vT~lo
-//   (B,NT,D,64) bf16; P_dv (B,NT,64,64) bf16; n_ckpt (B,NT,A) fp32.
+//   qR, kR, qQ, kQ (B, NT, 64 A) bf16 tiles; vR, vQ, vQ~hi, vQ~lo (B, NT, 64 D);
+//   P_dv (B, NT, 64, 64) bf16 tiles; n_ckpt (B, NT, A) fp32.
 // Other shapes use the generic kernel of fm_chunk.hip (atomics into zeroed
-// fp32 outputs) on the natural layouts only.
+// fp32 outputs) on natural bf16 copies of q and k.
 #include "ulm_common.h"
 
 namespace ulm {
@@ -32,14 +33,15 @@ int launch_la_kgroup(const uint16_t *a, const uint16_t *ua, const uint16_t *ualo
                      const uint16_t *cr, const uint16_t *P, const float *g, float *out, int B, int T, int K, int V,
                      bool reverse, hipStream_t s);
 // fm_chunks.hip
-int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t *hi, uint16_t *lo, const float *g,
-                           int decay, int B, int T, int X, hipStream_t s);
-int launch_chunk_scores(const uint16_t *a, const uint16_t *b, const float *g, uint16_t *Plo, uint16_t *Pup, int B,
+int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t *hi, uint16_t *lo, uint16_t *xr,
+                           const float *g, int decay, int B, int T, int X, hipStream_t s);
+int launch_chunk_scores(const uint16_t *aR, const uint16_t *bR, const float *g, uint16_t *Plo, uint16_t *Pup, int B,
                         int T, int K, hipStream_t s);
 int launch_partial_reduce(const float *part, int nK, size_t n, void *out, int odt, hipStream_t s);
 // fm_stats.hip
-int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16, uint16_t *k16,
-                     uint16_t *qT, uint16_t *kT, float *nck, int B, int T, int A, hipStream_t s);
+int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
+                     uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, int B, int T, int A,
+                     hipStream_t s);
 size_t bwd_stats_partial_bytes(int B, int A);
 int launch_bwd_stats(const float *dqf, const float *dqo, const float *q, const float *r, const float *nck,
                      const float *w, const float *g, const float *dkf, float *dr, float *dw, float *dg, void *part,
@@ -69,25 +71,30 @@ bool fm_aligned(int B, int T, int A, int D) {
 }
 
 struct Saved {
-    uint16_t *q16, *k16, *qT, *kT, *vT, *vTh, *vTl, *Pdv;
+    uint16_t *q16n, *k16n;                          // generic path
+    uint16_t *qR, *kR, *qQ, *kQ, *vR, *vQ, *vQh, *vQl, *Pdv;   // K-group path
     float *nck;
     size_t bytes;
 };
 
 Saved saved_layout(void *base, int B, int T, int A, int D) {
-    const size_t NT = nt_of(T), na = static_cast<size_t>(B) * T * A;
-    const bool al = fm_aligned(B, T, A, D);
+    const size_t NT = nt_of(T);
+    const size_t na = static_cast<size_t>(B) * T * A, ta = B * NT * 64 * A, td = B * NT * 64 * D;
     Carver c(base);
     Saved s{};
-    s.q16 = c.take<uint16_t>(na);
-    s.k16 = c.take<uint16_t>(na);
-    if (al) {
-        s.qT = c.take<uint16_t>(B * NT * A * ULM_CHUNK);
-        s.kT = c.take<uint16_t>(B * NT * A * ULM_CHUNK);
-        s.vT = c.take<uint16_t>(B * NT * D * ULM_CHUNK);
-        s.vTh = c.take<uint16_t>(B * NT * D * ULM_CHUNK);
-        s.vTl = c.take<uint16_t>(B * NT * D * ULM_CHUNK);
+    if (fm_aligned(B, T, A, D)) {
+        s.qR = c.take<uint16_t>(ta);
+        s.kR = c.take<uint16_t>(ta);
+        s.qQ = c.take<uint16_t>(ta);
+        s.kQ = c.take<uint16_t>(ta);
+        s.vR = c.take<uint16_t>(td);
+        s.vQ = c.take<uint16_t>(td);
+        s.vQh = c.take<uint16_t>(td);
+        s.vQl = c.take<uint16_t>(td);
         s.Pdv = c.take<uint16_t>(B * NT * ULM_CHUNK * ULM_CHUNK);
+    } else {
+        s.q16n = c.take<uint16_t>(na);
+        s.k16n = c.take<uint16_t>(na);
     }
     s.nck = c.take<float>(B * NT * A);
     s.bytes = c.off;
@@ -116,7 +123,8 @@ FwdWs fwd_layout(void *base, int B, int T, int A, int D, int fast_dtype) {
 }
 
 struct BwdWs {
-    uint16_t *do16, *doT, *doTh, *doTl, *Pdq, *Pdk;
+    uint16_t *do16;                           // generic path
+    uint16_t *doR, *doQ, *doQh, *doQl, *Pdq, *Pdk;   // K-group path
     float *dqf, *dkf, *part;
     void *stats;
     size_t bytes;
@@ -124,15 +132,16 @@ struct BwdWs {
 
 BwdWs bwd_layout(void *base, int B, int T, int A, int D) {
     const size_t NT = nt_of(T), nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
+    const size_t td = B * NT * 64 * D;
     Carver c(base);
     BwdWs w{};
-    w.do16 = c.take<uint16_t>(nd);
     w.dqf = c.take<float>(na);
     w.dkf = c.take<float>(na);
     if (fm_aligned(B, T, A, D)) {
-        w.doT = c.take<uint16_t>(B * NT * D * ULM_CHUNK);
-        w.doTh = c.take<uint16_t>(B * NT * D * ULM_CHUNK);
-        w.doTl = c.take<uint16_t>(B * NT * D * ULM_CHUNK);
+        w.doR = c.take<uint16_t>(td);
+        w.doQ = c.take<uint16_t>(td);
+        w.doQh = c.take<uint16_t>(td);
+        w.doQl = c.take<uint16_t>(td);
         w.Pdq = c.take<uint16_t>(B * NT * ULM_CHUNK * ULM_CHUNK);
         w.Pdk = c.take<uint16_t>(B * NT * ULM_CHUNK * ULM_CHUNK);
         const int nkd = la_kgroup_groups(D), nka = la_kgroup_groups(A);
@@ -140,6 +149,7 @@ BwdWs bwd_layout(void *base, int B, int T, int A, int D) {
         if (nkd > 1) part = part > nkd * na ? part : nkd * na;
         w.part = c.take<float>(part);
     } else {
+        w.do16 = c.take<uint16_t>(nd);
         w.part = c.take<float>(nd);   // fp32 dv accumulator
     }
     w.stats = c.take<char>(bwd_stats_partial_bytes(B, A));
@@ -165,10 +175,11 @@ using namespace ulm;
 extern "C" size_t ulm_la_workspace_bytes(int B, int T, int K, int V) {
     if (B <= 0 || T <= 0 || K <= 0 || V <= 0) return 0;
     if (!la_kgroup_supported(B, T, K, V)) return 0;
-    const size_t NT = nt_of(T);
+    const size_t NT = nt_of(T), tk = B * NT * 64 * K, tv = B * NT * 64 * V;
     Carver c(nullptr);
-    c.take<uint16_t>(2 * B * NT * K * ULM_CHUNK);             // decayed b^T, hi and lo
-    c.take<uint16_t>(B * NT * V * ULM_CHUNK);                 // c^T
+    c.take<uint16_t>(2 * tk);                                 // a and b, R layout
+    c.take<uint16_t>(2 * tk);                                 // decayed b, Q layout, hi and lo
+    c.take<uint16_t>(tv);                                     // c, Q layout
     c.take<uint16_t>(2 * B * NT * ULM_CHUNK * ULM_CHUNK);     // P_lo, P_up
     const int nkg = la_kgroup_groups(K);
     if (nkg > 1) c.take<float>(static_cast<size_t>(nkg) * B * T * V);
@@ -188,20 +199,23 @@ extern "C" int ulm_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
         ULM_TRY(launch_fill_zero(out, static_cast<size_t>(B) * T * V * sizeof(float), s));
         return launch_la_generic(a, b, c, g, out, B, T, K, V, reverse != 0, s);
     }
-    const size_t NT = nt_of(T), nbT = B * NT * K * ULM_CHUNK;
+    const size_t NT = nt_of(T), tk = B * NT * 64 * K, tv = B * NT * 64 * V;
     Carver cv(workspace);
-    uint16_t *bTh = cv.take<uint16_t>(2 * nbT);
-    uint16_t *bTl = bTh + nbT;
-    uint16_t *cT = cv.take<uint16_t>(B * NT * V * ULM_CHUNK);
+    uint16_t *aR = cv.take<uint16_t>(2 * tk);
+    uint16_t *bR = aR + tk;
+    uint16_t *bQh = cv.take<uint16_t>(2 * tk);
+    uint16_t *bQl = bQh + tk;
+    uint16_t *cQ = cv.take<uint16_t>(tv);
     uint16_t *Plo = cv.take<uint16_t>(2 * B * NT * ULM_CHUNK * ULM_CHUNK);
     uint16_t *Pup = Plo + B * NT * ULM_CHUNK * ULM_CHUNK;
     const int nkg = la_kgroup_groups(K);
     float *part = nkg > 1 ? cv.take<float>(static_cast<size_t>(nkg) * B * T * V) : out;
     // the decay of the state update rides on b
-    ULM_TRY(launch_chunk_transpose(b, ULM_BF16, nullptr, bTh, split ? bTl : nullptr, g, reverse ? 2 : 1, B, T, K, s));
-    ULM_TRY(launch_chunk_transpose(c, ULM_BF16, cT, nullptr, nullptr, g, 0, B, T, V, s));
-    ULM_TRY(launch_chunk_scores(reverse ? b : a, reverse ? a : b, g, Plo, Pup, B, T, K, s));
-    ULM_TRY(launch_la_kgroup(a, bTh, split ? bTl : nullptr, cT, cT, reverse ? Pup : Plo, g, part, B, T, K, V,
+    ULM_TRY(launch_chunk_transpose(a, ULM_BF16, nullptr, nullptr, nullptr, aR, g, 0, B, T, K, s));
+    ULM_TRY(launch_chunk_transpose(b, ULM_BF16, nullptr, bQh, split ? bQl : nullptr, bR, g, reverse ? 2 : 1, B, T, K, s));
+    ULM_TRY(launch_chunk_transpose(c, ULM_BF16, cQ, nullptr, nullptr, nullptr, g, 0, B, T, V, s));
+    ULM_TRY(launch_chunk_scores(reverse ? bR : aR, reverse ? aR : bR, g, Plo, Pup, B, T, K, s));
+    ULM_TRY(launch_la_kgroup(aR, bQh, split ? bQl : nullptr, cQ, cQ, reverse ? Pup : Plo, g, part, B, T, K, V,
                              reverse != 0, s));
     if (nkg > 1) ULM_TRY(launch_partial_reduce(part, nkg, static_cast<size_t>(B) * T * V, out, ULM_F32, s));
     return ULM_OK;
@@ -235,20 +249,21 @@ extern "C" int ulm_fm_fwd(const float *r, const uint16_t *v16, const float *g, c
     const Saved sv = saved_layout(saved, B, T, A, D);
     const FwdWs ws = fwd_layout(workspace, B, T, A, D, fast_dtype);
     const size_t nf = static_cast<size_t>(B) * T * D;
-    ULM_TRY(launch_fwd_stats(r, w, g, q, sv.q16, sv.k16, sv.qT, sv.kT, sv.nck, B, T, A, s));
     if (fm_aligned(B, T, A, D)) {
         const int nkg = la_kgroup_groups(A);
         float *acc = ws.part ? ws.part : static_cast<float *>(fast);
-        ULM_TRY(launch_chunk_transpose(v16, ULM_BF16, sv.vT, sv.vTh, sv.vTl, g, 1, B, T, D, s));
-        ULM_TRY(launch_chunk_scores(sv.q16, sv.k16, g, ws.Pf, sv.Pdv, B, T, A, s));
+        ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, sv.qR, sv.kR, sv.qQ, sv.kQ, sv.nck, B, T, A, s));
+        ULM_TRY(launch_chunk_transpose(v16, ULM_BF16, sv.vQ, sv.vQh, sv.vQl, sv.vR, g, 1, B, T, D, s));
+        ULM_TRY(launch_chunk_scores(sv.qR, sv.kR, g, ws.Pf, sv.Pdv, B, T, A, s));
         // fast = LA(q, k, v): update k^T v~, intra on the raw v
-        ULM_TRY(launch_la_kgroup(sv.q16, sv.kT, nullptr, sv.vTh, sv.vT, ws.Pf, g, acc, B, T, A, D, false, s));
+        ULM_TRY(launch_la_kgroup(sv.qR, sv.kQ, nullptr, sv.vQh, sv.vQ, ws.Pf, g, acc, B, T, A, D, false, s));
         if (ws.part) ULM_TRY(launch_partial_reduce(ws.part, nkg, nf, fast, fast_dtype, s));
         return ULM_OK;
     }
+    ULM_TRY(launch_fwd_stats(r, w, g, q, sv.q16n, sv.k16n, nullptr, nullptr, nullptr, nullptr, sv.nck, B, T, A, s));
     float *acc = fast_dtype == ULM_F32 ? static_cast<float *>(fast) : ws.part;
     ULM_TRY(launch_fill_zero(acc, nf * sizeof(float), s));
-    ULM_TRY(launch_la_generic(sv.q16, sv.k16, v16, g, acc, B, T, A, D, false, s));
+    ULM_TRY(launch_la_generic(sv.q16n, sv.k16n, v16, g, acc, B, T, A, D, false, s));
     if (fast_dtype != ULM_F32) ULM_TRY(launch_convert(acc, ULM_F32, fast, fast_dtype, nf, s));
     return ULM_OK;
 }
@@ -275,38 +290,38 @@ extern "C" int ulm_fm_bwd(const float *r, const uint16_t *v16, const float *g, c
     const Saved sv = saved_layout(const_cast<void *>(saved), B, T, A, D);
     const BwdWs ws = bwd_layout(workspace, B, T, A, D);
     const size_t nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
-    const uint16_t *do16 = static_cast<const uint16_t *>(dfast);
-    if (dfast_dtype != ULM_BF16) {
-        ULM_TRY(launch_convert(dfast, dfast_dtype, ws.do16, ULM_BF16, nd, s));
-        do16 = ws.do16;
-    }
     if (fm_aligned(B, T, A, D)) {
         const int nkd = la_kgroup_groups(D), nka = la_kgroup_groups(A);
-        ULM_TRY(launch_chunk_transpose(do16, ULM_BF16, ws.doT, ws.doTh, ws.doTl, g, 2, B, T, D, s));
-        ULM_TRY(launch_chunk_scores(do16, v16, g, ws.Pdq, ws.Pdk, B, T, D, s));
+        ULM_TRY(launch_chunk_transpose(dfast, dfast_dtype, ws.doQ, ws.doQh, ws.doQl, ws.doR, g, 2, B, T, D, s));
+        ULM_TRY(launch_chunk_scores(ws.doR, sv.vR, g, ws.Pdq, ws.Pdk, B, T, D, s));
         // dq_f = LA(dfast, v, k): keys = D, values = A; update v~^T k.
         // dk_f = LA_rev(v, dfast, q): update dfast~^T q.
         // Both feed the positional d/dg identity, whose cancellation amplifies
         // rounding, so their decayed operand is carried as bf16 hi + lo.
-        ULM_TRY(launch_la_kgroup(do16, sv.vTh, sv.vTl, sv.kT, sv.kT, ws.Pdq, g, nkd > 1 ? ws.part : ws.dqf, B, T, D, A,
+        ULM_TRY(launch_la_kgroup(ws.doR, sv.vQh, sv.vQl, sv.kQ, sv.kQ, ws.Pdq, g, nkd > 1 ? ws.part : ws.dqf, B, T, D, A,
                                  false, s));
         if (nkd > 1) ULM_TRY(launch_partial_reduce(ws.part, nkd, na, ws.dqf, ULM_F32, s));
-        ULM_TRY(launch_la_kgroup(v16, ws.doTh, ws.doTl, sv.qT, sv.qT, ws.Pdk, g, nkd > 1 ? ws.part : ws.dkf, B, T, D, A,
+        ULM_TRY(launch_la_kgroup(sv.vR, ws.doQh, ws.doQl, sv.qQ, sv.qQ, ws.Pdk, g, nkd > 1 ? ws.part : ws.dkf, B, T, D, A,
                                  true, s));
         if (nkd > 1) ULM_TRY(launch_partial_reduce(ws.part, nkd, na, ws.dkf, ULM_F32, s));
         // dv = LA_rev(k, q, dfast): keys = A, values = D; update q^T dfast~, intra on the raw dfast
         const bool direct = nka == 1 && dv_dtype == ULM_F32;
-        ULM_TRY(launch_la_kgroup(sv.k16, sv.qT, nullptr, ws.doTh, ws.doT, sv.Pdv, g,
+        ULM_TRY(launch_la_kgroup(sv.kR, sv.qQ, nullptr, ws.doQh, ws.doQ, sv.Pdv, g,
                                  direct ? static_cast<float *>(dv) : ws.part, B, T, A, D, true, s));
         if (!direct) ULM_TRY(launch_partial_reduce(ws.part, nka, nd, dv, dv_dtype, s));
     } else {
+        const uint16_t *do16 = static_cast<const uint16_t *>(dfast);
+        if (dfast_dtype != ULM_BF16) {
+            ULM_TRY(launch_convert(dfast, dfast_dtype, ws.do16, ULM_BF16, nd, s));
+            do16 = ws.do16;
+        }
         ULM_TRY(launch_fill_zero(ws.dqf, na * 4, s));
-        ULM_TRY(launch_la_generic(do16, v16, sv.k16, g, ws.dqf, B, T, D, A, false, s));
+        ULM_TRY(launch_la_generic(do16, v16, sv.k16n, g, ws.dqf, B, T, D, A, false, s));
         ULM_TRY(launch_fill_zero(ws.dkf, na * 4, s));
-        ULM_TRY(launch_la_generic(v16, do16, sv.q16, g, ws.dkf, B, T, D, A, true, s));
+        ULM_TRY(launch_la_generic(v16, do16, sv.q16n, g, ws.dkf, B, T, D, A, true, s));
         float *dv_acc = dv_dtype == ULM_F32 ? static_cast<float *>(dv) : ws.part;
         ULM_TRY(launch_fill_zero(dv_acc, nd * 4, s));
-        ULM_TRY(launch_la_generic(sv.k16, sv.q16, do16, g, dv_acc, B, T, A, D, true, s));
+        ULM_TRY(launch_la_generic(sv.k16n, sv.q16n, do16, g, dv_acc, B, T, A, D, true, s));
         if (dv_dtype != ULM_F32) ULM_TRY(launch_convert(dv_acc, ULM_F32, dv, dv_dtype, nd, s));
     }
     return launch_bwd_stats(ws.dqf, dq_out, q, r, sv.nck, w, g, ws.dkf, dr, dw, dg, ws.stats, B, T, A, s);

@@ -30,16 +30,23 @@ __device__ __forceinline__ float pow_int(float x, int e) {
     return r;
 }
 
+// Outputs besides q and n_ckpt (each may be null): q16n, k16n natural bf16
+// copies; qR, kR in the R layout and qQ, kQ in the Q layout (the chunked
+// kernel's operand tiles; A % 32 == 0). Positions past T are zero in R and Q.
 __global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict__ r, const float *__restrict__ w,
                                                         const float *__restrict__ g, float *__restrict__ q,
-                                                        uint16_t *__restrict__ q16, uint16_t *__restrict__ k16,
-                                                        uint16_t *__restrict__ qT, uint16_t *__restrict__ kT,
+                                                        uint16_t *__restrict__ q16n, uint16_t *__restrict__ k16n,
+                                                        uint16_t *__restrict__ qR, uint16_t *__restrict__ kR,
+                                                        uint16_t *__restrict__ qQ, uint16_t *__restrict__ kQ,
                                                         float *__restrict__ nck, int T, int A, int NT) {
     __shared__ float tot[4][kSlots];
+    __shared__ __align__(16) uint16_t sq[ULM_CHUNK][kSlots + 8], sk[ULM_CHUNK][kSlots + 8];   // [position][slot]
     const int s = threadIdx.x % kSlots, j = threadIdx.x / kSlots;
-    const int a = blockIdx.x * kSlots + s;
+    const int a0 = blockIdx.x * kSlots;
+    const int a = a0 + s;
     const bool va = a < A;
-    const size_t b = blockIdx.y;
+    const int b = blockIdx.y;
+    const size_t bs = blockIdx.y;
     const float lam = __expf(g[0]);
     const float lam16 = pow_int(lam, kSeg);
     const float wa = va ? w[a] : 1.f;
@@ -50,9 +57,9 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict_
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
             const int t = t0 + i;
-            rv[i] = (va && t < T) ? r[(b * T + t) * A + a] : 0.f;
+            rv[i] = (va && t < T) ? r[(bs * T + t) * A + a] : 0.f;
         }
-        kv[0] = (va && t0 >= 1 && t0 - 1 < T) ? r[(b * T + t0 - 1) * A + a] : 0.f;
+        kv[0] = (va && t0 >= 1 && t0 - 1 < T) ? r[(bs * T + t0 - 1) * A + a] : 0.f;
 #pragma unroll
         for (int i = 1; i < kSeg; ++i) kv[i] = rv[i - 1];
         float acc = 0.f;
@@ -66,22 +73,26 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict_
         float cj = carry;
         for (int m = 0; m < j; ++m) cj = lam16 * cj + tot[m][s];
         float pw = lam;
-        uint32_t qpk[kSeg / 2], kpk[kSeg / 2];   // bf16 pairs for the chunk-transposed copies
+        uint32_t qpk[kSeg / 2], kpk[kSeg / 2];   // bf16 pairs of this thread's 16 positions
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
             const int t = t0 + i;
             const float ct = wa + (pw * cj + nl[i]);
             pw *= lam;
-            uint16_t qb = 0, kb = 0;   // positions past T are zero in the transposed copies
+            uint16_t qb = 0, kb = 0;   // positions past T are zero in the tiled copies
             if (va && t < T) {
-                const size_t o = (b * T + t) * A + a;
+                const size_t o = (bs * T + t) * A + a;
                 const float qt = rv[i] / ct;
                 qb = f32_to_bf16_bits(qt);
                 kb = f32_to_bf16_bits(kv[i]);
                 q[o] = qt;
-                q16[o] = qb;
-                k16[o] = kb;
+                if (q16n) {
+                    q16n[o] = qb;
+                    k16n[o] = kb;
+                }
             }
+            sq[j * kSeg + i][s] = qb;
+            sk[j * kSeg + i][s] = kb;
             if (i % 2 == 0) {
                 qpk[i / 2] = qb;
                 kpk[i / 2] = kb;
@@ -90,21 +101,34 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict_
                 kpk[i / 2] |= static_cast<uint32_t>(kb) << 16;
             }
         }
-        if (kT && va) {
-            // (B, NT, A, 64): this thread's 16 positions of slot a are 32 contiguous bytes
-            const size_t o = ((b * NT + n) * A + a) * ULM_CHUNK + j * kSeg;
-            uint4 *dq = reinterpret_cast<uint4 *>(qT + o);
-            uint4 *dk = reinterpret_cast<uint4 *>(kT + o);
-            dq[0] = make_uint4(qpk[0], qpk[1], qpk[2], qpk[3]);
-            dq[1] = make_uint4(qpk[4], qpk[5], qpk[6], qpk[7]);
-            dk[0] = make_uint4(kpk[0], kpk[1], kpk[2], kpk[3]);
-            dk[1] = make_uint4(kpk[4], kpk[5], kpk[6], kpk[7]);
+        if (qQ && va) {
+            // Q layout: this thread's positions 16 j .. 16 j + 15 of slot a are two lanes' 16 bytes
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const size_t o = q_index(b, n * ULM_CHUNK + kSeg * j + 8 * h, a, NT, A);
+                *reinterpret_cast<uint4 *>(qQ + o) = make_uint4(qpk[4 * h], qpk[4 * h + 1], qpk[4 * h + 2], qpk[4 * h + 3]);
+                *reinterpret_cast<uint4 *>(kQ + o) = make_uint4(kpk[4 * h], kpk[4 * h + 1], kpk[4 * h + 2], kpk[4 * h + 3]);
+            }
         }
-        if (j == 0 && va) nck[(b * NT + n) * A + a] = carry;
+        if (j == 0 && va) nck[(bs * NT + n) * A + a] = carry;
         float nc = carry;
         for (int m = 0; m < 4; ++m) nc = lam16 * nc + tot[m][s];
         carry = nc;
-        __syncthreads();
+        __syncthreads();   // sq, sk complete; tot free for the next chunk
+        if (qR) {
+            // R layout: the block's 64 positions x 64 slots are 8 tiles; thread -> 2 lanes of one tile
+            const int tl = threadIdx.x / 32, mt = tl / 4, tf4 = tl % 4;
+            if (a0 + 16 * tf4 < A) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int l = 2 * (threadIdx.x % 32) + u, row = 32 * mt + l % 32, col = 16 * tf4 + 8 * (l / 32);
+                    const size_t o = r_index(b, n * ULM_CHUNK + row, a0 + col, NT, A);
+                    *reinterpret_cast<uint4 *>(qR + o) = *reinterpret_cast<const uint4 *>(&sq[row][col]);
+                    *reinterpret_cast<uint4 *>(kR + o) = *reinterpret_cast<const uint4 *>(&sk[row][col]);
+                }
+            }
+        }
+        __syncthreads();   // sq, sk read before the next chunk writes them
     }
 }
 
@@ -239,13 +263,18 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(const float *__restri
     }
 }
 
-// qT, kT: (B, NT, A, 64) chunk-transposed bf16 copies of q and k (both or neither)
-int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16, uint16_t *k16,
-                     uint16_t *qT, uint16_t *kT, float *nck, int B, int T, int A, hipStream_t s) {
+// q16n, k16n: natural bf16 copies (both or neither); qR, kR, qQ, kQ: tiled
+// copies (all or none; A % 32 == 0).
+int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
+                     uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, int B, int T, int A,
+                     hipStream_t s) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
-    if ((qT == nullptr) != (kT == nullptr)) return fail(ULM_ERR_INVALID, "fwd stats: qT and kT go together");
-    fwd_stats_kernel<<<dim3((A + kSlots - 1) / kSlots, B), 256, 0, s>>>(r, w, g, q, q16, k16, qT, kT, nck, T, A,
-                                                                         NT);
+    if ((q16n == nullptr) != (k16n == nullptr)) return fail(ULM_ERR_INVALID, "fwd stats: q16n and k16n go together");
+    const bool tiled = qR || kR || qQ || kQ;
+    if (tiled && !(qR && kR && qQ && kQ && A % 32 == 0))
+        return fail(ULM_ERR_INVALID, "fwd stats: tiled copies need all four outputs and A %% 32 == 0");
+    fwd_stats_kernel<<<dim3((A + kSlots - 1) / kSlots, B), 256, 0, s>>>(r, w, g, q, q16n, k16n, qR, kR, qQ, kQ, nck,
+                                                                         T, A, NT);
     return check_launch("fwd_stats_kernel");
 }
 

@@ -73,7 +73,6 @@ __device__ __forceinline__ rsrc_t rsrc(const void *base, size_t bytes) {
 __device__ __forceinline__ bf16x8 bld(rsrc_t rs, uint32_t off) {
     return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off), 0, 0));
 }
-__device__ __forceinline__ int key_of_row(int rho) { return (rho & ~12) | ((rho & 4) << 1) | ((rho & 8) >> 1); }
 __device__ __forceinline__ float uniform(float x) {
     return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
 }
@@ -125,32 +124,35 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
     const float lam64 = state_lam64(gl);
     const bool tiny = lam64 < kRenorm;
 
-    // ---- operand buffers, one batch row each; byte offsets = lane part + uniform part
-    const size_t rowA = static_cast<size_t>(T) * K, rowU = static_cast<size_t>(NT) * K * C;
-    const size_t rowB = static_cast<size_t>(NT) * V * C, rowP = static_cast<size_t>(NT) * C * C;
+    // ---- operand buffers, one batch row each (tile layouts of ulm_common.h);
+    // byte offset of a tile load = 16 lane + a uniform tile offset
+    const int KT16 = K / 16, KT32 = K / 32, VT32 = V / 32;
+    const size_t rowA = static_cast<size_t>(2 * NT) * KT16 * kTileElems;    // R layout
+    const size_t rowU = static_cast<size_t>(NT) * KT32 * 4 * kTileElems;    // Q layout, keys
+    const size_t rowB = static_cast<size_t>(NT) * VT32 * 4 * kTileElems;    // Q layout, values
+    const size_t rowP = static_cast<size_t>(NT) * 8 * kTileElems;           // score tiles
     const rsrc_t ra = rsrc(A_ + b * rowA, rowA * 2);
     const rsrc_t rua = rsrc(UA + b * rowU, rowU * 2);
     const rsrc_t rul = rsrc((SPLIT ? UAlo : UA) + b * rowU, rowU * 2);
     const rsrc_t rub = rsrc(UB + b * rowB, rowB * 2);
     const rsrc_t rcr = rsrc(CR + b * rowB, rowB * 2);
     const rsrc_t rp = rsrc(P + b * rowP, rowP * 2);
-    uint32_t a_lane[2], ub_lane[2], cr_lane[2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) a_lane[mt] = static_cast<uint32_t>(((32 * mt + lr) * K + 8 * lh) * 2);
+    constexpr uint32_t TB = kTileElems * 2;   // bytes per tile
+    const uint32_t lane16 = static_cast<uint32_t>(lane * 16);
+    uint32_t ub_lane[2], cr_lane[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-        ub_lane[nt] = (nt == 0 || nt1) ? static_cast<uint32_t>(((32 * nt + lr) * C + 8 * lh) * 2) : OOB;
-        cr_lane[nt] = (nt == 0 || nt1) ? static_cast<uint32_t>(((32 * nt + lr) * C + 16 * iq + 8 * lh) * 2) : OOB;
+        ub_lane[nt] = (nt == 0 || nt1) ? lane16 + nt * 4 * TB : OOB;
+        cr_lane[nt] = (nt == 0 || nt1) ? lane16 + nt * 4 * TB + iq * TB : OOB;
     }
-    const uint32_t p_lane = static_cast<uint32_t>(((32 * imt + lr) * C + 16 * iq + 8 * lh) * 2);
-    const uint32_t ua_lane = static_cast<uint32_t>((key_of_row(lr) * C + 8 * lh) * 2);
+    const uint32_t p_lane = lane16 + (imt * 4 + iq) * TB;
     // uniform key-block offsets (bytes) into a rows and into the update operand; OOB past the group
     uint32_t a_blk[MH], u_blk[MH];
 #pragma unroll
     for (int mh = 0; mh < MH; ++mh) {
         const int blk = blk0 + wave + WAVES * mh;
-        a_blk[mh] = uniform(blk < blk1 ? static_cast<uint32_t>(blk * 64) : OOB);
-        u_blk[mh] = uniform(blk < blk1 ? static_cast<uint32_t>(blk * 32 * C * 2) : OOB);
+        a_blk[mh] = uniform(blk < blk1 ? static_cast<uint32_t>(2 * blk) * TB : OOB);
+        u_blk[mh] = uniform(blk < blk1 ? static_cast<uint32_t>(4 * blk) * TB : OOB);
     }
     float *out_k = out + static_cast<size_t>(kgi) * Btot * T * V;
 
@@ -165,7 +167,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
 
     for (int step = 0; step < NT; ++step) {
         const int n = REV ? NT - 1 - step : step;
-        const uint32_t cb = uniform(static_cast<uint32_t>((n * V + v0) * C * 2));   // this chunk's c^T columns
+        const uint32_t cb = uniform(static_cast<uint32_t>(n * VT32 + v0 / 32) * 4 * TB);   // this chunk's value tiles
 
         // ---- rescaling of G around the read-out (rarely): renormalisation
         // (G *= s, s = 1) before, when s fell below 2^-40, or, when lam^64 itself
@@ -184,7 +186,6 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
         // ---- read-out of H = s G, one 32-row half at a time, plus this wave's
         // share of the intra-chunk product; both halves go to the exchange buffer.
         f32x16 O[2][2];
-        const uint32_t arow = uniform(static_cast<uint32_t>(n * C * K * 2));
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
@@ -196,7 +197,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
                 for (int mh = 0; mh < MH; ++mh)
 #pragma unroll
                     for (int hb = 0; hb < 2; ++hb) {
-                        const bf16x8 aop = bld(ra, a_lane[mt] + arow + a_blk[mh] + 32 * hb);
+                        const bf16x8 aop = bld(ra, lane16 + uniform(static_cast<uint32_t>((2 * n + mt) * KT16) * TB) +
+                                                       a_blk[mh] + hb * TB);
                         bf16x8 gop[2];
 #pragma unroll
                         for (int nt = 0; nt < 2; ++nt)
@@ -218,7 +220,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
             }
         }
         if (intra) {
-            const bf16x8 pq = bld(rp, p_lane + uniform(static_cast<uint32_t>(n * C * C * 2)));
+            const bf16x8 pq = bld(rp, p_lane + uniform(static_cast<uint32_t>(n * 8) * TB));
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
                 const bf16x8 ci = bld(rcr, cr_lane[nt] + cb);
@@ -260,8 +262,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-                for (int ks = 0; ks < 4; ++ks) ub[nt][ks] = bld(rub, ub_lane[nt] + cb + 32 * ks);
-            const uint32_t urow = uniform(static_cast<uint32_t>(n * K * C * 2));
+                for (int ks = 0; ks < 4; ++ks) ub[nt][ks] = bld(rub, ub_lane[nt] + cb + ks * TB);
+            const uint32_t urow = uniform(static_cast<uint32_t>(n * KT32) * 4 * TB);
 #pragma unroll
             for (int pass = 0; pass < (SPLIT ? 2 : 1); ++pass) {
                 const rsrc_t ru = pass ? rul : rua;
@@ -269,7 +271,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
                 for (int mh = 0; mh < MH; ++mh) {
                     bf16x8 bop[4];
 #pragma unroll
-                    for (int ks = 0; ks < 4; ++ks) bop[ks] = bld(ru, ua_lane + urow + u_blk[mh] + 32 * ks);
+                    for (int ks = 0; ks < 4; ++ks) bop[ks] = bld(ru, lane16 + urow + u_blk[mh] + ks * TB);
 #pragma unroll
                     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
@@ -289,7 +291,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
             for (int w2 = 1; w2 < WAVES; ++w2)
 #pragma unroll
                 for (int q4 = 0; q4 < 2; ++q4) acc[q4] += *reinterpret_cast<const f32x4 *>(rb + w2 * (VT * OPITCH) + 4 * q4);
-            const int col = v0 + lane;
+            // value tiles hold their 32 columns in the order perm32
+            const int col = v0 + 32 * (lane / 32) + perm32(lane % 32);
             if (col < V) {
                 float *dst = out_k + (static_cast<size_t>(b) * T + n * C + ROWS_PER_WAVE * wave) * V + col;
 #pragma unroll

@@ -74,6 +74,43 @@ __device__ __forceinline__ void store_from_f32(void *p, size_t i, int dtype, flo
     else static_cast<_Float16 *>(p)[i] = static_cast<_Float16>(v);
 }
 
+// ---- operand tile layouts of the chunked kernels
+//
+// A tile is one v_mfma_f32_32x32x16_bf16 operand: 32 rows x 16 contraction
+// elements, 1 KB, where lane l = r + 32 h holds row r, elements 8h .. 8h+7, as
+// the 16 bytes at 16 l. A wave loads a tile with one fully coalesced 1 KB read.
+//
+// R layout (rows = positions, contraction = features), of X (B, T, F), F % 16 == 0,
+// positions padded with zeros to 64 NT:
+//   tile (b, t / 32, f / 16), lane (t % 32) + 32 ((f % 16) / 8), element f % 8.
+// Q layout (rows = features in blocks of 32, in the order perm32; contraction =
+// the 64 positions of a chunk, in quarters of 16), F % 32 == 0:
+//   tile (b, t / 64, f / 32, (t % 64) / 16), lane perm32(f % 32) + 32 ((t % 16) / 8),
+//   element t % 8.
+// perm32 exchanges bits 2 and 3 of a row index (an involution). Stored in that
+// order, the rows of an MFMA accumulator tile read 8 registers at a time form
+// the next product's B operand with contraction index 8 h + e <-> row 16 j + 8 h + e.
+__host__ __device__ __forceinline__ int perm32(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
+constexpr int kTileElems = 512;   // bf16 per tile
+
+// element offset of X[b][t][f] in the R layout (NT chunks, F features)
+__host__ __device__ __forceinline__ size_t r_index(int b, int t, int f, int NT, int F) {
+    const size_t tile = (static_cast<size_t>(b) * (2 * NT) + t / 32) * (F / 16) + f / 16;
+    return tile * kTileElems + ((t % 32) + 32 * ((f % 16) / 8)) * 8 + f % 8;
+}
+// element offset of X[b][t][f] in the Q layout
+__host__ __device__ __forceinline__ size_t q_index(int b, int t, int f, int NT, int F) {
+    const size_t tile = ((static_cast<size_t>(b) * NT + t / 64) * (F / 32) + f / 32) * 4 + (t % 64) / 16;
+    return tile * kTileElems + (perm32(f % 32) + 32 * ((t % 16) / 8)) * 8 + t % 8;
+}
+// element offset of P[b][n][i][j] (a 64 x 64 chunk matrix) in tile layout:
+//   tile (b, n, i / 32, j / 16), lane (i % 32) + 32 ((j % 16) / 8), element j % 8
+__host__ __device__ __forceinline__ size_t p_index(int b, int n, int i, int j, int NT) {
+    const size_t tile = ((static_cast<size_t>(b) * NT + n) * 2 + i / 32) * 4 + j / 16;
+    return tile * kTileElems + ((i % 32) + 32 * ((j % 16) / 8)) * 8 + j % 8;
+}
+
 // ---- scale schedule of the chunked state H = s G. The K-group kernel and the
 // producer of its pre-decayed update operand both follow it with the same
 // float operations, so the divisor folded into the operand is the one the

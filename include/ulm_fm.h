@@ -50,38 +50,41 @@ const char *ulm_last_error(void);
  * fast = causal scalar-decay linear attention of (q, k, v).
  *
  *   r      (B,T,A) fp32          read addresses
- *   v16    (B,T,D) bf16          values, already cast to bf16 (kernel.py:205)
+ *   v      (B,T,D) v_dtype       values (the reference casts them to bf16 in
+ *                                 Python, kernel.py:205; here the cast is
+ *                                 inside, so the backward can also keep the
+ *                                 bf16 remainder of an fp32 v)
  *   w      (A,)    fp32          prior mass
  *   q      (B,T,A) fp32   out    returned and saved
  *   fast   (B,T,D) fast_dtype out  (v.dtype in the reference, kernel.py:211)
  *   saved  ulm_fm_saved_bytes() bytes, out: what the backward needs besides
- *          r, v16, g, w and q (the reference saves c, q16, k16, kernel.py:212;
- *          this holds bf16 copies of q and k in natural and chunk-transposed
- *          layouts, the transposed values, the score tiles of the dv product
- *          and the evidence n at every chunk start in place of c). Opaque to
- *          the caller; pass it unchanged to ulm_fm_bwd.
+ *          r, g, w and q (the reference saves v16, c, q16, k16, kernel.py:212;
+ *          this holds the bf16 operand tiles of q, k and v, the score tiles
+ *          of the dv product and the evidence n at every chunk start in place
+ *          of c). Opaque; pass it unchanged to ulm_fm_bwd.
  */
-size_t ulm_fm_saved_bytes(int B, int T, int A, int D);
+size_t ulm_fm_saved_bytes(int B, int T, int A, int D, int v_dtype);
 size_t ulm_fm_fwd_workspace_bytes(int B, int T, int A, int D, int fast_dtype);
-int ulm_fm_fwd(const float *r, const uint16_t *v16, const float *g, const float *w,
+int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const float *g, const float *w,
                float *q, void *fast, int fast_dtype, void *saved, size_t saved_bytes,
                void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream);
 
 /* Replaces UnifiedMemory.backward (kernel.py:216-233): the three chunked
  * products dq, dk (reverse), dv (reverse) and the denominator chain rule.
  *
- *   saved  the buffer ulm_fm_fwd filled for the same r, v16, g, w, q
- *   dfast  (B,T,D) dfast_dtype   upstream gradient of fast
- *   dq_out (B,T,A) fp32 or NULL  upstream gradient of the returned q
+ *   saved   the buffer ulm_fm_fwd filled for the same r, g, w, q
+ *   v_dtype the dtype of the v given to ulm_fm_fwd
+ *   dfast   (B,T,D) dfast_dtype  upstream gradient of fast
+ *   dq_out  (B,T,A) fp32 or NULL upstream gradient of the returned q
  *                                 (HAS_DQO, kernel.py:166-167, 228)
- *   dr     (B,T,A) fp32  out
- *   dv     (B,T,D) dv_dtype out  (dfast.dtype in the reference, kernel.py:223)
- *   dg     (1,)    fp32  out     d loss / d g
- *   dw     (A,)    fp32  out
+ *   dr      (B,T,A) fp32  out
+ *   dv      (B,T,D) dv_dtype out (dfast.dtype in the reference, kernel.py:223)
+ *   dg      (1,)    fp32  out    d loss / d g
+ *   dw      (A,)    fp32  out
  * dg and dw are reduced deterministically (no atomics). */
-size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D);
-int ulm_fm_bwd(const float *r, const uint16_t *v16, const float *g, const float *w,
-               const float *q, const void *saved, size_t saved_bytes,
+size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D, int dfast_dtype);
+int ulm_fm_bwd(const float *r, const float *g, const float *w, const float *q,
+               const void *saved, size_t saved_bytes, int v_dtype,
                const void *dfast, int dfast_dtype, const float *dq_out,
                float *dr, void *dv, int dv_dtype, float *dg, float *dw,
                void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream);

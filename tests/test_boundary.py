@@ -34,7 +34,7 @@ def test_c_side_rejects_bad_sizes_without_touching_the_gpu():
     st = lib.ulm_la(None, None, None, None, None, 0, 10, 8, 8, 0, 0, None, 0, None)
     assert st == nat.ULM_ERR_INVALID
     assert b"bad sizes" in lib.ulm_last_error()
-    st = lib.ulm_fm_fwd(*([None] * 6), 0, None, 0, None, 0, 2, 64, 8, 8, None)
+    st = lib.ulm_fm_fwd(None, None, 0, *([None] * 4), 0, None, 0, None, 0, 2, 64, 8, 8, None)
     assert st == nat.ULM_ERR_INVALID and b"null pointer" in lib.ulm_last_error()
     st = lib.ulm_decode_state(*([None] * 8), 4, 8, 100000, None)
     assert st == nat.ULM_ERR_INVALID and b"LDS" in lib.ulm_last_error()
@@ -52,15 +52,20 @@ def test_workspace_sizes():
     # 4 key groups of 768 slots: fp32 partial outputs, plus the forward score tiles
     assert lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_F32) >= 4 * B * T * D * 4 + B * NT * 64 * 64 * 2
     assert lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * D * 4
-    assert lib.ulm_fm_bwd_workspace_bytes(B, T, A, D) >= B * T * (2 * A * 4 + D * 6)
+    assert lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * (2 * A * 4 + D * 6)
+    # an fp32 dfast adds the bf16 remainder tiles of its read-out operand
+    assert (lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32)
+            - lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16)) == B * T * D * 2
     # saved: bf16 q, k in natural and transposed layouts, three v copies, n checkpoints
-    assert lib.ulm_fm_saved_bytes(B, T, A, D) >= B * T * (8 * A + 6 * D) + B * NT * A * 4
-    # unaligned sizes keep only the natural copies and the checkpoints
-    assert lib.ulm_fm_saved_bytes(2, 70, 12, 8) >= 2 * 70 * 12 * 4 + 2 * 2 * 12 * 4
+    assert lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * (8 * A + 8 * D) + B * NT * A * 4
+    assert (lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_F32)
+            - lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_BF16)) == B * T * D * 2
+    # unaligned sizes keep only natural bf16 copies of q, k, v and the checkpoints
+    assert lib.ulm_fm_saved_bytes(2, 70, 12, 8, nat.ULM_F32) >= 2 * 70 * (12 * 4 + 8 * 2) + 2 * 2 * 12 * 4
     assert lib.ulm_la_workspace_bytes(2, 70, 12, 8) == 0
     assert lib.ulm_la_workspace_bytes(B, T, A, D) >= 2 * B * NT * A * 64 * 2 + 4 * B * T * D * 4
     assert lib.ulm_addr_bwd_workspace_bytes(B * T, A) >= A * 4
-    assert lib.ulm_fm_bwd_workspace_bytes(0, T, A, D) == 0
+    assert lib.ulm_fm_bwd_workspace_bytes(0, T, A, D, nat.ULM_F32) == 0
 
 
 def _fm_args(B=2, T=70, A=12, D=8, dtype=torch.float32):

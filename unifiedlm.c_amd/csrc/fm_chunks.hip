@@ -21,19 +21,20 @@ namespace chunks {
 constexpr int C = ULM_CHUNK;
 
 // grid (ceil(X/64), NT, B), 256 threads: one 64-position x 64-feature block of
-// X (B, T, X) in any float dtype, rounded to bf16 (X % 32 == 0). Outputs, each
-// optional: raw (Q layout), the pre-decayed update operand hi (+ lo, the
-// rounding remainder) in the Q layout, and xr (R layout). DEC = 1 / 2 decays
-// for the forward / reversed walk:
+// X (B, T, X) in any float dtype (X % 32 == 0). Outputs, each optional: raw =
+// bf16(x) in the Q layout; the pre-decayed update operand hi (+ lo, the
+// rounding remainder) in the Q layout, from the full-precision x; xr = bf16(x)
+// (+ xr_lo = bf16(x - xr)) in the R layout. DEC = 1 / 2 decays for the forward
+// / reversed walk:
 //   forward  lam^(63-i) x / s_{n+1}          at walk step n
 //   reversed lam^i      x / s_{NT-n}         at walk step NT-1-n
 // with s the state scale schedule of the chunked kernel (state_inv_scale).
 template <int DEC>
 __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__ src, int sdt, uint16_t *__restrict__ raw,
                                                         uint16_t *__restrict__ hi, uint16_t *__restrict__ lo,
-                                                        uint16_t *__restrict__ xr, const float *__restrict__ g, int T,
-                                                        int X, int NT) {
-    __shared__ __align__(16) uint16_t tile[C][C + 8];   // [position][feature]
+                                                        uint16_t *__restrict__ xr, uint16_t *__restrict__ xr_lo,
+                                                        const float *__restrict__ g, int T, int X, int NT) {
+    __shared__ float tile[C][C + 1];   // [position][feature]
     const int x0 = blockIdx.x * C, n = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
     {
@@ -44,7 +45,7 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
             const int x = x0 + c0 + e;
-            tile[i][c0 + e] = (ok && x < X) ? f32_to_bf16_bits(load_as_f32(src, row + x, sdt)) : 0;
+            tile[i][c0 + e] = (ok && x < X) ? load_as_f32(src, row + x, sdt) : 0.f;
         }
     }
     __syncthreads();
@@ -55,8 +56,18 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int l = 2 * (tid % 32) + u, row = 32 * mt + l % 32, col = 16 * tf4 + 8 * (l / 32);
-                *reinterpret_cast<uint4 *>(xr + r_index(b, n * C + row, x0 + col, NT, X)) =
-                    *reinterpret_cast<const uint4 *>(&tile[row][col]);
+                uint32_t wh[4], wl[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float v0 = tile[row][col + 2 * e], v1 = tile[row][col + 2 * e + 1];
+                    const uint16_t h0 = f32_to_bf16_bits(v0), h1 = f32_to_bf16_bits(v1);
+                    wh[e] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+                    wl[e] = static_cast<uint32_t>(f32_to_bf16_bits(v0 - bf16_to_f32(h0))) |
+                            (static_cast<uint32_t>(f32_to_bf16_bits(v1 - bf16_to_f32(h1))) << 16);
+                }
+                const size_t o = r_index(b, n * C + row, x0 + col, NT, X);
+                *reinterpret_cast<uint4 *>(xr + o) = make_uint4(wh[0], wh[1], wh[2], wh[3]);
+                if (xr_lo) *reinterpret_cast<uint4 *>(xr_lo + o) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
             }
         }
     }
@@ -70,8 +81,8 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__
             uint32_t w[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                w[e] = static_cast<uint32_t>(tile[i0 + 8 * h + 2 * e][xl]) |
-                       (static_cast<uint32_t>(tile[i0 + 8 * h + 2 * e + 1][xl]) << 16);
+                w[e] = static_cast<uint32_t>(f32_to_bf16_bits(tile[i0 + 8 * h + 2 * e][xl])) |
+                       (static_cast<uint32_t>(f32_to_bf16_bits(tile[i0 + 8 * h + 2 * e + 1][xl])) << 16);
             *reinterpret_cast<uint4 *>(raw + q_index(b, n * C + i0 + 8 * h, x, NT, X)) = make_uint4(w[0], w[1], w[2], w[3]);
         }
     }
@@ -84,7 +95,7 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__
         for (int e = 0; e < 16; ++e) {
             const int i = i0 + e;
             const float f = __expf(gl * static_cast<float>(DEC == 1 ? C - 1 - i : i)) * inv_s;
-            const float v = bf16_to_f32(tile[i][xl]) * f;
+            const float v = tile[i][xl] * f;
             const uint16_t h = f32_to_bf16_bits(v);
             const uint16_t l = f32_to_bf16_bits(v - bf16_to_f32(h));
             if (e % 2 == 0) {
@@ -112,7 +123,11 @@ __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
 // computes the score tile (mt, nt) = (w/2, w%2) of the 64 x 64 chunk over all K
 // (tile (0, 1) lies strictly above the diagonal and is zero in both outputs);
 // P_lo and P_up go out in the tile layout (p_index) through an LDS transpose.
-__global__ __launch_bounds__(256) void scores_kernel(const uint16_t *__restrict__ aR, const uint16_t *__restrict__ bR,
+// ALO / BLO: a / b also come with bf16 remainders (a = ah + al, b = bh + bl);
+// the product takes ah bh + ah bl + al bh over the parts present.
+template <bool ALO, bool BLO>
+__global__ __launch_bounds__(256) void scores_kernel(const uint16_t *__restrict__ aR, const uint16_t *__restrict__ aL,
+                                                     const uint16_t *__restrict__ bR, const uint16_t *__restrict__ bL,
                                                      const float *__restrict__ g, uint16_t *__restrict__ Plo,
                                                      uint16_t *__restrict__ Pup, int K, int NT) {
     __shared__ __align__(16) uint16_t slo[C][C + 8], sup[C][C + 8];   // [i][j]
@@ -123,18 +138,27 @@ __global__ __launch_bounds__(256) void scores_kernel(const uint16_t *__restrict_
     const int KT = K / 16;   // tiles per R row block
     f32x16 acc[4] = {};
     if (!(mt == 0 && nt == 1)) {
-        const uint16_t *pa = aR + ((static_cast<size_t>(b) * (2 * NT) + 2 * n + mt) * KT) * kTileElems + 8 * lane;
-        const uint16_t *pb = bR + ((static_cast<size_t>(b) * (2 * NT) + 2 * n + nt) * KT) * kTileElems + 8 * lane;
+        const size_t oa = ((static_cast<size_t>(b) * (2 * NT) + 2 * n + mt) * KT) * kTileElems + 8 * lane;
+        const size_t ob = ((static_cast<size_t>(b) * (2 * NT) + 2 * n + nt) * KT) * kTileElems + 8 * lane;
+        const uint16_t *pa = aR + oa, *pb = bR + ob;
         int ks = 0;
         for (; ks + 4 <= KT; ks += 4) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                acc[u] = mfma(*reinterpret_cast<const bf16x8 *>(pa + (ks + u) * kTileElems),
-                              *reinterpret_cast<const bf16x8 *>(pb + (ks + u) * kTileElems), acc[u]);
+            for (int u = 0; u < 4; ++u) {
+                const size_t t = static_cast<size_t>(ks + u) * kTileElems;
+                const bf16x8 x = *reinterpret_cast<const bf16x8 *>(pa + t), y = *reinterpret_cast<const bf16x8 *>(pb + t);
+                acc[u] = mfma(x, y, acc[u]);
+                if (BLO) acc[u] = mfma(x, *reinterpret_cast<const bf16x8 *>(bL + ob + t), acc[u]);
+                if (ALO) acc[u] = mfma(*reinterpret_cast<const bf16x8 *>(aL + oa + t), y, acc[u]);
+            }
         }
-        for (; ks < KT; ++ks)
-            acc[0] = mfma(*reinterpret_cast<const bf16x8 *>(pa + ks * kTileElems),
-                          *reinterpret_cast<const bf16x8 *>(pb + ks * kTileElems), acc[0]);
+        for (; ks < KT; ++ks) {
+            const size_t t = static_cast<size_t>(ks) * kTileElems;
+            const bf16x8 x = *reinterpret_cast<const bf16x8 *>(pa + t), y = *reinterpret_cast<const bf16x8 *>(pb + t);
+            acc[0] = mfma(x, y, acc[0]);
+            if (BLO) acc[0] = mfma(x, *reinterpret_cast<const bf16x8 *>(bL + ob + t), acc[0]);
+            if (ALO) acc[0] = mfma(*reinterpret_cast<const bf16x8 *>(aL + oa + t), y, acc[0]);
+        }
     }
     const float gl = g[0];
     const int j = 32 * nt + lr;
@@ -192,27 +216,34 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(const float *__rest
 
 }  // namespace chunks
 
-// Tiled copies of X (B, T, X): raw, hi, lo in the Q layout and xr in the R
-// layout, each bf16 or null (X % 32 == 0). decay 0: no hi / lo; 1 / 2: hi (+ lo)
-// hold the pre-decayed update operand of the forward / reversed walk.
+// Tiled copies of X (B, T, X): raw, hi, lo in the Q layout and xr (+ xr_lo) in
+// the R layout, each bf16 or null (X % 32 == 0). decay 0: no hi / lo; 1 / 2: hi
+// (+ lo) hold the pre-decayed update operand of the forward / reversed walk.
 int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t *hi, uint16_t *lo, uint16_t *xr,
-                           const float *g, int decay, int B, int T, int X, hipStream_t s) {
+                           uint16_t *xr_lo, const float *g, int decay, int B, int T, int X, hipStream_t s) {
     if (X % 32) return fail(ULM_ERR_INVALID, "chunk transpose: X=%d is not a multiple of 32", X);
     if (decay && !(hi && g)) return fail(ULM_ERR_INVALID, "chunk transpose: decayed output needs hi and g");
+    if (xr_lo && !xr) return fail(ULM_ERR_INVALID, "chunk transpose: xr_lo needs xr");
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
     const dim3 grid((X + ULM_CHUNK - 1) / ULM_CHUNK, NT, B);
-    if (decay == 1) chunks::transpose_kernel<1><<<grid, 256, 0, s>>>(src, src_dt, raw, hi, lo, xr, g, T, X, NT);
-    else if (decay == 2) chunks::transpose_kernel<2><<<grid, 256, 0, s>>>(src, src_dt, raw, hi, lo, xr, g, T, X, NT);
-    else chunks::transpose_kernel<0><<<grid, 256, 0, s>>>(src, src_dt, raw, nullptr, nullptr, xr, g, T, X, NT);
+    if (decay == 1) chunks::transpose_kernel<1><<<grid, 256, 0, s>>>(src, src_dt, raw, hi, lo, xr, xr_lo, g, T, X, NT);
+    else if (decay == 2)
+        chunks::transpose_kernel<2><<<grid, 256, 0, s>>>(src, src_dt, raw, hi, lo, xr, xr_lo, g, T, X, NT);
+    else chunks::transpose_kernel<0><<<grid, 256, 0, s>>>(src, src_dt, raw, nullptr, nullptr, xr, xr_lo, g, T, X, NT);
     return check_launch("chunk transpose_kernel");
 }
 
-// a, b in the R layout (K % 16 == 0); P_lo, P_up in the tile layout of p_index.
-int launch_chunk_scores(const uint16_t *aR, const uint16_t *bR, const float *g, uint16_t *Plo, uint16_t *Pup, int B,
-                        int T, int K, hipStream_t s) {
+// a, b in the R layout (K % 16 == 0), with optional bf16 remainders aL, bL;
+// P_lo, P_up in the tile layout of p_index.
+int launch_chunk_scores(const uint16_t *aR, const uint16_t *aL, const uint16_t *bR, const uint16_t *bL, const float *g,
+                        uint16_t *Plo, uint16_t *Pup, int B, int T, int K, hipStream_t s) {
     if (K % 16) return fail(ULM_ERR_UNSUPPORTED, "chunk scores: K=%d is not a multiple of 16", K);
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
-    chunks::scores_kernel<<<dim3(NT, B), 256, 0, s>>>(aR, bR, g, Plo, Pup, K, NT);
+    const dim3 grid(NT, B);
+    if (aL && bL) chunks::scores_kernel<true, true><<<grid, 256, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
+    else if (aL) chunks::scores_kernel<true, false><<<grid, 256, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
+    else if (bL) chunks::scores_kernel<false, true><<<grid, 256, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
+    else chunks::scores_kernel<false, false><<<grid, 256, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
     return check_launch("chunk scores_kernel");
 }
 

@@ -14,11 +14,15 @@
 // P_dv = P_fwd^T, P_dk = P_dq^T. The decay of the state update always rides on
 // the D-sized tensor of the product (v or dfast), pre-multiplied into a bf16
 // hi + lo copy: v forward for fast and dq, dfast reversed for dk and dv.
+// When v or dfast arrive in fp32 (or fp16), the products behind the d/dg
+// identity (dq, dk and their scores) also take their read-out operand as
+// bf16 hi + lo, so both sides of the identity see the same full-precision v
+// and dfast (the bf16 rounding of either one alone breaks the cancellation).
 // The forward keeps what the backward needs in one "saved" buffer:
-//   qR, kR, qQ, kQ (B, NT, 64 A) bf16 tiles; vR, vQ, vQ~hi, vQ~lo (B, NT, 64 D);
-//   P_dv (B, NT, 64, 64) bf16 tiles; n_ckpt (B, NT, A) fp32.
+//   qR, kR, qQ, kQ (B, NT, 64 A) bf16 tiles; vR (+ vR~lo), vQ, vQ~hi, vQ~lo
+//   (B, NT, 64 D); P_dv (B, NT, 64, 64) bf16 tiles; n_ckpt (B, NT, A) fp32.
 // Other shapes use the generic kernel of fm_chunk.hip (atomics into zeroed
-// fp32 outputs) on natural bf16 copies of q and k.
+// fp32 outputs) on natural bf16 copies of q, k and v.
 #include "ulm_common.h"
 
 namespace ulm {
@@ -29,14 +33,14 @@ int launch_la_generic(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
 // la_kgroup.hip
 int la_kgroup_groups(int K);
 bool la_kgroup_supported(int B, int T, int K, int V);
-int launch_la_kgroup(const uint16_t *a, const uint16_t *ua, const uint16_t *ualo, const uint16_t *ub,
-                     const uint16_t *cr, const uint16_t *P, const float *g, float *out, int B, int T, int K, int V,
-                     bool reverse, hipStream_t s);
+int launch_la_kgroup(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo,
+                     const uint16_t *ub, const uint16_t *cr, const uint16_t *P, const float *g, float *out, int B,
+                     int T, int K, int V, bool reverse, hipStream_t s);
 // fm_chunks.hip
 int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t *hi, uint16_t *lo, uint16_t *xr,
-                           const float *g, int decay, int B, int T, int X, hipStream_t s);
-int launch_chunk_scores(const uint16_t *aR, const uint16_t *bR, const float *g, uint16_t *Plo, uint16_t *Pup, int B,
-                        int T, int K, hipStream_t s);
+                           uint16_t *xr_lo, const float *g, int decay, int B, int T, int X, hipStream_t s);
+int launch_chunk_scores(const uint16_t *aR, const uint16_t *aL, const uint16_t *bR, const uint16_t *bL, const float *g,
+                        uint16_t *Plo, uint16_t *Pup, int B, int T, int K, hipStream_t s);
 int launch_partial_reduce(const float *part, int nK, size_t n, void *out, int odt, hipStream_t s);
 // fm_stats.hip
 int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
@@ -71,13 +75,13 @@ bool fm_aligned(int B, int T, int A, int D) {
 }
 
 struct Saved {
-    uint16_t *q16n, *k16n;                          // generic path
-    uint16_t *qR, *kR, *qQ, *kQ, *vR, *vQ, *vQh, *vQl, *Pdv;   // K-group path
+    uint16_t *q16n, *k16n, *v16n;                                     // generic path
+    uint16_t *qR, *kR, *qQ, *kQ, *vR, *vRl, *vQ, *vQh, *vQl, *Pdv;   // K-group path
     float *nck;
     size_t bytes;
 };
 
-Saved saved_layout(void *base, int B, int T, int A, int D) {
+Saved saved_layout(void *base, int B, int T, int A, int D, int v_dtype) {
     const size_t NT = nt_of(T);
     const size_t na = static_cast<size_t>(B) * T * A, ta = B * NT * 64 * A, td = B * NT * 64 * D;
     Carver c(base);
@@ -88,6 +92,7 @@ Saved saved_layout(void *base, int B, int T, int A, int D) {
         s.qQ = c.take<uint16_t>(ta);
         s.kQ = c.take<uint16_t>(ta);
         s.vR = c.take<uint16_t>(td);
+        if (v_dtype != ULM_BF16) s.vRl = c.take<uint16_t>(td);
         s.vQ = c.take<uint16_t>(td);
         s.vQh = c.take<uint16_t>(td);
         s.vQl = c.take<uint16_t>(td);
@@ -95,6 +100,7 @@ Saved saved_layout(void *base, int B, int T, int A, int D) {
     } else {
         s.q16n = c.take<uint16_t>(na);
         s.k16n = c.take<uint16_t>(na);
+        s.v16n = c.take<uint16_t>(static_cast<size_t>(B) * T * D);
     }
     s.nck = c.take<float>(B * NT * A);
     s.bytes = c.off;
@@ -123,14 +129,14 @@ FwdWs fwd_layout(void *base, int B, int T, int A, int D, int fast_dtype) {
 }
 
 struct BwdWs {
-    uint16_t *do16;                           // generic path
-    uint16_t *doR, *doQ, *doQh, *doQl, *Pdq, *Pdk;   // K-group path
+    uint16_t *do16;                                          // generic path
+    uint16_t *doR, *doRl, *doQ, *doQh, *doQl, *Pdq, *Pdk;   // K-group path
     float *dqf, *dkf, *part;
     void *stats;
     size_t bytes;
 };
 
-BwdWs bwd_layout(void *base, int B, int T, int A, int D) {
+BwdWs bwd_layout(void *base, int B, int T, int A, int D, int dfast_dtype) {
     const size_t NT = nt_of(T), nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
     const size_t td = B * NT * 64 * D;
     Carver c(base);
@@ -139,6 +145,7 @@ BwdWs bwd_layout(void *base, int B, int T, int A, int D) {
     w.dkf = c.take<float>(na);
     if (fm_aligned(B, T, A, D)) {
         w.doR = c.take<uint16_t>(td);
+        if (dfast_dtype != ULM_BF16) w.doRl = c.take<uint16_t>(td);
         w.doQ = c.take<uint16_t>(td);
         w.doQh = c.take<uint16_t>(td);
         w.doQl = c.take<uint16_t>(td);
@@ -211,11 +218,12 @@ extern "C" int ulm_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
     const int nkg = la_kgroup_groups(K);
     float *part = nkg > 1 ? cv.take<float>(static_cast<size_t>(nkg) * B * T * V) : out;
     // the decay of the state update rides on b
-    ULM_TRY(launch_chunk_transpose(a, ULM_BF16, nullptr, nullptr, nullptr, aR, g, 0, B, T, K, s));
-    ULM_TRY(launch_chunk_transpose(b, ULM_BF16, nullptr, bQh, split ? bQl : nullptr, bR, g, reverse ? 2 : 1, B, T, K, s));
-    ULM_TRY(launch_chunk_transpose(c, ULM_BF16, cQ, nullptr, nullptr, nullptr, g, 0, B, T, V, s));
-    ULM_TRY(launch_chunk_scores(reverse ? bR : aR, reverse ? aR : bR, g, Plo, Pup, B, T, K, s));
-    ULM_TRY(launch_la_kgroup(aR, bQh, split ? bQl : nullptr, cQ, cQ, reverse ? Pup : Plo, g, part, B, T, K, V,
+    ULM_TRY(launch_chunk_transpose(a, ULM_BF16, nullptr, nullptr, nullptr, aR, nullptr, g, 0, B, T, K, s));
+    ULM_TRY(launch_chunk_transpose(b, ULM_BF16, nullptr, bQh, split ? bQl : nullptr, bR, nullptr, g, reverse ? 2 : 1, B,
+                                   T, K, s));
+    ULM_TRY(launch_chunk_transpose(c, ULM_BF16, cQ, nullptr, nullptr, nullptr, nullptr, g, 0, B, T, V, s));
+    ULM_TRY(launch_chunk_scores(reverse ? bR : aR, nullptr, reverse ? aR : bR, nullptr, g, Plo, Pup, B, T, K, s));
+    ULM_TRY(launch_la_kgroup(aR, nullptr, bQh, split ? bQl : nullptr, cQ, cQ, reverse ? Pup : Plo, g, part, B, T, K, V,
                              reverse != 0, s));
     if (nkg > 1) ULM_TRY(launch_partial_reduce(part, nkg, static_cast<size_t>(B) * T * V, out, ULM_F32, s));
     return ULM_OK;
@@ -224,9 +232,9 @@ extern "C" int ulm_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
 // ---------------------------------------------------------------------------
 // fused operator
 
-extern "C" size_t ulm_fm_saved_bytes(int B, int T, int A, int D) {
-    if (B <= 0 || T <= 0 || A <= 0 || D <= 0) return 0;
-    return saved_layout(nullptr, B, T, A, D).bytes;
+extern "C" size_t ulm_fm_saved_bytes(int B, int T, int A, int D, int v_dtype) {
+    if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(v_dtype)) return 0;
+    return saved_layout(nullptr, B, T, A, D, v_dtype).bytes;
 }
 
 extern "C" size_t ulm_fm_fwd_workspace_bytes(int B, int T, int A, int D, int fast_dtype) {
@@ -234,79 +242,81 @@ extern "C" size_t ulm_fm_fwd_workspace_bytes(int B, int T, int A, int D, int fas
     return fwd_layout(nullptr, B, T, A, D, fast_dtype).bytes;
 }
 
-extern "C" int ulm_fm_fwd(const float *r, const uint16_t *v16, const float *g, const float *w, float *q, void *fast,
-                          int fast_dtype, void *saved, size_t saved_bytes, void *workspace, size_t workspace_bytes,
-                          int B, int T, int A, int D, void *stream) {
+extern "C" int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const float *g, const float *w, float *q,
+                          void *fast, int fast_dtype, void *saved, size_t saved_bytes, void *workspace,
+                          size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
     ULM_REQUIRE(B > 0 && T > 0 && A > 0 && D > 0, "ulm_fm_fwd: bad sizes B=%d T=%d A=%d D=%d", B, T, A, D);
-    ULM_REQUIRE(valid_dtype(fast_dtype), "ulm_fm_fwd: bad fast dtype %d", fast_dtype);
-    ULM_REQUIRE(r && v16 && g && w && q && fast && saved, "ulm_fm_fwd: null pointer");
-    const size_t need_s = ulm_fm_saved_bytes(B, T, A, D);
+    ULM_REQUIRE(valid_dtype(v_dtype) && valid_dtype(fast_dtype), "ulm_fm_fwd: bad dtype %d/%d", v_dtype, fast_dtype);
+    ULM_REQUIRE(r && v && g && w && q && fast && saved, "ulm_fm_fwd: null pointer");
+    const size_t need_s = ulm_fm_saved_bytes(B, T, A, D, v_dtype);
     ULM_REQUIRE(saved_bytes >= need_s, "ulm_fm_fwd: saved buffer of %zu bytes, need %zu", saved_bytes, need_s);
     const size_t need = ulm_fm_fwd_workspace_bytes(B, T, A, D, fast_dtype);
     ULM_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), "ulm_fm_fwd: workspace of %zu bytes, need %zu",
                 workspace_bytes, need);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const Saved sv = saved_layout(saved, B, T, A, D);
+    const Saved sv = saved_layout(saved, B, T, A, D, v_dtype);
     const FwdWs ws = fwd_layout(workspace, B, T, A, D, fast_dtype);
     const size_t nf = static_cast<size_t>(B) * T * D;
     if (fm_aligned(B, T, A, D)) {
         const int nkg = la_kgroup_groups(A);
         float *acc = ws.part ? ws.part : static_cast<float *>(fast);
         ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, sv.qR, sv.kR, sv.qQ, sv.kQ, sv.nck, B, T, A, s));
-        ULM_TRY(launch_chunk_transpose(v16, ULM_BF16, sv.vQ, sv.vQh, sv.vQl, sv.vR, g, 1, B, T, D, s));
-        ULM_TRY(launch_chunk_scores(sv.qR, sv.kR, g, ws.Pf, sv.Pdv, B, T, A, s));
-        // fast = LA(q, k, v): update k^T v~, intra on the raw v
-        ULM_TRY(launch_la_kgroup(sv.qR, sv.kQ, nullptr, sv.vQh, sv.vQ, ws.Pf, g, acc, B, T, A, D, false, s));
+        ULM_TRY(launch_chunk_transpose(v, v_dtype, sv.vQ, sv.vQh, sv.vQl, sv.vR, sv.vRl, g, 1, B, T, D, s));
+        ULM_TRY(launch_chunk_scores(sv.qR, nullptr, sv.kR, nullptr, g, ws.Pf, sv.Pdv, B, T, A, s));
+        // fast = LA(q, k, v): update k^T v~, intra on bf16(v), as the reference's bf16 v (kernel.py:205)
+        ULM_TRY(launch_la_kgroup(sv.qR, nullptr, sv.kQ, nullptr, sv.vQh, sv.vQ, ws.Pf, g, acc, B, T, A, D, false, s));
         if (ws.part) ULM_TRY(launch_partial_reduce(ws.part, nkg, nf, fast, fast_dtype, s));
         return ULM_OK;
     }
     ULM_TRY(launch_fwd_stats(r, w, g, q, sv.q16n, sv.k16n, nullptr, nullptr, nullptr, nullptr, sv.nck, B, T, A, s));
+    ULM_TRY(launch_convert(v, v_dtype, sv.v16n, ULM_BF16, nf, s));
     float *acc = fast_dtype == ULM_F32 ? static_cast<float *>(fast) : ws.part;
     ULM_TRY(launch_fill_zero(acc, nf * sizeof(float), s));
-    ULM_TRY(launch_la_generic(sv.q16n, sv.k16n, v16, g, acc, B, T, A, D, false, s));
+    ULM_TRY(launch_la_generic(sv.q16n, sv.k16n, sv.v16n, g, acc, B, T, A, D, false, s));
     if (fast_dtype != ULM_F32) ULM_TRY(launch_convert(acc, ULM_F32, fast, fast_dtype, nf, s));
     return ULM_OK;
 }
 
-extern "C" size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D) {
-    if (B <= 0 || T <= 0 || A <= 0 || D <= 0) return 0;
-    return bwd_layout(nullptr, B, T, A, D).bytes;
+extern "C" size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D, int dfast_dtype) {
+    if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(dfast_dtype)) return 0;
+    return bwd_layout(nullptr, B, T, A, D, dfast_dtype).bytes;
 }
 
-extern "C" int ulm_fm_bwd(const float *r, const uint16_t *v16, const float *g, const float *w, const float *q,
-                          const void *saved, size_t saved_bytes, const void *dfast, int dfast_dtype,
-                          const float *dq_out, float *dr, void *dv, int dv_dtype, float *dg, float *dw,
-                          void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
+extern "C" int ulm_fm_bwd(const float *r, const float *g, const float *w, const float *q, const void *saved,
+                          size_t saved_bytes, int v_dtype, const void *dfast, int dfast_dtype, const float *dq_out,
+                          float *dr, void *dv, int dv_dtype, float *dg, float *dw, void *workspace,
+                          size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
     ULM_REQUIRE(B > 0 && T > 0 && A > 0 && D > 0, "ulm_fm_bwd: bad sizes B=%d T=%d A=%d D=%d", B, T, A, D);
-    ULM_REQUIRE(valid_dtype(dfast_dtype) && valid_dtype(dv_dtype), "ulm_fm_bwd: bad dtype %d/%d", dfast_dtype,
-                dv_dtype);
-    ULM_REQUIRE(r && v16 && g && w && q && saved && dfast && dr && dv && dg && dw, "ulm_fm_bwd: null pointer");
-    const size_t need_s = ulm_fm_saved_bytes(B, T, A, D);
+    ULM_REQUIRE(valid_dtype(v_dtype) && valid_dtype(dfast_dtype) && valid_dtype(dv_dtype),
+                "ulm_fm_bwd: bad dtype %d/%d/%d", v_dtype, dfast_dtype, dv_dtype);
+    ULM_REQUIRE(r && g && w && q && saved && dfast && dr && dv && dg && dw, "ulm_fm_bwd: null pointer");
+    const size_t need_s = ulm_fm_saved_bytes(B, T, A, D, v_dtype);
     ULM_REQUIRE(saved_bytes >= need_s, "ulm_fm_bwd: saved buffer of %zu bytes, need %zu", saved_bytes, need_s);
-    const size_t need = ulm_fm_bwd_workspace_bytes(B, T, A, D);
+    const size_t need = ulm_fm_bwd_workspace_bytes(B, T, A, D, dfast_dtype);
     ULM_REQUIRE(workspace && workspace_bytes >= need, "ulm_fm_bwd: workspace of %zu bytes, need %zu",
                 workspace_bytes, need);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const Saved sv = saved_layout(const_cast<void *>(saved), B, T, A, D);
-    const BwdWs ws = bwd_layout(workspace, B, T, A, D);
+    const Saved sv = saved_layout(const_cast<void *>(saved), B, T, A, D, v_dtype);
+    const BwdWs ws = bwd_layout(workspace, B, T, A, D, dfast_dtype);
     const size_t nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
     if (fm_aligned(B, T, A, D)) {
         const int nkd = la_kgroup_groups(D), nka = la_kgroup_groups(A);
-        ULM_TRY(launch_chunk_transpose(dfast, dfast_dtype, ws.doQ, ws.doQh, ws.doQl, ws.doR, g, 2, B, T, D, s));
-        ULM_TRY(launch_chunk_scores(ws.doR, sv.vR, g, ws.Pdq, ws.Pdk, B, T, D, s));
+        ULM_TRY(launch_chunk_transpose(dfast, dfast_dtype, ws.doQ, ws.doQh, ws.doQl, ws.doR, ws.doRl, g, 2, B, T, D, s));
+        ULM_TRY(launch_chunk_scores(ws.doR, ws.doRl, sv.vR, sv.vRl, g, ws.Pdq, ws.Pdk, B, T, D, s));
         // dq_f = LA(dfast, v, k): keys = D, values = A; update v~^T k.
         // dk_f = LA_rev(v, dfast, q): update dfast~^T q.
         // Both feed the positional d/dg identity, whose cancellation amplifies
-        // rounding, so their decayed operand is carried as bf16 hi + lo.
-        ULM_TRY(launch_la_kgroup(ws.doR, sv.vQh, sv.vQl, sv.kQ, sv.kQ, ws.Pdq, g, nkd > 1 ? ws.part : ws.dqf, B, T, D, A,
-                                 false, s));
+        // rounding, so their decayed operand is carried as bf16 hi + lo (and
+        // their read-out operand too when it arrived in more than bf16).
+        ULM_TRY(launch_la_kgroup(ws.doR, ws.doRl, sv.vQh, sv.vQl, sv.kQ, sv.kQ, ws.Pdq, g, nkd > 1 ? ws.part : ws.dqf, B,
+                                 T, D, A, false, s));
         if (nkd > 1) ULM_TRY(launch_partial_reduce(ws.part, nkd, na, ws.dqf, ULM_F32, s));
-        ULM_TRY(launch_la_kgroup(sv.vR, ws.doQh, ws.doQl, sv.qQ, sv.qQ, ws.Pdk, g, nkd > 1 ? ws.part : ws.dkf, B, T, D, A,
-                                 true, s));
+        ULM_TRY(launch_la_kgroup(sv.vR, sv.vRl, ws.doQh, ws.doQl, sv.qQ, sv.qQ, ws.Pdk, g, nkd > 1 ? ws.part : ws.dkf, B,
+                                 T, D, A, true, s));
         if (nkd > 1) ULM_TRY(launch_partial_reduce(ws.part, nkd, na, ws.dkf, ULM_F32, s));
-        // dv = LA_rev(k, q, dfast): keys = A, values = D; update q^T dfast~, intra on the raw dfast
+        // dv = LA_rev(k, q, dfast): keys = A, values = D; update q^T dfast~, intra on bf16(dfast)
         const bool direct = nka == 1 && dv_dtype == ULM_F32;
-        ULM_TRY(launch_la_kgroup(sv.kR, sv.qQ, nullptr, ws.doQh, ws.doQ, sv.Pdv, g,
+        ULM_TRY(launch_la_kgroup(sv.kR, nullptr, sv.qQ, nullptr, ws.doQh, ws.doQ, sv.Pdv, g,
                                  direct ? static_cast<float *>(dv) : ws.part, B, T, A, D, true, s));
         if (!direct) ULM_TRY(launch_partial_reduce(ws.part, nka, nd, dv, dv_dtype, s));
     } else {
@@ -316,9 +326,9 @@ extern "C" int ulm_fm_bwd(const float *r, const uint16_t *v16, const float *g, c
             do16 = ws.do16;
         }
         ULM_TRY(launch_fill_zero(ws.dqf, na * 4, s));
-        ULM_TRY(launch_la_generic(do16, v16, sv.k16n, g, ws.dqf, B, T, D, A, false, s));
+        ULM_TRY(launch_la_generic(do16, sv.v16n, sv.k16n, g, ws.dqf, B, T, D, A, false, s));
         ULM_TRY(launch_fill_zero(ws.dkf, na * 4, s));
-        ULM_TRY(launch_la_generic(v16, do16, sv.q16n, g, ws.dkf, B, T, D, A, true, s));
+        ULM_TRY(launch_la_generic(sv.v16n, do16, sv.q16n, g, ws.dkf, B, T, D, A, true, s));
         float *dv_acc = dv_dtype == ULM_F32 ? static_cast<float *>(dv) : ws.part;
         ULM_TRY(launch_fill_zero(dv_acc, nd * 4, s));
         ULM_TRY(launch_la_generic(sv.k16n, sv.q16n, do16, g, dv_acc, B, T, A, D, true, s));

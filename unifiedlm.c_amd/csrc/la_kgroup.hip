@@ -80,9 +80,12 @@ __device__ __forceinline__ uint32_t uniform(uint32_t x) { return __builtin_amdgc
 // own LDS traffic done, then meet the other waves
 __device__ __forceinline__ void sync_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// MH: key blocks per wave (blocks past the group's end read as zero).
-template <int MH, bool REV, bool SPLIT>
+// MH: key blocks per wave (blocks past the group's end read as zero). SPLIT: the
+// update operand comes as bf16 hi + lo (UA, UAlo); ASPLIT: the read-out operand
+// as hi + lo (A_, Alo).
+template <int MH, bool REV, bool SPLIT, bool ASPLIT>
 __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t *__restrict__ A_,
+                                                                  const uint16_t *__restrict__ Alo,
                                                                   const uint16_t *__restrict__ UA,
                                                                   const uint16_t *__restrict__ UAlo,
                                                                   const uint16_t *__restrict__ UB,
@@ -132,6 +135,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
     const size_t rowB = static_cast<size_t>(NT) * VT32 * 4 * kTileElems;    // Q layout, values
     const size_t rowP = static_cast<size_t>(NT) * 8 * kTileElems;           // score tiles
     const rsrc_t ra = rsrc(A_ + b * rowA, rowA * 2);
+    const rsrc_t ral = rsrc((ASPLIT ? Alo : A_) + b * rowA, rowA * 2);
     const rsrc_t rua = rsrc(UA + b * rowU, rowU * 2);
     const rsrc_t rul = rsrc((SPLIT ? UAlo : UA) + b * rowU, rowU * 2);
     const rsrc_t rub = rsrc(UB + b * rowB, rowB * 2);
@@ -197,15 +201,20 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
                 for (int mh = 0; mh < MH; ++mh)
 #pragma unroll
                     for (int hb = 0; hb < 2; ++hb) {
-                        const bf16x8 aop = bld(ra, lane16 + uniform(static_cast<uint32_t>((2 * n + mt) * KT16) * TB) +
-                                                       a_blk[mh] + hb * TB);
+                        const uint32_t aoff = lane16 + uniform(static_cast<uint32_t>((2 * n + mt) * KT16) * TB) +
+                                              a_blk[mh] + hb * TB;
+                        const bf16x8 aop = bld(ra, aoff);
+                        const bf16x8 aol = ASPLIT ? bld(ral, aoff) : bf16x8{};
                         bf16x8 gop[2];
 #pragma unroll
                         for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
                             for (int e = 0; e < 8; ++e) gop[nt][e] = static_cast<bf16>(G[mh][nt][8 * hb + e]);
 #pragma unroll
-                        for (int nt = 0; nt < 2; ++nt) O[mt][nt] = mfma(aop, gop[nt], O[mt][nt]);
+                        for (int nt = 0; nt < 2; ++nt) {
+                            O[mt][nt] = mfma(aop, gop[nt], O[mt][nt]);
+                            if (ASPLIT) O[mt][nt] = mfma(aol, gop[nt], O[mt][nt]);
+                        }
                     }
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -305,9 +314,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
     }
 }
 
-template <int MH, bool REV, bool SPLIT>
-int launch(const uint16_t *a, const uint16_t *ua, const uint16_t *ualo, const uint16_t *ub, const uint16_t *cr,
-           const uint16_t *P, const float *g, float *out, int B, int T, int K, int V, int nKG, int bpg, hipStream_t s) {
+template <int MH, bool REV, bool SPLIT, bool ASPLIT>
+int launch(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo, const uint16_t *ub,
+           const uint16_t *cr, const uint16_t *P, const float *g, float *out, int B, int T, int K, int V, int nKG,
+           int bpg, hipStream_t s) {
     const int NT = (T + C - 1) / C;
     const int nVT = (V + VT - 1) / VT;
     const long long total = static_cast<long long>(B) * nKG * nVT;
@@ -315,30 +325,35 @@ int launch(const uint16_t *a, const uint16_t *ua, const uint16_t *ualo, const ui
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return check_launch("hipGetDevice");
     if (!attr_done[dev]) {
-        const void *fn = reinterpret_cast<const void *>(&la_kgroup_kernel<MH, REV, SPLIT>);
+        const void *fn = reinterpret_cast<const void *>(&la_kgroup_kernel<MH, REV, SPLIT, ASPLIT>);
         if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES) != hipSuccess)
             return check_launch("la_kgroup_kernel attribute");
         attr_done[dev] = true;
     }
     int st = la_timer_begin(s);
     if (st) return st;
-    la_kgroup_kernel<MH, REV, SPLIT><<<dim3(static_cast<unsigned>(total)), WAVES * kWave, LDS_BYTES, s>>>(
-        a, ua, ualo, ub, cr, P, g, out, B, T, K, V, NT, nKG, bpg, nVT, static_cast<int>(total));
+    la_kgroup_kernel<MH, REV, SPLIT, ASPLIT><<<dim3(static_cast<unsigned>(total)), WAVES * kWave, LDS_BYTES, s>>>(
+        a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, NT, nKG, bpg, nVT, static_cast<int>(total));
     st = check_launch("la_kgroup_kernel");
     if (st) return st;
     return la_timer_end(s);
 }
 
 template <int MH>
-int launch_mh(const uint16_t *a, const uint16_t *ua, const uint16_t *ualo, const uint16_t *ub, const uint16_t *cr,
-              const uint16_t *P, const float *g, float *out, int B, int T, int K, int V, int nKG, int bpg, bool reverse,
-              hipStream_t s) {
-    const bool split = ualo != nullptr;
-    if (reverse)
-        return split ? launch<MH, true, true>(a, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s)
-                     : launch<MH, true, false>(a, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
-    return split ? launch<MH, false, true>(a, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s)
-                 : launch<MH, false, false>(a, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
+int launch_mh(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo, const uint16_t *ub,
+              const uint16_t *cr, const uint16_t *P, const float *g, float *out, int B, int T, int K, int V, int nKG,
+              int bpg, bool reverse, hipStream_t s) {
+    const int sel = (reverse ? 4 : 0) + (ualo ? 2 : 0) + (alo ? 1 : 0);
+    switch (sel) {
+    case 0: return launch<MH, false, false, false>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
+    case 1: return launch<MH, false, false, true>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
+    case 2: return launch<MH, false, true, false>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
+    case 3: return launch<MH, false, true, true>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
+    case 4: return launch<MH, true, false, false>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
+    case 5: return launch<MH, true, false, true>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
+    case 6: return launch<MH, true, true, false>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
+    default: return launch<MH, true, true, true>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
+    }
 }
 
 }  // namespace kgrp
@@ -360,15 +375,15 @@ bool la_kgroup_supported(int B, int T, int K, int V) {
     return total <= 0x7fffffffLL && rowmax < (1LL << 30);
 }
 
-// Operands (bf16): a (B,T,K) natural; ua, ualo (B,NT,K,64) and ub, cr (B,NT,V,64)
-// chunk-transposed. The update adds ua^T ub (+ ualo^T ub when ualo is given);
-// one of ua / ub carries the decay and 1/s of the state scale schedule
-// (chunk_decayed). cr is the raw c of the intra-chunk product. P (B,NT,64,64)
-// is P_lo (forward) or P_up (reverse) of chunk_scores.
+// Operands (bf16 tiles, ulm_common.h): a (+ alo) in the R layout; ua (+ ualo)
+// and ub, cr in the Q layout. The update adds ua^T ub (+ ualo^T ub); one of ua
+// / ub carries the decay and 1/s of the state scale schedule (chunk_transpose).
+// The read-out contracts a (+ alo) with the state. cr is the raw c of the
+// intra-chunk product; P is P_lo (forward) or P_up (reverse) of chunk_scores.
 // out: la_kgroup_groups(K) x (B, T, V) fp32, fully written (no accumulation).
-int launch_la_kgroup(const uint16_t *a, const uint16_t *ua, const uint16_t *ualo, const uint16_t *ub,
-                     const uint16_t *cr, const uint16_t *P, const float *g, float *out, int B, int T, int K, int V,
-                     bool reverse, hipStream_t s) {
+int launch_la_kgroup(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo,
+                     const uint16_t *ub, const uint16_t *cr, const uint16_t *P, const float *g, float *out, int B,
+                     int T, int K, int V, bool reverse, hipStream_t s) {
     if (!la_kgroup_supported(B, T, K, V))
         return fail(ULM_ERR_UNSUPPORTED, "K-group kernel: B=%d T=%d K=%d V=%d unsupported", B, T, K, V);
     const int nKG = la_kgroup_groups(K);
@@ -376,9 +391,9 @@ int launch_la_kgroup(const uint16_t *a, const uint16_t *ua, const uint16_t *ualo
     const int bpg = (nb + nKG - 1) / nKG;   // <= 24 blocks, so at most 3 per wave
     const int mh = (bpg + kgrp::WAVES - 1) / kgrp::WAVES;
     switch (mh) {
-    case 1: return kgrp::launch_mh<1>(a, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, reverse, s);
-    case 2: return kgrp::launch_mh<2>(a, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, reverse, s);
-    default: return kgrp::launch_mh<3>(a, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, reverse, s);
+    case 1: return kgrp::launch_mh<1>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, reverse, s);
+    case 2: return kgrp::launch_mh<2>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, reverse, s);
+    default: return kgrp::launch_mh<3>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, reverse, s);
     }
 }
 

@@ -50,10 +50,11 @@ def _check_fm(r, v, g, w):
 
 
 class UnifiedMemory(torch.autograd.Function):
-    """Replaces kernel.py:199-233. Saves r, v16, g, w, q and one opaque buffer
-    that the forward fills with what the backward needs (bf16 copies of q and
-    k, chunk-transposed operands, score tiles and the per-chunk evidence
-    checkpoints that stand in for the full c tensor)."""
+    """Replaces kernel.py:199-233. Saves r, g, w, q and one opaque buffer that
+    the forward fills with what the backward needs (bf16 operand tiles of q, k
+    and v, score tiles and the per-chunk evidence checkpoints that stand in for
+    the full c tensor). v is passed in its own dtype; the library casts it to
+    bf16 for the products (kernel.py:205)."""
 
     @staticmethod
     def forward(ctx, r, v, g, w):
@@ -61,40 +62,39 @@ class UnifiedMemory(torch.autograd.Function):
         B, T, A = r.shape
         D = v.shape[-1]
         r32 = r.float().contiguous()
-        v16 = v.to(torch.bfloat16).contiguous()
+        vc = v.contiguous()
         g1 = g.float().reshape(1).contiguous()
         w32 = w.float().contiguous()
         q = torch.empty_like(r32)
         fast = torch.empty(B, T, D, device=r.device, dtype=v.dtype)
-        saved_bytes = nat.lib().ulm_fm_saved_bytes(B, T, A, D)
+        vdt = nat.dtype_code(v.dtype)
+        saved_bytes = nat.lib().ulm_fm_saved_bytes(B, T, A, D, vdt)
         saved = torch.empty(saved_bytes, device=r.device, dtype=torch.uint8)
-        fdt = nat.dtype_code(v.dtype)
-        ws_bytes = nat.lib().ulm_fm_fwd_workspace_bytes(B, T, A, D, fdt)
+        ws_bytes = nat.lib().ulm_fm_fwd_workspace_bytes(B, T, A, D, vdt)
         ws = torch.empty(max(ws_bytes, 1), device=r.device, dtype=torch.uint8)
-        call("ulm_fm_fwd", ptr(r32), ptr(v16), ptr(g1), ptr(w32), ptr(q), ptr(fast), fdt, ptr(saved), saved_bytes,
+        call("ulm_fm_fwd", ptr(r32), ptr(vc), vdt, ptr(g1), ptr(w32), ptr(q), ptr(fast), vdt, ptr(saved), saved_bytes,
              ptr(ws), ws_bytes, B, T, A, D, nat.stream_of(r))
-        ctx.save_for_backward(r32, v16, g1, w32, q, saved)
-        ctx.g_shape = g.shape
+        ctx.save_for_backward(r32, g1, w32, q, saved)
+        ctx.g_shape, ctx.D, ctx.vdt = g.shape, D, vdt
         return q, fast
 
     @staticmethod
     def backward(ctx, dq_out, dfast):
-        r, v16, g1, w, q, saved = ctx.saved_tensors
+        r, g1, w, q, saved = ctx.saved_tensors
         B, T, A = r.shape
-        D = v16.shape[-1]
+        D = ctx.D
         if dfast is None:
             dfast = torch.zeros(B, T, D, device=r.device, dtype=torch.float32)
-        nat.dtype_code(dfast.dtype)
+        ddt = nat.dtype_code(dfast.dtype)
         dfast = dfast.contiguous()
         dqo = dq_out.float().contiguous() if dq_out is not None else None
         dr = torch.empty_like(r)
         dv = torch.empty(B, T, D, device=r.device, dtype=dfast.dtype)
         dg = torch.empty(1, device=r.device, dtype=torch.float32)
         dw = torch.empty(A, device=r.device, dtype=torch.float32)
-        ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D)
+        ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D, ddt)
         ws = torch.empty(ws_bytes, device=r.device, dtype=torch.uint8)
-        ddt = nat.dtype_code(dfast.dtype)
-        call("ulm_fm_bwd", ptr(r), ptr(v16), ptr(g1), ptr(w), ptr(q), ptr(saved), saved.numel(), ptr(dfast), ddt,
+        call("ulm_fm_bwd", ptr(r), ptr(g1), ptr(w), ptr(q), ptr(saved), saved.numel(), ctx.vdt, ptr(dfast), ddt,
              ptr(dqo), ptr(dr), ptr(dv), ddt, ptr(dg), ptr(dw), ptr(ws), ws_bytes, B, T, A, D, nat.stream_of(r))
         return dr, dv, dg.reshape(ctx.g_shape), dw
 

@@ -35,7 +35,7 @@ for _p in (ROOT, PKG):
 METRIC = "fast-memory fwd+bwd Mtokens/s at 110M shape (% bf16 MFMA peak); decode GB/s"
 PEAK_BF16_TFLOPS = 2516.6
 PEAK_HBM_GBPS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "la_kgroup_kernel_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "la_kgroup_kernel_traffic.txt")
 
 
 def log(msg):
@@ -53,6 +53,9 @@ def parse():
     p.add_argument("--decode-seqs", type=int, default=256)
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--copy-probe", type=int, default=0, metavar="MB",
+                   help="first run one plain fp32 copy kernel over MB megabytes (a known-size reference for "
+                        "hardware byte counters)")
     return p.parse_args()
 
 
@@ -201,6 +204,14 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    if args.copy_probe > 0:
+        n = args.copy_probe * (1 << 20) // 4
+        x = torch.ones(n, device="cuda:0")
+        y = torch.empty_like(x)
+        torch.mul(x, 1.0, out=y)   # reads and writes exactly 4 n bytes
+        torch.cuda.synchronize()
+        log(f"copy probe: {4 * n} bytes read, {4 * n} bytes written")
+        del x, y
     train = bench_training(torch, args)
     cpu = None if args.no_cpu else bench_cpu_baseline(torch, train)
     decode = None if args.no_decode else bench_decode(torch, args)

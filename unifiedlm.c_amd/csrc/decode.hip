@@ -112,20 +112,19 @@ __global__ __launch_bounds__(256) void decode_state_kernel(float *__restrict__ S
         const float vd = v[n * D + d];
         float acc = 0.f;
         if (VEC4) {
+            // S is touched once per token: non-temporal 16-byte loads and stores
+            // keep it from evicting the staged and reused data in the caches
             const int A4 = A / 4;
-            float4 *S4 = reinterpret_cast<float4 *>(Sr);
-            const float4 *q4 = reinterpret_cast<const float4 *>(sq);
-            const float4 *p4 = reinterpret_cast<const float4 *>(srp);
+            f32x4 *S4 = reinterpret_cast<f32x4 *>(Sr);
+            const f32x4 *q4 = reinterpret_cast<const f32x4 *>(sq);
+            const f32x4 *p4 = reinterpret_cast<const f32x4 *>(srp);
 #pragma unroll 4
             for (int j = lane; j < A4; j += kWave) {
-                float4 s = S4[j];
-                const float4 rp = p4[j], qq = q4[j];
-                s.x = lam * s.x + vd * rp.x;
-                s.y = lam * s.y + vd * rp.y;
-                s.z = lam * s.z + vd * rp.z;
-                s.w = lam * s.w + vd * rp.w;
-                S4[j] = s;
-                acc += s.x * qq.x + s.y * qq.y + s.z * qq.z + s.w * qq.w;
+                f32x4 s = __builtin_nontemporal_load(S4 + j);
+                const f32x4 rp = p4[j], qq = q4[j];
+                s = lam * s + vd * rp;
+                __builtin_nontemporal_store(s, S4 + j);
+                acc += s[0] * qq[0] + s[1] * qq[1] + s[2] * qq[2] + s[3] * qq[3];
             }
         } else {
             for (int a = lane; a < A; a += kWave) {

@@ -94,26 +94,35 @@ class UnifiedBlock(nn.Module):
         return x + self.dropout(self.mu((q * w).type_as(x)) + fast.type_as(x))
 
     # ---- token-by-token form (model.py:87-111)
+    @torch.no_grad()
     def init_state(self, batch: int, device):
+        """Decode state of one block, plus the fp32 views of its parameters that
+        every step uses (taken once per decode session: the weights do not
+        change while a session decodes)."""
         d, m = self.mu.out_features, self.mu.in_features
         kw = self.conv.kernel_size[0] - 1
+        f = lambda t: t.detach().to(device=device, dtype=torch.float32).contiguous()
+        w = f(self._w())
+        params = {"norm_w": f(self.norm.weight), "conv_w": f(self.conv.weight[:, 0, :]), "key_wt": f(self.key.weight.t()),
+                  "key_b": f(self.key.bias), "log_eps": f(self.log_eps).reshape(1), "val_wt": f(self.val.weight.t()),
+                  "mu_wt": f(self.mu.weight.t()), "w": w, "g": f(-self.log_rate.exp()).reshape(1)}
         return {"buf": torch.zeros(batch, d, kw, device=device, dtype=torch.float32),
                 "S": torch.zeros(batch, d, m, device=device, dtype=torch.float32),
-                "c": self._w().detach().float().expand(batch, m).contiguous(),
-                "r_prev": torch.zeros(batch, m, device=device, dtype=torch.float32)}
+                "c": w.expand(batch, m).clone(),   # updated in place: never a view of w
+                "r_prev": torch.zeros(batch, m, device=device, dtype=torch.float32),
+                "params": params}
 
     @torch.no_grad()
     def step(self, x, s):
         """x: (B, d), one position. Write (key r_{t-1}, value v_t), then read."""
+        p = s["params"]
         x32 = x.float().contiguous()
-        f = lambda t: t.detach().float().contiguous()
-        h, u = decode_pre(x32, f(self.norm.weight), f(self.conv.weight[:, 0, :]), s["buf"], self.norm.eps)
-        pre = u @ f(self.key.weight).t()
-        v = h @ f(self.val.weight).t()
-        g = f(-self.log_rate.exp()).reshape(1)
-        r, q, wq = decode_addr(pre, f(self.key.bias), f(self.log_eps).reshape(1), f(self._w()), g, s["r_prev"], s["c"])
-        ymu = wq @ f(self.mu.weight).t()
-        out = decode_state(s["S"], v, s["r_prev"], q, g, x32, ymu)
+        h, u = decode_pre(x32, p["norm_w"], p["conv_w"], s["buf"], self.norm.eps)
+        pre = u @ p["key_wt"]
+        v = h @ p["val_wt"]
+        r, q, wq = decode_addr(pre, p["key_b"], p["log_eps"], p["w"], p["g"], s["r_prev"], s["c"])
+        ymu = wq @ p["mu_wt"]
+        out = decode_state(s["S"], v, s["r_prev"], q, p["g"], x32, ymu)
         s["r_prev"] = r
         return out.to(x.dtype)
 

@@ -58,7 +58,7 @@ const char *ulm_last_error(void);
  *   q      (B,T,A) fp32   out    returned and saved
  *   fast   (B,T,D) fast_dtype out  (v.dtype in the reference, kernel.py:211)
  *   saved  ulm_fm_saved_bytes() bytes, out: what the backward needs besides
- *          r, g, w and q (the reference saves v16, c, q16, k16, kernel.py:212;
+ *          r, g and w (the reference saves v16, q, c, q16, k16, kernel.py:212;
  *          this holds the bf16 operand tiles of q, k and v, the score tiles
  *          of the dv product and the evidence n at every chunk start in place
  *          of c). Opaque; pass it unchanged to ulm_fm_bwd.
@@ -72,7 +72,8 @@ int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const float *g, const
 /* Replaces UnifiedMemory.backward (kernel.py:216-233): the three chunked
  * products dq, dk (reverse), dv (reverse) and the denominator chain rule.
  *
- *   saved   the buffer ulm_fm_fwd filled for the same r, g, w, q
+ *   saved   the buffer ulm_fm_fwd filled for the same r, g, w (q is not
+ *           needed: it is recomputed as r / c from the saved checkpoints)
  *   v_dtype the dtype of the v given to ulm_fm_fwd
  *   dfast   (B,T,D) dfast_dtype  upstream gradient of fast
  *   dq_out  (B,T,A) fp32 or NULL upstream gradient of the returned q
@@ -83,7 +84,7 @@ int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const float *g, const
  *   dw      (A,)    fp32  out
  * dg and dw are reduced deterministically (no atomics). */
 size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D, int dfast_dtype);
-int ulm_fm_bwd(const float *r, const float *g, const float *w, const float *q,
+int ulm_fm_bwd(const float *r, const float *g, const float *w,
                const void *saved, size_t saved_bytes, int v_dtype,
                const void *dfast, int dfast_dtype, const float *dq_out,
                float *dr, void *dv, int dv_dtype, float *dg, float *dw,

@@ -38,15 +38,52 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__
     const int x0 = blockIdx.x * C, n = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
     {
-        const int i = tid / 4, c0 = (tid % 4) * 16;   // position row i, 16 features
+        // position row i, 16 contiguous features (X % 16 == 0: wholly in or out)
+        const int i = tid / 4, c0 = (tid % 4) * 16;
         const int t = n * C + i;
-        const bool ok = t < T;
-        const size_t row = (static_cast<size_t>(b) * T + (ok ? t : 0)) * X;
+        float vals[16];
+        const bool vec = reinterpret_cast<uintptr_t>(src) % 16 == 0;   // 16-byte loads (else one element at a time)
+        if (t < T && x0 + c0 < X && !vec) {
+            const size_t o = (static_cast<size_t>(b) * T + t) * X + x0 + c0;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int x = x0 + c0 + e;
-            tile[i][c0 + e] = (ok && x < X) ? load_as_f32(src, row + x, sdt) : 0.f;
+            for (int e = 0; e < 16; ++e) vals[e] = load_as_f32(src, o + e, sdt);
+        } else if (t < T && x0 + c0 < X) {
+            const size_t o = (static_cast<size_t>(b) * T + t) * X + x0 + c0;
+            if (sdt == ULM_F32) {
+                const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(src) + o);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float4 w = p[k];
+                    vals[4 * k] = w.x;
+                    vals[4 * k + 1] = w.y;
+                    vals[4 * k + 2] = w.z;
+                    vals[4 * k + 3] = w.w;
+                }
+            } else {
+                const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(src) + o);
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const uint4 w = p[k];
+                    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int h = 0; h < 4; ++h) {
+                        const uint16_t lo16 = static_cast<uint16_t>(ws[h] & 0xffffu), hi16 = static_cast<uint16_t>(ws[h] >> 16);
+                        if (sdt == ULM_BF16) {
+                            vals[8 * k + 2 * h] = bf16_to_f32(lo16);
+                            vals[8 * k + 2 * h + 1] = bf16_to_f32(hi16);
+                        } else {
+                            vals[8 * k + 2 * h] = static_cast<float>(__builtin_bit_cast(_Float16, lo16));
+                            vals[8 * k + 2 * h + 1] = static_cast<float>(__builtin_bit_cast(_Float16, hi16));
+                        }
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) vals[e] = 0.f;
         }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tile[i][c0 + e] = vals[e];
     }
     __syncthreads();
     if (xr) {
@@ -119,67 +156,103 @@ __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// grid (NT, B), 256 threads. From a and b in the R layout (K % 16 == 0), wave w
-// computes the score tile (mt, nt) = (w/2, w%2) of the 64 x 64 chunk over all K
-// (tile (0, 1) lies strictly above the diagonal and is zero in both outputs);
-// P_lo and P_up go out in the tile layout (p_index) through an LDS transpose.
+// grid (NT, B), 768 threads. From a and b in the R layout (K % 16 == 0), the
+// three score tiles (mt, nt) of the 64 x 64 chunk on or below the diagonal,
+// (0,0), (1,0), (1,1), are each computed by 4 waves over a quarter of K and
+// summed through LDS in a fixed order (tile (0, 1) lies strictly above the
+// diagonal and is zero in both outputs). P_lo and P_up go out in the tile
+// layout (p_index) through an LDS transpose.
 // ALO / BLO: a / b also come with bf16 remainders (a = ah + al, b = bh + bl);
 // the product takes ah bh + ah bl + al bh over the parts present.
+constexpr int kScoreWaves = 12;
+
 template <bool ALO, bool BLO>
-__global__ __launch_bounds__(256) void scores_kernel(const uint16_t *__restrict__ aR, const uint16_t *__restrict__ aL,
-                                                     const uint16_t *__restrict__ bR, const uint16_t *__restrict__ bL,
-                                                     const float *__restrict__ g, uint16_t *__restrict__ Plo,
-                                                     uint16_t *__restrict__ Pup, int K, int NT) {
+__global__ __launch_bounds__(kScoreWaves * 64) void scores_kernel(const uint16_t *__restrict__ aR,
+                                                                  const uint16_t *__restrict__ aL,
+                                                                  const uint16_t *__restrict__ bR,
+                                                                  const uint16_t *__restrict__ bL,
+                                                                  const float *__restrict__ g,
+                                                                  uint16_t *__restrict__ Plo,
+                                                                  uint16_t *__restrict__ Pup, int K, int NT) {
     __shared__ __align__(16) uint16_t slo[C][C + 8], sup[C][C + 8];   // [i][j]
+    __shared__ float red[3][3][16][kWave];                             // partials of quarters 1..3
     const int n = blockIdx.x, b = blockIdx.y;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int lr = lane % 32, lh = lane / 32;
-    const int mt = wave >> 1, nt = wave & 1;
+    const int tile = wave / 4, kq = wave % 4;
+    const int mt = tile == 0 ? 0 : 1, nt = tile == 2 ? 1 : 0;
     const int KT = K / 16;   // tiles per R row block
-    f32x16 acc[4] = {};
-    if (!(mt == 0 && nt == 1)) {
+    const int k0 = (KT * kq) / 4, k1 = (KT * (kq + 1)) / 4;
+    // the tile above the diagonal is zero in both outputs
+    for (int e = threadIdx.x; e < 32 * 32; e += kScoreWaves * 64) {
+        slo[e / 32][32 + e % 32] = 0;
+        sup[32 + e / 32][e % 32] = 0;
+    }
+    f32x16 acc[2] = {};
+    {
         const size_t oa = ((static_cast<size_t>(b) * (2 * NT) + 2 * n + mt) * KT) * kTileElems + 8 * lane;
         const size_t ob = ((static_cast<size_t>(b) * (2 * NT) + 2 * n + nt) * KT) * kTileElems + 8 * lane;
-        const uint16_t *pa = aR + oa, *pb = bR + ob;
-        int ks = 0;
-        for (; ks + 4 <= KT; ks += 4) {
+        // batches of 8 tile pairs: all loads of a batch in flight before its MFMAs;
+        // two accumulators with fixed register indices
+        constexpr int NB = 8;
+        int ks = k0;
+        for (; ks + NB <= k1; ks += NB) {
+            bf16x8 x[NB], y[NB], xl[NB], yl[NB];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < NB; ++u) {
                 const size_t t = static_cast<size_t>(ks + u) * kTileElems;
-                const bf16x8 x = *reinterpret_cast<const bf16x8 *>(pa + t), y = *reinterpret_cast<const bf16x8 *>(pb + t);
-                acc[u] = mfma(x, y, acc[u]);
-                if (BLO) acc[u] = mfma(x, *reinterpret_cast<const bf16x8 *>(bL + ob + t), acc[u]);
-                if (ALO) acc[u] = mfma(*reinterpret_cast<const bf16x8 *>(aL + oa + t), y, acc[u]);
+                x[u] = *reinterpret_cast<const bf16x8 *>(aR + oa + t);
+                y[u] = *reinterpret_cast<const bf16x8 *>(bR + ob + t);
+                if (ALO) xl[u] = *reinterpret_cast<const bf16x8 *>(aL + oa + t);
+                if (BLO) yl[u] = *reinterpret_cast<const bf16x8 *>(bL + ob + t);
+            }
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                f32x16 &c = acc[u & 1];
+                c = mfma(x[u], y[u], c);
+                if (BLO) c = mfma(x[u], yl[u], c);
+                if (ALO) c = mfma(xl[u], y[u], c);
             }
         }
-        for (; ks < KT; ++ks) {
+        for (; ks < k1; ++ks) {
             const size_t t = static_cast<size_t>(ks) * kTileElems;
-            const bf16x8 x = *reinterpret_cast<const bf16x8 *>(pa + t), y = *reinterpret_cast<const bf16x8 *>(pb + t);
+            const bf16x8 x = *reinterpret_cast<const bf16x8 *>(aR + oa + t);
+            const bf16x8 y = *reinterpret_cast<const bf16x8 *>(bR + ob + t);
             acc[0] = mfma(x, y, acc[0]);
             if (BLO) acc[0] = mfma(x, *reinterpret_cast<const bf16x8 *>(bL + ob + t), acc[0]);
             if (ALO) acc[0] = mfma(*reinterpret_cast<const bf16x8 *>(aL + oa + t), y, acc[0]);
         }
     }
-    const float gl = g[0];
-    const int j = 32 * nt + lr;
+    if (kq > 0) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int i = 32 * mt + 8 * (r / 4) + 4 * lh + (r % 4);
-        const float sv = acc[0][r] + acc[1][r] + acc[2][r] + acc[3][r];
-        const int lag = i - j;
-        const uint16_t v = f32_to_bf16_bits(lag >= 0 ? sv * __expf(gl * static_cast<float>(lag)) : 0.f);
-        slo[i][j] = v;   // P_lo[i][j]
-        sup[j][i] = v;   // P_up[j][i] = P_lo[i][j]
+        for (int r = 0; r < 16; ++r) red[tile][kq - 1][r][lane] = acc[0][r] + acc[1][r];
     }
     __syncthreads();
-    // 2 x 8 tiles of 1 KB: thread -> 2 lanes of one tile of each
-    const int tl = threadIdx.x / 32, tm = tl / 4, tq = tl % 4;
+    if (kq == 0) {
+        const float gl = g[0];
+        const int j = 32 * nt + lr;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int l = 2 * (threadIdx.x % 32) + u, i = 32 * tm + l % 32, j0 = 16 * tq + 8 * (l / 32);
-        const size_t o = p_index(b, n, i, j0, NT);
-        *reinterpret_cast<uint4 *>(Plo + o) = *reinterpret_cast<const uint4 *>(&slo[i][j0]);
-        *reinterpret_cast<uint4 *>(Pup + o) = *reinterpret_cast<const uint4 *>(&sup[i][j0]);
+        for (int r = 0; r < 16; ++r) {
+            const int i = 32 * mt + 8 * (r / 4) + 4 * lh + (r % 4);
+            const float sv = (acc[0][r] + acc[1][r]) + red[tile][0][r][lane] + red[tile][1][r][lane] +
+                             red[tile][2][r][lane];
+            const int lag = i - j;
+            const uint16_t v = f32_to_bf16_bits(lag >= 0 ? sv * __expf(gl * static_cast<float>(lag)) : 0.f);
+            slo[i][j] = v;   // P_lo[i][j]
+            sup[j][i] = v;   // P_up[j][i] = P_lo[i][j]
+        }
+    }
+    __syncthreads();
+    // 2 x 8 tiles of 1 KB: the first 256 threads, 2 lanes of one tile of each
+    if (threadIdx.x < 256) {
+        const int tl = threadIdx.x / 32, tm = tl / 4, tq = tl % 4;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int l = 2 * (threadIdx.x % 32) + u, i = 32 * tm + l % 32, j0 = 16 * tq + 8 * (l / 32);
+            const size_t o = p_index(b, n, i, j0, NT);
+            *reinterpret_cast<uint4 *>(Plo + o) = *reinterpret_cast<const uint4 *>(&slo[i][j0]);
+            *reinterpret_cast<uint4 *>(Pup + o) = *reinterpret_cast<const uint4 *>(&sup[i][j0]);
+        }
     }
 }
 
@@ -240,10 +313,11 @@ int launch_chunk_scores(const uint16_t *aR, const uint16_t *aL, const uint16_t *
     if (K % 16) return fail(ULM_ERR_UNSUPPORTED, "chunk scores: K=%d is not a multiple of 16", K);
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
     const dim3 grid(NT, B);
-    if (aL && bL) chunks::scores_kernel<true, true><<<grid, 256, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
-    else if (aL) chunks::scores_kernel<true, false><<<grid, 256, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
-    else if (bL) chunks::scores_kernel<false, true><<<grid, 256, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
-    else chunks::scores_kernel<false, false><<<grid, 256, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
+    const int nthreads = chunks::kScoreWaves * kWave;
+    if (aL && bL) chunks::scores_kernel<true, true><<<grid, nthreads, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
+    else if (aL) chunks::scores_kernel<true, false><<<grid, nthreads, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
+    else if (bL) chunks::scores_kernel<false, true><<<grid, nthreads, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
+    else chunks::scores_kernel<false, false><<<grid, nthreads, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
     return check_launch("chunk scores_kernel");
 }
 

@@ -47,7 +47,7 @@ int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, u
                      uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, int B, int T, int A,
                      hipStream_t s);
 size_t bwd_stats_partial_bytes(int B, int A);
-int launch_bwd_stats(const float *dqf, const float *dqo, const float *q, const float *r, const float *nck,
+int launch_bwd_stats(const float *dqf, const float *dqo, const float *r, const float *nck,
                      const float *w, const float *g, const float *dkf, float *dr, float *dw, float *dg, void *part,
                      int B, int T, int A, hipStream_t s);
 
@@ -282,14 +282,14 @@ extern "C" size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D, int dfa
     return bwd_layout(nullptr, B, T, A, D, dfast_dtype).bytes;
 }
 
-extern "C" int ulm_fm_bwd(const float *r, const float *g, const float *w, const float *q, const void *saved,
+extern "C" int ulm_fm_bwd(const float *r, const float *g, const float *w, const void *saved,
                           size_t saved_bytes, int v_dtype, const void *dfast, int dfast_dtype, const float *dq_out,
                           float *dr, void *dv, int dv_dtype, float *dg, float *dw, void *workspace,
                           size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
     ULM_REQUIRE(B > 0 && T > 0 && A > 0 && D > 0, "ulm_fm_bwd: bad sizes B=%d T=%d A=%d D=%d", B, T, A, D);
     ULM_REQUIRE(valid_dtype(v_dtype) && valid_dtype(dfast_dtype) && valid_dtype(dv_dtype),
                 "ulm_fm_bwd: bad dtype %d/%d/%d", v_dtype, dfast_dtype, dv_dtype);
-    ULM_REQUIRE(r && g && w && q && saved && dfast && dr && dv && dg && dw, "ulm_fm_bwd: null pointer");
+    ULM_REQUIRE(r && g && w && saved && dfast && dr && dv && dg && dw, "ulm_fm_bwd: null pointer");
     const size_t need_s = ulm_fm_saved_bytes(B, T, A, D, v_dtype);
     ULM_REQUIRE(saved_bytes >= need_s, "ulm_fm_bwd: saved buffer of %zu bytes, need %zu", saved_bytes, need_s);
     const size_t need = ulm_fm_bwd_workspace_bytes(B, T, A, D, dfast_dtype);
@@ -334,5 +334,5 @@ extern "C" int ulm_fm_bwd(const float *r, const float *g, const float *w, const 
         ULM_TRY(launch_la_generic(sv.k16n, sv.q16n, do16, g, dv_acc, B, T, A, D, true, s));
         if (dv_dtype != ULM_F32) ULM_TRY(launch_convert(dv_acc, ULM_F32, dv, dv_dtype, nd, s));
     }
-    return launch_bwd_stats(ws.dqf, dq_out, q, r, sv.nck, w, g, ws.dkf, dr, dw, dg, ws.stats, B, T, A, s);
+    return launch_bwd_stats(ws.dqf, dq_out, r, sv.nck, w, g, ws.dkf, dr, dw, dg, ws.stats, B, T, A, s);
 }

@@ -133,7 +133,7 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict_
 }
 
 __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict__ dqf, const float *__restrict__ dqo,
-                                                        const float *__restrict__ q, const float *__restrict__ r,
+                                                        const float *__restrict__ r,
                                                         const float *__restrict__ nck, const float *__restrict__ w,
                                                         const float *__restrict__ g, const float *__restrict__ dkf,
                                                         float *__restrict__ dr, float *__restrict__ dw_part,
@@ -192,8 +192,9 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
         float racc = 0.f;
 #pragma unroll
         for (int i = kSeg - 1; i >= 0; --i) {
-            const int t = t0 + i;
-            const float qt = (va && t < T) ? q[(b * T + t) * A + a] : 0.f;
+            // q = r / c, recomputed with the forward's operations (c is rebuilt
+            // exactly from its checkpoint), so q is not read back from HBM
+            const float qt = rv[i] / cv[i];
             dc[i] = -dq[i] * qt / cv[i];
             racc = dc[i] + lam * racc;
             rl[i] = racc;
@@ -246,20 +247,26 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
     if (threadIdx.x == 0) dg_part[b * gridDim.x + blockIdx.x] = dg_sh[0] + dg_sh[1] + dg_sh[2] + dg_sh[3];
 }
 
-// dw[a] = sum_b dw_part[b, a]; dg = sum of all dg partials, in a fixed order.
+// dw[a] = sum_b dw_part[b, a]; dg = sum of all dg partials. Every sum runs in a
+// fixed order (thread-strided partial sums, then a fixed shuffle tree), so the
+// result does not depend on scheduling.
 __global__ __launch_bounds__(256) void stats_reduce_kernel(const float *__restrict__ dw_part,
                                                            const double *__restrict__ dg_part, float *__restrict__ dw,
                                                            float *__restrict__ dg, int B, int A, int ndg) {
+    __shared__ double red[4];
     const int a = blockIdx.x * 256 + threadIdx.x;
     if (a < A) {
         float s = 0.f;
         for (int b = 0; b < B; ++b) s += dw_part[static_cast<size_t>(b) * A + a];
         dw[a] = s;
     }
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
+    if (blockIdx.x == 0) {
         double s = 0.0;
-        for (int k = 0; k < ndg; ++k) s += dg_part[k];
-        dg[0] = static_cast<float>(s);
+        for (int k = threadIdx.x; k < ndg; k += 256) s += dg_part[k];
+        s = wave_sum(s);
+        if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = s;
+        __syncthreads();
+        if (threadIdx.x == 0) dg[0] = static_cast<float>((red[0] + red[1]) + (red[2] + red[3]));
     }
 }
 
@@ -283,7 +290,7 @@ size_t bwd_stats_partial_bytes(int B, int A) {
     return align_up(static_cast<size_t>(B) * A * sizeof(float), 256) + align_up(B * nb * sizeof(double), 256);
 }
 
-int launch_bwd_stats(const float *dqf, const float *dqo, const float *q, const float *r, const float *nck,
+int launch_bwd_stats(const float *dqf, const float *dqo, const float *r, const float *nck,
                      const float *w, const float *g, const float *dkf, float *dr, float *dw, float *dg, void *part,
                      int B, int T, int A, hipStream_t s) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
@@ -291,7 +298,7 @@ int launch_bwd_stats(const float *dqf, const float *dqo, const float *q, const f
     float *dw_part = static_cast<float *>(part);
     double *dg_part = reinterpret_cast<double *>(static_cast<char *>(part) +
                                                  align_up(static_cast<size_t>(B) * A * sizeof(float), 256));
-    bwd_stats_kernel<<<dim3(nb, B), 256, 0, s>>>(dqf, dqo, q, r, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT);
+    bwd_stats_kernel<<<dim3(nb, B), 256, 0, s>>>(dqf, dqo, r, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT);
     int st = check_launch("bwd_stats_kernel");
     if (st) return st;
     stats_reduce_kernel<<<(A + 255) / 256, 256, 0, s>>>(dw_part, dg_part, dw, dg, B, A, B * nb);

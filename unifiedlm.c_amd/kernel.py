@@ -50,7 +50,7 @@ def _check_fm(r, v, g, w):
 
 
 class UnifiedMemory(torch.autograd.Function):
-    """Replaces kernel.py:199-233. Saves r, g, w, q and one opaque buffer that
+    """Replaces kernel.py:199-233. Saves r, g, w and one opaque buffer that
     the forward fills with what the backward needs (bf16 operand tiles of q, k
     and v, score tiles and the per-chunk evidence checkpoints that stand in for
     the full c tensor). v is passed in its own dtype; the library casts it to
@@ -74,13 +74,13 @@ class UnifiedMemory(torch.autograd.Function):
         ws = torch.empty(max(ws_bytes, 1), device=r.device, dtype=torch.uint8)
         call("ulm_fm_fwd", ptr(r32), ptr(vc), vdt, ptr(g1), ptr(w32), ptr(q), ptr(fast), vdt, ptr(saved), saved_bytes,
              ptr(ws), ws_bytes, B, T, A, D, nat.stream_of(r))
-        ctx.save_for_backward(r32, g1, w32, q, saved)
+        ctx.save_for_backward(r32, g1, w32, saved)
         ctx.g_shape, ctx.D, ctx.vdt = g.shape, D, vdt
         return q, fast
 
     @staticmethod
     def backward(ctx, dq_out, dfast):
-        r, g1, w, q, saved = ctx.saved_tensors
+        r, g1, w, saved = ctx.saved_tensors
         B, T, A = r.shape
         D = ctx.D
         if dfast is None:
@@ -94,7 +94,7 @@ class UnifiedMemory(torch.autograd.Function):
         dw = torch.empty(A, device=r.device, dtype=torch.float32)
         ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D, ddt)
         ws = torch.empty(ws_bytes, device=r.device, dtype=torch.uint8)
-        call("ulm_fm_bwd", ptr(r), ptr(g1), ptr(w), ptr(q), ptr(saved), saved.numel(), ctx.vdt, ptr(dfast), ddt,
+        call("ulm_fm_bwd", ptr(r), ptr(g1), ptr(w), ptr(saved), saved.numel(), ctx.vdt, ptr(dfast), ddt,
              ptr(dqo), ptr(dr), ptr(dv), ddt, ptr(dg), ptr(dw), ptr(ws), ws_bytes, B, T, A, D, nat.stream_of(r))
         return dr, dv, dg.reshape(ctx.g_shape), dw
 

@@ -26,7 +26,7 @@ SIGNATURES = {
     "ulm_fm_fwd_workspace_bytes": (SZ, [I, I, I, I, I]),
     "ulm_fm_fwd": (I, [P, P, I, P, P, P, P, I, P, SZ, P, SZ, I, I, I, I, P]),
     "ulm_fm_bwd_workspace_bytes": (SZ, [I, I, I, I, I]),
-    "ulm_fm_bwd": (I, [P, P, P, P, P, SZ, I, P, I, P, P, P, I, P, P, P, SZ, I, I, I, I, P]),
+    "ulm_fm_bwd": (I, [P, P, P, P, SZ, I, P, I, P, P, P, I, P, P, P, SZ, I, I, I, I, P]),
     "ulm_la_workspace_bytes": (SZ, [I, I, I, I]),
     "ulm_la": (I, [P, P, P, P, P, I, I, I, I, I, I, P, SZ, P]),
     "ulm_addr_fwd": (I, [P, I, P, P, P, P, I, I, P]),

@@ -52,18 +52,18 @@ def test_workspace_sizes():
     # 4 key groups of 768 slots: fp32 partial outputs, plus the forward score tiles
     assert lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_F32) >= 4 * B * T * D * 4 + B * NT * 64 * 64 * 2
     assert lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * D * 4
-    assert lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * (2 * A * 4 + D * 6)
-    # an fp32 dfast adds the bf16 remainder tiles of its read-out operand
+    assert lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * (2 * A * 4 + D * 4)
+    # an fp32 dfast adds the bf16 remainder tiles of its two tiled copies
     assert (lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32)
-            - lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16)) == B * T * D * 2
-    # saved: bf16 q, k in natural and transposed layouts, three v copies, n checkpoints
-    assert lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * (8 * A + 8 * D) + B * NT * A * 4
+            - lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16)) == 2 * B * T * D * 2
+    # saved: bf16 q, k in both tiled layouts, two v copies, n checkpoints
+    assert lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * (8 * A + 4 * D) + B * NT * A * 4
     assert (lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_F32)
-            - lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_BF16)) == B * T * D * 2
+            - lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_BF16)) == 2 * B * T * D * 2
     # unaligned sizes keep only natural bf16 copies of q, k, v and the checkpoints
     assert lib.ulm_fm_saved_bytes(2, 70, 12, 8, nat.ULM_F32) >= 2 * 70 * (12 * 4 + 8 * 2) + 2 * 2 * 12 * 4
     assert lib.ulm_la_workspace_bytes(2, 70, 12, 8) == 0
-    assert lib.ulm_la_workspace_bytes(B, T, A, D) >= 2 * B * NT * A * 64 * 2 + 4 * B * T * D * 4
+    assert lib.ulm_la_workspace_bytes(B, T, A, D) >= 3 * B * NT * A * 64 * 2 + 4 * B * T * D * 4
     assert lib.ulm_addr_bwd_workspace_bytes(B * T, A) >= A * 4
     assert lib.ulm_fm_bwd_workspace_bytes(0, T, A, D, nat.ULM_F32) == 0
 

@@ -2,7 +2,7 @@
 //
 //  * chunk_transpose: the tiled copies of a (B, T, X) tensor that the chunked
 //    kernel loads (R and Q layouts of ulm_common.h; positions past T are zero),
-//    optionally with the pre-decayed copy its state update consumes.
+//    each optionally with its bf16 rounding remainder.
 //  * chunk_scores: per chunk n, with S[i][j] = a_{64n+i} . b_{64n+j},
 //      P_lo[i][j] = S[i][j] lam^(i-j)  (j <= i, else 0)   forward walk
 //      P_up[i][j] = S[j][i] lam^(j-i)  (j >= i, else 0)   = P_lo^T
@@ -22,18 +22,11 @@ constexpr int C = ULM_CHUNK;
 
 // grid (ceil(X/64), NT, B), 256 threads: one 64-position x 64-feature block of
 // X (B, T, X) in any float dtype (X % 32 == 0). Outputs, each optional: raw =
-// bf16(x) in the Q layout; the pre-decayed update operand hi (+ lo, the
-// rounding remainder) in the Q layout, from the full-precision x; xr = bf16(x)
-// (+ xr_lo = bf16(x - xr)) in the R layout. DEC = 1 / 2 decays for the forward
-// / reversed walk:
-//   forward  lam^(63-i) x / s_{n+1}          at walk step n
-//   reversed lam^i      x / s_{NT-n}         at walk step NT-1-n
-// with s the state scale schedule of the chunked kernel (state_inv_scale).
-template <int DEC>
+// bf16(x) (+ raw_lo = bf16(x - raw), the rounding remainder) in the Q layout;
+// xr = bf16(x) (+ xr_lo) in the R layout.
 __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__ src, int sdt, uint16_t *__restrict__ raw,
-                                                        uint16_t *__restrict__ hi, uint16_t *__restrict__ lo,
-                                                        uint16_t *__restrict__ xr, uint16_t *__restrict__ xr_lo,
-                                                        const float *__restrict__ g, int T, int X, int NT) {
+                                                        uint16_t *__restrict__ raw_lo, uint16_t *__restrict__ xr,
+                                                        uint16_t *__restrict__ xr_lo, int T, int X, int NT) {
     __shared__ float tile[C][C + 1];   // [position][feature]
     const int x0 = blockIdx.x * C, n = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
@@ -115,39 +108,18 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__
     if (raw) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            uint32_t w[4];
+            uint32_t wh[4], wl[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                w[e] = static_cast<uint32_t>(f32_to_bf16_bits(tile[i0 + 8 * h + 2 * e][xl])) |
-                       (static_cast<uint32_t>(f32_to_bf16_bits(tile[i0 + 8 * h + 2 * e + 1][xl])) << 16);
-            *reinterpret_cast<uint4 *>(raw + q_index(b, n * C + i0 + 8 * h, x, NT, X)) = make_uint4(w[0], w[1], w[2], w[3]);
-        }
-    }
-    if (DEC) {
-        const float gl = g[0];
-        const int step = DEC == 1 ? n : NT - 1 - n;
-        const float inv_s = state_inv_scale(state_lam64(gl), step);
-        uint32_t wh[8], wl[8];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int i = i0 + e;
-            const float f = __expf(gl * static_cast<float>(DEC == 1 ? C - 1 - i : i)) * inv_s;
-            const float v = tile[i][xl] * f;
-            const uint16_t h = f32_to_bf16_bits(v);
-            const uint16_t l = f32_to_bf16_bits(v - bf16_to_f32(h));
-            if (e % 2 == 0) {
-                wh[e / 2] = h;
-                wl[e / 2] = l;
-            } else {
-                wh[e / 2] |= static_cast<uint32_t>(h) << 16;
-                wl[e / 2] |= static_cast<uint32_t>(l) << 16;
+            for (int e = 0; e < 4; ++e) {
+                const float v0 = tile[i0 + 8 * h + 2 * e][xl], v1 = tile[i0 + 8 * h + 2 * e + 1][xl];
+                const uint16_t h0 = f32_to_bf16_bits(v0), h1 = f32_to_bf16_bits(v1);
+                wh[e] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+                wl[e] = static_cast<uint32_t>(f32_to_bf16_bits(v0 - bf16_to_f32(h0))) |
+                        (static_cast<uint32_t>(f32_to_bf16_bits(v1 - bf16_to_f32(h1))) << 16);
             }
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
             const size_t o = q_index(b, n * C + i0 + 8 * h, x, NT, X);
-            *reinterpret_cast<uint4 *>(hi + o) = make_uint4(wh[4 * h], wh[4 * h + 1], wh[4 * h + 2], wh[4 * h + 3]);
-            if (lo) *reinterpret_cast<uint4 *>(lo + o) = make_uint4(wl[4 * h], wl[4 * h + 1], wl[4 * h + 2], wl[4 * h + 3]);
+            *reinterpret_cast<uint4 *>(raw + o) = make_uint4(wh[0], wh[1], wh[2], wh[3]);
+            if (raw_lo) *reinterpret_cast<uint4 *>(raw_lo + o) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
         }
     }
 }
@@ -289,20 +261,16 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(const float *__rest
 
 }  // namespace chunks
 
-// Tiled copies of X (B, T, X): raw, hi, lo in the Q layout and xr (+ xr_lo) in
-// the R layout, each bf16 or null (X % 32 == 0). decay 0: no hi / lo; 1 / 2: hi
-// (+ lo) hold the pre-decayed update operand of the forward / reversed walk.
-int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t *hi, uint16_t *lo, uint16_t *xr,
-                           uint16_t *xr_lo, const float *g, int decay, int B, int T, int X, hipStream_t s) {
+// Tiled copies of X (B, T, X): raw (+ raw_lo) in the Q layout and xr (+ xr_lo)
+// in the R layout, each bf16 or null (X % 32 == 0).
+int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t *raw_lo, uint16_t *xr,
+                           uint16_t *xr_lo, int B, int T, int X, hipStream_t s) {
     if (X % 32) return fail(ULM_ERR_INVALID, "chunk transpose: X=%d is not a multiple of 32", X);
-    if (decay && !(hi && g)) return fail(ULM_ERR_INVALID, "chunk transpose: decayed output needs hi and g");
+    if (raw_lo && !raw) return fail(ULM_ERR_INVALID, "chunk transpose: raw_lo needs raw");
     if (xr_lo && !xr) return fail(ULM_ERR_INVALID, "chunk transpose: xr_lo needs xr");
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
     const dim3 grid((X + ULM_CHUNK - 1) / ULM_CHUNK, NT, B);
-    if (decay == 1) chunks::transpose_kernel<1><<<grid, 256, 0, s>>>(src, src_dt, raw, hi, lo, xr, xr_lo, g, T, X, NT);
-    else if (decay == 2)
-        chunks::transpose_kernel<2><<<grid, 256, 0, s>>>(src, src_dt, raw, hi, lo, xr, xr_lo, g, T, X, NT);
-    else chunks::transpose_kernel<0><<<grid, 256, 0, s>>>(src, src_dt, raw, nullptr, nullptr, xr, xr_lo, g, T, X, NT);
+    chunks::transpose_kernel<<<grid, 256, 0, s>>>(src, src_dt, raw, raw_lo, xr, xr_lo, T, X, NT);
     return check_launch("chunk transpose_kernel");
 }
 

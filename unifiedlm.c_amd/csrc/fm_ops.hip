@@ -11,15 +11,15 @@
 // intra-chunk product in the Q layout, the intra-chunk matrices from
 // chunk_scores. The reversed products walk the forward chunks backwards, so one
 // tiled copy per tensor serves both directions and the score tiles pair up:
-// P_dv = P_fwd^T, P_dk = P_dq^T. The decay of the state update always rides on
-// the D-sized tensor of the product (v or dfast), pre-multiplied into a bf16
-// hi + lo copy: v forward for fast and dq, dfast reversed for dk and dv.
-// When v or dfast arrive in fp32 (or fp16), the products behind the d/dg
-// identity (dq, dk and their scores) also take their read-out operand as
-// bf16 hi + lo, so both sides of the identity see the same full-precision v
-// and dfast (the bf16 rounding of either one alone breaks the cancellation).
+// P_dv = P_fwd^T, P_dk = P_dq^T. The decay of the state update is applied in
+// the kernel to c, the value operand. The products behind the d/dg identity
+// (dq and dk) add the bf16 rounding remainder of the decayed c as a second
+// update pass. When v or dfast arrive in fp32 (or fp16), every operand made
+// from them is also carried as bf16 hi + lo, so both sides of the identity see
+// the same full-precision v and dfast (the bf16 rounding of either one alone
+// breaks the cancellation).
 // The forward keeps what the backward needs in one "saved" buffer:
-//   qR, kR, qQ, kQ (B, NT, 64 A) bf16 tiles; vR (+ vR~lo), vQ, vQ~hi, vQ~lo
+//   qR, kR, qQ, kQ (B, NT, 64 A) bf16 tiles; vR, vQ (+ their remainders)
 //   (B, NT, 64 D); P_dv (B, NT, 64, 64) bf16 tiles; n_ckpt (B, NT, A) fp32.
 // Other shapes use the generic kernel of fm_chunk.hip (atomics into zeroed
 // fp32 outputs) on natural bf16 copies of q, k and v.
@@ -34,11 +34,11 @@ int launch_la_generic(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
 int la_kgroup_groups(int K);
 bool la_kgroup_supported(int B, int T, int K, int V);
 int launch_la_kgroup(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo,
-                     const uint16_t *ub, const uint16_t *cr, const uint16_t *P, const float *g, float *out, int B,
-                     int T, int K, int V, bool reverse, hipStream_t s);
+                     const uint16_t *c, const uint16_t *clo, const uint16_t *P, const float *g, float *out, int B,
+                     int T, int K, int V, bool reverse, bool ubsplit, hipStream_t s);
 // fm_chunks.hip
-int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t *hi, uint16_t *lo, uint16_t *xr,
-                           uint16_t *xr_lo, const float *g, int decay, int B, int T, int X, hipStream_t s);
+int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t *raw_lo, uint16_t *xr,
+                           uint16_t *xr_lo, int B, int T, int X, hipStream_t s);
 int launch_chunk_scores(const uint16_t *aR, const uint16_t *aL, const uint16_t *bR, const uint16_t *bL, const float *g,
                         uint16_t *Plo, uint16_t *Pup, int B, int T, int K, hipStream_t s);
 int launch_partial_reduce(const float *part, int nK, size_t n, void *out, int odt, hipStream_t s);
@@ -76,7 +76,7 @@ bool fm_aligned(int B, int T, int A, int D) {
 
 struct Saved {
     uint16_t *q16n, *k16n, *v16n;                                     // generic path
-    uint16_t *qR, *kR, *qQ, *kQ, *vR, *vRl, *vQ, *vQh, *vQl, *Pdv;   // K-group path
+    uint16_t *qR, *kR, *qQ, *kQ, *vR, *vRl, *vQ, *vQl, *Pdv;   // K-group path
     float *nck;
     size_t bytes;
 };
@@ -94,8 +94,7 @@ Saved saved_layout(void *base, int B, int T, int A, int D, int v_dtype) {
         s.vR = c.take<uint16_t>(td);
         if (v_dtype != ULM_BF16) s.vRl = c.take<uint16_t>(td);
         s.vQ = c.take<uint16_t>(td);
-        s.vQh = c.take<uint16_t>(td);
-        s.vQl = c.take<uint16_t>(td);
+        if (v_dtype != ULM_BF16) s.vQl = c.take<uint16_t>(td);
         s.Pdv = c.take<uint16_t>(B * NT * ULM_CHUNK * ULM_CHUNK);
     } else {
         s.q16n = c.take<uint16_t>(na);
@@ -130,7 +129,7 @@ FwdWs fwd_layout(void *base, int B, int T, int A, int D, int fast_dtype) {
 
 struct BwdWs {
     uint16_t *do16;                                          // generic path
-    uint16_t *doR, *doRl, *doQ, *doQh, *doQl, *Pdq, *Pdk;   // K-group path
+    uint16_t *doR, *doRl, *doQ, *doQl, *Pdq, *Pdk;   // K-group path
     float *dqf, *dkf, *part;
     void *stats;
     size_t bytes;
@@ -147,8 +146,7 @@ BwdWs bwd_layout(void *base, int B, int T, int A, int D, int dfast_dtype) {
         w.doR = c.take<uint16_t>(td);
         if (dfast_dtype != ULM_BF16) w.doRl = c.take<uint16_t>(td);
         w.doQ = c.take<uint16_t>(td);
-        w.doQh = c.take<uint16_t>(td);
-        w.doQl = c.take<uint16_t>(td);
+        if (dfast_dtype != ULM_BF16) w.doQl = c.take<uint16_t>(td);
         w.Pdq = c.take<uint16_t>(B * NT * ULM_CHUNK * ULM_CHUNK);
         w.Pdk = c.take<uint16_t>(B * NT * ULM_CHUNK * ULM_CHUNK);
         const int nkd = la_kgroup_groups(D), nka = la_kgroup_groups(A);
@@ -185,7 +183,7 @@ extern "C" size_t ulm_la_workspace_bytes(int B, int T, int K, int V) {
     const size_t NT = nt_of(T), tk = B * NT * 64 * K, tv = B * NT * 64 * V;
     Carver c(nullptr);
     c.take<uint16_t>(2 * tk);                                 // a and b, R layout
-    c.take<uint16_t>(2 * tk);                                 // decayed b, Q layout, hi and lo
+    c.take<uint16_t>(tk);                                     // b, Q layout
     c.take<uint16_t>(tv);                                     // c, Q layout
     c.take<uint16_t>(2 * B * NT * ULM_CHUNK * ULM_CHUNK);     // P_lo, P_up
     const int nkg = la_kgroup_groups(K);
@@ -210,21 +208,18 @@ extern "C" int ulm_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
     Carver cv(workspace);
     uint16_t *aR = cv.take<uint16_t>(2 * tk);
     uint16_t *bR = aR + tk;
-    uint16_t *bQh = cv.take<uint16_t>(2 * tk);
-    uint16_t *bQl = bQh + tk;
+    uint16_t *bQ = cv.take<uint16_t>(tk);
     uint16_t *cQ = cv.take<uint16_t>(tv);
     uint16_t *Plo = cv.take<uint16_t>(2 * B * NT * ULM_CHUNK * ULM_CHUNK);
     uint16_t *Pup = Plo + B * NT * ULM_CHUNK * ULM_CHUNK;
     const int nkg = la_kgroup_groups(K);
     float *part = nkg > 1 ? cv.take<float>(static_cast<size_t>(nkg) * B * T * V) : out;
-    // the decay of the state update rides on b
-    ULM_TRY(launch_chunk_transpose(a, ULM_BF16, nullptr, nullptr, nullptr, aR, nullptr, g, 0, B, T, K, s));
-    ULM_TRY(launch_chunk_transpose(b, ULM_BF16, nullptr, bQh, split ? bQl : nullptr, bR, nullptr, g, reverse ? 2 : 1, B,
-                                   T, K, s));
-    ULM_TRY(launch_chunk_transpose(c, ULM_BF16, cQ, nullptr, nullptr, nullptr, nullptr, g, 0, B, T, V, s));
+    ULM_TRY(launch_chunk_transpose(a, ULM_BF16, nullptr, nullptr, aR, nullptr, B, T, K, s));
+    ULM_TRY(launch_chunk_transpose(b, ULM_BF16, bQ, nullptr, bR, nullptr, B, T, K, s));
+    ULM_TRY(launch_chunk_transpose(c, ULM_BF16, cQ, nullptr, nullptr, nullptr, B, T, V, s));
     ULM_TRY(launch_chunk_scores(reverse ? bR : aR, nullptr, reverse ? aR : bR, nullptr, g, Plo, Pup, B, T, K, s));
-    ULM_TRY(launch_la_kgroup(aR, nullptr, bQh, split ? bQl : nullptr, cQ, cQ, reverse ? Pup : Plo, g, part, B, T, K, V,
-                             reverse != 0, s));
+    ULM_TRY(launch_la_kgroup(aR, nullptr, bQ, nullptr, cQ, nullptr, reverse ? Pup : Plo, g, part, B, T, K, V,
+                             reverse != 0, split != 0, s));
     if (nkg > 1) ULM_TRY(launch_partial_reduce(part, nkg, static_cast<size_t>(B) * T * V, out, ULM_F32, s));
     return ULM_OK;
 }
@@ -261,10 +256,12 @@ extern "C" int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const floa
         const int nkg = la_kgroup_groups(A);
         float *acc = ws.part ? ws.part : static_cast<float *>(fast);
         ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, sv.qR, sv.kR, sv.qQ, sv.kQ, sv.nck, B, T, A, s));
-        ULM_TRY(launch_chunk_transpose(v, v_dtype, sv.vQ, sv.vQh, sv.vQl, sv.vR, sv.vRl, g, 1, B, T, D, s));
+        ULM_TRY(launch_chunk_transpose(v, v_dtype, sv.vQ, sv.vQl, sv.vR, sv.vRl, B, T, D, s));
         ULM_TRY(launch_chunk_scores(sv.qR, nullptr, sv.kR, nullptr, g, ws.Pf, sv.Pdv, B, T, A, s));
-        // fast = LA(q, k, v): update k^T v~, intra on bf16(v), as the reference's bf16 v (kernel.py:205)
-        ULM_TRY(launch_la_kgroup(sv.qR, nullptr, sv.kQ, nullptr, sv.vQh, sv.vQ, ws.Pf, g, acc, B, T, A, D, false, s));
+        // fast = LA(q, k, v): update k^T v~ (v~ from the full-precision v), intra on
+        // bf16(v), as the reference's bf16 v (kernel.py:205)
+        ULM_TRY(launch_la_kgroup(sv.qR, nullptr, sv.kQ, nullptr, sv.vQ, sv.vQl, ws.Pf, g, acc, B, T, A, D, false, false,
+                                 s));
         if (ws.part) ULM_TRY(launch_partial_reduce(ws.part, nkg, nf, fast, fast_dtype, s));
         return ULM_OK;
     }
@@ -301,23 +298,24 @@ extern "C" int ulm_fm_bwd(const float *r, const float *g, const float *w, const 
     const size_t nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
     if (fm_aligned(B, T, A, D)) {
         const int nkd = la_kgroup_groups(D), nka = la_kgroup_groups(A);
-        ULM_TRY(launch_chunk_transpose(dfast, dfast_dtype, ws.doQ, ws.doQh, ws.doQl, ws.doR, ws.doRl, g, 2, B, T, D, s));
+        ULM_TRY(launch_chunk_transpose(dfast, dfast_dtype, ws.doQ, ws.doQl, ws.doR, ws.doRl, B, T, D, s));
         ULM_TRY(launch_chunk_scores(ws.doR, ws.doRl, sv.vR, sv.vRl, g, ws.Pdq, ws.Pdk, B, T, D, s));
-        // dq_f = LA(dfast, v, k): keys = D, values = A; update v~^T k.
-        // dk_f = LA_rev(v, dfast, q): update dfast~^T q.
+        // dq_f = LA(dfast, v, k): keys = D, values = A; update v^T k~.
+        // dk_f = LA_rev(v, dfast, q): update dfast^T q~.
         // Both feed the positional d/dg identity, whose cancellation amplifies
-        // rounding, so their decayed operand is carried as bf16 hi + lo (and
-        // their read-out operand too when it arrived in more than bf16).
-        ULM_TRY(launch_la_kgroup(ws.doR, ws.doRl, sv.vQh, sv.vQl, sv.kQ, sv.kQ, ws.Pdq, g, nkd > 1 ? ws.part : ws.dqf, B,
-                                 T, D, A, false, s));
+        // rounding, so the decayed k~ / q~ take their bf16 remainder as a second
+        // pass (and v, dfast their hi + lo pairs when they arrived in more than bf16).
+        ULM_TRY(launch_la_kgroup(ws.doR, ws.doRl, sv.vQ, sv.vQl, sv.kQ, nullptr, ws.Pdq, g, nkd > 1 ? ws.part : ws.dqf,
+                                 B, T, D, A, false, true, s));
         if (nkd > 1) ULM_TRY(launch_partial_reduce(ws.part, nkd, na, ws.dqf, ULM_F32, s));
-        ULM_TRY(launch_la_kgroup(sv.vR, sv.vRl, ws.doQh, ws.doQl, sv.qQ, sv.qQ, ws.Pdk, g, nkd > 1 ? ws.part : ws.dkf, B,
-                                 T, D, A, true, s));
+        ULM_TRY(launch_la_kgroup(sv.vR, sv.vRl, ws.doQ, ws.doQl, sv.qQ, nullptr, ws.Pdk, g, nkd > 1 ? ws.part : ws.dkf,
+                                 B, T, D, A, true, true, s));
         if (nkd > 1) ULM_TRY(launch_partial_reduce(ws.part, nkd, na, ws.dkf, ULM_F32, s));
-        // dv = LA_rev(k, q, dfast): keys = A, values = D; update q^T dfast~, intra on bf16(dfast)
+        // dv = LA_rev(k, q, dfast): keys = A, values = D; update q^T dfast~ (from the
+        // full-precision dfast), intra on bf16(dfast)
         const bool direct = nka == 1 && dv_dtype == ULM_F32;
-        ULM_TRY(launch_la_kgroup(sv.kR, nullptr, sv.qQ, nullptr, ws.doQh, ws.doQ, sv.Pdv, g,
-                                 direct ? static_cast<float *>(dv) : ws.part, B, T, A, D, true, s));
+        ULM_TRY(launch_la_kgroup(sv.kR, nullptr, sv.qQ, nullptr, ws.doQ, ws.doQl, sv.Pdv, g,
+                                 direct ? static_cast<float *>(dv) : ws.part, B, T, A, D, true, false, s));
         if (!direct) ULM_TRY(launch_partial_reduce(ws.part, nka, nd, dv, dv_dtype, s));
     } else {
         const uint16_t *do16 = static_cast<const uint16_t *>(dfast);

@@ -7,16 +7,33 @@
 // out per chunk (the reference stores it to HBM in bf16, kernel.py:38).
 //
 // Workgroup = (batch row b, key group of up to 24 blocks of 32 keys, 64 value
-// columns), 4 waves. Wave w holds the state of key blocks w, w+4, ... (up to
-// 6) of the group x 64 columns (192 fp32 registers per lane) and walks the
-// chunks; per chunk n (positions 64n .. 64n+63):
+// columns), 8 waves, two per SIMD. Wave w holds the state of key blocks w,
+// w+8, w+16 of the group x 64 columns (MH <= 3 blocks, 32 fp32 registers per
+// block and 32-column tile) and walks the chunks; per chunk n (positions
+// 64n .. 64n+63), with s the state scale after the previous update:
 //   read-out  O_w  = diag(s lam^(i+1)) a_n[:, keys_w] bf16(G_w)
-//   intra     O_w += P_n[:, 16w:16w+16] c_n[16w:16w+16, :]     (key group 0 only)
-//   exchange  O = sum_w O_w through LDS; wave w stores rows 16w .. 16w+15
+//   intra     O_w += P_n[rows_w, 16 iq_w : 16 iq_w + 16] c_n[16 iq_w : 16 iq_w + 16, :]
+//             (key group 0 only; wave w takes one of the 2 x 4 row-half x
+//             position-quarter blocks of the 64 x 64 product)
+//   exchange  O = sum_w O_w through LDS; wave w stores rows 8w .. 8w+7
 //   update    G_w += b_n[:, keys_w]^T (lam^(63-j) c_n[j] / s')
-// Every operand is one 16-byte global load per lane:
-//   a in its natural layout (B, T, K); b and c in the chunk-transposed layout
-//   (B, NT, K|V, 64) of chunk_transpose; P (B, NT, 64, 64) from chunk_scores.
+// The decayed update operand is made here, once per workgroup: wave w loads
+// tile w of the chunk's eight raw c tiles (two 32-column tiles x four
+// 16-position quarters), multiplies position j by lam^(63-j) / s' (s' the scale
+// after this update) and stages the bf16 result, with its rounding remainder
+// when UBSPLIT, and the raw tile for the intra product in LDS. Every wave then
+// reads the eight staged tiles from LDS instead of global memory.
+//
+// Operands are bf16 tiles of 32 rows x 16 contraction elements (ulm_common.h):
+// a in the R layout, b and c in the Q layout, P from chunk_scores. Every tile
+// load is one 16-byte buffer load per lane; offsets past a buffer's range read
+// as zero, which covers keys past the group and a missing second value tile.
+//
+// Pipelining: the read-out operand of chunk n+1 and the raw c tile of chunk
+// n+1 are loaded before the update of chunk n; the update operand b_n is
+// loaded right after the read-out of chunk n. Every load therefore has the
+// barrier, LDS exchange and MFMA work of a phase to arrive in.
+//
 // The rows of a 32-key state block are held in the order key(rho) = rho with
 // bits 2 and 3 exchanged. In that order the accumulator layout of
 // v_mfma_f32_32x32x16_bf16 (lane l, register r -> row 8(r/4) + 4(l/32) + r%4,
@@ -32,8 +49,13 @@
 //
 // State scaling: H = s G with a wave-uniform scalar s, so the per-chunk decay
 // lam^64 folds into s; G is rescaled (s = 1) only when s would fall below
-// 2^-40. SPLIT carries the decayed update operand as a bf16 hi + lo pair
-// (twice the update MFMAs), exact to fp32 accumulation for bf16 inputs.
+// 2^-40 (state_inv_scale gives the same schedule on the host side).
+//
+// Precision: UBSPLIT adds the bf16 rounding remainder of the decayed c as a
+// second update pass (exact to fp32 accumulation when b is bf16). FULL takes
+// the inputs that are not bf16 as hi + lo pairs where given: the read-out
+// operand (alo), the update operand (ualo, one more pass against the hi part
+// of c) and c itself (clo, summed before the decay).
 //
 // With more than one key group, group k writes its partial output to
 // out + k*B*T*V (fp32), summed afterwards by partial_reduce.
@@ -50,15 +72,25 @@ int la_timer_end(hipStream_t s);
 namespace kgrp {
 
 constexpr int C = ULM_CHUNK;
-constexpr int WAVES = 8;                    // two per SIMD
-constexpr int MAX_MH = 3;                   // key blocks per wave, at most
+constexpr int WAVES = 8;                       // two per SIMD
+constexpr int MAX_MH = 3;                      // key blocks per wave, at most
 constexpr int GROUP_BLOCKS = WAVES * MAX_MH;   // 24 blocks = 768 keys per workgroup
-constexpr int VT = 64;                      // value columns per workgroup
-constexpr int OPITCH = C + 4;               // floats per column of the exchange buffer
-constexpr int OBUF = WAVES * VT * OPITCH;   // floats of the exchange buffer
-constexpr int LDS_BYTES = OBUF * 4;
-constexpr int ROWS_PER_WAVE = C / WAVES;    // output rows each wave reduces and stores
-constexpr uint32_t OOB = 0x80000000u;       // buffer offset past every range: the load returns zeros
+constexpr int VT = 64;                         // value columns per workgroup
+constexpr int ROWS_PER_WAVE = C / WAVES;       // output rows each wave reduces and stores
+constexpr uint32_t TB = kTileElems * 2;        // bytes per operand tile
+constexpr uint32_t OOB = 0x80000000u;          // buffer offset past every range: the load returns zeros
+// LDS: the staged c tiles (decayed hi, decayed lo, raw: eight 1 KB tiles
+// each), then the exchange buffer, one 64-column x 64-row fp32 partial per
+// wave, column-major with a pitch of 68 floats (the 16-byte row quads of
+// consecutive columns land on distinct banks). Everything a wave addresses in
+// a phase is one lane-dependent base plus immediate offsets below 64 KB.
+constexpr uint32_t UB_HI = 0;                          // byte offsets
+constexpr uint32_t UB_LO = UB_HI + 8 * TB;
+constexpr uint32_t C_RAW = UB_LO + 8 * TB;
+constexpr uint32_t XBUF = C_RAW + 8 * TB;
+constexpr int OPITCH = C + 4;                          // floats per column of a partial
+constexpr int XPART = VT * OPITCH;                     // floats per partial
+constexpr uint32_t LDS_BYTES = XBUF + WAVES * XPART * 4;   // 163840, the whole LDS of a CU
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
@@ -79,22 +111,28 @@ __device__ __forceinline__ float uniform(float x) {
 __device__ __forceinline__ uint32_t uniform(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 // own LDS traffic done, then meet the other waves
 __device__ __forceinline__ void sync_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// keep the scheduler from moving instructions across this point
+__device__ __forceinline__ void phase() { __builtin_amdgcn_sched_barrier(0); }
 
-// MH: key blocks per wave (blocks past the group's end read as zero). SPLIT: the
-// update operand comes as bf16 hi + lo (UA, UAlo); ASPLIT: the read-out operand
-// as hi + lo (A_, Alo).
-template <int MH, bool REV, bool SPLIT, bool ASPLIT>
+__device__ __forceinline__ bf16x8 lds_tile(const char *lds, uint32_t off) {
+    return *reinterpret_cast<const bf16x8 *>(lds + off);
+}
+
+// MH: key blocks per wave (blocks past the group's end read as zero).
+template <int MH, bool REV, bool UBSPLIT, bool FULL>
 __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t *__restrict__ A_,
                                                                   const uint16_t *__restrict__ Alo,
                                                                   const uint16_t *__restrict__ UA,
                                                                   const uint16_t *__restrict__ UAlo,
-                                                                  const uint16_t *__restrict__ UB,
-                                                                  const uint16_t *__restrict__ CR,
+                                                                  const uint16_t *__restrict__ Cq,
+                                                                  const uint16_t *__restrict__ Clo,
                                                                   const uint16_t *__restrict__ P,
                                                                   const float *__restrict__ g, float *__restrict__ out,
                                                                   int Btot, int T, int K, int V, int NT, int nKG, int bpg,
                                                                   int nVT, int total) {
-    extern __shared__ __align__(16) float obuf[];   // [WAVES][VT][OPITCH]
+    extern __shared__ __align__(16) float lds_f[];   // staged c tiles, then the exchange partials
+    char *const lds = reinterpret_cast<char *>(lds_f);
+    float *const xbuf = reinterpret_cast<float *>(lds + XBUF);
 
     int tile = blockIdx.x;
     if (total % 8 == 0) tile = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;   // XCD-local tiles
@@ -112,6 +150,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
     const bool nt1 = v0 + 32 < V;   // the second 32-column tile lies inside V (the first always does)
     const bool intra = kgi == 0;
     const int iq = wave % 4, imt = wave / 4;   // intra-chunk share: position quarter iq of row half imt
+    const bool has_alo = FULL && Alo != nullptr;
+    const bool has_ualo = FULL && UAlo != nullptr;
+    const bool has_clo = FULL && Clo != nullptr;
 
     // ---- read-out row factors lam^(i+1) (lam^(64-i) reversed), i = 32 mt + 8 q + 4 lh + m
     const float gl = g[0];
@@ -124,31 +165,31 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
     float rrow[4];       // lane part
 #pragma unroll
     for (int m = 0; m < 4; ++m) rrow[m] = __expf(gl * static_cast<float>(REV ? 8 - 4 * lh - m : 1 + 4 * lh + m));
-    const float lam64 = state_lam64(gl);
+    const float lam64 = uniform(state_lam64(gl));
     const bool tiny = lam64 < kRenorm;
+    // state scale after the update of walk step st, from the one after step st-1
+    auto scale_after = [&](float s_prev, int st) {
+        const float s = (st > 0 && !tiny && s_prev < kRenorm) ? 1.f : s_prev;
+        return tiny ? 1.f : lam64 * s;
+    };
 
     // ---- operand buffers, one batch row each (tile layouts of ulm_common.h);
     // byte offset of a tile load = 16 lane + a uniform tile offset
     const int KT16 = K / 16, KT32 = K / 32, VT32 = V / 32;
     const size_t rowA = static_cast<size_t>(2 * NT) * KT16 * kTileElems;    // R layout
     const size_t rowU = static_cast<size_t>(NT) * KT32 * 4 * kTileElems;    // Q layout, keys
-    const size_t rowB = static_cast<size_t>(NT) * VT32 * 4 * kTileElems;    // Q layout, values
+    const size_t rowC = static_cast<size_t>(NT) * VT32 * 4 * kTileElems;    // Q layout, values
     const size_t rowP = static_cast<size_t>(NT) * 8 * kTileElems;           // score tiles
     const rsrc_t ra = rsrc(A_ + b * rowA, rowA * 2);
-    const rsrc_t ral = rsrc((ASPLIT ? Alo : A_) + b * rowA, rowA * 2);
+    const rsrc_t ral = rsrc((has_alo ? Alo : A_) + b * rowA, rowA * 2);
     const rsrc_t rua = rsrc(UA + b * rowU, rowU * 2);
-    const rsrc_t rul = rsrc((SPLIT ? UAlo : UA) + b * rowU, rowU * 2);
-    const rsrc_t rub = rsrc(UB + b * rowB, rowB * 2);
-    const rsrc_t rcr = rsrc(CR + b * rowB, rowB * 2);
+    const rsrc_t rul = rsrc((has_ualo ? UAlo : UA) + b * rowU, rowU * 2);
+    const rsrc_t rc = rsrc(Cq + b * rowC, rowC * 2);
+    const rsrc_t rcl = rsrc((has_clo ? Clo : Cq) + b * rowC, rowC * 2);
     const rsrc_t rp = rsrc(P + b * rowP, rowP * 2);
-    constexpr uint32_t TB = kTileElems * 2;   // bytes per tile
     const uint32_t lane16 = static_cast<uint32_t>(lane * 16);
-    uint32_t ub_lane[2], cr_lane[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        ub_lane[nt] = (nt == 0 || nt1) ? lane16 + nt * 4 * TB : OOB;
-        cr_lane[nt] = (nt == 0 || nt1) ? lane16 + nt * 4 * TB + iq * TB : OOB;
-    }
+    // this wave's raw c tile: 32-column tile wave / 4, position quarter wave % 4
+    const uint32_t c_lane = (wave < 4 || nt1) ? lane16 + wave * TB : OOB;
     const uint32_t p_lane = lane16 + (imt * 4 + iq) * TB;
     // uniform key-block offsets (bytes) into a rows and into the update operand; OOB past the group
     uint32_t a_blk[MH], u_blk[MH];
@@ -160,6 +201,46 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
     }
     float *out_k = out + static_cast<size_t>(kgi) * Btot * T * V;
 
+    auto chunk_of = [&](int st) { return REV ? NT - 1 - st : st; };
+    auto c_off = [&](int n) { return uniform(static_cast<uint32_t>(n * VT32 + v0 / 32) * 4 * TB); };
+    auto p_off = [&](int n) { return uniform(static_cast<uint32_t>(n * 8) * TB); };
+    auto a_off = [&](int n, int mh, int hb, int mt) {
+        return lane16 + uniform(static_cast<uint32_t>((2 * n + mt) * KT16) * TB) + a_blk[mh] + hb * TB;
+    };
+    auto load_a = [&](bf16x8 (&a)[MH][2][2], int n) {
+#pragma unroll
+        for (int mh = 0; mh < MH; ++mh)
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) a[mh][hb][mt] = bld(ra, a_off(n, mh, hb, mt));
+    };
+    // Stage this wave's c tile for walk step st: decayed by lam^(63-j) / s'
+    // (lam^j / s' reversed) as bf16 hi (+ lo), and raw for the intra product.
+    // Lane element e is chunk position j = 16 (wave % 4) + 8 lh + e; its decay
+    // is a lane part times a uniform part, both powers of lam at most 1:
+    //   forward  lam^(56 - 16 (wave%4) - 8 lh) * lam^(7-e)
+    //   reversed lam^(16 (wave%4) + 8 lh)      * lam^e
+    const float dlane = __expf(gl * static_cast<float>(REV ? 16 * (wave % 4) + 8 * lh : 56 - 16 * (wave % 4) - 8 * lh));
+    float duni[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) duni[e] = uniform(__expf(gl * static_cast<float>(REV ? e : 7 - e)));
+    auto stage_c = [&](bf16x8 raw, bf16x8 rlo, float s_new) {
+        const float dl = dlane * (1.f / s_new);
+        bf16x8 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float x = static_cast<float>(raw[e]);
+            if (has_clo) x += static_cast<float>(rlo[e]);
+            const float y = x * (dl * duni[e]);
+            hi[e] = static_cast<bf16>(y);
+            lo[e] = static_cast<bf16>(y - static_cast<float>(hi[e]));
+        }
+        *reinterpret_cast<bf16x8 *>(lds + UB_HI + wave * TB + lane16) = hi;
+        if (UBSPLIT) *reinterpret_cast<bf16x8 *>(lds + UB_LO + wave * TB + lane16) = lo;
+        if (intra) *reinterpret_cast<bf16x8 *>(lds + C_RAW + wave * TB + lane16) = raw;
+    };
+
     f32x16 G[MH][2];
 #pragma unroll
     for (int mh = 0; mh < MH; ++mh)
@@ -169,14 +250,25 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
             for (int r = 0; r < 16; ++r) G[mh][nt][r] = 0.f;
     float s_state = 1.f;
 
+    // ---- prologue: step 0's c staged (visible after the first barrier),
+    // step 1's read-out operand in registers
+    bf16x8 a_cur[MH][2][2];
+    {
+        const int n0 = chunk_of(0);
+        const bf16x8 raw = bld(rc, c_lane + c_off(n0));
+        const bf16x8 rlo = has_clo ? bld(rcl, c_lane + c_off(n0)) : bf16x8{};
+        if (NT > 1) load_a(a_cur, chunk_of(1));
+        stage_c(raw, rlo, scale_after(1.f, 0));
+    }
+
     for (int step = 0; step < NT; ++step) {
-        const int n = REV ? NT - 1 - step : step;
-        const uint32_t cb = uniform(static_cast<uint32_t>(n * VT32 + v0 / 32) * 4 * TB);   // this chunk's value tiles
+        const int n = chunk_of(step);
+        const bool readout = step > 0;
+        const bool update = step + 1 < NT;   // the last chunk's update is never read
 
         // ---- rescaling of G around the read-out (rarely): renormalisation
         // (G *= s, s = 1) before, when s fell below 2^-40, or, when lam^64 itself
         // is below that, the decay G *= lam^64 after.
-        const bool readout = step > 0;
         if (readout && !tiny && s_state < kRenorm) {
 #pragma unroll
             for (int mh = 0; mh < MH; ++mh)
@@ -187,35 +279,55 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
             s_state = 1.f;
         }
 
-        // ---- read-out of H = s G, one 32-row half at a time, plus this wave's
-        // share of the intra-chunk product; both halves go to the exchange buffer.
+        // ---- read-out of H = s G (both 32-row halves; G converted once per block)
         f32x16 O[2][2];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) O[mt][nt][r] = 0.f;
-            if (readout) {
+        if (readout) {
 #pragma unroll
-                for (int mh = 0; mh < MH; ++mh)
+            for (int mh = 0; mh < MH; ++mh)
 #pragma unroll
-                    for (int hb = 0; hb < 2; ++hb) {
-                        const uint32_t aoff = lane16 + uniform(static_cast<uint32_t>((2 * n + mt) * KT16) * TB) +
-                                              a_blk[mh] + hb * TB;
-                        const bf16x8 aop = bld(ra, aoff);
-                        const bf16x8 aol = ASPLIT ? bld(ral, aoff) : bf16x8{};
-                        bf16x8 gop[2];
+                for (int hb = 0; hb < 2; ++hb) {
+                    bf16x8 gop[2];
 #pragma unroll
-                        for (int nt = 0; nt < 2; ++nt)
+                    for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-                            for (int e = 0; e < 8; ++e) gop[nt][e] = static_cast<bf16>(G[mh][nt][8 * hb + e]);
+                        for (int e = 0; e < 8; ++e) gop[nt][e] = static_cast<bf16>(G[mh][nt][8 * hb + e]);
 #pragma unroll
-                        for (int nt = 0; nt < 2; ++nt) {
-                            O[mt][nt] = mfma(aop, gop[nt], O[mt][nt]);
-                            if (ASPLIT) O[mt][nt] = mfma(aol, gop[nt], O[mt][nt]);
+                    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+                        for (int nt = 0; nt < 2; ++nt) O[mt][nt] = mfma(a_cur[mh][hb][mt], gop[nt], O[mt][nt]);
+                        if (has_alo) {
+                            const bf16x8 aol = bld(ral, a_off(n, mh, hb, mt));
+#pragma unroll
+                            for (int nt = 0; nt < 2; ++nt) O[mt][nt] = mfma(aol, gop[nt], O[mt][nt]);
                         }
                     }
+                    phase();   // one converted block of G live at a time
+                }
+        }
+        phase();
+
+        // ---- this chunk's update operand b_n and intra matrix tile, in flight
+        // during the exchange (b_n loaded on the last step too: conditional
+        // loads would keep the registers they replace alive across the whole
+        // iteration)
+        const bf16x8 p_cur = intra ? bld(rp, p_lane + p_off(n)) : bf16x8{};
+        bf16x8 ua[MH][4];
+        const uint32_t urow = uniform(static_cast<uint32_t>(n * KT32) * 4 * TB);
+#pragma unroll
+        for (int mh = 0; mh < MH; ++mh)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) ua[mh][ks] = bld(rua, lane16 + urow + u_blk[mh] + ks * TB);
+        phase();
+
+        if (readout) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const float f = s_state * upart[mt][q];
@@ -226,31 +338,31 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
                         O[mt][1][4 * q + m] *= sc;
                     }
                 }
+            if (tiny) {
+#pragma unroll
+                for (int mh = 0; mh < MH; ++mh)
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) G[mh][nt][r] *= lam64;
             }
-        }
-        if (intra) {
-            const bf16x8 pq = bld(rp, p_lane + uniform(static_cast<uint32_t>(n * 8) * TB));
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const bf16x8 ci = bld(rcr, cr_lane[nt] + cb);
-                if (imt == 0) O[0][nt] = mfma(pq, ci, O[0][nt]);
-                else O[1][nt] = mfma(pq, ci, O[1][nt]);
-            }
-        }
-        if (readout && tiny) {
-#pragma unroll
-            for (int mh = 0; mh < MH; ++mh)
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) G[mh][nt][r] *= lam64;
         }
         s_state = tiny ? 1.f : lam64 * s_state;   // scale after this chunk's update
 
-        // every wave has finished reducing the previous chunk's partials
-        if (step > 0) sync_lds();
+        // every wave has finished reducing the previous chunk's partials, and
+        // this chunk's c tiles are staged
+        sync_lds();
+        if (intra) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const bf16x8 ci = lds_tile(lds, C_RAW + (nt * 4 + iq) * TB + lane16);
+                if (imt == 0) O[0][nt] = mfma(p_cur, ci, O[0][nt]);
+                else O[1][nt] = mfma(p_cur, ci, O[1][nt]);
+            }
+        }
         {
-            float *ob = obuf + wave * (VT * OPITCH);
+            // partial of wave w: column c, row i at floats w XPART + OPITCH c + i
+            float *ob = xbuf + wave * XPART + lr * OPITCH + 4 * lh;
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -260,31 +372,62 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
                         f32x4 x;
 #pragma unroll
                         for (int m = 0; m < 4; ++m) x[m] = O[mt][nt][4 * q + m];
-                        *reinterpret_cast<f32x4 *>(ob + (32 * nt + lr) * OPITCH + 32 * mt + 8 * q + 4 * lh) = x;
+                        *reinterpret_cast<f32x4 *>(ob + 32 * nt * OPITCH + 32 * mt + 8 * q) = x;
                     }
         }
+        phase();
 
-        // ---- state update G += UA^T UB (the decay and 1/s are inside the stored
-        // operand); the lo part of a split operand in a second pass
-        if (step + 1 < NT) {
-            bf16x8 ub[2][4];
+        // ---- next chunk's operands: c and P now, the read-out operand in two
+        // halves inside the update, each once the update operand registers it
+        // replaces are consumed
+        // (on the last step they re-read this chunk, unused)
+        bf16x8 a_nxt[MH][2][2];
+        bf16x8 rlo_n = {};
+        const int nn = update ? chunk_of(step + 1) : n;
+        const bf16x8 raw_n = bld(rc, c_lane + c_off(nn));
+        if (has_clo) rlo_n = bld(rcl, c_lane + c_off(nn));
+        phase();
+
+        // ---- state update G += b_n^T c~_n (+ the lo passes); skipped on the
+        // last step, whose update is never read
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
+        for (int ks = 0; ks < 4; ++ks) {
+            if (update) {
+                bf16x8 ubh[2], ubl[2];
 #pragma unroll
-                for (int ks = 0; ks < 4; ++ks) ub[nt][ks] = bld(rub, ub_lane[nt] + cb + ks * TB);
-            const uint32_t urow = uniform(static_cast<uint32_t>(n * KT32) * 4 * TB);
+                for (int nt = 0; nt < 2; ++nt) {
+                    ubh[nt] = lds_tile(lds, UB_HI + (nt * 4 + ks) * TB + lane16);
+                    if (UBSPLIT) ubl[nt] = lds_tile(lds, UB_LO + (nt * 4 + ks) * TB + lane16);
+                }
 #pragma unroll
-            for (int pass = 0; pass < (SPLIT ? 2 : 1); ++pass) {
-                const rsrc_t ru = pass ? rul : rua;
+                for (int mh = 0; mh < MH; ++mh)
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) {
+                        G[mh][nt] = mfma(ua[mh][ks], ubh[nt], G[mh][nt]);
+                        if (UBSPLIT) G[mh][nt] = mfma(ua[mh][ks], ubl[nt], G[mh][nt]);
+                    }
+            }
+            if (ks % 2 == 1) {
+                phase();
+                const int hb = ks / 2;
+#pragma unroll
+                for (int mh = 0; mh < MH; ++mh)
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt) a_nxt[mh][hb][mt] = bld(ra, a_off(nn, mh, hb, mt));
+                phase();
+            }
+        }
+        if (update && has_ualo) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                bf16x8 ubh[2];
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) ubh[nt] = lds_tile(lds, UB_HI + (nt * 4 + ks) * TB + lane16);
 #pragma unroll
                 for (int mh = 0; mh < MH; ++mh) {
-                    bf16x8 bop[4];
+                    const bf16x8 ul = bld(rul, lane16 + urow + u_blk[mh] + ks * TB);
 #pragma unroll
-                    for (int ks = 0; ks < 4; ++ks) bop[ks] = bld(ru, lane16 + urow + u_blk[mh] + ks * TB);
-#pragma unroll
-                    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-                        for (int nt = 0; nt < 2; ++nt) G[mh][nt] = mfma(bop[ks], ub[nt][ks], G[mh][nt]);
+                    for (int nt = 0; nt < 2; ++nt) G[mh][nt] = mfma(ul, ubh[nt], G[mh][nt]);
                 }
             }
         }
@@ -292,31 +435,40 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
         // ---- exchange: wave w sums rows 8w .. 8w+7 of the eight partials, lane = column
         sync_lds();
         {
-            const float *rb = obuf + lane * OPITCH + ROWS_PER_WAVE * wave;
+            const float *rb = xbuf + lane * OPITCH + ROWS_PER_WAVE * wave;
             f32x4 acc[2];
 #pragma unroll
-            for (int q4 = 0; q4 < 2; ++q4) acc[q4] = *reinterpret_cast<const f32x4 *>(rb + 4 * q4);
+            for (int k = 0; k < 2; ++k) acc[k] = *reinterpret_cast<const f32x4 *>(rb + 4 * k);
 #pragma unroll
             for (int w2 = 1; w2 < WAVES; ++w2)
 #pragma unroll
-                for (int q4 = 0; q4 < 2; ++q4) acc[q4] += *reinterpret_cast<const f32x4 *>(rb + w2 * (VT * OPITCH) + 4 * q4);
+                for (int k = 0; k < 2; ++k) acc[k] += *reinterpret_cast<const f32x4 *>(rb + w2 * XPART + 4 * k);
             // value tiles hold their 32 columns in the order perm32
             const int col = v0 + 32 * (lane / 32) + perm32(lane % 32);
             if (col < V) {
                 float *dst = out_k + (static_cast<size_t>(b) * T + n * C + ROWS_PER_WAVE * wave) * V + col;
 #pragma unroll
-                for (int q4 = 0; q4 < 2; ++q4)
+                for (int k = 0; k < 2; ++k)
 #pragma unroll
                     for (int m = 0; m < 4; ++m)
-                        if (n * C + ROWS_PER_WAVE * wave + 4 * q4 + m < T) dst[static_cast<size_t>(4 * q4 + m) * V] = acc[q4][m];
+                        if (n * C + ROWS_PER_WAVE * wave + 4 * k + m < T) dst[static_cast<size_t>(4 * k + m) * V] = acc[k][m];
             }
         }
+
+        // ---- stage the next chunk's c (every wave is past this chunk's update)
+        if (update) stage_c(raw_n, rlo_n, scale_after(s_state, step + 1));
+#pragma unroll
+        for (int mh = 0; mh < MH; ++mh)
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) a_cur[mh][hb][mt] = a_nxt[mh][hb][mt];
     }
 }
 
-template <int MH, bool REV, bool SPLIT, bool ASPLIT>
-int launch(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo, const uint16_t *ub,
-           const uint16_t *cr, const uint16_t *P, const float *g, float *out, int B, int T, int K, int V, int nKG,
+template <int MH, bool REV, bool UBSPLIT, bool FULL>
+int launch(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo, const uint16_t *c,
+           const uint16_t *clo, const uint16_t *P, const float *g, float *out, int B, int T, int K, int V, int nKG,
            int bpg, hipStream_t s) {
     const int NT = (T + C - 1) / C;
     const int nVT = (V + VT - 1) / VT;
@@ -325,34 +477,35 @@ int launch(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uin
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return check_launch("hipGetDevice");
     if (!attr_done[dev]) {
-        const void *fn = reinterpret_cast<const void *>(&la_kgroup_kernel<MH, REV, SPLIT, ASPLIT>);
+        const void *fn = reinterpret_cast<const void *>(&la_kgroup_kernel<MH, REV, UBSPLIT, FULL>);
         if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES) != hipSuccess)
             return check_launch("la_kgroup_kernel attribute");
         attr_done[dev] = true;
     }
     int st = la_timer_begin(s);
     if (st) return st;
-    la_kgroup_kernel<MH, REV, SPLIT, ASPLIT><<<dim3(static_cast<unsigned>(total)), WAVES * kWave, LDS_BYTES, s>>>(
-        a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, NT, nKG, bpg, nVT, static_cast<int>(total));
+    la_kgroup_kernel<MH, REV, UBSPLIT, FULL><<<dim3(static_cast<unsigned>(total)), WAVES * kWave, LDS_BYTES, s>>>(
+        a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, NT, nKG, bpg, nVT, static_cast<int>(total));
     st = check_launch("la_kgroup_kernel");
     if (st) return st;
     return la_timer_end(s);
 }
 
 template <int MH>
-int launch_mh(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo, const uint16_t *ub,
-              const uint16_t *cr, const uint16_t *P, const float *g, float *out, int B, int T, int K, int V, int nKG,
-              int bpg, bool reverse, hipStream_t s) {
-    const int sel = (reverse ? 4 : 0) + (ualo ? 2 : 0) + (alo ? 1 : 0);
+int launch_mh(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo, const uint16_t *c,
+              const uint16_t *clo, const uint16_t *P, const float *g, float *out, int B, int T, int K, int V, int nKG,
+              int bpg, bool reverse, bool ubsplit, hipStream_t s) {
+    const bool full = alo || ualo || clo;
+    const int sel = (reverse ? 4 : 0) + (ubsplit ? 2 : 0) + (full ? 1 : 0);
     switch (sel) {
-    case 0: return launch<MH, false, false, false>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
-    case 1: return launch<MH, false, false, true>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
-    case 2: return launch<MH, false, true, false>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
-    case 3: return launch<MH, false, true, true>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
-    case 4: return launch<MH, true, false, false>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
-    case 5: return launch<MH, true, false, true>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
-    case 6: return launch<MH, true, true, false>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
-    default: return launch<MH, true, true, true>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, s);
+    case 0: return launch<MH, false, false, false>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
+    case 1: return launch<MH, false, false, true>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
+    case 2: return launch<MH, false, true, false>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
+    case 3: return launch<MH, false, true, true>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
+    case 4: return launch<MH, true, false, false>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
+    case 5: return launch<MH, true, false, true>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
+    case 6: return launch<MH, true, true, false>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
+    default: return launch<MH, true, true, true>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
     }
 }
 
@@ -376,14 +529,15 @@ bool la_kgroup_supported(int B, int T, int K, int V) {
 }
 
 // Operands (bf16 tiles, ulm_common.h): a (+ alo) in the R layout; ua (+ ualo)
-// and ub, cr in the Q layout. The update adds ua^T ub (+ ualo^T ub); one of ua
-// / ub carries the decay and 1/s of the state scale schedule (chunk_transpose).
-// The read-out contracts a (+ alo) with the state. cr is the raw c of the
-// intra-chunk product; P is P_lo (forward) or P_up (reverse) of chunk_scores.
+// and c (+ clo) in the Q layout. The read-out contracts a with the state; the
+// update adds ua^T c~, where c~ is c decayed and scaled in the kernel (+ the
+// rounding remainder of c~ when ubsplit, + ualo^T c~). c is also the value
+// operand of the intra-chunk product with P (P_lo forward or P_up reversed, of
+// chunk_scores). alo, ualo, clo may each be null.
 // out: la_kgroup_groups(K) x (B, T, V) fp32, fully written (no accumulation).
 int launch_la_kgroup(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo,
-                     const uint16_t *ub, const uint16_t *cr, const uint16_t *P, const float *g, float *out, int B,
-                     int T, int K, int V, bool reverse, hipStream_t s) {
+                     const uint16_t *c, const uint16_t *clo, const uint16_t *P, const float *g, float *out, int B,
+                     int T, int K, int V, bool reverse, bool ubsplit, hipStream_t s) {
     if (!la_kgroup_supported(B, T, K, V))
         return fail(ULM_ERR_UNSUPPORTED, "K-group kernel: B=%d T=%d K=%d V=%d unsupported", B, T, K, V);
     const int nKG = la_kgroup_groups(K);
@@ -391,9 +545,12 @@ int launch_la_kgroup(const uint16_t *a, const uint16_t *alo, const uint16_t *ua,
     const int bpg = (nb + nKG - 1) / nKG;   // <= 24 blocks, so at most 3 per wave
     const int mh = (bpg + kgrp::WAVES - 1) / kgrp::WAVES;
     switch (mh) {
-    case 1: return kgrp::launch_mh<1>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, reverse, s);
-    case 2: return kgrp::launch_mh<2>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, reverse, s);
-    default: return kgrp::launch_mh<3>(a, alo, ua, ualo, ub, cr, P, g, out, B, T, K, V, nKG, bpg, reverse, s);
+    case 1:
+        return kgrp::launch_mh<1>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
+    case 2:
+        return kgrp::launch_mh<2>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
+    default:
+        return kgrp::launch_mh<3>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
     }
 }
 

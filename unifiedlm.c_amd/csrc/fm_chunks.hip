@@ -4,13 +4,19 @@
 //    kernel loads (R and Q layouts of ulm_common.h; positions past T are zero),
 //    each optionally with its bf16 rounding remainder.
 //  * chunk_scores: per chunk n, with S[i][j] = a_{64n+i} . b_{64n+j},
-//      P_lo[i][j] = S[i][j] lam^(i-j)  (j <= i, else 0)   forward walk
-//      P_up[i][j] = S[j][i] lam^(j-i)  (j >= i, else 0)   = P_lo^T
+//      P_lo[i][j] = S[i][j] lam^(i-j) / f_lo(i)  (j <= i, else 0)   forward walk
+//      P_up[i][j] = S[j][i] lam^(j-i) / f_up(i)  (j >= i, else 0)   reversed walk
 //    as bf16. P_lo is the intra-chunk matrix of o = LA(a, b, .) and P_up that
 //    of the reversed product with a and b exchanged (LA_rev(b, a, .)), so one
 //    pass serves fwd + dv (a = q, b = k) and dq + dk (a = dfast, b = v). This
 //    is the _la_attn_kernel product (kernel.py:51-72), computed once per chunk
-//    and shared by every value tile.
+//    and shared by every value tile. With `scaled`, f is the chunked kernel's
+//    read-out row factor, s lam^(i+1) forward and s lam^(64-i) reversed with s
+//    the state scale at that walk step (readout_scale), and the chunked kernel
+//    multiplies its summed row i by f once; that keeps every factor below 2^80
+//    unless lam^64 < 2^-40, where f = 1. Without `scaled`, f = 1 and P_up is
+//    exactly P_lo^T in bf16: the products behind the d/dg identity (dq, dk)
+//    need their intra-chunk terms rounded identically on both sides.
 //  * partial_reduce: out = sum over nK fp32 partial outputs, in out's dtype.
 #include "ulm_common.h"
 
@@ -145,7 +151,8 @@ __global__ __launch_bounds__(kScoreWaves * 64) void scores_kernel(const uint16_t
                                                                   const uint16_t *__restrict__ bL,
                                                                   const float *__restrict__ g,
                                                                   uint16_t *__restrict__ Plo,
-                                                                  uint16_t *__restrict__ Pup, int K, int NT) {
+                                                                  uint16_t *__restrict__ Pup, int K, int NT,
+                                                                  int scaled) {
     __shared__ __align__(16) uint16_t slo[C][C + 8], sup[C][C + 8];   // [i][j]
     __shared__ float red[3][3][16][kWave];                             // partials of quarters 1..3
     const int n = blockIdx.x, b = blockIdx.y;
@@ -202,16 +209,25 @@ __global__ __launch_bounds__(kScoreWaves * 64) void scores_kernel(const uint16_t
     __syncthreads();
     if (kq == 0) {
         const float gl = g[0];
+        const float lam64 = state_lam64(gl);
+        const bool tiny = !scaled || lam64 < kRenorm;
+        // unless tiny, the read-out row factors s lam^(i+1) (forward) and
+        // s lam^(64-i) (reversed) are divided out here and applied after the
+        // chunked kernel's cross-wave sum
+        const float inv_f = tiny ? 1.f : 1.f / readout_scale(lam64, n);
+        const float inv_r = tiny ? 1.f : 1.f / readout_scale(lam64, NT - 1 - n);
         const int j = 32 * nt + lr;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int i = 32 * mt + 8 * (r / 4) + 4 * lh + (r % 4);
             const float sv = (acc[0][r] + acc[1][r]) + red[tile][0][r][lane] + red[tile][1][r][lane] +
                              red[tile][2][r][lane];
-            const int lag = i - j;
-            const uint16_t v = f32_to_bf16_bits(lag >= 0 ? sv * __expf(gl * static_cast<float>(lag)) : 0.f);
-            slo[i][j] = v;   // P_lo[i][j]
-            sup[j][i] = v;   // P_up[j][i] = P_lo[i][j]
+            const bool on = i >= j;
+            // P_lo[i][j] = lam^(i-j) S / (s lam^(i+1));  P_up[j][i] = lam^(i-j) S / (s lam^(64-j))
+            const float elo = tiny ? static_cast<float>(i - j) : -static_cast<float>(j + 1);
+            const float eup = tiny ? static_cast<float>(i - j) : static_cast<float>(i - C);
+            slo[i][j] = f32_to_bf16_bits(on ? sv * (__expf(gl * elo) * inv_f) : 0.f);
+            sup[j][i] = f32_to_bf16_bits(on ? sv * (__expf(gl * eup) * inv_r) : 0.f);
         }
     }
     __syncthreads();
@@ -277,15 +293,15 @@ int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t 
 // a, b in the R layout (K % 16 == 0), with optional bf16 remainders aL, bL;
 // P_lo, P_up in the tile layout of p_index.
 int launch_chunk_scores(const uint16_t *aR, const uint16_t *aL, const uint16_t *bR, const uint16_t *bL, const float *g,
-                        uint16_t *Plo, uint16_t *Pup, int B, int T, int K, hipStream_t s) {
+                        uint16_t *Plo, uint16_t *Pup, int B, int T, int K, bool scaled, hipStream_t s) {
     if (K % 16) return fail(ULM_ERR_UNSUPPORTED, "chunk scores: K=%d is not a multiple of 16", K);
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
     const dim3 grid(NT, B);
     const int nthreads = chunks::kScoreWaves * kWave;
-    if (aL && bL) chunks::scores_kernel<true, true><<<grid, nthreads, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
-    else if (aL) chunks::scores_kernel<true, false><<<grid, nthreads, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
-    else if (bL) chunks::scores_kernel<false, true><<<grid, nthreads, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
-    else chunks::scores_kernel<false, false><<<grid, nthreads, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT);
+    if (aL && bL) chunks::scores_kernel<true, true><<<grid, nthreads, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT, scaled ? 1 : 0);
+    else if (aL) chunks::scores_kernel<true, false><<<grid, nthreads, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT, scaled ? 1 : 0);
+    else if (bL) chunks::scores_kernel<false, true><<<grid, nthreads, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT, scaled ? 1 : 0);
+    else chunks::scores_kernel<false, false><<<grid, nthreads, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT, scaled ? 1 : 0);
     return check_launch("chunk scores_kernel");
 }
 

@@ -34,13 +34,13 @@ int launch_la_generic(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
 int la_kgroup_groups(int K);
 bool la_kgroup_supported(int B, int T, int K, int V);
 int launch_la_kgroup(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo,
-                     const uint16_t *c, const uint16_t *clo, const uint16_t *P, const float *g, float *out, int B,
-                     int T, int K, int V, bool reverse, bool ubsplit, hipStream_t s);
+                     const uint16_t *c, const uint16_t *clo, const uint16_t *P, bool pscaled, const float *g,
+                     float *out, int B, int T, int K, int V, bool reverse, bool ubsplit, hipStream_t s);
 // fm_chunks.hip
 int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t *raw_lo, uint16_t *xr,
                            uint16_t *xr_lo, int B, int T, int X, hipStream_t s);
 int launch_chunk_scores(const uint16_t *aR, const uint16_t *aL, const uint16_t *bR, const uint16_t *bL, const float *g,
-                        uint16_t *Plo, uint16_t *Pup, int B, int T, int K, hipStream_t s);
+                        uint16_t *Plo, uint16_t *Pup, int B, int T, int K, bool scaled, hipStream_t s);
 int launch_partial_reduce(const float *part, int nK, size_t n, void *out, int odt, hipStream_t s);
 // fm_stats.hip
 int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
@@ -217,8 +217,10 @@ extern "C" int ulm_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
     ULM_TRY(launch_chunk_transpose(a, ULM_BF16, nullptr, nullptr, aR, nullptr, B, T, K, s));
     ULM_TRY(launch_chunk_transpose(b, ULM_BF16, bQ, nullptr, bR, nullptr, B, T, K, s));
     ULM_TRY(launch_chunk_transpose(c, ULM_BF16, cQ, nullptr, nullptr, nullptr, B, T, V, s));
-    ULM_TRY(launch_chunk_scores(reverse ? bR : aR, nullptr, reverse ? aR : bR, nullptr, g, Plo, Pup, B, T, K, s));
-    ULM_TRY(launch_la_kgroup(aR, nullptr, bQ, nullptr, cQ, nullptr, reverse ? Pup : Plo, g, part, B, T, K, V,
+    // split products keep P_up = P_lo^T exactly, as dq and dk do
+    ULM_TRY(launch_chunk_scores(reverse ? bR : aR, nullptr, reverse ? aR : bR, nullptr, g, Plo, Pup, B, T, K, !split,
+                                s));
+    ULM_TRY(launch_la_kgroup(aR, nullptr, bQ, nullptr, cQ, nullptr, reverse ? Pup : Plo, !split, g, part, B, T, K, V,
                              reverse != 0, split != 0, s));
     if (nkg > 1) ULM_TRY(launch_partial_reduce(part, nkg, static_cast<size_t>(B) * T * V, out, ULM_F32, s));
     return ULM_OK;
@@ -257,11 +259,11 @@ extern "C" int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const floa
         float *acc = ws.part ? ws.part : static_cast<float *>(fast);
         ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, sv.qR, sv.kR, sv.qQ, sv.kQ, sv.nck, B, T, A, s));
         ULM_TRY(launch_chunk_transpose(v, v_dtype, sv.vQ, sv.vQl, sv.vR, sv.vRl, B, T, D, s));
-        ULM_TRY(launch_chunk_scores(sv.qR, nullptr, sv.kR, nullptr, g, ws.Pf, sv.Pdv, B, T, A, s));
+        ULM_TRY(launch_chunk_scores(sv.qR, nullptr, sv.kR, nullptr, g, ws.Pf, sv.Pdv, B, T, A, true, s));
         // fast = LA(q, k, v): update k^T v~ (v~ from the full-precision v), intra on
         // bf16(v), as the reference's bf16 v (kernel.py:205)
-        ULM_TRY(launch_la_kgroup(sv.qR, nullptr, sv.kQ, nullptr, sv.vQ, sv.vQl, ws.Pf, g, acc, B, T, A, D, false, false,
-                                 s));
+        ULM_TRY(launch_la_kgroup(sv.qR, nullptr, sv.kQ, nullptr, sv.vQ, sv.vQl, ws.Pf, true, g, acc, B, T, A, D, false,
+                                 false, s));
         if (ws.part) ULM_TRY(launch_partial_reduce(ws.part, nkg, nf, fast, fast_dtype, s));
         return ULM_OK;
     }
@@ -299,22 +301,24 @@ extern "C" int ulm_fm_bwd(const float *r, const float *g, const float *w, const 
     if (fm_aligned(B, T, A, D)) {
         const int nkd = la_kgroup_groups(D), nka = la_kgroup_groups(A);
         ULM_TRY(launch_chunk_transpose(dfast, dfast_dtype, ws.doQ, ws.doQl, ws.doR, ws.doRl, B, T, D, s));
-        ULM_TRY(launch_chunk_scores(ws.doR, ws.doRl, sv.vR, sv.vRl, g, ws.Pdq, ws.Pdk, B, T, D, s));
+        // unscaled: P_dk = P_dq^T exactly, so the intra-chunk terms of dq and dk
+        // cancel in the d/dg identity
+        ULM_TRY(launch_chunk_scores(ws.doR, ws.doRl, sv.vR, sv.vRl, g, ws.Pdq, ws.Pdk, B, T, D, false, s));
         // dq_f = LA(dfast, v, k): keys = D, values = A; update v^T k~.
         // dk_f = LA_rev(v, dfast, q): update dfast^T q~.
         // Both feed the positional d/dg identity, whose cancellation amplifies
         // rounding, so the decayed k~ / q~ take their bf16 remainder as a second
         // pass (and v, dfast their hi + lo pairs when they arrived in more than bf16).
-        ULM_TRY(launch_la_kgroup(ws.doR, ws.doRl, sv.vQ, sv.vQl, sv.kQ, nullptr, ws.Pdq, g, nkd > 1 ? ws.part : ws.dqf,
-                                 B, T, D, A, false, true, s));
+        ULM_TRY(launch_la_kgroup(ws.doR, ws.doRl, sv.vQ, sv.vQl, sv.kQ, nullptr, ws.Pdq, false, g,
+                                 nkd > 1 ? ws.part : ws.dqf, B, T, D, A, false, true, s));
         if (nkd > 1) ULM_TRY(launch_partial_reduce(ws.part, nkd, na, ws.dqf, ULM_F32, s));
-        ULM_TRY(launch_la_kgroup(sv.vR, sv.vRl, ws.doQ, ws.doQl, sv.qQ, nullptr, ws.Pdk, g, nkd > 1 ? ws.part : ws.dkf,
-                                 B, T, D, A, true, true, s));
+        ULM_TRY(launch_la_kgroup(sv.vR, sv.vRl, ws.doQ, ws.doQl, sv.qQ, nullptr, ws.Pdk, false, g,
+                                 nkd > 1 ? ws.part : ws.dkf, B, T, D, A, true, true, s));
         if (nkd > 1) ULM_TRY(launch_partial_reduce(ws.part, nkd, na, ws.dkf, ULM_F32, s));
         // dv = LA_rev(k, q, dfast): keys = A, values = D; update q^T dfast~ (from the
         // full-precision dfast), intra on bf16(dfast)
         const bool direct = nka == 1 && dv_dtype == ULM_F32;
-        ULM_TRY(launch_la_kgroup(sv.kR, nullptr, sv.qQ, nullptr, ws.doQ, ws.doQl, sv.Pdv, g,
+        ULM_TRY(launch_la_kgroup(sv.kR, nullptr, sv.qQ, nullptr, ws.doQ, ws.doQl, sv.Pdv, true, g,
                                  direct ? static_cast<float *>(dv) : ws.part, B, T, A, D, true, false, s));
         if (!direct) ULM_TRY(launch_partial_reduce(ws.part, nka, nd, dv, dv_dtype, s));
     } else {

@@ -11,11 +11,16 @@
 // w+8, w+16 of the group x 64 columns (MH <= 3 blocks, 32 fp32 registers per
 // block and 32-column tile) and walks the chunks; per chunk n (positions
 // 64n .. 64n+63), with s the state scale after the previous update:
-//   read-out  O_w  = diag(s lam^(i+1)) a_n[:, keys_w] bf16(G_w)
+//   read-out  O_w  = a_n[:, keys_w] bf16(G_w)
 //   intra     O_w += P_n[rows_w, 16 iq_w : 16 iq_w + 16] c_n[16 iq_w : 16 iq_w + 16, :]
 //             (key group 0 only; wave w takes one of the 2 x 4 row-half x
 //             position-quarter blocks of the 64 x 64 product)
-//   exchange  O = sum_w O_w through LDS; wave w stores rows 8w .. 8w+7
+//   exchange  O = diag(s lam^(i+1)) sum_w O_w through LDS; wave w stores rows
+//             8w .. 8w+7
+// The row factor s lam^(i+1) of the read-out is applied once, after the sum,
+// when chunk_scores has divided it out of P (pscaled). Otherwise, and whenever
+// lam^64 < 2^-40, the kernel scales the read-out rows of every partial instead
+// and P carries no factor.
 //   update    G_w += b_n[:, keys_w]^T (lam^(63-j) c_n[j] / s')
 // The decayed update operand is made here, once per workgroup: wave w loads
 // tile w of the chunk's eight raw c tiles (two 32-column tiles x four
@@ -126,7 +131,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
                                                                   const uint16_t *__restrict__ UAlo,
                                                                   const uint16_t *__restrict__ Cq,
                                                                   const uint16_t *__restrict__ Clo,
-                                                                  const uint16_t *__restrict__ P,
+                                                                  const uint16_t *__restrict__ P, int pscaled,
                                                                   const float *__restrict__ g, float *__restrict__ out,
                                                                   int Btot, int T, int K, int V, int NT, int nKG, int bpg,
                                                                   int nVT, int total) {
@@ -154,19 +159,14 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
     const bool has_ualo = FULL && UAlo != nullptr;
     const bool has_clo = FULL && Clo != nullptr;
 
-    // ---- read-out row factors lam^(i+1) (lam^(64-i) reversed), i = 32 mt + 8 q + 4 lh + m
     const float gl = g[0];
-    float upart[2][4];   // uniform part
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            upart[mt][q] = uniform(__expf(gl * static_cast<float>(REV ? 32 * (1 - mt) + 8 * (3 - q) : 32 * mt + 8 * q)));
-    float rrow[4];       // lane part
-#pragma unroll
-    for (int m = 0; m < 4; ++m) rrow[m] = __expf(gl * static_cast<float>(REV ? 8 - 4 * lh - m : 1 + 4 * lh + m));
     const float lam64 = uniform(state_lam64(gl));
     const bool tiny = lam64 < kRenorm;
+    const bool rows_here = tiny || !pscaled;   // read-out rows scaled per partial
+    // row factor lam^(i+1) (lam^(64-i) reversed) of exchange row i = 8 wave
+    // (uniform), and the ratio between consecutive rows
+    const float xrow0 = uniform(__expf(gl * static_cast<float>(REV ? C - ROWS_PER_WAVE * wave : ROWS_PER_WAVE * wave + 1)));
+    const float xstep = uniform(__expf(REV ? -gl : gl));
     // state scale after the update of walk step st, from the one after step st-1
     auto scale_after = [&](float s_prev, int st) {
         const float s = (st > 0 && !tiny && s_prev < kRenorm) ? 1.f : s_prev;
@@ -190,7 +190,12 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
     const uint32_t lane16 = static_cast<uint32_t>(lane * 16);
     // this wave's raw c tile: 32-column tile wave / 4, position quarter wave % 4
     const uint32_t c_lane = (wave < 4 || nt1) ? lane16 + wave * TB : OOB;
-    const uint32_t p_lane = lane16 + (imt * 4 + iq) * TB;
+    // the intra matrix tiles of both row halves: this wave's own (imt) half, the
+    // other out of range (zeros), so the product needs no branch; every tile
+    // out of range outside key group 0
+    uint32_t p_lane[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) p_lane[mt] = (intra && mt == imt) ? lane16 + (mt * 4 + iq) * TB : OOB;
     // uniform key-block offsets (bytes) into a rows and into the update operand; OOB past the group
     uint32_t a_blk[MH], u_blk[MH];
 #pragma unroll
@@ -238,7 +243,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
         }
         *reinterpret_cast<bf16x8 *>(lds + UB_HI + wave * TB + lane16) = hi;
         if (UBSPLIT) *reinterpret_cast<bf16x8 *>(lds + UB_LO + wave * TB + lane16) = lo;
-        if (intra) *reinterpret_cast<bf16x8 *>(lds + C_RAW + wave * TB + lane16) = raw;
+        *reinterpret_cast<bf16x8 *>(lds + C_RAW + wave * TB + lane16) = raw;
     };
 
     f32x16 G[MH][2];
@@ -261,6 +266,42 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
         stage_c(raw, rlo, scale_after(1.f, 0));
     }
 
+    // Exchange of chunk nx: wave w sums rows 8w .. 8w+7 of the eight partials
+    // (lane = column), applies the read-out row factor when P carries none of
+    // it, and stores. It runs in the shadow of the next chunk's read-out MFMAs.
+    auto exchange = [&](int nx, float s_rd) {
+        const float *rb = xbuf + lane * OPITCH + ROWS_PER_WAVE * wave;
+        f32x4 acc[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) acc[k] = *reinterpret_cast<const f32x4 *>(rb + 4 * k);
+#pragma unroll
+        for (int w2 = 1; w2 < WAVES; ++w2)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) acc[k] += *reinterpret_cast<const f32x4 *>(rb + w2 * XPART + 4 * k);
+        if (!rows_here) {
+            float f = s_rd * xrow0;
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    acc[k][m] *= f;
+                    f *= xstep;
+                }
+        }
+        // value tiles hold their 32 columns in the order perm32
+        const int col = v0 + 32 * (lane / 32) + perm32(lane % 32);
+        if (col < V) {
+            float *dst = out_k + (static_cast<size_t>(b) * T + nx * C + ROWS_PER_WAVE * wave) * V + col;
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                    if (nx * C + ROWS_PER_WAVE * wave + 4 * k + m < T) dst[static_cast<size_t>(4 * k + m) * V] = acc[k][m];
+        }
+    };
+    float s_read_prev = 1.f;   // read-out scale of the previous step
+    bf16x8 raw_c = {}, rlo_c = {};   // the next step's raw c tile, staged at the top of that step
+
     for (int step = 0; step < NT; ++step) {
         const int n = chunk_of(step);
         const bool readout = step > 0;
@@ -278,6 +319,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
                     for (int r = 0; r < 16; ++r) G[mh][nt][r] *= s_state;
             s_state = 1.f;
         }
+
+        // ---- stage this chunk's c (every wave is past the previous update)
+        if (step > 0) stage_c(raw_c, rlo_c, scale_after(s_state, step));
 
         // ---- read-out of H = s G (both 32-row halves; G converted once per block)
         f32x16 O[2][2];
@@ -311,12 +355,16 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
                 }
         }
         phase();
+        if (step > 0) exchange(chunk_of(step - 1), s_read_prev);
+        phase();
 
         // ---- this chunk's update operand b_n and intra matrix tile, in flight
         // during the exchange (b_n loaded on the last step too: conditional
         // loads would keep the registers they replace alive across the whole
         // iteration)
-        const bf16x8 p_cur = intra ? bld(rp, p_lane + p_off(n)) : bf16x8{};
+        bf16x8 p_cur[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) p_cur[mt] = bld(rp, p_lane[mt] + p_off(n));
         bf16x8 ua[MH][4];
         const uint32_t urow = uniform(static_cast<uint32_t>(n * KT32) * 4 * TB);
 #pragma unroll
@@ -325,40 +373,47 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
             for (int ks = 0; ks < 4; ++ks) ua[mh][ks] = bld(rua, lane16 + urow + u_blk[mh] + ks * TB);
         phase();
 
-        if (readout) {
+        const float s_read = s_state;   // the state scale of this read-out
+        if (readout && rows_here) {
+            // the read-out rows take s lam^(i+1) (s lam^(64-i) reversed) here.
+            // Row i of the lane is 32 mt + 8 q + 4 lh + m; the factors run by
+            // repeated multiplication from the row with the largest one, so
+            // none overflows, and the loop keeps a single factor register.
+            float glv = gl;
+            asm volatile("" : "+v"(glv));   // recomputed per chunk, not held across the loop
+            const float lam = __expf(glv), lam4 = __expf(4.f * glv);
+            float f = s_read * __expf(glv * static_cast<float>(REV ? 5 - 4 * lh : 1 + 4 * lh));
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
+            for (int u = 0; u < 8; ++u) {
+                const int mt = REV ? 1 - u / 4 : u / 4, q = REV ? 3 - u % 4 : u % 4;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float f = s_state * upart[mt][q];
-#pragma unroll
-                    for (int m = 0; m < 4; ++m) {
-                        const float sc = f * rrow[m];
-                        O[mt][0][4 * q + m] *= sc;
-                        O[mt][1][4 * q + m] *= sc;
-                    }
+                for (int v = 0; v < 4; ++v) {
+                    const int m = REV ? 3 - v : v;
+                    O[mt][0][4 * q + m] *= f;
+                    O[mt][1][4 * q + m] *= f;
+                    f *= lam;
                 }
-            if (tiny) {
-#pragma unroll
-                for (int mh = 0; mh < MH; ++mh)
-#pragma unroll
-                    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) G[mh][nt][r] *= lam64;
+                f *= lam4;
             }
+        }
+        if (readout && tiny) {   // lam^64 < 2^-40 (s = 1): G decays by lam^64 after the read-out
+#pragma unroll
+            for (int mh = 0; mh < MH; ++mh)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) G[mh][nt][r] *= lam64;
         }
         s_state = tiny ? 1.f : lam64 * s_state;   // scale after this chunk's update
 
         // every wave has finished reducing the previous chunk's partials, and
         // this chunk's c tiles are staged
         sync_lds();
-        if (intra) {
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const bf16x8 ci = lds_tile(lds, C_RAW + (nt * 4 + iq) * TB + lane16);
-                if (imt == 0) O[0][nt] = mfma(p_cur, ci, O[0][nt]);
-                else O[1][nt] = mfma(p_cur, ci, O[1][nt]);
-            }
+        for (int nt = 0; nt < 2; ++nt) {
+            const bf16x8 ci = lds_tile(lds, C_RAW + (nt * 4 + iq) * TB + lane16);
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) O[mt][nt] = mfma(p_cur[mt], ci, O[mt][nt]);
         }
         {
             // partial of wave w: column c, row i at floats w XPART + OPITCH c + i
@@ -382,10 +437,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
         // replaces are consumed
         // (on the last step they re-read this chunk, unused)
         bf16x8 a_nxt[MH][2][2];
-        bf16x8 rlo_n = {};
         const int nn = update ? chunk_of(step + 1) : n;
-        const bf16x8 raw_n = bld(rc, c_lane + c_off(nn));
-        if (has_clo) rlo_n = bld(rcl, c_lane + c_off(nn));
+        raw_c = bld(rc, c_lane + c_off(nn));
+        if (has_clo) rlo_c = bld(rcl, c_lane + c_off(nn));
         phase();
 
         // ---- state update G += b_n^T c~_n (+ the lo passes); skipped on the
@@ -432,31 +486,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
             }
         }
 
-        // ---- exchange: wave w sums rows 8w .. 8w+7 of the eight partials, lane = column
+        // every partial of this chunk is written (exchanged at the next step's
+        // read-out); every wave is past this chunk's update
         sync_lds();
-        {
-            const float *rb = xbuf + lane * OPITCH + ROWS_PER_WAVE * wave;
-            f32x4 acc[2];
-#pragma unroll
-            for (int k = 0; k < 2; ++k) acc[k] = *reinterpret_cast<const f32x4 *>(rb + 4 * k);
-#pragma unroll
-            for (int w2 = 1; w2 < WAVES; ++w2)
-#pragma unroll
-                for (int k = 0; k < 2; ++k) acc[k] += *reinterpret_cast<const f32x4 *>(rb + w2 * XPART + 4 * k);
-            // value tiles hold their 32 columns in the order perm32
-            const int col = v0 + 32 * (lane / 32) + perm32(lane % 32);
-            if (col < V) {
-                float *dst = out_k + (static_cast<size_t>(b) * T + n * C + ROWS_PER_WAVE * wave) * V + col;
-#pragma unroll
-                for (int k = 0; k < 2; ++k)
-#pragma unroll
-                    for (int m = 0; m < 4; ++m)
-                        if (n * C + ROWS_PER_WAVE * wave + 4 * k + m < T) dst[static_cast<size_t>(4 * k + m) * V] = acc[k][m];
-            }
-        }
-
-        // ---- stage the next chunk's c (every wave is past this chunk's update)
-        if (update) stage_c(raw_n, rlo_n, scale_after(s_state, step + 1));
+        s_read_prev = s_read;
 #pragma unroll
         for (int mh = 0; mh < MH; ++mh)
 #pragma unroll
@@ -464,12 +497,13 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
 #pragma unroll
                 for (int mt = 0; mt < 2; ++mt) a_cur[mh][hb][mt] = a_nxt[mh][hb][mt];
     }
+    exchange(chunk_of(NT - 1), s_read_prev);
 }
 
 template <int MH, bool REV, bool UBSPLIT, bool FULL>
 int launch(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo, const uint16_t *c,
-           const uint16_t *clo, const uint16_t *P, const float *g, float *out, int B, int T, int K, int V, int nKG,
-           int bpg, hipStream_t s) {
+           const uint16_t *clo, const uint16_t *P, bool pscaled, const float *g, float *out, int B, int T, int K, int V,
+           int nKG, int bpg, hipStream_t s) {
     const int NT = (T + C - 1) / C;
     const int nVT = (V + VT - 1) / VT;
     const long long total = static_cast<long long>(B) * nKG * nVT;
@@ -485,7 +519,7 @@ int launch(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uin
     int st = la_timer_begin(s);
     if (st) return st;
     la_kgroup_kernel<MH, REV, UBSPLIT, FULL><<<dim3(static_cast<unsigned>(total)), WAVES * kWave, LDS_BYTES, s>>>(
-        a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, NT, nKG, bpg, nVT, static_cast<int>(total));
+        a, alo, ua, ualo, c, clo, P, pscaled ? 1 : 0, g, out, B, T, K, V, NT, nKG, bpg, nVT, static_cast<int>(total));
     st = check_launch("la_kgroup_kernel");
     if (st) return st;
     return la_timer_end(s);
@@ -493,19 +527,19 @@ int launch(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uin
 
 template <int MH>
 int launch_mh(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo, const uint16_t *c,
-              const uint16_t *clo, const uint16_t *P, const float *g, float *out, int B, int T, int K, int V, int nKG,
-              int bpg, bool reverse, bool ubsplit, hipStream_t s) {
+              const uint16_t *clo, const uint16_t *P, bool pscaled, const float *g, float *out, int B, int T, int K,
+              int V, int nKG, int bpg, bool reverse, bool ubsplit, hipStream_t s) {
     const bool full = alo || ualo || clo;
     const int sel = (reverse ? 4 : 0) + (ubsplit ? 2 : 0) + (full ? 1 : 0);
     switch (sel) {
-    case 0: return launch<MH, false, false, false>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
-    case 1: return launch<MH, false, false, true>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
-    case 2: return launch<MH, false, true, false>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
-    case 3: return launch<MH, false, true, true>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
-    case 4: return launch<MH, true, false, false>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
-    case 5: return launch<MH, true, false, true>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
-    case 6: return launch<MH, true, true, false>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
-    default: return launch<MH, true, true, true>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, s);
+    case 0: return launch<MH, false, false, false>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
+    case 1: return launch<MH, false, false, true>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
+    case 2: return launch<MH, false, true, false>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
+    case 3: return launch<MH, false, true, true>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
+    case 4: return launch<MH, true, false, false>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
+    case 5: return launch<MH, true, false, true>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
+    case 6: return launch<MH, true, true, false>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
+    default: return launch<MH, true, true, true>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
     }
 }
 
@@ -533,11 +567,11 @@ bool la_kgroup_supported(int B, int T, int K, int V) {
 // update adds ua^T c~, where c~ is c decayed and scaled in the kernel (+ the
 // rounding remainder of c~ when ubsplit, + ualo^T c~). c is also the value
 // operand of the intra-chunk product with P (P_lo forward or P_up reversed, of
-// chunk_scores). alo, ualo, clo may each be null.
+// chunk_scores, pscaled as chunk_scores' `scaled`). alo, ualo, clo may each be null.
 // out: la_kgroup_groups(K) x (B, T, V) fp32, fully written (no accumulation).
 int launch_la_kgroup(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo,
-                     const uint16_t *c, const uint16_t *clo, const uint16_t *P, const float *g, float *out, int B,
-                     int T, int K, int V, bool reverse, bool ubsplit, hipStream_t s) {
+                     const uint16_t *c, const uint16_t *clo, const uint16_t *P, bool pscaled, const float *g,
+                     float *out, int B, int T, int K, int V, bool reverse, bool ubsplit, hipStream_t s) {
     if (!la_kgroup_supported(B, T, K, V))
         return fail(ULM_ERR_UNSUPPORTED, "K-group kernel: B=%d T=%d K=%d V=%d unsupported", B, T, K, V);
     const int nKG = la_kgroup_groups(K);
@@ -546,11 +580,11 @@ int launch_la_kgroup(const uint16_t *a, const uint16_t *alo, const uint16_t *ua,
     const int mh = (bpg + kgrp::WAVES - 1) / kgrp::WAVES;
     switch (mh) {
     case 1:
-        return kgrp::launch_mh<1>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
+        return kgrp::launch_mh<1>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
     case 2:
-        return kgrp::launch_mh<2>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
+        return kgrp::launch_mh<2>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
     default:
-        return kgrp::launch_mh<3>(a, alo, ua, ualo, c, clo, P, g, out, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
+        return kgrp::launch_mh<3>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
     }
 }
 

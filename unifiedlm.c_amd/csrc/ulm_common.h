@@ -132,6 +132,18 @@ __device__ inline float state_inv_scale(float lam64, int k) {
     return 1.f / s;
 }
 
+// The scale s of H = s G in effect at the read-out of walk step k (after the
+// renormalisation that step applies; 1 at k = 0 and whenever lam^64 < 2^-40).
+__device__ inline float readout_scale(float lam64, int k) {
+    if (lam64 < kRenorm) return 1.f;
+    float s = 1.f;
+    for (int i = 0; i < k; ++i) {
+        if (i > 0 && s < kRenorm) s = 1.f;
+        s = lam64 * s;
+    }
+    return (k > 0 && s < kRenorm) ? 1.f : s;
+}
+
 inline bool valid_dtype(int dt) { return dt == ULM_F32 || dt == ULM_BF16 || dt == ULM_F16; }
 
 // Generic elementwise helpers (elementwise.hip).

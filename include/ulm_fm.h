@@ -69,6 +69,23 @@ int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const float *g, const
                float *q, void *fast, int fast_dtype, void *saved, size_t saved_bytes,
                void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream);
 
+/* Chunked prefill: the forward of ulm_fm_fwd (no autograd state kept) plus the
+ * decode state after position T-1, so decoding can continue from a prompt
+ * processed in one parallel pass instead of the token-by-token loop of
+ * UnifiedLM.forward_recurrent (model.py:164-175; the state of
+ * UnifiedBlock.init_state / step, model.py:88-111).
+ *
+ *   S      (B,D,A) fp32 out, 16-byte aligned: sum_{s<T} lam^(T-1-s) v_s k_s^T,
+ *          the S of ulm_decode_state
+ *   c_last (B,A)   fp32 out: w + sum_{s<T} lam^(T-1-s) k_s, the decode c
+ *   r, v, g, w, q, fast as for ulm_fm_fwd; workspace of
+ *   ulm_fm_prefill_workspace_bytes() bytes (0: unsupported shape).
+ * A and D must be multiples of 32. */
+size_t ulm_fm_prefill_workspace_bytes(int B, int T, int A, int D, int v_dtype, int fast_dtype);
+int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const float *g, const float *w,
+                   float *q, void *fast, int fast_dtype, float *S, float *c_last,
+                   void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream);
+
 /* Replaces UnifiedMemory.backward (kernel.py:216-233): the three chunked
  * products dq, dk (reverse), dv (reverse) and the denominator chain rule.
  *

@@ -20,6 +20,9 @@ How each function is pinned (tests/test_oracle.py):
   dense_fast_memory     closed form; brute-force double loop on tiny shapes;
                         special cases lam -> 0, lam = 1, T = 1, zero rows.
   chunked_fast_memory   equals dense for chunk 1, 7, 16, 64 (test_all.py:100-107).
+  fast_memory_state     S q_{T-1} and r_{T-1} / c give the dense fast and q at the
+                        last position; equals the block decode state of
+                        forward_recurrent's own steps (U - mu w, c).
   address               row sums z/(eps+z) < 1, zero where pre <= 0,
                         gradcheck of its backward formula.
   fast_memory_grads     torch.autograd.gradcheck at tiny shapes and the
@@ -89,6 +92,23 @@ def chunked_fast_memory(r, v, lam, w, chunk=64):
         state = lam ** L * state + (kc * tail).transpose(1, 2) @ vc
         mass = lam ** L * mass + (kc * tail).sum(1, keepdim=True)
     return torch.cat(qs, 1), torch.cat(fs, 1)
+
+
+def fast_memory_state(r, v, lam, w):
+    """The decode state after the last position, by the token recurrence of
+    UnifiedBlock.step (model.py:96-111) without its constant prior term:
+    S <- lam S + v_t k_t^T and c <- lam c + (1 - lam) w + k_t, k_t = r_{t-1},
+    from S = 0, c = w. Returns S (B, D, A) and c (B, A)."""
+    B, T, A = r.shape
+    D = v.shape[-1]
+    k = shift_keys(r)
+    vv = v.to(r.dtype)
+    S = r.new_zeros(B, D, A)
+    c = w.expand(B, A).clone()
+    for t in range(T):
+        S = lam * S + vv[:, t, :, None] * k[:, t, None, :]
+        c = lam * c + (1 - lam) * w + k[:, t]
+    return S, c
 
 
 def la_dense(a, b, c, lam, reverse=False):

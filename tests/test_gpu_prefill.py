@@ -1,0 +1,90 @@
+"""Chunked prefill (needs an MI355X): the forward of the fast memory plus the
+decode state after the last position, against the float64 oracle.
+
+Tolerances: q and c are fp32 scans (1e-5); fast and the state S come from bf16
+MFMA products with fp32 accumulation, the training path's 1e-2 (test_all.py:166).
+Every case prints its name before touching the GPU.
+"""
+import pytest
+import torch
+
+from helpers import fm_inputs, oracle_params, rel, say, tiny_model
+from oracle import fastmem as fm
+
+pytestmark = pytest.mark.gpu
+
+import kernel  # noqa: E402
+
+PREFILL_CASES = [
+    # B, T, A, D, lam, dtype of v
+    (2, 200, 96, 64, 0.93, torch.float32),      # ragged last chunk, a wave without keys
+    (1, 64, 128, 32, 0.93, torch.bfloat16),     # one whole chunk, a half-empty value tile
+    (2, 1, 64, 64, 0.93, torch.float32),        # a single position
+    (2, 300, 64, 128, 0.5, torch.float32),      # lam^64 below 2^-40
+    (1, 600, 1600, 64, 0.93, torch.bfloat16),   # 3 key groups; the state scale renormalises
+    (1, 512, 3072, 768, None, torch.bfloat16),  # 110M block shape
+]
+
+
+@pytest.mark.parametrize("B,T,A,D,lam,vdt", PREFILL_CASES)
+def test_fm_prefill_matches_oracle_state(B, T, A, D, lam, vdt):
+    say(f"fm_prefill B={B} T={T} A={A} D={D} lam={lam} v={vdt}")
+    r, v, g, w = fm_inputs(B, T, A, D, seed=T + A, device="cpu", lam=lam)
+    q, fast, S, c = kernel.fm_prefill(r.float().cuda(), v.to(vdt).cuda(), g.float().cuda(), w.float().cuda())
+    torch.cuda.synchronize()
+    vr = v.to(vdt).double()
+    qr, fr = fm.fast_memory(r, vr, g, w, "chunked")
+    Sr, cr = fm.fast_memory_state(r, vr, g.exp(), w)
+    errs = {"q": rel(q, qr), "fast": rel(fast, fr), "S": rel(S, Sr), "c": rel(c, cr)}
+    say(f"  rel errors {errs}")
+    assert S.shape == (B, D, A) and c.shape == (B, A)
+    assert errs["q"] < 1e-5 and errs["c"] < 1e-5
+    assert errs["fast"] < 1e-2 and errs["S"] < 1e-2
+
+
+def _oracle_states(p, tokens, n_layers):
+    """The oracle's per-block decode states after every position of tokens."""
+    B, T = tokens.shape
+    states = [fm.init_state(p, f"layers.{i}.", B) for i in range(n_layers)]
+    for t in range(T):
+        h = p["tok_embeddings.weight"][tokens[:, t]]
+        for i in range(n_layers):
+            h = fm.block_step(p, f"layers.{i}.", h, states[i])
+    return states
+
+
+def test_model_prefill_then_step_matches_recurrent():
+    say("UnifiedLM.prefill of 50 positions, then 20 steps, vs the oracle's forward_recurrent")
+    kw = dict(dim=32, n_layers=3, hidden_dim=64, vocab_size=97, max_seq_len=80)
+    model = tiny_model(**kw).cuda()
+    x = torch.randint(0, 97, (3, 70), generator=torch.Generator().manual_seed(2))
+    T0 = 50
+    logits0, states = model.prefill(x[:, :T0].cuda())
+    cont = torch.stack([model.step(x[:, t].cuda(), states) for t in range(T0, 70)], 1)
+    torch.cuda.synchronize()
+    p = oracle_params(model)
+    ref = fm.forward_recurrent(p, x)
+    assert rel(logits0, ref[:, T0 - 1]) < 1e-2
+    assert rel(cont, ref[:, T0:]) < 1e-2
+    # the states right after the prompt (S = U - mu w)
+    model2 = tiny_model(**kw).cuda()
+    _, st = model2.prefill(x[:, :T0].cuda())
+    so = _oracle_states(p, x[:, :T0], kw["n_layers"])
+    for i, (a, o) in enumerate(zip(st, so)):
+        w = fm.prior_mass(p[f"layers.{i}.log_w"])
+        errs = {"S": rel(a["S"], o["U"] - p[f"layers.{i}.mu.weight"] * w), "c": rel(a["c"], o["c"]),
+                "r_prev": rel(a["r_prev"], o["r_prev"]), "buf": rel(a["buf"], o["buf"])}
+        say(f"  block {i} rel errors {errs}")
+        assert max(errs.values()) < 1e-2, errs
+
+
+def test_model_prefill_short_prompt():
+    """A prompt shorter than the conv window (T = 2 < 3): the window keeps its zeros."""
+    say("UnifiedLM.prefill of 2 positions vs forward_recurrent")
+    model = tiny_model(dim=32, n_layers=2, hidden_dim=64, vocab_size=97, max_seq_len=40).cuda()
+    x = torch.randint(0, 97, (2, 6), generator=torch.Generator().manual_seed(4)).cuda()
+    logits0, states = model.prefill(x[:, :2])
+    cont = torch.stack([model.step(x[:, t], states) for t in range(2, 6)], 1)
+    ref = model.forward_recurrent(x)
+    assert rel(logits0, ref[:, 1]) < 1e-2
+    assert rel(cont, ref[:, 2:]) < 1e-2

@@ -101,6 +101,41 @@ def test_recurrent_form_matches_dense():
     assert (f - fr).abs().max() < 1e-12
 
 
+@pytest.mark.parametrize("T", [1, 2, 37])
+def test_state_reads_out_the_last_position(T):
+    """fast_{T-1} = S_{T-1} q_{T-1} and q_{T-1} = r_{T-1} / c_{T-1}, against the dense form."""
+    r, v, g, w = _inputs(B=2, T=T, A=6, D=4, lam=0.7)
+    q, f = fm.dense_fast_memory(r, v, g.exp(), w)
+    S, c = fm.fast_memory_state(r, v, g.exp(), w)
+    assert (torch.einsum("bda,ba->bd", S, q[:, -1]) - f[:, -1]).abs().max() < 1e-12
+    assert (r[:, -1] / c - q[:, -1]).abs().max() < 1e-12
+
+
+def test_state_matches_block_decode_state():
+    """The state of one block after T calls of block_step (its U minus the prior
+    mu w, and its c) from that block's own addresses and values."""
+    p = fm.tiny_params(seed=3, n_layers=1)
+    pre = "layers.0."
+    B, T = 2, 23
+    x = torch.randn(B, T, p[pre + "norm.weight"].shape[0], generator=torch.Generator().manual_seed(5),
+                    dtype=torch.float64)
+    st = fm.init_state(p, pre, B)
+    rs, vs = [], []
+    for t in range(T):
+        h = fm.rmsnorm(x[:, t], p[pre + "norm.weight"], 1e-5)
+        win = torch.cat([st["buf"], h[:, :, None]], dim=-1)
+        u = (win * p[pre + "conv.weight"][:, 0, :]).sum(-1)
+        rs.append(fm.address(torch.nn.functional.linear(u, p[pre + "key.weight"], p[pre + "key.bias"]),
+                             p[pre + "log_eps"]))
+        vs.append(torch.nn.functional.linear(h, p[pre + "val.weight"]))
+        fm.block_step(p, pre, x[:, t], st)
+    lam = torch.exp(fm.decay_log(p[pre + "log_rate"]))
+    w = fm.prior_mass(p[pre + "log_w"])
+    S, c = fm.fast_memory_state(torch.stack(rs, 1), torch.stack(vs, 1), lam, w)
+    assert (S - (st["U"] - p[pre + "mu.weight"] * w)).abs().max() < 1e-12
+    assert (c - st["c"]).abs().max() < 1e-12
+
+
 @pytest.mark.parametrize("chunk", [1, 7, 16, 64])
 def test_chunked_equals_dense(chunk):
     r, v, g, w = _inputs(B=2, T=150, A=9, D=5)

@@ -35,7 +35,7 @@ int la_kgroup_groups(int K);
 bool la_kgroup_supported(int B, int T, int K, int V);
 int launch_la_kgroup(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo,
                      const uint16_t *c, const uint16_t *clo, const uint16_t *P, bool pscaled, const float *g,
-                     float *out, int B, int T, int K, int V, bool reverse, bool ubsplit, hipStream_t s);
+                     float *out, float *state, int B, int T, int K, int V, bool reverse, bool ubsplit, hipStream_t s);
 // fm_chunks.hip
 int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t *raw_lo, uint16_t *xr,
                            uint16_t *xr_lo, int B, int T, int X, hipStream_t s);
@@ -44,8 +44,8 @@ int launch_chunk_scores(const uint16_t *aR, const uint16_t *aL, const uint16_t *
 int launch_partial_reduce(const float *part, int nK, size_t n, void *out, int odt, hipStream_t s);
 // fm_stats.hip
 int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
-                     uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, int B, int T, int A,
-                     hipStream_t s);
+                     uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, float *c_last, int B, int T,
+                     int A, hipStream_t s);
 size_t bwd_stats_partial_bytes(int B, int A);
 int launch_bwd_stats(const float *dqf, const float *dqo, const float *r, const float *nck,
                      const float *w, const float *g, const float *dkf, float *dr, float *dw, float *dg, void *part,
@@ -220,8 +220,8 @@ extern "C" int ulm_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
     // split products keep P_up = P_lo^T exactly, as dq and dk do
     ULM_TRY(launch_chunk_scores(reverse ? bR : aR, nullptr, reverse ? aR : bR, nullptr, g, Plo, Pup, B, T, K, !split,
                                 s));
-    ULM_TRY(launch_la_kgroup(aR, nullptr, bQ, nullptr, cQ, nullptr, reverse ? Pup : Plo, !split, g, part, B, T, K, V,
-                             reverse != 0, split != 0, s));
+    ULM_TRY(launch_la_kgroup(aR, nullptr, bQ, nullptr, cQ, nullptr, reverse ? Pup : Plo, !split, g, part, nullptr, B, T,
+                             K, V, reverse != 0, split != 0, s));
     if (nkg > 1) ULM_TRY(launch_partial_reduce(part, nkg, static_cast<size_t>(B) * T * V, out, ULM_F32, s));
     return ULM_OK;
 }
@@ -239,6 +239,43 @@ extern "C" size_t ulm_fm_fwd_workspace_bytes(int B, int T, int A, int D, int fas
     return fwd_layout(nullptr, B, T, A, D, fast_dtype).bytes;
 }
 
+namespace {
+
+// The forward composite of ulm_fm_fwd; with state (B, D, A) and c_last (B, A)
+// (aligned shapes only) it also emits the decode state after position T-1.
+int fm_forward(const float *r, const void *v, int v_dtype, const float *g, const float *w, float *q, void *fast,
+               int fast_dtype, void *saved, void *workspace, float *state, float *c_last, int B, int T, int A, int D,
+               hipStream_t s) {
+    const Saved sv = saved_layout(saved, B, T, A, D, v_dtype);
+    const FwdWs ws = fwd_layout(workspace, B, T, A, D, fast_dtype);
+    const size_t nf = static_cast<size_t>(B) * T * D;
+    if (fm_aligned(B, T, A, D)) {
+        const int nkg = la_kgroup_groups(A);
+        float *acc = ws.part ? ws.part : static_cast<float *>(fast);
+        ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, sv.qR, sv.kR, sv.qQ, sv.kQ, sv.nck, c_last, B, T, A, s));
+        ULM_TRY(launch_chunk_transpose(v, v_dtype, sv.vQ, sv.vQl, sv.vR, sv.vRl, B, T, D, s));
+        ULM_TRY(launch_chunk_scores(sv.qR, nullptr, sv.kR, nullptr, g, ws.Pf, sv.Pdv, B, T, A, true, s));
+        // fast = LA(q, k, v): update k^T v~ (v~ from the full-precision v), intra on
+        // bf16(v), as the reference's bf16 v (kernel.py:205). Its state, transposed,
+        // is the decode state S (model.py:96-111).
+        ULM_TRY(launch_la_kgroup(sv.qR, nullptr, sv.kQ, nullptr, sv.vQ, sv.vQl, ws.Pf, true, g, acc, state, B, T, A, D,
+                                 false, false, s));
+        if (ws.part) ULM_TRY(launch_partial_reduce(ws.part, nkg, nf, fast, fast_dtype, s));
+        return ULM_OK;
+    }
+    if (state || c_last) return fail(ULM_ERR_UNSUPPORTED, "prefill state: A=%d and D=%d must be multiples of 32", A, D);
+    ULM_TRY(launch_fwd_stats(r, w, g, q, sv.q16n, sv.k16n, nullptr, nullptr, nullptr, nullptr, sv.nck, nullptr, B, T, A,
+                             s));
+    ULM_TRY(launch_convert(v, v_dtype, sv.v16n, ULM_BF16, nf, s));
+    float *acc = fast_dtype == ULM_F32 ? static_cast<float *>(fast) : ws.part;
+    ULM_TRY(launch_fill_zero(acc, nf * sizeof(float), s));
+    ULM_TRY(launch_la_generic(sv.q16n, sv.k16n, sv.v16n, g, acc, B, T, A, D, false, s));
+    if (fast_dtype != ULM_F32) ULM_TRY(launch_convert(acc, ULM_F32, fast, fast_dtype, nf, s));
+    return ULM_OK;
+}
+
+}  // namespace
+
 extern "C" int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const float *g, const float *w, float *q,
                           void *fast, int fast_dtype, void *saved, size_t saved_bytes, void *workspace,
                           size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
@@ -250,30 +287,34 @@ extern "C" int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const floa
     const size_t need = ulm_fm_fwd_workspace_bytes(B, T, A, D, fast_dtype);
     ULM_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), "ulm_fm_fwd: workspace of %zu bytes, need %zu",
                 workspace_bytes, need);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const Saved sv = saved_layout(saved, B, T, A, D, v_dtype);
-    const FwdWs ws = fwd_layout(workspace, B, T, A, D, fast_dtype);
-    const size_t nf = static_cast<size_t>(B) * T * D;
-    if (fm_aligned(B, T, A, D)) {
-        const int nkg = la_kgroup_groups(A);
-        float *acc = ws.part ? ws.part : static_cast<float *>(fast);
-        ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, sv.qR, sv.kR, sv.qQ, sv.kQ, sv.nck, B, T, A, s));
-        ULM_TRY(launch_chunk_transpose(v, v_dtype, sv.vQ, sv.vQl, sv.vR, sv.vRl, B, T, D, s));
-        ULM_TRY(launch_chunk_scores(sv.qR, nullptr, sv.kR, nullptr, g, ws.Pf, sv.Pdv, B, T, A, true, s));
-        // fast = LA(q, k, v): update k^T v~ (v~ from the full-precision v), intra on
-        // bf16(v), as the reference's bf16 v (kernel.py:205)
-        ULM_TRY(launch_la_kgroup(sv.qR, nullptr, sv.kQ, nullptr, sv.vQ, sv.vQl, ws.Pf, true, g, acc, B, T, A, D, false,
-                                 false, s));
-        if (ws.part) ULM_TRY(launch_partial_reduce(ws.part, nkg, nf, fast, fast_dtype, s));
-        return ULM_OK;
-    }
-    ULM_TRY(launch_fwd_stats(r, w, g, q, sv.q16n, sv.k16n, nullptr, nullptr, nullptr, nullptr, sv.nck, B, T, A, s));
-    ULM_TRY(launch_convert(v, v_dtype, sv.v16n, ULM_BF16, nf, s));
-    float *acc = fast_dtype == ULM_F32 ? static_cast<float *>(fast) : ws.part;
-    ULM_TRY(launch_fill_zero(acc, nf * sizeof(float), s));
-    ULM_TRY(launch_la_generic(sv.q16n, sv.k16n, sv.v16n, g, acc, B, T, A, D, false, s));
-    if (fast_dtype != ULM_F32) ULM_TRY(launch_convert(acc, ULM_F32, fast, fast_dtype, nf, s));
-    return ULM_OK;
+    return fm_forward(r, v, v_dtype, g, w, q, fast, fast_dtype, saved, workspace, nullptr, nullptr, B, T, A, D,
+                      static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// chunked prefill: the forward plus the decode state after position T-1
+
+extern "C" size_t ulm_fm_prefill_workspace_bytes(int B, int T, int A, int D, int v_dtype, int fast_dtype) {
+    if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(v_dtype) || !valid_dtype(fast_dtype)) return 0;
+    if (!fm_aligned(B, T, A, D)) return 0;
+    return align_up(saved_layout(nullptr, B, T, A, D, v_dtype).bytes, 256) + fwd_layout(nullptr, B, T, A, D, fast_dtype).bytes;
+}
+
+extern "C" int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const float *g, const float *w, float *q,
+                              void *fast, int fast_dtype, float *S, float *c_last, void *workspace,
+                              size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
+    ULM_REQUIRE(B > 0 && T > 0 && A > 0 && D > 0, "ulm_fm_prefill: bad sizes B=%d T=%d A=%d D=%d", B, T, A, D);
+    ULM_REQUIRE(valid_dtype(v_dtype) && valid_dtype(fast_dtype), "ulm_fm_prefill: bad dtype %d/%d", v_dtype,
+                fast_dtype);
+    ULM_REQUIRE(r && v && g && w && q && fast && S && c_last && workspace, "ulm_fm_prefill: null pointer");
+    ULM_REQUIRE(fm_aligned(B, T, A, D), "ulm_fm_prefill: A=%d and D=%d must be multiples of 32", A, D);
+    ULM_REQUIRE(reinterpret_cast<uintptr_t>(S) % 16 == 0, "ulm_fm_prefill: S must be 16-byte aligned");
+    const size_t need = ulm_fm_prefill_workspace_bytes(B, T, A, D, v_dtype, fast_dtype);
+    ULM_REQUIRE(workspace_bytes >= need, "ulm_fm_prefill: workspace of %zu bytes, need %zu", workspace_bytes, need);
+    char *saved = static_cast<char *>(workspace);
+    char *ws = saved + align_up(saved_layout(nullptr, B, T, A, D, v_dtype).bytes, 256);
+    return fm_forward(r, v, v_dtype, g, w, q, fast, fast_dtype, saved, ws, S, c_last, B, T, A, D,
+                      static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D, int dfast_dtype) {
@@ -310,16 +351,16 @@ extern "C" int ulm_fm_bwd(const float *r, const float *g, const float *w, const 
         // rounding, so the decayed k~ / q~ take their bf16 remainder as a second
         // pass (and v, dfast their hi + lo pairs when they arrived in more than bf16).
         ULM_TRY(launch_la_kgroup(ws.doR, ws.doRl, sv.vQ, sv.vQl, sv.kQ, nullptr, ws.Pdq, false, g,
-                                 nkd > 1 ? ws.part : ws.dqf, B, T, D, A, false, true, s));
+                                 nkd > 1 ? ws.part : ws.dqf, nullptr, B, T, D, A, false, true, s));
         if (nkd > 1) ULM_TRY(launch_partial_reduce(ws.part, nkd, na, ws.dqf, ULM_F32, s));
         ULM_TRY(launch_la_kgroup(sv.vR, sv.vRl, ws.doQ, ws.doQl, sv.qQ, nullptr, ws.Pdk, false, g,
-                                 nkd > 1 ? ws.part : ws.dkf, B, T, D, A, true, true, s));
+                                 nkd > 1 ? ws.part : ws.dkf, nullptr, B, T, D, A, true, true, s));
         if (nkd > 1) ULM_TRY(launch_partial_reduce(ws.part, nkd, na, ws.dkf, ULM_F32, s));
         // dv = LA_rev(k, q, dfast): keys = A, values = D; update q^T dfast~ (from the
         // full-precision dfast), intra on bf16(dfast)
         const bool direct = nka == 1 && dv_dtype == ULM_F32;
         ULM_TRY(launch_la_kgroup(sv.kR, nullptr, sv.qQ, nullptr, ws.doQ, ws.doQl, sv.Pdv, true, g,
-                                 direct ? static_cast<float *>(dv) : ws.part, B, T, A, D, true, false, s));
+                                 direct ? static_cast<float *>(dv) : ws.part, nullptr, B, T, A, D, true, false, s));
         if (!direct) ULM_TRY(launch_partial_reduce(ws.part, nka, nd, dv, dv_dtype, s));
     } else {
         const uint16_t *do16 = static_cast<const uint16_t *>(dfast);

@@ -32,13 +32,15 @@ __device__ __forceinline__ float pow_int(float x, int e) {
 
 // Outputs besides q and n_ckpt (each may be null): q16n, k16n natural bf16
 // copies; qR, kR in the R layout and qQ, kQ in the Q layout (the chunked
-// kernel's operand tiles; A % 32 == 0). Positions past T are zero in R and Q.
+// kernel's operand tiles; A % 32 == 0); c_last = c at position T-1 (B, A), the
+// decode state after the sequence. Positions past T are zero in R and Q.
 __global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict__ r, const float *__restrict__ w,
                                                         const float *__restrict__ g, float *__restrict__ q,
                                                         uint16_t *__restrict__ q16n, uint16_t *__restrict__ k16n,
                                                         uint16_t *__restrict__ qR, uint16_t *__restrict__ kR,
                                                         uint16_t *__restrict__ qQ, uint16_t *__restrict__ kQ,
-                                                        float *__restrict__ nck, int T, int A, int NT) {
+                                                        float *__restrict__ nck, float *__restrict__ c_last, int T,
+                                                        int A, int NT) {
     __shared__ float tot[4][kSlots];
     __shared__ __align__(16) uint16_t sq[ULM_CHUNK][kSlots + 8], sk[ULM_CHUNK][kSlots + 8];   // [position][slot]
     const int s = threadIdx.x % kSlots, j = threadIdx.x / kSlots;
@@ -83,6 +85,7 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict_
             if (va && t < T) {
                 const size_t o = (bs * T + t) * A + a;
                 const float qt = rv[i] / ct;
+                if (c_last && t == T - 1) c_last[bs * A + a] = ct;
                 qb = f32_to_bf16_bits(qt);
                 kb = f32_to_bf16_bits(kv[i]);
                 q[o] = qt;
@@ -273,15 +276,15 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(const float *__restri
 // q16n, k16n: natural bf16 copies (both or neither); qR, kR, qQ, kQ: tiled
 // copies (all or none; A % 32 == 0).
 int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
-                     uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, int B, int T, int A,
-                     hipStream_t s) {
+                     uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, float *c_last, int B, int T,
+                     int A, hipStream_t s) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
     if ((q16n == nullptr) != (k16n == nullptr)) return fail(ULM_ERR_INVALID, "fwd stats: q16n and k16n go together");
     const bool tiled = qR || kR || qQ || kQ;
     if (tiled && !(qR && kR && qQ && kQ && A % 32 == 0))
         return fail(ULM_ERR_INVALID, "fwd stats: tiled copies need all four outputs and A %% 32 == 0");
     fwd_stats_kernel<<<dim3((A + kSlots - 1) / kSlots, B), 256, 0, s>>>(r, w, g, q, q16n, k16n, qR, kR, qQ, kQ, nck,
-                                                                         T, A, NT);
+                                                                         c_last, T, A, NT);
     return check_launch("fwd_stats_kernel");
 }
 

@@ -133,6 +133,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
                                                                   const uint16_t *__restrict__ Clo,
                                                                   const uint16_t *__restrict__ P, int pscaled,
                                                                   const float *__restrict__ g, float *__restrict__ out,
+                                                                  float *__restrict__ state,
                                                                   int Btot, int T, int K, int V, int NT, int nKG, int bpg,
                                                                   int nVT, int total) {
     extern __shared__ __align__(16) float lds_f[];   // staged c tiles, then the exchange partials
@@ -162,6 +163,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
     const float gl = g[0];
     const float lam64 = uniform(state_lam64(gl));
     const bool tiny = lam64 < kRenorm;
+    // final state (forward walk only): the last chunk's update also runs, with
+    // its decay taken relative to position T-1 (Tl positions of that chunk)
+    const bool want_state = !REV && state != nullptr;
+    const int Tl = T - (NT - 1) * C;
+    const float lamTl = uniform(__expf(gl * static_cast<float>(Tl)));
     const bool rows_here = tiny || !pscaled;   // read-out rows scaled per partial
     // row factor lam^(i+1) (lam^(64-i) reversed) of exchange row i = 8 wave
     // (uniform), and the ratio between consecutive rows
@@ -230,14 +236,22 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
     float duni[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) duni[e] = uniform(__expf(gl * static_cast<float>(REV ? e : 7 - e)));
-    auto stage_c = [&](bf16x8 raw, bf16x8 rlo, float s_new) {
-        const float dl = dlane * (1.f / s_new);
+    // fin: the final update of the state output, position j decayed by
+    // lam^(Tl-1-j) / s' (zero past the Tl positions of the chunk)
+    auto stage_c = [&](bf16x8 raw, bf16x8 rlo, float s_new, bool fin) {
+        const float inv_s = 1.f / s_new;
+        const float dl = dlane * inv_s;
         bf16x8 hi, lo;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             float x = static_cast<float>(raw[e]);
             if (has_clo) x += static_cast<float>(rlo[e]);
-            const float y = x * (dl * duni[e]);
+            float f = dl * duni[e];
+            if (fin) {
+                const int j = 16 * (wave % 4) + 8 * lh + e;
+                f = j < Tl ? __expf(gl * static_cast<float>(Tl - 1 - j)) * inv_s : 0.f;
+            }
+            const float y = x * f;
             hi[e] = static_cast<bf16>(y);
             lo[e] = static_cast<bf16>(y - static_cast<float>(hi[e]));
         }
@@ -263,7 +277,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
         const bf16x8 raw = bld(rc, c_lane + c_off(n0));
         const bf16x8 rlo = has_clo ? bld(rcl, c_lane + c_off(n0)) : bf16x8{};
         if (NT > 1) load_a(a_cur, chunk_of(1));
-        stage_c(raw, rlo, scale_after(1.f, 0));
+        const bool fin = want_state && NT == 1;
+        stage_c(raw, rlo, fin ? (tiny ? 1.f : lamTl) : scale_after(1.f, 0), fin);
     }
 
     // Exchange of chunk nx: wave w sums rows 8w .. 8w+7 of the eight partials
@@ -305,7 +320,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
     for (int step = 0; step < NT; ++step) {
         const int n = chunk_of(step);
         const bool readout = step > 0;
-        const bool update = step + 1 < NT;   // the last chunk's update is never read
+        const bool last = step + 1 == NT;
+        const bool update = !last || want_state;   // the last chunk's update is read only as the final state
 
         // ---- rescaling of G around the read-out (rarely): renormalisation
         // (G *= s, s = 1) before, when s fell below 2^-40, or, when lam^64 itself
@@ -321,7 +337,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
         }
 
         // ---- stage this chunk's c (every wave is past the previous update)
-        if (step > 0) stage_c(raw_c, rlo_c, scale_after(s_state, step));
+        if (step > 0) {
+            const bool fin = want_state && last;
+            stage_c(raw_c, rlo_c, fin ? (tiny ? 1.f : lamTl * s_state) : scale_after(s_state, step), fin);
+        }
 
         // ---- read-out of H = s G (both 32-row halves; G converted once per block)
         f32x16 O[2][2];
@@ -402,9 +421,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) G[mh][nt][r] *= lam64;
+                    for (int r = 0; r < 16; ++r) G[mh][nt][r] *= (want_state && last) ? lamTl : lam64;
         }
-        s_state = tiny ? 1.f : lam64 * s_state;   // scale after this chunk's update
+        s_state = tiny ? 1.f : ((want_state && last) ? lamTl : lam64) * s_state;   // scale after this chunk's update
 
         // every wave has finished reducing the previous chunk's partials, and
         // this chunk's c tiles are staged
@@ -437,7 +456,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
         // replaces are consumed
         // (on the last step they re-read this chunk, unused)
         bf16x8 a_nxt[MH][2][2];
-        const int nn = update ? chunk_of(step + 1) : n;
+        const int nn = !last ? chunk_of(step + 1) : n;
         raw_c = bld(rc, c_lane + c_off(nn));
         if (has_clo) rlo_c = bld(rcl, c_lane + c_off(nn));
         phase();
@@ -498,12 +517,38 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
                 for (int mt = 0; mt < 2; ++mt) a_cur[mh][hb][mt] = a_nxt[mh][hb][mt];
     }
     exchange(chunk_of(NT - 1), s_read_prev);
+
+    // ---- final state H = s G as state[b][column][key] (fp32, (B, V, K)). In a
+    // state tile, registers 8k .. 8k+7 of lane (lr, lh) hold keys 16k + 8 lh + 0..7
+    // (rows in the order perm32) of column perm32(lr) of the 32-column tile.
+    if (want_state) {
+#pragma unroll
+        for (int mh = 0; mh < MH; ++mh) {
+            const int blk = blk0 + wave + WAVES * mh;
+            if (blk >= blk1) continue;
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const int col = v0 + 32 * nt + perm32(lr);
+                if (col >= V) continue;
+                float *dst = state + (static_cast<size_t>(b) * V + col) * K + 32 * blk + 8 * lh;
+#pragma unroll
+                for (int k = 0; k < 2; ++k)
+#pragma unroll
+                    for (int h4 = 0; h4 < 2; ++h4) {
+                        f32x4 x;
+#pragma unroll
+                        for (int m = 0; m < 4; ++m) x[m] = s_state * G[mh][nt][8 * k + 4 * h4 + m];
+                        *reinterpret_cast<f32x4 *>(dst + 16 * k + 4 * h4) = x;
+                    }
+            }
+        }
+    }
 }
 
 template <int MH, bool REV, bool UBSPLIT, bool FULL>
 int launch(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo, const uint16_t *c,
-           const uint16_t *clo, const uint16_t *P, bool pscaled, const float *g, float *out, int B, int T, int K, int V,
-           int nKG, int bpg, hipStream_t s) {
+           const uint16_t *clo, const uint16_t *P, bool pscaled, const float *g, float *out, float *state, int B, int T,
+           int K, int V, int nKG, int bpg, hipStream_t s) {
     const int NT = (T + C - 1) / C;
     const int nVT = (V + VT - 1) / VT;
     const long long total = static_cast<long long>(B) * nKG * nVT;
@@ -519,7 +564,7 @@ int launch(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uin
     int st = la_timer_begin(s);
     if (st) return st;
     la_kgroup_kernel<MH, REV, UBSPLIT, FULL><<<dim3(static_cast<unsigned>(total)), WAVES * kWave, LDS_BYTES, s>>>(
-        a, alo, ua, ualo, c, clo, P, pscaled ? 1 : 0, g, out, B, T, K, V, NT, nKG, bpg, nVT, static_cast<int>(total));
+        a, alo, ua, ualo, c, clo, P, pscaled ? 1 : 0, g, out, state, B, T, K, V, NT, nKG, bpg, nVT, static_cast<int>(total));
     st = check_launch("la_kgroup_kernel");
     if (st) return st;
     return la_timer_end(s);
@@ -527,19 +572,19 @@ int launch(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uin
 
 template <int MH>
 int launch_mh(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo, const uint16_t *c,
-              const uint16_t *clo, const uint16_t *P, bool pscaled, const float *g, float *out, int B, int T, int K,
-              int V, int nKG, int bpg, bool reverse, bool ubsplit, hipStream_t s) {
+              const uint16_t *clo, const uint16_t *P, bool pscaled, const float *g, float *out, float *state, int B,
+              int T, int K, int V, int nKG, int bpg, bool reverse, bool ubsplit, hipStream_t s) {
     const bool full = alo || ualo || clo;
     const int sel = (reverse ? 4 : 0) + (ubsplit ? 2 : 0) + (full ? 1 : 0);
     switch (sel) {
-    case 0: return launch<MH, false, false, false>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
-    case 1: return launch<MH, false, false, true>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
-    case 2: return launch<MH, false, true, false>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
-    case 3: return launch<MH, false, true, true>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
-    case 4: return launch<MH, true, false, false>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
-    case 5: return launch<MH, true, false, true>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
-    case 6: return launch<MH, true, true, false>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
-    default: return launch<MH, true, true, true>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, s);
+    case 0: return launch<MH, false, false, false>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, state, B, T, K, V, nKG, bpg, s);
+    case 1: return launch<MH, false, false, true>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, state, B, T, K, V, nKG, bpg, s);
+    case 2: return launch<MH, false, true, false>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, state, B, T, K, V, nKG, bpg, s);
+    case 3: return launch<MH, false, true, true>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, state, B, T, K, V, nKG, bpg, s);
+    case 4: return launch<MH, true, false, false>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, state, B, T, K, V, nKG, bpg, s);
+    case 5: return launch<MH, true, false, true>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, state, B, T, K, V, nKG, bpg, s);
+    case 6: return launch<MH, true, true, false>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, state, B, T, K, V, nKG, bpg, s);
+    default: return launch<MH, true, true, true>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, state, B, T, K, V, nKG, bpg, s);
     }
 }
 
@@ -569,22 +614,26 @@ bool la_kgroup_supported(int B, int T, int K, int V) {
 // operand of the intra-chunk product with P (P_lo forward or P_up reversed, of
 // chunk_scores, pscaled as chunk_scores' `scaled`). alo, ualo, clo may each be null.
 // out: la_kgroup_groups(K) x (B, T, V) fp32, fully written (no accumulation).
+// state (forward walk only, may be null): the state after position T-1,
+// sum_s lam^(T-1-s) b_s c_s^T, as fp32 (B, V, K), 16-byte aligned.
 int launch_la_kgroup(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uint16_t *ualo,
                      const uint16_t *c, const uint16_t *clo, const uint16_t *P, bool pscaled, const float *g,
-                     float *out, int B, int T, int K, int V, bool reverse, bool ubsplit, hipStream_t s) {
+                     float *out, float *state, int B, int T, int K, int V, bool reverse, bool ubsplit, hipStream_t s) {
     if (!la_kgroup_supported(B, T, K, V))
         return fail(ULM_ERR_UNSUPPORTED, "K-group kernel: B=%d T=%d K=%d V=%d unsupported", B, T, K, V);
+    if (state && (reverse || reinterpret_cast<uintptr_t>(state) % 16))
+        return fail(ULM_ERR_INVALID, "K-group kernel: the state output needs the forward walk and 16-byte alignment");
     const int nKG = la_kgroup_groups(K);
     const int nb = K / 32;
     const int bpg = (nb + nKG - 1) / nKG;   // <= 24 blocks, so at most 3 per wave
     const int mh = (bpg + kgrp::WAVES - 1) / kgrp::WAVES;
     switch (mh) {
     case 1:
-        return kgrp::launch_mh<1>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
+        return kgrp::launch_mh<1>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, state, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
     case 2:
-        return kgrp::launch_mh<2>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
+        return kgrp::launch_mh<2>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, state, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
     default:
-        return kgrp::launch_mh<3>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
+        return kgrp::launch_mh<3>(a, alo, ua, ualo, c, clo, P, pscaled, g, out, state, B, T, K, V, nKG, bpg, reverse, ubsplit, s);
     }
 }
 

@@ -177,6 +177,34 @@ def relu2_address(pre, bias, log_eps):
 # ---------------------------------------------------------------------------
 # per-token decode (model.py:96-111), N sequences at once, fp32
 
+@torch.no_grad()
+def fm_prefill(r, v, g, w):
+    """The forward of unified_memory (no autograd) plus the decode state after
+    the last position: returns (q, fast, S, c) with S (B, D, A) fp32 =
+    sum_s lam^(T-1-s) v_s k_s^T and c (B, A) fp32 = w + sum_s lam^(T-1-s) k_s,
+    the state UnifiedBlock.step carries (model.py:88-111). A and D must be
+    multiples of 32."""
+    _check_fm(r, v, g, w)
+    B, T, A = r.shape
+    D = v.shape[-1]
+    r32 = r.float().contiguous()
+    vc = v.contiguous()
+    g1 = g.float().reshape(1).contiguous()
+    w32 = w.float().contiguous()
+    vdt = nat.dtype_code(v.dtype)
+    ws_bytes = nat.lib().ulm_fm_prefill_workspace_bytes(B, T, A, D, vdt, vdt)
+    if ws_bytes == 0:
+        raise RuntimeError(f"fm_prefill: A={A} and D={D} must be multiples of 32")
+    q = torch.empty_like(r32)
+    fast = torch.empty(B, T, D, device=r.device, dtype=v.dtype)
+    S = torch.empty(B, D, A, device=r.device, dtype=torch.float32)
+    c = torch.empty(B, A, device=r.device, dtype=torch.float32)
+    ws = torch.empty(ws_bytes, device=r.device, dtype=torch.uint8)
+    call("ulm_fm_prefill", ptr(r32), ptr(vc), vdt, ptr(g1), ptr(w32), ptr(q), ptr(fast), vdt, ptr(S), ptr(c), ptr(ws),
+         ws_bytes, B, T, A, D, nat.stream_of(r))
+    return q, fast, S, c
+
+
 def _f32c(t):
     if t.dtype != torch.float32 or not t.is_contiguous():
         raise ValueError("decode tensors must be contiguous float32")

@@ -22,7 +22,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from kernel import CHUNK, decode_addr, decode_pre, decode_state, relu2_address, unified_memory
+from kernel import CHUNK, decode_addr, decode_pre, decode_state, fm_prefill, relu2_address, unified_memory
 
 
 @dataclass
@@ -95,22 +95,48 @@ class UnifiedBlock(nn.Module):
 
     # ---- token-by-token form (model.py:87-111)
     @torch.no_grad()
+    def _step_params(self, device):
+        """The fp32 views of the parameters that every step uses (taken once per
+        decode session: the weights do not change while a session decodes)."""
+        f = lambda t: t.detach().to(device=device, dtype=torch.float32).contiguous()
+        return {"norm_w": f(self.norm.weight), "conv_w": f(self.conv.weight[:, 0, :]), "key_wt": f(self.key.weight.t()),
+                "key_b": f(self.key.bias), "log_eps": f(self.log_eps).reshape(1), "val_wt": f(self.val.weight.t()),
+                "mu_wt": f(self.mu.weight.t()), "w": f(self._w()), "g": f(-self.log_rate.exp()).reshape(1)}
+
+    @torch.no_grad()
     def init_state(self, batch: int, device):
-        """Decode state of one block, plus the fp32 views of its parameters that
-        every step uses (taken once per decode session: the weights do not
-        change while a session decodes)."""
+        """Decode state of one block before any position, plus its parameter views."""
         d, m = self.mu.out_features, self.mu.in_features
         kw = self.conv.kernel_size[0] - 1
-        f = lambda t: t.detach().to(device=device, dtype=torch.float32).contiguous()
-        w = f(self._w())
-        params = {"norm_w": f(self.norm.weight), "conv_w": f(self.conv.weight[:, 0, :]), "key_wt": f(self.key.weight.t()),
-                  "key_b": f(self.key.bias), "log_eps": f(self.log_eps).reshape(1), "val_wt": f(self.val.weight.t()),
-                  "mu_wt": f(self.mu.weight.t()), "w": w, "g": f(-self.log_rate.exp()).reshape(1)}
+        params = self._step_params(device)
         return {"buf": torch.zeros(batch, d, kw, device=device, dtype=torch.float32),
                 "S": torch.zeros(batch, d, m, device=device, dtype=torch.float32),
-                "c": w.expand(batch, m).clone(),   # updated in place: never a view of w
+                "c": params["w"].expand(batch, m).clone(),   # updated in place: never a view of w
                 "r_prev": torch.zeros(batch, m, device=device, dtype=torch.float32),
                 "params": params}
+
+    @torch.no_grad()
+    def prefill(self, x):
+        """`forward` over a whole prompt x (B, T, d) in one chunked pass, also
+        returning the decode state after position T-1: the state that T calls of
+        `step` would leave (model.py:88-111), with S and c from the chunked
+        kernels (bf16 operands, fp32 accumulation) instead of T fp32 updates."""
+        h = self.norm(x)
+        u = self.conv(h.transpose(1, 2))[..., : h.size(1)].transpose(1, 2)
+        r = self.code(u)
+        v = self.val(h)
+        w = self._w()
+        q, fast, S, c = fm_prefill(r, v, -self.log_rate.exp(), w)
+        out = x + self.mu((q * w).type_as(x)) + fast.type_as(x)
+        B, T, d = x.shape
+        kw = self.conv.kernel_size[0] - 1
+        buf = torch.zeros(B, d, kw, device=x.device, dtype=torch.float32)
+        if kw > 0:
+            tail = h.float()[:, max(0, T - kw):, :].transpose(1, 2)   # the last (up to) kw positions, oldest first
+            buf[:, :, kw - tail.size(-1):] = tail
+        state = {"buf": buf, "S": S, "c": c, "r_prev": r[:, -1, :].float().contiguous(),
+                 "params": self._step_params(x.device)}
+        return out, state
 
     @torch.no_grad()
     def step(self, x, s):
@@ -175,6 +201,18 @@ class UnifiedLM(nn.Module):
 
     def init_states(self, batch: int, device):
         return [layer.init_state(batch, device) for layer in self.layers]
+
+    @torch.no_grad()
+    def prefill(self, tokens: torch.Tensor):
+        """A prompt (B, T) in one chunked pass: returns the logits of its last
+        position (B, V) and the per-block decode states, from which `step`
+        continues exactly as after T calls of `step`."""
+        h = self.tok_embeddings(tokens)
+        states = []
+        for layer in self.layers:
+            h, s = layer.prefill(h)
+            states.append(s)
+        return self.output(self.norm(h[:, -1, :])), states
 
     @torch.no_grad()
     def step(self, tokens: torch.Tensor, states) -> torch.Tensor:

@@ -223,6 +223,32 @@ class UnifiedLM(nn.Module):
         return self.output(self.norm(h))
 
     @torch.no_grad()
+    def decode_greedy(self, prompt: torch.Tensor, steps: int, prefill: bool = True) -> torch.Tensor:
+        """The generate loop of the reference's C decoder at temperature 0
+        (run.c:542-571, without its BOS stop): positions 0 .. steps-1 are run,
+        the prompt (B, T0) is forced and every later token is the argmax of the
+        previous position's logits (first maximum on ties, run.c:460-469).
+        Returns (B, steps + 1) tokens. With `prefill` the prompt goes through
+        one chunked pass (`prefill`, slots and width multiples of 32) instead of
+        T0 calls of `step`."""
+        B, T0 = prompt.shape
+        if steps < T0:
+            raise ValueError(f"steps={steps} is shorter than the prompt ({T0})")
+        if prefill:
+            logits, states = self.prefill(prompt)
+        else:
+            states = self.init_states(B, prompt.device)
+            for t in range(T0):
+                logits = self.step(prompt[:, t], states)
+        out = [prompt]
+        for pos in range(T0 - 1, steps):
+            nxt = logits.argmax(-1)
+            out.append(nxt[:, None])
+            if pos + 1 < steps:
+                logits = self.step(nxt, states)
+        return torch.cat(out, 1)
+
+    @torch.no_grad()
     def forward_recurrent(self, tokens: torch.Tensor) -> torch.Tensor:
         """Token-by-token inference with constant state per block, exactly what run.c computes."""
         B, T = tokens.shape

@@ -54,6 +54,7 @@ def parse():
     p.add_argument("--decode-seqs", type=int, default=256)
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-block", action="store_true")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                    help="first run one plain fp32 copy kernel over MB megabytes (a known-size reference for "
                         "hardware byte counters)")
@@ -107,6 +108,54 @@ def bench_training(torch, args):
                           "kernel": "la_kgroup_kernel", "flops_per_launch": la_flops,
                           "avg_launch_ms": round(la_ms, 4), "launches_timed": timer.launches},
                 path_tflops=path_tflops)
+
+
+def bench_block(torch, args):
+    """Whole UnifiedBlocks (model.py:77-85) forward + backward over the training
+    workload's shape under bf16 autocast: the fused block and the op-by-op
+    path (forward_composed) on the same weights and input."""
+    import workloads
+    from model import ModelArgs, UnifiedLM
+    cfg = workloads.SHAPES[args.shape]
+    B, T, D, A, L = cfg["B"], cfg["T"], cfg["D"], cfg["A"], cfg["blocks"]
+    dev = torch.device("cuda:0")
+    log(f"block workload {args.shape}: B={B} T={T} D={D} A={A} blocks={L}, bf16 autocast")
+    model = UnifiedLM(ModelArgs(dim=D, n_layers=L, hidden_dim=A, vocab_size=256, max_seq_len=T))
+    workloads.init_decode_model(model, seed=43)
+    blocks = model.layers.to(dev).train()
+    gen = torch.Generator(device=dev).manual_seed(7)
+    x0 = torch.randn(B, T, D, device=dev, generator=gen)
+    dout = torch.randn(B, T, D, device=dev, generator=gen)
+
+    def step(fused):
+        for prm in blocks.parameters():
+            prm.grad = None
+        x = x0.detach().requires_grad_(True)
+        h = x
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            for blk in blocks:
+                h = blk(h) if fused else blk.forward_composed(h)
+        h.backward(dout)
+
+    def timed(fused):
+        for _ in range(args.warmup):
+            step(fused)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step(fused)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / args.steps
+
+    ms = timed(True)
+    ms_c = timed(False)
+    ftok = workloads.block_flops_per_token(T, A, D) * L
+    log(f"block step {ms:.2f} ms fused, {ms_c:.2f} ms op by op")
+    return {"workload": f"UnifiedBlock fwd+bwd, {L} blocks of the {args.shape} shape, bf16 autocast",
+            "ms_per_step": round(ms, 3), "Mtok_per_s": round(B * T / (ms * 1e-3) / 1e6, 4),
+            "tflops": round(ftok * B * T / (ms * 1e-3) / 1e12, 2),
+            "composed_ms_per_step": round(ms_c, 3), "composed_Mtok_per_s": round(B * T / (ms_c * 1e-3) / 1e6, 4),
+            "speedup_vs_composed": round(ms_c / ms, 3)}
 
 
 def bench_cpu_baseline(torch, train):
@@ -221,6 +270,7 @@ def main():
         del x, y
     train = bench_training(torch, args)
     cpu = None if args.no_cpu else bench_cpu_baseline(torch, train)
+    block = None if args.no_block else bench_block(torch, args)
     decode = None if args.no_decode else bench_decode(torch, args)
     out = {
         "metric": METRIC,
@@ -242,6 +292,7 @@ def main():
         "path_frac_bf16_peak": round(train["path_tflops"] / PEAK_BF16_TFLOPS, 4),
         "roofline": train["roofline"],
         "cpu_baseline": cpu,
+        "block": block,
         "decode": decode,
     }
     print(json.dumps(out), flush=True)

@@ -132,12 +132,72 @@ int ulm_addr_fwd(const void *pre, int pre_dtype, const float *bias, const float 
                  float *r, float *denom, int M, int A, void *stream);
 
 /* Backward of ulm_addr_fwd: dpre (M,A) pre_dtype, dbias (A,) fp32 (may be
- * NULL when bias is NULL), dlog_eps (1,) fp32. */
+ * NULL when bias is NULL), dlog_eps (1,) fp32, both summed in a fixed order.
+ * A <= 8192. */
 size_t ulm_addr_bwd_workspace_bytes(int M, int A);
 int ulm_addr_bwd(const void *pre, int pre_dtype, const float *bias, const float *log_eps,
                  const float *r, const float *denom, const float *dr,
                  void *dpre, float *dbias, float *dlog_eps,
                  void *workspace, size_t workspace_bytes, int M, int A, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Training: the rest of UnifiedBlock.forward (model.py:77-85) around the fast
+ * memory. The block runs as
+ *   h, u  = ulm_norm_conv_fwd(x)               RMSNorm + causal conv (78-79)
+ *   pre   = u K^T,  v = h W_v^T                 caller's GEMMs (key, val)
+ *   r     = ulm_addr_fwd(pre)                   relu^2 address (code, 70-72)
+ *   qw, y = ulm_block_fm_fwd(r, v, x)          qw = w q, y = x + fast (84-85)
+ *   out   = y + qw mu^T                         caller's GEMM, accumulating into y
+ * and backward in reverse, with ulm_block_fm_bwd taking d(w q) = dout mu and
+ * ulm_norm_conv_bwd joining the conv, RMSNorm and residual gradients.
+ */
+
+/* h = (x rstd) * norm_w with rstd = (mean x^2 + eps)^-1/2 per position
+ * (RMSNorm, model.py:31-42); u = the depthwise causal conv of h with Kc taps,
+ * conv_w (D, Kc) oldest tap first, zero before position 0 (nn.Conv1d with
+ * groups = D, padding Kc - 1, truncated to T: model.py:63, 79).
+ *   x (B,T,D) x_dtype (F32 or BF16); h, u (B,T,D) out, in one dtype
+ *   (h_dtype == u_dtype); rstd (B,T) fp32 out, saved for the backward.
+ *   1 <= Kc <= 8. */
+int ulm_norm_conv_fwd(const void *x, int x_dtype, const float *norm_w, const float *conv_w, int Kc,
+                      float norm_eps, void *h, int h_dtype, void *u, int u_dtype, float *rstd,
+                      int B, int T, int D, void *stream);
+
+/* Backward of ulm_norm_conv_fwd plus the residual branch:
+ *   dx = dres + d(RMSNorm)(dhv + conv^T du),
+ *   dnorm_w (D,) and dconv_w (D, Kc) fp32 out, summed deterministically.
+ *   du (B,T,D) du_dtype; dhv (B,T,D) or NULL, the value GEMM's gradient of
+ *   h, in the same dtype (dhv_dtype == du_dtype); dres (B,T,D) fp32 or
+ *   NULL; dx (B,T,D) fp32 out, may be
+ *   dres itself. Workspace of ulm_norm_conv_bwd_workspace_bytes() bytes
+ *   (0: D too large). */
+size_t ulm_norm_conv_bwd_workspace_bytes(int B, int T, int D, int Kc);
+int ulm_norm_conv_bwd(const void *x, int x_dtype, const float *rstd, const float *norm_w,
+                      const float *conv_w, int Kc, const void *du, int du_dtype, const void *dhv,
+                      int dhv_dtype, const float *dres, float *dx, float *dnorm_w, float *dconv_w,
+                      void *workspace, size_t workspace_bytes, int B, int T, int D, void *stream);
+
+/* ulm_fm_fwd inside the block: instead of q and fast it writes
+ *   qw (B,T,A) qw_dtype out: w q, the operand of the mu GEMM ((q*w), model.py:85)
+ *   y  (B,T,D) fp32 out:     x + fast, x (B,T,D) fp32 the residual (y != x)
+ * saved as for ulm_fm_fwd (ulm_fm_saved_bytes). */
+size_t ulm_block_fm_fwd_workspace_bytes(int B, int T, int A, int D);
+int ulm_block_fm_fwd(const float *r, const void *v, int v_dtype, const float *g, const float *w,
+                     void *qw, int qw_dtype, const float *x, float *y, void *saved, size_t saved_bytes,
+                     void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream);
+
+/* ulm_fm_bwd inside the block: dqw (B,T,A) dqw_dtype is d loss / d(w q); the
+ * q gradient is w dqw and dw also gets sum_t q dqw. Workspace of
+ * ulm_fm_bwd_workspace_bytes() bytes; other arguments as for ulm_fm_bwd. */
+int ulm_block_fm_bwd(const float *r, const float *g, const float *w, const void *saved,
+                     size_t saved_bytes, int v_dtype, const void *dfast, int dfast_dtype,
+                     const void *dqw, int dqw_dtype, float *dr, void *dv, int dv_dtype, float *dg,
+                     float *dw, void *workspace, size_t workspace_bytes, int B, int T, int A, int D,
+                     void *stream);
+
+/* dst = src converted elementwise (n elements; F32/BF16/F16, bf16 rounding to
+ * nearest even): the autocast casts around the block's GEMMs. */
+int ulm_cast(const void *src, int src_dtype, void *dst, int dst_dtype, size_t n, void *stream);
 
 /* ------------------------------------------------------------------------
  * Batched recurrent decode, N sequences, one block, one position. Together

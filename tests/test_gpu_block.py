@@ -1,0 +1,161 @@
+"""UnifiedBlock around the fast memory (needs an MI355X): the fused RMSNorm +
+causal conv kernels against float64 autograd of the oracle's rmsnorm and
+causal_conv, and one whole block (model.py:77-85) forward and backward against
+the oracle's block_forward.
+
+Tolerances: the norm/conv kernels compute in fp32 (1e-5, fp32 outputs); the
+block's GEMMs and fast-memory products take bf16 (autocast) or fp32 operands
+with fp32 accumulation, held to the reference's 1e-2 (test_all.py:166), the
+decay gradient under bf16 autocast to 2e-2 (docs/kernel.md:32).
+Every case prints its name before touching the GPU.
+"""
+import pytest
+import torch
+
+from helpers import rel, say, tiny_model
+from oracle import fastmem as fm
+
+pytestmark = pytest.mark.gpu
+
+import ulm_native as nat  # noqa: E402
+from ulm_native import call, ptr  # noqa: E402
+
+NC_CASES = [
+    # B, T, D, Kc
+    (2, 37, 64, 4),       # the model's conv_size, ragged position tile
+    (1, 5, 300, 4),       # T shorter than a tile, D not a multiple of 256
+    (2, 200, 768, 4),     # 110M width
+    (1, 3, 96, 1),        # a single tap: no halo
+    (2, 70, 130, 8),      # the largest tap count
+    (1, 40, 2100, 4),     # wide rows: the backward's 8-position tile
+]
+
+
+def _nc_inputs(B, T, D, Kc, seed):
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, T, D, generator=gen, dtype=torch.float64)
+    nw = 1.0 + 0.3 * torch.randn(D, generator=gen, dtype=torch.float64)
+    cw = 0.5 * torch.randn(D, 1, Kc, generator=gen, dtype=torch.float64)
+    return x, nw, cw
+
+
+@pytest.mark.parametrize("B,T,D,Kc", NC_CASES)
+def test_norm_conv_fwd_matches_oracle(B, T, D, Kc):
+    say(f"ulm_norm_conv_fwd B={B} T={T} D={D} Kc={Kc}")
+    x, nw, cw = _nc_inputs(B, T, D, Kc, seed=T + D)
+    xd, nwd, cwd = (t.float().cuda().contiguous() for t in (x, nw, cw.reshape(D, Kc)))
+    h = torch.empty(B, T, D, device="cuda")
+    u = torch.empty(B, T, D, device="cuda")
+    hb = torch.empty(B, T, D, device="cuda", dtype=torch.bfloat16)
+    ub = torch.empty(B, T, D, device="cuda", dtype=torch.bfloat16)
+    rstd = torch.empty(B, T, device="cuda")
+    s = nat.stream_of(xd)
+    call("ulm_norm_conv_fwd", ptr(xd), nat.ULM_F32, ptr(nwd), ptr(cwd), Kc, 1e-5, ptr(h), nat.ULM_F32, ptr(u),
+         nat.ULM_F32, ptr(rstd), B, T, D, s)
+    call("ulm_norm_conv_fwd", ptr(xd), nat.ULM_F32, ptr(nwd), ptr(cwd), Kc, 1e-5, ptr(hb), nat.ULM_BF16, ptr(ub),
+         nat.ULM_BF16, ptr(rstd), B, T, D, s)
+    torch.cuda.synchronize()
+    hr = fm.rmsnorm(x, nw, 1e-5)
+    ur = fm.causal_conv(hr, cw)
+    rr = torch.rsqrt(x.pow(2).mean(-1) + 1e-5)
+    errs = {"h": rel(h, hr), "u": rel(u, ur), "rstd": rel(rstd, rr), "h16": rel(hb, hr), "u16": rel(ub, ur)}
+    say(f"  rel errors {errs}")
+    assert errs["h"] < 1e-6 and errs["u"] < 1e-6 and errs["rstd"] < 1e-6
+    assert errs["h16"] < 1e-2 and errs["u16"] < 1e-2   # bf16 rounding of the outputs
+
+
+@pytest.mark.parametrize("B,T,D,Kc", NC_CASES)
+def test_norm_conv_bwd_matches_autograd(B, T, D, Kc):
+    say(f"ulm_norm_conv_bwd B={B} T={T} D={D} Kc={Kc}")
+    x, nw, cw = _nc_inputs(B, T, D, Kc, seed=3 * T + D)
+    gen = torch.Generator().manual_seed(D)
+    du, dhv, dres = (torch.randn(B, T, D, generator=gen, dtype=torch.float64) for _ in range(3))
+    # float64 autograd of the oracle: L = <du, u> + <dhv, h>, dx gets dres on top
+    xr, nwr, cwr = (t.clone().requires_grad_() for t in (x, nw, cw))
+    hr = fm.rmsnorm(xr, nwr, 1e-5)
+    ur = fm.causal_conv(hr, cwr)
+    ((du * ur).sum() + (dhv * hr).sum()).backward()
+    dx_ref = xr.grad + dres
+    xd, nwd, cwd = (t.float().cuda().contiguous() for t in (x, nw, cw.reshape(D, Kc)))
+    dud, dhvd, dresd = (t.float().cuda().contiguous() for t in (du, dhv, dres))
+    s = nat.stream_of(xd)
+    h = torch.empty(B, T, D, device="cuda")
+    u = torch.empty(B, T, D, device="cuda")
+    rstd = torch.empty(B, T, device="cuda")
+    call("ulm_norm_conv_fwd", ptr(xd), nat.ULM_F32, ptr(nwd), ptr(cwd), Kc, 1e-5, ptr(h), nat.ULM_F32, ptr(u),
+         nat.ULM_F32, ptr(rstd), B, T, D, s)
+    dx = torch.empty(B, T, D, device="cuda")
+    dnw = torch.empty(D, device="cuda")
+    dcw = torch.empty(D, Kc, device="cuda")
+    wsb = nat.lib().ulm_norm_conv_bwd_workspace_bytes(B, T, D, Kc)
+    assert wsb > 0
+    ws = torch.empty(wsb, device="cuda", dtype=torch.uint8)
+    call("ulm_norm_conv_bwd", ptr(xd), nat.ULM_F32, ptr(rstd), ptr(nwd), ptr(cwd), Kc, ptr(dud), nat.ULM_F32,
+         ptr(dhvd), nat.ULM_F32, ptr(dresd), ptr(dx), ptr(dnw), ptr(dcw), ptr(ws), wsb, B, T, D, s)
+    # in place on the residual gradient, and without the value-GEMM term
+    dx2 = dresd.clone()
+    dnw2 = torch.empty(D, device="cuda")
+    dcw2 = torch.empty(D, Kc, device="cuda")
+    call("ulm_norm_conv_bwd", ptr(xd), nat.ULM_F32, ptr(rstd), ptr(nwd), ptr(cwd), Kc, ptr(dud), nat.ULM_F32,
+         None, nat.ULM_F32, ptr(dx2), ptr(dx2), ptr(dnw2), ptr(dcw2), ptr(ws), wsb, B, T, D, s)
+    torch.cuda.synchronize()
+    errs = {"dx": rel(dx, dx_ref), "dnorm_w": rel(dnw, nwr.grad), "dconv_w": rel(dcw, cwr.grad.reshape(D, Kc))}
+    say(f"  rel errors {errs}")
+    assert max(errs.values()) < 1e-5, errs
+    # the second call: L = <du, u> only
+    xr2, nwr2, cwr2 = (t.clone().requires_grad_() for t in (x, nw, cw))
+    (du * fm.causal_conv(fm.rmsnorm(xr2, nwr2, 1e-5), cwr2)).sum().backward()
+    errs2 = {"dx": rel(dx2, xr2.grad + dres), "dnorm_w": rel(dnw2, nwr2.grad),
+             "dconv_w": rel(dcw2, cwr2.grad.reshape(D, Kc))}
+    say(f"  in place, no dhv: rel errors {errs2}")
+    assert max(errs2.values()) < 1e-5, errs2
+
+
+BLOCK_CASES = [
+    # B, T, D, A, autocast
+    (2, 200, 64, 140, False),     # the reference test's shape (test_all.py:140-154)
+    (2, 200, 64, 140, True),
+    (1, 70, 96, 320, False),      # A, D multiples of 32: the K-group products
+    (2, 256, 128, 256, True),
+    (1, 512, 768, 3072, True),    # 110M block shape
+]
+
+
+def _head_loss(out, head, targets):
+    """Cross-entropy of a fixed classifier over the block output: the upstream
+    gradient has the structure of a training step (UnifiedLM.forward,
+    model.py:149-162) rather than white noise, whose random signs the scalar
+    gradients (log_eps, log_rate) would sum with heavy cancellation."""
+    return torch.nn.functional.cross_entropy((out @ head.t()).reshape(-1, head.shape[0]), targets.reshape(-1))
+
+
+@pytest.mark.parametrize("B,T,D,A,autocast", BLOCK_CASES)
+def test_block_matches_oracle(B, T, D, A, autocast):
+    say(f"UnifiedBlock fwd+bwd B={B} T={T} D={D} A={A} autocast={autocast}")
+    model = tiny_model(seed=T + A, dim=D, hidden_dim=A, n_layers=1, vocab_size=97, max_seq_len=max(T, 64))
+    blk = model.layers[0]
+    gen = torch.Generator().manual_seed(A)
+    with torch.no_grad():
+        blk.norm.weight.copy_(1.0 + 0.2 * torch.randn(D, generator=gen))
+    blk = blk.cuda().train()
+    x = torch.randn(B, T, D, generator=gen)
+    head = torch.randn(97, D, generator=gen, dtype=torch.float64) / D ** 0.5
+    targets = torch.randint(0, 97, (B, T), generator=gen)
+    xg = x.cuda().requires_grad_()
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        out = blk(xg)
+    _head_loss(out, head.float().cuda(), targets.cuda()).backward()
+    torch.cuda.synchronize()
+    p = {n: t.detach().double().cpu().requires_grad_() for n, t in blk.named_parameters()}
+    xr = x.double().requires_grad_()
+    ref = fm.block_forward(p, "", xr, norm_eps=blk.norm.eps)
+    _head_loss(ref, head, targets).backward()
+    errs = {"out": rel(out, ref), "dx": rel(xg.grad, xr.grad)}
+    for n, t in blk.named_parameters():
+        errs[n] = rel(t.grad, p[n].grad)
+    say(f"  worst {max(errs.values()):.3e}: {errs}")
+    # test_all.py:157-166 holds loss and every gradient to 1e-2 in fp32. Under
+    # bf16 autocast the reference documents the decay gradient dlam at up to
+    # 1.7e-2 operator-level (docs/kernel.md:32): log_rate gets 2e-2 there.
+    tol = {n: 2e-2 if (autocast and n == "log_rate") else 1e-2 for n in errs}
+    assert all(errs[n] < tol[n] for n in errs), errs

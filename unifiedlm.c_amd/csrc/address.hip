@@ -8,147 +8,234 @@
 //   dpre_a = 2 relu(pre_a + b_a) (dr_a - rho) / denom
 //   dbias  = sum over rows of dpre,   dlog_eps = -sum_rows rho / denom * exp(log_eps) [inside the clamp]
 //
-// Layout: one 256-thread block owns a group of rows, each thread a fixed set of
-// columns (a = tid + 256 j), so loads are coalesced along the slot index and
-// the per-row sums need one block reduction for kRowGroup rows at a time. The
-// pass over HBM is bound by bandwidth: fwd moves sizeof(pre) + 4 bytes per
-// element, bwd 2*4 + 2*sizeof(pre).
+// Layout: one wave per row, each lane 4 consecutive slots per step (16-byte
+// fp32 and 8-byte 16-bit accesses, coalesced along the slot index), so the
+// per-row sums are wave reductions with no block barrier. The pass over HBM is
+// bound by bandwidth: fwd moves sizeof(pre) + 4 bytes per element, bwd
+// 2*4 + 2*sizeof(pre); each row's second read is served by the cache.
 #include "ulm_common.h"
 
 namespace ulm {
 
-constexpr int kRowGroup = 8;     // rows reduced together
-constexpr int kFwdRows = 8;      // rows per block, forward
-constexpr int kBwdRows = 64;     // rows per block, backward (amortises the dbias partial)
+constexpr int kFwdRowsPerWave = 2;
+constexpr int kBwdRowsPerWave = 8;   // amortises the per-block dbias partial row
+constexpr int kAddrWaves = 4;
+constexpr int kAddrSplit = 32;       // first-level row ranges of the dbias column sum
 
-template <typename T> __device__ __forceinline__ float ld(const T *p, size_t i);
-template <> __device__ __forceinline__ float ld<float>(const float *p, size_t i) { return p[i]; }
-template <> __device__ __forceinline__ float ld<uint16_t>(const uint16_t *p, size_t i) { return bf16_to_f32(p[i]); }
-template <> __device__ __forceinline__ float ld<_Float16>(const _Float16 *p, size_t i) { return static_cast<float>(p[i]); }
-
-template <typename T> __device__ __forceinline__ void st(T *p, size_t i, float v);
-template <> __device__ __forceinline__ void st<float>(float *p, size_t i, float v) { p[i] = v; }
-template <> __device__ __forceinline__ void st<uint16_t>(uint16_t *p, size_t i, float v) { p[i] = f32_to_bf16_bits(v); }
-template <> __device__ __forceinline__ void st<_Float16>(_Float16 *p, size_t i, float v) { p[i] = static_cast<_Float16>(v); }
-
-// Sums kRowGroup per-thread values over the 256-thread block.
-__device__ __forceinline__ void block_sum_group(float (&v)[kRowGroup], float (*red)[kRowGroup]) {
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+// Loads and stores of W consecutive elements (W = 4: one 16-byte fp32 or
+// 8-byte 16-bit access; W = 1: scalar, for A % 4 != 0).
+template <typename T, int W> struct Vec;
+template <int W> struct Vec<float, W> {
+    static __device__ __forceinline__ void ld(const float *p, size_t i, float (&v)[W]) {
+        if constexpr (W == 4) {
+            const float4 x = *reinterpret_cast<const float4 *>(p + i);
+            v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
+        } else {
+            v[0] = p[i];
+        }
+    }
+    static __device__ __forceinline__ void st(float *p, size_t i, const float (&v)[W]) {
+        if constexpr (W == 4) *reinterpret_cast<float4 *>(p + i) = make_float4(v[0], v[1], v[2], v[3]);
+        else p[i] = v[0];
+    }
+};
+template <int W> struct Vec<uint16_t, W> {
+    static __device__ __forceinline__ void ld(const uint16_t *p, size_t i, float (&v)[W]) {
+        if constexpr (W == 4) {
+            const uint2 x = *reinterpret_cast<const uint2 *>(p + i);
+            v[0] = __uint_as_float(x.x << 16), v[1] = __uint_as_float(x.x & 0xffff0000u);
+            v[2] = __uint_as_float(x.y << 16), v[3] = __uint_as_float(x.y & 0xffff0000u);
+        } else {
+            v[0] = bf16_to_f32(p[i]);
+        }
+    }
+    static __device__ __forceinline__ void st(uint16_t *p, size_t i, const float (&v)[W]) {
+        if constexpr (W == 4) {
+            const uint32_t a = f32_to_bf16_bits(v[0]) | (static_cast<uint32_t>(f32_to_bf16_bits(v[1])) << 16);
+            const uint32_t b = f32_to_bf16_bits(v[2]) | (static_cast<uint32_t>(f32_to_bf16_bits(v[3])) << 16);
+            *reinterpret_cast<uint2 *>(p + i) = make_uint2(a, b);
+        } else {
+            p[i] = f32_to_bf16_bits(v[0]);
+        }
+    }
+};
+template <int W> struct Vec<_Float16, W> {
+    static __device__ __forceinline__ void ld(const _Float16 *p, size_t i, float (&v)[W]) {
 #pragma unroll
-    for (int i = 0; i < kRowGroup; ++i) v[i] = wave_sum(v[i]);
-    __syncthreads();
-    if (lane == 0)
-        for (int i = 0; i < kRowGroup; ++i) red[wave][i] = v[i];
-    __syncthreads();
+        for (int k = 0; k < W; ++k) v[k] = static_cast<float>(p[i + k]);
+    }
+    static __device__ __forceinline__ void st(_Float16 *p, size_t i, const float (&v)[W]) {
 #pragma unroll
-    for (int i = 0; i < kRowGroup; ++i) v[i] = red[0][i] + red[1][i] + red[2][i] + red[3][i];
-}
+        for (int k = 0; k < W; ++k) p[i + k] = static_cast<_Float16>(v[k]);
+    }
+};
 
 __device__ __forceinline__ float eps_of(const float *log_eps) {
     return __expf(fminf(fmaxf(log_eps[0], -10.f), 10.f));
 }
 
-template <typename T>
-__global__ __launch_bounds__(256) void addr_fwd_kernel(const T *__restrict__ pre, const float *__restrict__ bias,
-                                                       const float *__restrict__ log_eps, float *__restrict__ r,
-                                                       float *__restrict__ denom, int M, int A) {
-    __shared__ float red[4][kRowGroup];
-    const float E = eps_of(log_eps);
-    const int row0 = blockIdx.x * kFwdRows;
-    for (int rg = row0; rg < row0 + kFwdRows && rg < M; rg += kRowGroup) {
-        float s[kRowGroup];
+// z = relu(pre + bias) for W columns at a
+template <typename T, int W>
+__device__ __forceinline__ void relu_row(const T *pre, const float *bias, size_t base, int a, float (&p)[W]) {
+    Vec<T, W>::ld(pre, base + a, p);
+    float b[W];
+    if (bias) Vec<float, W>::ld(bias, a, b);
 #pragma unroll
-        for (int i = 0; i < kRowGroup; ++i) {
-            s[i] = 0.f;
-            const int row = rg + i;
-            if (row >= M) continue;
-            const size_t base = static_cast<size_t>(row) * A;
-            for (int a = threadIdx.x; a < A; a += 256) {
-                float p = ld(pre, base + a) + (bias ? bias[a] : 0.f);
-                p = p > 0.f ? p : 0.f;
-                s[i] += p * p;
-            }
-        }
-        block_sum_group(s, red);
-#pragma unroll
-        for (int i = 0; i < kRowGroup; ++i) {
-            const int row = rg + i;
-            if (row >= M) continue;
-            const float dn = E + s[i];
-            const size_t base = static_cast<size_t>(row) * A;
-            for (int a = threadIdx.x; a < A; a += 256) {
-                float p = ld(pre, base + a) + (bias ? bias[a] : 0.f);
-                p = p > 0.f ? p : 0.f;
-                r[base + a] = (p * p) / dn;
-            }
-            if (threadIdx.x == 0) denom[row] = dn;
-        }
+    for (int k = 0; k < W; ++k) {
+        const float x = p[k] + (bias ? b[k] : 0.f);
+        p[k] = x > 0.f ? x : 0.f;
     }
 }
 
-// Writes dpre and, per block, the partial column sums of dpre (dbias) and the
-// partial dlog_eps; addr_reduce_kernel sums the partials in a fixed order.
-template <typename T>
-__global__ __launch_bounds__(256) void addr_bwd_kernel(const T *__restrict__ pre, const float *__restrict__ bias,
-                                                       const float *__restrict__ log_eps, const float *__restrict__ r,
-                                                       const float *__restrict__ denom, const float *__restrict__ dr,
-                                                       T *__restrict__ dpre, float *__restrict__ dbias_part,
-                                                       float *__restrict__ dle_part, int M, int A) {
-    extern __shared__ float sdb[];   // A column partials
-    __shared__ float red[4][kRowGroup];
-    for (int a = threadIdx.x; a < A; a += 256) sdb[a] = 0.f;
+// One wave per row: the row sum of z^2 by a wave reduction, then r written
+// with the row's second read of pre served by the cache.
+template <typename T, int W>
+__global__ __launch_bounds__(kAddrWaves * 64) void addr_fwd_kernel(const T *__restrict__ pre,
+                                                                   const float *__restrict__ bias,
+                                                                   const float *__restrict__ log_eps,
+                                                                   float *__restrict__ r, float *__restrict__ denom,
+                                                                   int M, int A) {
+    const float E = eps_of(log_eps);
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int row0 = (blockIdx.x * kAddrWaves + wave) * kFwdRowsPerWave;
+    for (int row = row0; row < row0 + kFwdRowsPerWave && row < M; ++row) {
+        const size_t base = static_cast<size_t>(row) * A;
+        float ss = 0.f;
+#pragma unroll 4
+        for (int a = W * lane; a < A; a += W * kWave) {
+            float p[W];
+            relu_row<T, W>(pre, bias, base, a, p);
+#pragma unroll
+            for (int k = 0; k < W; ++k) ss += p[k] * p[k];
+        }
+        const float dn = E + wave_sum(ss);
+        const float inv = 1.f / dn;
+#pragma unroll 4
+        for (int a = W * lane; a < A; a += W * kWave) {
+            float p[W];
+            relu_row<T, W>(pre, bias, base, a, p);
+#pragma unroll
+            for (int k = 0; k < W; ++k) p[k] = (p[k] * p[k]) * inv;
+            Vec<float, W>::st(r, base + a, p);
+        }
+        if (lane == 0) denom[row] = dn;
+    }
+}
+
+// One wave per row: rho = sum_a dr r by a wave reduction, then dpre. Each wave
+// keeps its dbias column partials in its own LDS row; the block writes their
+// sum as one partial row, and the dlog_eps partial.
+template <typename T, int W>
+__global__ __launch_bounds__(kAddrWaves * 64) void addr_bwd_kernel(const T *__restrict__ pre,
+                                                                   const float *__restrict__ bias,
+                                                                   const float *__restrict__ log_eps,
+                                                                   const float *__restrict__ r,
+                                                                   const float *__restrict__ denom,
+                                                                   const float *__restrict__ dr,
+                                                                   T *__restrict__ dpre, float *__restrict__ dbias_part,
+                                                                   float *__restrict__ dle_part, int M, int A) {
+    extern __shared__ __align__(16) float sdb[];   // [kAddrWaves][A]
+    __shared__ float dle_w[kAddrWaves];
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    float *const mine = sdb + static_cast<size_t>(wave) * A;
+    for (int a = lane; a < A; a += kWave) mine[a] = 0.f;
     const float E = eps_of(log_eps);
     float dle = 0.f;
-    const int row0 = blockIdx.x * kBwdRows;
-    for (int rg = row0; rg < row0 + kBwdRows && rg < M; rg += kRowGroup) {
-        float rho[kRowGroup];
+    const int row0 = (blockIdx.x * kAddrWaves + wave) * kBwdRowsPerWave;
+    for (int row = row0; row < row0 + kBwdRowsPerWave && row < M; ++row) {
+        const size_t base = static_cast<size_t>(row) * A;
+        float rho = 0.f;
+#pragma unroll 4
+        for (int a = W * lane; a < A; a += W * kWave) {
+            float x[W], y[W];
+            Vec<float, W>::ld(dr, base + a, x);
+            Vec<float, W>::ld(r, base + a, y);
 #pragma unroll
-        for (int i = 0; i < kRowGroup; ++i) {
-            rho[i] = 0.f;
-            const int row = rg + i;
-            if (row >= M) continue;
-            const size_t base = static_cast<size_t>(row) * A;
-            for (int a = threadIdx.x; a < A; a += 256) rho[i] += dr[base + a] * r[base + a];
+            for (int k = 0; k < W; ++k) rho += x[k] * y[k];
         }
-        block_sum_group(rho, red);
+        rho = wave_sum(rho);
+        const float inv = 1.f / denom[row];
+#pragma unroll 4
+        for (int a = W * lane; a < A; a += W * kWave) {
+            float p[W], x[W], acc[W];
+            relu_row<T, W>(pre, bias, base, a, p);
+            Vec<float, W>::ld(dr, base + a, x);
+            Vec<float, W>::ld(mine, a, acc);
 #pragma unroll
-        for (int i = 0; i < kRowGroup; ++i) {
-            const int row = rg + i;
-            if (row >= M) continue;
-            const float dn = denom[row];
-            const size_t base = static_cast<size_t>(row) * A;
-            for (int a = threadIdx.x; a < A; a += 256) {
-                float p = ld(pre, base + a) + (bias ? bias[a] : 0.f);
-                p = p > 0.f ? p : 0.f;
-                const float g = 2.f * p * (dr[base + a] - rho[i]) / dn;
-                st(dpre, base + a, g);
-                sdb[a] += g;
+            for (int k = 0; k < W; ++k) {
+                p[k] = 2.f * p[k] * (x[k] - rho) * inv;
+                acc[k] += p[k];
             }
-            dle += -rho[i] / dn;
+            Vec<T, W>::st(dpre, base + a, p);
+            Vec<float, W>::st(mine, a, acc);
         }
+        dle -= rho * inv;
     }
+    if (lane == 0) dle_w[wave] = dle;
     __syncthreads();
-    for (int a = threadIdx.x; a < A; a += 256) dbias_part[static_cast<size_t>(blockIdx.x) * A + a] = sdb[a];
+    for (int a = threadIdx.x; a < A; a += kAddrWaves * kWave) {
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < kAddrWaves; ++w) sum += sdb[static_cast<size_t>(w) * A + a];
+        dbias_part[static_cast<size_t>(blockIdx.x) * A + a] = sum;
+    }
     if (threadIdx.x == 0) {
         const float le = log_eps[0];
-        dle_part[blockIdx.x] = (le > -10.f && le < 10.f) ? dle * E : 0.f;
+        const float d = dle_w[0] + dle_w[1] + dle_w[2] + dle_w[3];
+        dle_part[blockIdx.x] = (le > -10.f && le < 10.f) ? d * E : 0.f;
     }
 }
 
-__global__ __launch_bounds__(256) void addr_reduce_kernel(const float *__restrict__ dbias_part,
-                                                          const float *__restrict__ dle_part, float *__restrict__ dbias,
-                                                          float *__restrict__ dle, int nblk, int A) {
-    const int a = blockIdx.x * 256 + threadIdx.x;
-    if (dbias && a < A) {
-        float s = 0.f;
-        for (int k = 0; k < nblk; ++k) s += dbias_part[static_cast<size_t>(k) * A + a];
-        dbias[a] = s;
-    }
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        double s = 0.0;
-        for (int k = 0; k < nblk; ++k) s += dle_part[k];
-        dle[0] = static_cast<float>(s);
-    }
+// dlog_eps = sum of the per-block partials, in a fixed order
+__global__ void addr_dle_kernel(const float *__restrict__ dle_part, float *__restrict__ dle, int nblk) {
+    if (threadIdx.x != 0) return;
+    double s = 0.0;
+    for (int k = 0; k < nblk; ++k) s += dle_part[k];
+    dle[0] = static_cast<float>(s);
+}
+
+int addr_blocks(int M, int rows_per_wave) {
+    return (M + kAddrWaves * rows_per_wave - 1) / (kAddrWaves * rows_per_wave);
+}
+
+template <typename T>
+int launch_addr_fwd(const void *pre, const float *bias, const float *log_eps, float *r, float *denom, int M, int A,
+                    hipStream_t s) {
+    const int nblk = addr_blocks(M, kFwdRowsPerWave);
+    const bool vec = A % 4 == 0 && reinterpret_cast<uintptr_t>(pre) % (4 * sizeof(T)) == 0 &&
+                     reinterpret_cast<uintptr_t>(r) % 16 == 0 && reinterpret_cast<uintptr_t>(bias) % 16 == 0;
+    if (vec)
+        addr_fwd_kernel<T, 4><<<nblk, kAddrWaves * 64, 0, s>>>(static_cast<const T *>(pre), bias, log_eps, r, denom,
+                                                               M, A);
+    else
+        addr_fwd_kernel<T, 1><<<nblk, kAddrWaves * 64, 0, s>>>(static_cast<const T *>(pre), bias, log_eps, r, denom,
+                                                               M, A);
+    return check_launch("addr_fwd_kernel");
+}
+
+template <typename T>
+int launch_addr_bwd(const void *pre, const float *bias, const float *log_eps, const float *r, const float *denom,
+                    const float *dr, void *dpre, float *dbias_part, float *dle_part, int M, int A, hipStream_t s) {
+    const int nblk = addr_blocks(M, kBwdRowsPerWave);
+    const size_t lds = static_cast<size_t>(kAddrWaves) * A * sizeof(float);
+    const bool vec = A % 4 == 0 && reinterpret_cast<uintptr_t>(pre) % (4 * sizeof(T)) == 0 &&
+                     reinterpret_cast<uintptr_t>(dpre) % (4 * sizeof(T)) == 0 &&
+                     reinterpret_cast<uintptr_t>(r) % 16 == 0 && reinterpret_cast<uintptr_t>(dr) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(bias) % 16 == 0;
+    const void *fn = vec ? reinterpret_cast<const void *>(&addr_bwd_kernel<T, 4>)
+                         : reinterpret_cast<const void *>(&addr_bwd_kernel<T, 1>);
+    if (lds > 65536 && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) !=
+                           hipSuccess)
+        return check_launch("addr_bwd_kernel attribute");
+    if (vec)
+        addr_bwd_kernel<T, 4><<<nblk, kAddrWaves * 64, lds, s>>>(static_cast<const T *>(pre), bias, log_eps, r, denom,
+                                                                 dr, static_cast<T *>(dpre), dbias_part, dle_part, M,
+                                                                 A);
+    else
+        addr_bwd_kernel<T, 1><<<nblk, kAddrWaves * 64, lds, s>>>(static_cast<const T *>(pre), bias, log_eps, r, denom,
+                                                                 dr, static_cast<T *>(dpre), dbias_part, dle_part, M,
+                                                                 A);
+    return check_launch("addr_bwd_kernel");
 }
 
 }  // namespace ulm
@@ -161,56 +248,58 @@ extern "C" int ulm_addr_fwd(const void *pre, int pre_dtype, const float *bias, c
     ULM_REQUIRE(valid_dtype(pre_dtype), "ulm_addr_fwd: bad pre dtype %d", pre_dtype);
     ULM_REQUIRE(pre && log_eps && r && denom, "ulm_addr_fwd: null pointer");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid((M + kFwdRows - 1) / kFwdRows);
-    if (pre_dtype == ULM_F32)
-        addr_fwd_kernel<float><<<grid, 256, 0, s>>>(static_cast<const float *>(pre), bias, log_eps, r, denom, M, A);
-    else if (pre_dtype == ULM_BF16)
-        addr_fwd_kernel<uint16_t><<<grid, 256, 0, s>>>(static_cast<const uint16_t *>(pre), bias, log_eps, r, denom, M, A);
-    else
-        addr_fwd_kernel<_Float16><<<grid, 256, 0, s>>>(static_cast<const _Float16 *>(pre), bias, log_eps, r, denom, M, A);
-    return check_launch("addr_fwd_kernel");
+    if (pre_dtype == ULM_F32) return launch_addr_fwd<float>(pre, bias, log_eps, r, denom, M, A, s);
+    if (pre_dtype == ULM_BF16) return launch_addr_fwd<uint16_t>(pre, bias, log_eps, r, denom, M, A, s);
+    return launch_addr_fwd<_Float16>(pre, bias, log_eps, r, denom, M, A, s);
 }
+
+namespace {
+
+struct AddrWs {
+    float *dbias_part, *dle_part, *tmp;
+    size_t bytes;
+};
+
+AddrWs addr_ws(void *base, int M, int A) {
+    const size_t nblk = addr_blocks(M, kBwdRowsPerWave);
+    Carver c(base);
+    AddrWs w{};
+    w.dbias_part = c.take<float>(nblk * A);
+    w.dle_part = c.take<float>(nblk);
+    w.tmp = c.take<float>(static_cast<size_t>(kAddrSplit) * A);
+    w.bytes = c.off;
+    return w;
+}
+
+}  // namespace
 
 extern "C" size_t ulm_addr_bwd_workspace_bytes(int M, int A) {
     if (M <= 0 || A <= 0) return 0;
-    const size_t nblk = (M + kBwdRows - 1) / kBwdRows;
-    return align_up(nblk * A * sizeof(float), 256) + align_up(nblk * sizeof(float), 256);
+    return addr_ws(nullptr, M, A).bytes;
 }
 
 extern "C" int ulm_addr_bwd(const void *pre, int pre_dtype, const float *bias, const float *log_eps, const float *r,
                             const float *denom, const float *dr, void *dpre, float *dbias, float *dlog_eps,
                             void *workspace, size_t workspace_bytes, int M, int A, void *stream) {
     ULM_REQUIRE(M > 0 && A > 0, "ulm_addr_bwd: bad sizes M=%d A=%d", M, A);
-    ULM_REQUIRE(A <= 16384, "ulm_addr_bwd: A=%d exceeds the LDS column-partial limit 16384", A);
+    ULM_REQUIRE(A <= 8192, "ulm_addr_bwd: A=%d exceeds the LDS column-partial limit 8192", A);
     ULM_REQUIRE(valid_dtype(pre_dtype), "ulm_addr_bwd: bad pre dtype %d", pre_dtype);
     ULM_REQUIRE(pre && log_eps && r && denom && dr && dpre && dlog_eps, "ulm_addr_bwd: null pointer");
     ULM_REQUIRE(!bias || dbias, "ulm_addr_bwd: dbias is required when bias is given");
     ULM_REQUIRE(workspace && workspace_bytes >= ulm_addr_bwd_workspace_bytes(M, A),
                 "ulm_addr_bwd: workspace of %zu bytes, need %zu", workspace_bytes, ulm_addr_bwd_workspace_bytes(M, A));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int nblk = (M + kBwdRows - 1) / kBwdRows;
-    float *dbias_part = static_cast<float *>(workspace);
-    float *dle_part = reinterpret_cast<float *>(static_cast<char *>(workspace) +
-                                                align_up(static_cast<size_t>(nblk) * A * sizeof(float), 256));
-    const size_t lds = static_cast<size_t>(A) * sizeof(float);
-    if (lds > 65536) {
-        const void *fn = pre_dtype == ULM_F32    ? reinterpret_cast<const void *>(&addr_bwd_kernel<float>)
-                         : pre_dtype == ULM_BF16 ? reinterpret_cast<const void *>(&addr_bwd_kernel<uint16_t>)
-                                                 : reinterpret_cast<const void *>(&addr_bwd_kernel<_Float16>);
-        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
-            return check_launch("addr_bwd_kernel attribute");
-    }
+    const AddrWs ws = addr_ws(workspace, M, A);
+    const int nblk = addr_blocks(M, kBwdRowsPerWave);
+    int st;
     if (pre_dtype == ULM_F32)
-        addr_bwd_kernel<float><<<nblk, 256, lds, s>>>(static_cast<const float *>(pre), bias, log_eps, r, denom, dr,
-                                                      static_cast<float *>(dpre), dbias_part, dle_part, M, A);
+        st = launch_addr_bwd<float>(pre, bias, log_eps, r, denom, dr, dpre, ws.dbias_part, ws.dle_part, M, A, s);
     else if (pre_dtype == ULM_BF16)
-        addr_bwd_kernel<uint16_t><<<nblk, 256, lds, s>>>(static_cast<const uint16_t *>(pre), bias, log_eps, r, denom,
-                                                         dr, static_cast<uint16_t *>(dpre), dbias_part, dle_part, M, A);
+        st = launch_addr_bwd<uint16_t>(pre, bias, log_eps, r, denom, dr, dpre, ws.dbias_part, ws.dle_part, M, A, s);
     else
-        addr_bwd_kernel<_Float16><<<nblk, 256, lds, s>>>(static_cast<const _Float16 *>(pre), bias, log_eps, r, denom,
-                                                         dr, static_cast<_Float16 *>(dpre), dbias_part, dle_part, M, A);
-    int st = check_launch("addr_bwd_kernel");
+        st = launch_addr_bwd<_Float16>(pre, bias, log_eps, r, denom, dr, dpre, ws.dbias_part, ws.dle_part, M, A, s);
     if (st) return st;
-    addr_reduce_kernel<<<(A + 255) / 256, 256, 0, s>>>(dbias_part, dle_part, bias ? dbias : nullptr, dlog_eps, nblk, A);
-    return check_launch("addr_reduce_kernel");
+    if (bias) ULM_TRY(launch_column_sum(ws.dbias_part, nblk, A, ws.tmp, kAddrSplit, dbias, s));
+    addr_dle_kernel<<<1, 64, 0, s>>>(ws.dle_part, dlog_eps, nblk);
+    return check_launch("addr_dle_kernel");
 }

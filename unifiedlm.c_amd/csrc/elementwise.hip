@@ -38,4 +38,25 @@ int launch_convert(const void *src, int src_dt, void *dst, int dst_dt, size_t n,
     return check_launch("convert_kernel");
 }
 
+// out[c] = sum_r in[r * ncol + c] over rows r of [r0, r1) for split blockIdx.y
+// (rows split into gridDim.y contiguous ranges), written to out[blockIdx.y * ncol + c].
+__global__ __launch_bounds__(256) void column_sum_kernel(const float *__restrict__ in, size_t nrow, size_t ncol,
+                                                              float *__restrict__ out) {
+    const size_t c = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (c >= ncol) return;
+    const size_t per = (nrow + gridDim.y - 1) / gridDim.y;
+    const size_t r0 = blockIdx.y * per, r1 = min(nrow, r0 + per);
+    float s = 0.f;
+    for (size_t r = r0; r < r1; ++r) s += in[r * ncol + c];
+    out[blockIdx.y * ncol + c] = s;
+}
+
+int launch_column_sum(const float *in, size_t nrow, size_t ncol, float *tmp, int nsplit, float *out, hipStream_t s) {
+    const unsigned gx = static_cast<unsigned>((ncol + 256 - 1) / 256);
+    column_sum_kernel<<<dim3(gx, nsplit), 256, 0, s>>>(in, nrow, ncol, tmp);
+    ULM_TRY(check_launch("column_sum_kernel"));
+    column_sum_kernel<<<dim3(gx, 1), 256, 0, s>>>(tmp, nsplit, ncol, out);
+    return check_launch("column_sum_kernel");
+}
+
 }  // namespace ulm

@@ -17,7 +17,8 @@
 //    unless lam^64 < 2^-40, where f = 1. Without `scaled`, f = 1 and P_up is
 //    exactly P_lo^T in bf16: the products behind the d/dg identity (dq, dk)
 //    need their intra-chunk terms rounded identically on both sides.
-//  * partial_reduce: out = sum over nK fp32 partial outputs, in out's dtype.
+//  * partial_reduce: out = sum over nK fp32 partial outputs (plus an optional fp32
+//    residual), in out's dtype.
 #include "ulm_common.h"
 
 namespace ulm {
@@ -246,11 +247,19 @@ __global__ __launch_bounds__(kScoreWaves * 64) void scores_kernel(const uint16_t
 
 // out[i] = sum_k part[k * n + i], written in out's dtype
 __global__ __launch_bounds__(256) void partial_reduce_kernel(const float *__restrict__ part, int nK, size_t n,
+                                                             const float *__restrict__ resid,
                                                              void *__restrict__ out, int odt, bool vec) {
     const size_t n4 = vec ? n / 4 : 0;
     const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
     for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride) {
         float4 s = reinterpret_cast<const float4 *>(part)[i];
+        if (resid) {
+            const float4 x = reinterpret_cast<const float4 *>(resid)[i];
+            s.x += x.x;
+            s.y += x.y;
+            s.z += x.z;
+            s.w += x.w;
+        }
         for (int k = 1; k < nK; ++k) {
             const float4 x = reinterpret_cast<const float4 *>(part + k * n)[i];
             s.x += x.x;
@@ -269,8 +278,8 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(const float *__rest
     }
     // scalar tail (n % 4)
     for (size_t i = 4 * n4 + static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
-        float s = 0.f;
-        for (int k = 0; k < nK; ++k) s += part[k * n + i];
+        float s = part[i] + (resid ? resid[i] : 0.f);
+        for (int k = 1; k < nK; ++k) s += part[k * n + i];
         store_from_f32(out, i, odt, s);
     }
 }
@@ -305,14 +314,17 @@ int launch_chunk_scores(const uint16_t *aR, const uint16_t *aL, const uint16_t *
     return check_launch("chunk scores_kernel");
 }
 
-int launch_partial_reduce(const float *part, int nK, size_t n, void *out, int odt, hipStream_t s) {
+// out = sum of the nK partial rows of part (+ resid when not null), as odt.
+int launch_partial_reduce(const float *part, int nK, size_t n, void *out, int odt, hipStream_t s,
+                          const float *resid) {
     if (n == 0) return ULM_OK;
-    // float4 path when every partial row and the output are 16-byte aligned
+    // float4 path when every partial row, the residual and the output are 16-byte aligned
     const bool vec = n % 4 == 0 && reinterpret_cast<uintptr_t>(part) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(resid) % 16 == 0 &&
                      (odt != ULM_F32 || reinterpret_cast<uintptr_t>(out) % 16 == 0);
     size_t blocks = ((vec ? n / 4 : n) + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    chunks::partial_reduce_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(part, nK, n, out, odt, vec);
+    chunks::partial_reduce_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(part, nK, n, resid, out, odt, vec);
     return check_launch("partial_reduce_kernel");
 }
 

@@ -41,31 +41,18 @@ int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t 
                            uint16_t *xr_lo, int B, int T, int X, hipStream_t s);
 int launch_chunk_scores(const uint16_t *aR, const uint16_t *aL, const uint16_t *bR, const uint16_t *bL, const float *g,
                         uint16_t *Plo, uint16_t *Pup, int B, int T, int K, bool scaled, hipStream_t s);
-int launch_partial_reduce(const float *part, int nK, size_t n, void *out, int odt, hipStream_t s);
+int launch_partial_reduce(const float *part, int nK, size_t n, void *out, int odt, hipStream_t s,
+                          const float *resid = nullptr);
 // fm_stats.hip
 int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
                      uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, float *c_last, int B, int T,
-                     int A, hipStream_t s);
+                     int A, hipStream_t s, void *qw = nullptr, int qw_dt = ULM_BF16);
 size_t bwd_stats_partial_bytes(int B, int A);
 int launch_bwd_stats(const float *dqf, const float *dqo, const float *r, const float *nck,
                      const float *w, const float *g, const float *dkf, float *dr, float *dw, float *dg, void *part,
-                     int B, int T, int A, hipStream_t s);
+                     int B, int T, int A, hipStream_t s, const void *dqw = nullptr, int dqw_dt = ULM_BF16);
 
 namespace {
-
-// Carves consecutive 256-byte aligned regions out of a buffer; with a null
-// base it only measures.
-struct Carver {
-    char *base;
-    size_t off = 0;
-    explicit Carver(void *b) : base(static_cast<char *>(b)) {}
-    template <class T>
-    T *take(size_t count) {
-        T *p = base ? reinterpret_cast<T *>(base + off) : nullptr;
-        off += align_up(count * sizeof(T), 256);
-        return p;
-    }
-};
 
 size_t nt_of(int T) { return static_cast<size_t>((T + ULM_CHUNK - 1) / ULM_CHUNK); }
 
@@ -112,15 +99,16 @@ struct FwdWs {
     size_t bytes;
 };
 
-FwdWs fwd_layout(void *base, int B, int T, int A, int D, int fast_dtype) {
+// resid: the output is x + fast, so the products always go through fp32 partials
+FwdWs fwd_layout(void *base, int B, int T, int A, int D, int fast_dtype, bool resid = false) {
     const size_t NT = nt_of(T), nd = static_cast<size_t>(B) * T * D;
     Carver c(base);
     FwdWs w{};
     if (fm_aligned(B, T, A, D)) {
         w.Pf = c.take<uint16_t>(B * NT * ULM_CHUNK * ULM_CHUNK);
         const int nkg = la_kgroup_groups(A);
-        if (nkg > 1 || fast_dtype != ULM_F32) w.part = c.take<float>(nkg * nd);
-    } else if (fast_dtype != ULM_F32) {
+        if (nkg > 1 || fast_dtype != ULM_F32 || resid) w.part = c.take<float>(nkg * nd);
+    } else if (fast_dtype != ULM_F32 || resid) {
         w.part = c.take<float>(nd);
     }
     w.bytes = c.off;
@@ -167,12 +155,6 @@ BwdWs bwd_layout(void *base, int B, int T, int A, int D, int dfast_dtype) {
 }  // namespace ulm
 
 using namespace ulm;
-
-#define ULM_TRY(x)              \
-    do {                        \
-        int _st = (x);          \
-        if (_st) return _st;    \
-    } while (0)
 
 // ---------------------------------------------------------------------------
 // bare chunked product
@@ -243,16 +225,19 @@ namespace {
 
 // The forward composite of ulm_fm_fwd; with state (B, D, A) and c_last (B, A)
 // (aligned shapes only) it also emits the decode state after position T-1.
-int fm_forward(const float *r, const void *v, int v_dtype, const float *g, const float *w, float *q, void *fast,
-               int fast_dtype, void *saved, void *workspace, float *state, float *c_last, int B, int T, int A, int D,
-               hipStream_t s) {
+// q (fp32) and qw (w q in qw_dt) are each optional; with resid (fp32 (B,T,D))
+// the output is resid + fast.
+int fm_forward(const float *r, const void *v, int v_dtype, const float *g, const float *w, float *q, void *qw,
+               int qw_dt, const float *resid, void *fast, int fast_dtype, void *saved, void *workspace, float *state,
+               float *c_last, int B, int T, int A, int D, hipStream_t s) {
     const Saved sv = saved_layout(saved, B, T, A, D, v_dtype);
-    const FwdWs ws = fwd_layout(workspace, B, T, A, D, fast_dtype);
+    const FwdWs ws = fwd_layout(workspace, B, T, A, D, fast_dtype, resid != nullptr);
     const size_t nf = static_cast<size_t>(B) * T * D;
     if (fm_aligned(B, T, A, D)) {
         const int nkg = la_kgroup_groups(A);
         float *acc = ws.part ? ws.part : static_cast<float *>(fast);
-        ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, sv.qR, sv.kR, sv.qQ, sv.kQ, sv.nck, c_last, B, T, A, s));
+        ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, sv.qR, sv.kR, sv.qQ, sv.kQ, sv.nck, c_last, B, T, A, s,
+                                 qw, qw_dt));
         ULM_TRY(launch_chunk_transpose(v, v_dtype, sv.vQ, sv.vQl, sv.vR, sv.vRl, B, T, D, s));
         ULM_TRY(launch_chunk_scores(sv.qR, nullptr, sv.kR, nullptr, g, ws.Pf, sv.Pdv, B, T, A, true, s));
         // fast = LA(q, k, v): update k^T v~ (v~ from the full-precision v), intra on
@@ -260,17 +245,17 @@ int fm_forward(const float *r, const void *v, int v_dtype, const float *g, const
         // is the decode state S (model.py:96-111).
         ULM_TRY(launch_la_kgroup(sv.qR, nullptr, sv.kQ, nullptr, sv.vQ, sv.vQl, ws.Pf, true, g, acc, state, B, T, A, D,
                                  false, false, s));
-        if (ws.part) ULM_TRY(launch_partial_reduce(ws.part, nkg, nf, fast, fast_dtype, s));
+        if (ws.part) ULM_TRY(launch_partial_reduce(ws.part, nkg, nf, fast, fast_dtype, s, resid));
         return ULM_OK;
     }
     if (state || c_last) return fail(ULM_ERR_UNSUPPORTED, "prefill state: A=%d and D=%d must be multiples of 32", A, D);
     ULM_TRY(launch_fwd_stats(r, w, g, q, sv.q16n, sv.k16n, nullptr, nullptr, nullptr, nullptr, sv.nck, nullptr, B, T, A,
-                             s));
+                             s, qw, qw_dt));
     ULM_TRY(launch_convert(v, v_dtype, sv.v16n, ULM_BF16, nf, s));
-    float *acc = fast_dtype == ULM_F32 ? static_cast<float *>(fast) : ws.part;
+    float *acc = ws.part ? ws.part : static_cast<float *>(fast);
     ULM_TRY(launch_fill_zero(acc, nf * sizeof(float), s));
     ULM_TRY(launch_la_generic(sv.q16n, sv.k16n, sv.v16n, g, acc, B, T, A, D, false, s));
-    if (fast_dtype != ULM_F32) ULM_TRY(launch_convert(acc, ULM_F32, fast, fast_dtype, nf, s));
+    if (ws.part) ULM_TRY(launch_partial_reduce(acc, 1, nf, fast, fast_dtype, s, resid));
     return ULM_OK;
 }
 
@@ -287,8 +272,8 @@ extern "C" int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const floa
     const size_t need = ulm_fm_fwd_workspace_bytes(B, T, A, D, fast_dtype);
     ULM_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), "ulm_fm_fwd: workspace of %zu bytes, need %zu",
                 workspace_bytes, need);
-    return fm_forward(r, v, v_dtype, g, w, q, fast, fast_dtype, saved, workspace, nullptr, nullptr, B, T, A, D,
-                      static_cast<hipStream_t>(stream));
+    return fm_forward(r, v, v_dtype, g, w, q, nullptr, ULM_F32, nullptr, fast, fast_dtype, saved, workspace, nullptr,
+                      nullptr, B, T, A, D, static_cast<hipStream_t>(stream));
 }
 
 // ---------------------------------------------------------------------------
@@ -313,8 +298,8 @@ extern "C" int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const 
     ULM_REQUIRE(workspace_bytes >= need, "ulm_fm_prefill: workspace of %zu bytes, need %zu", workspace_bytes, need);
     char *saved = static_cast<char *>(workspace);
     char *ws = saved + align_up(saved_layout(nullptr, B, T, A, D, v_dtype).bytes, 256);
-    return fm_forward(r, v, v_dtype, g, w, q, fast, fast_dtype, saved, ws, S, c_last, B, T, A, D,
-                      static_cast<hipStream_t>(stream));
+    return fm_forward(r, v, v_dtype, g, w, q, nullptr, ULM_F32, nullptr, fast, fast_dtype, saved, ws, S, c_last, B, T,
+                      A, D, static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D, int dfast_dtype) {
@@ -322,20 +307,13 @@ extern "C" size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D, int dfa
     return bwd_layout(nullptr, B, T, A, D, dfast_dtype).bytes;
 }
 
-extern "C" int ulm_fm_bwd(const float *r, const float *g, const float *w, const void *saved,
-                          size_t saved_bytes, int v_dtype, const void *dfast, int dfast_dtype, const float *dq_out,
-                          float *dr, void *dv, int dv_dtype, float *dg, float *dw, void *workspace,
-                          size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
-    ULM_REQUIRE(B > 0 && T > 0 && A > 0 && D > 0, "ulm_fm_bwd: bad sizes B=%d T=%d A=%d D=%d", B, T, A, D);
-    ULM_REQUIRE(valid_dtype(v_dtype) && valid_dtype(dfast_dtype) && valid_dtype(dv_dtype),
-                "ulm_fm_bwd: bad dtype %d/%d/%d", v_dtype, dfast_dtype, dv_dtype);
-    ULM_REQUIRE(r && g && w && saved && dfast && dr && dv && dg && dw, "ulm_fm_bwd: null pointer");
-    const size_t need_s = ulm_fm_saved_bytes(B, T, A, D, v_dtype);
-    ULM_REQUIRE(saved_bytes >= need_s, "ulm_fm_bwd: saved buffer of %zu bytes, need %zu", saved_bytes, need_s);
-    const size_t need = ulm_fm_bwd_workspace_bytes(B, T, A, D, dfast_dtype);
-    ULM_REQUIRE(workspace && workspace_bytes >= need, "ulm_fm_bwd: workspace of %zu bytes, need %zu",
-                workspace_bytes, need);
-    hipStream_t s = static_cast<hipStream_t>(stream);
+namespace {
+
+// The backward composite of ulm_fm_bwd (arguments checked by the caller); dqw
+// (d(w q) in dqw_dt, may be null) adds w dqw to dq_out and sum_t q dqw to dw.
+int fm_backward(const float *r, const float *g, const float *w, const void *saved, int v_dtype, const void *dfast,
+                int dfast_dtype, const float *dq_out, const void *dqw, int dqw_dt, float *dr, void *dv, int dv_dtype,
+                float *dg, float *dw, void *workspace, int B, int T, int A, int D, hipStream_t s) {
     const Saved sv = saved_layout(const_cast<void *>(saved), B, T, A, D, v_dtype);
     const BwdWs ws = bwd_layout(workspace, B, T, A, D, dfast_dtype);
     const size_t nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
@@ -377,5 +355,66 @@ extern "C" int ulm_fm_bwd(const float *r, const float *g, const float *w, const 
         ULM_TRY(launch_la_generic(sv.k16n, sv.q16n, do16, g, dv_acc, B, T, A, D, true, s));
         if (dv_dtype != ULM_F32) ULM_TRY(launch_convert(dv_acc, ULM_F32, dv, dv_dtype, nd, s));
     }
-    return launch_bwd_stats(ws.dqf, dq_out, r, sv.nck, w, g, ws.dkf, dr, dw, dg, ws.stats, B, T, A, s);
+    return launch_bwd_stats(ws.dqf, dq_out, r, sv.nck, w, g, ws.dkf, dr, dw, dg, ws.stats, B, T, A, s, dqw, dqw_dt);
+}
+
+}  // namespace
+
+extern "C" int ulm_fm_bwd(const float *r, const float *g, const float *w, const void *saved,
+                          size_t saved_bytes, int v_dtype, const void *dfast, int dfast_dtype, const float *dq_out,
+                          float *dr, void *dv, int dv_dtype, float *dg, float *dw, void *workspace,
+                          size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
+    ULM_REQUIRE(B > 0 && T > 0 && A > 0 && D > 0, "ulm_fm_bwd: bad sizes B=%d T=%d A=%d D=%d", B, T, A, D);
+    ULM_REQUIRE(valid_dtype(v_dtype) && valid_dtype(dfast_dtype) && valid_dtype(dv_dtype),
+                "ulm_fm_bwd: bad dtype %d/%d/%d", v_dtype, dfast_dtype, dv_dtype);
+    ULM_REQUIRE(r && g && w && saved && dfast && dr && dv && dg && dw, "ulm_fm_bwd: null pointer");
+    const size_t need_s = ulm_fm_saved_bytes(B, T, A, D, v_dtype);
+    ULM_REQUIRE(saved_bytes >= need_s, "ulm_fm_bwd: saved buffer of %zu bytes, need %zu", saved_bytes, need_s);
+    const size_t need = ulm_fm_bwd_workspace_bytes(B, T, A, D, dfast_dtype);
+    ULM_REQUIRE(workspace && workspace_bytes >= need, "ulm_fm_bwd: workspace of %zu bytes, need %zu",
+                workspace_bytes, need);
+    return fm_backward(r, g, w, saved, v_dtype, dfast, dfast_dtype, dq_out, nullptr, ULM_BF16, dr, dv, dv_dtype, dg, dw,
+                       workspace, B, T, A, D, static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// the fast memory inside UnifiedBlock.forward (model.py:77-85): the read-out
+// side emits w q for the mu GEMM and adds the residual to fast
+
+extern "C" size_t ulm_block_fm_fwd_workspace_bytes(int B, int T, int A, int D) {
+    if (B <= 0 || T <= 0 || A <= 0 || D <= 0) return 0;
+    return fwd_layout(nullptr, B, T, A, D, ULM_F32, true).bytes;
+}
+
+extern "C" int ulm_block_fm_fwd(const float *r, const void *v, int v_dtype, const float *g, const float *w, void *qw,
+                                int qw_dtype, const float *x, float *y, void *saved, size_t saved_bytes,
+                                void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
+    ULM_REQUIRE(B > 0 && T > 0 && A > 0 && D > 0, "ulm_block_fm_fwd: bad sizes B=%d T=%d A=%d D=%d", B, T, A, D);
+    ULM_REQUIRE(valid_dtype(v_dtype) && valid_dtype(qw_dtype), "ulm_block_fm_fwd: bad dtype %d/%d", v_dtype,
+                qw_dtype);
+    ULM_REQUIRE(r && v && g && w && qw && x && y && saved && workspace, "ulm_block_fm_fwd: null pointer");
+    ULM_REQUIRE(static_cast<const void *>(x) != static_cast<const void *>(y), "ulm_block_fm_fwd: y must not alias x");
+    const size_t need_s = ulm_fm_saved_bytes(B, T, A, D, v_dtype);
+    ULM_REQUIRE(saved_bytes >= need_s, "ulm_block_fm_fwd: saved buffer of %zu bytes, need %zu", saved_bytes, need_s);
+    const size_t need = ulm_block_fm_fwd_workspace_bytes(B, T, A, D);
+    ULM_REQUIRE(workspace_bytes >= need, "ulm_block_fm_fwd: workspace of %zu bytes, need %zu", workspace_bytes, need);
+    return fm_forward(r, v, v_dtype, g, w, nullptr, qw, qw_dtype, x, y, ULM_F32, saved, workspace, nullptr, nullptr, B,
+                      T, A, D, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ulm_block_fm_bwd(const float *r, const float *g, const float *w, const void *saved,
+                                size_t saved_bytes, int v_dtype, const void *dfast, int dfast_dtype, const void *dqw,
+                                int dqw_dtype, float *dr, void *dv, int dv_dtype, float *dg, float *dw,
+                                void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
+    ULM_REQUIRE(B > 0 && T > 0 && A > 0 && D > 0, "ulm_block_fm_bwd: bad sizes B=%d T=%d A=%d D=%d", B, T, A, D);
+    ULM_REQUIRE(valid_dtype(v_dtype) && valid_dtype(dfast_dtype) && valid_dtype(dv_dtype) && valid_dtype(dqw_dtype),
+                "ulm_block_fm_bwd: bad dtype %d/%d/%d/%d", v_dtype, dfast_dtype, dv_dtype, dqw_dtype);
+    ULM_REQUIRE(r && g && w && saved && dfast && dqw && dr && dv && dg && dw, "ulm_block_fm_bwd: null pointer");
+    const size_t need_s = ulm_fm_saved_bytes(B, T, A, D, v_dtype);
+    ULM_REQUIRE(saved_bytes >= need_s, "ulm_block_fm_bwd: saved buffer of %zu bytes, need %zu", saved_bytes, need_s);
+    const size_t need = ulm_fm_bwd_workspace_bytes(B, T, A, D, dfast_dtype);
+    ULM_REQUIRE(workspace && workspace_bytes >= need, "ulm_block_fm_bwd: workspace of %zu bytes, need %zu",
+                workspace_bytes, need);
+    return fm_backward(r, g, w, saved, v_dtype, dfast, dfast_dtype, nullptr, dqw, dqw_dtype, dr, dv, dv_dtype, dg, dw,
+                       workspace, B, T, A, D, static_cast<hipStream_t>(stream));
 }

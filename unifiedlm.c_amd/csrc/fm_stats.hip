@@ -9,6 +9,9 @@
 //   dg = sum_t (t - tau) [q dq_f + dc (c - w) - k dk_f - k dkc]_t   (any tau; tau = (T-1)/2)
 //   with the bf16 copies of q and k in the dq_f and dk_f terms (the values the
 //   chunked products used), so the pair terms cancel exactly between the sums.
+// The block's read-out x + mu(w q) (model.py:85) is served by two options: the
+// forward can write w q in the GEMM's dtype instead of q, and the backward can
+// take d(w q) for dq_out, adding w d(w q) to dq and sum_t q d(w q) to dw.
 //
 // Thread layout: a 256-thread block owns 64 slots of one batch row; thread
 // (slot s, segment j) holds 16 consecutive positions of each 64-position chunk,
@@ -30,12 +33,13 @@ __device__ __forceinline__ float pow_int(float x, int e) {
     return r;
 }
 
-// Outputs besides q and n_ckpt (each may be null): q16n, k16n natural bf16
+// Outputs besides n_ckpt (each may be null): q (fp32); qw = w q in qw_dt; q16n, k16n natural bf16
 // copies; qR, kR in the R layout and qQ, kQ in the Q layout (the chunked
 // kernel's operand tiles; A % 32 == 0); c_last = c at position T-1 (B, A), the
 // decode state after the sequence. Positions past T are zero in R and Q.
 __global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict__ r, const float *__restrict__ w,
                                                         const float *__restrict__ g, float *__restrict__ q,
+                                                        void *__restrict__ qw, int qw_dt,
                                                         uint16_t *__restrict__ q16n, uint16_t *__restrict__ k16n,
                                                         uint16_t *__restrict__ qR, uint16_t *__restrict__ kR,
                                                         uint16_t *__restrict__ qQ, uint16_t *__restrict__ kQ,
@@ -88,7 +92,8 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict_
                 if (c_last && t == T - 1) c_last[bs * A + a] = ct;
                 qb = f32_to_bf16_bits(qt);
                 kb = f32_to_bf16_bits(kv[i]);
-                q[o] = qt;
+                if (q) q[o] = qt;
+                if (qw) store_from_f32(qw, o, qw_dt, qt * wa);
                 if (q16n) {
                     q16n[o] = qb;
                     k16n[o] = kb;
@@ -135,7 +140,18 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict_
     }
 }
 
-__global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict__ dqf, const float *__restrict__ dqo,
+// The extra gradient of q, by template so that every load is a plain one:
+// XQ = 0 none, 1 dq_out fp32, 2/3/4 d(w q) as fp32/bf16/fp16.
+template <int XQ>
+__device__ __forceinline__ float load_xq(const void *p, size_t o) {
+    if constexpr (XQ == 1 || XQ == 2) return static_cast<const float *>(p)[o];
+    else if constexpr (XQ == 3) return bf16_to_f32(static_cast<const uint16_t *>(p)[o]);
+    else if constexpr (XQ == 4) return static_cast<float>(static_cast<const _Float16 *>(p)[o]);
+    else return 0.f;
+}
+
+template <int XQ>
+__global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict__ dqf, const void *__restrict__ xq,
                                                         const float *__restrict__ r,
                                                         const float *__restrict__ nck, const float *__restrict__ w,
                                                         const float *__restrict__ g, const float *__restrict__ dkf,
@@ -159,7 +175,7 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
     double dg_acc = 0.0;
     for (int n = NT - 1; n >= 0; --n) {
         const int t0 = n * ULM_CHUNK + j * kSeg;
-        float rv[kSeg], kv[kSeg], cv[kSeg], dq[kSeg], dc[kSeg], dqfv[kSeg];
+        float rv[kSeg], kv[kSeg], cv[kSeg], dq[kSeg], dc[kSeg], dqfv[kSeg], dqwv[kSeg];
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
             const int t = t0 + i;
@@ -167,7 +183,12 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
             const size_t o = (b * T + t) * A + a;
             rv[i] = ok ? r[o] : 0.f;
             dqfv[i] = ok ? dqf[o] : 0.f;
-            dq[i] = dqfv[i] + ((ok && dqo) ? dqo[o] : 0.f);
+            // an unconditional load (index 0 when out of range) keeps the 16-bit
+            // conversions out of a branch that would wait on each load
+            float x = XQ != 0 ? load_xq<XQ>(xq, ok ? o : 0) : 0.f;
+            x = ok ? x : 0.f;
+            dqwv[i] = XQ >= 2 ? x : 0.f;
+            dq[i] = dqfv[i] + (XQ == 1 ? x : wa * dqwv[i]);
         }
         kv[0] = (va && t0 >= 1 && t0 - 1 < T) ? r[(b * T + t0 - 1) * A + a] : 0.f;
 #pragma unroll
@@ -228,6 +249,7 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
                 const float nxt = (i + 1 < kSeg) ? dkt[i + 1] : after;
                 dr[(b * T + t) * A + a] = dq[i] / cv[i] + nxt;
                 dw_acc += dc[i];
+                if constexpr (XQ >= 2) dw_acc += rv[i] * dqwv[i];   // rv holds q
                 // The fast-read terms take the bf16 q and k that the dq and dk
                 // products contracted with, so each (t, s) pair enters both sums
                 // with the same value and the position weights cancel to t - s.
@@ -277,14 +299,14 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(const float *__restri
 // copies (all or none; A % 32 == 0).
 int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
                      uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, float *c_last, int B, int T,
-                     int A, hipStream_t s) {
+                     int A, hipStream_t s, void *qw, int qw_dt) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
     if ((q16n == nullptr) != (k16n == nullptr)) return fail(ULM_ERR_INVALID, "fwd stats: q16n and k16n go together");
     const bool tiled = qR || kR || qQ || kQ;
     if (tiled && !(qR && kR && qQ && kQ && A % 32 == 0))
         return fail(ULM_ERR_INVALID, "fwd stats: tiled copies need all four outputs and A %% 32 == 0");
-    fwd_stats_kernel<<<dim3((A + kSlots - 1) / kSlots, B), 256, 0, s>>>(r, w, g, q, q16n, k16n, qR, kR, qQ, kQ, nck,
-                                                                         c_last, T, A, NT);
+    fwd_stats_kernel<<<dim3((A + kSlots - 1) / kSlots, B), 256, 0, s>>>(r, w, g, q, qw, qw_dt, q16n, k16n, qR, kR, qQ,
+                                                                         kQ, nck, c_last, T, A, NT);
     return check_launch("fwd_stats_kernel");
 }
 
@@ -295,13 +317,23 @@ size_t bwd_stats_partial_bytes(int B, int A) {
 
 int launch_bwd_stats(const float *dqf, const float *dqo, const float *r, const float *nck,
                      const float *w, const float *g, const float *dkf, float *dr, float *dw, float *dg, void *part,
-                     int B, int T, int A, hipStream_t s) {
+                     int B, int T, int A, hipStream_t s, const void *dqw, int dqw_dt) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
     const int nb = (A + kSlots - 1) / kSlots;
     float *dw_part = static_cast<float *>(part);
     double *dg_part = reinterpret_cast<double *>(static_cast<char *>(part) +
                                                  align_up(static_cast<size_t>(B) * A * sizeof(float), 256));
-    bwd_stats_kernel<<<dim3(nb, B), 256, 0, s>>>(dqf, dqo, r, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT);
+    const int xq = dqw ? 2 + dqw_dt : (dqo ? 1 : 0);   // ULM_F32, ULM_BF16, ULM_F16 = 0, 1, 2
+    const void *xp = dqw ? dqw : static_cast<const void *>(dqo);
+    if (dqw && dqo) return fail(ULM_ERR_INVALID, "bwd stats: dq_out and d(w q) are exclusive");
+    switch (xq) {
+    case 0: bwd_stats_kernel<0><<<dim3(nb, B), 256, 0, s>>>(dqf, xp, r, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
+    case 1: bwd_stats_kernel<1><<<dim3(nb, B), 256, 0, s>>>(dqf, xp, r, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
+    case 2: bwd_stats_kernel<2><<<dim3(nb, B), 256, 0, s>>>(dqf, xp, r, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
+    case 3: bwd_stats_kernel<3><<<dim3(nb, B), 256, 0, s>>>(dqf, xp, r, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
+    case 4: bwd_stats_kernel<4><<<dim3(nb, B), 256, 0, s>>>(dqf, xp, r, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
+    default: return fail(ULM_ERR_INVALID, "bwd stats: bad d(w q) dtype %d", dqw_dt);
+    }
     int st = check_launch("bwd_stats_kernel");
     if (st) return st;
     stats_reduce_kernel<<<(A + 255) / 256, 256, 0, s>>>(dw_part, dg_part, dw, dg, B, A, B * nb);

@@ -149,5 +149,29 @@ inline bool valid_dtype(int dt) { return dt == ULM_F32 || dt == ULM_BF16 || dt =
 // Generic elementwise helpers (elementwise.hip).
 int launch_fill_zero(void *p, size_t bytes, hipStream_t s);
 int launch_convert(const void *src, int src_dt, void *dst, int dst_dt, size_t n, hipStream_t s);
+// out[c] = sum over the nrow rows of in (nrow x ncol fp32) in a fixed order:
+// nsplit contiguous row ranges into tmp (nsplit x ncol), then their sum.
+int launch_column_sum(const float *in, size_t nrow, size_t ncol, float *tmp, int nsplit, float *out, hipStream_t s);
+
+// Carves consecutive 256-byte aligned regions out of a buffer; with a null
+// base it only measures.
+struct Carver {
+    char *base;
+    size_t off = 0;
+    explicit Carver(void *b) : base(static_cast<char *>(b)) {}
+    template <class T>
+    T *take(size_t count) {
+        T *p = base ? reinterpret_cast<T *>(base + off) : nullptr;
+        off += align_up(count * sizeof(T), 256);
+        return p;
+    }
+};
 
 }  // namespace ulm
+
+// return a nonzero status from the enclosing function
+#define ULM_TRY(x)              \
+    do {                        \
+        int _st = (x);          \
+        if (_st) return _st;    \
+    } while (0)

@@ -175,6 +175,154 @@ def relu2_address(pre, bias, log_eps):
 
 
 # ---------------------------------------------------------------------------
+# UnifiedBlock.forward (model.py:77-85) with the fast memory and its
+# elementwise ends fused; the GEMMs are plain library GEMMs (hipBLASLt through
+# torch.mm) with fp32 accumulation
+
+def _mm(a, b, out_dtype):
+    """a @ b, written in out_dtype straight from the fp32 accumulator."""
+    return torch.mm(a, b) if a.dtype == out_dtype else torch.mm(a, b, out_dtype=out_dtype)
+
+
+def _addmm(c, a, b):
+    """c + a @ b with c fp32, accumulated in the GEMM's epilogue."""
+    return torch.addmm(c, a, b) if a.dtype == c.dtype else torch.addmm(c, a, b, out_dtype=c.dtype)
+
+
+class UnifiedBlockFn(torch.autograd.Function):
+    """out = x + mu(w q) + fast for one UnifiedBlock (model.py:77-85):
+
+        h, u   = RMSNorm(x), causal conv(h)            ulm_norm_conv_fwd
+        pre, v = u K^T, h W_v^T                         GEMMs in cdt
+        r      = relu^2 address(pre + b)                ulm_addr_fwd
+        wq, y  = w q, x + fast                          ulm_block_fm_fwd
+        out    = y + wq mu^T                            GEMM accumulating into y
+
+    cdt is the GEMM operand dtype: bf16 under bf16 autocast (the reference's
+    training configuration, train.py), fp32 otherwise. x is the fp32 residual
+    stream; every gradient is returned in fp32."""
+
+    @staticmethod
+    def forward(ctx, x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, g, w, norm_eps, cdt):
+        B, T, D = x.shape
+        A = key_w.shape[0]
+        Kc = conv_w.shape[-1]
+        M = B * T
+        dev = x.device
+        s = nat.stream_of(x)
+        cd = nat.dtype_code(cdt)
+        f32 = torch.float32
+        x32 = x.contiguous()
+        nw = norm_w.float().contiguous()
+        cw = conv_w.float().reshape(D, Kc).contiguous()
+        h = torch.empty(B, T, D, device=dev, dtype=cdt)
+        u = torch.empty(B, T, D, device=dev, dtype=cdt)
+        rstd = torch.empty(B, T, device=dev, dtype=f32)
+        call("ulm_norm_conv_fwd", ptr(x32), nat.ULM_F32, ptr(nw), ptr(cw), Kc, float(norm_eps), ptr(h), cd, ptr(u), cd,
+             ptr(rstd), B, T, D, s)
+        kw, vw, mw = (t.to(cdt).contiguous() for t in (key_w, val_w, mu_w))
+        pre = torch.mm(u.view(M, D), kw.t())
+        v = torch.mm(h.view(M, D), vw.t())
+        b32 = key_b.float().contiguous() if key_b is not None else None
+        le = log_eps.float().reshape(1).contiguous()
+        r = torch.empty(M, A, device=dev, dtype=f32)
+        denom = torch.empty(M, device=dev, dtype=f32)
+        call("ulm_addr_fwd", ptr(pre), cd, ptr(b32), ptr(le), ptr(r), ptr(denom), M, A, s)
+        g1 = g.float().reshape(1).contiguous()
+        w32 = w.float().contiguous()
+        saved_bytes = nat.lib().ulm_fm_saved_bytes(B, T, A, D, cd)
+        saved = torch.empty(saved_bytes, device=dev, dtype=torch.uint8)
+        ws_bytes = nat.lib().ulm_block_fm_fwd_workspace_bytes(B, T, A, D)
+        ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+        qw = torch.empty(M, A, device=dev, dtype=cdt)
+        y = torch.empty(M, D, device=dev, dtype=f32)
+        call("ulm_block_fm_fwd", ptr(r), ptr(v), cd, ptr(g1), ptr(w32), ptr(qw), cd, ptr(x32), ptr(y), ptr(saved),
+             saved_bytes, ptr(ws), ws_bytes, B, T, A, D, s)
+        del ws, v
+        out = _addmm(y, qw, mw.t())
+        ctx.save_for_backward(x32, rstd, nw, cw, h, u, pre, b32, le, r, denom, g1, w32, saved, qw, kw, vw, mw)
+        ctx.meta = (B, T, A, D, Kc, cdt, conv_w.shape, log_eps.shape, g.shape, key_b is not None)
+        return out.view(B, T, D)
+
+    @staticmethod
+    def backward(ctx, dout):
+        # the GEMM dtypes are explicit: no autocast re-casting in the backward
+        with torch.autocast("cuda", enabled=False):
+            return UnifiedBlockFn._backward(ctx, dout)
+
+    @staticmethod
+    def _backward(ctx, dout):
+        x32, rstd, nw, cw, h, u, pre, b32, le, r, denom, g1, w32, saved, qw, kw, vw, mw = ctx.saved_tensors
+        B, T, A, D, Kc, cdt, cw_shape, le_shape, g_shape, has_bias = ctx.meta
+        M = B * T
+        dev = x32.device
+        s = nat.stream_of(x32)
+        cd = nat.dtype_code(cdt)
+        f32 = torch.float32
+        dout = dout.float().contiguous()
+        if cdt == f32:
+            d16 = dout
+        else:
+            d16 = torch.empty(B, T, D, device=dev, dtype=cdt)
+            call("ulm_cast", ptr(dout), nat.ULM_F32, ptr(d16), cd, M * D, s)
+        d2 = d16.view(M, D)
+        dqw = torch.mm(d2, mw)                       # d(w q) = dout mu
+        dmu = _mm(d2.t(), qw, f32)
+        dr = torch.empty(M, A, device=dev, dtype=f32)
+        dv = torch.empty(M, D, device=dev, dtype=cdt)
+        dg = torch.empty(1, device=dev, dtype=f32)
+        dw = torch.empty(A, device=dev, dtype=f32)
+        ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D, cd)
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+        call("ulm_block_fm_bwd", ptr(r), ptr(g1), ptr(w32), ptr(saved), saved.numel(), cd, ptr(d16), cd, ptr(dqw), cd,
+             ptr(dr), ptr(dv), cd, ptr(dg), ptr(dw), ptr(ws), ws_bytes, B, T, A, D, s)
+        del ws, dqw
+        dpre = torch.empty_like(pre)
+        dbias = torch.empty(A, device=dev, dtype=f32) if has_bias else None
+        dle = torch.empty(1, device=dev, dtype=f32)
+        ws_bytes = nat.lib().ulm_addr_bwd_workspace_bytes(M, A)
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+        call("ulm_addr_bwd", ptr(pre), cd, ptr(b32), ptr(le), ptr(r), ptr(denom), ptr(dr), ptr(dpre), ptr(dbias),
+             ptr(dle), ptr(ws), ws_bytes, M, A, s)
+        del ws, dr
+        du = _mm(dpre, kw, f32)
+        dkey = _mm(dpre.t(), u.view(M, D), f32)
+        dhv = _mm(dv, vw, f32)
+        dval = _mm(dv.t(), h.view(M, D), f32)
+        dx = torch.empty(B, T, D, device=dev, dtype=f32)
+        dnw = torch.empty(D, device=dev, dtype=f32)
+        dcw = torch.empty(D, Kc, device=dev, dtype=f32)
+        ws_bytes = nat.lib().ulm_norm_conv_bwd_workspace_bytes(B, T, D, Kc)
+        if ws_bytes == 0:
+            raise ValueError(f"ulm_norm_conv_bwd: unsupported D={D}")
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+        call("ulm_norm_conv_bwd", ptr(x32), nat.ULM_F32, ptr(rstd), ptr(nw), ptr(cw), Kc, ptr(du), nat.ULM_F32, ptr(dhv),
+             nat.ULM_F32, ptr(dout), ptr(dx), ptr(dnw), ptr(dcw), ptr(ws), ws_bytes, B, T, D, s)
+        return (dx, dnw, dcw.view(cw_shape), dkey, dbias, dle.reshape(le_shape), dval, dmu, dg.reshape(g_shape), dw,
+                None, None)
+
+
+def unified_block(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, g, w, norm_eps, cdt=torch.float32):
+    """x + mu(w q) + fast of one UnifiedBlock (model.py:77-85) in one fused
+    forward and backward. x (B, T, D) fp32; key_w (A, D), mu_w (D, A),
+    val_w (D, D), conv_w (D, 1, Kc); g = -exp(log_rate), w = prior mass (A,)."""
+    if x.dim() != 3 or x.dtype != torch.float32:
+        raise ValueError(f"x must be (B, T, D) fp32, got {tuple(x.shape)} {x.dtype}")
+    B, T, D = x.shape
+    A = key_w.shape[0]
+    if B == 0 or T == 0 or D == 0:
+        raise ValueError(f"empty input {tuple(x.shape)}")
+    if key_w.shape != (A, D) or mu_w.shape != (D, A) or val_w.shape != (D, D) or w.shape != (A,):
+        raise ValueError("block weights disagree with x: key (A, D), mu (D, A), val (D, D), w (A,)")
+    if conv_w.numel() % D or not 1 <= conv_w.shape[-1] <= 8:
+        raise ValueError(f"conv_w must be (D, 1, Kc) with 1 <= Kc <= 8, got {tuple(conv_w.shape)}")
+    if cdt not in (torch.float32, torch.bfloat16, torch.float16):
+        raise ValueError(f"unsupported GEMM dtype {cdt}")
+    nat.require_device(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, g, w)
+    return UnifiedBlockFn.apply(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, g, w, norm_eps, cdt)
+
+
+# ---------------------------------------------------------------------------
 # per-token decode (model.py:96-111), N sequences at once, fp32
 
 @torch.no_grad()

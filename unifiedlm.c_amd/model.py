@@ -22,7 +22,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from kernel import CHUNK, decode_addr, decode_pre, decode_state, fm_prefill, relu2_address, unified_memory
+from kernel import (CHUNK, decode_addr, decode_pre, decode_state, fm_prefill, relu2_address, unified_block,
+                    unified_memory)
 
 
 @dataclass
@@ -85,6 +86,22 @@ class UnifiedBlock(nn.Module):
         return self.log_w.clamp(-7.0, 12.0).exp()
 
     def forward(self, x):
+        """model.py:77-85. One fused block (fast memory, RMSNorm + conv, address,
+        w q and the residual in native kernels around the library GEMMs) for an
+        fp32 residual stream; GEMM operands take the autocast dtype, as the
+        reference's bf16-autocast training step runs them (train.py)."""
+        if x.dtype != torch.float32 or (self.training and self.dropout.p > 0):
+            return self.forward_composed(x)
+        cdt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else torch.float32
+        with torch.autocast("cuda", enabled=False):
+            return unified_block(x, self.norm.weight, self.conv.weight, self.key.weight, self.key.bias,
+                                 self.log_eps, self.val.weight, self.mu.weight, -self.log_rate.exp(), self._w(),
+                                 self.norm.eps, cdt)
+
+    def forward_composed(self, x):
+        """The same block op by op (model.py:77-85): the fast memory and the
+        address in native kernels, the rest in torch; the path for dropout and
+        for a non-fp32 residual stream."""
         h = self.norm(x)
         u = self.conv(h.transpose(1, 2))[..., : h.size(1)].transpose(1, 2)
         r = self.code(u)

@@ -34,6 +34,13 @@ SIGNATURES = {
     "ulm_addr_fwd": (I, [P, I, P, P, P, P, I, I, P]),
     "ulm_addr_bwd_workspace_bytes": (SZ, [I, I]),
     "ulm_addr_bwd": (I, [P, I, P, P, P, P, P, P, P, P, P, SZ, I, I, P]),
+    "ulm_norm_conv_fwd": (I, [P, I, P, P, I, F, P, I, P, I, P, I, I, I, P]),
+    "ulm_norm_conv_bwd_workspace_bytes": (SZ, [I, I, I, I]),
+    "ulm_norm_conv_bwd": (I, [P, I, P, P, P, I, P, I, P, I, P, P, P, P, P, SZ, I, I, I, P]),
+    "ulm_block_fm_fwd_workspace_bytes": (SZ, [I, I, I, I]),
+    "ulm_block_fm_fwd": (I, [P, P, I, P, P, P, I, P, P, P, SZ, P, SZ, I, I, I, I, P]),
+    "ulm_block_fm_bwd": (I, [P, P, P, P, SZ, I, P, I, P, I, P, P, I, P, P, P, SZ, I, I, I, I, P]),
+    "ulm_cast": (I, [P, I, P, I, SZ, P]),
     "ulm_decode_pre": (I, [P, P, P, P, P, P, I, I, I, F, P]),
     "ulm_decode_addr": (I, [P, P, P, P, P, P, P, P, P, P, I, I, P]),
     "ulm_decode_state": (I, [P, P, P, P, P, P, P, P, I, I, I, P]),

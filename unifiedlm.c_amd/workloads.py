@@ -81,6 +81,13 @@ def la_flops(B, T, K, V, chunk=64):
     return B * T * (4 * K * V + 2 * chunk * (K + V))
 
 
+def block_flops_per_token(T, A, D, chunk=64):
+    """Algorithmic flops of one UnifiedBlock per token, forward + backward: the
+    key, value and mu GEMMs (2AD + 2D^2 + 2AD forward, twice that backward) and
+    the four chunked fast-memory products, 16AD + 8C(A + D)."""
+    return 3 * (4 * A * D + 2 * D * D) + 16 * A * D + 8 * chunk * (A + D)
+
+
 def la_kernel_flops(B, T, K, V, chunk=64):
     """Algorithmic flops of one launch of the K-group chunked kernel: state
     update 2KV, read-out 2KV and intra apply 2CV per token. The intra scores

@@ -195,6 +195,16 @@ int ulm_block_fm_bwd(const float *r, const float *g, const float *w, const void 
                      float *dw, void *workspace, size_t workspace_bytes, int B, int T, int A, int D,
                      void *stream);
 
+/* Weight gradient of a linear layer over the token dimension: C = A^T B, i.e.
+ * C[i][j] = sum_k A[k][i] B[k][j], A (K,N1) and B (K,N2) bf16 row-major,
+ * C (N1,N2) fp32 out. The backward of F.linear's weight under bf16 autocast
+ * (model.py:64-68: key, val, mu), with K = batch x positions. N1 and N2
+ * multiples of 8, A and B 16-byte aligned; split over K, summed in a fixed
+ * order. Workspace of ulm_wgrad_workspace_bytes() bytes (may be 0). */
+size_t ulm_wgrad_workspace_bytes(int K, int N1, int N2);
+int ulm_wgrad(const void *a, const void *b, float *c, int K, int N1, int N2, void *workspace,
+              size_t workspace_bytes, void *stream);
+
 /* dst = src converted elementwise (n elements; F32/BF16/F16, bf16 rounding to
  * nearest even): the autocast casts around the block's GEMMs. */
 int ulm_cast(const void *src, int src_dtype, void *dst, int dst_dtype, size_t n, void *stream);

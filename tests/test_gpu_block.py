@@ -159,3 +159,36 @@ def test_block_matches_oracle(B, T, D, A, autocast):
     # 1.7e-2 operator-level (docs/kernel.md:32): log_rate gets 2e-2 there.
     tol = {n: 2e-2 if (autocast and n == "log_rate") else 1e-2 for n in errs}
     assert all(errs[n] < tol[n] for n in errs), errs
+
+
+WGRAD_CASES = [
+    # K, N1, N2
+    (1000, 200, 136),      # ragged K chunk and partial tiles on both sides
+    (64, 8, 16),           # one k-step, tiny tiles
+    (4096, 768, 768),      # value projection shape
+    (16384, 768, 3072),    # mu weight gradient at the 110M shape
+    (16384, 3072, 768),    # key weight gradient at the 110M shape
+]
+
+
+@pytest.mark.parametrize("K,N1,N2", WGRAD_CASES)
+def test_wgrad_matches_fp32_product(K, N1, N2):
+    """C = A^T B against the fp32 product of the same bf16 operands (float64
+    on the CPU for the small cases)."""
+    say(f"ulm_wgrad K={K} N1={N1} N2={N2}")
+    gen = torch.Generator().manual_seed(K + N1)
+    a = torch.randn(K, N1, generator=gen).to(torch.bfloat16)
+    b = torch.randn(K, N2, generator=gen).to(torch.bfloat16)
+    ad, bd = a.cuda(), b.cuda()
+    c = torch.empty(N1, N2, device="cuda")
+    wsb = nat.lib().ulm_wgrad_workspace_bytes(K, N1, N2)
+    ws = torch.empty(max(wsb, 1), device="cuda", dtype=torch.uint8)
+    call("ulm_wgrad", ptr(ad), ptr(bd), ptr(c), K, N1, N2, ptr(ws), wsb, nat.stream_of(ad))
+    torch.cuda.synchronize()
+    if K * N1 * N2 <= 1 << 28:
+        ref = a.double().t() @ b.double()
+    else:
+        ref = (ad.double().t() @ bd.double()).cpu()
+    err = rel(c, ref)
+    say(f"  rel error {err:.2e}")
+    assert err < 1e-5

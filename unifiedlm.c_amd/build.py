@@ -20,7 +20,7 @@ LIB = os.path.join(HERE, "libulm_fm.so")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 
 SOURCES = ["status.hip", "elementwise.hip", "decode.hip", "address.hip", "fm_stats.hip", "fm_chunk.hip",
-           "fm_chunks.hip", "la_kgroup.hip", "fm_ops.hip", "block.hip", "probe.hip"]
+           "fm_chunks.hip", "la_kgroup.hip", "fm_ops.hip", "block.hip", "wgrad.hip", "probe.hip"]
 ARCH = "gfx950"
 FLAGS = [f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-munsafe-fp-atomics",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -186,12 +186,14 @@ __global__ __launch_bounds__(kAddrWaves * 64) void addr_bwd_kernel(const T *__re
     }
 }
 
-// dlog_eps = sum of the per-block partials, in a fixed order
-__global__ void addr_dle_kernel(const float *__restrict__ dle_part, float *__restrict__ dle, int nblk) {
-    if (threadIdx.x != 0) return;
+// dlog_eps = sum of the per-block partials in a fixed order (lane-strided
+// partial sums, then the fixed shuffle tree of one wave)
+__global__ __launch_bounds__(64) void addr_dle_kernel(const float *__restrict__ dle_part, float *__restrict__ dle,
+                                                      int nblk) {
     double s = 0.0;
-    for (int k = 0; k < nblk; ++k) s += dle_part[k];
-    dle[0] = static_cast<float>(s);
+    for (int k = threadIdx.x; k < nblk; k += kWave) s += dle_part[k];
+    s = wave_sum(s);
+    if (threadIdx.x == 0) dle[0] = static_cast<float>(s);
 }
 
 int addr_blocks(int M, int rows_per_wave) {

@@ -22,6 +22,7 @@ namespace blk {
 constexpr int kThreads = 256;
 constexpr int kFwdTP = 32;    // positions per forward workgroup
 constexpr int kMaxTaps = 8;   // conv windows are kMaxTaps wide; unused taps are zero
+constexpr int kBatch = 8;     // rows whose loads a channel walk issues together
 
 template <typename T> __device__ __forceinline__ float ldf(const T *p, size_t i);
 template <> __device__ __forceinline__ float ldf<float>(const float *p, size_t i) { return p[i]; }
@@ -57,6 +58,7 @@ __global__ __launch_bounds__(kThreads) void norm_conv_fwd_kernel(const TX *__res
         float ss = 0.f;
         if (ok) {
             const TX *xr = x + (row0 + t) * D;
+#pragma unroll 4
             for (int d = lane; d < D; d += kWave) {
                 const float v = ldf(xr, d);
                 ss += v * v;
@@ -79,18 +81,27 @@ __global__ __launch_bounds__(kThreads) void norm_conv_fwd_kernel(const TX *__res
             win[m] = 0.f;
         }
         const float nwd = nw[d];
-        for (int t = tfirst; t < tend; ++t) {
-            const size_t o = (row0 + t) * D + d;
-            const float hv = (ldf(x, o) * rs[t - t0 + halo]) * nwd;
+        // rows in batches of kBatch: the batch's loads are issued together
+        for (int tb = tfirst; tb < tend; tb += kBatch) {
+            float xv[kBatch];
 #pragma unroll
-            for (int m = 0; m + 1 < kMaxTaps; ++m) win[m] = win[m + 1];
-            win[kMaxTaps - 1] = hv;
-            if (t >= t0) {
-                float acc = 0.f;
+            for (int k = 0; k < kBatch; ++k) xv[k] = ldf(x, (row0 + min(tb + k, tend - 1)) * D + d);
 #pragma unroll
-                for (int m = 0; m < kMaxTaps; ++m) acc += wa[m] * win[m];
-                stf(h, o, hv);
-                stf(u, o, acc);
+            for (int k = 0; k < kBatch; ++k) {
+                const int t = tb + k;
+                if (t >= tend) break;
+                const size_t o = (row0 + t) * D + d;
+                const float hv = (xv[k] * rs[t - t0 + halo]) * nwd;
+#pragma unroll
+                for (int m = 0; m + 1 < kMaxTaps; ++m) win[m] = win[m + 1];
+                win[kMaxTaps - 1] = hv;
+                if (t >= t0) {
+                    float acc = 0.f;
+#pragma unroll
+                    for (int m = 0; m < kMaxTaps; ++m) acc += wa[m] * win[m];
+                    stf(h, o, hv);
+                    stf(u, o, acc);
+                }
             }
         }
     }
@@ -140,25 +151,37 @@ __global__ __launch_bounds__(kThreads) void norm_conv_bwd_kernel(const TX *__res
         dv[0] = 0.f;
         const float nwd = nw[d];
         float gnw = 0.f;
-        for (int t = t0; t < tend; ++t) {
-            const size_t o = (row0 + t) * D + d;
-            const float xn = ldf(x, o) * rs[t - t0];
-            const int tn = t + Kc - 1;
-            const bool okn = tn < T;
-            const float vn = ldf(du, (row0 + (okn ? tn : t)) * D + d);
+        for (int tb = t0; tb < tend; tb += kBatch) {
+            // the batch's loads first: x, the next du and dhv of up to kBatch rows
+            float xv[kBatch], nv[kBatch], hv[kBatch];
 #pragma unroll
-            for (int m = 0; m + 1 < kMaxTaps; ++m) dv[m] = dv[m + 1];
-            dv[kMaxTaps - 1] = okn ? vn : 0.f;
-            float dh = dhv ? ldf(dhv, o) : 0.f;
-            const float ht = xn * nwd;
-#pragma unroll
-            for (int j = 0; j < kMaxTaps; ++j) {
-                dh += cl[j] * dv[kMaxTaps - 1 - j];
-                gcw[j] += ht * dv[kMaxTaps - 1 - j];
+            for (int k = 0; k < kBatch; ++k) {
+                const int t = min(tb + k, tend - 1), tn = t + Kc - 1;
+                const size_t o = (row0 + t) * D + d;
+                xv[k] = ldf(x, o);
+                nv[k] = ldf(du, (row0 + (tn < T ? tn : t)) * D + d);
+                nv[k] = tn < T ? nv[k] : 0.f;
+                hv[k] = dhv ? ldf(dhv, o) : 0.f;
             }
-            gnw += dh * xn;
-            dh_s[static_cast<size_t>(t - t0) * D + d] = dh;
-            rdot[(t - t0) * kThreads + threadIdx.x] += dh * nwd * xn;
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const int t = tb + k;
+                if (t >= tend) break;
+                const float xn = xv[k] * rs[t - t0];
+#pragma unroll
+                for (int m = 0; m + 1 < kMaxTaps; ++m) dv[m] = dv[m + 1];
+                dv[kMaxTaps - 1] = nv[k];
+                float dh = hv[k];
+                const float ht = xn * nwd;
+#pragma unroll
+                for (int j = 0; j < kMaxTaps; ++j) {
+                    dh += cl[j] * dv[kMaxTaps - 1 - j];
+                    gcw[j] += ht * dv[kMaxTaps - 1 - j];
+                }
+                gnw += dh * xn;
+                dh_s[static_cast<size_t>(t - t0) * D + d] = dh;
+                rdot[(t - t0) * kThreads + threadIdx.x] += dh * nwd * xn;
+            }
         }
         pnw[tile * D + d] = gnw;
 #pragma unroll
@@ -177,6 +200,7 @@ __global__ __launch_bounds__(kThreads) void norm_conv_bwd_kernel(const TX *__res
     for (int t = t0; t < tend; ++t) {
         const float rst = rs[t - t0];
         const float dot = rdot[(t - t0) * kThreads] * invD;
+#pragma unroll 4
         for (int d = threadIdx.x; d < D; d += kThreads) {
             const size_t o = (row0 + t) * D + d;
             const float xn = ldf(x, o) * rst;

@@ -184,6 +184,22 @@ def _mm(a, b, out_dtype):
     return torch.mm(a, b) if a.dtype == out_dtype else torch.mm(a, b, out_dtype=out_dtype)
 
 
+def _wgrad(a, b):
+    """a^T b in fp32 for a (K, N1), b (K, N2) with K the token dimension: the
+    split-K MFMA kernel for bf16 operands whose widths are multiples of 8,
+    the library GEMM otherwise."""
+    K, N1 = a.shape
+    N2 = b.shape[1]
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16 or N1 % 8 or N2 % 8:
+        return _mm(a.t(), b, torch.float32)
+    a, b = a.contiguous(), b.contiguous()
+    c = torch.empty(N1, N2, device=a.device, dtype=torch.float32)
+    ws_bytes = nat.lib().ulm_wgrad_workspace_bytes(K, N1, N2)
+    ws = torch.empty(max(ws_bytes, 1), device=a.device, dtype=torch.uint8)
+    call("ulm_wgrad", ptr(a), ptr(b), ptr(c), K, N1, N2, ptr(ws), ws_bytes, nat.stream_of(a))
+    return c
+
+
 def _addmm(c, a, b):
     """c + a @ b with c fp32, accumulated in the GEMM's epilogue."""
     return torch.addmm(c, a, b) if a.dtype == c.dtype else torch.addmm(c, a, b, out_dtype=c.dtype)
@@ -267,7 +283,7 @@ class UnifiedBlockFn(torch.autograd.Function):
             call("ulm_cast", ptr(dout), nat.ULM_F32, ptr(d16), cd, M * D, s)
         d2 = d16.view(M, D)
         dqw = torch.mm(d2, mw)                       # d(w q) = dout mu
-        dmu = _mm(d2.t(), qw, f32)
+        dmu = _wgrad(d2, qw)
         dr = torch.empty(M, A, device=dev, dtype=f32)
         dv = torch.empty(M, D, device=dev, dtype=cdt)
         dg = torch.empty(1, device=dev, dtype=f32)
@@ -286,9 +302,9 @@ class UnifiedBlockFn(torch.autograd.Function):
              ptr(dle), ptr(ws), ws_bytes, M, A, s)
         del ws, dr
         du = _mm(dpre, kw, f32)
-        dkey = _mm(dpre.t(), u.view(M, D), f32)
+        dkey = _wgrad(dpre, u.view(M, D))
         dhv = _mm(dv, vw, f32)
-        dval = _mm(dv.t(), h.view(M, D), f32)
+        dval = _wgrad(dv, h.view(M, D))
         dx = torch.empty(B, T, D, device=dev, dtype=f32)
         dnw = torch.empty(D, device=dev, dtype=f32)
         dcw = torch.empty(D, Kc, device=dev, dtype=f32)

@@ -211,7 +211,9 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
             cv[i] = wa + (pw * cj + cv[i]);
             pw *= lam;
         }
-        // dc and its reverse decayed scan
+        // dc and its reverse decayed scan. The dw terms and the q-side dg terms
+        // are summed here, where q is formed, so dq_f, d(w q) and dc die with
+        // this loop (positions past T contribute exact zeros to every term).
         float rl[kSeg];
         float racc = 0.f;
 #pragma unroll
@@ -222,13 +224,20 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
             dc[i] = -dq[i] * qt / cv[i];
             racc = dc[i] + lam * racc;
             rl[i] = racc;
-            rv[i] = qt;   // rv now holds q
+            dw_acc += dc[i];
+            if constexpr (XQ >= 2) dw_acc += qt * dqwv[i];
+            // The fast-read terms take the bf16 q and k that the dq and dk
+            // products contracted with, so each (t, s) pair enters both sums
+            // with the same value and the position weights cancel to t - s.
+            const float q16 = bf16_to_f32(f32_to_bf16_bits(qt));
+            const double pos = static_cast<double>(t0 + i) - tau;
+            dg_acc += pos * static_cast<double>(q16 * dqfv[i] + dc[i] * (cv[i] - wa));
         }
         tot[j][s] = racc;
         __syncthreads();
         float rj = dkc_next;
         for (int m = 3; m > j; --m) rj = tot[m][s] + lam16 * rj;
-        float dkt[kSeg], dkfv[kSeg], dkcv[kSeg];
+        float dkfv[kSeg], dkcv[kSeg];   // dkt = dkfv + dkcv
         float pr = lam;   // lam^(16-i) for i = 15 .. 0
 #pragma unroll
         for (int i = kSeg - 1; i >= 0; --i) {
@@ -236,29 +245,19 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
             dkfv[i] = (va && t < T) ? dkf[(b * T + t) * A + a] : 0.f;
             dkcv[i] = rl[i] + pr * rj;
             pr *= lam;
-            dkt[i] = dkfv[i] + dkcv[i];
         }
-        first_dkt[j][s] = dkt[0];
+        first_dkt[j][s] = dkfv[0] + dkcv[0];
         if (j == 0) tot[0][s] = rl[0] + pow_int(lam, kSeg) * rj;   // dkc at chunk start (rl[0] + lam^16 r_0)
         __syncthreads();
         const float after = (j == 3) ? dkt_next : first_dkt[j + 1][s];
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
             const int t = t0 + i;
-            if (va && t < T) {
-                const float nxt = (i + 1 < kSeg) ? dkt[i + 1] : after;
-                dr[(b * T + t) * A + a] = dq[i] / cv[i] + nxt;
-                dw_acc += dc[i];
-                if constexpr (XQ >= 2) dw_acc += rv[i] * dqwv[i];   // rv holds q
-                // The fast-read terms take the bf16 q and k that the dq and dk
-                // products contracted with, so each (t, s) pair enters both sums
-                // with the same value and the position weights cancel to t - s.
-                const float q16 = bf16_to_f32(f32_to_bf16_bits(rv[i]));
-                const float k16 = bf16_to_f32(f32_to_bf16_bits(kv[i]));
-                const double pos = static_cast<double>(t) - tau;
-                dg_acc += pos * (static_cast<double>(q16 * dqfv[i] + dc[i] * (cv[i] - wa)) -
-                                 static_cast<double>(k16 * dkfv[i] + kv[i] * dkcv[i]));
-            }
+            const float nxt = (i + 1 < kSeg) ? dkfv[i + 1] + dkcv[i + 1] : after;
+            if (va && t < T) dr[(b * T + t) * A + a] = dq[i] / cv[i] + nxt;
+            const float k16 = bf16_to_f32(f32_to_bf16_bits(kv[i]));
+            const double pos = static_cast<double>(t) - tau;
+            dg_acc -= pos * static_cast<double>(k16 * dkfv[i] + kv[i] * dkcv[i]);
         }
         dkc_next = tot[0][s];
         dkt_next = first_dkt[0][s];

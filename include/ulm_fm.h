@@ -125,7 +125,7 @@ int ulm_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float 
  *   pre   (M,A) pre_dtype        K u without the bias
  *   bias  (A,)  fp32 or NULL
  *   log_eps (1,) fp32 device scalar
- *   r     (M,A) fp32 out
+ *   r     (M,A) fp32 out, or NULL: only denom (ulm_block_fm_fwd forms r itself)
  *   denom (M,)  fp32 out         exp(clamp(log_eps)) + sum_a z, saved for backward
  */
 int ulm_addr_fwd(const void *pre, int pre_dtype, const float *bias, const float *log_eps,
@@ -133,7 +133,7 @@ int ulm_addr_fwd(const void *pre, int pre_dtype, const float *bias, const float 
 
 /* Backward of ulm_addr_fwd: dpre (M,A) pre_dtype, dbias (A,) fp32 (may be
  * NULL when bias is NULL), dlog_eps (1,) fp32, both summed in a fixed order.
- * A <= 8192. */
+ * r may be NULL: it is then formed again from pre, bias and denom. A <= 8192. */
 size_t ulm_addr_bwd_workspace_bytes(int M, int A);
 int ulm_addr_bwd(const void *pre, int pre_dtype, const float *bias, const float *log_eps,
                  const float *r, const float *denom, const float *dr,
@@ -145,11 +145,14 @@ int ulm_addr_bwd(const void *pre, int pre_dtype, const float *bias, const float 
  * memory. The block runs as
  *   h, u  = ulm_norm_conv_fwd(x)               RMSNorm + causal conv (78-79)
  *   pre   = u K^T,  v = h W_v^T                 caller's GEMMs (key, val)
- *   r     = ulm_addr_fwd(pre)                   relu^2 address (code, 70-72)
- *   qw, y = ulm_block_fm_fwd(r, v, x)          qw = w q, y = x + fast (84-85)
+ *   denom = ulm_addr_fwd(pre), r = NULL         relu^2 address (code, 70-72)
+ *   qw, y = ulm_block_fm_fwd(pre, denom, v, x)  qw = w q, y = x + fast (84-85)
  *   out   = y + qw mu^T                         caller's GEMM, accumulating into y
  * and backward in reverse, with ulm_block_fm_bwd taking d(w q) = dout mu and
- * ulm_norm_conv_bwd joining the conv, RMSNorm and residual gradients.
+ * ulm_norm_conv_bwd joining the conv, RMSNorm and residual gradients. The
+ * address r (B,T,A) fp32 is never written: the fast memory's statistics form
+ * r = relu(pre + bias)^2 / denom where they read it, and ulm_addr_bwd forms
+ * it again, from the bf16 pre-activation (half of r's bytes).
  */
 
 /* h = (x rstd) * norm_w with rstd = (mean x^2 + eps)^-1/2 per position
@@ -177,23 +180,28 @@ int ulm_norm_conv_bwd(const void *x, int x_dtype, const float *rstd, const float
                       int dhv_dtype, const float *dres, float *dx, float *dnorm_w, float *dconv_w,
                       void *workspace, size_t workspace_bytes, int B, int T, int D, void *stream);
 
-/* ulm_fm_fwd inside the block: instead of q and fast it writes
+/* ulm_fm_fwd inside the block. r is given by the address inputs, pre (B,T,A)
+ * pre_dtype, bias (A,) fp32 or NULL and denom (B,T) from ulm_addr_fwd, as
+ * r = relu(pre + bias)^2 * (1 / denom) (within 1 ulp of ulm_addr_fwd's r).
+ * Instead of q and fast it writes
  *   qw (B,T,A) qw_dtype out: w q, the operand of the mu GEMM ((q*w), model.py:85)
  *   y  (B,T,D) fp32 out:     x + fast, x (B,T,D) fp32 the residual (y != x)
  * saved as for ulm_fm_fwd (ulm_fm_saved_bytes). */
 size_t ulm_block_fm_fwd_workspace_bytes(int B, int T, int A, int D);
-int ulm_block_fm_fwd(const float *r, const void *v, int v_dtype, const float *g, const float *w,
-                     void *qw, int qw_dtype, const float *x, float *y, void *saved, size_t saved_bytes,
-                     void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream);
+int ulm_block_fm_fwd(const void *pre, int pre_dtype, const float *bias, const float *denom,
+                     const void *v, int v_dtype, const float *g, const float *w, void *qw, int qw_dtype,
+                     const float *x, float *y, void *saved, size_t saved_bytes, void *workspace,
+                     size_t workspace_bytes, int B, int T, int A, int D, void *stream);
 
-/* ulm_fm_bwd inside the block: dqw (B,T,A) dqw_dtype is d loss / d(w q); the
- * q gradient is w dqw and dw also gets sum_t q dqw. Workspace of
+/* ulm_fm_bwd inside the block: r given by the address inputs as for
+ * ulm_block_fm_fwd; dqw (B,T,A) dqw_dtype is d loss / d(w q), the q gradient
+ * is w dqw and dw also gets sum_t q dqw. Workspace of
  * ulm_fm_bwd_workspace_bytes() bytes; other arguments as for ulm_fm_bwd. */
-int ulm_block_fm_bwd(const float *r, const float *g, const float *w, const void *saved,
-                     size_t saved_bytes, int v_dtype, const void *dfast, int dfast_dtype,
-                     const void *dqw, int dqw_dtype, float *dr, void *dv, int dv_dtype, float *dg,
-                     float *dw, void *workspace, size_t workspace_bytes, int B, int T, int A, int D,
-                     void *stream);
+int ulm_block_fm_bwd(const void *pre, int pre_dtype, const float *bias, const float *denom,
+                     const float *g, const float *w, const void *saved, size_t saved_bytes,
+                     int v_dtype, const void *dfast, int dfast_dtype, const void *dqw, int dqw_dtype,
+                     float *dr, void *dv, int dv_dtype, float *dg, float *dw, void *workspace,
+                     size_t workspace_bytes, int B, int T, int A, int D, void *stream);
 
 /* Weight gradient of a linear layer over the token dimension: C = A^T B, i.e.
  * C[i][j] = sum_k A[k][i] B[k][j], A (K,N1) and B (K,N2) bf16 row-major,

@@ -109,14 +109,15 @@ __global__ __launch_bounds__(kAddrWaves * 64) void addr_fwd_kernel(const T *__re
             for (int k = 0; k < W; ++k) ss += p[k] * p[k];
         }
         const float dn = E + wave_sum(ss);
-        const float inv = 1.f / dn;
+        if (r) {   // null: only the denominators (the block forms r where it reads it)
 #pragma unroll 4
-        for (int a = W * lane; a < A; a += W * kWave) {
-            float p[W];
-            relu_row<T, W>(pre, bias, base, a, p);
+            for (int a = W * lane; a < A; a += W * kWave) {
+                float p[W];
+                relu_row<T, W>(pre, bias, base, a, p);
 #pragma unroll
-            for (int k = 0; k < W; ++k) p[k] = (p[k] * p[k]) * inv;
-            Vec<float, W>::st(r, base + a, p);
+                for (int k = 0; k < W; ++k) p[k] = (p[k] * p[k]) / dn;
+                Vec<float, W>::st(r, base + a, p);
+            }
         }
         if (lane == 0) denom[row] = dn;
     }
@@ -124,8 +125,9 @@ __global__ __launch_bounds__(kAddrWaves * 64) void addr_fwd_kernel(const T *__re
 
 // One wave per row: rho = sum_a dr r by a wave reduction, then dpre. Each wave
 // keeps its dbias column partials in its own LDS row; the block writes their
-// sum as one partial row, and the dlog_eps partial.
-template <typename T, int W>
+// sum as one partial row, and the dlog_eps partial. Without HAS_R, r is formed
+// from pre, bias and denom with the forward's operations.
+template <typename T, int W, bool HAS_R>
 __global__ __launch_bounds__(kAddrWaves * 64) void addr_bwd_kernel(const T *__restrict__ pre,
                                                                    const float *__restrict__ bias,
                                                                    const float *__restrict__ log_eps,
@@ -144,17 +146,24 @@ __global__ __launch_bounds__(kAddrWaves * 64) void addr_bwd_kernel(const T *__re
     const int row0 = (blockIdx.x * kAddrWaves + wave) * kBwdRowsPerWave;
     for (int row = row0; row < row0 + kBwdRowsPerWave && row < M; ++row) {
         const size_t base = static_cast<size_t>(row) * A;
+        const float dn = denom[row];
+        const float inv = 1.f / dn;
         float rho = 0.f;
 #pragma unroll 4
         for (int a = W * lane; a < A; a += W * kWave) {
             float x[W], y[W];
             Vec<float, W>::ld(dr, base + a, x);
-            Vec<float, W>::ld(r, base + a, y);
+            if constexpr (HAS_R) {
+                Vec<float, W>::ld(r, base + a, y);
+            } else {
+                relu_row<T, W>(pre, bias, base, a, y);
+#pragma unroll
+                for (int k = 0; k < W; ++k) y[k] = (y[k] * y[k]) * inv;   // as the fast memory's statistics form it
+            }
 #pragma unroll
             for (int k = 0; k < W; ++k) rho += x[k] * y[k];
         }
         rho = wave_sum(rho);
-        const float inv = 1.f / denom[row];
 #pragma unroll 4
         for (int a = W * lane; a < A; a += W * kWave) {
             float p[W], x[W], acc[W];
@@ -215,6 +224,19 @@ int launch_addr_fwd(const void *pre, const float *bias, const float *log_eps, fl
     return check_launch("addr_fwd_kernel");
 }
 
+template <typename T, int W, bool HAS_R>
+int launch_addr_bwd_kernel(const T *pre, const float *bias, const float *log_eps, const float *r, const float *denom,
+                           const float *dr, T *dpre, float *dbias_part, float *dle_part, int M, int A, int nblk,
+                           size_t lds, hipStream_t s) {
+    if (lds > 65536 &&
+        hipFuncSetAttribute(reinterpret_cast<const void *>(&addr_bwd_kernel<T, W, HAS_R>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
+        return check_launch("addr_bwd_kernel attribute");
+    addr_bwd_kernel<T, W, HAS_R><<<nblk, kAddrWaves * 64, lds, s>>>(pre, bias, log_eps, r, denom, dr, dpre, dbias_part,
+                                                                    dle_part, M, A);
+    return check_launch("addr_bwd_kernel");
+}
+
 template <typename T>
 int launch_addr_bwd(const void *pre, const float *bias, const float *log_eps, const float *r, const float *denom,
                     const float *dr, void *dpre, float *dbias_part, float *dle_part, int M, int A, hipStream_t s) {
@@ -224,20 +246,12 @@ int launch_addr_bwd(const void *pre, const float *bias, const float *log_eps, co
                      reinterpret_cast<uintptr_t>(dpre) % (4 * sizeof(T)) == 0 &&
                      reinterpret_cast<uintptr_t>(r) % 16 == 0 && reinterpret_cast<uintptr_t>(dr) % 16 == 0 &&
                      reinterpret_cast<uintptr_t>(bias) % 16 == 0;
-    const void *fn = vec ? reinterpret_cast<const void *>(&addr_bwd_kernel<T, 4>)
-                         : reinterpret_cast<const void *>(&addr_bwd_kernel<T, 1>);
-    if (lds > 65536 && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) !=
-                           hipSuccess)
-        return check_launch("addr_bwd_kernel attribute");
-    if (vec)
-        addr_bwd_kernel<T, 4><<<nblk, kAddrWaves * 64, lds, s>>>(static_cast<const T *>(pre), bias, log_eps, r, denom,
-                                                                 dr, static_cast<T *>(dpre), dbias_part, dle_part, M,
-                                                                 A);
-    else
-        addr_bwd_kernel<T, 1><<<nblk, kAddrWaves * 64, lds, s>>>(static_cast<const T *>(pre), bias, log_eps, r, denom,
-                                                                 dr, static_cast<T *>(dpre), dbias_part, dle_part, M,
-                                                                 A);
-    return check_launch("addr_bwd_kernel");
+    const T *pt = static_cast<const T *>(pre);
+    T *dp = static_cast<T *>(dpre);
+    if (vec && r) return launch_addr_bwd_kernel<T, 4, true>(pt, bias, log_eps, r, denom, dr, dp, dbias_part, dle_part, M, A, nblk, lds, s);
+    if (vec) return launch_addr_bwd_kernel<T, 4, false>(pt, bias, log_eps, r, denom, dr, dp, dbias_part, dle_part, M, A, nblk, lds, s);
+    if (r) return launch_addr_bwd_kernel<T, 1, true>(pt, bias, log_eps, r, denom, dr, dp, dbias_part, dle_part, M, A, nblk, lds, s);
+    return launch_addr_bwd_kernel<T, 1, false>(pt, bias, log_eps, r, denom, dr, dp, dbias_part, dle_part, M, A, nblk, lds, s);
 }
 
 }  // namespace ulm
@@ -248,7 +262,7 @@ extern "C" int ulm_addr_fwd(const void *pre, int pre_dtype, const float *bias, c
                             float *denom, int M, int A, void *stream) {
     ULM_REQUIRE(M > 0 && A > 0, "ulm_addr_fwd: bad sizes M=%d A=%d", M, A);
     ULM_REQUIRE(valid_dtype(pre_dtype), "ulm_addr_fwd: bad pre dtype %d", pre_dtype);
-    ULM_REQUIRE(pre && log_eps && r && denom, "ulm_addr_fwd: null pointer");
+    ULM_REQUIRE(pre && log_eps && denom, "ulm_addr_fwd: null pointer");
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (pre_dtype == ULM_F32) return launch_addr_fwd<float>(pre, bias, log_eps, r, denom, M, A, s);
     if (pre_dtype == ULM_BF16) return launch_addr_fwd<uint16_t>(pre, bias, log_eps, r, denom, M, A, s);
@@ -286,7 +300,7 @@ extern "C" int ulm_addr_bwd(const void *pre, int pre_dtype, const float *bias, c
     ULM_REQUIRE(M > 0 && A > 0, "ulm_addr_bwd: bad sizes M=%d A=%d", M, A);
     ULM_REQUIRE(A <= 8192, "ulm_addr_bwd: A=%d exceeds the LDS column-partial limit 8192", A);
     ULM_REQUIRE(valid_dtype(pre_dtype), "ulm_addr_bwd: bad pre dtype %d", pre_dtype);
-    ULM_REQUIRE(pre && log_eps && r && denom && dr && dpre && dlog_eps, "ulm_addr_bwd: null pointer");
+    ULM_REQUIRE(pre && log_eps && denom && dr && dpre && dlog_eps, "ulm_addr_bwd: null pointer");
     ULM_REQUIRE(!bias || dbias, "ulm_addr_bwd: dbias is required when bias is given");
     ULM_REQUIRE(workspace && workspace_bytes >= ulm_addr_bwd_workspace_bytes(M, A),
                 "ulm_addr_bwd: workspace of %zu bytes, need %zu", workspace_bytes, ulm_addr_bwd_workspace_bytes(M, A));

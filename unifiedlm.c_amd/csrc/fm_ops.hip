@@ -44,11 +44,11 @@ int launch_chunk_scores(const uint16_t *aR, const uint16_t *aL, const uint16_t *
 int launch_partial_reduce(const float *part, int nK, size_t n, void *out, int odt, hipStream_t s,
                           const float *resid = nullptr);
 // fm_stats.hip
-int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
+int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
                      uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, float *c_last, int B, int T,
                      int A, hipStream_t s, void *qw = nullptr, int qw_dt = ULM_BF16);
 size_t bwd_stats_partial_bytes(int B, int A);
-int launch_bwd_stats(const float *dqf, const float *dqo, const float *r, const float *nck,
+int launch_bwd_stats(const float *dqf, const float *dqo, const RSrc &src, const float *nck,
                      const float *w, const float *g, const float *dkf, float *dr, float *dw, float *dg, void *part,
                      int B, int T, int A, hipStream_t s, const void *dqw = nullptr, int dqw_dt = ULM_BF16);
 
@@ -227,7 +227,7 @@ namespace {
 // (aligned shapes only) it also emits the decode state after position T-1.
 // q (fp32) and qw (w q in qw_dt) are each optional; with resid (fp32 (B,T,D))
 // the output is resid + fast.
-int fm_forward(const float *r, const void *v, int v_dtype, const float *g, const float *w, float *q, void *qw,
+int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const float *w, float *q, void *qw,
                int qw_dt, const float *resid, void *fast, int fast_dtype, void *saved, void *workspace, float *state,
                float *c_last, int B, int T, int A, int D, hipStream_t s) {
     const Saved sv = saved_layout(saved, B, T, A, D, v_dtype);
@@ -272,7 +272,9 @@ extern "C" int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const floa
     const size_t need = ulm_fm_fwd_workspace_bytes(B, T, A, D, fast_dtype);
     ULM_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), "ulm_fm_fwd: workspace of %zu bytes, need %zu",
                 workspace_bytes, need);
-    return fm_forward(r, v, v_dtype, g, w, q, nullptr, ULM_F32, nullptr, fast, fast_dtype, saved, workspace, nullptr,
+    RSrc rs;
+    rs.r = r;
+    return fm_forward(rs, v, v_dtype, g, w, q, nullptr, ULM_F32, nullptr, fast, fast_dtype, saved, workspace, nullptr,
                       nullptr, B, T, A, D, static_cast<hipStream_t>(stream));
 }
 
@@ -298,7 +300,9 @@ extern "C" int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const 
     ULM_REQUIRE(workspace_bytes >= need, "ulm_fm_prefill: workspace of %zu bytes, need %zu", workspace_bytes, need);
     char *saved = static_cast<char *>(workspace);
     char *ws = saved + align_up(saved_layout(nullptr, B, T, A, D, v_dtype).bytes, 256);
-    return fm_forward(r, v, v_dtype, g, w, q, nullptr, ULM_F32, nullptr, fast, fast_dtype, saved, ws, S, c_last, B, T,
+    RSrc rs;
+    rs.r = r;
+    return fm_forward(rs, v, v_dtype, g, w, q, nullptr, ULM_F32, nullptr, fast, fast_dtype, saved, ws, S, c_last, B, T,
                       A, D, static_cast<hipStream_t>(stream));
 }
 
@@ -311,7 +315,7 @@ namespace {
 
 // The backward composite of ulm_fm_bwd (arguments checked by the caller); dqw
 // (d(w q) in dqw_dt, may be null) adds w dqw to dq_out and sum_t q dqw to dw.
-int fm_backward(const float *r, const float *g, const float *w, const void *saved, int v_dtype, const void *dfast,
+int fm_backward(const RSrc &r, const float *g, const float *w, const void *saved, int v_dtype, const void *dfast,
                 int dfast_dtype, const float *dq_out, const void *dqw, int dqw_dt, float *dr, void *dv, int dv_dtype,
                 float *dg, float *dw, void *workspace, int B, int T, int A, int D, hipStream_t s) {
     const Saved sv = saved_layout(const_cast<void *>(saved), B, T, A, D, v_dtype);
@@ -373,8 +377,10 @@ extern "C" int ulm_fm_bwd(const float *r, const float *g, const float *w, const 
     const size_t need = ulm_fm_bwd_workspace_bytes(B, T, A, D, dfast_dtype);
     ULM_REQUIRE(workspace && workspace_bytes >= need, "ulm_fm_bwd: workspace of %zu bytes, need %zu",
                 workspace_bytes, need);
-    return fm_backward(r, g, w, saved, v_dtype, dfast, dfast_dtype, dq_out, nullptr, ULM_BF16, dr, dv, dv_dtype, dg, dw,
-                       workspace, B, T, A, D, static_cast<hipStream_t>(stream));
+    RSrc rs;
+    rs.r = r;
+    return fm_backward(rs, g, w, saved, v_dtype, dfast, dfast_dtype, dq_out, nullptr, ULM_BF16, dr, dv, dv_dtype, dg,
+                       dw, workspace, B, T, A, D, static_cast<hipStream_t>(stream));
 }
 
 // ---------------------------------------------------------------------------
@@ -386,35 +392,49 @@ extern "C" size_t ulm_block_fm_fwd_workspace_bytes(int B, int T, int A, int D) {
     return fwd_layout(nullptr, B, T, A, D, ULM_F32, true).bytes;
 }
 
-extern "C" int ulm_block_fm_fwd(const float *r, const void *v, int v_dtype, const float *g, const float *w, void *qw,
-                                int qw_dtype, const float *x, float *y, void *saved, size_t saved_bytes,
-                                void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
+extern "C" int ulm_block_fm_fwd(const void *pre, int pre_dtype, const float *bias, const float *denom, const void *v,
+                                int v_dtype, const float *g, const float *w, void *qw, int qw_dtype, const float *x,
+                                float *y, void *saved, size_t saved_bytes, void *workspace, size_t workspace_bytes,
+                                int B, int T, int A, int D, void *stream) {
     ULM_REQUIRE(B > 0 && T > 0 && A > 0 && D > 0, "ulm_block_fm_fwd: bad sizes B=%d T=%d A=%d D=%d", B, T, A, D);
-    ULM_REQUIRE(valid_dtype(v_dtype) && valid_dtype(qw_dtype), "ulm_block_fm_fwd: bad dtype %d/%d", v_dtype,
-                qw_dtype);
-    ULM_REQUIRE(r && v && g && w && qw && x && y && saved && workspace, "ulm_block_fm_fwd: null pointer");
+    ULM_REQUIRE(valid_dtype(pre_dtype) && valid_dtype(v_dtype) && valid_dtype(qw_dtype),
+                "ulm_block_fm_fwd: bad dtype %d/%d/%d", pre_dtype, v_dtype, qw_dtype);
+    ULM_REQUIRE(pre && denom && v && g && w && qw && x && y && saved && workspace, "ulm_block_fm_fwd: null pointer");
     ULM_REQUIRE(static_cast<const void *>(x) != static_cast<const void *>(y), "ulm_block_fm_fwd: y must not alias x");
     const size_t need_s = ulm_fm_saved_bytes(B, T, A, D, v_dtype);
     ULM_REQUIRE(saved_bytes >= need_s, "ulm_block_fm_fwd: saved buffer of %zu bytes, need %zu", saved_bytes, need_s);
     const size_t need = ulm_block_fm_fwd_workspace_bytes(B, T, A, D);
     ULM_REQUIRE(workspace_bytes >= need, "ulm_block_fm_fwd: workspace of %zu bytes, need %zu", workspace_bytes, need);
-    return fm_forward(r, v, v_dtype, g, w, nullptr, qw, qw_dtype, x, y, ULM_F32, saved, workspace, nullptr, nullptr, B,
+    RSrc rs;
+    rs.pre = pre;
+    rs.pre_dt = pre_dtype;
+    rs.bias = bias;
+    rs.denom = denom;
+    return fm_forward(rs, v, v_dtype, g, w, nullptr, qw, qw_dtype, x, y, ULM_F32, saved, workspace, nullptr, nullptr, B,
                       T, A, D, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int ulm_block_fm_bwd(const float *r, const float *g, const float *w, const void *saved,
-                                size_t saved_bytes, int v_dtype, const void *dfast, int dfast_dtype, const void *dqw,
-                                int dqw_dtype, float *dr, void *dv, int dv_dtype, float *dg, float *dw,
-                                void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
+extern "C" int ulm_block_fm_bwd(const void *pre, int pre_dtype, const float *bias, const float *denom, const float *g,
+                                const float *w, const void *saved, size_t saved_bytes, int v_dtype, const void *dfast,
+                                int dfast_dtype, const void *dqw, int dqw_dtype, float *dr, void *dv, int dv_dtype,
+                                float *dg, float *dw, void *workspace, size_t workspace_bytes, int B, int T, int A,
+                                int D, void *stream) {
     ULM_REQUIRE(B > 0 && T > 0 && A > 0 && D > 0, "ulm_block_fm_bwd: bad sizes B=%d T=%d A=%d D=%d", B, T, A, D);
-    ULM_REQUIRE(valid_dtype(v_dtype) && valid_dtype(dfast_dtype) && valid_dtype(dv_dtype) && valid_dtype(dqw_dtype),
-                "ulm_block_fm_bwd: bad dtype %d/%d/%d/%d", v_dtype, dfast_dtype, dv_dtype, dqw_dtype);
-    ULM_REQUIRE(r && g && w && saved && dfast && dqw && dr && dv && dg && dw, "ulm_block_fm_bwd: null pointer");
+    ULM_REQUIRE(valid_dtype(pre_dtype) && valid_dtype(v_dtype) && valid_dtype(dfast_dtype) &&
+                    valid_dtype(dv_dtype) && valid_dtype(dqw_dtype),
+                "ulm_block_fm_bwd: bad dtype %d/%d/%d/%d/%d", pre_dtype, v_dtype, dfast_dtype, dv_dtype, dqw_dtype);
+    ULM_REQUIRE(pre && denom && g && w && saved && dfast && dqw && dr && dv && dg && dw,
+                "ulm_block_fm_bwd: null pointer");
     const size_t need_s = ulm_fm_saved_bytes(B, T, A, D, v_dtype);
     ULM_REQUIRE(saved_bytes >= need_s, "ulm_block_fm_bwd: saved buffer of %zu bytes, need %zu", saved_bytes, need_s);
     const size_t need = ulm_fm_bwd_workspace_bytes(B, T, A, D, dfast_dtype);
     ULM_REQUIRE(workspace && workspace_bytes >= need, "ulm_block_fm_bwd: workspace of %zu bytes, need %zu",
                 workspace_bytes, need);
-    return fm_backward(r, g, w, saved, v_dtype, dfast, dfast_dtype, nullptr, dqw, dqw_dtype, dr, dv, dv_dtype, dg, dw,
+    RSrc rs;
+    rs.pre = pre;
+    rs.pre_dt = pre_dtype;
+    rs.bias = bias;
+    rs.denom = denom;
+    return fm_backward(rs, g, w, saved, v_dtype, dfast, dfast_dtype, nullptr, dqw, dqw_dtype, dr, dv, dv_dtype, dg, dw,
                        workspace, B, T, A, D, static_cast<hipStream_t>(stream));
 }

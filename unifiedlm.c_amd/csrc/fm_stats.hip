@@ -33,11 +33,80 @@ __device__ __forceinline__ float pow_int(float x, int e) {
     return r;
 }
 
+// Sources of r for the kernels below (RSrc): loads are unconditional, at a
+// clamped index, and masked after, so none waits inside a branch.
+struct RTensor {
+    const float *r;
+    __device__ __forceinline__ float slot_const(int) const { return 0.f; }
+    static constexpr bool kRowConst = false;
+    __device__ __forceinline__ float row_const(size_t, bool) const { return 1.f; }
+    __device__ __forceinline__ float at(size_t row, int a, int A, float, float, bool ok) const {
+        const float v = r[(ok ? row : 0) * A + (ok ? a : 0)];
+        return ok ? v : 0.f;
+    }
+};
+
+template <typename TP> __device__ __forceinline__ float ld_pre(const TP *p, size_t i);
+template <> __device__ __forceinline__ float ld_pre<float>(const float *p, size_t i) { return p[i]; }
+template <> __device__ __forceinline__ float ld_pre<uint16_t>(const uint16_t *p, size_t i) { return bf16_to_f32(p[i]); }
+template <> __device__ __forceinline__ float ld_pre<_Float16>(const _Float16 *p, size_t i) { return static_cast<float>(p[i]); }
+
+// r = relu(pre + bias)^2 * (1 / denom[row]); addr_bwd_kernel forms r with the
+// same operations, so every kernel of the block sees the same r. The
+// reciprocal depends on the position only, which is uniform over a wave (its
+// lanes are 64 slots), so row_const forms it once per position.
+template <typename TP>
+struct RAddr {
+    const TP *pre;
+    const float *bias, *denom;
+    __device__ __forceinline__ float slot_const(int a) const { return bias ? bias[a] : 0.f; }
+    static constexpr bool kRowConst = true;
+    __device__ __forceinline__ float row_const(size_t row, bool tok) const { return 1.f / denom[tok ? row : 0]; }
+    __device__ __forceinline__ float at(size_t row, int a, int A, float b, float inv, bool ok) const {
+        const size_t rr = ok ? row : 0;
+        float p = ld_pre(pre, rr * A + (ok ? a : 0)) + b;
+        p = p > 0.f ? p : 0.f;
+        const float v = (p * p) * inv;
+        return ok ? v : 0.f;
+    }
+};
+
+// The per-position constants of a thread segment (positions t0 .. t0+15 and
+// t0 - 1): lane l < 16 loads position t0 + l, lane 16 position t0 - 1, and
+// v_readlane hands each value to the whole wave.
+template <class RS>
+__device__ __forceinline__ float seg_row_consts(const RS &rs, size_t row_t0, int t0, int T, int lane) {
+    if constexpr (RS::kRowConst) {
+        const int tl = lane < kSeg ? t0 + lane : t0 - 1;
+        return rs.row_const(row_t0 + (tl - t0), tl >= 0 && tl < T);
+    } else {
+        return 1.f;
+    }
+}
+
+__device__ __forceinline__ float lane_value(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Calls f(source) with the RTensor or RAddr<T> that src describes.
+template <class F>
+int with_rsrc(const RSrc &src, F &&f) {
+    if (src.r) return f(RTensor{src.r});
+    if (!src.pre || !src.denom) return fail(ULM_ERR_INVALID, "stats: neither r nor the address inputs given");
+    switch (src.pre_dt) {
+    case ULM_F32: return f(RAddr<float>{static_cast<const float *>(src.pre), src.bias, src.denom});
+    case ULM_BF16: return f(RAddr<uint16_t>{static_cast<const uint16_t *>(src.pre), src.bias, src.denom});
+    case ULM_F16: return f(RAddr<_Float16>{static_cast<const _Float16 *>(src.pre), src.bias, src.denom});
+    }
+    return fail(ULM_ERR_INVALID, "stats: bad pre dtype %d", src.pre_dt);
+}
+
 // Outputs besides n_ckpt (each may be null): q (fp32); qw = w q in qw_dt; q16n, k16n natural bf16
 // copies; qR, kR in the R layout and qQ, kQ in the Q layout (the chunked
 // kernel's operand tiles; A % 32 == 0); c_last = c at position T-1 (B, A), the
 // decode state after the sequence. Positions past T are zero in R and Q.
-__global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict__ r, const float *__restrict__ w,
+template <class RS>
+__global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__restrict__ w,
                                                         const float *__restrict__ g, float *__restrict__ q,
                                                         void *__restrict__ qw, int qw_dt,
                                                         uint16_t *__restrict__ q16n, uint16_t *__restrict__ k16n,
@@ -47,7 +116,8 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict_
                                                         int A, int NT) {
     __shared__ float tot[4][kSlots];
     __shared__ __align__(16) uint16_t sq[ULM_CHUNK][kSlots + 8], sk[ULM_CHUNK][kSlots + 8];   // [position][slot]
-    const int s = threadIdx.x % kSlots, j = threadIdx.x / kSlots;
+    const int s = threadIdx.x % kSlots;
+    const int j = __builtin_amdgcn_readfirstlane(threadIdx.x / kSlots);   // wave-uniform (kSlots = wave size)
     const int a0 = blockIdx.x * kSlots;
     const int a = a0 + s;
     const bool va = a < A;
@@ -56,16 +126,18 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(const float *__restrict_
     const float lam = __expf(g[0]);
     const float lam16 = pow_int(lam, kSeg);
     const float wa = va ? w[a] : 1.f;
+    const float rb = va ? rs.slot_const(a) : 0.f;   // the slot's key bias when r is formed here
     float carry = 0.f;   // n at the position before the chunk
     for (int n = 0; n < NT; ++n) {
         const int t0 = n * ULM_CHUNK + j * kSeg;
+        const float seg_c = seg_row_consts(rs, bs * T + t0, t0, T, s);
         float rv[kSeg], kv[kSeg], nl[kSeg];
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
             const int t = t0 + i;
-            rv[i] = (va && t < T) ? r[(bs * T + t) * A + a] : 0.f;
+            rv[i] = rs.at(bs * T + t, a, A, rb, lane_value(seg_c, i), va && t < T);
         }
-        kv[0] = (va && t0 >= 1 && t0 - 1 < T) ? r[(bs * T + t0 - 1) * A + a] : 0.f;
+        kv[0] = rs.at(bs * T + t0 - 1, a, A, rb, lane_value(seg_c, kSeg), va && t0 >= 1 && t0 - 1 < T);
 #pragma unroll
         for (int i = 1; i < kSeg; ++i) kv[i] = rv[i - 1];
         float acc = 0.f;
@@ -150,9 +222,9 @@ __device__ __forceinline__ float load_xq(const void *p, size_t o) {
     else return 0.f;
 }
 
-template <int XQ>
+template <int XQ, class RS>
 __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict__ dqf, const void *__restrict__ xq,
-                                                        const float *__restrict__ r,
+                                                        RS rs,
                                                         const float *__restrict__ nck, const float *__restrict__ w,
                                                         const float *__restrict__ g, const float *__restrict__ dkf,
                                                         float *__restrict__ dr, float *__restrict__ dw_part,
@@ -161,13 +233,15 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
     __shared__ float first_dkt[4][kSlots];
     __shared__ float dw_sh[4][kSlots];
     __shared__ double dg_sh[4];
-    const int s = threadIdx.x % kSlots, j = threadIdx.x / kSlots;
+    const int s = threadIdx.x % kSlots;
+    const int j = __builtin_amdgcn_readfirstlane(threadIdx.x / kSlots);   // wave-uniform (kSlots = wave size)
     const int a = blockIdx.x * kSlots + s;
     const bool va = a < A;
     const size_t b = blockIdx.y;
     const float lam = __expf(g[0]);
     const float lam16 = pow_int(lam, kSeg);
     const float wa = va ? w[a] : 1.f;
+    const float rb = va ? rs.slot_const(a) : 0.f;   // the slot's key bias when r is formed here
     const double tau = 0.5 * (T - 1);
     float dkc_next = 0.f;   // dkc at the first position after the chunk
     float dkt_next = 0.f;   // dkt at the first position after the chunk
@@ -175,13 +249,14 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
     double dg_acc = 0.0;
     for (int n = NT - 1; n >= 0; --n) {
         const int t0 = n * ULM_CHUNK + j * kSeg;
+        const float seg_c = seg_row_consts(rs, b * T + t0, t0, T, s);
         float rv[kSeg], kv[kSeg], cv[kSeg], dq[kSeg], dc[kSeg], dqfv[kSeg], dqwv[kSeg];
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
             const int t = t0 + i;
             const bool ok = va && t < T;
             const size_t o = (b * T + t) * A + a;
-            rv[i] = ok ? r[o] : 0.f;
+            rv[i] = rs.at(b * T + t, a, A, rb, lane_value(seg_c, i), ok);
             dqfv[i] = ok ? dqf[o] : 0.f;
             // an unconditional load (index 0 when out of range) keeps the 16-bit
             // conversions out of a branch that would wait on each load
@@ -190,7 +265,7 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
             dqwv[i] = XQ >= 2 ? x : 0.f;
             dq[i] = dqfv[i] + (XQ == 1 ? x : wa * dqwv[i]);
         }
-        kv[0] = (va && t0 >= 1 && t0 - 1 < T) ? r[(b * T + t0 - 1) * A + a] : 0.f;
+        kv[0] = rs.at(b * T + t0 - 1, a, A, rb, lane_value(seg_c, kSeg), va && t0 >= 1 && t0 - 1 < T);
 #pragma unroll
         for (int i = 1; i < kSeg; ++i) kv[i] = rv[i - 1];
         // rebuild n (hence c) inside the chunk from its checkpoint
@@ -296,7 +371,7 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(const float *__restri
 
 // q16n, k16n: natural bf16 copies (both or neither); qR, kR, qQ, kQ: tiled
 // copies (all or none; A % 32 == 0).
-int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
+int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
                      uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, float *c_last, int B, int T,
                      int A, hipStream_t s, void *qw, int qw_dt) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
@@ -304,9 +379,11 @@ int launch_fwd_stats(const float *r, const float *w, const float *g, float *q, u
     const bool tiled = qR || kR || qQ || kQ;
     if (tiled && !(qR && kR && qQ && kQ && A % 32 == 0))
         return fail(ULM_ERR_INVALID, "fwd stats: tiled copies need all four outputs and A %% 32 == 0");
-    fwd_stats_kernel<<<dim3((A + kSlots - 1) / kSlots, B), 256, 0, s>>>(r, w, g, q, qw, qw_dt, q16n, k16n, qR, kR, qQ,
-                                                                         kQ, nck, c_last, T, A, NT);
-    return check_launch("fwd_stats_kernel");
+    return with_rsrc(src, [&](auto rs) {
+        fwd_stats_kernel<decltype(rs)><<<dim3((A + kSlots - 1) / kSlots, B), 256, 0, s>>>(
+            rs, w, g, q, qw, qw_dt, q16n, k16n, qR, kR, qQ, kQ, nck, c_last, T, A, NT);
+        return check_launch("fwd_stats_kernel");
+    });
 }
 
 size_t bwd_stats_partial_bytes(int B, int A) {
@@ -314,7 +391,7 @@ size_t bwd_stats_partial_bytes(int B, int A) {
     return align_up(static_cast<size_t>(B) * A * sizeof(float), 256) + align_up(B * nb * sizeof(double), 256);
 }
 
-int launch_bwd_stats(const float *dqf, const float *dqo, const float *r, const float *nck,
+int launch_bwd_stats(const float *dqf, const float *dqo, const RSrc &src, const float *nck,
                      const float *w, const float *g, const float *dkf, float *dr, float *dw, float *dg, void *part,
                      int B, int T, int A, hipStream_t s, const void *dqw, int dqw_dt) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
@@ -325,14 +402,19 @@ int launch_bwd_stats(const float *dqf, const float *dqo, const float *r, const f
     const int xq = dqw ? 2 + dqw_dt : (dqo ? 1 : 0);   // ULM_F32, ULM_BF16, ULM_F16 = 0, 1, 2
     const void *xp = dqw ? dqw : static_cast<const void *>(dqo);
     if (dqw && dqo) return fail(ULM_ERR_INVALID, "bwd stats: dq_out and d(w q) are exclusive");
-    switch (xq) {
-    case 0: bwd_stats_kernel<0><<<dim3(nb, B), 256, 0, s>>>(dqf, xp, r, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
-    case 1: bwd_stats_kernel<1><<<dim3(nb, B), 256, 0, s>>>(dqf, xp, r, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
-    case 2: bwd_stats_kernel<2><<<dim3(nb, B), 256, 0, s>>>(dqf, xp, r, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
-    case 3: bwd_stats_kernel<3><<<dim3(nb, B), 256, 0, s>>>(dqf, xp, r, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
-    case 4: bwd_stats_kernel<4><<<dim3(nb, B), 256, 0, s>>>(dqf, xp, r, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
-    default: return fail(ULM_ERR_INVALID, "bwd stats: bad d(w q) dtype %d", dqw_dt);
-    }
+    if (xq < 0 || xq > 4) return fail(ULM_ERR_INVALID, "bwd stats: bad d(w q) dtype %d", dqw_dt);
+    ULM_TRY(with_rsrc(src, [&](auto rs) {
+        using RS = decltype(rs);
+        const dim3 grid(nb, B);
+        switch (xq) {
+        case 0: bwd_stats_kernel<0, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
+        case 1: bwd_stats_kernel<1, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
+        case 2: bwd_stats_kernel<2, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
+        case 3: bwd_stats_kernel<3, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
+        default: bwd_stats_kernel<4, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
+        }
+        return ULM_OK;
+    }));
     int st = check_launch("bwd_stats_kernel");
     if (st) return st;
     stats_reduce_kernel<<<(A + 255) / 256, 256, 0, s>>>(dw_part, dg_part, dw, dg, B, A, B * nb);

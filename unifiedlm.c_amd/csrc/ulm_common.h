@@ -153,6 +153,18 @@ int launch_convert(const void *src, int src_dt, void *dst, int dst_dt, size_t n,
 // nsplit contiguous row ranges into tmp (nsplit x ncol), then their sum.
 int launch_column_sum(const float *in, size_t nrow, size_t ncol, float *tmp, int nsplit, float *out, hipStream_t s);
 
+// Where the statistics kernels take the read address r (B,T,A) from: an fp32
+// tensor r, or, when r is null, the block's address inputs, forming
+// r = relu(pre + bias)^2 / denom[row] on the fly (model.py:70-72) so that the
+// block never writes r.
+struct RSrc {
+    const float *r = nullptr;
+    const void *pre = nullptr;
+    int pre_dt = ULM_F32;
+    const float *bias = nullptr;
+    const float *denom = nullptr;
+};
+
 // Carves consecutive 256-byte aligned regions out of a buffer; with a null
 // base it only measures.
 struct Carver {

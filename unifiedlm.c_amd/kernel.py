@@ -200,9 +200,11 @@ def _wgrad(a, b):
     return c
 
 
-def _addmm(c, a, b):
-    """c + a @ b with c fp32, accumulated in the GEMM's epilogue."""
-    return torch.addmm(c, a, b) if a.dtype == c.dtype else torch.addmm(c, a, b, out_dtype=c.dtype)
+def _addmm_(c, a, b):
+    """c += a @ b in place, c fp32, accumulated in the GEMM's epilogue."""
+    if a.dtype == c.dtype:
+        return torch.addmm(c, a, b, out=c)
+    return torch.addmm(c, a, b, out_dtype=c.dtype, out=c)
 
 
 class UnifiedBlockFn(torch.autograd.Function):
@@ -210,8 +212,8 @@ class UnifiedBlockFn(torch.autograd.Function):
 
         h, u   = RMSNorm(x), causal conv(h)            ulm_norm_conv_fwd
         pre, v = u K^T, h W_v^T                         GEMMs in cdt
-        r      = relu^2 address(pre + b)                ulm_addr_fwd
-        wq, y  = w q, x + fast                          ulm_block_fm_fwd
+        denom  = the relu^2 address's row sums of pre + b  ulm_addr_fwd (r not written)
+        wq, y  = w q, x + fast                          ulm_block_fm_fwd (r formed from pre)
         out    = y + wq mu^T                            GEMM accumulating into y
 
     cdt is the GEMM operand dtype: bf16 under bf16 autocast (the reference's
@@ -241,9 +243,9 @@ class UnifiedBlockFn(torch.autograd.Function):
         v = torch.mm(h.view(M, D), vw.t())
         b32 = key_b.float().contiguous() if key_b is not None else None
         le = log_eps.float().reshape(1).contiguous()
-        r = torch.empty(M, A, device=dev, dtype=f32)
         denom = torch.empty(M, device=dev, dtype=f32)
-        call("ulm_addr_fwd", ptr(pre), cd, ptr(b32), ptr(le), ptr(r), ptr(denom), M, A, s)
+        # r itself is never written: the fast memory forms it from pre, bias and denom
+        call("ulm_addr_fwd", ptr(pre), cd, ptr(b32), ptr(le), None, ptr(denom), M, A, s)
         g1 = g.float().reshape(1).contiguous()
         w32 = w.float().contiguous()
         saved_bytes = nat.lib().ulm_fm_saved_bytes(B, T, A, D, cd)
@@ -252,11 +254,11 @@ class UnifiedBlockFn(torch.autograd.Function):
         ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
         qw = torch.empty(M, A, device=dev, dtype=cdt)
         y = torch.empty(M, D, device=dev, dtype=f32)
-        call("ulm_block_fm_fwd", ptr(r), ptr(v), cd, ptr(g1), ptr(w32), ptr(qw), cd, ptr(x32), ptr(y), ptr(saved),
-             saved_bytes, ptr(ws), ws_bytes, B, T, A, D, s)
+        call("ulm_block_fm_fwd", ptr(pre), cd, ptr(b32), ptr(denom), ptr(v), cd, ptr(g1), ptr(w32), ptr(qw), cd,
+             ptr(x32), ptr(y), ptr(saved), saved_bytes, ptr(ws), ws_bytes, B, T, A, D, s)
         del ws, v
-        out = _addmm(y, qw, mw.t())
-        ctx.save_for_backward(x32, rstd, nw, cw, h, u, pre, b32, le, r, denom, g1, w32, saved, qw, kw, vw, mw)
+        out = _addmm_(y, qw, mw.t())
+        ctx.save_for_backward(x32, rstd, nw, cw, h, u, pre, b32, le, denom, g1, w32, saved, qw, kw, vw, mw)
         ctx.meta = (B, T, A, D, Kc, cdt, conv_w.shape, log_eps.shape, g.shape, key_b is not None)
         return out.view(B, T, D)
 
@@ -268,7 +270,7 @@ class UnifiedBlockFn(torch.autograd.Function):
 
     @staticmethod
     def _backward(ctx, dout):
-        x32, rstd, nw, cw, h, u, pre, b32, le, r, denom, g1, w32, saved, qw, kw, vw, mw = ctx.saved_tensors
+        x32, rstd, nw, cw, h, u, pre, b32, le, denom, g1, w32, saved, qw, kw, vw, mw = ctx.saved_tensors
         B, T, A, D, Kc, cdt, cw_shape, le_shape, g_shape, has_bias = ctx.meta
         M = B * T
         dev = x32.device
@@ -290,15 +292,15 @@ class UnifiedBlockFn(torch.autograd.Function):
         dw = torch.empty(A, device=dev, dtype=f32)
         ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D, cd)
         ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
-        call("ulm_block_fm_bwd", ptr(r), ptr(g1), ptr(w32), ptr(saved), saved.numel(), cd, ptr(d16), cd, ptr(dqw), cd,
-             ptr(dr), ptr(dv), cd, ptr(dg), ptr(dw), ptr(ws), ws_bytes, B, T, A, D, s)
+        call("ulm_block_fm_bwd", ptr(pre), cd, ptr(b32), ptr(denom), ptr(g1), ptr(w32), ptr(saved), saved.numel(), cd,
+             ptr(d16), cd, ptr(dqw), cd, ptr(dr), ptr(dv), cd, ptr(dg), ptr(dw), ptr(ws), ws_bytes, B, T, A, D, s)
         del ws, dqw
         dpre = torch.empty_like(pre)
         dbias = torch.empty(A, device=dev, dtype=f32) if has_bias else None
         dle = torch.empty(1, device=dev, dtype=f32)
         ws_bytes = nat.lib().ulm_addr_bwd_workspace_bytes(M, A)
         ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
-        call("ulm_addr_bwd", ptr(pre), cd, ptr(b32), ptr(le), ptr(r), ptr(denom), ptr(dr), ptr(dpre), ptr(dbias),
+        call("ulm_addr_bwd", ptr(pre), cd, ptr(b32), ptr(le), None, ptr(denom), ptr(dr), ptr(dpre), ptr(dbias),
              ptr(dle), ptr(ws), ws_bytes, M, A, s)
         del ws, dr
         du = _mm(dpre, kw, f32)

@@ -125,3 +125,62 @@ def test_model_parameters_match_reference_layout():
     assert names == expect
     assert m.output.weight is m.tok_embeddings.weight
     assert torch.all(m.layers[0].val.weight == 0) and torch.all(m.layers[0].conv.weight[:, 0, -1] == 1)
+
+
+def test_block_entry_points_reject_bad_arguments_without_touching_the_gpu():
+    lib = nat.lib()
+    P = None
+    # norm/conv: taps outside 1..8, h and u in different dtypes, D too wide for the backward
+    st = lib.ulm_norm_conv_fwd(P, nat.ULM_F32, P, P, 9, 1e-5, P, nat.ULM_F32, P, nat.ULM_F32, P, 2, 8, 16, P)
+    assert st == nat.ULM_ERR_INVALID and b"Kc=9" in lib.ulm_last_error()
+    st = lib.ulm_norm_conv_fwd(P, nat.ULM_F32, P, P, 4, 1e-5, P, nat.ULM_BF16, P, nat.ULM_F32, P, 2, 8, 16, P)
+    assert st == nat.ULM_ERR_INVALID and b"share one" in lib.ulm_last_error()
+    st = lib.ulm_norm_conv_bwd(P, nat.ULM_F32, P, P, P, 4, P, nat.ULM_F32, P, nat.ULM_F32, P, P, P, P, P, 0, 2, 8,
+                               1 << 20, P)
+    assert st == nat.ULM_ERR_INVALID and b"too large" in lib.ulm_last_error()
+    assert lib.ulm_norm_conv_bwd_workspace_bytes(2, 8, 1 << 20, 4) == 0
+    # the block's fast memory: address inputs missing, y aliasing x
+    st = lib.ulm_block_fm_fwd(P, nat.ULM_BF16, P, P, P, nat.ULM_BF16, P, P, P, nat.ULM_BF16, P, P, P, 0, P, 0,
+                              2, 64, 32, 32, P)
+    assert st == nat.ULM_ERR_INVALID and b"null pointer" in lib.ulm_last_error()
+    x = ctypes.c_void_p(16)
+    st = lib.ulm_block_fm_fwd(x, nat.ULM_BF16, P, x, x, nat.ULM_BF16, x, x, x, nat.ULM_BF16, x, x, x, 1 << 40, x,
+                              1 << 40, 2, 64, 32, 32, P)
+    assert st == nat.ULM_ERR_INVALID and b"alias" in lib.ulm_last_error()
+    st = lib.ulm_block_fm_bwd(P, 7, P, P, P, P, P, 0, nat.ULM_BF16, P, nat.ULM_BF16, P, nat.ULM_BF16, P, P,
+                              nat.ULM_BF16, P, P, P, 0, 2, 64, 32, 32, P)
+    assert st == nat.ULM_ERR_INVALID and b"bad dtype" in lib.ulm_last_error()
+    # weight gradient: widths must be multiples of 8
+    st = lib.ulm_wgrad(x, x, x, 64, 12, 16, P, 0, P)
+    assert st == nat.ULM_ERR_INVALID and b"multiples of 8" in lib.ulm_last_error()
+    st = lib.ulm_cast(P, 5, P, nat.ULM_F32, 4, P)
+    assert st == nat.ULM_ERR_INVALID and b"bad dtype" in lib.ulm_last_error()
+
+
+def test_block_workspace_sizes():
+    lib = nat.lib()
+    B, T, A, D = 16, 1024, 3072, 768
+    # the forward with a residual always goes through fp32 partials of the 4 key groups
+    assert lib.ulm_block_fm_fwd_workspace_bytes(B, T, A, D) >= 4 * B * T * D * 4
+    # one fp32 partial per split; one round of 256 workgroups of 256 x 256 tiles
+    tiles = (768 // 256) * (3072 // 256)
+    assert lib.ulm_wgrad_workspace_bytes(B * T, 768, 3072) == (256 // tiles) * 768 * 3072 * 4
+    assert lib.ulm_wgrad_workspace_bytes(64, 8, 16) == 0   # too short to split: writes C directly
+    # norm/conv backward: per-tile partials of dnorm_w and dconv_w, plus the column-sum staging
+    assert lib.ulm_norm_conv_bwd_workspace_bytes(B, T, D, 4) >= B * (T // 16) * D * 5 * 4
+
+
+def test_unified_block_input_checks():
+    import kernel
+    D, A = 8, 16
+    args = dict(norm_w=torch.ones(D), conv_w=torch.zeros(D, 1, 4), key_w=torch.zeros(A, D), key_b=torch.zeros(A),
+                log_eps=torch.zeros(()), val_w=torch.zeros(D, D), mu_w=torch.zeros(D, A), g=torch.tensor(-0.1),
+                w=torch.ones(A), norm_eps=1e-5)
+    with pytest.raises(ValueError, match="fp32"):
+        kernel.unified_block(torch.zeros(2, 4, D, dtype=torch.bfloat16), **args)
+    with pytest.raises(ValueError, match="disagree"):
+        kernel.unified_block(torch.zeros(2, 4, D), **{**args, "mu_w": torch.zeros(A, D)})
+    with pytest.raises(ValueError, match="Kc"):
+        kernel.unified_block(torch.zeros(2, 4, D), **{**args, "conv_w": torch.zeros(D, 1, 9)})
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        kernel.unified_block(torch.zeros(2, 4, D), **args)

@@ -209,13 +209,15 @@ def bench_decode(torch, args):
     gen = torch.Generator(device=dev).manual_seed(3)
     prompt = torch.randint(0, V, (N, args.prefill), device=dev, generator=gen)
     # the prompt in one chunked pass (UnifiedLM.prefill), which leaves the same
-    # decode states as stepping through it position by position
-    warm = model.prefill(prompt)   # untimed: first launches and the allocator's first 40 GB
-    del warm
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    logits, states = model.prefill(prompt)
-    torch.cuda.synchronize()
+    # decode states as stepping through it position by position; its GEMMs take
+    # bf16 operands under autocast, as the training step's do
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        warm = model.prefill(prompt)   # untimed: first launches and the allocator's first 40 GB
+        del warm
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        logits, states = model.prefill(prompt)
+        torch.cuda.synchronize()
     t_pre = time.perf_counter()
     log(f"  prefill {args.prefill} positions x {N} sequences in one chunked pass: {(t_pre - t0) * 1e3:.1f} ms")
     nxt = logits.argmax(-1)
@@ -239,7 +241,8 @@ def bench_decode(torch, args):
     log(f"decode {step_ms:.2f} ms/step, {gbps:.0f} GB/s; chunked prefill {pre_ms:.1f} ms "
         f"({N * args.prefill / (pre_ms * 1e-3) / 1e6:.2f} Mtok/s)")
     return {"metric": "decode GB/s", "value": round(gbps, 1), "unit": "GB/s", "ms_per_step": round(step_ms, 3),
-            "tok_per_s": round(N / (step_ms * 1e-3), 1), "prefill": "chunked (UnifiedLM.prefill)",
+            "tok_per_s": round(N / (step_ms * 1e-3), 1),
+            "prefill": "chunked (UnifiedLM.prefill, fused blocks, GEMMs bf16 under autocast)",
             "prefill_ms": round(pre_ms, 2), "prefill_ms_per_position": round(pre_ms / max(args.prefill, 1), 4),
             "prefill_Mtok_per_s": round(N * args.prefill / (pre_ms * 1e-3) / 1e6, 3), "bytes_per_step": bytes_step,
             "state_GB": round(N * L * D * A * 4 / 1e9, 2),

@@ -203,6 +203,16 @@ int ulm_block_fm_bwd(const void *pre, int pre_dtype, const float *bias, const fl
                      float *dr, void *dv, int dv_dtype, float *dg, float *dw, void *workspace,
                      size_t workspace_bytes, int B, int T, int A, int D, void *stream);
 
+/* The block's chunked prefill (UnifiedBlock.prefill, no autograd state):
+ * ulm_block_fm_fwd plus the decode state after position T-1, S (B,D,A) and
+ * c_last (B,A) as for ulm_fm_prefill. A and D multiples of 32; workspace of
+ * ulm_block_fm_prefill_workspace_bytes() bytes (0: unsupported shape). */
+size_t ulm_block_fm_prefill_workspace_bytes(int B, int T, int A, int D, int v_dtype);
+int ulm_block_fm_prefill(const void *pre, int pre_dtype, const float *bias, const float *denom,
+                         const void *v, int v_dtype, const float *g, const float *w, void *qw,
+                         int qw_dtype, const float *x, float *y, float *S, float *c_last, void *workspace,
+                         size_t workspace_bytes, int B, int T, int A, int D, void *stream);
+
 /* Weight gradient of a linear layer over the token dimension: C = A^T B, i.e.
  * C[i][j] = sum_k A[k][i] B[k][j], A (K,N1) and B (K,N2) bf16 row-major,
  * C (N1,N2) fp32 out. The backward of F.linear's weight under bf16 autocast

@@ -88,3 +88,22 @@ def test_model_prefill_short_prompt():
     ref = model.forward_recurrent(x)
     assert rel(logits0, ref[:, 1]) < 1e-2
     assert rel(cont, ref[:, 2:]) < 1e-2
+
+
+def test_model_prefill_under_autocast():
+    """The fused prefill with bf16 GEMM operands (the bench's configuration):
+    logits and the decode states after the prompt against the oracle, 1e-2."""
+    say("UnifiedLM.prefill under bf16 autocast, 100 positions, vs the oracle's states and forward_recurrent")
+    kw = dict(dim=64, n_layers=2, hidden_dim=128, vocab_size=97, max_seq_len=160)
+    model = tiny_model(**kw).cuda()
+    x = torch.randint(0, 97, (2, 120), generator=torch.Generator().manual_seed(6))
+    T0 = 100
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        logits0, states = model.prefill(x[:, :T0].cuda())
+    cont = torch.stack([model.step(x[:, t].cuda(), states) for t in range(T0, 120)], 1)
+    torch.cuda.synchronize()
+    p = oracle_params(model)
+    ref = fm.forward_recurrent(p, x)
+    errs = {"logits": rel(logits0.float(), ref[:, T0 - 1]), "continued": rel(cont, ref[:, T0:])}
+    say(f"  rel errors {errs}")
+    assert max(errs.values()) < 1e-2, errs

@@ -438,3 +438,38 @@ extern "C" int ulm_block_fm_bwd(const void *pre, int pre_dtype, const float *bia
     return fm_backward(rs, g, w, saved, v_dtype, dfast, dfast_dtype, nullptr, dqw, dqw_dtype, dr, dv, dv_dtype, dg, dw,
                        workspace, B, T, A, D, static_cast<hipStream_t>(stream));
 }
+
+// the block's chunked prefill: ulm_block_fm_fwd plus the decode state after T-1
+
+extern "C" size_t ulm_block_fm_prefill_workspace_bytes(int B, int T, int A, int D, int v_dtype) {
+    if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(v_dtype)) return 0;
+    if (!fm_aligned(B, T, A, D)) return 0;
+    return align_up(saved_layout(nullptr, B, T, A, D, v_dtype).bytes, 256) +
+           fwd_layout(nullptr, B, T, A, D, ULM_F32, true).bytes;
+}
+
+extern "C" int ulm_block_fm_prefill(const void *pre, int pre_dtype, const float *bias, const float *denom,
+                                    const void *v, int v_dtype, const float *g, const float *w, void *qw, int qw_dtype,
+                                    const float *x, float *y, float *S, float *c_last, void *workspace,
+                                    size_t workspace_bytes, int B, int T, int A, int D, void *stream) {
+    ULM_REQUIRE(B > 0 && T > 0 && A > 0 && D > 0, "ulm_block_fm_prefill: bad sizes B=%d T=%d A=%d D=%d", B, T, A, D);
+    ULM_REQUIRE(valid_dtype(pre_dtype) && valid_dtype(v_dtype) && valid_dtype(qw_dtype),
+                "ulm_block_fm_prefill: bad dtype %d/%d/%d", pre_dtype, v_dtype, qw_dtype);
+    ULM_REQUIRE(pre && denom && v && g && w && qw && x && y && S && c_last && workspace,
+                "ulm_block_fm_prefill: null pointer");
+    ULM_REQUIRE(static_cast<const void *>(x) != static_cast<const void *>(y), "ulm_block_fm_prefill: y must not alias x");
+    ULM_REQUIRE(fm_aligned(B, T, A, D), "ulm_block_fm_prefill: A=%d and D=%d must be multiples of 32", A, D);
+    ULM_REQUIRE(reinterpret_cast<uintptr_t>(S) % 16 == 0, "ulm_block_fm_prefill: S must be 16-byte aligned");
+    const size_t need = ulm_block_fm_prefill_workspace_bytes(B, T, A, D, v_dtype);
+    ULM_REQUIRE(workspace_bytes >= need, "ulm_block_fm_prefill: workspace of %zu bytes, need %zu", workspace_bytes,
+                need);
+    char *saved = static_cast<char *>(workspace);
+    char *ws = saved + align_up(saved_layout(nullptr, B, T, A, D, v_dtype).bytes, 256);
+    RSrc rs;
+    rs.pre = pre;
+    rs.pre_dt = pre_dtype;
+    rs.bias = bias;
+    rs.denom = denom;
+    return fm_forward(rs, v, v_dtype, g, w, nullptr, qw, qw_dtype, x, y, ULM_F32, saved, ws, S, c_last, B, T, A, D,
+                      static_cast<hipStream_t>(stream));
+}

@@ -344,6 +344,63 @@ def unified_block(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, g, w, n
 # per-token decode (model.py:96-111), N sequences at once, fp32
 
 @torch.no_grad()
+@torch.no_grad()
+def block_prefill(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, g, w, norm_eps, cdt=torch.float32):
+    """UnifiedBlock.forward over a prompt (no autograd), fused as in
+    UnifiedBlockFn, plus what decoding continues from: returns (out, S, c,
+    r_prev, h) with S (B, D, A) and c (B, A) the fast-memory state after the
+    last position (as fm_prefill), r_prev (B, A) fp32 the address at that
+    position and h (B, T, D) the normalised input in cdt (its last positions
+    fill the conv window). A and D must be multiples of 32."""
+    if x.dim() != 3 or x.dtype != torch.float32:
+        raise ValueError(f"x must be (B, T, D) fp32, got {tuple(x.shape)} {x.dtype}")
+    B, T, D = x.shape
+    A = key_w.shape[0]
+    Kc = conv_w.shape[-1]
+    M = B * T
+    nat.require_device(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, g, w)
+    cd = nat.dtype_code(cdt)
+    ws_bytes = nat.lib().ulm_block_fm_prefill_workspace_bytes(B, T, A, D, cd)
+    if ws_bytes == 0:
+        raise ValueError(f"block_prefill: A={A} and D={D} must be multiples of 32")
+    dev = x.device
+    s = nat.stream_of(x)
+    f32 = torch.float32
+    x32 = x.contiguous()
+    nw = norm_w.float().contiguous()
+    cw = conv_w.float().reshape(D, Kc).contiguous()
+    h = torch.empty(B, T, D, device=dev, dtype=cdt)
+    u = torch.empty(B, T, D, device=dev, dtype=cdt)
+    rstd = torch.empty(B, T, device=dev, dtype=f32)
+    call("ulm_norm_conv_fwd", ptr(x32), nat.ULM_F32, ptr(nw), ptr(cw), Kc, float(norm_eps), ptr(h), cd, ptr(u), cd,
+         ptr(rstd), B, T, D, s)
+    kw, vw, mw = (t.to(cdt).contiguous() for t in (key_w, val_w, mu_w))
+    pre = torch.mm(u.view(M, D), kw.t())
+    v = torch.mm(h.view(M, D), vw.t())
+    del u
+    b32 = key_b.float().contiguous() if key_b is not None else None
+    le = log_eps.float().reshape(1).contiguous()
+    denom = torch.empty(M, device=dev, dtype=f32)
+    call("ulm_addr_fwd", ptr(pre), cd, ptr(b32), ptr(le), None, ptr(denom), M, A, s)
+    g1 = g.float().reshape(1).contiguous()
+    w32 = w.float().contiguous()
+    qw = torch.empty(M, A, device=dev, dtype=cdt)
+    y = torch.empty(M, D, device=dev, dtype=f32)
+    S = torch.empty(B, D, A, device=dev, dtype=f32)
+    c = torch.empty(B, A, device=dev, dtype=f32)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    call("ulm_block_fm_prefill", ptr(pre), cd, ptr(b32), ptr(denom), ptr(v), cd, ptr(g1), ptr(w32), ptr(qw), cd,
+         ptr(x32), ptr(y), ptr(S), ptr(c), ptr(ws), ws_bytes, B, T, A, D, s)
+    del ws, v
+    out = _addmm_(y, qw, mw.t())
+    # the address at the last position, the decode state's r_prev
+    pre_last = pre.view(B, T, A)[:, -1].contiguous()
+    r_prev = torch.empty(B, A, device=dev, dtype=f32)
+    dn_last = torch.empty(B, device=dev, dtype=f32)
+    call("ulm_addr_fwd", ptr(pre_last), cd, ptr(b32), ptr(le), ptr(r_prev), ptr(dn_last), B, A, s)
+    return out.view(B, T, D), S, c, r_prev, h
+
+
 def fm_prefill(r, v, g, w):
     """The forward of unified_memory (no autograd) plus the decode state after
     the last position: returns (q, fast, S, c) with S (B, D, A) fp32 =

@@ -22,8 +22,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from kernel import (CHUNK, decode_addr, decode_pre, decode_state, fm_prefill, relu2_address, unified_block,
-                    unified_memory)
+from kernel import (CHUNK, block_prefill, decode_addr, decode_pre, decode_state, fm_prefill, relu2_address,
+                    unified_block, unified_memory)
 
 
 @dataclass
@@ -137,22 +137,33 @@ class UnifiedBlock(nn.Module):
         """`forward` over a whole prompt x (B, T, d) in one chunked pass, also
         returning the decode state after position T-1: the state that T calls of
         `step` would leave (model.py:88-111), with S and c from the chunked
-        kernels (bf16 operands, fp32 accumulation) instead of T fp32 updates."""
-        h = self.norm(x)
-        u = self.conv(h.transpose(1, 2))[..., : h.size(1)].transpose(1, 2)
-        r = self.code(u)
-        v = self.val(h)
-        w = self._w()
-        q, fast, S, c = fm_prefill(r, v, -self.log_rate.exp(), w)
-        out = x + self.mu((q * w).type_as(x)) + fast.type_as(x)
+        kernels (bf16 operands, fp32 accumulation) instead of T fp32 updates.
+        With A and d multiples of 32 and an fp32 x the block runs fused
+        (kernel.block_prefill), its GEMMs in the autocast dtype."""
         B, T, d = x.shape
+        A = self.mu.in_features
+        w = self._w()
+        g = -self.log_rate.exp()
+        if x.dtype == torch.float32 and A % 32 == 0 and d % 32 == 0:
+            cdt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else torch.float32
+            with torch.autocast("cuda", enabled=False):
+                out, S, c, r_prev, h = block_prefill(x, self.norm.weight, self.conv.weight, self.key.weight,
+                                                     self.key.bias, self.log_eps, self.val.weight, self.mu.weight, g,
+                                                     w, self.norm.eps, cdt)
+        else:
+            h = self.norm(x)
+            u = self.conv(h.transpose(1, 2))[..., : h.size(1)].transpose(1, 2)
+            r = self.code(u)
+            v = self.val(h)
+            q, fast, S, c = fm_prefill(r, v, g, w)
+            out = x + self.mu((q * w).type_as(x)) + fast.type_as(x)
+            r_prev = r[:, -1, :].float().contiguous()
         kw = self.conv.kernel_size[0] - 1
         buf = torch.zeros(B, d, kw, device=x.device, dtype=torch.float32)
         if kw > 0:
             tail = h.float()[:, max(0, T - kw):, :].transpose(1, 2)   # the last (up to) kw positions, oldest first
             buf[:, :, kw - tail.size(-1):] = tail
-        state = {"buf": buf, "S": S, "c": c, "r_prev": r[:, -1, :].float().contiguous(),
-                 "params": self._step_params(x.device)}
+        state = {"buf": buf, "S": S, "c": c, "r_prev": r_prev, "params": self._step_params(x.device)}
         return out, state
 
     @torch.no_grad()

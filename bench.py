@@ -13,6 +13,11 @@ Inputs are resident in HBM before the timed region. Prints one JSON line:
              the 2516.6 TFLOP/s dense bf16 peak
   cpu_baseline  the oracle's chunked PyTorch form on the host cores (fp32,
              fwd+bwd of one block at B=1, T=1024), scaled to the 12-block step
+  block      whole UnifiedBlocks (fused) fwd+bwd over the same shape under bf16
+             autocast, and the same blocks op by op
+  train_step one training step of the whole 12-layer UnifiedLM (embedding,
+             fused blocks, 32000-way classifier, cross-entropy), fwd+bwd, bf16
+             autocast, token ids uniform
   decode     batched recurrent decode at the 110M shape: 256 sequences, 12
              blocks, fp32 state (29 GB); the 512-position prompt in one
              chunked pass (UnifiedLM.prefill), then greedy steps; GB/s of the
@@ -55,6 +60,7 @@ def parse():
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-block", action="store_true")
+    p.add_argument("--no-step", action="store_true")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                    help="first run one plain fp32 copy kernel over MB megabytes (a known-size reference for "
                         "hardware byte counters)")
@@ -156,6 +162,50 @@ def bench_block(torch, args):
             "tflops": round(ftok * B * T / (ms * 1e-3) / 1e12, 2),
             "composed_ms_per_step": round(ms_c, 3), "composed_Mtok_per_s": round(B * T / (ms_c * 1e-3) / 1e6, 4),
             "speedup_vs_composed": round(ms_c / ms, 3)}
+
+
+def bench_train_step(torch, args):
+    """One training step of the whole 12-layer UnifiedLM at the 110M shape
+    (model.py:149-162): embedding, the fused blocks, final RMSNorm, the tied
+    32000-way classifier and the cross-entropy loss, forward + backward under
+    bf16 autocast, token ids uniform over the vocabulary; no optimizer step."""
+    import workloads
+    from model import ModelArgs, UnifiedLM
+    cfg = workloads.SHAPES[args.shape]
+    B, T, D, A, L = cfg["B"], cfg["T"], cfg["D"], cfg["A"], cfg["blocks"]
+    V = workloads.DECODE_110M["vocab"]
+    dev = torch.device("cuda:0")
+    log(f"training step {args.shape}: B={B} T={T} D={D} A={A} blocks={L} vocab={V}, bf16 autocast")
+    torch.manual_seed(1)
+    model = UnifiedLM(ModelArgs(dim=D, n_layers=L, hidden_dim=A, vocab_size=V, max_seq_len=T))
+    workloads.init_decode_model(model, seed=44)
+    model = model.to(dev).train()
+    gen = torch.Generator(device=dev).manual_seed(9)
+    tokens = torch.randint(0, V, (B, T + 1), device=dev, generator=gen)
+    x, y = tokens[:, :-1].contiguous(), tokens[:, 1:].contiguous()
+
+    def step():
+        for prm in model.parameters():
+            prm.grad = None
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            model(x, y)
+        model.last_loss.backward()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    # per token: every block's GEMMs and fast memory, plus the classifier (2 V D forward, twice that backward)
+    ftok = workloads.block_flops_per_token(T, A, D) * L + 6 * V * D
+    log(f"training step {ms:.2f} ms, loss {model.last_loss.item():.3f}")
+    return {"workload": f"UnifiedLM {args.shape} training step fwd+bwd: embedding, {L} fused blocks, classifier "
+                        f"over {V} tokens, cross-entropy; bf16 autocast; no optimizer",
+            "ms_per_step": round(ms, 3), "Mtok_per_s": round(B * T / (ms * 1e-3) / 1e6, 4),
+            "tflops": round(ftok * B * T / (ms * 1e-3) / 1e12, 2), "loss": round(model.last_loss.item(), 4)}
 
 
 def bench_cpu_baseline(torch, train):
@@ -274,6 +324,7 @@ def main():
     train = bench_training(torch, args)
     cpu = None if args.no_cpu else bench_cpu_baseline(torch, train)
     block = None if args.no_block else bench_block(torch, args)
+    train_step = None if args.no_step else bench_train_step(torch, args)
     decode = None if args.no_decode else bench_decode(torch, args)
     out = {
         "metric": METRIC,
@@ -296,6 +347,7 @@ def main():
         "roofline": train["roofline"],
         "cpu_baseline": cpu,
         "block": block,
+        "train_step": train_step,
         "decode": decode,
     }
     print(json.dumps(out), flush=True)

@@ -105,7 +105,8 @@ int with_rsrc(const RSrc &src, F &&f) {
 // copies; qR, kR in the R layout and qQ, kQ in the Q layout (the chunked
 // kernel's operand tiles; A % 32 == 0); c_last = c at position T-1 (B, A), the
 // decode state after the sequence. Positions past T are zero in R and Q.
-template <class RS>
+// QW: the dtype of the w q output (-1 none, else a ulm_dtype); HAS_Q: the fp32 q output.
+template <class RS, int QW, bool HAS_Q>
 __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__restrict__ w,
                                                         const float *__restrict__ g, float *__restrict__ q,
                                                         void *__restrict__ qw, int qw_dt,
@@ -164,8 +165,10 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
                 if (c_last && t == T - 1) c_last[bs * A + a] = ct;
                 qb = f32_to_bf16_bits(qt);
                 kb = f32_to_bf16_bits(kv[i]);
-                if (q) q[o] = qt;
-                if (qw) store_from_f32(qw, o, qw_dt, qt * wa);
+                if constexpr (HAS_Q) q[o] = qt;
+                if constexpr (QW == ULM_F32) static_cast<float *>(qw)[o] = qt * wa;
+                if constexpr (QW == ULM_BF16) static_cast<uint16_t *>(qw)[o] = f32_to_bf16_bits(qt * wa);
+                if constexpr (QW == ULM_F16) static_cast<_Float16 *>(qw)[o] = static_cast<_Float16>(qt * wa);
                 if (q16n) {
                     q16n[o] = qb;
                     k16n[o] = kb;
@@ -379,9 +382,30 @@ int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, 
     const bool tiled = qR || kR || qQ || kQ;
     if (tiled && !(qR && kR && qQ && kQ && A % 32 == 0))
         return fail(ULM_ERR_INVALID, "fwd stats: tiled copies need all four outputs and A %% 32 == 0");
+    if (qw && !valid_dtype(qw_dt)) return fail(ULM_ERR_INVALID, "fwd stats: bad w q dtype %d", qw_dt);
+    const int qwk = qw ? qw_dt : -1;
     return with_rsrc(src, [&](auto rs) {
-        fwd_stats_kernel<decltype(rs)><<<dim3((A + kSlots - 1) / kSlots, B), 256, 0, s>>>(
-            rs, w, g, q, qw, qw_dt, q16n, k16n, qR, kR, qQ, kQ, nck, c_last, T, A, NT);
+        using RS = decltype(rs);
+        const dim3 grid((A + kSlots - 1) / kSlots, B);
+#define ULM_FWD_STATS(QWK, HQ)                                                                                    \
+    fwd_stats_kernel<RS, QWK, HQ><<<grid, 256, 0, s>>>(rs, w, g, q, qw, qw_dt, q16n, k16n, qR, kR, qQ, kQ, nck,   \
+                                                       c_last, T, A, NT)
+        if (q) {
+            switch (qwk) {
+            case ULM_F32: ULM_FWD_STATS(ULM_F32, true); break;
+            case ULM_BF16: ULM_FWD_STATS(ULM_BF16, true); break;
+            case ULM_F16: ULM_FWD_STATS(ULM_F16, true); break;
+            default: ULM_FWD_STATS(-1, true); break;
+            }
+        } else {
+            switch (qwk) {
+            case ULM_F32: ULM_FWD_STATS(ULM_F32, false); break;
+            case ULM_BF16: ULM_FWD_STATS(ULM_BF16, false); break;
+            case ULM_F16: ULM_FWD_STATS(ULM_F16, false); break;
+            default: ULM_FWD_STATS(-1, false); break;
+            }
+        }
+#undef ULM_FWD_STATS
         return check_launch("fwd_stats_kernel");
     });
 }

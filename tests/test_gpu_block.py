@@ -192,3 +192,71 @@ def test_wgrad_matches_fp32_product(K, N1, N2):
     err = rel(c, ref)
     say(f"  rel error {err:.2e}")
     assert err < 1e-5
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+def test_fused_model_is_causal_and_finite(autocast):
+    """test_all.py:119-137 on the native path: perturbing tokens from position
+    25 on leaves the logits before 25 unchanged (every reduction on the path
+    is within a row or over earlier positions, in a fixed order), and a
+    training step's gradients are finite."""
+    say(f"fused UnifiedLM causality and finite gradients, autocast={autocast}")
+    model = tiny_model(dim=64, n_layers=2, hidden_dim=128, vocab_size=97, max_seq_len=100).cuda().train()
+    gen = torch.Generator().manual_seed(12)
+    x = torch.randint(0, 97, (2, 90), generator=gen)
+    x2 = x.clone()
+    x2[:, 25:] = torch.randint(0, 97, (2, 65), generator=gen)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        a = model(x.cuda(), x.cuda()).float()     # with targets: the logits of every position
+        b = model(x2.cuda(), x2.cuda()).float()
+    diff = (a[:, :25] - b[:, :25]).abs().max().item()
+    say(f"  max |logit change| before position 25: {diff}; after: {(a[:, 25:] - b[:, 25:]).abs().max().item():.3f}")
+    assert diff == 0.0
+    assert (a[:, 25:] - b[:, 25:]).abs().max().item() > 0
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        model(x.cuda(), x.cuda())
+    model.last_loss.backward()
+    for name, p in model.named_parameters():
+        assert p.grad is not None and torch.isfinite(p.grad).all(), name
+
+
+def test_native_reductions_are_deterministic():
+    """The fast-memory backward (dg, dw), the split-K weight gradient and the
+    norm/conv weight gradients sum in a fixed order: repeated calls agree
+    bit for bit."""
+    import kernel
+    from helpers import fm_inputs
+    say("determinism of ulm_fm_bwd, ulm_wgrad, ulm_norm_conv_bwd")
+    r, v, g, w = fm_inputs(2, 256, 256, 128, seed=5, device="cuda")
+    r, v, g, w = (t.float().requires_grad_() for t in (r, v, g, w))
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    dq, df = torch.randn(2, 256, 256, device="cuda", generator=gen), torch.randn(2, 256, 128, device="cuda", generator=gen)
+    grads = []
+    for _ in range(2):
+        q, fast = kernel.unified_memory(r, v, g, w)
+        grads.append(torch.autograd.grad((q, fast), (r, v, g, w), (dq, df)))
+    for a_, b_ in zip(*grads):
+        assert torch.equal(a_, b_)
+    a = torch.randn(4096, 256, device="cuda", generator=gen).to(torch.bfloat16)
+    b = torch.randn(4096, 512, device="cuda", generator=gen).to(torch.bfloat16)
+    c1, c2 = kernel._wgrad(a, b), kernel._wgrad(a, b)
+    assert torch.equal(c1, c2)
+    B, T, D, Kc = 2, 300, 256, 4
+    x = torch.randn(B, T, D, device="cuda", generator=gen)
+    nw, cw = torch.ones(D, device="cuda"), torch.randn(D, Kc, device="cuda", generator=gen)
+    du = torch.randn(B, T, D, device="cuda", generator=gen)
+    h, u = torch.empty_like(x), torch.empty_like(x)
+    rstd = torch.empty(B, T, device="cuda")
+    s = nat.stream_of(x)
+    call("ulm_norm_conv_fwd", ptr(x), nat.ULM_F32, ptr(nw), ptr(cw), Kc, 1e-5, ptr(h), nat.ULM_F32, ptr(u),
+         nat.ULM_F32, ptr(rstd), B, T, D, s)
+    wsb = nat.lib().ulm_norm_conv_bwd_workspace_bytes(B, T, D, Kc)
+    ws = torch.empty(wsb, device="cuda", dtype=torch.uint8)
+    outs = []
+    for _ in range(2):
+        dx, dnw, dcw = torch.empty_like(x), torch.empty(D, device="cuda"), torch.empty(D, Kc, device="cuda")
+        call("ulm_norm_conv_bwd", ptr(x), nat.ULM_F32, ptr(rstd), ptr(nw), ptr(cw), Kc, ptr(du), nat.ULM_F32, None,
+             nat.ULM_F32, None, ptr(dx), ptr(dnw), ptr(dcw), ptr(ws), wsb, B, T, D, s)
+        outs.append((dx, dnw, dcw))
+    for a_, b_ in zip(*outs):
+        assert torch.equal(a_, b_)

@@ -170,6 +170,36 @@ def dg_identity(r, v, g, w, dq_out, dfast):
     return ((pos * (q * dq_f + dc * (c - w))).sum() - (pos * k * (dk_f + dk_c)).sum()), P
 
 
+def dg_bf16_floor(r, v, g, w, dq_out, dfast, round_bf16=True):
+    """d loss / d g as a bf16-operand kernel of this path computes it, in exact
+    arithmetic otherwise: the fast-read products take v, dfast, q and k rounded
+    to bf16, and the positional identity (kernel.py:155-175, with tau =
+    (T-1)/2) weights the dq_f and dk_f terms with the same rounded q and k.
+    With round_bf16=False it is the exact dg (pinned against autograd in
+    tests/test_oracle.py). Its distance from the exact dg is the error that
+    bf16 operands alone leave in dg, before any accumulation error: the floor
+    for a kernel with bf16 MFMA operands. dg is the small difference of two
+    large positional sums, so for inputs without the structure of a training
+    loss (white-noise upstream gradients, long T) this floor can exceed 1e-2."""
+    r, v, w, g = r.double(), v.double(), w.double(), g.double()
+    rnd = (lambda x: x.to(torch.bfloat16).double()) if round_bf16 else (lambda x: x)
+    lam = torch.exp(g)
+    B, T, A = r.shape
+    k = shift_keys(r)
+    M = decay_mask(T, lam)
+    c = w + M @ k
+    q = r / c
+    V, DO, K, Q = rnd(v), rnd(dfast.double()), rnd(k), rnd(q)
+    S = (DO @ V.transpose(1, 2)) * M
+    dq_f = S @ K
+    dk_f = S.transpose(1, 2) @ Q
+    dq = dq_f + (dq_out.double() if dq_out is not None else 0.0)
+    dc = -dq * q / c
+    dk_c = M.transpose(0, 1) @ dc
+    pos = torch.arange(T, dtype=torch.float64, device=r.device)[None, :, None] - 0.5 * (T - 1)
+    return (pos * (Q * dq_f + dc * (c - w))).sum() - (pos * (K * dk_f + k * dk_c)).sum()
+
+
 # ---------------------------------------------------------------------------
 # relu^2 slot address (model.py:70-72) and the block (model.py:31-42, 77-85)
 

@@ -118,6 +118,7 @@ BLOCK_CASES = [
     (1, 70, 96, 320, False),      # A, D multiples of 32: the K-group products
     (2, 256, 128, 256, True),
     (1, 512, 768, 3072, True),    # 110M block shape
+    (1, 1024, 512, 2048, True),   # 42M block shape, one row of 1024 positions
 ]
 
 

@@ -75,6 +75,9 @@ OP_CASES = [
     (4, 256, 1152, 288, torch.bfloat16),   # 15M-shape block, fewer rows
     (2, 200, 128, 64, torch.float32),      # K-group kernels with a ragged last chunk
     (1, 512, 3072, 768, torch.bfloat16),   # 110M-shape block, one row of 512 positions
+    (8, 512, 128, 64, torch.float32),      # 260K-shape block (all 8 rows of 512 positions)
+    (1, 1024, 2048, 512, torch.bfloat16),  # 42M-shape block, one row: 3 key groups of 704 / 704 / 640 slots;
+                                           # dg there is ill-conditioned under white-noise gradients (see below)
 ]
 
 
@@ -101,8 +104,15 @@ def test_unified_memory_matches_oracle(B, T, A, D, vdt):
     assert rel(q, qr) < 1e-5
     assert rel(fast, fr) < 1e-2
     errs = {"dr": rel(rg.grad, dr), "dv": rel(vg.grad, dv), "dg": rel(gg.grad, dgr), "dw": rel(wg.grad, dw)}
-    say(f"  rel errors {errs}")
-    assert max(errs.values()) < 1e-2, errs
+    # dg is the small difference of two large positional sums: under these
+    # white-noise upstream gradients bf16 operands alone can move it by more
+    # than 1e-2 (T = 1024 at the 42M shape: 15% in exact arithmetic). It is
+    # held to 1e-2 or to that floor (oracle.fastmem.dg_bf16_floor), whichever
+    # is larger; every other output and gradient to 1e-2.
+    floor = rel(fm.dg_bf16_floor(r, vr, g, w, dq, df), dgr)
+    say(f"  rel errors {errs}, dg floor of bf16 operands {floor:.2e}")
+    tol = {"dr": 1e-2, "dv": 1e-2, "dw": 1e-2, "dg": max(1e-2, floor)}
+    assert all(errs[n] < tol[n] for n in errs), (errs, floor)
 
 
 @pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])

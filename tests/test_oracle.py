@@ -230,6 +230,21 @@ def test_dg_identity_matches_autograd():
     assert abs(dg.item() - dg_id.item()) < 1e-10 * max(1.0, abs(dg.item()))
 
 
+def test_dg_bf16_floor_without_rounding_is_the_exact_dg():
+    """dg_bf16_floor's positional identity (tau = (T-1)/2, the kernel's) with
+    float64 operands equals autograd's dg; rounding only its operands then
+    moves it by the bf16 floor the GPU dg check allows."""
+    r, v, g, w = _inputs(B=2, T=70, A=6, D=4)
+    gen = torch.Generator().manual_seed(11)
+    dq = torch.randn(r.shape, generator=gen, dtype=torch.float64)
+    df = torch.randn(v.shape, generator=gen, dtype=torch.float64)
+    _, _, dg, _ = fm.fast_memory_grads(r, v, g, w, dq, df, "dense")
+    exact = fm.dg_bf16_floor(r, v, g, w, dq, df, round_bf16=False)
+    assert abs(dg.item() - exact.item()) < 1e-10 * max(1.0, abs(dg.item()))
+    rounded = fm.dg_bf16_floor(r, v, g, w, dq, df)
+    assert 0 < abs(rounded.item() - dg.item()) < 0.1 * abs(dg.item())
+
+
 # ----- model level (test_all.py:100-137)
 
 def _tokens(B=3, T=40, V=97, seed=0):

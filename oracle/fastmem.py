@@ -27,6 +27,9 @@ How each function is pinned (tests/test_oracle.py):
                         gradcheck of its backward formula.
   fast_memory_grads     torch.autograd.gradcheck at tiny shapes and the
                         reference's dg identity (kernel.py:173-175).
+  dg_bf16_floor         with rounding off equals autograd's dg (the identity
+                        with the kernel's tau); rounding its operands to bf16
+                        is the only difference.
   lm_forward            parallel == forward_recurrent (test_all.py:110-116),
                         causality (test_all.py:119-128), finite grads.
   forward_recurrent     logits of the reference's own run.c (compiled under

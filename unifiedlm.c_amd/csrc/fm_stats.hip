@@ -33,23 +33,29 @@ __device__ __forceinline__ float pow_int(float x, int e) {
     return r;
 }
 
-// Sources of r for the kernels below (RSrc): loads are unconditional, at a
-// clamped index, and masked after, so none waits inside a branch.
+// Sources of r for the kernels below (RSrc). at(row, ac, ...) reads row
+// `row` (wave-uniform, clamped by the caller to a valid row) at slot `ac`
+// (clamped per lane); loads are unconditional and masked after, so none waits
+// inside a branch.
 struct RTensor {
     const float *r;
     __device__ __forceinline__ float slot_const(int) const { return 0.f; }
     static constexpr bool kRowConst = false;
     __device__ __forceinline__ float row_const(size_t, bool) const { return 1.f; }
-    __device__ __forceinline__ float at(size_t row, int a, int A, float, float, bool ok) const {
-        const float v = r[(ok ? row : 0) * A + (ok ? a : 0)];
+    __device__ __forceinline__ float at(size_t row, uint32_t ac, int A, float, float, bool ok) const {
+        const float v = ld_row(r + row * A, 4u * ac);
         return ok ? v : 0.f;
     }
 };
 
-template <typename TP> __device__ __forceinline__ float ld_pre(const TP *p, size_t i);
-template <> __device__ __forceinline__ float ld_pre<float>(const float *p, size_t i) { return p[i]; }
-template <> __device__ __forceinline__ float ld_pre<uint16_t>(const uint16_t *p, size_t i) { return bf16_to_f32(p[i]); }
-template <> __device__ __forceinline__ float ld_pre<_Float16>(const _Float16 *p, size_t i) { return static_cast<float>(p[i]); }
+template <typename TP> __device__ __forceinline__ float ld_pre(const TP *row, uint32_t ac);
+template <> __device__ __forceinline__ float ld_pre<float>(const float *row, uint32_t ac) { return ld_row(row, 4u * ac); }
+template <> __device__ __forceinline__ float ld_pre<uint16_t>(const uint16_t *row, uint32_t ac) {
+    return bf16_to_f32(ld_row(row, 2u * ac));
+}
+template <> __device__ __forceinline__ float ld_pre<_Float16>(const _Float16 *row, uint32_t ac) {
+    return static_cast<float>(ld_row(row, 2u * ac));
+}
 
 // r = relu(pre + bias)^2 * (1 / denom[row]); addr_bwd_kernel forms r with the
 // same operations, so every kernel of the block sees the same r. The
@@ -62,9 +68,8 @@ struct RAddr {
     __device__ __forceinline__ float slot_const(int a) const { return bias ? bias[a] : 0.f; }
     static constexpr bool kRowConst = true;
     __device__ __forceinline__ float row_const(size_t row, bool tok) const { return 1.f / denom[tok ? row : 0]; }
-    __device__ __forceinline__ float at(size_t row, int a, int A, float b, float inv, bool ok) const {
-        const size_t rr = ok ? row : 0;
-        float p = ld_pre(pre, rr * A + (ok ? a : 0)) + b;
+    __device__ __forceinline__ float at(size_t row, uint32_t ac, int A, float b, float inv, bool ok) const {
+        float p = ld_pre(pre + row * A, ac) + b;
         p = p > 0.f ? p : 0.f;
         const float v = (p * p) * inv;
         return ok ? v : 0.f;
@@ -87,6 +92,10 @@ __device__ __forceinline__ float seg_row_consts(const RS &rs, size_t row_t0, int
 __device__ __forceinline__ float lane_value(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
+
+// Row b T + t of a (B, T, ...) tensor when 0 <= t < T, else row 0: the clamp
+// depends on wave-uniform values only, so the row stays in scalar registers.
+__device__ __forceinline__ size_t urow(size_t b, int t, int T) { return (t >= 0 && t < T) ? b * T + t : 0; }
 
 // Calls f(source) with the RTensor or RAddr<T> that src describes.
 template <class F>
@@ -122,6 +131,7 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
     const int a0 = blockIdx.x * kSlots;
     const int a = a0 + s;
     const bool va = a < A;
+    const uint32_t ac = va ? a : 0;   // the lane's slot, clamped for loads
     const int b = blockIdx.y;
     const size_t bs = blockIdx.y;
     const float lam = __expf(g[0]);
@@ -136,9 +146,9 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
             const int t = t0 + i;
-            rv[i] = rs.at(bs * T + t, a, A, rb, lane_value(seg_c, i), va && t < T);
+            rv[i] = rs.at(urow(bs, t, T), ac, A, rb, lane_value(seg_c, i), va && t < T);
         }
-        kv[0] = rs.at(bs * T + t0 - 1, a, A, rb, lane_value(seg_c, kSeg), va && t0 >= 1 && t0 - 1 < T);
+        kv[0] = rs.at(urow(bs, t0 - 1, T), ac, A, rb, lane_value(seg_c, kSeg), va && t0 >= 1 && t0 - 1 < T);
 #pragma unroll
         for (int i = 1; i < kSeg; ++i) kv[i] = rv[i - 1];
         float acc = 0.f;
@@ -160,18 +170,18 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
             pw *= lam;
             uint16_t qb = 0, kb = 0;   // positions past T are zero in the tiled copies
             if (va && t < T) {
-                const size_t o = (bs * T + t) * A + a;
+                const size_t ro = (bs * T + t) * A;   // wave-uniform row offset
                 const float qt = rv[i] / ct;
                 if (c_last && t == T - 1) c_last[bs * A + a] = ct;
                 qb = f32_to_bf16_bits(qt);
                 kb = f32_to_bf16_bits(kv[i]);
-                if constexpr (HAS_Q) q[o] = qt;
-                if constexpr (QW == ULM_F32) static_cast<float *>(qw)[o] = qt * wa;
-                if constexpr (QW == ULM_BF16) static_cast<uint16_t *>(qw)[o] = f32_to_bf16_bits(qt * wa);
-                if constexpr (QW == ULM_F16) static_cast<_Float16 *>(qw)[o] = static_cast<_Float16>(qt * wa);
+                if constexpr (HAS_Q) st_row(q + ro, 4u * ac, qt);
+                if constexpr (QW == ULM_F32) st_row(static_cast<float *>(qw) + ro, 4u * ac, qt * wa);
+                if constexpr (QW == ULM_BF16) st_row(static_cast<uint16_t *>(qw) + ro, 2u * ac, f32_to_bf16_bits(qt * wa));
+                if constexpr (QW == ULM_F16) st_row(static_cast<_Float16 *>(qw) + ro, 2u * ac, static_cast<_Float16>(qt * wa));
                 if (q16n) {
-                    q16n[o] = qb;
-                    k16n[o] = kb;
+                    st_row(q16n + ro, 2u * ac, qb);
+                    st_row(k16n + ro, 2u * ac, kb);
                 }
             }
             sq[j * kSeg + i][s] = qb;
@@ -218,10 +228,10 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
 // The extra gradient of q, by template so that every load is a plain one:
 // XQ = 0 none, 1 dq_out fp32, 2/3/4 d(w q) as fp32/bf16/fp16.
 template <int XQ>
-__device__ __forceinline__ float load_xq(const void *p, size_t o) {
-    if constexpr (XQ == 1 || XQ == 2) return static_cast<const float *>(p)[o];
-    else if constexpr (XQ == 3) return bf16_to_f32(static_cast<const uint16_t *>(p)[o]);
-    else if constexpr (XQ == 4) return static_cast<float>(static_cast<const _Float16 *>(p)[o]);
+__device__ __forceinline__ float load_xq(const void *p, size_t ro, uint32_t ac) {
+    if constexpr (XQ == 1 || XQ == 2) return ld_row(static_cast<const float *>(p) + ro, 4u * ac);
+    else if constexpr (XQ == 3) return bf16_to_f32(ld_row(static_cast<const uint16_t *>(p) + ro, 2u * ac));
+    else if constexpr (XQ == 4) return static_cast<float>(ld_row(static_cast<const _Float16 *>(p) + ro, 2u * ac));
     else return 0.f;
 }
 
@@ -240,6 +250,7 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
     const int j = __builtin_amdgcn_readfirstlane(threadIdx.x / kSlots);   // wave-uniform (kSlots = wave size)
     const int a = blockIdx.x * kSlots + s;
     const bool va = a < A;
+    const uint32_t ac = va ? a : 0;   // the lane's slot, clamped for loads
     const size_t b = blockIdx.y;
     const float lam = __expf(g[0]);
     const float lam16 = pow_int(lam, kSeg);
@@ -253,22 +264,26 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
     for (int n = NT - 1; n >= 0; --n) {
         const int t0 = n * ULM_CHUNK + j * kSeg;
         const float seg_c = seg_row_consts(rs, b * T + t0, t0, T, s);
-        float rv[kSeg], kv[kSeg], cv[kSeg], dq[kSeg], dc[kSeg], dqfv[kSeg], dqwv[kSeg];
+        // xv: the extra gradient of q (dq_out or d(w q), by XQ); dq is formed
+        // from dqfv and xv where q is, so neither outlives the reverse scan
+        float rv[kSeg], kv[kSeg], cv[kSeg], dqc[kSeg], dqfv[kSeg], xv[kSeg], dkfv[kSeg];
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
             const int t = t0 + i;
             const bool ok = va && t < T;
-            const size_t o = (b * T + t) * A + a;
-            rv[i] = rs.at(b * T + t, a, A, rb, lane_value(seg_c, i), ok);
-            dqfv[i] = ok ? dqf[o] : 0.f;
-            // an unconditional load (index 0 when out of range) keeps the 16-bit
-            // conversions out of a branch that would wait on each load
-            float x = XQ != 0 ? load_xq<XQ>(xq, ok ? o : 0) : 0.f;
-            x = ok ? x : 0.f;
-            dqwv[i] = XQ >= 2 ? x : 0.f;
-            dq[i] = dqfv[i] + (XQ == 1 ? x : wa * dqwv[i]);
+            const size_t ro = urow(b, t, T) * A;   // wave-uniform row offset
+            rv[i] = rs.at(urow(b, t, T), ac, A, rb, lane_value(seg_c, i), ok);
+            // unconditional loads at the clamped row and slot keep the waits and
+            // the 16-bit conversions out of a branch; dk_f is loaded with the
+            // rest so that all of the chunk's reads are in flight together
+            const float f = ld_row(dqf + ro, 4u * ac);
+            dqfv[i] = ok ? f : 0.f;
+            const float x = XQ != 0 ? load_xq<XQ>(xq, ro, ac) : 0.f;
+            xv[i] = ok ? x : 0.f;
+            const float fk = ld_row(dkf + ro, 4u * ac);
+            dkfv[i] = ok ? fk : 0.f;
         }
-        kv[0] = rs.at(b * T + t0 - 1, a, A, rb, lane_value(seg_c, kSeg), va && t0 >= 1 && t0 - 1 < T);
+        kv[0] = rs.at(urow(b, t0 - 1, T), ac, A, rb, lane_value(seg_c, kSeg), va && t0 >= 1 && t0 - 1 < T);
 #pragma unroll
         for (int i = 1; i < kSeg; ++i) kv[i] = rv[i - 1];
         // rebuild n (hence c) inside the chunk from its checkpoint
@@ -290,37 +305,45 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
             pw *= lam;
         }
         // dc and its reverse decayed scan. The dw terms and the q-side dg terms
-        // are summed here, where q is formed, so dq_f, d(w q) and dc die with
-        // this loop (positions past T contribute exact zeros to every term).
+        // are summed here, where q is formed, and dq / c is kept for dr, so c,
+        // dq_f, the extra gradient and dc die with this loop (positions past T
+        // contribute exact zeros to every term).
         float rl[kSeg];
         float racc = 0.f;
+        // dg weights position t0 + i by (t0 - tau) + i: sums of e and i e per segment
+        double e0 = 0.0, e1 = 0.0;
 #pragma unroll
         for (int i = kSeg - 1; i >= 0; --i) {
             // q = r / c, recomputed with the forward's operations (c is rebuilt
             // exactly from its checkpoint), so q is not read back from HBM
             const float qt = rv[i] / cv[i];
-            dc[i] = -dq[i] * qt / cv[i];
-            racc = dc[i] + lam * racc;
+            const float dq = dqfv[i] + (XQ == 1 ? xv[i] : wa * xv[i]);
+            const float dc = -dq * qt / cv[i];
+            dqc[i] = dq / cv[i];
+            racc = dc + lam * racc;
             rl[i] = racc;
-            dw_acc += dc[i];
-            if constexpr (XQ >= 2) dw_acc += qt * dqwv[i];
+            dw_acc += dc;
+            if constexpr (XQ >= 2) dw_acc += qt * xv[i];
             // The fast-read terms take the bf16 q and k that the dq and dk
             // products contracted with, so each (t, s) pair enters both sums
             // with the same value and the position weights cancel to t - s.
             const float q16 = bf16_to_f32(f32_to_bf16_bits(qt));
-            const double pos = static_cast<double>(t0 + i) - tau;
-            dg_acc += pos * static_cast<double>(q16 * dqfv[i] + dc[i] * (cv[i] - wa));
+            const double e = static_cast<double>(q16 * dqfv[i] + dc * (cv[i] - wa));
+            e0 += e;
+            e1 += i * e;
         }
+        // finish the q-side sums here: left to the compiler, they sink past the
+        // barriers and keep q, dq_f, the extra gradient, dc and c alive through
+        // the final phase
+        asm volatile("" : "+v"(e0), "+v"(e1), "+v"(dw_acc));
         tot[j][s] = racc;
         __syncthreads();
         float rj = dkc_next;
         for (int m = 3; m > j; --m) rj = tot[m][s] + lam16 * rj;
-        float dkfv[kSeg], dkcv[kSeg];   // dkt = dkfv + dkcv
+        float dkcv[kSeg];   // dkt = dkfv + dkcv
         float pr = lam;   // lam^(16-i) for i = 15 .. 0
 #pragma unroll
         for (int i = kSeg - 1; i >= 0; --i) {
-            const int t = t0 + i;
-            dkfv[i] = (va && t < T) ? dkf[(b * T + t) * A + a] : 0.f;
             dkcv[i] = rl[i] + pr * rj;
             pr *= lam;
         }
@@ -332,11 +355,13 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
         for (int i = 0; i < kSeg; ++i) {
             const int t = t0 + i;
             const float nxt = (i + 1 < kSeg) ? dkfv[i + 1] + dkcv[i + 1] : after;
-            if (va && t < T) dr[(b * T + t) * A + a] = dq[i] / cv[i] + nxt;
+            if (va && t < T) st_row(dr + (b * T + t) * A, 4u * ac, dqc[i] + nxt);
             const float k16 = bf16_to_f32(f32_to_bf16_bits(kv[i]));
-            const double pos = static_cast<double>(t) - tau;
-            dg_acc -= pos * static_cast<double>(k16 * dkfv[i] + kv[i] * dkcv[i]);
+            const double e = static_cast<double>(k16 * dkfv[i] + kv[i] * dkcv[i]);
+            e0 -= e;
+            e1 -= i * e;
         }
+        dg_acc += (static_cast<double>(t0) - tau) * e0 + e1;
         dkc_next = tot[0][s];
         dkt_next = first_dkt[0][s];
         __syncthreads();

@@ -74,6 +74,33 @@ __device__ __forceinline__ void store_from_f32(void *p, size_t i, int dtype, flo
     else static_cast<_Float16 *>(p)[i] = static_cast<_Float16>(v);
 }
 
+// Access at a wave-uniform row pointer plus a lane's 32-bit byte offset: the
+// row lives in scalar registers and every access of a row segment shares one
+// offset VGPR (a global access with a scalar base), instead of each access
+// carrying a 64-bit per-lane address (which the compiler otherwise forms by
+// hoisting each access's loop-invariant lane part into its own VGPR pair). Empty
+// asm statements, which emit no instruction, pin the row to a scalar register
+// pair and keep the 32-bit offset opaque at the access, so that instruction
+// selection sees "scalar base + zero-extended 32-bit offset". The row must
+// therefore be wave-uniform. Callers clamp the row on wave-uniform conditions
+// and the offset per lane, and mask the value after.
+using gchar = __attribute__((address_space(1))) char;
+
+__device__ __forceinline__ gchar *row_addr(const void *row, uint32_t byte_off) {
+    uint64_t v = reinterpret_cast<uint64_t>(row);
+    asm("" : "+s"(v));
+    asm("" : "+v"(byte_off));
+    return reinterpret_cast<gchar *>(v) + byte_off;
+}
+
+template <typename T> __device__ __forceinline__ T ld_row(const T *row, uint32_t byte_off) {
+    return *reinterpret_cast<const __attribute__((address_space(1))) T *>(row_addr(row, byte_off));
+}
+
+template <typename T> __device__ __forceinline__ void st_row(T *row, uint32_t byte_off, T v) {
+    *reinterpret_cast<__attribute__((address_space(1))) T *>(row_addr(row, byte_off)) = v;
+}
+
 // ---- operand tile layouts of the chunked kernels
 //
 // A tile is one v_mfma_f32_32x32x16_bf16 operand: 32 rows x 16 contraction

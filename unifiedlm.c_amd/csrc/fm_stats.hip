@@ -33,60 +33,72 @@ __device__ __forceinline__ float pow_int(float x, int e) {
     return r;
 }
 
-// Sources of r for the kernels below (RSrc). at(row, ac, ...) reads row
-// `row` (wave-uniform, clamped by the caller to a valid row) at slot `ac`
-// (clamped per lane); loads are unconditional and masked after, so none waits
-// inside a branch.
+// Sources of r for the kernels below (RSrc). raw(row, ac, A) loads the stored
+// element of row `row` (wave-uniform, clamped by the caller to a valid row) at
+// slot `ac` (clamped per lane); make() turns it into r with the slot and
+// position constants and the validity mask. Keeping the two apart lets a kernel
+// issue a chunk's loads ahead of the arithmetic that waits on them; at() does
+// both. Loads are unconditional and masked after, so none waits in a branch.
 struct RTensor {
     const float *r;
+    using raw_t = float;
     __device__ __forceinline__ float slot_const(int) const { return 0.f; }
     static constexpr bool kRowConst = false;
-    __device__ __forceinline__ float row_const(size_t, bool) const { return 1.f; }
-    __device__ __forceinline__ float at(size_t row, uint32_t ac, int A, float, float, bool ok) const {
-        const float v = ld_row(r + row * A, 4u * ac);
-        return ok ? v : 0.f;
+    __device__ __forceinline__ float row_raw(size_t, bool) const { return 1.f; }
+    __device__ __forceinline__ raw_t raw(size_t row, uint32_t ac, int A) const { return ld_row(r + row * A, 4u * ac); }
+    __device__ __forceinline__ float make(raw_t v, float, float, bool ok) const { return ok ? v : 0.f; }
+    __device__ __forceinline__ float at(size_t row, uint32_t ac, int A, float b, float inv, bool ok) const {
+        return make(raw(row, ac, A), b, inv, ok);
     }
 };
 
-template <typename TP> __device__ __forceinline__ float ld_pre(const TP *row, uint32_t ac);
-template <> __device__ __forceinline__ float ld_pre<float>(const float *row, uint32_t ac) { return ld_row(row, 4u * ac); }
-template <> __device__ __forceinline__ float ld_pre<uint16_t>(const uint16_t *row, uint32_t ac) {
-    return bf16_to_f32(ld_row(row, 2u * ac));
-}
-template <> __device__ __forceinline__ float ld_pre<_Float16>(const _Float16 *row, uint32_t ac) {
-    return static_cast<float>(ld_row(row, 2u * ac));
-}
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(uint16_t v) { return bf16_to_f32(v); }
+__device__ __forceinline__ float to_f32(_Float16 v) { return static_cast<float>(v); }
 
 // r = relu(pre + bias)^2 * (1 / denom[row]); addr_bwd_kernel forms r with the
 // same operations, so every kernel of the block sees the same r. The
 // reciprocal depends on the position only, which is uniform over a wave (its
-// lanes are 64 slots), so row_const forms it once per position.
+// lanes are 64 slots), so it is formed once per position from row_raw.
 template <typename TP>
 struct RAddr {
     const TP *pre;
     const float *bias, *denom;
+    using raw_t = TP;
     __device__ __forceinline__ float slot_const(int a) const { return bias ? bias[a] : 0.f; }
     static constexpr bool kRowConst = true;
-    __device__ __forceinline__ float row_const(size_t row, bool tok) const { return 1.f / denom[tok ? row : 0]; }
-    __device__ __forceinline__ float at(size_t row, uint32_t ac, int A, float b, float inv, bool ok) const {
-        float p = ld_pre(pre + row * A, ac) + b;
+    __device__ __forceinline__ float row_raw(size_t row, bool tok) const { return denom[tok ? row : 0]; }
+    __device__ __forceinline__ raw_t raw(size_t row, uint32_t ac, int A) const {
+        return ld_row(pre + row * A, static_cast<uint32_t>(sizeof(TP)) * ac);
+    }
+    __device__ __forceinline__ float make(raw_t v, float b, float inv, bool ok) const {
+        float p = to_f32(v) + b;
         p = p > 0.f ? p : 0.f;
-        const float v = (p * p) * inv;
-        return ok ? v : 0.f;
+        const float r = (p * p) * inv;
+        return ok ? r : 0.f;
+    }
+    __device__ __forceinline__ float at(size_t row, uint32_t ac, int A, float b, float inv, bool ok) const {
+        return make(raw(row, ac, A), b, inv, ok);
     }
 };
 
 // The per-position constants of a thread segment (positions t0 .. t0+15 and
 // t0 - 1): lane l < 16 loads position t0 + l, lane 16 position t0 - 1, and
-// v_readlane hands each value to the whole wave.
+// v_readlane hands each value to the whole wave. seg_row_raw loads the
+// denominators, seg_inv turns them into the factors make() takes.
 template <class RS>
-__device__ __forceinline__ float seg_row_consts(const RS &rs, size_t row_t0, int t0, int T, int lane) {
+__device__ __forceinline__ float seg_row_raw(const RS &rs, size_t row_t0, int t0, int T, int lane) {
     if constexpr (RS::kRowConst) {
         const int tl = lane < kSeg ? t0 + lane : t0 - 1;
-        return rs.row_const(row_t0 + (tl - t0), tl >= 0 && tl < T);
+        return rs.row_raw(row_t0 + (tl - t0), tl >= 0 && tl < T);
     } else {
         return 1.f;
     }
+}
+
+template <class RS> __device__ __forceinline__ float seg_inv(float d) {
+    if constexpr (RS::kRowConst) return 1.f / d;
+    else return 1.f;
 }
 
 __device__ __forceinline__ float lane_value(float v, int l) {
@@ -139,16 +151,26 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
     const float wa = va ? w[a] : 1.f;
     const float rb = va ? rs.slot_const(a) : 0.f;   // the slot's key bias when r is formed here
     float carry = 0.f;   // n at the position before the chunk
+    // the stored elements of the next chunk's positions t0 .. t0+15 and t0 - 1,
+    // and their denominators, loaded one chunk ahead
+    typename RS::raw_t pv[kSeg + 1];
+    float pd;
+    auto fetch = [&](int n) {
+        const int t0 = n * ULM_CHUNK + j * kSeg;
+        pd = seg_row_raw(rs, bs * T + t0, t0, T, s);
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) pv[i] = rs.raw(urow(bs, t0 + i, T), ac, A);
+        pv[kSeg] = rs.raw(urow(bs, t0 - 1, T), ac, A);
+    };
+    fetch(0);
     for (int n = 0; n < NT; ++n) {
         const int t0 = n * ULM_CHUNK + j * kSeg;
-        const float seg_c = seg_row_consts(rs, bs * T + t0, t0, T, s);
+        const float seg_c = seg_inv<RS>(pd);
         float rv[kSeg], kv[kSeg], nl[kSeg];
 #pragma unroll
-        for (int i = 0; i < kSeg; ++i) {
-            const int t = t0 + i;
-            rv[i] = rs.at(urow(bs, t, T), ac, A, rb, lane_value(seg_c, i), va && t < T);
-        }
-        kv[0] = rs.at(urow(bs, t0 - 1, T), ac, A, rb, lane_value(seg_c, kSeg), va && t0 >= 1 && t0 - 1 < T);
+        for (int i = 0; i < kSeg; ++i) rv[i] = rs.make(pv[i], rb, lane_value(seg_c, i), va && t0 + i < T);
+        kv[0] = rs.make(pv[kSeg], rb, lane_value(seg_c, kSeg), va && t0 >= 1 && t0 - 1 < T);
+        if (n + 1 < NT) fetch(n + 1);
 #pragma unroll
         for (int i = 1; i < kSeg; ++i) kv[i] = rv[i - 1];
         float acc = 0.f;
@@ -263,7 +285,7 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
     double dg_acc = 0.0;
     for (int n = NT - 1; n >= 0; --n) {
         const int t0 = n * ULM_CHUNK + j * kSeg;
-        const float seg_c = seg_row_consts(rs, b * T + t0, t0, T, s);
+        const float seg_c = seg_inv<RS>(seg_row_raw(rs, b * T + t0, t0, T, s));
         // xv: the extra gradient of q (dq_out or d(w q), by XQ); dq is formed
         // from dqfv and xv where q is, so neither outlives the reverse scan
         float rv[kSeg], kv[kSeg], cv[kSeg], dqc[kSeg], dqfv[kSeg], xv[kSeg], dkfv[kSeg];

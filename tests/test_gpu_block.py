@@ -27,6 +27,7 @@ NC_CASES = [
     (2, 200, 768, 4),     # 110M width
     (1, 3, 96, 1),        # a single tap: no halo
     (2, 70, 130, 8),      # the largest tap count
+    (1, 33, 1024, 4),     # the widest channel-per-thread backward (16 waves)
     (1, 40, 2100, 4),     # wide rows: the backward's 8-position tile
 ]
 

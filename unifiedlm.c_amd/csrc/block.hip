@@ -211,6 +211,116 @@ __global__ __launch_bounds__(kThreads) void norm_conv_bwd_kernel(const TX *__res
     }
 }
 
+// Channel-per-thread backward for D <= kColsMaxD: one workgroup per (kColTP
+// positions, batch row) with a thread per channel, which issues all of its
+// tile's loads at once (x, dh_v, d_res of the kColTP rows and du of the
+// kColTP + 7 rows of its window) and keeps dh, xn in registers, so x is read
+// once and no dh buffer is staged. The conv taps are right-aligned, ca[m] =
+// cw[Kc-1-m] (zero for m >= Kc), so with du_w[m] = du_{t0+m}:
+//   dh_{t0+i} = dhv + sum_m ca[m] du_w[i+m],   g2[m] += h_{t0+i} du_w[i+m],
+// and dconv_w[j] is g2[Kc-1-j]. The row dots <dxn, xn> are wave sums, then a
+// fixed-order sum over the waves in LDS. Partials: one row per tile,
+// [dnorm_w (D) | dconv_w (D, Kc)], summed over tiles by one column sum.
+constexpr int kColTP = 16;
+constexpr int kColsMaxD = 1024;
+constexpr int kColWin = kColTP + kMaxTaps - 1;
+
+template <typename T> __device__ __forceinline__ float ldrow(const T *row, uint32_t d);
+template <> __device__ __forceinline__ float ldrow<float>(const float *row, uint32_t d) { return ld_row(row, 4u * d); }
+template <> __device__ __forceinline__ float ldrow<uint16_t>(const uint16_t *row, uint32_t d) {
+    return bf16_to_f32(ld_row(row, 2u * d));
+}
+template <> __device__ __forceinline__ float ldrow<_Float16>(const _Float16 *row, uint32_t d) {
+    return static_cast<float>(ld_row(row, 2u * d));
+}
+
+template <typename TX, typename TD>
+__global__ __launch_bounds__(kColsMaxD) void norm_conv_bwd_cols_kernel(
+    const TX *__restrict__ x, const float *__restrict__ rstd, const float *__restrict__ nw,
+    const float *__restrict__ cw, int Kc, const TD *__restrict__ du, const TD *__restrict__ dhv,
+    const float *dres, float *dx, float *__restrict__ pw, int T, int D) {
+    __shared__ float part[kColTP][kColsMaxD / kWave];   // per-wave row-dot partials
+    const int d = threadIdx.x, wave = d / kWave, lane = d % kWave, nwave = blockDim.x / kWave;
+    const bool vd = d < D;
+    const uint32_t dc = vd ? d : 0;
+    const int t0 = blockIdx.x * kColTP;
+    const size_t row0 = static_cast<size_t>(blockIdx.y) * T;
+    const size_t tile = static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x;
+    // rows are clamped on wave-uniform conditions, channels per lane; values masked after
+    auto urow = [&](int t) { return row0 + static_cast<size_t>(t < T ? t : T - 1); };
+    float xv[kColTP], hv[kColTP], rv[kColTP], dv[kColWin], ca[kMaxTaps];
+#pragma unroll
+    for (int i = 0; i < kColTP; ++i) {
+        const int t = t0 + i;
+        const bool ok = vd && t < T;
+        const size_t r = urow(t);
+        const float a = ldrow(x + r * D, dc);
+        xv[i] = ok ? a : 0.f;
+        const float h = dhv ? ldrow(dhv + r * D, dc) : 0.f;
+        hv[i] = ok ? h : 0.f;
+        rv[i] = t < T ? rstd[r] : 0.f;
+    }
+#pragma unroll
+    for (int m = 0; m < kColWin; ++m) {
+        const int t = t0 + m;
+        const bool ok = vd && t < T && m < kColTP + Kc - 1;
+        const float v = ldrow(du + urow(t) * D, dc);
+        dv[m] = ok ? v : 0.f;
+    }
+#pragma unroll
+    for (int m = 0; m < kMaxTaps; ++m) ca[m] = m < Kc ? cw[static_cast<size_t>(dc) * Kc + (Kc - 1 - m)] : 0.f;
+    const float nwd = vd ? nw[dc] : 0.f;
+    float g2[kMaxTaps], dh[kColTP], rd[kColTP];
+#pragma unroll
+    for (int m = 0; m < kMaxTaps; ++m) g2[m] = 0.f;
+    float gnw = 0.f;
+#pragma unroll
+    for (int i = 0; i < kColTP; ++i) {
+        const float xn = xv[i] * rv[i];
+        const float ht = xn * nwd;
+        float a = hv[i];
+#pragma unroll
+        for (int m = 0; m < kMaxTaps; ++m) {
+            a += ca[m] * dv[i + m];
+            g2[m] += ht * dv[i + m];
+        }
+        dh[i] = a;
+        gnw += a * xn;
+        xv[i] = xn;
+        rd[i] = wave_sum(a * nwd * xn);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < kColTP; ++i) part[i][wave] = rd[i];
+    }
+    // d_res loads go out before the barrier, with the row sums in flight
+    float dr[kColTP];
+#pragma unroll
+    for (int i = 0; i < kColTP; ++i) {
+        const int t = t0 + i;
+        const float v = dres ? ld_row(dres + urow(t) * D, 4u * dc) : 0.f;
+        dr[i] = (vd && t < T) ? v : 0.f;
+    }
+    __syncthreads();
+    const float invD = 1.f / static_cast<float>(D);
+#pragma unroll
+    for (int i = 0; i < kColTP; ++i) {
+        const int t = t0 + i;
+        float dot = 0.f;
+        for (int w = 0; w < nwave; ++w) dot += part[i][w];
+        dot *= invD;
+        const float g = rv[i] * (dh[i] * nwd - xv[i] * dot);
+        if (vd && t < T) st_row(dx + (row0 + t) * D, 4u * dc, dr[i] + g);
+    }
+    if (vd) {
+        float *const row = pw + tile * D * (Kc + 1);
+        row[d] = gnw;
+#pragma unroll
+        for (int m = 0; m < kMaxTaps; ++m)
+            if (m < Kc) row[D + d * Kc + (Kc - 1 - m)] = g2[m];
+    }
+}
+
 constexpr int kSplit = 32;   // first-level row ranges of the weight-gradient sums
 
 constexpr size_t kBwdLds = 80 * 1024;   // two backward workgroups per CU (160 KiB of LDS)
@@ -219,8 +329,10 @@ size_t bwd_lds_bytes(int tp, int D, int) {
     return (static_cast<size_t>(tp) * D + static_cast<size_t>(tp) * kThreads + tp) * 4;
 }
 
-// positions per backward workgroup: the largest of 16, 8, 4, 2, 1 whose LDS fits kBwdLds
+// positions per backward workgroup: kColTP for the channel-per-thread kernel
+// (D <= kColsMaxD), else the largest of 16, 8, 4, 2, 1 whose LDS fits kBwdLds
 int bwd_tile(int D, int Kc) {
+    if (D <= kColsMaxD) return kColTP;
     for (int tp = 16; tp >= 1; tp /= 2)
         if (bwd_lds_bytes(tp, D, Kc) <= kBwdLds) return tp;
     return 0;
@@ -238,7 +350,7 @@ BwdWs bwd_layout(void *base, int B, int T, int D, int Kc) {
     BwdWs w{};
     w.pnw = c.take<float>(ntile * D);
     w.pcw = c.take<float>(ntile * D * Kc);
-    w.tmp = c.take<float>(static_cast<size_t>(kSplit) * D * Kc);
+    w.tmp = c.take<float>(static_cast<size_t>(kSplit) * D * (Kc + 1));
     w.bytes = c.off;
     return w;
 }
@@ -259,6 +371,16 @@ int launch_bwd(const void *x, const float *rstd, const float *nw, const float *c
     const int tp = bwd_tile(D, Kc);
     const BwdWs ws = bwd_layout(workspace, B, T, D, Kc);
     const int ntx = (T + tp - 1) / tp;
+    const size_t ntile = static_cast<size_t>(B) * ntx;
+    if (D <= kColsMaxD) {
+        const int nth = (D + kWave - 1) / kWave * kWave;
+        norm_conv_bwd_cols_kernel<TX, TD><<<dim3(ntx, B), nth, 0, s>>>(
+            static_cast<const TX *>(x), rstd, nw, cw, Kc, static_cast<const TD *>(du), static_cast<const TD *>(dhv),
+            dres, dx, ws.pnw, T, D);
+        ULM_TRY(check_launch("norm_conv_bwd_cols_kernel"));
+        // pnw and pcw are carved back to back: their span holds ntile rows of D (Kc + 1)
+        return launch_column_sum2(ws.pnw, ntile, D, static_cast<size_t>(D) * Kc, ws.tmp, kSplit, dnw, dcw, s);
+    }
     const size_t lds = bwd_lds_bytes(tp, D, Kc);
     static bool attr_done[64] = {};
     int dev = 0;
@@ -274,7 +396,6 @@ int launch_bwd(const void *x, const float *rstd, const float *nw, const float *c
         static_cast<const TX *>(x), rstd, nw, cw, Kc, static_cast<const TD *>(du), static_cast<const TD *>(dhv), dres,
         dx, ws.pnw, ws.pcw, T, D, tp);
     ULM_TRY(check_launch("norm_conv_bwd_kernel"));
-    const size_t ntile = static_cast<size_t>(B) * ntx;
     ULM_TRY(launch_column_sum(ws.pnw, ntile, D, ws.tmp, kSplit, dnw, s));
     return launch_column_sum(ws.pcw, ntile, static_cast<size_t>(D) * Kc, ws.tmp, kSplit, dcw, s);
 }

@@ -39,23 +39,38 @@ int launch_convert(const void *src, int src_dt, void *dst, int dst_dt, size_t n,
 }
 
 // out[c] = sum_r in[r * ncol + c] over rows r of [r0, r1) for split blockIdx.y
-// (rows split into gridDim.y contiguous ranges), written to out[blockIdx.y * ncol + c].
+// (rows split into gridDim.y contiguous ranges), written to out[blockIdx.y * ncol + c];
+// with out2 given (one split only), columns c >= ncol1 go to out2[c - ncol1] instead.
 __global__ __launch_bounds__(256) void column_sum_kernel(const float *__restrict__ in, size_t nrow, size_t ncol,
-                                                              float *__restrict__ out) {
+                                                              float *__restrict__ out, size_t ncol1,
+                                                              float *__restrict__ out2) {
     const size_t c = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
     if (c >= ncol) return;
     const size_t per = (nrow + gridDim.y - 1) / gridDim.y;
     const size_t r0 = blockIdx.y * per, r1 = min(nrow, r0 + per);
     float s = 0.f;
     for (size_t r = r0; r < r1; ++r) s += in[r * ncol + c];
-    out[blockIdx.y * ncol + c] = s;
+    if (out2 && c >= ncol1) out2[c - ncol1] = s;
+    else out[blockIdx.y * ncol + c] = s;
 }
 
 int launch_column_sum(const float *in, size_t nrow, size_t ncol, float *tmp, int nsplit, float *out, hipStream_t s) {
     const unsigned gx = static_cast<unsigned>((ncol + 256 - 1) / 256);
-    column_sum_kernel<<<dim3(gx, nsplit), 256, 0, s>>>(in, nrow, ncol, tmp);
+    column_sum_kernel<<<dim3(gx, nsplit), 256, 0, s>>>(in, nrow, ncol, tmp, ncol, nullptr);
     ULM_TRY(check_launch("column_sum_kernel"));
-    column_sum_kernel<<<dim3(gx, 1), 256, 0, s>>>(tmp, nsplit, ncol, out);
+    column_sum_kernel<<<dim3(gx, 1), 256, 0, s>>>(tmp, nsplit, ncol, out, ncol, nullptr);
+    return check_launch("column_sum_kernel");
+}
+
+// Column sums of rows [a (ncol1) | b (ncol2)] into out1 (ncol1) and out2 (ncol2),
+// in the same fixed order as launch_column_sum; tmp holds nsplit x (ncol1 + ncol2).
+int launch_column_sum2(const float *in, size_t nrow, size_t ncol1, size_t ncol2, float *tmp, int nsplit, float *out1,
+                       float *out2, hipStream_t s) {
+    const size_t ncol = ncol1 + ncol2;
+    const unsigned gx = static_cast<unsigned>((ncol + 256 - 1) / 256);
+    column_sum_kernel<<<dim3(gx, nsplit), 256, 0, s>>>(in, nrow, ncol, tmp, ncol, nullptr);
+    ULM_TRY(check_launch("column_sum_kernel"));
+    column_sum_kernel<<<dim3(gx, 1), 256, 0, s>>>(tmp, nsplit, ncol, out1, ncol1, out2);
     return check_launch("column_sum_kernel");
 }
 

@@ -179,6 +179,9 @@ int launch_convert(const void *src, int src_dt, void *dst, int dst_dt, size_t n,
 // out[c] = sum over the nrow rows of in (nrow x ncol fp32) in a fixed order:
 // nsplit contiguous row ranges into tmp (nsplit x ncol), then their sum.
 int launch_column_sum(const float *in, size_t nrow, size_t ncol, float *tmp, int nsplit, float *out, hipStream_t s);
+// the same over rows [a | b], into two outputs (elementwise.hip)
+int launch_column_sum2(const float *in, size_t nrow, size_t ncol1, size_t ncol2, float *tmp, int nsplit, float *out1,
+                       float *out2, hipStream_t s);
 
 // Where the statistics kernels take the read address r (B,T,A) from: an fp32
 // tensor r, or, when r is null, the block's address inputs, forming

@@ -227,6 +227,17 @@ int ulm_wgrad(const void *a, const void *b, float *c, int K, int N1, int N2, voi
  * nearest even): the autocast casts around the block's GEMMs. */
 int ulm_cast(const void *src, int src_dtype, void *dst, int dst_dtype, size_t n, void *stream);
 
+/* The block's fast-memory parameters from their logs, g[0] = -exp(log_rate[0])
+ * and w = exp(clamp(log_w, log_w_min, log_w_max)) over A slots (model.py:75,
+ * 84; the reference clamps to [-7, 12]), and the chain rule back from dg, dw:
+ * dlog_rate = dg g, dlog_w = dw w inside the clamp range and 0 outside it (the
+ * gradient of torch.clamp). One launch each instead of the parameter
+ * expressions' elementwise kernels and their autograd. */
+int ulm_block_params(const float *log_rate, const float *log_w, float log_w_min, float log_w_max, int A,
+                     float *g, float *w, void *stream);
+int ulm_block_params_bwd(const float *log_rate, const float *log_w, float log_w_min, float log_w_max,
+                         const float *dg, const float *dw, int A, float *dlog_rate, float *dlog_w, void *stream);
+
 /* ------------------------------------------------------------------------
  * Batched recurrent decode, N sequences, one block, one position. Together
  * these replace UnifiedBlock.step (model.py:96-111) / run.c:193-265. The

@@ -174,12 +174,14 @@ def test_unified_block_input_checks():
     import kernel
     D, A = 8, 16
     args = dict(norm_w=torch.ones(D), conv_w=torch.zeros(D, 1, 4), key_w=torch.zeros(A, D), key_b=torch.zeros(A),
-                log_eps=torch.zeros(()), val_w=torch.zeros(D, D), mu_w=torch.zeros(D, A), g=torch.tensor(-0.1),
-                w=torch.ones(A), norm_eps=1e-5)
+                log_eps=torch.zeros(()), val_w=torch.zeros(D, D), mu_w=torch.zeros(D, A), log_rate=torch.tensor(-2.3),
+                log_w=torch.zeros(A), norm_eps=1e-5)
     with pytest.raises(ValueError, match="fp32"):
         kernel.unified_block(torch.zeros(2, 4, D, dtype=torch.bfloat16), **args)
     with pytest.raises(ValueError, match="disagree"):
         kernel.unified_block(torch.zeros(2, 4, D), **{**args, "mu_w": torch.zeros(A, D)})
+    with pytest.raises(ValueError, match="log_rate"):
+        kernel.unified_block(torch.zeros(2, 4, D), **{**args, "log_rate": torch.zeros(2)})
     with pytest.raises(ValueError, match="Kc"):
         kernel.unified_block(torch.zeros(2, 4, D), **{**args, "conv_w": torch.zeros(D, 1, 9)})
     with pytest.raises(RuntimeError, match="ROCm GPU"):

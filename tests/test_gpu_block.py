@@ -173,6 +173,34 @@ WGRAD_CASES = [
 ]
 
 
+def test_block_params_match_autograd():
+    """g = -exp(log_rate), w = exp(clamp(log_w, -7, 12)) and their chain rule
+    (model.py:75, 84) against fp32 torch autograd, with log_w below, above and
+    exactly at both clamp bounds (where torch's clamp passes the gradient)."""
+    import kernel
+    say("ulm_block_params / ulm_block_params_bwd A=300")
+    A = 300
+    gen = torch.Generator().manual_seed(7)
+    lw = torch.randn(A, generator=gen) * 6.0
+    lw[:6] = torch.tensor([-7.0, 12.0, -7.5, 12.5, -30.0, 30.0])
+    lr = torch.tensor([-2.7])
+    dg, dw = torch.randn(1, generator=gen), torch.randn(A, generator=gen)
+    lrr, lwr = lr.clone().requires_grad_(), lw.clone().requires_grad_()
+    g_ref, w_ref = -lrr.exp(), lwr.clamp(kernel.LOG_W_MIN, kernel.LOG_W_MAX).exp()
+    ((g_ref * dg).sum() + (w_ref * dw).sum()).backward()
+    lrd, lwd, dgd, dwd = (t.cuda() for t in (lr, lw, dg, dw))
+    g, w = torch.empty(1, device="cuda"), torch.empty(A, device="cuda")
+    dlr, dlw = torch.empty(1, device="cuda"), torch.empty(A, device="cuda")
+    s = nat.stream_of(lrd)
+    call("ulm_block_params", ptr(lrd), ptr(lwd), kernel.LOG_W_MIN, kernel.LOG_W_MAX, A, ptr(g), ptr(w), s)
+    call("ulm_block_params_bwd", ptr(lrd), ptr(lwd), kernel.LOG_W_MIN, kernel.LOG_W_MAX, ptr(dgd), ptr(dwd), A,
+         ptr(dlr), ptr(dlw), s)
+    torch.cuda.synchronize()
+    for got, ref in ((g, g_ref), (w, w_ref), (dlr, lrr.grad), (dlw, lwr.grad)):
+        assert torch.allclose(got.cpu(), ref.detach(), rtol=1e-6, atol=0), (got, ref)
+    assert (dlw.cpu()[2:6] == 0).all() and (dlw.cpu()[:2] != 0).all()
+
+
 @pytest.mark.parametrize("K,N1,N2", WGRAD_CASES)
 def test_wgrad_matches_fp32_product(K, N1, N2):
     """C = A^T B against the fp32 product of the same bf16 operands (float64

@@ -400,6 +400,32 @@ int launch_bwd(const void *x, const float *rstd, const float *nw, const float *c
     return launch_column_sum(ws.pcw, ntile, static_cast<size_t>(D) * Kc, ws.tmp, kSplit, dcw, s);
 }
 
+// The block's fast-memory parameters from their logs (model.py:75, 84):
+// g = -exp(log_rate), w = exp(clamp(log_w, lo, hi)); and the chain rule back,
+// d log_rate = dg g, d log_w = dw w where lo <= log_w <= hi, else 0 (the
+// gradient torch's clamp passes).
+__global__ __launch_bounds__(256) void params_fwd_kernel(const float *__restrict__ log_rate,
+                                                         const float *__restrict__ log_w, float lo, float hi, int A,
+                                                         float *__restrict__ g, float *__restrict__ w) {
+    const int a = blockIdx.x * 256 + threadIdx.x;
+    if (a < A) w[a] = expf(fminf(fmaxf(log_w[a], lo), hi));
+    if (a == 0) g[0] = -expf(log_rate[0]);
+}
+
+__global__ __launch_bounds__(256) void params_bwd_kernel(const float *__restrict__ log_rate,
+                                                         const float *__restrict__ log_w, float lo, float hi,
+                                                         const float *__restrict__ dg, const float *__restrict__ dw,
+                                                         int A, float *__restrict__ dlog_rate,
+                                                         float *__restrict__ dlog_w) {
+    const int a = blockIdx.x * 256 + threadIdx.x;
+    if (a < A) {
+        const float x = log_w[a];
+        const float wa = expf(fminf(fmaxf(x, lo), hi));
+        dlog_w[a] = (x >= lo && x <= hi) ? dw[a] * wa : 0.f;
+    }
+    if (a == 0) dlog_rate[0] = dg[0] * -expf(log_rate[0]);
+}
+
 // Calls f.template operator()<T>() with T the element type of dtype dt.
 template <class F>
 int with_type(int dt, F &&f) {
@@ -464,6 +490,27 @@ extern "C" int ulm_norm_conv_bwd(const void *x, int x_dtype, const float *rstd, 
                                                               dnorm_w, dconv_w, workspace, B, T, D, s);
         });
     });
+}
+
+extern "C" int ulm_block_params(const float *log_rate, const float *log_w, float log_w_min, float log_w_max, int A,
+                                float *g, float *w, void *stream) {
+    ULM_REQUIRE(A > 0, "ulm_block_params: bad size A=%d", A);
+    ULM_REQUIRE(log_rate && log_w && g && w, "ulm_block_params: null pointer");
+    ULM_REQUIRE(log_w_min <= log_w_max, "ulm_block_params: empty clamp range [%g, %g]", log_w_min, log_w_max);
+    blk::params_fwd_kernel<<<(A + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(log_rate, log_w, log_w_min,
+                                                                                           log_w_max, A, g, w);
+    return check_launch("params_fwd_kernel");
+}
+
+extern "C" int ulm_block_params_bwd(const float *log_rate, const float *log_w, float log_w_min, float log_w_max,
+                                    const float *dg, const float *dw, int A, float *dlog_rate, float *dlog_w,
+                                    void *stream) {
+    ULM_REQUIRE(A > 0, "ulm_block_params_bwd: bad size A=%d", A);
+    ULM_REQUIRE(log_rate && log_w && dg && dw && dlog_rate && dlog_w, "ulm_block_params_bwd: null pointer");
+    ULM_REQUIRE(log_w_min <= log_w_max, "ulm_block_params_bwd: empty clamp range [%g, %g]", log_w_min, log_w_max);
+    blk::params_bwd_kernel<<<(A + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(
+        log_rate, log_w, log_w_min, log_w_max, dg, dw, A, dlog_rate, dlog_w);
+    return check_launch("params_bwd_kernel");
 }
 
 extern "C" int ulm_cast(const void *src, int src_dtype, void *dst, int dst_dtype, size_t n, void *stream) {

@@ -179,6 +179,10 @@ def relu2_address(pre, bias, log_eps):
 # elementwise ends fused; the GEMMs are plain library GEMMs (hipBLASLt through
 # torch.mm) with fp32 accumulation
 
+# clamp range of a block's log prior mass, w = exp(clamp(log_w, -7, 12)) (model.py:75)
+LOG_W_MIN, LOG_W_MAX = -7.0, 12.0
+
+
 def _mm(a, b, out_dtype):
     """a @ b, written in out_dtype straight from the fp32 accumulator."""
     return torch.mm(a, b) if a.dtype == out_dtype else torch.mm(a, b, out_dtype=out_dtype)
@@ -213,6 +217,7 @@ class UnifiedBlockFn(torch.autograd.Function):
         h, u   = RMSNorm(x), causal conv(h)            ulm_norm_conv_fwd
         pre, v = u K^T, h W_v^T                         GEMMs in cdt
         denom  = the relu^2 address's row sums of pre + b  ulm_addr_fwd (r not written)
+        g, w   = -exp(log_rate), exp(clamp(log_w))      ulm_block_params
         wq, y  = w q, x + fast                          ulm_block_fm_fwd (r formed from pre)
         out    = y + wq mu^T                            GEMM accumulating into y
 
@@ -221,7 +226,7 @@ class UnifiedBlockFn(torch.autograd.Function):
     stream; every gradient is returned in fp32."""
 
     @staticmethod
-    def forward(ctx, x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, g, w, norm_eps, cdt):
+    def forward(ctx, x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, norm_eps, cdt):
         B, T, D = x.shape
         A = key_w.shape[0]
         Kc = conv_w.shape[-1]
@@ -246,8 +251,11 @@ class UnifiedBlockFn(torch.autograd.Function):
         denom = torch.empty(M, device=dev, dtype=f32)
         # r itself is never written: the fast memory forms it from pre, bias and denom
         call("ulm_addr_fwd", ptr(pre), cd, ptr(b32), ptr(le), None, ptr(denom), M, A, s)
-        g1 = g.float().reshape(1).contiguous()
-        w32 = w.float().contiguous()
+        lr = log_rate.float().reshape(1).contiguous()
+        lw = log_w.float().contiguous()
+        g1 = torch.empty(1, device=dev, dtype=f32)
+        w32 = torch.empty(A, device=dev, dtype=f32)
+        call("ulm_block_params", ptr(lr), ptr(lw), LOG_W_MIN, LOG_W_MAX, A, ptr(g1), ptr(w32), s)
         saved_bytes = nat.lib().ulm_fm_saved_bytes(B, T, A, D, cd)
         saved = torch.empty(saved_bytes, device=dev, dtype=torch.uint8)
         ws_bytes = nat.lib().ulm_block_fm_fwd_workspace_bytes(B, T, A, D)
@@ -258,8 +266,8 @@ class UnifiedBlockFn(torch.autograd.Function):
              ptr(x32), ptr(y), ptr(saved), saved_bytes, ptr(ws), ws_bytes, B, T, A, D, s)
         del ws, v
         out = _addmm_(y, qw, mw.t())
-        ctx.save_for_backward(x32, rstd, nw, cw, h, u, pre, b32, le, denom, g1, w32, saved, qw, kw, vw, mw)
-        ctx.meta = (B, T, A, D, Kc, cdt, conv_w.shape, log_eps.shape, g.shape, key_b is not None)
+        ctx.save_for_backward(x32, rstd, nw, cw, h, u, pre, b32, le, denom, lr, lw, g1, w32, saved, qw, kw, vw, mw)
+        ctx.meta = (B, T, A, D, Kc, cdt, conv_w.shape, log_eps.shape, log_rate.shape, key_b is not None)
         return out.view(B, T, D)
 
     @staticmethod
@@ -270,8 +278,8 @@ class UnifiedBlockFn(torch.autograd.Function):
 
     @staticmethod
     def _backward(ctx, dout):
-        x32, rstd, nw, cw, h, u, pre, b32, le, denom, g1, w32, saved, qw, kw, vw, mw = ctx.saved_tensors
-        B, T, A, D, Kc, cdt, cw_shape, le_shape, g_shape, has_bias = ctx.meta
+        x32, rstd, nw, cw, h, u, pre, b32, le, denom, lr, lw, g1, w32, saved, qw, kw, vw, mw = ctx.saved_tensors
+        B, T, A, D, Kc, cdt, cw_shape, le_shape, lr_shape, has_bias = ctx.meta
         M = B * T
         dev = x32.device
         s = nat.stream_of(x32)
@@ -295,6 +303,9 @@ class UnifiedBlockFn(torch.autograd.Function):
         call("ulm_block_fm_bwd", ptr(pre), cd, ptr(b32), ptr(denom), ptr(g1), ptr(w32), ptr(saved), saved.numel(), cd,
              ptr(d16), cd, ptr(dqw), cd, ptr(dr), ptr(dv), cd, ptr(dg), ptr(dw), ptr(ws), ws_bytes, B, T, A, D, s)
         del ws, dqw
+        dlr = torch.empty(1, device=dev, dtype=f32)
+        dlw = torch.empty(A, device=dev, dtype=f32)
+        call("ulm_block_params_bwd", ptr(lr), ptr(lw), LOG_W_MIN, LOG_W_MAX, ptr(dg), ptr(dw), A, ptr(dlr), ptr(dlw), s)
         dpre = torch.empty_like(pre)
         dbias = torch.empty(A, device=dev, dtype=f32) if has_bias else None
         dle = torch.empty(1, device=dev, dtype=f32)
@@ -316,28 +327,33 @@ class UnifiedBlockFn(torch.autograd.Function):
         ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
         call("ulm_norm_conv_bwd", ptr(x32), nat.ULM_F32, ptr(rstd), ptr(nw), ptr(cw), Kc, ptr(du), nat.ULM_F32, ptr(dhv),
              nat.ULM_F32, ptr(dout), ptr(dx), ptr(dnw), ptr(dcw), ptr(ws), ws_bytes, B, T, D, s)
-        return (dx, dnw, dcw.view(cw_shape), dkey, dbias, dle.reshape(le_shape), dval, dmu, dg.reshape(g_shape), dw,
+        return (dx, dnw, dcw.view(cw_shape), dkey, dbias, dle.reshape(le_shape), dval, dmu, dlr.reshape(lr_shape), dlw,
                 None, None)
 
 
-def unified_block(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, g, w, norm_eps, cdt=torch.float32):
+def unified_block(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, norm_eps,
+                  cdt=torch.float32):
     """x + mu(w q) + fast of one UnifiedBlock (model.py:77-85) in one fused
     forward and backward. x (B, T, D) fp32; key_w (A, D), mu_w (D, A),
-    val_w (D, D), conv_w (D, 1, Kc); g = -exp(log_rate), w = prior mass (A,)."""
+    val_w (D, D), conv_w (D, 1, Kc); log_rate (a scalar) and log_w (A,) are the
+    block's parameters: g = -exp(log_rate), w = exp(clamp(log_w, LOG_W_MIN,
+    LOG_W_MAX)) (model.py:75, 84) are formed, and differentiated, natively."""
     if x.dim() != 3 or x.dtype != torch.float32:
         raise ValueError(f"x must be (B, T, D) fp32, got {tuple(x.shape)} {x.dtype}")
     B, T, D = x.shape
     A = key_w.shape[0]
     if B == 0 or T == 0 or D == 0:
         raise ValueError(f"empty input {tuple(x.shape)}")
-    if key_w.shape != (A, D) or mu_w.shape != (D, A) or val_w.shape != (D, D) or w.shape != (A,):
-        raise ValueError("block weights disagree with x: key (A, D), mu (D, A), val (D, D), w (A,)")
+    if key_w.shape != (A, D) or mu_w.shape != (D, A) or val_w.shape != (D, D) or log_w.shape != (A,):
+        raise ValueError("block weights disagree with x: key (A, D), mu (D, A), val (D, D), log_w (A,)")
+    if log_rate.numel() != 1:
+        raise ValueError(f"log_rate must hold one value, got {tuple(log_rate.shape)}")
     if conv_w.numel() % D or not 1 <= conv_w.shape[-1] <= 8:
         raise ValueError(f"conv_w must be (D, 1, Kc) with 1 <= Kc <= 8, got {tuple(conv_w.shape)}")
     if cdt not in (torch.float32, torch.bfloat16, torch.float16):
         raise ValueError(f"unsupported GEMM dtype {cdt}")
-    nat.require_device(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, g, w)
-    return UnifiedBlockFn.apply(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, g, w, norm_eps, cdt)
+    nat.require_device(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w)
+    return UnifiedBlockFn.apply(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, norm_eps, cdt)
 
 
 # ---------------------------------------------------------------------------

@@ -22,8 +22,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from kernel import (CHUNK, block_prefill, decode_addr, decode_pre, decode_state, fm_prefill, relu2_address,
-                    unified_block, unified_memory)
+from kernel import (CHUNK, LOG_W_MAX, LOG_W_MIN, block_prefill, decode_addr, decode_pre, decode_state, fm_prefill,
+                    relu2_address, unified_block, unified_memory)
 
 
 @dataclass
@@ -83,7 +83,7 @@ class UnifiedBlock(nn.Module):
         return relu2_address(F.linear(u, self.key.weight), self.key.bias, self.log_eps)
 
     def _w(self):
-        return self.log_w.clamp(-7.0, 12.0).exp()
+        return self.log_w.clamp(LOG_W_MIN, LOG_W_MAX).exp()
 
     def forward(self, x):
         """model.py:77-85. One fused block (fast memory, RMSNorm + conv, address,
@@ -95,7 +95,7 @@ class UnifiedBlock(nn.Module):
         cdt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else torch.float32
         with torch.autocast("cuda", enabled=False):
             return unified_block(x, self.norm.weight, self.conv.weight, self.key.weight, self.key.bias,
-                                 self.log_eps, self.val.weight, self.mu.weight, -self.log_rate.exp(), self._w(),
+                                 self.log_eps, self.val.weight, self.mu.weight, self.log_rate, self.log_w,
                                  self.norm.eps, cdt)
 
     def forward_composed(self, x):

@@ -41,6 +41,8 @@ SIGNATURES = {
     "ulm_block_fm_fwd": (I, [P, I, P, P, P, I, P, P, P, I, P, P, P, SZ, P, SZ, I, I, I, I, P]),
     "ulm_block_fm_bwd": (I, [P, I, P, P, P, P, P, SZ, I, P, I, P, I, P, P, I, P, P, P, SZ, I, I, I, I, P]),
     "ulm_cast": (I, [P, I, P, I, SZ, P]),
+    "ulm_block_params": (I, [P, P, F, F, I, P, P, P]),
+    "ulm_block_params_bwd": (I, [P, P, F, F, P, P, I, P, P, P]),
     "ulm_block_fm_prefill_workspace_bytes": (SZ, [I, I, I, I, I]),
     "ulm_block_fm_prefill": (I, [P, I, P, P, P, I, P, P, P, I, P, P, P, P, P, SZ, I, I, I, I, P]),
     "ulm_wgrad_workspace_bytes": (SZ, [I, I, I]),

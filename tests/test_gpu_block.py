@@ -120,6 +120,11 @@ BLOCK_CASES = [
     (2, 256, 128, 256, True),
     (1, 512, 768, 3072, True),    # 110M block shape
     (1, 1024, 512, 2048, True),   # 42M block shape, one row of 1024 positions
+    (3, 1, 64, 64, False),        # a single position
+    # D not a multiple of 32 (generic products), 3 key groups, ragged chunk; in fp32: under bf16
+    # autocast this shape's log_w gradient sits at the bf16-operand floor, about 1e-2 for eager
+    # torch op by op as for the fused block (9.3e-3 and 1.04e-2 measured)
+    (2, 130, 100, 1600, False),
 ]
 
 
@@ -153,8 +158,15 @@ def test_block_matches_oracle(B, T, D, A, autocast):
     ref = fm.block_forward(p, "", xr, norm_eps=blk.norm.eps)
     _head_loss(ref, head, targets).backward()
     errs = {"out": rel(out, ref), "dx": rel(xg.grad, xr.grad)}
+    # With one position the memory holds nothing (k_0 = 0, so fast = 0 and
+    # w q = r): the gradients of log_w, log_rate and the value weight are
+    # exactly zero, a relative error is undefined, and ours are held to 1e-6 of
+    # the input gradient's norm instead (fp32 rounding of terms that cancel).
+    zero = {"log_w", "log_rate", "val.weight"} if T == 1 else set()
     for n, t in blk.named_parameters():
-        errs[n] = rel(t.grad, p[n].grad)
+        errs[n] = (t.grad.norm() / xg.grad.norm()).item() if n in zero else rel(t.grad, p[n].grad)
+        if n in zero:
+            assert p[n].grad.abs().max().item() < 1e-12, (n, p[n].grad)
     say(f"  worst {max(errs.values()):.3e}: {errs}")
     # test_all.py:157-166 holds loss and every gradient to 1e-2 in fp32. Under
     # bf16 autocast the reference documents the decay gradient dlam at up to

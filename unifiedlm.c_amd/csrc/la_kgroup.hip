@@ -35,8 +35,9 @@
 // as zero, which covers keys past the group and a missing second value tile.
 //
 // Pipelining: the read-out operand of chunk n+1 and the raw c tile of chunk
-// n+1 are loaded before the update of chunk n; the update operand b_n is
-// loaded right after the read-out of chunk n. Every load therefore has the
+// n+1 are loaded before the update of chunk n; half of the update operand b_n
+// is loaded right after the read-out of chunk n, before the exchange of chunk
+// n-1's partials, and the other half after it. Every load therefore has the
 // barrier, LDS exchange and MFMA work of a phase to arrive in.
 //
 // The rows of a 32-key state block are held in the order key(rho) = rho with
@@ -81,7 +82,11 @@ constexpr int WAVES = 8;                       // two per SIMD
 constexpr int MAX_MH = 3;                      // key blocks per wave, at most
 constexpr int GROUP_BLOCKS = WAVES * MAX_MH;   // 24 blocks = 768 keys per workgroup
 constexpr int VT = 64;                         // value columns per workgroup
-constexpr int ROWS_PER_WAVE = C / WAVES;       // output rows each wave reduces and stores
+constexpr int ROWS_PER_WAVE = C / WAVES;
+// k-steps of the update operand b_n loaded before the previous chunk's
+// exchange (so in flight during it); the rest follow it. More than two spill
+// in the forward walk and measured slower in the reversed one.
+constexpr int UA_EARLY = 2;       // output rows each wave reduces and stores
 constexpr uint32_t TB = kTileElems * 2;        // bytes per operand tile
 constexpr uint32_t OOB = 0x80000000u;          // buffer offset past every range: the load returns zeros
 // LDS: the staged c tiles (decayed hi, decayed lo, raw: eight 1 KB tiles
@@ -374,22 +379,27 @@ __global__ __launch_bounds__(WAVES * 64, 1) void la_kgroup_kernel(const uint16_t
                 }
         }
         phase();
-        if (step > 0) exchange(chunk_of(step - 1), s_read_prev);
-        phase();
 
-        // ---- this chunk's update operand b_n and intra matrix tile, in flight
-        // during the exchange (b_n loaded on the last step too: conditional
-        // loads would keep the registers they replace alive across the whole
-        // iteration)
-        bf16x8 p_cur[2];
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) p_cur[mt] = bld(rp, p_lane[mt] + p_off(n));
+        // ---- this chunk's update operand b_n and intra matrix tile: the first
+        // half of b_n in flight during the exchange, the rest after it, as the
+        // registers allow (b_n loaded on the last step too: conditional loads
+        // would keep the registers they replace alive across the whole iteration)
         bf16x8 ua[MH][4];
         const uint32_t urow = uniform(static_cast<uint32_t>(n * KT32) * 4 * TB);
 #pragma unroll
         for (int mh = 0; mh < MH; ++mh)
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) ua[mh][ks] = bld(rua, lane16 + urow + u_blk[mh] + ks * TB);
+            for (int ks = 0; ks < UA_EARLY; ++ks) ua[mh][ks] = bld(rua, lane16 + urow + u_blk[mh] + ks * TB);
+        phase();
+        if (step > 0) exchange(chunk_of(step - 1), s_read_prev);
+        phase();
+        bf16x8 p_cur[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) p_cur[mt] = bld(rp, p_lane[mt] + p_off(n));
+#pragma unroll
+        for (int mh = 0; mh < MH; ++mh)
+#pragma unroll
+            for (int ks = UA_EARLY; ks < 4; ++ks) ua[mh][ks] = bld(rua, lane16 + urow + u_blk[mh] + ks * TB);
         phase();
 
         const float s_read = s_state;   // the state scale of this read-out

@@ -155,6 +155,13 @@ def test_block_entry_points_reject_bad_arguments_without_touching_the_gpu():
     assert st == nat.ULM_ERR_INVALID and b"multiples of 8" in lib.ulm_last_error()
     st = lib.ulm_cast(P, 5, P, nat.ULM_F32, 4, P)
     assert st == nat.ULM_ERR_INVALID and b"bad dtype" in lib.ulm_last_error()
+    # block parameters: sizes, pointers, the clamp range
+    st = lib.ulm_block_params(P, P, -7.0, 12.0, 0, P, P, P)
+    assert st == nat.ULM_ERR_INVALID and b"A=0" in lib.ulm_last_error()
+    st = lib.ulm_block_params(P, None, -7.0, 12.0, 16, P, P, P)
+    assert st == nat.ULM_ERR_INVALID and b"null pointer" in lib.ulm_last_error()
+    st = lib.ulm_block_params_bwd(x, x, 12.0, -7.0, x, x, 16, x, x, P)
+    assert st == nat.ULM_ERR_INVALID and b"empty clamp range" in lib.ulm_last_error()
 
 
 def test_block_workspace_sizes():

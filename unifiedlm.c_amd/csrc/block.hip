@@ -240,6 +240,7 @@ __global__ __launch_bounds__(kColsMaxD) void norm_conv_bwd_cols_kernel(
     const float *__restrict__ cw, int Kc, const TD *__restrict__ du, const TD *__restrict__ dhv,
     const float *dres, float *dx, float *__restrict__ pw, int T, int D) {
     __shared__ float part[kColTP][kColsMaxD / kWave];   // per-wave row-dot partials
+    __shared__ float dots[kColTP];
     const int d = threadIdx.x, wave = d / kWave, lane = d % kWave, nwave = blockDim.x / kWave;
     const bool vd = d < D;
     const uint32_t dc = vd ? d : 0;
@@ -302,13 +303,17 @@ __global__ __launch_bounds__(kColsMaxD) void norm_conv_bwd_cols_kernel(
         dr[i] = (vd && t < T) ? v : 0.f;
     }
     __syncthreads();
-    const float invD = 1.f / static_cast<float>(D);
+    // thread i < kColTP sums row i over the waves in a fixed order
+    if (d < kColTP) {
+        float dot = 0.f;
+        for (int w = 0; w < nwave; ++w) dot += part[d][w];
+        dots[d] = dot * (1.f / static_cast<float>(D));
+    }
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < kColTP; ++i) {
         const int t = t0 + i;
-        float dot = 0.f;
-        for (int w = 0; w < nwave; ++w) dot += part[i][w];
-        dot *= invD;
+        const float dot = dots[i];
         const float g = rv[i] * (dh[i] * nwd - xv[i] * dot);
         if (vd && t < T) st_row(dx + (row0 + t) * D, 4u * dc, dr[i] + g);
     }
@@ -318,6 +323,75 @@ __global__ __launch_bounds__(kColsMaxD) void norm_conv_bwd_cols_kernel(
 #pragma unroll
         for (int m = 0; m < kMaxTaps; ++m)
             if (m < Kc) row[D + d * Kc + (Kc - 1 - m)] = g2[m];
+    }
+}
+
+// Channel-per-thread forward for D <= kColsMaxD: one workgroup per
+// (kColTP positions, batch row), a thread per channel. Each thread loads x of
+// its channel at the tile's kColTP rows and the kMaxTaps - 1 rows before them
+// once (halo rows a conv with Kc < kMaxTaps does not reach are clamped onto
+// the tile's first row, already loaded); the rows' mean squares are wave sums
+// plus a fixed-order sum over the waves in LDS; h and the conv output u
+// (taps right-aligned, wa[q] = cw[q - (kMaxTaps - Kc)]) go out from registers.
+template <typename TX, typename TO>
+__global__ __launch_bounds__(1024) void norm_conv_fwd_cols_kernel(const TX *__restrict__ x,
+                                                                  const float *__restrict__ nw,
+                                                                  const float *__restrict__ cw, int Kc, float eps,
+                                                                  TO *__restrict__ h, TO *__restrict__ u,
+                                                                  float *__restrict__ rstd, int T, int D) {
+    constexpr int halo = kMaxTaps - 1;
+    constexpr int W = kColTP + halo;   // rows t0 - halo .. t0 + kColTP - 1
+    __shared__ float part[W][1024 / kWave];
+    __shared__ float rs[W];
+    const int d = threadIdx.x, wave = d / kWave, lane = d % kWave, nwave = blockDim.x / kWave;
+    const bool vd = d < D;
+    const uint32_t dc = vd ? d : 0;
+    const int t0 = blockIdx.x * kColTP;
+    const size_t row0 = static_cast<size_t>(blockIdx.y) * T;
+    const int first = kMaxTaps - Kc;   // rows m < first meet zero taps only
+    float xv[W];
+#pragma unroll
+    for (int m = 0; m < W; ++m) {
+        const int t = t0 - halo + m;
+        const bool used = m >= first && t >= 0 && t < T;   // wave-uniform
+        const int tr = used ? t : min(t0, T - 1);
+        const float v = ldrow(x + (row0 + tr) * D, dc);
+        xv[m] = (used && vd) ? v : 0.f;
+    }
+#pragma unroll
+    for (int m = 0; m < W; ++m) {
+        const float ss = wave_sum(xv[m] * xv[m]);
+        if (lane == 0) part[m][wave] = ss;
+    }
+    float wa[kMaxTaps];
+#pragma unroll
+    for (int q = 0; q < kMaxTaps; ++q) wa[q] = q >= first ? cw[static_cast<size_t>(dc) * Kc + (q - first)] : 0.f;
+    const float nwd = vd ? nw[dc] : 0.f;
+    __syncthreads();
+    // thread m < W sums row m over the waves in a fixed order
+    if (d < W) {
+        const int t = t0 - halo + d;
+        float ss = 0.f;
+        for (int w = 0; w < nwave; ++w) ss += part[d][w];
+        const bool ok = d >= first && t >= 0 && t < T;
+        const float r = ok ? rsqrtf(ss * (1.f / static_cast<float>(D)) + eps) : 0.f;
+        rs[d] = r;
+        if (d >= halo && t < T) rstd[row0 + t] = r;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < W; ++m) xv[m] = (xv[m] * rs[m]) * nwd;   // h
+#pragma unroll
+    for (int i = 0; i < kColTP; ++i) {
+        const int t = t0 + i;
+        float acc = 0.f;
+#pragma unroll
+        for (int q = 0; q < kMaxTaps; ++q) acc += wa[q] * xv[i + q];
+        if (vd && t < T) {
+            const size_t o = (row0 + t) * D + d;
+            stf(h, o, xv[halo + i]);
+            stf(u, o, acc);
+        }
     }
 }
 
@@ -358,6 +432,12 @@ BwdWs bwd_layout(void *base, int B, int T, int D, int Kc) {
 template <typename TX, typename TO>
 int launch_fwd(const void *x, const float *nw, const float *cw, int Kc, float eps, void *h, void *u, float *rstd, int B,
                int T, int D, hipStream_t s) {
+    if (D <= kColsMaxD) {
+        const int nth = (D + kWave - 1) / kWave * kWave;
+        norm_conv_fwd_cols_kernel<TX, TO><<<dim3((T + kColTP - 1) / kColTP, B), nth, 0, s>>>(
+            static_cast<const TX *>(x), nw, cw, Kc, eps, static_cast<TO *>(h), static_cast<TO *>(u), rstd, T, D);
+        return check_launch("norm_conv_fwd_cols_kernel");
+    }
     const dim3 grid((T + kFwdTP - 1) / kFwdTP, B);
     norm_conv_fwd_kernel<TX, TO><<<grid, kThreads, 0, s>>>(static_cast<const TX *>(x), nw, cw, Kc, eps,
                                                            static_cast<TO *>(h), static_cast<TO *>(u), rstd, T, D);

@@ -236,9 +236,12 @@ int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const 
     if (fm_aligned(B, T, A, D)) {
         const int nkg = la_kgroup_groups(A);
         float *acc = ws.part ? ws.part : static_cast<float *>(fast);
-        ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, sv.qR, sv.kR, sv.qQ, sv.kQ, sv.nck, c_last, B, T, A, s,
-                                 qw, qw_dt));
-        ULM_TRY(launch_chunk_transpose(v, v_dtype, sv.vQ, sv.vQl, sv.vR, sv.vRl, B, T, D, s));
+        // a prefill (state wanted) has no backward, the only reader of q in the Q
+        // layout and of v in the R layout: those tiles are not written then
+        ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, sv.qR, sv.kR, state ? nullptr : sv.qQ, sv.kQ, sv.nck,
+                                 c_last, B, T, A, s, qw, qw_dt));
+        ULM_TRY(launch_chunk_transpose(v, v_dtype, sv.vQ, sv.vQl, state ? nullptr : sv.vR, state ? nullptr : sv.vRl, B,
+                                       T, D, s));
         ULM_TRY(launch_chunk_scores(sv.qR, nullptr, sv.kR, nullptr, g, ws.Pf, sv.Pdv, B, T, A, true, s));
         // fast = LA(q, k, v): update k^T v~ (v~ from the full-precision v), intra on
         // bf16(v), as the reference's bf16 v (kernel.py:205). Its state, transposed,

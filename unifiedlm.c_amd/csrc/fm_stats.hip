@@ -216,13 +216,14 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
                 kpk[i / 2] |= static_cast<uint32_t>(kb) << 16;
             }
         }
-        if (qQ && va) {
+        if ((qQ || kQ) && va) {
             // Q layout: this thread's positions 16 j .. 16 j + 15 of slot a are two lanes' 16 bytes
+            // (qQ is null where no backward follows, as in a prefill)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const size_t o = q_index(b, n * ULM_CHUNK + kSeg * j + 8 * h, a, NT, A);
-                *reinterpret_cast<uint4 *>(qQ + o) = make_uint4(qpk[4 * h], qpk[4 * h + 1], qpk[4 * h + 2], qpk[4 * h + 3]);
-                *reinterpret_cast<uint4 *>(kQ + o) = make_uint4(kpk[4 * h], kpk[4 * h + 1], kpk[4 * h + 2], kpk[4 * h + 3]);
+                if (qQ) *reinterpret_cast<uint4 *>(qQ + o) = make_uint4(qpk[4 * h], qpk[4 * h + 1], qpk[4 * h + 2], qpk[4 * h + 3]);
+                if (kQ) *reinterpret_cast<uint4 *>(kQ + o) = make_uint4(kpk[4 * h], kpk[4 * h + 1], kpk[4 * h + 2], kpk[4 * h + 3]);
             }
         }
         if (j == 0 && va) nck[(bs * NT + n) * A + a] = carry;
@@ -426,9 +427,10 @@ int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, 
                      int A, hipStream_t s, void *qw, int qw_dt) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
     if ((q16n == nullptr) != (k16n == nullptr)) return fail(ULM_ERR_INVALID, "fwd stats: q16n and k16n go together");
+    // the tiled copies: qR, kR and kQ together (qQ, read only by a backward, may be left out)
     const bool tiled = qR || kR || qQ || kQ;
-    if (tiled && !(qR && kR && qQ && kQ && A % 32 == 0))
-        return fail(ULM_ERR_INVALID, "fwd stats: tiled copies need all four outputs and A %% 32 == 0");
+    if (tiled && !(qR && kR && kQ && A % 32 == 0))
+        return fail(ULM_ERR_INVALID, "fwd stats: tiled copies need qR, kR, kQ and A %% 32 == 0");
     if (qw && !valid_dtype(qw_dt)) return fail(ULM_ERR_INVALID, "fwd stats: bad w q dtype %d", qw_dt);
     const int qwk = qw ? qw_dt : -1;
     return with_rsrc(src, [&](auto rs) {

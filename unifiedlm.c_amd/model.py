@@ -161,7 +161,7 @@ class UnifiedBlock(nn.Module):
         kw = self.conv.kernel_size[0] - 1
         buf = torch.zeros(B, d, kw, device=x.device, dtype=torch.float32)
         if kw > 0:
-            tail = h.float()[:, max(0, T - kw):, :].transpose(1, 2)   # the last (up to) kw positions, oldest first
+            tail = h[:, max(0, T - kw):, :].float().transpose(1, 2)   # the last (up to) kw positions, oldest first
             buf[:, :, kw - tail.size(-1):] = tail
         state = {"buf": buf, "S": S, "c": c, "r_prev": r_prev, "params": self._step_params(x.device)}
         return out, state

@@ -361,20 +361,22 @@ def unified_block(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rat
 
 @torch.no_grad()
 @torch.no_grad()
-def block_prefill(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, g, w, norm_eps, cdt=torch.float32):
+def block_prefill(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, norm_eps,
+                  cdt=torch.float32):
     """UnifiedBlock.forward over a prompt (no autograd), fused as in
     UnifiedBlockFn, plus what decoding continues from: returns (out, S, c,
     r_prev, h) with S (B, D, A) and c (B, A) the fast-memory state after the
     last position (as fm_prefill), r_prev (B, A) fp32 the address at that
     position and h (B, T, D) the normalised input in cdt (its last positions
-    fill the conv window). A and D must be multiples of 32."""
+    fill the conv window). A and D must be multiples of 32. log_rate and log_w
+    are the block's parameters, as for unified_block."""
     if x.dim() != 3 or x.dtype != torch.float32:
         raise ValueError(f"x must be (B, T, D) fp32, got {tuple(x.shape)} {x.dtype}")
     B, T, D = x.shape
     A = key_w.shape[0]
     Kc = conv_w.shape[-1]
     M = B * T
-    nat.require_device(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, g, w)
+    nat.require_device(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w)
     cd = nat.dtype_code(cdt)
     ws_bytes = nat.lib().ulm_block_fm_prefill_workspace_bytes(B, T, A, D, cd)
     if ws_bytes == 0:
@@ -398,8 +400,11 @@ def block_prefill(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, g, w, n
     le = log_eps.float().reshape(1).contiguous()
     denom = torch.empty(M, device=dev, dtype=f32)
     call("ulm_addr_fwd", ptr(pre), cd, ptr(b32), ptr(le), None, ptr(denom), M, A, s)
-    g1 = g.float().reshape(1).contiguous()
-    w32 = w.float().contiguous()
+    lr = log_rate.float().reshape(1).contiguous()
+    lw = log_w.float().contiguous()
+    g1 = torch.empty(1, device=dev, dtype=f32)
+    w32 = torch.empty(A, device=dev, dtype=f32)
+    call("ulm_block_params", ptr(lr), ptr(lw), LOG_W_MIN, LOG_W_MAX, A, ptr(g1), ptr(w32), s)
     qw = torch.empty(M, A, device=dev, dtype=cdt)
     y = torch.empty(M, D, device=dev, dtype=f32)
     S = torch.empty(B, D, A, device=dev, dtype=f32)

@@ -142,15 +142,15 @@ class UnifiedBlock(nn.Module):
         (kernel.block_prefill), its GEMMs in the autocast dtype."""
         B, T, d = x.shape
         A = self.mu.in_features
-        w = self._w()
-        g = -self.log_rate.exp()
         if x.dtype == torch.float32 and A % 32 == 0 and d % 32 == 0:
             cdt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else torch.float32
             with torch.autocast("cuda", enabled=False):
                 out, S, c, r_prev, h = block_prefill(x, self.norm.weight, self.conv.weight, self.key.weight,
-                                                     self.key.bias, self.log_eps, self.val.weight, self.mu.weight, g,
-                                                     w, self.norm.eps, cdt)
+                                                     self.key.bias, self.log_eps, self.val.weight, self.mu.weight,
+                                                     self.log_rate, self.log_w, self.norm.eps, cdt)
         else:
+            w = self._w()
+            g = -self.log_rate.exp()
             h = self.norm(x)
             u = self.conv(h.transpose(1, 2))[..., : h.size(1)].transpose(1, 2)
             r = self.code(u)

@@ -82,11 +82,10 @@ constexpr int WAVES = 8;                       // two per SIMD
 constexpr int MAX_MH = 3;                      // key blocks per wave, at most
 constexpr int GROUP_BLOCKS = WAVES * MAX_MH;   // 24 blocks = 768 keys per workgroup
 constexpr int VT = 64;                         // value columns per workgroup
-constexpr int ROWS_PER_WAVE = C / WAVES;
+constexpr int ROWS_PER_WAVE = C / WAVES;       // output rows each wave reduces and stores
 // k-steps of the update operand b_n loaded before the previous chunk's
-// exchange (so in flight during it); the rest follow it. More than two spill
-// in the forward walk and measured slower in the reversed one.
-constexpr int UA_EARLY = 2;       // output rows each wave reduces and stores
+// exchange (so in flight during it); the rest follow it. More measured slower.
+constexpr int UA_EARLY = 2;
 constexpr uint32_t TB = kTileElems * 2;        // bytes per operand tile
 constexpr uint32_t OOB = 0x80000000u;          // buffer offset past every range: the load returns zeros
 // LDS: the staged c tiles (decayed hi, decayed lo, raw: eight 1 KB tiles

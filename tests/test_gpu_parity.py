@@ -76,18 +76,27 @@ OP_CASES = [
     (2, 200, 128, 64, torch.float32),      # K-group kernels with a ragged last chunk
     (1, 512, 3072, 768, torch.bfloat16),   # 110M-shape block, one row of 512 positions
     (8, 512, 128, 64, torch.float32),      # 260K-shape block (all 8 rows of 512 positions)
-    (1, 1024, 2048, 512, torch.bfloat16),  # 42M-shape block, one row: 3 key groups of 704 / 704 / 640 slots;
-                                           # dg there is ill-conditioned under white-noise gradients (see below)
+    (1, 1024, 2048, 512, torch.bfloat16),  # 42M-shape block, one row
+    (1, 1024, 3072, 768, torch.float32),   # 110M-shape block, one row of 1024 positions, fp32 v
 ]
 
 
 @pytest.mark.parametrize("B,T,A,D,vdt", OP_CASES)
 def test_unified_memory_matches_oracle(B, T, A, D, vdt):
+    """q, fast and every gradient against the float64 oracle, within 1e-2.
+
+    The upstream gradients are those of L = 0.5 |fast|^2 + 0.05 |q|^2 (dfast =
+    fast, dq = 0.1 q, from the oracle), the structure a training loss gives
+    them. Under white-noise upstream gradients the decay gradient dg is a sum
+    of random-sign terms that can land far below its natural scale: with this
+    file's 42M-shape seed it is 1/60 of it, and rounding dfast to bf16 alone
+    (as the reference does, kernel.py:217) moves it by 17%. With the loss above
+    bf16 operands move dg by about 1e-5, so dg is held to 1e-2 like the rest."""
     say(f"unified_memory B={B} T={T} A={A} D={D} v={vdt}")
     r, v, g, w = fm_inputs(B, T, A, D, seed=T + A, device="cpu")
-    gen = torch.Generator().manual_seed(7)
-    dq = torch.randn(B, T, A, generator=gen, dtype=torch.float64) * 0.1
-    df = torch.randn(B, T, D, generator=gen, dtype=torch.float64)
+    vr = v.to(vdt).double()
+    qr, fr = fm.fast_memory(r, vr, g, w, "chunked")
+    dq, df = 0.1 * qr, fr.clone()
     # GPU: fp32 inputs (v in vdt), grads for all four
     rg = r.float().cuda().requires_grad_(True)
     vg = v.to(vdt).cuda().requires_grad_(True)
@@ -98,21 +107,21 @@ def test_unified_memory_matches_oracle(B, T, A, D, vdt):
     ((q * dq.float().cuda()).sum() + (fast.float() * df.float().cuda()).sum()).backward()
     torch.cuda.synchronize()
     # oracle: float64 on the same (rounded) inputs
-    vr = v.to(vdt).double()
-    qr, fr = fm.fast_memory(r, vr, g, w, "chunked")
     dr, dv, dgr, dw = fm.fast_memory_grads(r, vr, g, w, dq, df)
     assert rel(q, qr) < 1e-5
     assert rel(fast, fr) < 1e-2
     errs = {"dr": rel(rg.grad, dr), "dv": rel(vg.grad, dv), "dg": rel(gg.grad, dgr), "dw": rel(wg.grad, dw)}
-    # dg is the small difference of two large positional sums: under these
-    # white-noise upstream gradients bf16 operands alone can move it by more
-    # than 1e-2 (T = 1024 at the 42M shape: 15% in exact arithmetic). It is
-    # held to 1e-2 or to that floor (oracle.fastmem.dg_bf16_floor), whichever
-    # is larger; every other output and gradient to 1e-2.
-    floor = rel(fm.dg_bf16_floor(r, vr, g, w, dq, df), dgr)
-    say(f"  rel errors {errs}, dg floor of bf16 operands {floor:.2e}")
-    tol = {"dr": 1e-2, "dv": 1e-2, "dw": 1e-2, "dg": max(1e-2, floor)}
-    assert all(errs[n] < tol[n] for n in errs), (errs, floor)
+    say(f"  rel errors {errs}")
+    assert max(errs.values()) < 1e-2, errs
+
+
+@pytest.mark.parametrize("path", ["chunked", "pair"])
+@pytest.mark.parametrize("B,T,A,D", [(2, 200, 128, 64), (2, 130, 96, 160), (1, 512, 3072, 768)])
+def test_unified_memory_paths(B, T, A, D, path, monkeypatch):
+    """Both evaluations of the aligned products, forced by ULM_FM_PATH: the
+    chunked state form and the block-pair form, each against the oracle."""
+    monkeypatch.setenv("ULM_FM_PATH", path)
+    test_unified_memory_matches_oracle(B, T, A, D, torch.bfloat16)
 
 
 @pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])

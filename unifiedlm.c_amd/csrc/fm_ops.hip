@@ -25,6 +25,8 @@
 // fp32 outputs) on natural bf16 copies of q, k and v.
 #include "ulm_common.h"
 
+#include <stdlib.h>
+
 namespace ulm {
 
 // fm_chunk.hip
@@ -50,7 +52,18 @@ int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, 
 size_t bwd_stats_partial_bytes(int B, int A);
 int launch_bwd_stats(const float *dqf, const float *dqo, const RSrc &src, const float *nck,
                      const float *w, const float *g, const float *dkf, float *dr, float *dw, float *dg, void *part,
-                     int B, int T, int A, hipStream_t s, const void *dqw = nullptr, int dqw_dt = ULM_BF16);
+                     int B, int T, int A, hipStream_t s, const void *dqw = nullptr, int dqw_dt = ULM_BF16,
+                     const double *dg_extra = nullptr, int nextra = 0);
+// pair.hip
+int pair_tq(int B, int T);
+size_t pair_p_bytes(int B, int T);
+int pair_dscore_jobs(int B, int T);
+double pair_flops_per_token(int B, int T, int A, int D);
+int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *vQ, const float *g, uint16_t *P,
+                        void *out, int out_dt, const float *resid, int B, int T, int A, int D, hipStream_t s);
+int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t *doQ, const uint16_t *kQ,
+                         const uint16_t *qQ, const uint16_t *P, const float *g, uint16_t *dS, double *dg_part,
+                         float *dqf, float *dkf, void *dv, int dv_dt, int B, int T, int A, int D, hipStream_t s);
 
 namespace {
 
@@ -61,19 +74,44 @@ bool fm_aligned(int B, int T, int A, int D) {
     return la_kgroup_supported(B, T, A, D) && la_kgroup_supported(B, T, D, A);
 }
 
+// How the training entries evaluate the products: the generic kernel (A or D
+// not a multiple of 32), the chunked state form (K-group kernel) or the
+// block-pair form (pair.hip), whichever needs fewer flops: the pair form costs
+// about T (A + D) per token and product, the state form 4 A D, so the pair form
+// serves sequences up to a few thousand positions. ULM_FM_PATH=chunked or
+// =pair in the environment forces one of the two for aligned shapes (it must
+// not change between a forward and its backward).
+enum Path { PATH_GENERIC = 0, PATH_CHUNKED = 1, PATH_PAIR = 2 };
+
+Path train_path(int B, int T, int A, int D) {
+    if (!fm_aligned(B, T, A, D)) return PATH_GENERIC;
+    const char *env = getenv("ULM_FM_PATH");
+    if (env && env[0] == 'c') return PATH_CHUNKED;
+    if (T > 4096) return PATH_CHUNKED;
+    if (env && env[0] == 'p') return PATH_PAIR;
+    const double chunked = 16.0 * A * D + 8.0 * ULM_CHUNK * (A + D);
+    return pair_flops_per_token(B, T, A, D) < 0.8 * chunked ? PATH_PAIR : PATH_CHUNKED;
+}
+
 struct Saved {
     uint16_t *q16n, *k16n, *v16n;                                     // generic path
-    uint16_t *qR, *kR, *qQ, *kQ, *vR, *vRl, *vQ, *vQl, *Pdv;   // K-group path
+    uint16_t *qR, *kR, *qQ, *kQ, *vR, *vRl, *vQ, *vQl, *Pdv;   // K-group path (pair: qQ, kQ, vR)
+    uint16_t *P;                                                      // pair path: the scores
     float *nck;
     size_t bytes;
 };
 
-Saved saved_layout(void *base, int B, int T, int A, int D, int v_dtype) {
+Saved saved_layout(void *base, int B, int T, int A, int D, int v_dtype, Path path) {
     const size_t NT = nt_of(T);
     const size_t na = static_cast<size_t>(B) * T * A, ta = B * NT * 64 * A, td = B * NT * 64 * D;
     Carver c(base);
     Saved s{};
-    if (fm_aligned(B, T, A, D)) {
+    if (path == PATH_PAIR) {
+        s.qQ = c.take<uint16_t>(ta);
+        s.kQ = c.take<uint16_t>(ta);
+        s.vR = c.take<uint16_t>(td);
+        s.P = c.take<uint16_t>(pair_p_bytes(B, T) / 2);
+    } else if (path == PATH_CHUNKED) {
         s.qR = c.take<uint16_t>(ta);
         s.kR = c.take<uint16_t>(ta);
         s.qQ = c.take<uint16_t>(ta);
@@ -95,16 +133,21 @@ Saved saved_layout(void *base, int B, int T, int A, int D, int v_dtype) {
 
 struct FwdWs {
     uint16_t *Pf;
+    uint16_t *qR, *kR, *vQ;   // pair path: the forward's operand tiles
     float *part;   // fp32 output or partials
     size_t bytes;
 };
 
-// resid: the output is x + fast, so the products always go through fp32 partials
-FwdWs fwd_layout(void *base, int B, int T, int A, int D, int fast_dtype, bool resid = false) {
+// resid: the output is x + fast, so the chunked products always go through fp32 partials
+FwdWs fwd_layout(void *base, int B, int T, int A, int D, int fast_dtype, Path path, bool resid = false) {
     const size_t NT = nt_of(T), nd = static_cast<size_t>(B) * T * D;
     Carver c(base);
     FwdWs w{};
-    if (fm_aligned(B, T, A, D)) {
+    if (path == PATH_PAIR) {
+        w.qR = c.take<uint16_t>(B * NT * 64 * A);
+        w.kR = c.take<uint16_t>(B * NT * 64 * A);
+        w.vQ = c.take<uint16_t>(B * NT * 64 * D);
+    } else if (path == PATH_CHUNKED) {
         w.Pf = c.take<uint16_t>(B * NT * ULM_CHUNK * ULM_CHUNK);
         const int nkg = la_kgroup_groups(A);
         if (nkg > 1 || fast_dtype != ULM_F32 || resid) w.part = c.take<float>(nkg * nd);
@@ -117,20 +160,27 @@ FwdWs fwd_layout(void *base, int B, int T, int A, int D, int fast_dtype, bool re
 
 struct BwdWs {
     uint16_t *do16;                                          // generic path
-    uint16_t *doR, *doRl, *doQ, *doQl, *Pdq, *Pdk;   // K-group path
+    uint16_t *doR, *doRl, *doQ, *doQl, *Pdq, *Pdk;   // K-group path (pair: doR, doQ)
+    uint16_t *dS;                                            // pair path: the score gradients
+    double *dgx;                                             // pair path: dg partials of the pair products
     float *dqf, *dkf, *part;
     void *stats;
     size_t bytes;
 };
 
-BwdWs bwd_layout(void *base, int B, int T, int A, int D, int dfast_dtype) {
+BwdWs bwd_layout(void *base, int B, int T, int A, int D, int dfast_dtype, Path path) {
     const size_t NT = nt_of(T), nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
     const size_t td = B * NT * 64 * D;
     Carver c(base);
     BwdWs w{};
     w.dqf = c.take<float>(na);
     w.dkf = c.take<float>(na);
-    if (fm_aligned(B, T, A, D)) {
+    if (path == PATH_PAIR) {
+        w.doR = c.take<uint16_t>(td);
+        w.doQ = c.take<uint16_t>(td);
+        w.dS = c.take<uint16_t>(pair_p_bytes(B, T) / 2);
+        w.dgx = c.take<double>(pair_dscore_jobs(B, T));
+    } else if (path == PATH_CHUNKED) {
         w.doR = c.take<uint16_t>(td);
         if (dfast_dtype != ULM_BF16) w.doRl = c.take<uint16_t>(td);
         w.doQ = c.take<uint16_t>(td);
@@ -213,27 +263,35 @@ extern "C" int ulm_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
 
 extern "C" size_t ulm_fm_saved_bytes(int B, int T, int A, int D, int v_dtype) {
     if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(v_dtype)) return 0;
-    return saved_layout(nullptr, B, T, A, D, v_dtype).bytes;
+    return saved_layout(nullptr, B, T, A, D, v_dtype, train_path(B, T, A, D)).bytes;
 }
 
 extern "C" size_t ulm_fm_fwd_workspace_bytes(int B, int T, int A, int D, int fast_dtype) {
     if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(fast_dtype)) return 0;
-    return fwd_layout(nullptr, B, T, A, D, fast_dtype).bytes;
+    return fwd_layout(nullptr, B, T, A, D, fast_dtype, train_path(B, T, A, D)).bytes;
 }
 
 namespace {
 
 // The forward composite of ulm_fm_fwd; with state (B, D, A) and c_last (B, A)
-// (aligned shapes only) it also emits the decode state after position T-1.
-// q (fp32) and qw (w q in qw_dt) are each optional; with resid (fp32 (B,T,D))
-// the output is resid + fast.
+// (aligned shapes, the chunked path) it also emits the decode state after
+// position T-1. q (fp32) and qw (w q in qw_dt) are each optional; with resid
+// (fp32 (B,T,D)) the output is resid + fast.
 int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const float *w, float *q, void *qw,
                int qw_dt, const float *resid, void *fast, int fast_dtype, void *saved, void *workspace, float *state,
-               float *c_last, int B, int T, int A, int D, hipStream_t s) {
-    const Saved sv = saved_layout(saved, B, T, A, D, v_dtype);
-    const FwdWs ws = fwd_layout(workspace, B, T, A, D, fast_dtype, resid != nullptr);
+               float *c_last, int B, int T, int A, int D, Path path, hipStream_t s) {
+    const Saved sv = saved_layout(saved, B, T, A, D, v_dtype, path);
+    const FwdWs ws = fwd_layout(workspace, B, T, A, D, fast_dtype, path, resid != nullptr);
     const size_t nf = static_cast<size_t>(B) * T * D;
-    if (fm_aligned(B, T, A, D)) {
+    if (path == PATH_PAIR) {
+        if (state || c_last) return fail(ULM_ERR_INVALID, "prefill state: not on the block-pair path");
+        ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, ws.qR, ws.kR, sv.qQ, sv.kQ, sv.nck, nullptr, B, T, A, s,
+                                 qw, qw_dt));
+        // v: Q layout for the apply product, R layout (saved) for the backward's dscores
+        ULM_TRY(launch_chunk_transpose(v, v_dtype, ws.vQ, nullptr, sv.vR, nullptr, B, T, D, s));
+        return launch_pair_forward(ws.qR, ws.kR, ws.vQ, g, sv.P, fast, fast_dtype, resid, B, T, A, D, s);
+    }
+    if (path == PATH_CHUNKED) {
         const int nkg = la_kgroup_groups(A);
         float *acc = ws.part ? ws.part : static_cast<float *>(fast);
         // a prefill (state wanted) has no backward, the only reader of q in the Q
@@ -278,7 +336,7 @@ extern "C" int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const floa
     RSrc rs;
     rs.r = r;
     return fm_forward(rs, v, v_dtype, g, w, q, nullptr, ULM_F32, nullptr, fast, fast_dtype, saved, workspace, nullptr,
-                      nullptr, B, T, A, D, static_cast<hipStream_t>(stream));
+                      nullptr, B, T, A, D, train_path(B, T, A, D), static_cast<hipStream_t>(stream));
 }
 
 // ---------------------------------------------------------------------------
@@ -287,7 +345,8 @@ extern "C" int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const floa
 extern "C" size_t ulm_fm_prefill_workspace_bytes(int B, int T, int A, int D, int v_dtype, int fast_dtype) {
     if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(v_dtype) || !valid_dtype(fast_dtype)) return 0;
     if (!fm_aligned(B, T, A, D)) return 0;
-    return align_up(saved_layout(nullptr, B, T, A, D, v_dtype).bytes, 256) + fwd_layout(nullptr, B, T, A, D, fast_dtype).bytes;
+    return align_up(saved_layout(nullptr, B, T, A, D, v_dtype, PATH_CHUNKED).bytes, 256) +
+           fwd_layout(nullptr, B, T, A, D, fast_dtype, PATH_CHUNKED).bytes;
 }
 
 extern "C" int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const float *g, const float *w, float *q,
@@ -302,16 +361,16 @@ extern "C" int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const 
     const size_t need = ulm_fm_prefill_workspace_bytes(B, T, A, D, v_dtype, fast_dtype);
     ULM_REQUIRE(workspace_bytes >= need, "ulm_fm_prefill: workspace of %zu bytes, need %zu", workspace_bytes, need);
     char *saved = static_cast<char *>(workspace);
-    char *ws = saved + align_up(saved_layout(nullptr, B, T, A, D, v_dtype).bytes, 256);
+    char *ws = saved + align_up(saved_layout(nullptr, B, T, A, D, v_dtype, PATH_CHUNKED).bytes, 256);
     RSrc rs;
     rs.r = r;
     return fm_forward(rs, v, v_dtype, g, w, q, nullptr, ULM_F32, nullptr, fast, fast_dtype, saved, ws, S, c_last, B, T,
-                      A, D, static_cast<hipStream_t>(stream));
+                      A, D, PATH_CHUNKED, static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D, int dfast_dtype) {
     if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(dfast_dtype)) return 0;
-    return bwd_layout(nullptr, B, T, A, D, dfast_dtype).bytes;
+    return bwd_layout(nullptr, B, T, A, D, dfast_dtype, train_path(B, T, A, D)).bytes;
 }
 
 namespace {
@@ -321,10 +380,18 @@ namespace {
 int fm_backward(const RSrc &r, const float *g, const float *w, const void *saved, int v_dtype, const void *dfast,
                 int dfast_dtype, const float *dq_out, const void *dqw, int dqw_dt, float *dr, void *dv, int dv_dtype,
                 float *dg, float *dw, void *workspace, int B, int T, int A, int D, hipStream_t s) {
-    const Saved sv = saved_layout(const_cast<void *>(saved), B, T, A, D, v_dtype);
-    const BwdWs ws = bwd_layout(workspace, B, T, A, D, dfast_dtype);
+    const Path path = train_path(B, T, A, D);
+    const Saved sv = saved_layout(const_cast<void *>(saved), B, T, A, D, v_dtype, path);
+    const BwdWs ws = bwd_layout(workspace, B, T, A, D, dfast_dtype, path);
     const size_t nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
-    if (fm_aligned(B, T, A, D)) {
+    if (path == PATH_PAIR) {
+        ULM_TRY(launch_chunk_transpose(dfast, dfast_dtype, ws.doQ, nullptr, ws.doR, nullptr, B, T, D, s));
+        ULM_TRY(launch_pair_backward(sv.vR, ws.doR, ws.doQ, sv.kQ, sv.qQ, sv.P, g, ws.dS, ws.dgx, ws.dqf, ws.dkf, dv,
+                                     dv_dtype, B, T, A, D, s));
+        return launch_bwd_stats(ws.dqf, dq_out, r, sv.nck, w, g, ws.dkf, dr, dw, dg, ws.stats, B, T, A, s, dqw, dqw_dt,
+                                ws.dgx, pair_dscore_jobs(B, T));
+    }
+    if (path == PATH_CHUNKED) {
         const int nkd = la_kgroup_groups(D), nka = la_kgroup_groups(A);
         ULM_TRY(launch_chunk_transpose(dfast, dfast_dtype, ws.doQ, ws.doQl, ws.doR, ws.doRl, B, T, D, s));
         // unscaled: P_dk = P_dq^T exactly, so the intra-chunk terms of dq and dk
@@ -392,7 +459,7 @@ extern "C" int ulm_fm_bwd(const float *r, const float *g, const float *w, const 
 
 extern "C" size_t ulm_block_fm_fwd_workspace_bytes(int B, int T, int A, int D) {
     if (B <= 0 || T <= 0 || A <= 0 || D <= 0) return 0;
-    return fwd_layout(nullptr, B, T, A, D, ULM_F32, true).bytes;
+    return fwd_layout(nullptr, B, T, A, D, ULM_F32, train_path(B, T, A, D), true).bytes;
 }
 
 extern "C" int ulm_block_fm_fwd(const void *pre, int pre_dtype, const float *bias, const float *denom, const void *v,
@@ -414,7 +481,7 @@ extern "C" int ulm_block_fm_fwd(const void *pre, int pre_dtype, const float *bia
     rs.bias = bias;
     rs.denom = denom;
     return fm_forward(rs, v, v_dtype, g, w, nullptr, qw, qw_dtype, x, y, ULM_F32, saved, workspace, nullptr, nullptr, B,
-                      T, A, D, static_cast<hipStream_t>(stream));
+                      T, A, D, train_path(B, T, A, D), static_cast<hipStream_t>(stream));
 }
 
 extern "C" int ulm_block_fm_bwd(const void *pre, int pre_dtype, const float *bias, const float *denom, const float *g,
@@ -447,8 +514,8 @@ extern "C" int ulm_block_fm_bwd(const void *pre, int pre_dtype, const float *bia
 extern "C" size_t ulm_block_fm_prefill_workspace_bytes(int B, int T, int A, int D, int v_dtype) {
     if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(v_dtype)) return 0;
     if (!fm_aligned(B, T, A, D)) return 0;
-    return align_up(saved_layout(nullptr, B, T, A, D, v_dtype).bytes, 256) +
-           fwd_layout(nullptr, B, T, A, D, ULM_F32, true).bytes;
+    return align_up(saved_layout(nullptr, B, T, A, D, v_dtype, PATH_CHUNKED).bytes, 256) +
+           fwd_layout(nullptr, B, T, A, D, ULM_F32, PATH_CHUNKED, true).bytes;
 }
 
 extern "C" int ulm_block_fm_prefill(const void *pre, int pre_dtype, const float *bias, const float *denom,
@@ -467,12 +534,12 @@ extern "C" int ulm_block_fm_prefill(const void *pre, int pre_dtype, const float 
     ULM_REQUIRE(workspace_bytes >= need, "ulm_block_fm_prefill: workspace of %zu bytes, need %zu", workspace_bytes,
                 need);
     char *saved = static_cast<char *>(workspace);
-    char *ws = saved + align_up(saved_layout(nullptr, B, T, A, D, v_dtype).bytes, 256);
+    char *ws = saved + align_up(saved_layout(nullptr, B, T, A, D, v_dtype, PATH_CHUNKED).bytes, 256);
     RSrc rs;
     rs.pre = pre;
     rs.pre_dt = pre_dtype;
     rs.bias = bias;
     rs.denom = denom;
     return fm_forward(rs, v, v_dtype, g, w, nullptr, qw, qw_dtype, x, y, ULM_F32, saved, ws, S, c_last, B, T, A, D,
-                      static_cast<hipStream_t>(stream));
+                      PATH_CHUNKED, static_cast<hipStream_t>(stream));
 }

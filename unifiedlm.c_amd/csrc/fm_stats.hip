@@ -264,7 +264,8 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
                                                         const float *__restrict__ nck, const float *__restrict__ w,
                                                         const float *__restrict__ g, const float *__restrict__ dkf,
                                                         float *__restrict__ dr, float *__restrict__ dw_part,
-                                                        double *__restrict__ dg_part, int T, int A, int NT) {
+                                                        double *__restrict__ dg_part, int T, int A, int NT,
+                                                        int fast_dg) {
     __shared__ float tot[4][kSlots];
     __shared__ float first_dkt[4][kSlots];
     __shared__ float dw_sh[4][kSlots];
@@ -351,7 +352,7 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
             // products contracted with, so each (t, s) pair enters both sums
             // with the same value and the position weights cancel to t - s.
             const float q16 = bf16_to_f32(f32_to_bf16_bits(qt));
-            const double e = static_cast<double>(q16 * dqfv[i] + dc * (cv[i] - wa));
+            const double e = static_cast<double>((fast_dg ? q16 * dqfv[i] : 0.f) + dc * (cv[i] - wa));
             e0 += e;
             e1 += i * e;
         }
@@ -380,7 +381,7 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
             const float nxt = (i + 1 < kSeg) ? dkfv[i + 1] + dkcv[i + 1] : after;
             if (va && t < T) st_row(dr + (b * T + t) * A, 4u * ac, dqc[i] + nxt);
             const float k16 = bf16_to_f32(f32_to_bf16_bits(kv[i]));
-            const double e = static_cast<double>(k16 * dkfv[i] + kv[i] * dkcv[i]);
+            const double e = static_cast<double>((fast_dg ? k16 * dkfv[i] : 0.f) + kv[i] * dkcv[i]);
             e0 -= e;
             e1 -= i * e;
         }
@@ -397,12 +398,14 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
     if (threadIdx.x == 0) dg_part[b * gridDim.x + blockIdx.x] = dg_sh[0] + dg_sh[1] + dg_sh[2] + dg_sh[3];
 }
 
-// dw[a] = sum_b dw_part[b, a]; dg = sum of all dg partials. Every sum runs in a
-// fixed order (thread-strided partial sums, then a fixed shuffle tree), so the
-// result does not depend on scheduling.
+// dw[a] = sum_b dw_part[b, a]; dg = sum of all dg partials (those of the
+// statistics and, when given, nextra more). Every sum runs in a fixed order
+// (thread-strided partial sums, then a fixed shuffle tree), so the result does
+// not depend on scheduling.
 __global__ __launch_bounds__(256) void stats_reduce_kernel(const float *__restrict__ dw_part,
-                                                           const double *__restrict__ dg_part, float *__restrict__ dw,
-                                                           float *__restrict__ dg, int B, int A, int ndg) {
+                                                           const double *__restrict__ dg_part,
+                                                           const double *__restrict__ dg_extra, float *__restrict__ dw,
+                                                           float *__restrict__ dg, int B, int A, int ndg, int nextra) {
     __shared__ double red[4];
     const int a = blockIdx.x * 256 + threadIdx.x;
     if (a < A) {
@@ -413,6 +416,7 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(const float *__restri
     if (blockIdx.x == 0) {
         double s = 0.0;
         for (int k = threadIdx.x; k < ndg; k += 256) s += dg_part[k];
+        for (int k = threadIdx.x; k < nextra; k += 256) s += dg_extra[k];
         s = wave_sum(s);
         if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = s;
         __syncthreads();
@@ -464,9 +468,13 @@ size_t bwd_stats_partial_bytes(int B, int A) {
     return align_up(static_cast<size_t>(B) * A * sizeof(float), 256) + align_up(B * nb * sizeof(double), 256);
 }
 
+// dg_extra: nextra more partials of dg (the block-pair products' fast-read
+// part); when given, the dq_f / dk_f terms of the positional identity are left
+// out here (fast_dg = 0), since those partials hold that part already.
 int launch_bwd_stats(const float *dqf, const float *dqo, const RSrc &src, const float *nck,
                      const float *w, const float *g, const float *dkf, float *dr, float *dw, float *dg, void *part,
-                     int B, int T, int A, hipStream_t s, const void *dqw, int dqw_dt) {
+                     int B, int T, int A, hipStream_t s, const void *dqw, int dqw_dt, const double *dg_extra,
+                     int nextra) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
     const int nb = (A + kSlots - 1) / kSlots;
     float *dw_part = static_cast<float *>(part);
@@ -476,21 +484,23 @@ int launch_bwd_stats(const float *dqf, const float *dqo, const RSrc &src, const 
     const void *xp = dqw ? dqw : static_cast<const void *>(dqo);
     if (dqw && dqo) return fail(ULM_ERR_INVALID, "bwd stats: dq_out and d(w q) are exclusive");
     if (xq < 0 || xq > 4) return fail(ULM_ERR_INVALID, "bwd stats: bad d(w q) dtype %d", dqw_dt);
+    const int fast_dg = dg_extra ? 0 : 1;
     ULM_TRY(with_rsrc(src, [&](auto rs) {
         using RS = decltype(rs);
         const dim3 grid(nb, B);
         switch (xq) {
-        case 0: bwd_stats_kernel<0, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
-        case 1: bwd_stats_kernel<1, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
-        case 2: bwd_stats_kernel<2, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
-        case 3: bwd_stats_kernel<3, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
-        default: bwd_stats_kernel<4, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT); break;
+        case 0: bwd_stats_kernel<0, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT, fast_dg); break;
+        case 1: bwd_stats_kernel<1, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT, fast_dg); break;
+        case 2: bwd_stats_kernel<2, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT, fast_dg); break;
+        case 3: bwd_stats_kernel<3, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT, fast_dg); break;
+        default: bwd_stats_kernel<4, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT, fast_dg); break;
         }
         return ULM_OK;
     }));
     int st = check_launch("bwd_stats_kernel");
     if (st) return st;
-    stats_reduce_kernel<<<(A + 255) / 256, 256, 0, s>>>(dw_part, dg_part, dw, dg, B, A, B * nb);
+    stats_reduce_kernel<<<(A + 255) / 256, 256, 0, s>>>(dw_part, dg_part, dg_extra, dw, dg, B, A, B * nb,
+                                                        dg_extra ? nextra : 0);
     return check_launch("stats_reduce_kernel");
 }
 

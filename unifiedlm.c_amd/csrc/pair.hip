@@ -1,0 +1,549 @@
+// Block-pair products of the fast memory: the same sums as the chunked
+// products (la_kgroup.hip), evaluated over pairs of position blocks instead of
+// through a carried state. For one batch row, with lam = exp(g):
+//
+//   scores   P[t][s]  = lam^(t-s) (q_t . k_s)             s <= t, else 0
+//   apply    fast_t   = sum_s P[t][s] v_s                  (_la's output, kernel.py:75-101)
+//   dscores  dS[t][s] = lam^(t-s) (dfast_t . v_s)         s <= t, else 0
+//            dg      += sum_{s<=t} (t-s) P[t][s] (dfast_t . v_s)
+//   dq_f     dq_f_t   = sum_s dS[t][s] k_s                 dk_f_s = sum_t dS[t][s] q_t
+//   dv       dv_s     = sum_t P[t][s] dfast_t
+//
+// These are the four products of the role table (docs/kernel.md:22-27) with
+// the intra-chunk matrix of _la_attn_kernel (kernel.py:51-72) extended to every
+// earlier block. Per token and product the state form costs 4 K V flops
+// (update + read-out), this form about T (K + V) / 2: it is the cheaper one
+// for sequences up to a few thousand positions at the widths of the trained
+// models, and it needs no state in registers. The decay gradient is summed
+// directly over the (t, s) pairs with its lag weight, so it involves no
+// difference of large positional sums.
+//
+// Every product is a tile GEMM C[m][n] = sum_k A[m][k] B[n][k] per batch row
+// on bf16 operand tiles (ulm_common.h: 32 rows x 16 contraction elements,
+// 1 KB, one v_mfma_f32_32x32x16_bf16 operand per lane-ordered tile):
+//
+//   product  m  n  k   A                      B      contraction range
+//   scores   s  t  a   k (R layout)           q (R)  all slots; tiles with s-block <= t-block
+//   apply    t  d  s   P                      v (Q)  s < end of t's block
+//   dscores  s  t  d   v (R)                  dO (R) all features; s-block <= t-block
+//   dq_f     t  a  s   dS                     k (Q)  s < end of t's block
+//   dk_f     s  a  t   dS read transposed     q (Q)  t >= start of s's block
+//   dv       s  d  t   P read transposed      dO (Q) t >= start of s's block
+//
+// P and dS are stored per batch row as bf16 tiles with rows t and contraction
+// s (the "P layout", the R layout of a Tq x Tq matrix, Tq = T padded to the
+// block). The scores / dscores epilogue holds, in the MFMA accumulator, one t
+// per lane and four consecutive s per register group, so each lane writes 8
+// contiguous bytes of a P-layout tile. The transposed reads of the dk_f and dv
+// products use ds_read_b64_tr_b16 on the staged tiles.
+//
+// Workgroup: TM x TN output tile, 4 waves (2 x 2), one wave per SIMD holding a
+// (TM/2) x (TN/2) fp32 accumulator. Each 64-element k-step of A and B is
+// copied into LDS by buffer_load ... lds (no registers), two stages, so the
+// copy of step k+1 runs during the MFMAs of step k. All global loads are
+// range-checked buffer loads (rows or contraction past a matrix read as zero)
+// and all global stores of the P-layout outputs are range-checked buffer
+// stores.
+#include "ulm_common.h"
+
+namespace ulm {
+
+int la_timer_begin(hipStream_t s);
+int la_timer_end(hipStream_t s);
+
+namespace pair {
+
+constexpr uint32_t TB = 1024;           // bytes per operand tile
+constexpr uint32_t OOB = 0x80000000u;   // buffer offset past every range: loads return zeros
+constexpr int NSTAGE = 4;               // LDS stages of operand copies (NSTAGE - 1 k-steps in flight)
+constexpr int WAVES = 4;
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef uint32_t v2u32_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ rsrc_t rsrc(const void *base, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ uint32_t uniform(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// One operand matrix of one batch row in tile layout: element (row r,
+// contraction k) lies in tile (r / 32, k / 16) at byte
+//   (r / 32) rt + (k / 64) ks + ((k % 64) / 16) TB + 16 (r % 32 + 32 ((k % 16) / 8)) + 2 (k % 8).
+// Tiles at or past nrt row tiles or nkt contraction tiles read as zero.
+struct Mat {
+    const uint16_t *p;   // batch row 0
+    size_t bstride;      // bytes per batch row
+    uint32_t rt, ks;     // bytes between 32-row tiles and between 64-element k-steps
+    int nrt, nkt;
+};
+
+enum Epi { EPI_SCORES = 0, EPI_DSCORES = 1, EPI_ROWS = 2 };
+enum KRange { K_FULL = 0, K_CAUSAL = 1, K_ANTI = 2 };
+
+struct Args {
+    Mat a, b;
+    int T;
+    int mt, nt;              // output tiles per batch row along m and n
+    int tri;                 // only tiles with m-tile <= n-tile (TM == TN)
+    int krange, nks;         // contraction range kind, k-steps of the whole contraction
+    int jobs_per_row, jobs;
+    const float *g;
+    // EPI_SCORES / EPI_DSCORES: bf16 output in the P layout
+    uint16_t *pout;
+    size_t p_bstride;
+    uint32_t p_rt;
+    const uint16_t *pin;     // EPI_DSCORES: P, for the decay gradient
+    double *dg_part;         // EPI_DSCORES: one sum per job
+    // EPI_ROWS: (B, T, F) row-major output, rows = positions, columns = features
+    void *out;
+    int out_dt, F, nperm;    // nperm: B's rows are features in the order perm32 within 32-blocks
+    const float *resid;      // fp32 (B, T, F) added, or null
+};
+
+// tile job -> (m-tile, n-tile) of one batch row
+__device__ __forceinline__ void job_tiles(const Args &p, int j, int &mb, int &nb) {
+    if (p.tri) {
+        // n-tile nb holds m-tiles 0 .. nb, in rows of the lower triangle
+        int n = static_cast<int>((sqrtf(8.f * j + 1.f) - 1.f) * 0.5f);
+        while ((n + 1) * (n + 2) / 2 <= j) ++n;
+        while (n * (n + 1) / 2 > j) --n;
+        nb = n;
+        mb = j - n * (n + 1) / 2;
+    } else if (p.krange == K_CAUSAL) {   // work grows with the m-tile: the longest first
+        mb = p.mt - 1 - j / p.nt;
+        nb = j % p.nt;
+    } else {                             // K_ANTI: work shrinks with the m-tile
+        mb = j / p.nt;
+        nb = j % p.nt;
+    }
+}
+
+// s_waitcnt vmcnt(n) for n = 0 .. 3 k-steps of LPW copies each
+template <int LPW>
+__device__ __forceinline__ void wait_copies(int ksteps) {
+    switch (ksteps) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LPW) : "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * LPW) : "memory"); break;
+    }
+}
+
+// Output element types of the row epilogue: OUT % 3 = ulm_dtype of the
+// output, OUT >= 3 adds an fp32 residual.
+template <int TM, int TN, int KT, bool TA, int EPI, int OUT>
+__global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Args p) {
+    constexpr int MI = TM / 64, NI = TN / 64;          // 32-row / 32-column tiles per wave
+    constexpr int KS = 16 * KT;                        // contraction elements per k-step
+    constexpr int A_TILES = TM / 32 * KT, B_TILES = TN / 32 * KT;   // tiles per k-step
+    constexpr uint32_t STAGE = (A_TILES + B_TILES) * TB;
+    constexpr int AC = A_TILES / WAVES, BC = B_TILES / WAVES;       // copies per wave per k-step
+    constexpr int LPW = AC + BC;
+    static_assert(KT % 2 == 0 && NSTAGE >= 2 && NSTAGE - 2 <= 3, "k-step and stage count");
+    extern __shared__ __align__(16) char lds[];
+
+    const int wave = uniform(threadIdx.x / 64);
+    const int lane = threadIdx.x % 64;
+    const int wm = wave / 2, wn = wave % 2;
+
+    int logical = blockIdx.x;
+    if (p.jobs % 8 == 0) logical = (blockIdx.x % 8) * (p.jobs / 8) + blockIdx.x / 8;   // XCD-local rows
+    const int b = logical / p.jobs_per_row;
+    int mb, nb;
+    job_tiles(p, logical % p.jobs_per_row, mb, nb);
+    const int m0 = mb * TM, n0 = nb * TN;
+
+    int kb = 0, ke = p.nks;
+    if (p.krange == K_CAUSAL) ke = min(p.nks, (m0 + TM) / KS);
+    else if (p.krange == K_ANTI) kb = m0 / KS;
+
+    const rsrc_t ra = rsrc(reinterpret_cast<const char *>(p.a.p) + b * p.a.bstride, p.a.bstride);
+    const rsrc_t rb = rsrc(reinterpret_cast<const char *>(p.b.p) + b * p.b.bstride, p.b.bstride);
+    const uint32_t lane16 = 16u * lane;
+
+    // The tile copies of k-step kk into stage st. Wave w copies the tiles
+    // q = w + 4 c of each operand. Plain operand: tile q is row tile q / KT at
+    // contraction tile KT kk + q % KT. Transposed A (stored rows = this
+    // product's contraction): tile q is stored row tile (KS / 32) kk +
+    // q / (TM / 16) at stored contraction tile m0 / 16 + q % (TM / 16). An
+    // invalid tile gets an offset past the buffer range and reads as zero.
+    auto issue = [&](int kk, int st) {
+        char *base = lds + st * STAGE;
+#pragma unroll
+        for (int c = 0; c < AC; ++c) {
+            const int q = wave + WAVES * c;
+            int rt, kt;
+            if constexpr (!TA) {
+                rt = m0 / 32 + q / KT;
+                kt = KT * kk + q % KT;
+            } else {
+                rt = (KS / 32) * kk + q / (TM / 16);
+                kt = m0 / 16 + q % (TM / 16);
+            }
+            const bool ok = rt < p.a.nrt && kt < p.a.nkt;
+            const uint32_t off = rt * p.a.rt + (kt / 4) * p.a.ks + (kt % 4) * TB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(base + q * TB), 16, (off + lane16) | (ok ? 0u : OOB),
+                                                     0, 0, 0);
+        }
+#pragma unroll
+        for (int c = 0; c < BC; ++c) {
+            const int q = wave + WAVES * c;
+            const int rt = n0 / 32 + q / KT, kt = KT * kk + q % KT;
+            const bool ok = rt < p.b.nrt && kt < p.b.nkt;
+            const uint32_t off = rt * p.b.rt + (kt / 4) * p.b.ks + (kt % 4) * TB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void *)(base + (A_TILES + q) * TB), 16,
+                                                     (off + lane16) | (ok ? 0u : OOB), 0, 0, 0);
+        }
+    };
+
+    f32x16 acc[MI][NI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // transposed A operand: lane (g = lane / 16, q = lane % 16) reads stored row
+    // 16 (u % 2) + 8 (g / 2) + q / 4 (+ 4) of stored k-tile 2 ir + g % 2
+    const int tg = lane / 16, tq = lane % 16;
+    const uint32_t tr_lane = 16u * (8 * (tg / 2) + tq / 4 + 32 * ((tq >> 1) & 1)) + 8u * (tq & 1) + (tg % 2) * TB;
+    // the MFMA operands of substep u (16 contraction elements) of stage st
+    auto frags = [&](int st, int u, bf16x8 (&af)[MI], bf16x8 (&bf)[NI]) {
+        const char *sa = lds + st * STAGE;
+        const char *sb = sa + A_TILES * TB;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            const int ir = wm * MI + i;   // 32-row tile of the workgroup tile
+            if constexpr (!TA) {
+                af[i] = *reinterpret_cast<const bf16x8 *>(sa + (ir * KT + u) * TB + lane16);
+            } else {
+                const char *t0 = sa + ((u / 2) * (TM / 16) + 2 * ir) * TB + (u % 2) * 256 + tr_lane;
+                const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)t0);
+                const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)(t0 + 64));
+                af[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NI; ++j) bf[j] = *reinterpret_cast<const bf16x8 *>(sb + ((wn * NI + j) * KT + u) * TB + lane16);
+    };
+
+    // Pipeline: NSTAGE - 1 k-steps of copies in flight. Before the last
+    // substep of step kk each wave finishes its reads of that stage, waits for
+    // the copies of step kk + 1 and meets the others at the barrier (a bare
+    // s_barrier: a fence would also wait for the later steps' copies); then the
+    // copies of step kk + NSTAGE go into step kk's stage, and the operands of
+    // step kk + 1's first substep load while step kk's last MFMAs run.
+    bf16x8 af[2][MI], bf[2][NI];
+    if (kb < ke) {
+#pragma unroll
+        for (int d = 0; d < NSTAGE - 1; ++d)
+            if (kb + d < ke) issue(kb + d, d);
+        wait_copies<LPW>(min(NSTAGE - 2, ke - 1 - kb));
+        __builtin_amdgcn_s_barrier();
+        if (kb + NSTAGE - 1 < ke) issue(kb + NSTAGE - 1, NSTAGE - 1);
+        frags(0, 0, af[0], bf[0]);
+    }
+    for (int kk = kb; kk < ke; ++kk) {
+        const int st = (kk - kb) % NSTAGE;
+#pragma unroll
+        for (int u = 0; u < KT; ++u) {
+            if (u + 1 < KT) {
+                frags(st, u + 1, af[(u + 1) % 2], bf[(u + 1) % 2]);
+            } else if (kk + 1 < ke) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                wait_copies<LPW>(min(NSTAGE - 2, ke - 2 - kk));
+                __builtin_amdgcn_s_barrier();
+                if (kk + NSTAGE < ke) issue(kk + NSTAGE, st);
+                frags((st + 1) % NSTAGE, 0, af[0], bf[0]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j) acc[i][j] = mfma(af[u % 2][i], bf[u % 2][j], acc[i][j]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // ---- epilogue. Accumulator (lane l, register r) -> row 8 (r / 4) + 4 (l / 32) + r % 4,
+    // column l % 32 of its 32 x 32 tile.
+    const int h = lane / 32, lc = lane % 32;
+    if constexpr (EPI == EPI_SCORES || EPI == EPI_DSCORES) {
+        const float g = p.g[0];
+        const rsrc_t rp = rsrc(reinterpret_cast<char *>(p.pout) + b * p.p_bstride, p.p_bstride);
+        const rsrc_t rpin = rsrc(EPI == EPI_DSCORES ? reinterpret_cast<const char *>(p.pin) + b * p.p_bstride
+                                                    : reinterpret_cast<const char *>(p.pout), p.p_bstride);
+        float dg = 0.f;
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const int t = n0 + wn * (TN / 2) + 32 * j + lc;
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int s0 = m0 + wm * (TM / 2) + 32 * i + 8 * r4 + 4 * h;
+                    const uint32_t off = (t / 32) * p.p_rt + (s0 / 16) * TB + 16u * (t % 32 + 32 * ((s0 % 16) / 8)) +
+                                         2u * (s0 % 8);
+                    float x[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int s = s0 + e;
+                        const bool ok = s <= t && t < p.T;
+                        x[e] = ok ? acc[i][j][4 * r4 + e] * __expf(g * static_cast<float>(t - s)) : 0.f;
+                    }
+                    if constexpr (EPI == EPI_DSCORES) {
+                        const v2u32_t pv = __builtin_amdgcn_raw_buffer_load_b64(rpin, off, 0, 0);
+                        const float pe[4] = {bf16_to_f32(pv[0] & 0xffffu), bf16_to_f32(pv[0] >> 16),
+                                             bf16_to_f32(pv[1] & 0xffffu), bf16_to_f32(pv[1] >> 16)};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int s = s0 + e;
+                            if (s <= t && t < p.T) dg += static_cast<float>(t - s) * pe[e] * acc[i][j][4 * r4 + e];
+                        }
+                    }
+                    v2u32_t v;
+                    v[0] = static_cast<uint32_t>(f32_to_bf16_bits(x[0])) | (static_cast<uint32_t>(f32_to_bf16_bits(x[1])) << 16);
+                    v[1] = static_cast<uint32_t>(f32_to_bf16_bits(x[2])) | (static_cast<uint32_t>(f32_to_bf16_bits(x[3])) << 16);
+                    __builtin_amdgcn_raw_buffer_store_b64(v, rp, off, 0, 0);
+                }
+        }
+        if constexpr (EPI == EPI_DSCORES) {
+            __shared__ double red[WAVES];
+            const double w = wave_sum(static_cast<double>(dg));
+            if (lane == 0) red[wave] = w;
+            __syncthreads();
+            if (threadIdx.x == 0) p.dg_part[logical] = (red[0] + red[1]) + (red[2] + red[3]);
+        }
+    } else {
+        // rows = positions, columns = features of a (B, T, F) tensor, written
+        // through a range-checked buffer of this batch row; invalid elements
+        // get an offset past the range
+        constexpr int DT = OUT % 3;
+        constexpr uint32_t ES = DT == ULM_F32 ? 4 : 2;
+        const size_t row0 = static_cast<size_t>(b) * p.T * p.F;
+        const uint32_t nbytes = static_cast<uint32_t>(p.T) * p.F * ES;
+        const rsrc_t ro = rsrc(static_cast<char *>(p.out) + row0 * ES, nbytes);
+        const rsrc_t rr = rsrc(OUT >= 3 ? reinterpret_cast<const char *>(p.resid + row0) : static_cast<const char *>(p.out),
+                               static_cast<uint32_t>(p.T) * p.F * 4);
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const int n = n0 + wn * (TN / 2) + 32 * j + lc;
+            const int f = p.nperm ? (n & ~31) + perm32(n & 31) : n;
+            const bool fok = f < p.F;
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int pos = m0 + wm * (TM / 2) + 32 * i + 8 * (r / 4) + 4 * h + r % 4;
+                    const uint32_t el = static_cast<uint32_t>(pos) * p.F + f;
+                    const uint32_t bad = (fok && pos < p.T) ? 0u : OOB;
+                    float v = acc[i][j][r];
+                    if constexpr (OUT >= 3) v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, (4u * el) | bad, 0, 0));
+                    if constexpr (DT == ULM_F32) {
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ro, (4u * el) | bad, 0, 0);
+                    } else {
+                        const uint16_t hv = DT == ULM_BF16 ? f32_to_bf16_bits(v)
+                                                           : __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+                        __builtin_amdgcn_raw_buffer_store_b16(hv, ro, (2u * el) | bad, 0, 0);
+                    }
+                }
+        }
+    }
+}
+
+}  // namespace pair
+}  // namespace ulm
+
+namespace ulm {
+namespace pair {
+
+// the tile matrices of the operands (layouts of ulm_common.h)
+Mat r_mat(const uint16_t *p, int NT, int F) {   // R layout: rows = positions, contraction = features
+    Mat m{p, static_cast<size_t>(2 * NT) * (F / 16) * TB, static_cast<uint32_t>(F / 16) * TB, 4 * TB, 2 * NT, F / 16};
+    return m;
+}
+Mat q_mat(const uint16_t *p, int NT, int F) {   // Q layout: rows = features (perm32), contraction = positions
+    Mat m{p, static_cast<size_t>(NT) * (F / 32) * 4 * TB, 4 * TB, static_cast<uint32_t>(F / 32) * 4 * TB, F / 32, 4 * NT};
+    return m;
+}
+Mat p_mat(const uint16_t *p, int Tq) {          // P layout: rows = t, contraction = s
+    Mat m{p, static_cast<size_t>(Tq / 32) * (Tq / 16) * TB, static_cast<uint32_t>(Tq / 16) * TB, 4 * TB, Tq / 32, Tq / 16};
+    return m;
+}
+
+constexpr int KT = 2;   // contraction tiles per k-step (32 elements): four 32 KB stages at 256 x 256
+
+template <int G, bool TA, int EPI, int OUT>
+int launch_g(Args a, int B, hipStream_t s) {
+    const void *fn = reinterpret_cast<const void *>(&pair_kernel<G, G, KT, TA, EPI, OUT>);
+    constexpr int lds = NSTAGE * (G / 32 * KT) * 2 * TB;
+    static bool attr_done[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return check_launch("hipGetDevice");
+    if (!attr_done[dev]) {
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+            return check_launch("pair_kernel attribute");
+        attr_done[dev] = true;
+    }
+    a.mt = a.mt ? a.mt : 1;
+    a.jobs_per_row = a.tri ? a.mt * (a.mt + 1) / 2 : a.mt * a.nt;
+    a.jobs = B * a.jobs_per_row;
+    int st = la_timer_begin(s);
+    if (st) return st;
+    pair_kernel<G, G, KT, TA, EPI, OUT><<<dim3(static_cast<unsigned>(a.jobs)), WAVES * 64, lds, s>>>(a);
+    st = check_launch("pair_kernel");
+    if (st) return st;
+    return la_timer_end(s);
+}
+
+template <bool TA, int EPI, int OUT>
+int launch_o(const Args &a, int G, int B, hipStream_t s) {
+    return G == 256 ? launch_g<256, TA, EPI, OUT>(a, B, s) : launch_g<128, TA, EPI, OUT>(a, B, s);
+}
+
+template <bool TA, int EPI>
+int launch(const Args &a, int G, int B, hipStream_t s) {
+    if constexpr (EPI != EPI_ROWS) {
+        return launch_o<TA, EPI, 0>(a, G, B, s);
+    } else {
+        const int out = a.out_dt + (a.resid ? 3 : 0);
+        switch (out) {
+        case 0: return launch_o<TA, EPI, 0>(a, G, B, s);
+        case 1: return launch_o<TA, EPI, 1>(a, G, B, s);
+        case 2: return launch_o<TA, EPI, 2>(a, G, B, s);
+        case 3: return launch_o<TA, EPI, 3>(a, G, B, s);
+        case 4: return launch_o<TA, EPI, 4>(a, G, B, s);
+        default: return launch_o<TA, EPI, 5>(a, G, B, s);
+        }
+    }
+}
+
+}  // namespace pair
+
+// ---- the operator's products in block-pair form (A, D multiples of 32)
+
+// Block (output tile) size of the block-pair products at T positions and B
+// batch rows: 256 when the scores product then has at least 128 tiles, else 128.
+int pair_block(int B, int T) {
+    const long long nb = (T + 255) / 256;
+    return static_cast<long long>(B) * nb * (nb + 1) / 2 >= 128 ? 256 : 128;
+}
+int pair_tq(int B, int T) {
+    const int G = pair_block(B, T);
+    return (T + G - 1) / G * G;
+}
+size_t pair_p_bytes(int B, int T) {
+    const size_t Tq = pair_tq(B, T);
+    return static_cast<size_t>(B) * Tq * Tq * 2;
+}
+int pair_dscore_jobs(int B, int T) {
+    const int nb = pair_tq(B, T) / pair_block(B, T);
+    return B * nb * (nb + 1) / 2;
+}
+
+// Flops per token of the six block-pair products, fwd + bwd, with their
+// tile-granular causal ranges.
+double pair_flops_per_token(int B, int T, int A, int D) {
+    const double G = pair_block(B, T), nb = pair_tq(B, T) / G;
+    return nb * (nb + 1) * G * G * 3.0 * (A + D) / T;
+}
+
+// P = scores(q, k) in the P layout (Tq x Tq per batch row), then
+// out = P v (+ resid) in out_dt (B, T, D). kR, qR: R layout (A); vQ: Q layout (D).
+int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *vQ, const float *g, uint16_t *P,
+                        void *out, int out_dt, const float *resid, int B, int T, int A, int D, hipStream_t s) {
+    using namespace pair;
+    const int G = pair_block(B, T), Tq = pair_tq(B, T), NT = (T + 63) / 64;
+    Args a{};
+    a.T = T;
+    a.g = g;
+    a.a = r_mat(kR, NT, A);
+    a.b = r_mat(qR, NT, A);
+    a.mt = a.nt = Tq / G;
+    a.tri = 1;
+    a.krange = K_FULL;
+    a.nks = (A + 16 * KT - 1) / (16 * KT);
+    const Mat pm = p_mat(P, Tq);
+    a.pout = P;
+    a.p_bstride = pm.bstride;
+    a.p_rt = pm.rt;
+    ULM_TRY((launch<false, EPI_SCORES>(a, G, B, s)));
+    Args f{};
+    f.T = T;
+    f.g = g;
+    f.a = pm;
+    f.b = q_mat(vQ, NT, D);
+    f.mt = Tq / G;
+    f.nt = (D + G - 1) / G;
+    f.krange = K_CAUSAL;
+    f.nks = Tq / (16 * KT);
+    f.out = out;
+    f.out_dt = out_dt;
+    f.F = D;
+    f.nperm = 1;
+    f.resid = resid;
+    return launch<false, EPI_ROWS>(f, G, B, s);
+}
+
+// The backward products: dS = dscores(dfast, v) with the pair part of the
+// decay gradient into dg_part (pair_dscore_jobs doubles), dq_f = dS k,
+// dk_f = dS^T q (fp32 (B, T, A)), dv = P^T dfast in dv_dt (B, T, D).
+// vR, doR: R layout (D); kQ, qQ: Q layout (A); doQ: Q layout (D).
+int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t *doQ, const uint16_t *kQ,
+                         const uint16_t *qQ, const uint16_t *P, const float *g, uint16_t *dS, double *dg_part,
+                         float *dqf, float *dkf, void *dv, int dv_dt, int B, int T, int A, int D, hipStream_t s) {
+    using namespace pair;
+    const int G = pair_block(B, T), Tq = pair_tq(B, T), NT = (T + 63) / 64;
+    const Mat pm = p_mat(P, Tq), sm = p_mat(dS, Tq);
+    Args a{};
+    a.T = T;
+    a.g = g;
+    a.a = r_mat(vR, NT, D);
+    a.b = r_mat(doR, NT, D);
+    a.mt = a.nt = Tq / G;
+    a.tri = 1;
+    a.krange = K_FULL;
+    a.nks = (D + 16 * KT - 1) / (16 * KT);
+    a.pout = dS;
+    a.p_bstride = sm.bstride;
+    a.p_rt = sm.rt;
+    a.pin = P;
+    a.dg_part = dg_part;
+    ULM_TRY((launch<false, EPI_DSCORES>(a, G, B, s)));
+    Args r{};
+    r.T = T;
+    r.g = g;
+    r.mt = Tq / G;
+    r.nks = Tq / (16 * KT);
+    r.nperm = 1;
+    // dq_f = dS k
+    r.a = sm;
+    r.b = q_mat(kQ, NT, A);
+    r.nt = (A + G - 1) / G;
+    r.krange = K_CAUSAL;
+    r.out = dqf;
+    r.out_dt = ULM_F32;
+    r.F = A;
+    ULM_TRY((launch<false, EPI_ROWS>(r, G, B, s)));
+    // dk_f = dS^T q
+    r.b = q_mat(qQ, NT, A);
+    r.krange = K_ANTI;
+    r.out = dkf;
+    ULM_TRY((launch<true, EPI_ROWS>(r, G, B, s)));
+    // dv = P^T dfast
+    r.a = pm;
+    r.b = q_mat(doQ, NT, D);
+    r.nt = (D + G - 1) / G;
+    r.out = dv;
+    r.out_dt = dv_dt;
+    r.F = D;
+    return launch<true, EPI_ROWS>(r, G, B, s);
+}
+
+}  // namespace ulm

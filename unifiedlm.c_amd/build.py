@@ -58,7 +58,9 @@ def build(verbose=False):
         if err and verbose:
             print(err, file=sys.stderr)
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + [o for o, _ in results]
+    # -z defs: an undefined symbol (a kernel whose host stub was not emitted, say)
+    # fails the link instead of the first call
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp] + [o for o, _ in results]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")

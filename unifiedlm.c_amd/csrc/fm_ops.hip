@@ -60,10 +60,12 @@ size_t pair_p_bytes(int B, int T);
 int pair_dscore_jobs(int B, int T);
 double pair_flops_per_token(int B, int T, int A, int D);
 int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *vQ, const float *g, uint16_t *P,
-                        void *out, int out_dt, const float *resid, int B, int T, int A, int D, hipStream_t s);
+                        uint16_t *Pt, void *out, int out_dt, const float *resid, int B, int T, int A, int D,
+                        hipStream_t s);
 int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t *doQ, const uint16_t *kQ,
-                         const uint16_t *qQ, const uint16_t *P, const float *g, uint16_t *dS, double *dg_part,
-                         float *dqf, float *dkf, void *dv, int dv_dt, int B, int T, int A, int D, hipStream_t s);
+                         const uint16_t *qQ, const uint16_t *P, const uint16_t *Pt, const float *g, uint16_t *dS,
+                         uint16_t *dSt, double *dg_part, float *dqf, float *dkf, void *dv, int dv_dt, int B, int T,
+                         int A, int D, hipStream_t s);
 
 namespace {
 
@@ -96,7 +98,7 @@ Path train_path(int B, int T, int A, int D) {
 struct Saved {
     uint16_t *q16n, *k16n, *v16n;                                     // generic path
     uint16_t *qR, *kR, *qQ, *kQ, *vR, *vRl, *vQ, *vQl, *Pdv;   // K-group path (pair: qQ, kQ, vR)
-    uint16_t *P;                                                      // pair path: the scores
+    uint16_t *P, *Pt;                                                 // pair path: the scores and their transpose
     float *nck;
     size_t bytes;
 };
@@ -111,6 +113,7 @@ Saved saved_layout(void *base, int B, int T, int A, int D, int v_dtype, Path pat
         s.kQ = c.take<uint16_t>(ta);
         s.vR = c.take<uint16_t>(td);
         s.P = c.take<uint16_t>(pair_p_bytes(B, T) / 2);
+        s.Pt = c.take<uint16_t>(pair_p_bytes(B, T) / 2);
     } else if (path == PATH_CHUNKED) {
         s.qR = c.take<uint16_t>(ta);
         s.kR = c.take<uint16_t>(ta);
@@ -144,6 +147,7 @@ FwdWs fwd_layout(void *base, int B, int T, int A, int D, int fast_dtype, Path pa
     Carver c(base);
     FwdWs w{};
     if (path == PATH_PAIR) {
+        // the block-pair products write the output directly
         w.qR = c.take<uint16_t>(B * NT * 64 * A);
         w.kR = c.take<uint16_t>(B * NT * 64 * A);
         w.vQ = c.take<uint16_t>(B * NT * 64 * D);
@@ -161,7 +165,7 @@ FwdWs fwd_layout(void *base, int B, int T, int A, int D, int fast_dtype, Path pa
 struct BwdWs {
     uint16_t *do16;                                          // generic path
     uint16_t *doR, *doRl, *doQ, *doQl, *Pdq, *Pdk;   // K-group path (pair: doR, doQ)
-    uint16_t *dS;                                            // pair path: the score gradients
+    uint16_t *dS, *dSt;                                      // pair path: the score gradients, transposed
     double *dgx;                                             // pair path: dg partials of the pair products
     float *dqf, *dkf, *part;
     void *stats;
@@ -179,6 +183,7 @@ BwdWs bwd_layout(void *base, int B, int T, int A, int D, int dfast_dtype, Path p
         w.doR = c.take<uint16_t>(td);
         w.doQ = c.take<uint16_t>(td);
         w.dS = c.take<uint16_t>(pair_p_bytes(B, T) / 2);
+        w.dSt = c.take<uint16_t>(pair_p_bytes(B, T) / 2);
         w.dgx = c.take<double>(pair_dscore_jobs(B, T));
     } else if (path == PATH_CHUNKED) {
         w.doR = c.take<uint16_t>(td);
@@ -285,11 +290,13 @@ int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const 
     const size_t nf = static_cast<size_t>(B) * T * D;
     if (path == PATH_PAIR) {
         if (state || c_last) return fail(ULM_ERR_INVALID, "prefill state: not on the block-pair path");
+        // q, k: R layout for the scores (this pass only), Q layout for the
+        // backward's dk_f, dq_f; v: Q layout for the apply, R layout for the
+        // backward's dscores
         ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, ws.qR, ws.kR, sv.qQ, sv.kQ, sv.nck, nullptr, B, T, A, s,
                                  qw, qw_dt));
-        // v: Q layout for the apply product, R layout (saved) for the backward's dscores
         ULM_TRY(launch_chunk_transpose(v, v_dtype, ws.vQ, nullptr, sv.vR, nullptr, B, T, D, s));
-        return launch_pair_forward(ws.qR, ws.kR, ws.vQ, g, sv.P, fast, fast_dtype, resid, B, T, A, D, s);
+        return launch_pair_forward(ws.qR, ws.kR, ws.vQ, g, sv.P, sv.Pt, fast, fast_dtype, resid, B, T, A, D, s);
     }
     if (path == PATH_CHUNKED) {
         const int nkg = la_kgroup_groups(A);
@@ -386,8 +393,8 @@ int fm_backward(const RSrc &r, const float *g, const float *w, const void *saved
     const size_t nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
     if (path == PATH_PAIR) {
         ULM_TRY(launch_chunk_transpose(dfast, dfast_dtype, ws.doQ, nullptr, ws.doR, nullptr, B, T, D, s));
-        ULM_TRY(launch_pair_backward(sv.vR, ws.doR, ws.doQ, sv.kQ, sv.qQ, sv.P, g, ws.dS, ws.dgx, ws.dqf, ws.dkf, dv,
-                                     dv_dtype, B, T, A, D, s));
+        ULM_TRY(launch_pair_backward(sv.vR, ws.doR, ws.doQ, sv.kQ, sv.qQ, sv.P, sv.Pt, g, ws.dS, ws.dSt, ws.dgx, ws.dqf,
+                                     ws.dkf, dv, dv_dtype, B, T, A, D, s));
         return launch_bwd_stats(ws.dqf, dq_out, r, sv.nck, w, g, ws.dkf, dr, dw, dg, ws.stats, B, T, A, s, dqw, dqw_dt,
                                 ws.dgx, pair_dscore_jobs(B, T));
     }

@@ -431,10 +431,11 @@ int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, 
                      int A, hipStream_t s, void *qw, int qw_dt) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
     if ((q16n == nullptr) != (k16n == nullptr)) return fail(ULM_ERR_INVALID, "fwd stats: q16n and k16n go together");
-    // the tiled copies: qR, kR and kQ together (qQ, read only by a backward, may be left out)
+    // the tiled copies: kQ always, qR and kR together (the chunked products'
+    // R layout), qQ when a backward follows
     const bool tiled = qR || kR || qQ || kQ;
-    if (tiled && !(qR && kR && kQ && A % 32 == 0))
-        return fail(ULM_ERR_INVALID, "fwd stats: tiled copies need qR, kR, kQ and A %% 32 == 0");
+    if (tiled && !(kQ && (qR != nullptr) == (kR != nullptr) && A % 32 == 0))
+        return fail(ULM_ERR_INVALID, "fwd stats: tiled copies need kQ, qR with kR, and A %% 32 == 0");
     if (qw && !valid_dtype(qw_dt)) return fail(ULM_ERR_INVALID, "fwd stats: bad w q dtype %d", qw_dt);
     const int qwk = qw ? qw_dt : -1;
     return with_rsrc(src, [&](auto rs) {

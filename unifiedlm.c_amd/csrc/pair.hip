@@ -46,6 +46,8 @@
 // stores.
 #include "ulm_common.h"
 
+#include <type_traits>
+
 namespace ulm {
 
 int la_timer_begin(hipStream_t s);
@@ -55,7 +57,9 @@ namespace pair {
 
 constexpr uint32_t TB = 1024;           // bytes per operand tile
 constexpr uint32_t OOB = 0x80000000u;   // buffer offset past every range: loads return zeros
-constexpr int NSTAGE = 4;               // LDS stages of operand copies (NSTAGE - 1 k-steps in flight)
+// LDS stages of operand copies (NSTAGE - 1 k-steps in flight): all 160 KB of LDS
+// at 256 x 256 tiles (32 KB per stage), 64 KB at 128 x 128 (two workgroups per CU)
+template <int TM> constexpr int nstage() { return TM == 256 ? 5 : 4; }
 constexpr int WAVES = 4;
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
@@ -94,7 +98,8 @@ struct Args {
     int jobs_per_row, jobs;
     const float *g;
     // EPI_SCORES / EPI_DSCORES: bf16 output in the P layout
-    uint16_t *pout;
+    uint16_t *pout;          // rows t, contraction s (the P layout)
+    uint16_t *pout_t;        // the transpose: rows s, contraction t
     size_t p_bstride;
     uint32_t p_rt;
     const uint16_t *pin;     // EPI_DSCORES: P, for the decay gradient
@@ -123,20 +128,27 @@ __device__ __forceinline__ void job_tiles(const Args &p, int j, int &mb, int &nb
     }
 }
 
-// s_waitcnt vmcnt(n) for n = 0 .. 3 k-steps of LPW copies each
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8). Issued through the builtin, not inline asm, so that the
+// compiler's own wait insertion knows which counters are already drained.
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kWaitLgkm0 = 0xC07F;   // lgkmcnt(0), nothing else
+
+// s_waitcnt vmcnt(n) for n = 0 .. 4 k-steps of LPW copies each
 template <int LPW>
 __device__ __forceinline__ void wait_copies(int ksteps) {
     switch (ksteps) {
-    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory"); break;
-    case 2: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LPW) : "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * LPW) : "memory"); break;
+    case 0: __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); break;
+    case 1: __builtin_amdgcn_s_waitcnt(waitcnt_vm(LPW)); break;
+    case 2: __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * LPW)); break;
+    case 3: __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * LPW)); break;
+    default: __builtin_amdgcn_s_waitcnt(waitcnt_vm(4 * LPW)); break;
     }
 }
 
 // Output element types of the row epilogue: OUT % 3 = ulm_dtype of the
 // output, OUT >= 3 adds an fp32 residual.
-template <int TM, int TN, int KT, bool TA, int EPI, int OUT>
+template <int TM, int TN, int KT, bool TA, bool TBt, int EPI, int OUT>
 __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Args p) {
     constexpr int MI = TM / 64, NI = TN / 64;          // 32-row / 32-column tiles per wave
     constexpr int KS = 16 * KT;                        // contraction elements per k-step
@@ -144,7 +156,8 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
     constexpr uint32_t STAGE = (A_TILES + B_TILES) * TB;
     constexpr int AC = A_TILES / WAVES, BC = B_TILES / WAVES;       // copies per wave per k-step
     constexpr int LPW = AC + BC;
-    static_assert(KT % 2 == 0 && NSTAGE >= 2 && NSTAGE - 2 <= 3, "k-step and stage count");
+    constexpr int NSTAGE = nstage<TM>();
+    static_assert(KT % 2 == 0 && NSTAGE >= 2 && NSTAGE - 2 <= 4, "k-step and stage count");
     extern __shared__ __align__(16) char lds[];
 
     const int wave = uniform(threadIdx.x / 64);
@@ -165,39 +178,60 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
     const rsrc_t ra = rsrc(reinterpret_cast<const char *>(p.a.p) + b * p.a.bstride, p.a.bstride);
     const rsrc_t rb = rsrc(reinterpret_cast<const char *>(p.b.p) + b * p.b.bstride, p.b.bstride);
     const uint32_t lane16 = 16u * lane;
+    // A tile read transposed is stored in LDS with its 16-byte chunks permuted,
+    // so that the transposed reads below fall on distinct banks while every 8
+    // consecutive lanes of a copy still read one 128-byte line: LDS chunk P
+    // (= the copying lane) holds tile chunk c with c's bits (x j4 j3 j2 j1 j0)
+    // = (P5, P4, P3 ^ t, P2 ^ P5, P1, P0), t the parity of the tile's LDS slot
+    // (the same for every tile a wave copies: slots w + 4 c).
+    const int tpar = wave & 1;
+    const uint32_t lane_tr = 16u * (32 * ((lane >> 5) & 1) + 16 * ((lane >> 4) & 1) + 8 * (((lane >> 3) & 1) ^ tpar) +
+                                    4 * (((lane >> 2) & 1) ^ ((lane >> 5) & 1)) + (lane & 3));
 
     // The tile copies of k-step kk into stage st. Wave w copies the tiles
     // q = w + 4 c of each operand. Plain operand: tile q is row tile q / KT at
-    // contraction tile KT kk + q % KT. Transposed A (stored rows = this
+    // contraction tile KT kk + q % KT. Transposed operand (stored rows = this
     // product's contraction): tile q is stored row tile (KS / 32) kk +
-    // q / (TM / 16) at stored contraction tile m0 / 16 + q % (TM / 16). An
-    // invalid tile gets an offset past the buffer range and reads as zero.
+    // q / (TM / 16) at stored contraction tile m0 / 16 + q % (TM / 16) (TN and
+    // n0 for B). An invalid tile gets an offset past the buffer range and reads
+    // as zero. The per-copy part of each offset (and its validity) is formed
+    // once; a k-step adds a part common to all copies of an operand.
+    static_assert(KT == 2, "the offset split below assumes 32-element k-steps");
+    // k-step part: plain operands advance 2 contraction tiles (the 64-element
+    // k-steps of the layouts hold 4), transposed ones one stored row tile
+    auto kstep_off = [&](const Mat &m, bool trans, int kk) -> uint32_t {
+        return trans ? kk * m.rt : (kk >> 1) * m.ks + (kk & 1) * 2 * TB;
+    };
+    // per-copy part of copy c's offset (OOB bit set when never valid) and the
+    // k-steps kk < lim for which it is valid; independent of kk, so hoisted
+    auto copy_off = [&](const Mat &m, bool trans, int tile0, int TX, uint32_t lane_off, int c, int &lim) -> uint32_t {
+        const int q = wave + WAVES * c;
+        if (!trans) {
+            const int rt = tile0 / 32 + q / KT;
+            lim = m.nkt / KT;                            // nkt is even: kt = 2 kk + q % 2 < nkt
+            return (rt * m.rt + (q % KT) * TB + lane_off) | (rt < m.nrt ? 0u : OOB);
+        }
+        const int skt = tile0 / 16 + q % (TX / 16);
+        lim = m.nrt - q / (TX / 16);                     // stored row tile kk + q / (TX / 16) < nrt
+        return (q / (TX / 16) * m.rt + (skt / 4) * m.ks + (skt % 4) * TB + lane_off) | (skt < m.nkt ? 0u : OOB);
+    };
     auto issue = [&](int kk, int st) {
         char *base = lds + st * STAGE;
+        const uint32_t ka = kstep_off(p.a, TA, kk), kb2 = kstep_off(p.b, TBt, kk);
+        const uint32_t past = kk < ke ? 0u : OOB;   // past this tile's contraction range: zeros, no traffic
 #pragma unroll
         for (int c = 0; c < AC; ++c) {
-            const int q = wave + WAVES * c;
-            int rt, kt;
-            if constexpr (!TA) {
-                rt = m0 / 32 + q / KT;
-                kt = KT * kk + q % KT;
-            } else {
-                rt = (KS / 32) * kk + q / (TM / 16);
-                kt = m0 / 16 + q % (TM / 16);
-            }
-            const bool ok = rt < p.a.nrt && kt < p.a.nkt;
-            const uint32_t off = rt * p.a.rt + (kt / 4) * p.a.ks + (kt % 4) * TB;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(base + q * TB), 16, (off + lane16) | (ok ? 0u : OOB),
-                                                     0, 0, 0);
+            int lim;
+            const uint32_t off = copy_off(p.a, TA, m0, TM, TA ? lane_tr : lane16, c, lim);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(base + (wave + WAVES * c) * TB), 16,
+                                                     (off + ka) | (kk < lim ? past : OOB), 0, 0, 0);
         }
 #pragma unroll
         for (int c = 0; c < BC; ++c) {
-            const int q = wave + WAVES * c;
-            const int rt = n0 / 32 + q / KT, kt = KT * kk + q % KT;
-            const bool ok = rt < p.b.nrt && kt < p.b.nkt;
-            const uint32_t off = rt * p.b.rt + (kt / 4) * p.b.ks + (kt % 4) * TB;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void *)(base + (A_TILES + q) * TB), 16,
-                                                     (off + lane16) | (ok ? 0u : OOB), 0, 0, 0);
+            int lim;
+            const uint32_t off = copy_off(p.b, TBt, n0, TN, TBt ? lane_tr : lane16, c, lim);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void *)(base + (A_TILES + wave + WAVES * c) * TB), 16,
+                                                     (off + kb2) | (kk < lim ? past : OOB), 0, 0, 0);
         }
     };
 
@@ -209,67 +243,86 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    // transposed A operand: lane (g = lane / 16, q = lane % 16) reads stored row
-    // 16 (u % 2) + 8 (g / 2) + q / 4 (+ 4) of stored k-tile 2 ir + g % 2
-    const int tg = lane / 16, tq = lane % 16;
-    const uint32_t tr_lane = 16u * (8 * (tg / 2) + tq / 4 + 32 * ((tq >> 1) & 1)) + 8u * (tq & 1) + (tg % 2) * TB;
+    // transposed operand: lane (g = lane / 16, q = lane % 16) reads stored row
+    // 16 (u % 2) + 8 (g / 2) + q / 4 (+ 4) of stored k-tile 2 ir + g % 2 (A) or
+    // 2 jn + g % 2 (B): 8 bytes of tile chunk (that row) + 32 x, x = (q >> 1) & 1,
+    // at the chunk's permuted LDS place (the caller adds the 16 (u % 2) rows)
+    const int tg = lane / 16, tq = lane % 16, tx = (tq >> 1) & 1;
+    const uint32_t tr_base = 16u * (32 * tx + 8 * ((tg / 2) ^ (tg % 2)) + tq / 4) + 8u * (tq & 1) + (tg % 2) * TB;
+    const uint32_t tr_lo = tr_base + 64u * tx, tr_hi = tr_base + 64u * (1 - tx);
     // the MFMA operands of substep u (16 contraction elements) of stage st
+    auto tr_read = [&](const char *t0) {
+        const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)(t0 + tr_lo));
+        const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)(t0 + tr_hi));
+        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
     auto frags = [&](int st, int u, bf16x8 (&af)[MI], bf16x8 (&bf)[NI]) {
         const char *sa = lds + st * STAGE;
         const char *sb = sa + A_TILES * TB;
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
             const int ir = wm * MI + i;   // 32-row tile of the workgroup tile
-            if constexpr (!TA) {
-                af[i] = *reinterpret_cast<const bf16x8 *>(sa + (ir * KT + u) * TB + lane16);
-            } else {
-                const char *t0 = sa + ((u / 2) * (TM / 16) + 2 * ir) * TB + (u % 2) * 256 + tr_lane;
-                const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)t0);
-                const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)(t0 + 64));
-                af[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-            }
+            if constexpr (!TA) af[i] = *reinterpret_cast<const bf16x8 *>(sa + (ir * KT + u) * TB + lane16);
+            else af[i] = tr_read(sa + ((u / 2) * (TM / 16) + 2 * ir) * TB + (u % 2) * 256);
         }
 #pragma unroll
-        for (int j = 0; j < NI; ++j) bf[j] = *reinterpret_cast<const bf16x8 *>(sb + ((wn * NI + j) * KT + u) * TB + lane16);
+        for (int j = 0; j < NI; ++j) {
+            const int jn = wn * NI + j;   // 32-column tile of the workgroup tile
+            if constexpr (!TBt) bf[j] = *reinterpret_cast<const bf16x8 *>(sb + (jn * KT + u) * TB + lane16);
+            else bf[j] = tr_read(sb + ((u / 2) * (TN / 16) + 2 * jn) * TB + (u % 2) * 256);
+        }
     };
 
     // Pipeline: NSTAGE - 1 k-steps of copies in flight. Before the last
     // substep of step kk each wave finishes its reads of that stage, waits for
     // the copies of step kk + 1 and meets the others at the barrier (a bare
-    // s_barrier: a fence would also wait for the later steps' copies); then the
-    // copies of step kk + NSTAGE go into step kk's stage, and the operands of
-    // step kk + 1's first substep load while step kk's last MFMAs run.
+    // s_barrier: a fence would also wait for the later steps' copies). Past the
+    // barrier the first half of the last substep's MFMAs is queued before the
+    // copies of step kk + NSTAGE go into step kk's stage, so the MFMA pipe
+    // does not drain while they issue. Copies are issued on every step (past
+    // the contraction they read zeros into a stage no one reads again), so
+    // that the number of copies in flight, and the wait, never change.
+    // Operands alternate between two register sets. The next substep's
+    // operands are read between the two halves of this substep's MFMAs: the set
+    // they overwrite was last read by MFMAs issued at least half a substep
+    // earlier (overwriting the set of MFMAs still queued waits for them to
+    // read it), and the reads have the second half to land.
     bf16x8 af[2][MI], bf[2][NI];
-    if (kb < ke) {
 #pragma unroll
-        for (int d = 0; d < NSTAGE - 1; ++d)
-            if (kb + d < ke) issue(kb + d, d);
-        wait_copies<LPW>(min(NSTAGE - 2, ke - 1 - kb));
-        __builtin_amdgcn_s_barrier();
-        if (kb + NSTAGE - 1 < ke) issue(kb + NSTAGE - 1, NSTAGE - 1);
-        frags(0, 0, af[0], bf[0]);
-    }
+    for (int d = 0; d < NSTAGE - 1; ++d) issue(kb + d, d);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm((NSTAGE - 2) * LPW));
+    __builtin_amdgcn_s_barrier();
+    issue(kb + NSTAGE - 1, NSTAGE - 1);
+    frags(0, 0, af[0], bf[0]);
+    // half h of a substep's MFMAs: A tiles [h MI / 2, (h + 1) MI / 2)
+    auto mfmas = [&](const bf16x8 (&a)[MI], const bf16x8 (&bb)[NI], int h) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = h * (MI / 2); i < (h + 1) * (MI / 2); ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j) acc[i][j] = mfma(a[i], bb[j], acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);
+    };
     for (int kk = kb; kk < ke; ++kk) {
         const int st = (kk - kb) % NSTAGE;
 #pragma unroll
-        for (int u = 0; u < KT; ++u) {
-            if (u + 1 < KT) {
-                frags(st, u + 1, af[(u + 1) % 2], bf[(u + 1) % 2]);
-            } else if (kk + 1 < ke) {
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                wait_copies<LPW>(min(NSTAGE - 2, ke - 2 - kk));
-                __builtin_amdgcn_s_barrier();
-                if (kk + NSTAGE < ke) issue(kk + NSTAGE, st);
-                frags((st + 1) % NSTAGE, 0, af[0], bf[0]);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int i = 0; i < MI; ++i)
-#pragma unroll
-                for (int j = 0; j < NI; ++j) acc[i][j] = mfma(af[u % 2][i], bf[u % 2][j], acc[i][j]);
-            __builtin_amdgcn_sched_barrier(0);
+        for (int u = 0; u + 1 < KT; ++u) {
+            mfmas(af[u % 2], bf[u % 2], 0);
+            frags(st, u + 1, af[(u + 1) % 2], bf[(u + 1) % 2]);
+            mfmas(af[u % 2], bf[u % 2], 1);
         }
+        // the last substep (its drain and barrier on every step, so that no
+        // path reaches its MFMAs without them); step kk + 1's first operands
+        // are read mid-substep (on the last step: stale data, unused)
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm((NSTAGE - 2) * LPW));
+        __builtin_amdgcn_s_barrier();
+        mfmas(af[(KT - 1) % 2], bf[(KT - 1) % 2], 0);
+        issue(kk + NSTAGE, st);
+        frags((st + 1) % NSTAGE, 0, af[0], bf[0]);
+        mfmas(af[(KT - 1) % 2], bf[(KT - 1) % 2], 1);
     }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));   // the trailing zero copies have landed
 
     // ---- epilogue. Accumulator (lane l, register r) -> row 8 (r / 4) + 4 (l / 32) + r % 4,
     // column l % 32 of its 32 x 32 tile.
@@ -277,6 +330,7 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
     if constexpr (EPI == EPI_SCORES || EPI == EPI_DSCORES) {
         const float g = p.g[0];
         const rsrc_t rp = rsrc(reinterpret_cast<char *>(p.pout) + b * p.p_bstride, p.p_bstride);
+        const rsrc_t rpt = rsrc(reinterpret_cast<char *>(p.pout_t) + b * p.p_bstride, p.p_bstride);
         const rsrc_t rpin = rsrc(EPI == EPI_DSCORES ? reinterpret_cast<const char *>(p.pin) + b * p.p_bstride
                                                     : reinterpret_cast<const char *>(p.pout), p.p_bstride);
         float dg = 0.f;
@@ -307,14 +361,28 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
                             if (s <= t && t < p.T) dg += static_cast<float>(t - s) * pe[e] * acc[i][j][4 * r4 + e];
                         }
                     }
+                    uint16_t xb[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) xb[e] = f32_to_bf16_bits(x[e]);
                     v2u32_t v;
-                    v[0] = static_cast<uint32_t>(f32_to_bf16_bits(x[0])) | (static_cast<uint32_t>(f32_to_bf16_bits(x[1])) << 16);
-                    v[1] = static_cast<uint32_t>(f32_to_bf16_bits(x[2])) | (static_cast<uint32_t>(f32_to_bf16_bits(x[3])) << 16);
+                    v[0] = static_cast<uint32_t>(xb[0]) | (static_cast<uint32_t>(xb[1]) << 16);
+                    v[1] = static_cast<uint32_t>(xb[2]) | (static_cast<uint32_t>(xb[3]) << 16);
                     __builtin_amdgcn_raw_buffer_store_b64(v, rp, off, 0, 0);
+                    // the transpose: element (row s, contraction t), one 2-byte store
+                    // each (the lanes of one s write 16-byte runs of t)
+                    const uint32_t off_t = (t / 16) * TB + 16u * 32 * ((t % 16) / 8) + 2u * (t % 8);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int s = s0 + e;
+                        __builtin_amdgcn_raw_buffer_store_b16(xb[e], rpt, off_t + (s / 32) * p.p_rt + 16u * (s % 32), 0, 0);
+                    }
                 }
         }
         if constexpr (EPI == EPI_DSCORES) {
-            __shared__ double red[WAVES];
+            // the wave sums meet in the stage memory, once every wave is past
+            // its last (unused) operand read
+            double *red = reinterpret_cast<double *>(lds);
+            __syncthreads();
             const double w = wave_sum(static_cast<double>(dg));
             if (lane == 0) red[wave] = w;
             __syncthreads();
@@ -379,10 +447,10 @@ Mat p_mat(const uint16_t *p, int Tq) {          // P layout: rows = t, contracti
 
 constexpr int KT = 2;   // contraction tiles per k-step (32 elements): four 32 KB stages at 256 x 256
 
-template <int G, bool TA, int EPI, int OUT>
+template <int G, bool TA, bool TBt, int EPI, int OUT>
 int launch_g(Args a, int B, hipStream_t s) {
-    const void *fn = reinterpret_cast<const void *>(&pair_kernel<G, G, KT, TA, EPI, OUT>);
-    constexpr int lds = NSTAGE * (G / 32 * KT) * 2 * TB;
+    const void *fn = reinterpret_cast<const void *>(&pair_kernel<G, G, KT, TA, TBt, EPI, OUT>);
+    constexpr int lds = nstage<G>() * (G / 32 * KT) * 2 * TB;
     static bool attr_done[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return check_launch("hipGetDevice");
@@ -396,30 +464,33 @@ int launch_g(Args a, int B, hipStream_t s) {
     a.jobs = B * a.jobs_per_row;
     int st = la_timer_begin(s);
     if (st) return st;
-    pair_kernel<G, G, KT, TA, EPI, OUT><<<dim3(static_cast<unsigned>(a.jobs)), WAVES * 64, lds, s>>>(a);
+    pair_kernel<G, G, KT, TA, TBt, EPI, OUT><<<dim3(static_cast<unsigned>(a.jobs)), WAVES * 64, lds, s>>>(a);
     st = check_launch("pair_kernel");
     if (st) return st;
     return la_timer_end(s);
 }
 
-template <bool TA, int EPI, int OUT>
+template <bool TA, bool TBt, int EPI, int OUT>
 int launch_o(const Args &a, int G, int B, hipStream_t s) {
-    return G == 256 ? launch_g<256, TA, EPI, OUT>(a, B, s) : launch_g<128, TA, EPI, OUT>(a, B, s);
+    if (G != 128) return fail(ULM_ERR_UNSUPPORTED, "block-pair products: tile size %d", G);
+    return launch_g<128, TA, TBt, EPI, OUT>(a, B, s);
 }
 
+// every product reads its operands plain (each matrix is stored in the
+// orientation its consumers contract over); TA is kept for the transposed read
 template <bool TA, int EPI>
 int launch(const Args &a, int G, int B, hipStream_t s) {
     if constexpr (EPI != EPI_ROWS) {
-        return launch_o<TA, EPI, 0>(a, G, B, s);
+        return launch_o<TA, false, EPI, 0>(a, G, B, s);
     } else {
         const int out = a.out_dt + (a.resid ? 3 : 0);
         switch (out) {
-        case 0: return launch_o<TA, EPI, 0>(a, G, B, s);
-        case 1: return launch_o<TA, EPI, 1>(a, G, B, s);
-        case 2: return launch_o<TA, EPI, 2>(a, G, B, s);
-        case 3: return launch_o<TA, EPI, 3>(a, G, B, s);
-        case 4: return launch_o<TA, EPI, 4>(a, G, B, s);
-        default: return launch_o<TA, EPI, 5>(a, G, B, s);
+        case 0: return launch_o<TA, false, EPI, 0>(a, G, B, s);
+        case 1: return launch_o<TA, false, EPI, 1>(a, G, B, s);
+        case 2: return launch_o<TA, false, EPI, 2>(a, G, B, s);
+        case 3: return launch_o<TA, false, EPI, 3>(a, G, B, s);
+        case 4: return launch_o<TA, false, EPI, 4>(a, G, B, s);
+        default: return launch_o<TA, false, EPI, 5>(a, G, B, s);
         }
     }
 }
@@ -428,12 +499,9 @@ int launch(const Args &a, int G, int B, hipStream_t s) {
 
 // ---- the operator's products in block-pair form (A, D multiples of 32)
 
-// Block (output tile) size of the block-pair products at T positions and B
-// batch rows: 256 when the scores product then has at least 128 tiles, else 128.
-int pair_block(int B, int T) {
-    const long long nb = (T + 255) / 256;
-    return static_cast<long long>(B) * nb * (nb + 1) / 2 >= 128 ? 256 : 128;
-}
+// Block (output tile) size of the block-pair products: 128 x 128 tiles, two
+// workgroups per CU (measured faster in total than 256 x 256 at the 110M shape).
+int pair_block(int, int) { return 128; }
 int pair_tq(int B, int T) {
     const int G = pair_block(B, T);
     return (T + G - 1) / G * G;
@@ -454,10 +522,12 @@ double pair_flops_per_token(int B, int T, int A, int D) {
     return nb * (nb + 1) * G * G * 3.0 * (A + D) / T;
 }
 
-// P = scores(q, k) in the P layout (Tq x Tq per batch row), then
-// out = P v (+ resid) in out_dt (B, T, D). kR, qR: R layout (A); vQ: Q layout (D).
+// P = scores(q, k) in the P layout (Tq x Tq per batch row) and its
+// transpose Pt, then out = P v (+ resid) in out_dt (B, T, D).
+// qR, kR: R layout (A); vQ: Q layout (D).
 int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *vQ, const float *g, uint16_t *P,
-                        void *out, int out_dt, const float *resid, int B, int T, int A, int D, hipStream_t s) {
+                        uint16_t *Pt, void *out, int out_dt, const float *resid, int B, int T, int A, int D,
+                        hipStream_t s) {
     using namespace pair;
     const int G = pair_block(B, T), Tq = pair_tq(B, T), NT = (T + 63) / 64;
     Args a{};
@@ -471,6 +541,7 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *
     a.nks = (A + 16 * KT - 1) / (16 * KT);
     const Mat pm = p_mat(P, Tq);
     a.pout = P;
+    a.pout_t = Pt;
     a.p_bstride = pm.bstride;
     a.p_rt = pm.rt;
     ULM_TRY((launch<false, EPI_SCORES>(a, G, B, s)));
@@ -491,16 +562,18 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *
     return launch<false, EPI_ROWS>(f, G, B, s);
 }
 
-// The backward products: dS = dscores(dfast, v) with the pair part of the
-// decay gradient into dg_part (pair_dscore_jobs doubles), dq_f = dS k,
-// dk_f = dS^T q (fp32 (B, T, A)), dv = P^T dfast in dv_dt (B, T, D).
-// vR, doR: R layout (D); kQ, qQ: Q layout (A); doQ: Q layout (D).
+// The backward products: dS = dscores(dfast, v) and its transpose dSt with the
+// pair part of the decay gradient into dg_part (pair_dscore_jobs doubles),
+// dq_f = dS k, dk_f = dS^T q (fp32 (B, T, A)), dv = P^T dfast in dv_dt (B, T, D).
+// vR, doR: R layout (D); kQ, qQ: Q layout (A); doQ: Q layout (D); P and Pt from
+// the forward.
 int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t *doQ, const uint16_t *kQ,
-                         const uint16_t *qQ, const uint16_t *P, const float *g, uint16_t *dS, double *dg_part,
-                         float *dqf, float *dkf, void *dv, int dv_dt, int B, int T, int A, int D, hipStream_t s) {
+                         const uint16_t *qQ, const uint16_t *P, const uint16_t *Pt, const float *g, uint16_t *dS,
+                         uint16_t *dSt, double *dg_part, float *dqf, float *dkf, void *dv, int dv_dt, int B, int T,
+                         int A, int D, hipStream_t s) {
     using namespace pair;
     const int G = pair_block(B, T), Tq = pair_tq(B, T), NT = (T + 63) / 64;
-    const Mat pm = p_mat(P, Tq), sm = p_mat(dS, Tq);
+    const Mat sm = p_mat(dS, Tq);
     Args a{};
     a.T = T;
     a.g = g;
@@ -511,6 +584,7 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
     a.krange = K_FULL;
     a.nks = (D + 16 * KT - 1) / (16 * KT);
     a.pout = dS;
+    a.pout_t = dSt;
     a.p_bstride = sm.bstride;
     a.p_rt = sm.rt;
     a.pin = P;
@@ -531,19 +605,20 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
     r.out_dt = ULM_F32;
     r.F = A;
     ULM_TRY((launch<false, EPI_ROWS>(r, G, B, s)));
-    // dk_f = dS^T q
+    // dk_f = dS^T q: rows s of dSt, contraction t >= the start of s's block
+    r.a = p_mat(dSt, Tq);
     r.b = q_mat(qQ, NT, A);
     r.krange = K_ANTI;
     r.out = dkf;
-    ULM_TRY((launch<true, EPI_ROWS>(r, G, B, s)));
+    ULM_TRY((launch<false, EPI_ROWS>(r, G, B, s)));
     // dv = P^T dfast
-    r.a = pm;
+    r.a = p_mat(Pt, Tq);
     r.b = q_mat(doQ, NT, D);
     r.nt = (D + G - 1) / G;
     r.out = dv;
     r.out_dt = dv_dt;
     r.F = D;
-    return launch<true, EPI_ROWS>(r, G, B, s);
+    return launch<false, EPI_ROWS>(r, G, B, s);
 }
 
 }  // namespace ulm

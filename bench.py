@@ -3,14 +3,24 @@
 
 One step = the fast-memory forward + backward (unified_memory and its
 backward) of all 12 UnifiedBlocks of the 110M shape on one synthetic batch:
-B=16, T=1024, D=768, A=3072 slots, chunk 64, v/dfast in bf16, r/q/stats fp32.
-Inputs are resident in HBM before the timed region. Prints one JSON line:
+B=16, T=1024, D=768, A=3072 slots, v/dfast in bf16, r/q/stats fp32. Inputs
+are resident in HBM before the timed region. Prints one JSON line:
 
   value      Mtok/s = B*T / step time
-  roofline   the chunked MFMA kernel (la_kgroup_kernel): algorithmic flops per
-             launch (B*T*(4*K*V + 2*64*V)) over its average launch time, measured
-             with HIP events on its own stream over the timed steps, against
-             the 2516.6 TFLOP/s dense bf16 peak
+  products   which evaluation the library picks at this shape (ulm_fm_path):
+             "pair" (block-pair tile GEMMs) or "chunked" (the chunked state form)
+  roofline   the dominant kernel (pair_kernel, or la_kgroup_kernel on the
+             chunked path): the algorithmic flops of every timed launch over
+             their summed launch time, measured with HIP events on the stream
+             each launch uses, against the 2516.6 TFLOP/s dense bf16 peak;
+             traffic is the HBM bytes per launch recorded under profiles/
+  path_tflops / chunked_equivalent_tflops
+             the whole step (statistics kernels included) in the chosen
+             evaluation's algorithmic flops, and in the chunked form's
+             16AD + 8C(A + D) flops per token (the same work priced as the
+             reference's algorithm)
+  configs    one block of the 15M (B=32, T=256, D=288, A=1152) and 42M (B=16,
+             T=1024, D=512, A=2048) shapes
   cpu_baseline  the oracle's chunked PyTorch form on the host cores (fp32,
              fwd+bwd of one block at B=1, T=1024), scaled to the 12-block step
   block      whole UnifiedBlocks (fused) fwd+bwd over the same shape under bf16
@@ -21,7 +31,8 @@ Inputs are resident in HBM before the timed region. Prints one JSON line:
   decode     batched recurrent decode at the 110M shape: 256 sequences, 12
              blocks, fp32 state (29 GB); the 512-position prompt in one
              chunked pass (UnifiedLM.prefill), then greedy steps; GB/s of the
-             algorithmic bytes per step against 8 TB/s
+             algorithmic bytes per step against 8 TB/s, with the oracle's
+             forward_recurrent on the host cores as its cpu_baseline
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--decode-steps N]
 """
@@ -41,7 +52,9 @@ for _p in (ROOT, PKG):
 METRIC = "fast-memory fwd+bwd Mtokens/s at 110M shape (% bf16 MFMA peak); decode GB/s"
 PEAK_BF16_TFLOPS = 2516.6
 PEAK_HBM_GBPS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "la_kgroup_kernel_traffic.txt")
+TRAFFIC_FILES = {"la_kgroup_kernel": os.path.join(ROOT, "profiles", "la_kgroup_kernel_traffic.txt"),
+                 "pair_kernel": os.path.join(ROOT, "profiles", "pair_kernel_traffic.txt"),
+                 "decode_state_kernel": os.path.join(ROOT, "profiles", "decode_state_kernel_traffic.txt")}
 
 
 def log(msg):
@@ -61,20 +74,33 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-block", action="store_true")
     p.add_argument("--no-step", action="store_true")
+    p.add_argument("--no-configs", action="store_true")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                    help="first run one plain fp32 copy kernel over MB megabytes (a known-size reference for "
                         "hardware byte counters)")
     return p.parse_args()
 
 
-def bench_training(torch, args):
+def fm_path_name(code):
+    return {0: "generic", 1: "chunked", 2: "pair"}.get(code, "invalid")
+
+
+def bench_training(torch, args, shape=None, steps=None, warmup=None):
+    """unified_memory forward + backward of every block of a shape (r fp32, v
+    and dfast bf16, the upstream gradient of q fp32). The roofline object
+    prices the launches the library times (every chunked or block-pair
+    product launch) with that evaluation's algorithmic flops."""
     import kernel
     import ulm_native
     import workloads
-    cfg = workloads.SHAPES[args.shape]
+    shape = shape or args.shape
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
+    cfg = workloads.SHAPES[shape]
     B, T, D, A, L = cfg["B"], cfg["T"], cfg["D"], cfg["A"], cfg["blocks"]
     dev = torch.device("cuda:0")
-    log(f"training workload {args.shape}: B={B} T={T} D={D} A={A} blocks={L}")
+    path = fm_path_name(ulm_native.lib().ulm_fm_path(B, T, A, D))
+    log(f"training workload {shape}: B={B} T={T} D={D} A={A} blocks={L}, {path} products")
     blocks = []
     for l in range(L):
         r, v, g, w = workloads.block_inputs(B, T, D, A, seed=1000 + l, device=dev, v_dtype=torch.bfloat16)
@@ -88,32 +114,63 @@ def bench_training(torch, args):
         for blk, (q, fast) in zip(reversed(blocks), reversed(outs)):
             torch.autograd.grad((q, fast), blk, (dq_up, df_up))
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    with ulm_native.LaTimer(max_launches=4 * L * args.steps + 16) as timer:
+    per_step = 6 if path == "pair" else 4
+    with ulm_native.LaTimer(max_launches=per_step * L * steps + 16) as timer:
         t0 = time.perf_counter()
-        for i in range(args.steps):
+        for i in range(steps):
             step()
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / args.steps
-    la_ms = timer.total_ms / max(timer.launches, 1)
-    la_flops = workloads.la_kernel_flops(B, T, A, D)
-    achieved = la_flops / (la_ms * 1e-3) / 1e12
+    ms_step = (t1 - t0) * 1e3 / steps
+    launch_ms = timer.total_ms / max(timer.launches, 1)
+    if path == "pair":
+        kname = "pair_kernel"
+        flops_launches = workloads.pair_flops(B, T, A, D) * L * steps   # all timed launches
+        flops_step = workloads.pair_flops(B, T, A, D) * L
+        note = ("the six block-pair products (scores, apply, dscores, dq_f, dk_f, dv) of every block, "
+                "algorithmic flops 6 (A + D) per causal pair (t, s); the kernels execute whole 128 x 128 "
+                f"diagonal tiles, {workloads.pair_tile_flops(B, T, A, D) / workloads.pair_flops(B, T, A, D):.3f}x that")
+    else:
+        kname = "la_kgroup_kernel"
+        # fwd and dv contract keys A into values D, dq and dk keys D into values A
+        flops_launches = (workloads.la_kernel_flops(B, T, A, D) + workloads.la_kernel_flops(B, T, D, A)) / 2 * timer.launches
+        flops_step = 4 * workloads.la_flops(B, T, A, D) * L
+        note = "the four chunked products of every block, 4 K V + 2 C V per token and product"
+    achieved = flops_launches / (timer.total_ms * 1e-3) / 1e12 if timer.total_ms > 0 else 0.0
     traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
+    tfile = TRAFFIC_FILES.get(kname)
+    if tfile and os.path.exists(tfile) and shape == "110M":
+        with open(tfile) as f:
             traffic = json.load(f).get("bytes_per_launch")
-    ftok = 4 * workloads.la_flops(B, T, A, D) / (B * T)
-    path_tflops = ftok * L * B * T / (ms_step * 1e-3) / 1e12
-    log(f"step {ms_step:.2f} ms, la_kgroup_kernel {la_ms:.3f} ms x {timer.launches} launches, {achieved:.1f} TFLOP/s")
-    return dict(B=B, T=T, D=D, A=A, L=L, ms_step=ms_step, value=B * T / (ms_step * 1e-3) / 1e6,
+    path_tflops = flops_step / (ms_step * 1e-3) / 1e12
+    chunk_eq = workloads.chunked_flops_per_token(A, D) * L * B * T / (ms_step * 1e-3) / 1e12
+    log(f"step {ms_step:.2f} ms, {kname} {launch_ms:.3f} ms x {timer.launches} launches, {achieved:.1f} TFLOP/s")
+    return dict(B=B, T=T, D=D, A=A, L=L, path=path, ms_step=ms_step, value=B * T / (ms_step * 1e-3) / 1e6,
                 roofline={"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
-                          "kernel": "la_kgroup_kernel", "flops_per_launch": la_flops,
-                          "avg_launch_ms": round(la_ms, 4), "launches_timed": timer.launches},
-                path_tflops=path_tflops)
+                          "traffic_source": "recorded (profiles/)" if traffic else None,
+                          "kernel": kname, "flops": note,
+                          "avg_launch_ms": round(launch_ms, 4), "launches_timed": timer.launches},
+                path_tflops=path_tflops, chunked_equivalent_tflops=chunk_eq)
+
+
+def bench_configs(torch, args):
+    """Single-block fast-memory fwd + bwd at the 15M (B=32, T=256, D=288,
+    A=1152) and 42M (B=16, T=1024, D=512, A=2048) shapes."""
+    out = {}
+    for shape in ("15M", "42M"):
+        t = bench_training(torch, args, shape=shape, steps=max(args.steps, 10), warmup=max(args.warmup, 3))
+        out[shape] = {"workload": f"fast-memory fwd+bwd, one block of the {shape} shape (B={t['B']}, T={t['T']}, "
+                                  f"D={t['D']}, A={t['A']})",
+                      "path": t["path"], "ms_per_block": round(t["ms_step"], 4), "Mtok_per_s": round(t["value"], 4),
+                      "tflops": round(t["path_tflops"], 2),
+                      "frac_bf16_peak": round(t["path_tflops"] / PEAK_BF16_TFLOPS, 4),
+                      "chunked_equivalent_tflops": round(t["chunked_equivalent_tflops"], 2),
+                      "roofline": t["roofline"]}
+    return out
 
 
 def bench_block(torch, args):
@@ -155,7 +212,9 @@ def bench_block(torch, args):
 
     ms = timed(True)
     ms_c = timed(False)
-    ftok = workloads.block_flops_per_token(T, A, D) * L
+    import ulm_native
+    path = fm_path_name(ulm_native.lib().ulm_fm_path(B, T, A, D))
+    ftok = workloads.block_flops_per_token(T, A, D, path=path) * L
     log(f"block step {ms:.2f} ms fused, {ms_c:.2f} ms op by op")
     return {"workload": f"UnifiedBlock fwd+bwd, {L} blocks of the {args.shape} shape, bf16 autocast",
             "ms_per_step": round(ms, 3), "Mtok_per_s": round(B * T / (ms * 1e-3) / 1e6, 4),
@@ -200,7 +259,9 @@ def bench_train_step(torch, args):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     # per token: every block's GEMMs and fast memory, plus the classifier (2 V D forward, twice that backward)
-    ftok = workloads.block_flops_per_token(T, A, D) * L + 6 * V * D
+    import ulm_native
+    path = fm_path_name(ulm_native.lib().ulm_fm_path(B, T, A, D))
+    ftok = workloads.block_flops_per_token(T, A, D, path=path) * L + 6 * V * D
     log(f"training step {ms:.2f} ms, loss {model.last_loss.item():.3f}")
     return {"workload": f"UnifiedLM {args.shape} training step fwd+bwd: embedding, {L} fused blocks, classifier "
                         f"over {V} tokens, cross-entropy; bf16 autocast; no optimizer",
@@ -290,6 +351,12 @@ def bench_decode(torch, args):
     gbps = bytes_step / (step_ms * 1e-3) / 1e9
     log(f"decode {step_ms:.2f} ms/step, {gbps:.0f} GB/s; chunked prefill {pre_ms:.1f} ms "
         f"({N * args.prefill / (pre_ms * 1e-3) / 1e6:.2f} Mtok/s)")
+    traffic = None
+    tfile = TRAFFIC_FILES["decode_state_kernel"]
+    if os.path.exists(tfile) and N == 256:
+        with open(tfile) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+    cpu = None if args.no_cpu else bench_decode_cpu(torch, model, c)
     return {"metric": "decode GB/s", "value": round(gbps, 1), "unit": "GB/s", "ms_per_step": round(step_ms, 3),
             "tok_per_s": round(N / (step_ms * 1e-3), 1),
             "prefill": "chunked (UnifiedLM.prefill, fused blocks, GEMMs bf16 under autocast)",
@@ -297,9 +364,39 @@ def bench_decode(torch, args):
             "prefill_Mtok_per_s": round(N * args.prefill / (pre_ms * 1e-3) / 1e6, 3), "bytes_per_step": bytes_step,
             "state_GB": round(N * L * D * A * 4 / 1e9, 2),
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                         "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None},
+                         "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": traffic,
+                         "traffic_kernel": "decode_state_kernel (S read + write and read-out, per block-step)",
+                         "traffic_source": "recorded (profiles/)" if traffic else None},
+            "cpu_baseline": cpu,
             "config": {"N": N, "D": D, "A": A, "blocks": L, "vocab": V, "prefill": args.prefill,
                        "steps": args.decode_steps}}
+
+
+def bench_decode_cpu(torch, model, c, n_seq=8, n_pos=12):
+    """The oracle's forward_recurrent (model.py:164-175) in fp32 on the host
+    cores: n_seq sequences of n_pos positions of the 110M decode model, timed
+    after one position of warm-up, in GB/s of the same algorithmic bytes per
+    decode position as the GPU figure (at N = n_seq)."""
+    from oracle import fastmem as fm
+    import workloads
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    params = {n: p.detach().float().cpu() for n, p in model.named_parameters()}
+    gen = torch.Generator().manual_seed(11)
+    tokens = torch.randint(0, c["vocab"], (n_seq, n_pos + 1), generator=gen)
+    with torch.no_grad():
+        fm.forward_recurrent(params, tokens[:, :1])   # warm-up
+        t0 = time.perf_counter()
+        fm.forward_recurrent(params, tokens[:, 1:])
+        dt = time.perf_counter() - t0
+    step_s = dt / n_pos
+    bytes_step = workloads.decode_bytes_per_step(n_seq, c["blocks"], c["A"], c["D"], c["vocab"])
+    log(f"decode cpu baseline: {step_s * 1e3:.1f} ms per position for {n_seq} sequences, {threads} threads")
+    return {"value": round(bytes_step / step_s / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "tok_per_s": round(n_seq / step_s, 2),
+            "sample": f"oracle forward_recurrent fp32 (the 110M decode model: D={c['D']}, A={c['A']}, "
+                      f"{c['blocks']} blocks, vocab {c['vocab']}), {n_seq} sequences x {n_pos} positions from the "
+                      f"prior state ({dt:.2f} s), algorithmic bytes per position at N={n_seq}"}
 
 
 def main():
@@ -322,6 +419,7 @@ def main():
         log(f"copy probe: {4 * n} bytes read, {4 * n} bytes written")
         del x, y
     train = bench_training(torch, args)
+    configs = None if args.no_configs else bench_configs(torch, args)
     cpu = None if args.no_cpu else bench_cpu_baseline(torch, train)
     block = None if args.no_block else bench_block(torch, args)
     train_step = None if args.no_step else bench_train_step(torch, args)
@@ -342,9 +440,13 @@ def main():
         "config": {"workload": f"fast-memory fwd+bwd, {train['L']} blocks of the {args.shape} shape",
                    "global_batch": train["B"], "seq_len": train["T"], "dim": train["D"], "slots": train["A"],
                    "blocks": train["L"], "chunk": 64, "parallelism": "single GPU"},
+        "products": train["path"],
         "path_tflops": round(train["path_tflops"], 2),
         "path_frac_bf16_peak": round(train["path_tflops"] / PEAK_BF16_TFLOPS, 4),
+        "chunked_equivalent_tflops": round(train["chunked_equivalent_tflops"], 2),
+        "chunked_equivalent_frac_bf16_peak": round(train["chunked_equivalent_tflops"] / PEAK_BF16_TFLOPS, 4),
         "roofline": train["roofline"],
+        "configs": configs,
         "cpu_baseline": cpu,
         "block": block,
         "train_step": train_step,

@@ -44,6 +44,17 @@ enum ulm_dtype { ULM_F32 = 0, ULM_BF16 = 1, ULM_F16 = 2 };
 int ulm_abi_version(void);
 const char *ulm_last_error(void);
 
+/* Which evaluation of the products ulm_fm_fwd / ulm_fm_bwd and the block
+ * entries use at this shape: 0 the generic kernel (A or D not a multiple of
+ * 32), 1 the chunked state form (`_la`'s algorithm, the K-group kernel), 2 the
+ * block-pair form (the same sums over pairs of 128-position blocks, six tile
+ * GEMMs), whichever needs fewer flops: about 4 A D per token and product for
+ * the first, T (A + D) / 2 for the second. The environment variable
+ * ULM_FM_PATH=chunked or =pair forces one of them for aligned shapes; it must
+ * not change between a forward and its backward. -1 for invalid sizes. No
+ * counterpart in the reference (one algorithm, kernel.py:183-196). */
+int ulm_fm_path(int B, int T, int A, int D);
+
 /* ------------------------------------------------------------------------
  * Training: fused fast memory. Replaces UnifiedMemory.forward
  * (kernel.py:202-213): q = r / c with c = w + decayed cumsum of k = shift(r),

@@ -266,6 +266,11 @@ extern "C" int ulm_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
 // ---------------------------------------------------------------------------
 // fused operator
 
+extern "C" int ulm_fm_path(int B, int T, int A, int D) {
+    if (B <= 0 || T <= 0 || A <= 0 || D <= 0) return -1;
+    return static_cast<int>(train_path(B, T, A, D));
+}
+
 extern "C" size_t ulm_fm_saved_bytes(int B, int T, int A, int D, int v_dtype) {
     if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(v_dtype)) return 0;
     return saved_layout(nullptr, B, T, A, D, v_dtype, train_path(B, T, A, D)).bytes;

@@ -22,6 +22,7 @@ P, I, SZ, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_float
 SIGNATURES = {
     "ulm_abi_version": (I, []),
     "ulm_last_error": (ctypes.c_char_p, []),
+    "ulm_fm_path": (I, [I, I, I, I]),
     "ulm_fm_saved_bytes": (SZ, [I, I, I, I, I]),
     "ulm_fm_fwd_workspace_bytes": (SZ, [I, I, I, I, I]),
     "ulm_fm_fwd": (I, [P, P, I, P, P, P, P, I, P, SZ, P, SZ, I, I, I, I, P]),

@@ -81,11 +81,13 @@ def la_flops(B, T, K, V, chunk=64):
     return B * T * (4 * K * V + 2 * chunk * (K + V))
 
 
-def block_flops_per_token(T, A, D, chunk=64):
+def block_flops_per_token(T, A, D, chunk=64, path="chunked"):
     """Algorithmic flops of one UnifiedBlock per token, forward + backward: the
     key, value and mu GEMMs (2AD + 2D^2 + 2AD forward, twice that backward) and
-    the four chunked fast-memory products, 16AD + 8C(A + D)."""
-    return 3 * (4 * A * D + 2 * D * D) + 16 * A * D + 8 * chunk * (A + D)
+    the fast memory, 16AD + 8C(A + D) in the chunked state form or
+    3 (A + D) (T + 1) in the block-pair form (its average over a sequence)."""
+    fm = 3 * (A + D) * (T + 1) if path == "pair" else 16 * A * D + 8 * chunk * (A + D)
+    return 3 * (4 * A * D + 2 * D * D) + fm
 
 
 def la_kernel_flops(B, T, K, V, chunk=64):
@@ -93,3 +95,27 @@ def la_kernel_flops(B, T, K, V, chunk=64):
     update 2KV, read-out 2KV and intra apply 2CV per token. The intra scores
     (2CK per token) are computed once per chunk by the scores kernel."""
     return B * T * (4 * K * V + 2 * chunk * V)
+
+
+PAIR_BLOCK = 128   # position block of the block-pair products
+
+
+def pair_flops(B, T, A, D):
+    """Algorithmic flops of the block-pair evaluation of one block's fast
+    memory, forward + backward: every causal pair (t, s), s <= t, of a batch
+    row costs 2A (scores) + 2D (apply) + 2D (dscores) + 2A (dq_f) + 2A (dk_f)
+    + 2D (dv)."""
+    return 3 * (A + D) * B * T * (T + 1)
+
+
+def pair_tile_flops(B, T, A, D, G=PAIR_BLOCK):
+    """The flops the six pair products execute: whole G x G tiles, the
+    diagonal ones included (their upper halves are computed and masked)."""
+    nb = -(-T // G)
+    return B * nb * (nb + 1) * G * G * 3 * (A + D)
+
+
+def chunked_flops_per_token(A, D, chunk=64):
+    """Flops per token of the chunked state form of one block, fwd + bwd:
+    16AD + 8C(A + D) (four chunked products)."""
+    return 16 * A * D + 8 * chunk * (A + D)

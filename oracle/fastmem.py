@@ -30,6 +30,12 @@ How each function is pinned (tests/test_oracle.py):
   dg_bf16_floor         with rounding off equals autograd's dg (the identity
                         with the kernel's tau); rounding its operands to bf16
                         is the only difference.
+  block_forward         autocast=False is the reference block; with autocast=True
+                        its forward and its scalar/bias gradients match torch's
+                        CPU bf16 autocast of the block's products (30x closer
+                        than the exact block), and a rounding left out (planted)
+                        breaks the agreement.
+  round_grad_bf16       equals the backward of torch's own bf16 round trip.
   lm_forward            parallel == forward_recurrent (test_all.py:110-116),
                         causality (test_all.py:119-128), finite grads.
   forward_recurrent     logits of the reference's own run.c (compiled under
@@ -235,30 +241,68 @@ def decay_log(log_rate):
     return -log_rate.exp()
 
 
-def block_forward(p, prefix, x, norm_eps=1e-5, form="chunked", chunk=64):
+def round_bf16(x):
+    """x rounded to bf16 in the forward, the identity in the backward: the
+    value of a bf16 operand with an exact gradient."""
+    return x + (x.to(torch.bfloat16).to(x.dtype) - x).detach()
+
+
+class _RoundGradBf16(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        return x.view_as(x)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(torch.bfloat16).to(g.dtype)
+
+
+def round_grad_bf16(x):
+    """The identity in the forward; the gradient arriving at x is rounded to
+    bf16 on its way back: the gradient of a tensor stored in bf16."""
+    return _RoundGradBf16.apply(x)
+
+
+def block_forward(p, prefix, x, norm_eps=1e-5, form="chunked", chunk=64, autocast=False):
     """UnifiedBlock.forward with the fast read replaced by a reference form
-    (model.py:77-85, test_all.py:64-72). ``p`` maps state_dict names to tensors."""
+    (model.py:77-85, test_all.py:64-72). ``p`` maps state_dict names to tensors.
+
+    autocast=True keeps the arithmetic exact but rounds to bf16 what bf16
+    autocast rounds around the block's GEMMs (train.py trains under
+    torch.autocast(bfloat16)). In the forward: the conv output u, both
+    operands of the key, value and mu products, and the key and value
+    outputs; the key bias is added after the rounding and the mu product's
+    output stays unrounded, as the fused block computes them. In the
+    backward, the gradients of the tensors held in bf16: of the key and value
+    outputs, of the mu product's operand w q, and the block's upstream
+    gradient as the mu product and the fast memory receive it (the residual
+    path keeps it exact). Every other gradient passes the roundings
+    unchanged."""
     g = lambda n: p[prefix + n]
+    rnd = round_bf16 if autocast else (lambda t: t)
+    rgr = round_grad_bf16 if autocast else (lambda t: t)
     h = rmsnorm(x, g("norm.weight"), norm_eps)
-    u = causal_conv(h, g("conv.weight"))
-    r = address(F.linear(u, g("key.weight"), g("key.bias")), g("log_eps"))
-    v = F.linear(h, g("val.weight"))
+    u = rnd(causal_conv(h, g("conv.weight")))
+    pre = rgr(rnd(F.linear(rnd(u), rnd(g("key.weight")))))
+    r = address(pre + g("key.bias"), g("log_eps"))
+    v = rgr(rnd(F.linear(rnd(h), rnd(g("val.weight")))))
     w = prior_mass(g("log_w"))
     q, fast = fast_memory(r, v, decay_log(g("log_rate")), w, form, chunk)
-    return x + F.linear(q * w, g("mu.weight")) + fast
+    return x + rgr(F.linear(rgr(rnd(q * w)), rnd(g("mu.weight"))) + fast)
 
 
 def n_layers_of(p):
     return 1 + max(int(k.split(".")[1]) for k in p if k.startswith("layers."))
 
 
-def lm_forward(p, tokens, targets=None, norm_eps=1e-5, form="chunked", chunk=64):
+def lm_forward(p, tokens, targets=None, norm_eps=1e-5, form="chunked", chunk=64, autocast=False):
     """UnifiedLM.forward in a reference form (test_all.py:64-75, model.py:149-162).
-    Returns (logits, loss); the classifier is tied to the embedding (model.py:127)."""
+    Returns (logits, loss); the classifier is tied to the embedding (model.py:127).
+    autocast: the blocks' bf16 roundings as in block_forward."""
     emb = p["tok_embeddings.weight"]
     h = emb[tokens]
     for i in range(n_layers_of(p)):
-        h = block_forward(p, f"layers.{i}.", h, norm_eps, form, chunk)
+        h = block_forward(p, f"layers.{i}.", h, norm_eps, form, chunk, autocast)
     logits = F.linear(rmsnorm(h, p["norm.weight"], norm_eps), p.get("output.weight", emb))
     loss = None
     if targets is not None:

@@ -45,10 +45,25 @@ def test_nonzero_status_surfaces_as_runtime_error():
         nat.call("ulm_la", None, None, None, None, None, 1, 0, 8, 8, 0, 0, None, 0, None)
 
 
-def test_workspace_sizes():
+def test_workspace_sizes(monkeypatch):
     lib = nat.lib()
     B, T, A, D = 16, 1024, 3072, 768
     NT = (T + 63) // 64
+    # at the 110M shape the block-pair form needs fewer flops than the chunked state form
+    assert lib.ulm_fm_path(B, T, A, D) == 2
+    assert lib.ulm_fm_path(B, 8192, A, D) == 1            # past 4096 positions: the state form
+    assert lib.ulm_fm_path(2, 70, 12, 8) == 0             # widths off the 32 grid: the generic kernel
+    # pair form, saved: bf16 q, k (Q layout), v (R layout), the scores P, their
+    # transpose and their bf16 residual (Tq x Tq per row), n checkpoints
+    Tq = (T + 127) // 128 * 128
+    for dt in (nat.ULM_BF16, nat.ULM_F32):
+        assert lib.ulm_fm_saved_bytes(B, T, A, D, dt) >= B * T * (4 * A + 2 * D) + 3 * B * Tq * Tq * 2 + B * NT * A * 4
+    # backward: fp32 dq_f and dk_f, two tiled dfast copies, dS and its transpose
+    assert lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32) >= B * T * (8 * A + 4 * D) + 2 * B * Tq * Tq * 2
+    assert (lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32)
+            == lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16))
+    monkeypatch.setenv("ULM_FM_PATH", "chunked")
+    assert lib.ulm_fm_path(B, T, A, D) == 1
     # 4 key groups of 768 slots: fp32 partial outputs, plus the forward score tiles
     assert lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_F32) >= 4 * B * T * D * 4 + B * NT * 64 * 64 * 2
     assert lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * D * 4

@@ -125,13 +125,17 @@ def test_unified_memory_paths(B, T, A, D, path, monkeypatch):
 
 
 @pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
-def test_address_matches_oracle(pdt):
-    say(f"relu2 address {pdt}")
+@pytest.mark.parametrize("log_eps", [0.3, -10.0, 10.0, 10.5])
+def test_address_matches_oracle(pdt, log_eps):
+    """The relu^2 address and its gradients; log_eps at and beyond the clamp
+    bounds (model.py:72: clamp(-10, 10)), where torch's clamp passes the
+    gradient at the bounds and zeroes it outside."""
+    say(f"relu2 address {pdt} log_eps={log_eps}")
     gen = torch.Generator().manual_seed(3)
     M, A = 300, 700
     pre = torch.randn(M, A, generator=gen).to(pdt)
     bias = torch.randn(A, generator=gen) * 0.5
-    le = torch.tensor(0.3)
+    le = torch.tensor(log_eps)
     dr = torch.randn(M, A, generator=gen)
     pg = pre.cuda().requires_grad_(True)
     bg = bias.cuda().requires_grad_(True)
@@ -147,7 +151,10 @@ def test_address_matches_oracle(pdt):
     tol = 1e-5 if pdt == torch.float32 else 1e-2
     assert rel(pg.grad, p64.grad) < tol
     assert rel(bg.grad, b64.grad) < 1e-5
-    assert rel(lg.grad, l64.grad) < 1e-5
+    if log_eps > 10.0:
+        assert lg.grad.item() == 0.0 and l64.grad.item() == 0.0
+    else:
+        assert l64.grad.item() != 0.0 and rel(lg.grad, l64.grad) < 1e-5
 
 
 def _decode_model(seed=0, **kw):

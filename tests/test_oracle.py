@@ -12,6 +12,7 @@ import tempfile
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import fastmem as fm
 from oracle import runc, ulme
@@ -283,6 +284,114 @@ def test_gradients_finite():
     loss.backward()
     for name, t in p.items():
         assert t.grad is not None and torch.isfinite(t.grad).all(), name
+
+
+def _block_inputs(seed=3, B=2, T=70, dim=32, hidden=48):
+    p = fm.tiny_params(seed, dim=dim, n_layers=1, hidden_dim=hidden)
+    x = torch.randn(B, T, dim, generator=torch.Generator().manual_seed(seed), dtype=torch.float64)
+    return p, x
+
+
+def _autocast_block_ref(p, x):
+    """The block with its three products run by torch's CPU bf16 autocast
+    (bf16 operands, fp32 accumulation, bf16 outputs) and the conv in fp32
+    with a bf16 output, the rest in float64."""
+    g = lambda n: p["layers.0." + n].float()
+    bf = torch.bfloat16
+    h = fm.rmsnorm(x.float(), g("norm.weight"), 1e-5)
+    u = fm.causal_conv(h, g("conv.weight")).to(bf)
+    with torch.autocast("cpu", dtype=bf):
+        pre = F.linear(u, g("key.weight"))
+        v = F.linear(h, g("val.weight"))
+    assert pre.dtype == bf and v.dtype == bf
+    r = fm.address(pre.double() + p["layers.0.key.bias"], p["layers.0.log_eps"])
+    w = fm.prior_mass(p["layers.0.log_w"])
+    q, fast = fm.fast_memory(r, v.double(), fm.decay_log(p["layers.0.log_rate"]), w)
+    if fast.requires_grad:
+        # the fused block hands the fast memory its upstream gradient in bf16
+        fast.register_hook(lambda d: d.to(bf).to(d.dtype))
+    with torch.autocast("cpu", dtype=bf):
+        mu = F.linear((q * w).float(), g("mu.weight"))
+    return x + mu.double() + fast
+
+
+def test_block_autocast_emulation_matches_torch_autocast(monkeypatch):
+    """block_forward(autocast=True) against the block whose products torch's
+    own bf16 autocast computes: 30x closer to it than the exact block is
+    (what remains is mostly the mu output, rounded by autocast, kept fp32
+    by the fused block).
+    A rounding left out (planted here: the value weight kept exact) moves the
+    emulation away from torch's result by far more than that."""
+    p, x = _block_inputs()
+    rel = lambda a, b: ((a - b).norm() / b.norm()).item()
+    exact = fm.block_forward(p, "layers.0.", x)
+    emu = fm.block_forward(p, "layers.0.", x, autocast=True)
+    ref = _autocast_block_ref(p, x)
+    assert rel(exact, ref) > 1e-4
+    assert rel(emu, ref) < 0.03 * rel(exact, ref)
+    keep = p["layers.0.val.weight"]
+    rounding = fm.round_bf16
+    monkeypatch.setattr(fm, "round_bf16", lambda t: t if t is keep else rounding(t))
+    planted = fm.block_forward(p, "layers.0.", x, autocast=True)
+    assert rel(planted, ref) > 10 * rel(emu, ref)
+
+
+def _head_grads(p, x, block):
+    gen = torch.Generator().manual_seed(5)
+    head = torch.randn(11, x.shape[-1], generator=gen, dtype=torch.float64)
+    target = torch.randint(0, 11, (x.shape[0] * x.shape[1],), generator=gen)
+    pp = {k: v.clone().requires_grad_() for k, v in p.items()}
+    xx = x.clone().requires_grad_()
+    F.cross_entropy((block(pp, xx) @ head.t()).reshape(-1, 11), target).backward()
+    return {"x": xx.grad, **{k: v.grad for k, v in pp.items() if v.grad is not None}}
+
+
+def test_block_autocast_gradients_match_torch_autocast(monkeypatch):
+    """The backward roundings of block_forward(autocast=True) against the same
+    torch-autocast block, under a classifier loss. The scalar and bias
+    gradients, which torch's autocast rounds nowhere else, come 30x closer to
+    torch's than the exact block's; the weight and input gradients at least
+    2x (torch also rounds the weight gradients and the products' input
+    gradients to bf16, which the fused block keeps in fp32). Dropping the
+    gradient roundings (planted: round_grad_bf16 as the identity) undoes the
+    agreement of the decay gradient."""
+    p, x = _block_inputs()
+    rel = lambda a, b: ((a - b).norm() / b.norm()).item()
+    ref = _head_grads(p, x, _autocast_block_ref)
+    exact = _head_grads(p, x, lambda pp, xx: fm.block_forward(pp, "layers.0.", xx))
+    emu = _head_grads(p, x, lambda pp, xx: fm.block_forward(pp, "layers.0.", xx, autocast=True))
+    assert set(ref) == set(emu)
+    for k in ref:
+        tight = k.split(".")[-1] in ("bias", "log_eps", "log_rate", "log_w")
+        assert rel(emu[k], ref[k]) < (1 / 30 if tight else 0.5) * rel(exact[k], ref[k]), k
+    monkeypatch.setattr(fm, "round_grad_bf16", lambda t: t)
+    planted = _head_grads(p, x, lambda pp, xx: fm.block_forward(pp, "layers.0.", xx, autocast=True))
+    k = "layers.0.log_rate"
+    assert rel(planted[k], ref[k]) > 10 * rel(emu[k], ref[k])
+
+
+def test_round_grad_bf16_is_torch_cast_backward():
+    """round_grad_bf16: the identity forward, and the backward of torch's own
+    bf16 round trip x.to(bf16).to(float64) on the gradient."""
+    gen = torch.Generator().manual_seed(1)
+    x = torch.randn(64, dtype=torch.float64, generator=gen).requires_grad_()
+    d = torch.randn(64, dtype=torch.float64, generator=gen)
+    y = fm.round_grad_bf16(x)
+    assert torch.equal(y, x)
+    (gx,) = torch.autograd.grad(y, x, d)
+    x2 = x.detach().to(torch.bfloat16).requires_grad_()
+    (g2,) = torch.autograd.grad(x2.to(torch.float64), x2, d)
+    assert torch.equal(gx, g2.double()) and not torch.equal(gx, d)
+
+
+def test_round_bf16_is_forward_only():
+    """round_bf16 leaves bf16 values unchanged and passes the gradient
+    through unrounded."""
+    x = torch.randn(4, 8, dtype=torch.float64).to(torch.bfloat16).double()
+    assert torch.equal(fm.round_bf16(x), x)
+    y = torch.randn(4, 8, dtype=torch.float64, requires_grad=True)
+    fm.round_bf16(y).sum().backward()
+    assert torch.equal(y.grad, torch.ones_like(y))     # the rounding passes gradients unchanged
 
 
 # ----- the reference's own C decoder

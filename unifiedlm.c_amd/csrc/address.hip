@@ -191,7 +191,7 @@ __global__ __launch_bounds__(kAddrWaves * 64) void addr_bwd_kernel(const T *__re
     if (threadIdx.x == 0) {
         const float le = log_eps[0];
         const float d = dle_w[0] + dle_w[1] + dle_w[2] + dle_w[3];
-        dle_part[blockIdx.x] = (le > -10.f && le < 10.f) ? d * E : 0.f;
+        dle_part[blockIdx.x] = (le >= -10.f && le <= 10.f) ? d * E : 0.f;   // torch clamp passes the gradient at the bounds
     }
 }
 

@@ -60,10 +60,11 @@ size_t pair_p_bytes(int B, int T);
 int pair_dscore_jobs(int B, int T);
 double pair_flops_per_token(int B, int T, int A, int D);
 int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *vQ, const float *g, uint16_t *P,
-                        uint16_t *Pt, void *out, int out_dt, const float *resid, int B, int T, int A, int D,
-                        hipStream_t s);
+                        uint16_t *Pt, uint16_t *Plo, void *out, int out_dt, const float *resid, int B, int T, int A,
+                        int D, hipStream_t s);
 int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t *doQ, const uint16_t *kQ,
-                         const uint16_t *qQ, const uint16_t *P, const uint16_t *Pt, const float *g, uint16_t *dS,
+                         const uint16_t *qQ, const uint16_t *P, const uint16_t *Pt, const uint16_t *Plo,
+                         const float *g, uint16_t *dS,
                          uint16_t *dSt, double *dg_part, float *dqf, float *dkf, void *dv, int dv_dt, int B, int T,
                          int A, int D, hipStream_t s);
 
@@ -98,7 +99,7 @@ Path train_path(int B, int T, int A, int D) {
 struct Saved {
     uint16_t *q16n, *k16n, *v16n;                                     // generic path
     uint16_t *qR, *kR, *qQ, *kQ, *vR, *vRl, *vQ, *vQl, *Pdv;   // K-group path (pair: qQ, kQ, vR)
-    uint16_t *P, *Pt;                                                 // pair path: the scores and their transpose
+    uint16_t *P, *Pt, *Plo;   // pair path: the scores, their transpose and their bf16 residual
     float *nck;
     size_t bytes;
 };
@@ -114,6 +115,7 @@ Saved saved_layout(void *base, int B, int T, int A, int D, int v_dtype, Path pat
         s.vR = c.take<uint16_t>(td);
         s.P = c.take<uint16_t>(pair_p_bytes(B, T) / 2);
         s.Pt = c.take<uint16_t>(pair_p_bytes(B, T) / 2);
+        s.Plo = c.take<uint16_t>(pair_p_bytes(B, T) / 2);
     } else if (path == PATH_CHUNKED) {
         s.qR = c.take<uint16_t>(ta);
         s.kR = c.take<uint16_t>(ta);
@@ -301,7 +303,7 @@ int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const 
         ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, ws.qR, ws.kR, sv.qQ, sv.kQ, sv.nck, nullptr, B, T, A, s,
                                  qw, qw_dt));
         ULM_TRY(launch_chunk_transpose(v, v_dtype, ws.vQ, nullptr, sv.vR, nullptr, B, T, D, s));
-        return launch_pair_forward(ws.qR, ws.kR, ws.vQ, g, sv.P, sv.Pt, fast, fast_dtype, resid, B, T, A, D, s);
+        return launch_pair_forward(ws.qR, ws.kR, ws.vQ, g, sv.P, sv.Pt, sv.Plo, fast, fast_dtype, resid, B, T, A, D, s);
     }
     if (path == PATH_CHUNKED) {
         const int nkg = la_kgroup_groups(A);
@@ -398,7 +400,7 @@ int fm_backward(const RSrc &r, const float *g, const float *w, const void *saved
     const size_t nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
     if (path == PATH_PAIR) {
         ULM_TRY(launch_chunk_transpose(dfast, dfast_dtype, ws.doQ, nullptr, ws.doR, nullptr, B, T, D, s));
-        ULM_TRY(launch_pair_backward(sv.vR, ws.doR, ws.doQ, sv.kQ, sv.qQ, sv.P, sv.Pt, g, ws.dS, ws.dSt, ws.dgx, ws.dqf,
+        ULM_TRY(launch_pair_backward(sv.vR, ws.doR, ws.doQ, sv.kQ, sv.qQ, sv.P, sv.Pt, sv.Plo, g, ws.dS, ws.dSt, ws.dgx, ws.dqf,
                                      ws.dkf, dv, dv_dtype, B, T, A, D, s));
         return launch_bwd_stats(ws.dqf, dq_out, r, sv.nck, w, g, ws.dkf, dr, dw, dg, ws.stats, B, T, A, s, dqw, dqw_dt,
                                 ws.dgx, pair_dscore_jobs(B, T));

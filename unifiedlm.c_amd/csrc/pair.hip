@@ -100,9 +100,11 @@ struct Args {
     // EPI_SCORES / EPI_DSCORES: bf16 output in the P layout
     uint16_t *pout;          // rows t, contraction s (the P layout)
     uint16_t *pout_t;        // the transpose: rows s, contraction t
+    uint16_t *pout_lo;       // EPI_SCORES: the bf16 residual P - bf16(P), P layout
     size_t p_bstride;
     uint32_t p_rt;
-    const uint16_t *pin;     // EPI_DSCORES: P, for the decay gradient
+    const uint16_t *pin;     // EPI_DSCORES: P and its residual, for the decay gradient
+    const uint16_t *pin_lo;
     double *dg_part;         // EPI_DSCORES: one sum per job
     // EPI_ROWS: (B, T, F) row-major output, rows = positions, columns = features
     void *out;
@@ -331,8 +333,12 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
         const float g = p.g[0];
         const rsrc_t rp = rsrc(reinterpret_cast<char *>(p.pout) + b * p.p_bstride, p.p_bstride);
         const rsrc_t rpt = rsrc(reinterpret_cast<char *>(p.pout_t) + b * p.p_bstride, p.p_bstride);
+        // DSCORES reads P and its residual; SCORES writes the residual
         const rsrc_t rpin = rsrc(EPI == EPI_DSCORES ? reinterpret_cast<const char *>(p.pin) + b * p.p_bstride
                                                     : reinterpret_cast<const char *>(p.pout), p.p_bstride);
+        const rsrc_t rplo = rsrc(EPI == EPI_DSCORES ? reinterpret_cast<const char *>(p.pin_lo) + b * p.p_bstride
+                                                    : reinterpret_cast<const char *>(p.pout_lo) + b * p.p_bstride,
+                                 p.p_bstride);
         float dg = 0.f;
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
@@ -352,9 +358,15 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
                         x[e] = ok ? acc[i][j][4 * r4 + e] * __expf(g * static_cast<float>(t - s)) : 0.f;
                     }
                     if constexpr (EPI == EPI_DSCORES) {
+                        // P to about 16 significant bits (bf16 value + bf16 residual):
+                        // the lag-weighted sum cancels heavily, and one bf16 rounding
+                        // of P alone moves it by about 1e-2
                         const v2u32_t pv = __builtin_amdgcn_raw_buffer_load_b64(rpin, off, 0, 0);
-                        const float pe[4] = {bf16_to_f32(pv[0] & 0xffffu), bf16_to_f32(pv[0] >> 16),
-                                             bf16_to_f32(pv[1] & 0xffffu), bf16_to_f32(pv[1] >> 16)};
+                        const v2u32_t pl = __builtin_amdgcn_raw_buffer_load_b64(rplo, off, 0, 0);
+                        const float pe[4] = {bf16_to_f32(pv[0] & 0xffffu) + bf16_to_f32(pl[0] & 0xffffu),
+                                             bf16_to_f32(pv[0] >> 16) + bf16_to_f32(pl[0] >> 16),
+                                             bf16_to_f32(pv[1] & 0xffffu) + bf16_to_f32(pl[1] & 0xffffu),
+                                             bf16_to_f32(pv[1] >> 16) + bf16_to_f32(pl[1] >> 16)};
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int s = s0 + e;
@@ -368,6 +380,15 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
                     v[0] = static_cast<uint32_t>(xb[0]) | (static_cast<uint32_t>(xb[1]) << 16);
                     v[1] = static_cast<uint32_t>(xb[2]) | (static_cast<uint32_t>(xb[3]) << 16);
                     __builtin_amdgcn_raw_buffer_store_b64(v, rp, off, 0, 0);
+                    if constexpr (EPI == EPI_SCORES) {
+                        uint16_t lb[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) lb[e] = f32_to_bf16_bits(x[e] - bf16_to_f32(xb[e]));
+                        v2u32_t vl;
+                        vl[0] = static_cast<uint32_t>(lb[0]) | (static_cast<uint32_t>(lb[1]) << 16);
+                        vl[1] = static_cast<uint32_t>(lb[2]) | (static_cast<uint32_t>(lb[3]) << 16);
+                        __builtin_amdgcn_raw_buffer_store_b64(vl, rplo, off, 0, 0);
+                    }
                     // the transpose: element (row s, contraction t), one 2-byte store
                     // each (the lanes of one s write 16-byte runs of t)
                     const uint32_t off_t = (t / 16) * TB + 16u * 32 * ((t % 16) / 8) + 2u * (t % 8);
@@ -522,12 +543,12 @@ double pair_flops_per_token(int B, int T, int A, int D) {
     return nb * (nb + 1) * G * G * 3.0 * (A + D) / T;
 }
 
-// P = scores(q, k) in the P layout (Tq x Tq per batch row) and its
-// transpose Pt, then out = P v (+ resid) in out_dt (B, T, D).
-// qR, kR: R layout (A); vQ: Q layout (D).
+// P = scores(q, k) in the P layout (Tq x Tq per batch row), its transpose
+// Pt and its bf16 residual Plo (P layout), then out = P v (+ resid) in out_dt
+// (B, T, D). qR, kR: R layout (A); vQ: Q layout (D).
 int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *vQ, const float *g, uint16_t *P,
-                        uint16_t *Pt, void *out, int out_dt, const float *resid, int B, int T, int A, int D,
-                        hipStream_t s) {
+                        uint16_t *Pt, uint16_t *Plo, void *out, int out_dt, const float *resid, int B, int T, int A,
+                        int D, hipStream_t s) {
     using namespace pair;
     const int G = pair_block(B, T), Tq = pair_tq(B, T), NT = (T + 63) / 64;
     Args a{};
@@ -542,6 +563,7 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *
     const Mat pm = p_mat(P, Tq);
     a.pout = P;
     a.pout_t = Pt;
+    a.pout_lo = Plo;
     a.p_bstride = pm.bstride;
     a.p_rt = pm.rt;
     ULM_TRY((launch<false, EPI_SCORES>(a, G, B, s)));
@@ -566,9 +588,10 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *
 // pair part of the decay gradient into dg_part (pair_dscore_jobs doubles),
 // dq_f = dS k, dk_f = dS^T q (fp32 (B, T, A)), dv = P^T dfast in dv_dt (B, T, D).
 // vR, doR: R layout (D); kQ, qQ: Q layout (A); doQ: Q layout (D); P and Pt from
-// the forward.
+// the forward (Plo: P's residual, for the decay gradient).
 int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t *doQ, const uint16_t *kQ,
-                         const uint16_t *qQ, const uint16_t *P, const uint16_t *Pt, const float *g, uint16_t *dS,
+                         const uint16_t *qQ, const uint16_t *P, const uint16_t *Pt, const uint16_t *Plo,
+                         const float *g, uint16_t *dS,
                          uint16_t *dSt, double *dg_part, float *dqf, float *dkf, void *dv, int dv_dt, int B, int T,
                          int A, int D, hipStream_t s) {
     using namespace pair;
@@ -588,6 +611,7 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
     a.p_bstride = sm.bstride;
     a.p_rt = sm.rt;
     a.pin = P;
+    a.pin_lo = Plo;
     a.dg_part = dg_part;
     ULM_TRY((launch<false, EPI_DSCORES>(a, G, B, s)));
     Args r{};

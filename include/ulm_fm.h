@@ -45,14 +45,16 @@ int ulm_abi_version(void);
 const char *ulm_last_error(void);
 
 /* Which evaluation of the products ulm_fm_fwd / ulm_fm_bwd and the block
- * entries use at this shape: 0 the generic kernel (A or D not a multiple of
- * 32), 1 the chunked state form (`_la`'s algorithm, the K-group kernel), 2 the
- * block-pair form (the same sums over pairs of 128-position blocks, six tile
- * GEMMs), whichever needs fewer flops: about 4 A D per token and product for
- * the first, T (A + D) / 2 for the second. The environment variable
- * ULM_FM_PATH=chunked or =pair forces one of them for aligned shapes; it must
- * not change between a forward and its backward. -1 for invalid sizes. No
- * counterpart in the reference (one algorithm, kernel.py:183-196). */
+ * entries use at this shape: 1 the chunked state form (`_la`'s algorithm, the
+ * K-group kernel; A and D multiples of 32), 2 the block-pair form (the same
+ * sums over pairs of 128-position blocks, six tile GEMMs; T <= 4096, any A and
+ * D on zero-padded tiles), whichever needs fewer flops where both apply: about
+ * 4 A D per token and product for the first, T (A + D) / 2 for the second;
+ * 0 the generic kernel (widths off the 32 grid past 4096 positions). The
+ * environment variable ULM_FM_PATH=chunked, =pair or =generic forces one of
+ * them where it applies; it must not change between a forward and its
+ * backward. -1 for invalid sizes. No counterpart in the reference (one
+ * algorithm, kernel.py:183-196). */
 int ulm_fm_path(int B, int T, int A, int D);
 
 /* ------------------------------------------------------------------------
@@ -70,9 +72,11 @@ int ulm_fm_path(int B, int T, int A, int D);
  *   fast   (B,T,D) fast_dtype out  (v.dtype in the reference, kernel.py:211)
  *   saved  ulm_fm_saved_bytes() bytes, out: what the backward needs besides
  *          r, g and w (the reference saves v16, q, c, q16, k16, kernel.py:212;
- *          this holds the bf16 operand tiles of q, k and v, the score tiles
- *          of the dv product and the evidence n at every chunk start in place
- *          of c). Opaque; pass it unchanged to ulm_fm_bwd.
+ *          this holds bf16 operand tiles of q, k and v, the evidence n at
+ *          every chunk start in place of c, and, by the evaluation
+ *          ulm_fm_path chooses, the bf16 scores P (with their transpose and
+ *          bf16 residual) of the block-pair form or the dv product's score
+ *          tiles of the chunked form). Opaque; pass it unchanged to ulm_fm_bwd.
  */
 size_t ulm_fm_saved_bytes(int B, int T, int A, int D, int v_dtype);
 size_t ulm_fm_fwd_workspace_bytes(int B, int T, int A, int D, int fast_dtype);
@@ -91,7 +95,7 @@ int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const float *g, const
  *   c_last (B,A)   fp32 out: w + sum_{s<T} lam^(T-1-s) k_s, the decode c
  *   r, v, g, w, q, fast as for ulm_fm_fwd; workspace of
  *   ulm_fm_prefill_workspace_bytes() bytes (0: unsupported shape).
- * A and D must be multiples of 32. */
+ * Any A and D (widths off the 32 grid run on zero-padded tiles). */
 size_t ulm_fm_prefill_workspace_bytes(int B, int T, int A, int D, int v_dtype, int fast_dtype);
 int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const float *g, const float *w,
                    float *q, void *fast, int fast_dtype, float *S, float *c_last,
@@ -110,7 +114,8 @@ int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const float *g, c
  *   dv      (B,T,D) dv_dtype out (dfast.dtype in the reference, kernel.py:223)
  *   dg      (1,)    fp32  out    d loss / d g
  *   dw      (A,)    fp32  out
- * dg and dw are reduced deterministically (no atomics). */
+ * Every output is reduced in a fixed order (no atomics): repeated calls agree
+ * bit for bit. */
 size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D, int dfast_dtype);
 int ulm_fm_bwd(const float *r, const float *g, const float *w,
                const void *saved, size_t saved_bytes, int v_dtype,
@@ -122,7 +127,9 @@ int ulm_fm_bwd(const float *r, const float *g, const float *w,
  * (s >= t when reverse != 0). Replaces `_la` (kernel.py:183-196) with the
  * chunk state kept in fp32 on chip. a, b (B,T,K) bf16; c (B,T,V) bf16;
  * out (B,T,V) fp32, overwritten. split != 0 carries the decayed state-update
- * operand as a bf16 hi + lo pair (used by the backward's dq and dk). */
+ * operand as a bf16 hi + lo pair (used by the backward's dq and dk). K or V
+ * off the 32 grid run the generic kernel, whose key tiles' partial outputs
+ * (workspace) are summed in a fixed order. */
 size_t ulm_la_workspace_bytes(int B, int T, int K, int V);
 int ulm_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out,
            int B, int T, int K, int V, int reverse, int split,

@@ -52,7 +52,8 @@ def test_workspace_sizes(monkeypatch):
     # at the 110M shape the block-pair form needs fewer flops than the chunked state form
     assert lib.ulm_fm_path(B, T, A, D) == 2
     assert lib.ulm_fm_path(B, 8192, A, D) == 1            # past 4096 positions: the state form
-    assert lib.ulm_fm_path(2, 70, 12, 8) == 0             # widths off the 32 grid: the generic kernel
+    assert lib.ulm_fm_path(2, 70, 12, 8) == 2             # widths off the 32 grid: padded pair tiles
+    assert lib.ulm_fm_path(2, 5000, 12, 8) == 0           # ... past 4096 positions: the generic kernel
     # pair form, saved: bf16 q, k (Q layout), v (R layout), the scores P, their
     # transpose and their bf16 residual (Tq x Tq per row), n checkpoints
     Tq = (T + 127) // 128 * 128
@@ -75,9 +76,11 @@ def test_workspace_sizes(monkeypatch):
     assert lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * (8 * A + 4 * D) + B * NT * A * 4
     assert (lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_F32)
             - lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_BF16)) == 2 * B * T * D * 2
-    # unaligned sizes keep only natural bf16 copies of q, k, v and the checkpoints
-    assert lib.ulm_fm_saved_bytes(2, 70, 12, 8, nat.ULM_F32) >= 2 * 70 * (12 * 4 + 8 * 2) + 2 * 2 * 12 * 4
+    # the generic kernel keeps natural bf16 copies of q, k, v and the checkpoints
+    assert lib.ulm_fm_saved_bytes(2, 5000, 12, 8, nat.ULM_F32) >= 2 * 5000 * (12 * 4 + 8 * 2) + 2 * 79 * 12 * 4
+    # its bare product needs partial planes only past one 128-key tile
     assert lib.ulm_la_workspace_bytes(2, 70, 12, 8) == 0
+    assert lib.ulm_la_workspace_bytes(2, 70, 300, 8) == 3 * 2 * 70 * 8 * 4
     assert lib.ulm_la_workspace_bytes(B, T, A, D) >= 3 * B * NT * A * 64 * 2 + 4 * B * T * D * 4
     assert lib.ulm_addr_bwd_workspace_bytes(B * T, A) >= A * 4
     assert lib.ulm_fm_bwd_workspace_bytes(0, T, A, D, nat.ULM_F32) == 0

@@ -125,9 +125,10 @@ BLOCK_CASES = [
     (1, 1024, 512, 2048, True),   # 42M block shape, one row of 1024 positions
     (1, 1024, 512, 2048, False),
     (3, 1, 64, 64, False),        # a single position
-    # D not a multiple of 32 (generic products), 3 key groups, ragged chunk
+    # D not a multiple of 32 (zero-padded features in the block-pair products), ragged chunk
     (2, 130, 100, 1600, False),
     (2, 130, 100, 1600, True),
+    (2, 256, 288, 712, True),     # the reference's 15M model widths (docs/models.md:11), A off the 32 grid
 ]
 
 
@@ -262,23 +263,28 @@ def test_fused_model_is_causal_and_finite(autocast):
         assert p.grad is not None and torch.isfinite(p.grad).all(), name
 
 
-def test_native_reductions_are_deterministic():
-    """The fast-memory backward (dg, dw), the split-K weight gradient and the
-    norm/conv weight gradients sum in a fixed order: repeated calls agree
-    bit for bit."""
+@pytest.mark.parametrize("path", ["chunked", "pair", "generic"])
+def test_native_reductions_are_deterministic(path, monkeypatch):
+    """The fast-memory operator (every output and gradient), the split-K
+    weight gradient and the norm/conv weight gradients sum in a fixed order:
+    repeated calls agree bit for bit, on every evaluation of the products and
+    at the reference test's widths (A=140, D=64)."""
     import kernel
     from helpers import fm_inputs
-    say("determinism of ulm_fm_bwd, ulm_wgrad, ulm_norm_conv_bwd")
-    r, v, g, w = fm_inputs(2, 256, 256, 128, seed=5, device="cuda")
-    r, v, g, w = (t.float().requires_grad_() for t in (r, v, g, w))
+    say(f"determinism of ulm_fm_bwd ({path}), ulm_wgrad, ulm_norm_conv_bwd")
+    monkeypatch.setenv("ULM_FM_PATH", path)
     gen = torch.Generator(device="cuda").manual_seed(5)
-    dq, df = torch.randn(2, 256, 256, device="cuda", generator=gen), torch.randn(2, 256, 128, device="cuda", generator=gen)
-    grads = []
-    for _ in range(2):
-        q, fast = kernel.unified_memory(r, v, g, w)
-        grads.append(torch.autograd.grad((q, fast), (r, v, g, w), (dq, df)))
-    for a_, b_ in zip(*grads):
-        assert torch.equal(a_, b_)
+    shapes = [(2, 256, 256, 128)] + ([(2, 200, 140, 64)] if path != "chunked" else [])
+    for B, T, A, D in shapes:
+        r, v, g, w = fm_inputs(B, T, A, D, seed=5, device="cuda")
+        r, v, g, w = (t.float().requires_grad_() for t in (r, v, g, w))
+        dq, df = torch.randn(B, T, A, device="cuda", generator=gen), torch.randn(B, T, D, device="cuda", generator=gen)
+        grads = []
+        for _ in range(2):
+            q, fast = kernel.unified_memory(r, v, g, w)
+            grads.append((q, fast) + torch.autograd.grad((q, fast), (r, v, g, w), (dq, df)))
+        for a_, b_ in zip(*grads):
+            assert torch.equal(a_, b_), (B, T, A, D)
     a = torch.randn(4096, 256, device="cuda", generator=gen).to(torch.bfloat16)
     b = torch.randn(4096, 512, device="cuda", generator=gen).to(torch.bfloat16)
     c1, c2 = kernel._wgrad(a, b), kernel._wgrad(a, b)

@@ -15,6 +15,7 @@ from oracle import fastmem as fm
 pytestmark = pytest.mark.gpu
 
 import kernel  # noqa: E402
+import ulm_native as nat  # noqa: E402
 
 
 def test_mfma_operand_layout():
@@ -47,6 +48,9 @@ LA_CASES = [
     (2, 300, 64, 128, True, 0.5, True),
     (1, 128, 32, 32, False, 0.99, False),
     (1, 1024, 768, 192, True, 0.953, True),
+    # widths off the 32 grid: the generic kernel, three key tiles summed in order
+    (2, 130, 300, 70, False, 0.93, False),
+    (2, 130, 300, 70, True, 0.93, False),
 ]
 
 
@@ -78,6 +82,10 @@ OP_CASES = [
     (8, 512, 128, 64, torch.float32),      # 260K-shape block (all 8 rows of 512 positions)
     (1, 1024, 2048, 512, torch.bfloat16),  # 42M-shape block, one row
     (1, 1024, 3072, 768, torch.float32),   # 110M-shape block, one row of 1024 positions, fp32 v
+    # the reference's model widths (hidden_dim 712 and 1912, docs/models.md:11): slots off the 32 grid,
+    # padded with zero slots in the block-pair products
+    (2, 256, 712, 288, torch.bfloat16),
+    (1, 512, 1912, 768, torch.bfloat16),
 ]
 
 
@@ -115,12 +123,22 @@ def test_unified_memory_matches_oracle(B, T, A, D, vdt):
     assert max(errs.values()) < 1e-2, errs
 
 
-@pytest.mark.parametrize("path", ["chunked", "pair"])
-@pytest.mark.parametrize("B,T,A,D", [(2, 200, 128, 64), (2, 130, 96, 160), (1, 512, 3072, 768)])
+PATH_CASES = [
+    # B, T, A, D, path
+    *[(*shape, path) for shape in [(2, 200, 128, 64), (2, 130, 96, 160), (1, 512, 3072, 768)]
+      for path in ("chunked", "pair", "generic")],
+    # widths off the 32 grid: the block-pair form on padded tiles, or the generic kernel
+    *[(*shape, path) for shape in [(2, 200, 140, 64), (2, 100, 100, 36)] for path in ("pair", "generic")],
+]
+
+
+@pytest.mark.parametrize("B,T,A,D,path", PATH_CASES)
 def test_unified_memory_paths(B, T, A, D, path, monkeypatch):
-    """Both evaluations of the aligned products, forced by ULM_FM_PATH: the
-    chunked state form and the block-pair form, each against the oracle."""
+    """Every evaluation of the products, forced by ULM_FM_PATH (the chunked
+    state form needs A, D multiples of 32), each against the oracle."""
     monkeypatch.setenv("ULM_FM_PATH", path)
+    code = {"generic": 0, "chunked": 1, "pair": 2}[path]
+    assert nat.lib().ulm_fm_path(B, T, A, D) == code
     test_unified_memory_matches_oracle(B, T, A, D, torch.bfloat16)
 
 

@@ -23,6 +23,10 @@ PREFILL_CASES = [
     (2, 300, 64, 128, 0.5, torch.float32),      # lam^64 below 2^-40
     (1, 600, 1600, 64, 0.93, torch.bfloat16),   # 3 key groups; the state scale renormalises
     (1, 512, 3072, 768, None, torch.bfloat16),  # 110M block shape
+    # widths off the 32 grid (zero-padded tiles): the reference test's and 15M model's widths, both ragged
+    (2, 200, 140, 64, 0.93, torch.float32),
+    (1, 300, 712, 288, None, torch.bfloat16),
+    (2, 130, 100, 36, 0.93, torch.float32),
 ]
 
 
@@ -53,9 +57,10 @@ def _oracle_states(p, tokens, n_layers):
     return states
 
 
-def test_model_prefill_then_step_matches_recurrent():
-    say("UnifiedLM.prefill of 50 positions, then 20 steps, vs the oracle's forward_recurrent")
-    kw = dict(dim=32, n_layers=3, hidden_dim=64, vocab_size=97, max_seq_len=80)
+@pytest.mark.parametrize("dim,hidden", [(32, 64), (64, 140)])
+def test_model_prefill_then_step_matches_recurrent(dim, hidden):
+    say(f"UnifiedLM.prefill of 50 positions, then 20 steps, vs the oracle's forward_recurrent, dim={dim} A={hidden}")
+    kw = dict(dim=dim, n_layers=3, hidden_dim=hidden, vocab_size=97, max_seq_len=80)
     model = tiny_model(**kw).cuda()
     x = torch.randint(0, 97, (3, 70), generator=torch.Generator().manual_seed(2))
     T0 = 50

@@ -18,9 +18,10 @@
 // H[k0:k0+128, v0:v0+256] of one batch row; wave w owns columns v0+64w ..
 // v0+64w+63, i.e. 4x2 MFMA accumulator tiles of 32x32 fp32 (128 registers
 // per lane). The contraction over K is split across workgroups, so each
-// workgroup's O is a partial sum, added to `out` with fp32 atomics; P is
-// likewise the partial score over the workgroup's 128 keys (P c is linear in
-// P, so the partial products sum to the full one).
+// workgroup's O is a partial sum over its 128 keys, stored to that key tile's
+// own partial plane and summed over the planes in a fixed order afterwards
+// (deterministic); P is likewise the partial score over the workgroup's keys
+// (P c is linear in P, so the partial products sum to the full one).
 //
 // MFMA: v_mfma_f32_32x32x16_bf16 (gfx950). Operand layouts, lane l,
 // lr = l % 32, lh = l / 32:  A: A[lr][8 lh + e];  B: B[8 lh + e][lr];
@@ -95,7 +96,7 @@ __device__ __forceinline__ int time_pos(int t, int T) { return REV ? T - 1 - t :
 template <bool REV, bool VEC>
 __global__ __launch_bounds__(kThreads, 1) void la_kernel(const uint16_t *__restrict__ A_, const uint16_t *__restrict__ B_,
                                                          const uint16_t *__restrict__ C_, const float *__restrict__ g,
-                                                         float *__restrict__ out, int T, int K, int V, int NT, int nK,
+                                                         float *__restrict__ out, size_t plane, int T, int K, int V, int NT, int nK,
                                                          int nV, int total) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     LaSmem &sm = *reinterpret_cast<LaSmem *>(smem_raw);
@@ -109,6 +110,7 @@ __global__ __launch_bounds__(kThreads, 1) void la_kernel(const uint16_t *__restr
     const int kt = (tile / nV) % nK;
     const int bb = tile / (nV * nK);
     const int k0 = kt * KT, v0 = vt * VT;
+    out += kt * plane;   // this key tile's partial plane (B, T, V)
 
     const int tid = threadIdx.x;
     const int wave = tid / kWave, lane = tid % kWave;
@@ -283,7 +285,8 @@ __global__ __launch_bounds__(kThreads, 1) void la_kernel(const uint16_t *__restr
                 for (int nt = 0; nt < 2; ++nt) O[mt][nt] = mfma(pp, cop[nt][ks], O[mt][nt]);
             }
 
-        // ---- accumulate the partial output
+        // ---- store the partial output (every position and column of the
+        // plane is written by exactly one workgroup, once)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
             const int col = v0 + wcol + 32 * nt + lr;
@@ -293,7 +296,7 @@ __global__ __launch_bounds__(kThreads, 1) void la_kernel(const uint16_t *__restr
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int t = n * C + 32 * mt + 8 * (r / 4) + 4 * lh + (r % 4);
-                        if (t < T) unsafeAtomicAdd(out + (rowA + time_pos<REV>(t, T)) * V + col, O[mt][nt][r]);
+                        if (t < T) out[(rowA + time_pos<REV>(t, T)) * V + col] = O[mt][nt][r];
                     }
             }
         }
@@ -346,11 +349,23 @@ int la_timer_end(hipStream_t s) {
     return ULM_OK;
 }
 
-// Generic chunked kernel, any K and V: out += o (fp32 atomics; the caller zeroes out).
-int launch_la_generic(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B,
-                      int T, int K, int V, bool reverse, hipStream_t s) {
+int launch_partial_reduce(const float *part, int nK, size_t n, void *out, int odt, hipStream_t s,
+                          const float *resid);
+
+// Key tiles of the generic kernel: the partial planes launch_la_generic needs.
+int la_generic_parts(int K) { return (K + KT - 1) / KT; }
+
+// Generic chunked kernel, any K and V: out (B, T, V) fp32 = o, fully written.
+// With more than one key tile (la_generic_parts(K) > 1) the tiles' partial
+// outputs go to part (la_generic_parts(K) x B x T x V fp32) and are summed
+// into out in tile order.
+int launch_la_generic(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, float *part,
+                      int B, int T, int K, int V, bool reverse, hipStream_t s) {
     const int NT = (T + C - 1) / C;
     const int nK = (K + KT - 1) / KT, nV = (V + VT - 1) / VT;
+    if (nK > 1 && !part) return fail(ULM_ERR_INVALID, "chunked kernel: %d key tiles need a partial buffer", nK);
+    const size_t plane = static_cast<size_t>(B) * T * V;
+    float *dst = nK > 1 ? part : out;
     const long long total = static_cast<long long>(B) * nK * nV;
     if (total > 0x7fffffffLL) return fail(ULM_ERR_UNSUPPORTED, "chunked kernel: grid of %lld workgroups", total);
     const bool vec = (K % 8 == 0) && (V % 8 == 0);
@@ -374,15 +389,17 @@ int launch_la_generic(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
     int st = la_timer_begin(s);
     if (st) return st;
     if (reverse) {
-        if (vec) la_kernel<true, true><<<grid, kThreads, lds, s>>>(a, b, c, g, out, T, K, V, NT, nK, nV, tot);
-        else la_kernel<true, false><<<grid, kThreads, lds, s>>>(a, b, c, g, out, T, K, V, NT, nK, nV, tot);
+        if (vec) la_kernel<true, true><<<grid, kThreads, lds, s>>>(a, b, c, g, dst, plane, T, K, V, NT, nK, nV, tot);
+        else la_kernel<true, false><<<grid, kThreads, lds, s>>>(a, b, c, g, dst, plane, T, K, V, NT, nK, nV, tot);
     } else {
-        if (vec) la_kernel<false, true><<<grid, kThreads, lds, s>>>(a, b, c, g, out, T, K, V, NT, nK, nV, tot);
-        else la_kernel<false, false><<<grid, kThreads, lds, s>>>(a, b, c, g, out, T, K, V, NT, nK, nV, tot);
+        if (vec) la_kernel<false, true><<<grid, kThreads, lds, s>>>(a, b, c, g, dst, plane, T, K, V, NT, nK, nV, tot);
+        else la_kernel<false, false><<<grid, kThreads, lds, s>>>(a, b, c, g, dst, plane, T, K, V, NT, nK, nV, tot);
     }
     st = check_launch("la_kernel");
     if (st) return st;
-    return la_timer_end(s);
+    st = la_timer_end(s);
+    if (st || nK == 1) return st;
+    return launch_partial_reduce(part, nK, plane, out, ULM_F32, s, nullptr);
 }
 
 // ---- layout probe: one wave, D (32x32) = A (32x16) B (16x32) through the

@@ -27,26 +27,28 @@ namespace chunks {
 
 constexpr int C = ULM_CHUNK;
 
-// grid (ceil(X/64), NT, B), 256 threads: one 64-position x 64-feature block of
-// X (B, T, X) in any float dtype (X % 32 == 0). Outputs, each optional: raw =
-// bf16(x) (+ raw_lo = bf16(x - raw), the rounding remainder) in the Q layout;
-// xr = bf16(x) (+ xr_lo) in the R layout.
+// grid (ceil(XL/64), NT, B), 256 threads: one 64-position x 64-feature block of
+// X (B, T, X) in any float dtype, into layouts XL features wide (XL % 32 == 0,
+// X <= XL; features X .. XL-1 are written as zeros). Outputs, each optional:
+// raw = bf16(x) (+ raw_lo = bf16(x - raw), the rounding remainder) in the Q
+// layout; xr = bf16(x) (+ xr_lo) in the R layout.
 __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__ src, int sdt, uint16_t *__restrict__ raw,
                                                         uint16_t *__restrict__ raw_lo, uint16_t *__restrict__ xr,
-                                                        uint16_t *__restrict__ xr_lo, int T, int X, int NT) {
+                                                        uint16_t *__restrict__ xr_lo, int T, int X, int XL, int NT) {
     __shared__ float tile[C][C + 1];   // [position][feature]
     const int x0 = blockIdx.x * C, n = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
     {
-        // position row i, 16 contiguous features (X % 16 == 0: wholly in or out)
+        // position row i, 16 contiguous features; with X % 16 == 0 and a
+        // 16-byte aligned source they are wholly in or out and 16-byte aligned
         const int i = tid / 4, c0 = (tid % 4) * 16;
         const int t = n * C + i;
         float vals[16];
-        const bool vec = reinterpret_cast<uintptr_t>(src) % 16 == 0;   // 16-byte loads (else one element at a time)
+        const bool vec = reinterpret_cast<uintptr_t>(src) % 16 == 0 && X % 16 == 0;   // else one element at a time
         if (t < T && x0 + c0 < X && !vec) {
             const size_t o = (static_cast<size_t>(b) * T + t) * X + x0 + c0;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) vals[e] = load_as_f32(src, o + e, sdt);
+            for (int e = 0; e < 16; ++e) vals[e] = x0 + c0 + e < X ? load_as_f32(src, o + e, sdt) : 0.f;
         } else if (t < T && x0 + c0 < X) {
             const size_t o = (static_cast<size_t>(b) * T + t) * X + x0 + c0;
             if (sdt == ULM_F32) {
@@ -89,7 +91,7 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__
     if (xr) {
         // R layout: 64 positions x 64 features are 8 tiles; thread -> 2 lanes of one tile
         const int tl = tid / 32, mt = tl / 4, tf4 = tl % 4;
-        if (x0 + 16 * tf4 < X) {
+        if (x0 + 16 * tf4 < XL) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int l = 2 * (tid % 32) + u, row = 32 * mt + l % 32, col = 16 * tf4 + 8 * (l / 32);
@@ -102,7 +104,7 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__
                     wl[e] = static_cast<uint32_t>(f32_to_bf16_bits(v0 - bf16_to_f32(h0))) |
                             (static_cast<uint32_t>(f32_to_bf16_bits(v1 - bf16_to_f32(h1))) << 16);
                 }
-                const size_t o = r_index(b, n * C + row, x0 + col, NT, X);
+                const size_t o = r_index(b, n * C + row, x0 + col, NT, XL);
                 *reinterpret_cast<uint4 *>(xr + o) = make_uint4(wh[0], wh[1], wh[2], wh[3]);
                 if (xr_lo) *reinterpret_cast<uint4 *>(xr_lo + o) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
             }
@@ -111,7 +113,7 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__
     // Q layouts: feature xl, positions i0 .. i0+15 = two lanes' 16 bytes
     const int xl = tid / 4, i0 = (tid % 4) * 16;
     const int x = x0 + xl;
-    if (x >= X) return;
+    if (x >= XL) return;
     if (raw) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__
                 wl[e] = static_cast<uint32_t>(f32_to_bf16_bits(v0 - bf16_to_f32(h0))) |
                         (static_cast<uint32_t>(f32_to_bf16_bits(v1 - bf16_to_f32(h1))) << 16);
             }
-            const size_t o = q_index(b, n * C + i0 + 8 * h, x, NT, X);
+            const size_t o = q_index(b, n * C + i0 + 8 * h, x, NT, XL);
             *reinterpret_cast<uint4 *>(raw + o) = make_uint4(wh[0], wh[1], wh[2], wh[3]);
             if (raw_lo) *reinterpret_cast<uint4 *>(raw_lo + o) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
         }
@@ -284,18 +286,38 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(const float *__rest
     }
 }
 
+// The padded-width form of partial_reduce: part holds nK partial (B, Rp, Fp)
+// arrays; out (B, R, F) takes, for r < R and f < F, sum_k part[k][b][r][f]
+// (+ resid[b][r][f]) in out's dtype. The padding rows and columns are dropped.
+__global__ __launch_bounds__(256) void unpad_sum_kernel(const float *__restrict__ part, int nK, int R, int Rp, int F,
+                                                        int Fp, size_t n, const float *__restrict__ resid,
+                                                        void *__restrict__ out, int odt) {
+    const size_t kstride = n / (static_cast<size_t>(R) * F) * Rp * Fp;   // B Rp Fp
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const size_t row = i / F;
+        const int f = static_cast<int>(i % F);
+        const size_t src = (row / R * Rp + row % R) * Fp + f;
+        float s = part[src] + (resid ? resid[i] : 0.f);
+        for (int k = 1; k < nK; ++k) s += part[k * kstride + src];
+        store_from_f32(out, i, odt, s);
+    }
+}
+
 }  // namespace chunks
 
 // Tiled copies of X (B, T, X): raw (+ raw_lo) in the Q layout and xr (+ xr_lo)
-// in the R layout, each bf16 or null (X % 32 == 0).
+// in the R layout, each bf16 or null, XL features wide (0: XL = X; XL % 32 ==
+// 0 and X <= XL, the features past X zero).
 int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t *raw_lo, uint16_t *xr,
-                           uint16_t *xr_lo, int B, int T, int X, hipStream_t s) {
-    if (X % 32) return fail(ULM_ERR_INVALID, "chunk transpose: X=%d is not a multiple of 32", X);
+                           uint16_t *xr_lo, int B, int T, int X, hipStream_t s, int XL) {
+    if (XL == 0) XL = X;
+    if (XL % 32 || X > XL) return fail(ULM_ERR_INVALID, "chunk transpose: layout width %d for X=%d", XL, X);
     if (raw_lo && !raw) return fail(ULM_ERR_INVALID, "chunk transpose: raw_lo needs raw");
     if (xr_lo && !xr) return fail(ULM_ERR_INVALID, "chunk transpose: xr_lo needs xr");
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
-    const dim3 grid((X + ULM_CHUNK - 1) / ULM_CHUNK, NT, B);
-    chunks::transpose_kernel<<<grid, 256, 0, s>>>(src, src_dt, raw, raw_lo, xr, xr_lo, T, X, NT);
+    const dim3 grid((XL + ULM_CHUNK - 1) / ULM_CHUNK, NT, B);
+    chunks::transpose_kernel<<<grid, 256, 0, s>>>(src, src_dt, raw, raw_lo, xr, xr_lo, T, X, XL, NT);
     return check_launch("chunk transpose_kernel");
 }
 
@@ -312,6 +334,19 @@ int launch_chunk_scores(const uint16_t *aR, const uint16_t *aL, const uint16_t *
     else if (bL) chunks::scores_kernel<false, true><<<grid, nthreads, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT, scaled ? 1 : 0);
     else chunks::scores_kernel<false, false><<<grid, nthreads, 0, s>>>(aR, aL, bR, bL, g, Plo, Pup, K, NT, scaled ? 1 : 0);
     return check_launch("chunk scores_kernel");
+}
+
+// out (B, R, F) = the sum of nK partial (B, Rp, Fp) arrays (+ resid (B, R, F)
+// when not null) without their padding, as odt.
+int launch_unpad_sum(const float *part, int nK, int B, int R, int Rp, int F, int Fp, void *out, int odt, hipStream_t s,
+                     const float *resid) {
+    if (R > Rp || F > Fp) return fail(ULM_ERR_INVALID, "unpad sum: %dx%d from %dx%d", R, F, Rp, Fp);
+    const size_t n = static_cast<size_t>(B) * R * F;
+    if (n == 0) return ULM_OK;
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    chunks::unpad_sum_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(part, nK, R, Rp, F, Fp, n, resid, out, odt);
+    return check_launch("unpad_sum_kernel");
 }
 
 // out = sum of the nK partial rows of part (+ resid when not null), as odt.

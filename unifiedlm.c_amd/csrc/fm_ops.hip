@@ -2,36 +2,47 @@
 // C ABI (UnifiedMemory.forward / backward, kernel.py:202-233) and the bare
 // chunked product ulm_la (`_la`, kernel.py:183-196).
 //
-// The four chunked products follow the role table of docs/kernel.md:22-27:
+// The four products follow the role table of docs/kernel.md:22-27:
 //   fast = LA(q, k, v)          dq_f = LA(dfast, v, k)
 //   dk_f = LA_rev(v, dfast, q)  dv   = LA_rev(k, q, dfast)
-// For aligned shapes (A and D multiples of 32) they run on the K-group kernel
-// (la_kgroup.hip), whose operands are the tiled copies of ulm_common.h: the
-// read-out operand a in the R layout, the update operands and the raw c of the
-// intra-chunk product in the Q layout, the intra-chunk matrices from
-// chunk_scores. The reversed products walk the forward chunks backwards, so one
-// tiled copy per tensor serves both directions and the score tiles pair up:
-// P_dv = P_fwd^T, P_dk = P_dq^T. The decay of the state update is applied in
-// the kernel to c, the value operand. The products behind the d/dg identity
-// (dq and dk) add the bf16 rounding remainder of the decayed c as a second
-// update pass. When v or dfast arrive in fp32 (or fp16), every operand made
-// from them is also carried as bf16 hi + lo, so both sides of the identity see
-// the same full-precision v and dfast (the bf16 rounding of either one alone
-// breaks the cancellation).
-// The forward keeps what the backward needs in one "saved" buffer:
-//   qR, kR, qQ, kQ (B, NT, 64 A) bf16 tiles; vR, vQ (+ their remainders)
-//   (B, NT, 64 D); P_dv (B, NT, 64, 64) bf16 tiles; n_ckpt (B, NT, A) fp32.
-// Other shapes use the generic kernel of fm_chunk.hip (atomics into zeroed
-// fp32 outputs) on natural bf16 copies of q, k and v.
+// and are evaluated in one of three forms (train_path below):
+//  * block-pair form (pair.hip), sequences up to 4096 positions: the scores
+//    P = (q k^T) o decay and dS = (dfast v^T) o decay as tile GEMMs, the
+//    products as GEMMs over them, the decay gradient's pair part summed over
+//    the (t, s) pairs. Saved: qQ, kQ (Q layout), vR (R layout), P, its
+//    transpose and its bf16 residual, n_ckpt.
+//  * chunked state form (la_kgroup.hip), A and D multiples of 32: operands are
+//    the tiled copies of ulm_common.h, the read-out operand a in the R layout,
+//    the update operands and the raw c of the intra-chunk product in the Q
+//    layout, the intra-chunk matrices from chunk_scores. The reversed products
+//    walk the forward chunks backwards, so one tiled copy per tensor serves
+//    both directions and the score tiles pair up: P_dv = P_fwd^T, P_dk =
+//    P_dq^T. The decay of the state update is applied in the kernel to c, the
+//    value operand. The products behind the d/dg identity (dq and dk) add the
+//    bf16 rounding remainder of the decayed c as a second update pass. When v
+//    or dfast arrive in fp32 (or fp16), every operand made from them is also
+//    carried as bf16 hi + lo, so both sides of the identity see the same
+//    full-precision v and dfast. Saved: qR, kR, qQ, kQ (B, NT, 64 A) bf16
+//    tiles; vR, vQ (+ their remainders) (B, NT, 64 D); P_dv (B, NT, 64, 64)
+//    bf16 tiles; n_ckpt (B, NT, A) fp32.
+//  * generic kernel (fm_chunk.hip), any widths, on natural bf16 copies of q,
+//    k and v: the widths off the 32 grid past 4096 positions.
+// The tiled copies are pad32(A) slots and pad32(D) features wide, the padding
+// zero, so widths off the 32 grid run the pair form (and the chunked prefill)
+// exactly. Every reduction runs in a fixed order: results are bitwise
+// reproducible.
 #include "ulm_common.h"
 
 #include <stdlib.h>
 
+#include <algorithm>
+
 namespace ulm {
 
 // fm_chunk.hip
-int launch_la_generic(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, int B,
-                      int T, int K, int V, bool reverse, hipStream_t s);
+int la_generic_parts(int K);
+int launch_la_generic(const uint16_t *a, const uint16_t *b, const uint16_t *c, const float *g, float *out, float *part,
+                      int B, int T, int K, int V, bool reverse, hipStream_t s);
 // la_kgroup.hip
 int la_kgroup_groups(int K);
 bool la_kgroup_supported(int B, int T, int K, int V);
@@ -40,15 +51,17 @@ int launch_la_kgroup(const uint16_t *a, const uint16_t *alo, const uint16_t *ua,
                      float *out, float *state, int B, int T, int K, int V, bool reverse, bool ubsplit, hipStream_t s);
 // fm_chunks.hip
 int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t *raw_lo, uint16_t *xr,
-                           uint16_t *xr_lo, int B, int T, int X, hipStream_t s);
+                           uint16_t *xr_lo, int B, int T, int X, hipStream_t s, int XL = 0);
 int launch_chunk_scores(const uint16_t *aR, const uint16_t *aL, const uint16_t *bR, const uint16_t *bL, const float *g,
                         uint16_t *Plo, uint16_t *Pup, int B, int T, int K, bool scaled, hipStream_t s);
 int launch_partial_reduce(const float *part, int nK, size_t n, void *out, int odt, hipStream_t s,
                           const float *resid = nullptr);
+int launch_unpad_sum(const float *part, int nK, int B, int R, int Rp, int F, int Fp, void *out, int odt, hipStream_t s,
+                     const float *resid);
 // fm_stats.hip
 int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
                      uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, float *c_last, int B, int T,
-                     int A, hipStream_t s, void *qw = nullptr, int qw_dt = ULM_BF16);
+                     int A, hipStream_t s, void *qw = nullptr, int qw_dt = ULM_BF16, int AL = 0);
 size_t bwd_stats_partial_bytes(int B, int A);
 int launch_bwd_stats(const float *dqf, const float *dqo, const RSrc &src, const float *nck,
                      const float *w, const float *g, const float *dkf, float *dr, float *dw, float *dg, void *part,
@@ -77,20 +90,27 @@ bool fm_aligned(int B, int T, int A, int D) {
     return la_kgroup_supported(B, T, A, D) && la_kgroup_supported(B, T, D, A);
 }
 
-// How the training entries evaluate the products: the generic kernel (A or D
-// not a multiple of 32), the chunked state form (K-group kernel) or the
-// block-pair form (pair.hip), whichever needs fewer flops: the pair form costs
-// about T (A + D) per token and product, the state form 4 A D, so the pair form
-// serves sequences up to a few thousand positions. ULM_FM_PATH=chunked or
-// =pair in the environment forces one of the two for aligned shapes (it must
-// not change between a forward and its backward).
+int pad32(int x) { return (x + 31) / 32 * 32; }
+
+// How the training entries evaluate the products: the chunked state form
+// (K-group kernel, A and D multiples of 32), the block-pair form (pair.hip,
+// any A and D: its operand tiles are padded to multiples of 32 with zero slots
+// and features, which add nothing to any product) or the generic kernel
+// (fm_chunk.hip; widths off the 32 grid past 4096 positions). For aligned
+// widths the cheaper of the first two serves: the pair form costs about
+// T (A + D) flops per token and product, the state form 4 A D, so the pair form
+// serves sequences up to a few thousand positions. ULM_FM_PATH=chunked, =pair
+// or =generic in the environment forces one where it applies (it must not
+// change between a forward and its backward).
 enum Path { PATH_GENERIC = 0, PATH_CHUNKED = 1, PATH_PAIR = 2 };
 
 Path train_path(int B, int T, int A, int D) {
-    if (!fm_aligned(B, T, A, D)) return PATH_GENERIC;
     const char *env = getenv("ULM_FM_PATH");
+    if (env && env[0] == 'g') return PATH_GENERIC;
+    const bool pair_ok = T <= 4096 && fm_aligned(B, T, pad32(A), pad32(D));
+    if (!fm_aligned(B, T, A, D)) return pair_ok ? PATH_PAIR : PATH_GENERIC;
     if (env && env[0] == 'c') return PATH_CHUNKED;
-    if (T > 4096) return PATH_CHUNKED;
+    if (!pair_ok) return PATH_CHUNKED;
     if (env && env[0] == 'p') return PATH_PAIR;
     const double chunked = 16.0 * A * D + 8.0 * ULM_CHUNK * (A + D);
     return pair_flops_per_token(B, T, A, D) < 0.8 * chunked ? PATH_PAIR : PATH_CHUNKED;
@@ -104,9 +124,11 @@ struct Saved {
     size_t bytes;
 };
 
+// The tiled operand copies (R and Q layouts) of the pair and chunked paths
+// are pad32(A) slots and pad32(D) features wide.
 Saved saved_layout(void *base, int B, int T, int A, int D, int v_dtype, Path path) {
     const size_t NT = nt_of(T);
-    const size_t na = static_cast<size_t>(B) * T * A, ta = B * NT * 64 * A, td = B * NT * 64 * D;
+    const size_t na = static_cast<size_t>(B) * T * A, ta = B * NT * 64 * pad32(A), td = B * NT * 64 * pad32(D);
     Carver c(base);
     Saved s{};
     if (path == PATH_PAIR) {
@@ -137,34 +159,43 @@ Saved saved_layout(void *base, int B, int T, int A, int D, int v_dtype, Path pat
 }
 
 struct FwdWs {
+    float *gpart;  // generic path: the key tiles' partial planes
     uint16_t *Pf;
     uint16_t *qR, *kR, *vQ;   // pair path: the forward's operand tiles
     float *part;   // fp32 output or partials
+    float *state;  // chunked prefill at widths off the 32 grid: the padded state
     size_t bytes;
 };
 
-// resid: the output is x + fast, so the chunked products always go through fp32 partials
-FwdWs fwd_layout(void *base, int B, int T, int A, int D, int fast_dtype, Path path, bool resid = false) {
+// resid: the output is x + fast, so the chunked products always go through fp32 partials.
+// state: a chunked prefill (widths off the 32 grid keep a padded state here).
+FwdWs fwd_layout(void *base, int B, int T, int A, int D, int fast_dtype, Path path, bool resid = false,
+                 bool state = false) {
     const size_t NT = nt_of(T), nd = static_cast<size_t>(B) * T * D;
+    const bool padded = A % 32 || D % 32;
     Carver c(base);
     FwdWs w{};
     if (path == PATH_PAIR) {
         // the block-pair products write the output directly
-        w.qR = c.take<uint16_t>(B * NT * 64 * A);
-        w.kR = c.take<uint16_t>(B * NT * 64 * A);
-        w.vQ = c.take<uint16_t>(B * NT * 64 * D);
+        w.qR = c.take<uint16_t>(B * NT * 64 * pad32(A));
+        w.kR = c.take<uint16_t>(B * NT * 64 * pad32(A));
+        w.vQ = c.take<uint16_t>(B * NT * 64 * pad32(D));
     } else if (path == PATH_CHUNKED) {
         w.Pf = c.take<uint16_t>(B * NT * ULM_CHUNK * ULM_CHUNK);
-        const int nkg = la_kgroup_groups(A);
-        if (nkg > 1 || fast_dtype != ULM_F32 || resid) w.part = c.take<float>(nkg * nd);
-    } else if (fast_dtype != ULM_F32 || resid) {
-        w.part = c.take<float>(nd);
+        const int nkg = la_kgroup_groups(pad32(A));
+        if (nkg > 1 || fast_dtype != ULM_F32 || resid || padded)
+            w.part = c.take<float>(nkg * static_cast<size_t>(B) * T * pad32(D));
+        if (state && padded) w.state = c.take<float>(static_cast<size_t>(B) * pad32(D) * pad32(A));
+    } else {
+        if (fast_dtype != ULM_F32 || resid) w.part = c.take<float>(nd);
+        if (la_generic_parts(A) > 1) w.gpart = c.take<float>(la_generic_parts(A) * nd);
     }
     w.bytes = c.off;
     return w;
 }
 
 struct BwdWs {
+    float *gpart;                                            // generic path: partial planes
     uint16_t *do16;                                          // generic path
     uint16_t *doR, *doRl, *doQ, *doQl, *Pdq, *Pdk;   // K-group path (pair: doR, doQ)
     uint16_t *dS, *dSt;                                      // pair path: the score gradients, transposed
@@ -182,8 +213,9 @@ BwdWs bwd_layout(void *base, int B, int T, int A, int D, int dfast_dtype, Path p
     w.dqf = c.take<float>(na);
     w.dkf = c.take<float>(na);
     if (path == PATH_PAIR) {
-        w.doR = c.take<uint16_t>(td);
-        w.doQ = c.take<uint16_t>(td);
+        const size_t tdp = B * NT * 64 * pad32(D);
+        w.doR = c.take<uint16_t>(tdp);
+        w.doQ = c.take<uint16_t>(tdp);
         w.dS = c.take<uint16_t>(pair_p_bytes(B, T) / 2);
         w.dSt = c.take<uint16_t>(pair_p_bytes(B, T) / 2);
         w.dgx = c.take<double>(pair_dscore_jobs(B, T));
@@ -201,6 +233,10 @@ BwdWs bwd_layout(void *base, int B, int T, int A, int D, int dfast_dtype, Path p
     } else {
         w.do16 = c.take<uint16_t>(nd);
         w.part = c.take<float>(nd);   // fp32 dv accumulator
+        // dq_f and dk_f contract over D, dv over A
+        const size_t gp = std::max(la_generic_parts(D) > 1 ? la_generic_parts(D) * na : 0,
+                                   la_generic_parts(A) > 1 ? la_generic_parts(A) * nd : 0);
+        if (gp) w.gpart = c.take<float>(gp);
     }
     w.stats = c.take<char>(bwd_stats_partial_bytes(B, A));
     w.bytes = c.off;
@@ -218,7 +254,11 @@ using namespace ulm;
 
 extern "C" size_t ulm_la_workspace_bytes(int B, int T, int K, int V) {
     if (B <= 0 || T <= 0 || K <= 0 || V <= 0) return 0;
-    if (!la_kgroup_supported(B, T, K, V)) return 0;
+    if (!la_kgroup_supported(B, T, K, V)) {
+        // the generic kernel's partial planes, one per key tile past the first
+        const int parts = la_generic_parts(K);
+        return parts > 1 ? static_cast<size_t>(parts) * B * T * V * sizeof(float) : 0;
+    }
     const size_t NT = nt_of(T), tk = B * NT * 64 * K, tv = B * NT * 64 * V;
     Carver c(nullptr);
     c.take<uint16_t>(2 * tk);                                 // a and b, R layout
@@ -239,10 +279,8 @@ extern "C" int ulm_la(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
     ULM_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), "ulm_la: workspace of %zu bytes, need %zu",
                 workspace_bytes, need);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (!la_kgroup_supported(B, T, K, V)) {
-        ULM_TRY(launch_fill_zero(out, static_cast<size_t>(B) * T * V * sizeof(float), s));
-        return launch_la_generic(a, b, c, g, out, B, T, K, V, reverse != 0, s);
-    }
+    if (!la_kgroup_supported(B, T, K, V))
+        return launch_la_generic(a, b, c, g, out, static_cast<float *>(workspace), B, T, K, V, reverse != 0, s);
     const size_t NT = nt_of(T), tk = B * NT * 64 * K, tv = B * NT * 64 * V;
     Carver cv(workspace);
     uint16_t *aR = cv.take<uint16_t>(2 * tk);
@@ -293,7 +331,7 @@ int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const 
                int qw_dt, const float *resid, void *fast, int fast_dtype, void *saved, void *workspace, float *state,
                float *c_last, int B, int T, int A, int D, Path path, hipStream_t s) {
     const Saved sv = saved_layout(saved, B, T, A, D, v_dtype, path);
-    const FwdWs ws = fwd_layout(workspace, B, T, A, D, fast_dtype, path, resid != nullptr);
+    const FwdWs ws = fwd_layout(workspace, B, T, A, D, fast_dtype, path, resid != nullptr, state != nullptr);
     const size_t nf = static_cast<size_t>(B) * T * D;
     if (path == PATH_PAIR) {
         if (state || c_last) return fail(ULM_ERR_INVALID, "prefill state: not on the block-pair path");
@@ -301,35 +339,44 @@ int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const 
         // backward's dk_f, dq_f; v: Q layout for the apply, R layout for the
         // backward's dscores
         ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, ws.qR, ws.kR, sv.qQ, sv.kQ, sv.nck, nullptr, B, T, A, s,
-                                 qw, qw_dt));
-        ULM_TRY(launch_chunk_transpose(v, v_dtype, ws.vQ, nullptr, sv.vR, nullptr, B, T, D, s));
+                                 qw, qw_dt, pad32(A)));
+        ULM_TRY(launch_chunk_transpose(v, v_dtype, ws.vQ, nullptr, sv.vR, nullptr, B, T, D, s, pad32(D)));
         return launch_pair_forward(ws.qR, ws.kR, ws.vQ, g, sv.P, sv.Pt, sv.Plo, fast, fast_dtype, resid, B, T, A, D, s);
     }
     if (path == PATH_CHUNKED) {
-        const int nkg = la_kgroup_groups(A);
+        // widths off the 32 grid (a prefill only) run on zero-padded tiles; the
+        // output and the state drop the padding on the way out
+        const int Ap = pad32(A), Dp = pad32(D);
+        const bool padded = Ap != A || Dp != D;
+        const int nkg = la_kgroup_groups(Ap);
         float *acc = ws.part ? ws.part : static_cast<float *>(fast);
         // a prefill (state wanted) has no backward, the only reader of q in the Q
         // layout and of v in the R layout: those tiles are not written then
         ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, sv.qR, sv.kR, state ? nullptr : sv.qQ, sv.kQ, sv.nck,
-                                 c_last, B, T, A, s, qw, qw_dt));
+                                 c_last, B, T, A, s, qw, qw_dt, Ap));
         ULM_TRY(launch_chunk_transpose(v, v_dtype, sv.vQ, sv.vQl, state ? nullptr : sv.vR, state ? nullptr : sv.vRl, B,
-                                       T, D, s));
-        ULM_TRY(launch_chunk_scores(sv.qR, nullptr, sv.kR, nullptr, g, ws.Pf, sv.Pdv, B, T, A, true, s));
+                                       T, D, s, Dp));
+        ULM_TRY(launch_chunk_scores(sv.qR, nullptr, sv.kR, nullptr, g, ws.Pf, sv.Pdv, B, T, Ap, true, s));
         // fast = LA(q, k, v): update k^T v~ (v~ from the full-precision v), intra on
         // bf16(v), as the reference's bf16 v (kernel.py:205). Its state, transposed,
         // is the decode state S (model.py:96-111).
-        ULM_TRY(launch_la_kgroup(sv.qR, nullptr, sv.kQ, nullptr, sv.vQ, sv.vQl, ws.Pf, true, g, acc, state, B, T, A, D,
+        float *st = state && padded ? ws.state : state;
+        ULM_TRY(launch_la_kgroup(sv.qR, nullptr, sv.kQ, nullptr, sv.vQ, sv.vQl, ws.Pf, true, g, acc, st, B, T, Ap, Dp,
                                  false, false, s));
-        if (ws.part) ULM_TRY(launch_partial_reduce(ws.part, nkg, nf, fast, fast_dtype, s, resid));
+        if (padded) {
+            ULM_TRY(launch_unpad_sum(ws.part, nkg, B, T, T, D, Dp, fast, fast_dtype, s, resid));
+            if (state) ULM_TRY(launch_unpad_sum(ws.state, 1, B, D, Dp, A, Ap, state, ULM_F32, s, nullptr));
+        } else if (ws.part) {
+            ULM_TRY(launch_partial_reduce(ws.part, nkg, nf, fast, fast_dtype, s, resid));
+        }
         return ULM_OK;
     }
-    if (state || c_last) return fail(ULM_ERR_UNSUPPORTED, "prefill state: A=%d and D=%d must be multiples of 32", A, D);
+    if (state || c_last) return fail(ULM_ERR_UNSUPPORTED, "prefill state: not on the generic path");
     ULM_TRY(launch_fwd_stats(r, w, g, q, sv.q16n, sv.k16n, nullptr, nullptr, nullptr, nullptr, sv.nck, nullptr, B, T, A,
                              s, qw, qw_dt));
     ULM_TRY(launch_convert(v, v_dtype, sv.v16n, ULM_BF16, nf, s));
     float *acc = ws.part ? ws.part : static_cast<float *>(fast);
-    ULM_TRY(launch_fill_zero(acc, nf * sizeof(float), s));
-    ULM_TRY(launch_la_generic(sv.q16n, sv.k16n, sv.v16n, g, acc, B, T, A, D, false, s));
+    ULM_TRY(launch_la_generic(sv.q16n, sv.k16n, sv.v16n, g, acc, ws.gpart, B, T, A, D, false, s));
     if (ws.part) ULM_TRY(launch_partial_reduce(acc, 1, nf, fast, fast_dtype, s, resid));
     return ULM_OK;
 }
@@ -358,9 +405,9 @@ extern "C" int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const floa
 
 extern "C" size_t ulm_fm_prefill_workspace_bytes(int B, int T, int A, int D, int v_dtype, int fast_dtype) {
     if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(v_dtype) || !valid_dtype(fast_dtype)) return 0;
-    if (!fm_aligned(B, T, A, D)) return 0;
+    if (!fm_aligned(B, T, pad32(A), pad32(D))) return 0;
     return align_up(saved_layout(nullptr, B, T, A, D, v_dtype, PATH_CHUNKED).bytes, 256) +
-           fwd_layout(nullptr, B, T, A, D, fast_dtype, PATH_CHUNKED).bytes;
+           fwd_layout(nullptr, B, T, A, D, fast_dtype, PATH_CHUNKED, false, true).bytes;
 }
 
 extern "C" int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const float *g, const float *w, float *q,
@@ -370,7 +417,8 @@ extern "C" int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const 
     ULM_REQUIRE(valid_dtype(v_dtype) && valid_dtype(fast_dtype), "ulm_fm_prefill: bad dtype %d/%d", v_dtype,
                 fast_dtype);
     ULM_REQUIRE(r && v && g && w && q && fast && S && c_last && workspace, "ulm_fm_prefill: null pointer");
-    ULM_REQUIRE(fm_aligned(B, T, A, D), "ulm_fm_prefill: A=%d and D=%d must be multiples of 32", A, D);
+    ULM_REQUIRE(fm_aligned(B, T, pad32(A), pad32(D)), "ulm_fm_prefill: unsupported sizes B=%d T=%d A=%d D=%d", B, T,
+                A, D);
     ULM_REQUIRE(reinterpret_cast<uintptr_t>(S) % 16 == 0, "ulm_fm_prefill: S must be 16-byte aligned");
     const size_t need = ulm_fm_prefill_workspace_bytes(B, T, A, D, v_dtype, fast_dtype);
     ULM_REQUIRE(workspace_bytes >= need, "ulm_fm_prefill: workspace of %zu bytes, need %zu", workspace_bytes, need);
@@ -399,7 +447,7 @@ int fm_backward(const RSrc &r, const float *g, const float *w, const void *saved
     const BwdWs ws = bwd_layout(workspace, B, T, A, D, dfast_dtype, path);
     const size_t nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
     if (path == PATH_PAIR) {
-        ULM_TRY(launch_chunk_transpose(dfast, dfast_dtype, ws.doQ, nullptr, ws.doR, nullptr, B, T, D, s));
+        ULM_TRY(launch_chunk_transpose(dfast, dfast_dtype, ws.doQ, nullptr, ws.doR, nullptr, B, T, D, s, pad32(D)));
         ULM_TRY(launch_pair_backward(sv.vR, ws.doR, ws.doQ, sv.kQ, sv.qQ, sv.P, sv.Pt, sv.Plo, g, ws.dS, ws.dSt, ws.dgx, ws.dqf,
                                      ws.dkf, dv, dv_dtype, B, T, A, D, s));
         return launch_bwd_stats(ws.dqf, dq_out, r, sv.nck, w, g, ws.dkf, dr, dw, dg, ws.stats, B, T, A, s, dqw, dqw_dt,
@@ -434,13 +482,10 @@ int fm_backward(const RSrc &r, const float *g, const float *w, const void *saved
             ULM_TRY(launch_convert(dfast, dfast_dtype, ws.do16, ULM_BF16, nd, s));
             do16 = ws.do16;
         }
-        ULM_TRY(launch_fill_zero(ws.dqf, na * 4, s));
-        ULM_TRY(launch_la_generic(do16, sv.v16n, sv.k16n, g, ws.dqf, B, T, D, A, false, s));
-        ULM_TRY(launch_fill_zero(ws.dkf, na * 4, s));
-        ULM_TRY(launch_la_generic(sv.v16n, do16, sv.q16n, g, ws.dkf, B, T, D, A, true, s));
+        ULM_TRY(launch_la_generic(do16, sv.v16n, sv.k16n, g, ws.dqf, ws.gpart, B, T, D, A, false, s));
+        ULM_TRY(launch_la_generic(sv.v16n, do16, sv.q16n, g, ws.dkf, ws.gpart, B, T, D, A, true, s));
         float *dv_acc = dv_dtype == ULM_F32 ? static_cast<float *>(dv) : ws.part;
-        ULM_TRY(launch_fill_zero(dv_acc, nd * 4, s));
-        ULM_TRY(launch_la_generic(sv.k16n, sv.q16n, do16, g, dv_acc, B, T, A, D, true, s));
+        ULM_TRY(launch_la_generic(sv.k16n, sv.q16n, do16, g, dv_acc, ws.gpart, B, T, A, D, true, s));
         if (dv_dtype != ULM_F32) ULM_TRY(launch_convert(dv_acc, ULM_F32, dv, dv_dtype, nd, s));
     }
     return launch_bwd_stats(ws.dqf, dq_out, r, sv.nck, w, g, ws.dkf, dr, dw, dg, ws.stats, B, T, A, s, dqw, dqw_dt);
@@ -527,9 +572,9 @@ extern "C" int ulm_block_fm_bwd(const void *pre, int pre_dtype, const float *bia
 
 extern "C" size_t ulm_block_fm_prefill_workspace_bytes(int B, int T, int A, int D, int v_dtype) {
     if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(v_dtype)) return 0;
-    if (!fm_aligned(B, T, A, D)) return 0;
+    if (!fm_aligned(B, T, pad32(A), pad32(D))) return 0;
     return align_up(saved_layout(nullptr, B, T, A, D, v_dtype, PATH_CHUNKED).bytes, 256) +
-           fwd_layout(nullptr, B, T, A, D, ULM_F32, PATH_CHUNKED, true).bytes;
+           fwd_layout(nullptr, B, T, A, D, ULM_F32, PATH_CHUNKED, true, true).bytes;
 }
 
 extern "C" int ulm_block_fm_prefill(const void *pre, int pre_dtype, const float *bias, const float *denom,
@@ -542,7 +587,8 @@ extern "C" int ulm_block_fm_prefill(const void *pre, int pre_dtype, const float 
     ULM_REQUIRE(pre && denom && v && g && w && qw && x && y && S && c_last && workspace,
                 "ulm_block_fm_prefill: null pointer");
     ULM_REQUIRE(static_cast<const void *>(x) != static_cast<const void *>(y), "ulm_block_fm_prefill: y must not alias x");
-    ULM_REQUIRE(fm_aligned(B, T, A, D), "ulm_block_fm_prefill: A=%d and D=%d must be multiples of 32", A, D);
+    ULM_REQUIRE(fm_aligned(B, T, pad32(A), pad32(D)), "ulm_block_fm_prefill: unsupported sizes B=%d T=%d A=%d D=%d",
+                B, T, A, D);
     ULM_REQUIRE(reinterpret_cast<uintptr_t>(S) % 16 == 0, "ulm_block_fm_prefill: S must be 16-byte aligned");
     const size_t need = ulm_block_fm_prefill_workspace_bytes(B, T, A, D, v_dtype);
     ULM_REQUIRE(workspace_bytes >= need, "ulm_block_fm_prefill: workspace of %zu bytes, need %zu", workspace_bytes,

@@ -123,9 +123,10 @@ int with_rsrc(const RSrc &src, F &&f) {
 }
 
 // Outputs besides n_ckpt (each may be null): q (fp32); qw = w q in qw_dt; q16n, k16n natural bf16
-// copies; qR, kR in the R layout and qQ, kQ in the Q layout (the chunked
-// kernel's operand tiles; A % 32 == 0); c_last = c at position T-1 (B, A), the
-// decode state after the sequence. Positions past T are zero in R and Q.
+// copies; qR, kR in the R layout and qQ, kQ in the Q layout (the products'
+// operand tiles, AL slots wide: AL % 32 == 0, A <= AL <= the grid's slots);
+// c_last = c at position T-1 (B, A), the decode state after the sequence.
+// Positions past T and slots past A are zero in R and Q.
 // QW: the dtype of the w q output (-1 none, else a ulm_dtype); HAS_Q: the fp32 q output.
 template <class RS, int QW, bool HAS_Q>
 __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__restrict__ w,
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
                                                         uint16_t *__restrict__ qR, uint16_t *__restrict__ kR,
                                                         uint16_t *__restrict__ qQ, uint16_t *__restrict__ kQ,
                                                         float *__restrict__ nck, float *__restrict__ c_last, int T,
-                                                        int A, int NT) {
+                                                        int A, int AL, int NT) {
     __shared__ float tot[4][kSlots];
     __shared__ __align__(16) uint16_t sq[ULM_CHUNK][kSlots + 8], sk[ULM_CHUNK][kSlots + 8];   // [position][slot]
     const int s = threadIdx.x % kSlots;
@@ -216,12 +217,12 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
                 kpk[i / 2] |= static_cast<uint32_t>(kb) << 16;
             }
         }
-        if ((qQ || kQ) && va) {
+        if ((qQ || kQ) && a < AL) {
             // Q layout: this thread's positions 16 j .. 16 j + 15 of slot a are two lanes' 16 bytes
             // (qQ is null where no backward follows, as in a prefill)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const size_t o = q_index(b, n * ULM_CHUNK + kSeg * j + 8 * h, a, NT, A);
+                const size_t o = q_index(b, n * ULM_CHUNK + kSeg * j + 8 * h, a, NT, AL);
                 if (qQ) *reinterpret_cast<uint4 *>(qQ + o) = make_uint4(qpk[4 * h], qpk[4 * h + 1], qpk[4 * h + 2], qpk[4 * h + 3]);
                 if (kQ) *reinterpret_cast<uint4 *>(kQ + o) = make_uint4(kpk[4 * h], kpk[4 * h + 1], kpk[4 * h + 2], kpk[4 * h + 3]);
             }
@@ -234,11 +235,11 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
         if (qR) {
             // R layout: the block's 64 positions x 64 slots are 8 tiles; thread -> 2 lanes of one tile
             const int tl = threadIdx.x / 32, mt = tl / 4, tf4 = tl % 4;
-            if (a0 + 16 * tf4 < A) {
+            if (a0 + 16 * tf4 < AL) {
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
                     const int l = 2 * (threadIdx.x % 32) + u, row = 32 * mt + l % 32, col = 16 * tf4 + 8 * (l / 32);
-                    const size_t o = r_index(b, n * ULM_CHUNK + row, a0 + col, NT, A);
+                    const size_t o = r_index(b, n * ULM_CHUNK + row, a0 + col, NT, AL);
                     *reinterpret_cast<uint4 *>(qR + o) = *reinterpret_cast<const uint4 *>(&sq[row][col]);
                     *reinterpret_cast<uint4 *>(kR + o) = *reinterpret_cast<const uint4 *>(&sk[row][col]);
                 }
@@ -425,17 +426,20 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(const float *__restri
 }
 
 // q16n, k16n: natural bf16 copies (both or neither); qR, kR, qQ, kQ: tiled
-// copies (all or none; A % 32 == 0).
+// copies AL slots wide (0: AL = A; AL % 32 == 0, the slots past A zero).
 int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
                      uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, float *c_last, int B, int T,
-                     int A, hipStream_t s, void *qw, int qw_dt) {
+                     int A, hipStream_t s, void *qw, int qw_dt, int AL) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
     if ((q16n == nullptr) != (k16n == nullptr)) return fail(ULM_ERR_INVALID, "fwd stats: q16n and k16n go together");
     // the tiled copies: kQ always, qR and kR together (the chunked products'
     // R layout), qQ when a backward follows
     const bool tiled = qR || kR || qQ || kQ;
-    if (tiled && !(kQ && (qR != nullptr) == (kR != nullptr) && A % 32 == 0))
-        return fail(ULM_ERR_INVALID, "fwd stats: tiled copies need kQ, qR with kR, and A %% 32 == 0");
+    if (AL == 0) AL = A;
+    // the grid's blocks of kSlots slots cover the layout's padding slots too
+    if (tiled && !(kQ && (qR != nullptr) == (kR != nullptr) && AL % 32 == 0 && A <= AL &&
+                   AL <= (A + kSlots - 1) / kSlots * kSlots))
+        return fail(ULM_ERR_INVALID, "fwd stats: tiled copies need kQ, qR with kR, and a layout width %d for A=%d", AL, A);
     if (qw && !valid_dtype(qw_dt)) return fail(ULM_ERR_INVALID, "fwd stats: bad w q dtype %d", qw_dt);
     const int qwk = qw ? qw_dt : -1;
     return with_rsrc(src, [&](auto rs) {
@@ -443,7 +447,7 @@ int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, 
         const dim3 grid((A + kSlots - 1) / kSlots, B);
 #define ULM_FWD_STATS(QWK, HQ)                                                                                    \
     fwd_stats_kernel<RS, QWK, HQ><<<grid, 256, 0, s>>>(rs, w, g, q, qw, qw_dt, q16n, k16n, qR, kR, qQ, kQ, nck,   \
-                                                       c_last, T, A, NT)
+                                                       c_last, T, A, AL, NT)
         if (q) {
             switch (qwk) {
             case ULM_F32: ULM_FWD_STATS(ULM_F32, true); break;

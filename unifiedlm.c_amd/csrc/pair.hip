@@ -518,7 +518,9 @@ int launch(const Args &a, int G, int B, hipStream_t s) {
 
 }  // namespace pair
 
-// ---- the operator's products in block-pair form (A, D multiples of 32)
+// ---- the operator's products in block-pair form. The operand tiles are
+// padded to multiples of 32 slots (A) and features (D) with zeros; the outputs
+// have the natural widths.
 
 // Block (output tile) size of the block-pair products: 128 x 128 tiles, two
 // workgroups per CU (measured faster in total than 256 x 256 at the 110M shape).
@@ -551,15 +553,16 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *
                         int D, hipStream_t s) {
     using namespace pair;
     const int G = pair_block(B, T), Tq = pair_tq(B, T), NT = (T + 63) / 64;
+    const int Ap = (A + 31) / 32 * 32, Dp = (D + 31) / 32 * 32;   // operand tile widths
     Args a{};
     a.T = T;
     a.g = g;
-    a.a = r_mat(kR, NT, A);
-    a.b = r_mat(qR, NT, A);
+    a.a = r_mat(kR, NT, Ap);
+    a.b = r_mat(qR, NT, Ap);
     a.mt = a.nt = Tq / G;
     a.tri = 1;
     a.krange = K_FULL;
-    a.nks = (A + 16 * KT - 1) / (16 * KT);
+    a.nks = (Ap + 16 * KT - 1) / (16 * KT);
     const Mat pm = p_mat(P, Tq);
     a.pout = P;
     a.pout_t = Pt;
@@ -571,7 +574,7 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *
     f.T = T;
     f.g = g;
     f.a = pm;
-    f.b = q_mat(vQ, NT, D);
+    f.b = q_mat(vQ, NT, Dp);
     f.mt = Tq / G;
     f.nt = (D + G - 1) / G;
     f.krange = K_CAUSAL;
@@ -596,16 +599,17 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
                          int A, int D, hipStream_t s) {
     using namespace pair;
     const int G = pair_block(B, T), Tq = pair_tq(B, T), NT = (T + 63) / 64;
+    const int Ap = (A + 31) / 32 * 32, Dp = (D + 31) / 32 * 32;   // operand tile widths
     const Mat sm = p_mat(dS, Tq);
     Args a{};
     a.T = T;
     a.g = g;
-    a.a = r_mat(vR, NT, D);
-    a.b = r_mat(doR, NT, D);
+    a.a = r_mat(vR, NT, Dp);
+    a.b = r_mat(doR, NT, Dp);
     a.mt = a.nt = Tq / G;
     a.tri = 1;
     a.krange = K_FULL;
-    a.nks = (D + 16 * KT - 1) / (16 * KT);
+    a.nks = (Dp + 16 * KT - 1) / (16 * KT);
     a.pout = dS;
     a.pout_t = dSt;
     a.p_bstride = sm.bstride;
@@ -622,7 +626,7 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
     r.nperm = 1;
     // dq_f = dS k
     r.a = sm;
-    r.b = q_mat(kQ, NT, A);
+    r.b = q_mat(kQ, NT, Ap);
     r.nt = (A + G - 1) / G;
     r.krange = K_CAUSAL;
     r.out = dqf;
@@ -631,13 +635,13 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
     ULM_TRY((launch<false, EPI_ROWS>(r, G, B, s)));
     // dk_f = dS^T q: rows s of dSt, contraction t >= the start of s's block
     r.a = p_mat(dSt, Tq);
-    r.b = q_mat(qQ, NT, A);
+    r.b = q_mat(qQ, NT, Ap);
     r.krange = K_ANTI;
     r.out = dkf;
     ULM_TRY((launch<false, EPI_ROWS>(r, G, B, s)));
     // dv = P^T dfast
     r.a = p_mat(Pt, Tq);
-    r.b = q_mat(doQ, NT, D);
+    r.b = q_mat(doQ, NT, Dp);
     r.nt = (D + G - 1) / G;
     r.out = dv;
     r.out_dt = dv_dt;

@@ -368,8 +368,8 @@ def block_prefill(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rat
     r_prev, h) with S (B, D, A) and c (B, A) the fast-memory state after the
     last position (as fm_prefill), r_prev (B, A) fp32 the address at that
     position and h (B, T, D) the normalised input in cdt (its last positions
-    fill the conv window). A and D must be multiples of 32. log_rate and log_w
-    are the block's parameters, as for unified_block."""
+    fill the conv window). log_rate and log_w are the block's parameters, as
+    for unified_block."""
     if x.dim() != 3 or x.dtype != torch.float32:
         raise ValueError(f"x must be (B, T, D) fp32, got {tuple(x.shape)} {x.dtype}")
     B, T, D = x.shape
@@ -380,7 +380,7 @@ def block_prefill(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rat
     cd = nat.dtype_code(cdt)
     ws_bytes = nat.lib().ulm_block_fm_prefill_workspace_bytes(B, T, A, D, cd)
     if ws_bytes == 0:
-        raise ValueError(f"block_prefill: A={A} and D={D} must be multiples of 32")
+        raise ValueError(f"block_prefill: unsupported sizes B={B} T={T} A={A} D={D}")
     dev = x.device
     s = nat.stream_of(x)
     f32 = torch.float32
@@ -426,8 +426,7 @@ def fm_prefill(r, v, g, w):
     """The forward of unified_memory (no autograd) plus the decode state after
     the last position: returns (q, fast, S, c) with S (B, D, A) fp32 =
     sum_s lam^(T-1-s) v_s k_s^T and c (B, A) fp32 = w + sum_s lam^(T-1-s) k_s,
-    the state UnifiedBlock.step carries (model.py:88-111). A and D must be
-    multiples of 32."""
+    the state UnifiedBlock.step carries (model.py:88-111)."""
     _check_fm(r, v, g, w)
     B, T, A = r.shape
     D = v.shape[-1]
@@ -438,7 +437,7 @@ def fm_prefill(r, v, g, w):
     vdt = nat.dtype_code(v.dtype)
     ws_bytes = nat.lib().ulm_fm_prefill_workspace_bytes(B, T, A, D, vdt, vdt)
     if ws_bytes == 0:
-        raise RuntimeError(f"fm_prefill: A={A} and D={D} must be multiples of 32")
+        raise RuntimeError(f"fm_prefill: unsupported sizes B={B} T={T} A={A} D={D}")
     q = torch.empty_like(r32)
     fast = torch.empty(B, T, D, device=r.device, dtype=v.dtype)
     S = torch.empty(B, D, A, device=r.device, dtype=torch.float32)

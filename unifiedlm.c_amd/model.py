@@ -138,11 +138,11 @@ class UnifiedBlock(nn.Module):
         returning the decode state after position T-1: the state that T calls of
         `step` would leave (model.py:88-111), with S and c from the chunked
         kernels (bf16 operands, fp32 accumulation) instead of T fp32 updates.
-        With A and d multiples of 32 and an fp32 x the block runs fused
-        (kernel.block_prefill), its GEMMs in the autocast dtype."""
+        With an fp32 x the block runs fused (kernel.block_prefill), its GEMMs in
+        the autocast dtype."""
         B, T, d = x.shape
         A = self.mu.in_features
-        if x.dtype == torch.float32 and A % 32 == 0 and d % 32 == 0:
+        if x.dtype == torch.float32:
             cdt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else torch.float32
             with torch.autocast("cuda", enabled=False):
                 out, S, c, r_prev, h = block_prefill(x, self.norm.weight, self.conv.weight, self.key.weight,
@@ -257,7 +257,7 @@ class UnifiedLM(nn.Module):
         the prompt (B, T0) is forced and every later token is the argmax of the
         previous position's logits (first maximum on ties, run.c:460-469).
         Returns (B, steps + 1) tokens. With `prefill` the prompt goes through
-        one chunked pass (`prefill`, slots and width multiples of 32) instead of
+        one chunked pass (`prefill`) instead of
         T0 calls of `step`."""
         B, T0 = prompt.shape
         if steps < T0:

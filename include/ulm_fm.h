@@ -158,6 +158,20 @@ int ulm_addr_bwd(const void *pre, int pre_dtype, const float *bias, const float 
                  void *dpre, float *dbias, float *dlog_eps,
                  void *workspace, size_t workspace_bytes, int M, int A, void *stream);
 
+/* ulm_addr_bwd with no workspace argument and no allocation of any kind, for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The scratch (ulm_addr_bwd_workspace_bytes(M, A) bytes) lives in a
+ * static device array of ULM_ADDR_BWD_NOALLOC_SCRATCH_BYTES bytes, one per
+ * GPU, held until the process ends; larger M x A are rejected
+ * (ULM_ERR_INVALID). Results are bitwise those of ulm_addr_bwd. Every call on
+ * one GPU shares that GPU's array: calls that overlap in time on one GPU (on
+ * different streams, or from several threads) race and must not be issued. */
+#define ULM_ADDR_BWD_NOALLOC_SCRATCH_BYTES (8u << 20)
+int ulm_addr_bwd_noalloc(const void *pre, int pre_dtype, const float *bias, const float *log_eps,
+                         const float *r, const float *denom, const float *dr,
+                         void *dpre, float *dbias, float *dlog_eps, int M, int A, void *stream);
+
 /* ------------------------------------------------------------------------
  * Training: the rest of UnifiedBlock.forward (model.py:77-85) around the fast
  * memory. The block runs as

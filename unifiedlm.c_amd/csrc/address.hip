@@ -15,6 +15,8 @@
 // 2*4 + 2*sizeof(pre); each row's second read is served by the cache.
 #include "ulm_common.h"
 
+#include <mutex>
+
 namespace ulm {
 
 constexpr int kFwdRowsPerWave = 2;
@@ -294,18 +296,15 @@ extern "C" size_t ulm_addr_bwd_workspace_bytes(int M, int A) {
     return addr_ws(nullptr, M, A).bytes;
 }
 
-extern "C" int ulm_addr_bwd(const void *pre, int pre_dtype, const float *bias, const float *log_eps, const float *r,
-                            const float *denom, const float *dr, void *dpre, float *dbias, float *dlog_eps,
-                            void *workspace, size_t workspace_bytes, int M, int A, void *stream) {
-    ULM_REQUIRE(M > 0 && A > 0, "ulm_addr_bwd: bad sizes M=%d A=%d", M, A);
-    ULM_REQUIRE(A <= 8192, "ulm_addr_bwd: A=%d exceeds the LDS column-partial limit 8192", A);
-    ULM_REQUIRE(valid_dtype(pre_dtype), "ulm_addr_bwd: bad pre dtype %d", pre_dtype);
-    ULM_REQUIRE(pre && log_eps && denom && dr && dpre && dlog_eps, "ulm_addr_bwd: null pointer");
-    ULM_REQUIRE(!bias || dbias, "ulm_addr_bwd: dbias is required when bias is given");
-    ULM_REQUIRE(workspace && workspace_bytes >= ulm_addr_bwd_workspace_bytes(M, A),
-                "ulm_addr_bwd: workspace of %zu bytes, need %zu", workspace_bytes, ulm_addr_bwd_workspace_bytes(M, A));
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const AddrWs ws = addr_ws(workspace, M, A);
+namespace {
+
+// The backward's launches on a scratch buffer of ulm_addr_bwd_workspace_bytes
+// (arguments checked by the caller). Every scratch word the kernels read was
+// written earlier in the same call: nothing needs to start at zero.
+int addr_bwd_run(const void *pre, int pre_dtype, const float *bias, const float *log_eps, const float *r,
+                 const float *denom, const float *dr, void *dpre, float *dbias, float *dlog_eps, void *scratch_buf,
+                 int M, int A, hipStream_t s) {
+    const AddrWs ws = addr_ws(scratch_buf, M, A);
     const int nblk = addr_blocks(M, kBwdRowsPerWave);
     int st;
     if (pre_dtype == ULM_F32)
@@ -318,4 +317,70 @@ extern "C" int ulm_addr_bwd(const void *pre, int pre_dtype, const float *bias, c
     if (bias) ULM_TRY(launch_column_sum(ws.dbias_part, nblk, A, ws.tmp, kAddrSplit, dbias, s));
     addr_dle_kernel<<<1, 64, 0, s>>>(ws.dle_part, dlog_eps, nblk);
     return check_launch("addr_dle_kernel");
+}
+
+}  // namespace
+
+#define ULM_ADDR_BWD_CHECKS(NAME)                                                                                 \
+    ULM_REQUIRE(M > 0 && A > 0, NAME ": bad sizes M=%d A=%d", M, A);                                              \
+    ULM_REQUIRE(A <= 8192, NAME ": A=%d exceeds the LDS column-partial limit 8192", A);                          \
+    ULM_REQUIRE(valid_dtype(pre_dtype), NAME ": bad pre dtype %d", pre_dtype);                                    \
+    ULM_REQUIRE(pre && log_eps && denom && dr && dpre && dlog_eps, NAME ": null pointer");                        \
+    ULM_REQUIRE(!bias || dbias, NAME ": dbias is required when bias is given")
+
+extern "C" int ulm_addr_bwd(const void *pre, int pre_dtype, const float *bias, const float *log_eps, const float *r,
+                            const float *denom, const float *dr, void *dpre, float *dbias, float *dlog_eps,
+                            void *workspace, size_t workspace_bytes, int M, int A, void *stream) {
+    ULM_ADDR_BWD_CHECKS("ulm_addr_bwd");
+    ULM_REQUIRE(workspace && workspace_bytes >= ulm_addr_bwd_workspace_bytes(M, A),
+                "ulm_addr_bwd: workspace of %zu bytes, need %zu", workspace_bytes, ulm_addr_bwd_workspace_bytes(M, A));
+    return addr_bwd_run(pre, pre_dtype, bias, log_eps, r, denom, dr, dpre, dbias, dlog_eps, workspace, M, A,
+                        static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// ulm_addr_bwd without a workspace argument and without any allocation: the
+// scratch lives in a fixed device array, one copy per GPU, held until the
+// process ends. Its device address is looked up once per device (with that
+// device current) and kept; the array's name is never used as an address on
+// the host.
+
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[ULM_ADDR_BWD_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+void *g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// scratch's device address on the current device, looked up on first use
+int scratch_ptr(void **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return check_launch("hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(ULM_ERR_UNSUPPORTED, "device %d past the %d supported", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p)
+            return check_launch("hipGetSymbolAddress(scratch)");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return ULM_OK;
+}
+
+}  // namespace
+
+extern "C" int ulm_addr_bwd_noalloc(const void *pre, int pre_dtype, const float *bias, const float *log_eps,
+                                    const float *r, const float *denom, const float *dr, void *dpre, float *dbias,
+                                    float *dlog_eps, int M, int A, void *stream) {
+    ULM_ADDR_BWD_CHECKS("ulm_addr_bwd_noalloc");
+    const size_t need = ulm_addr_bwd_workspace_bytes(M, A);
+    ULM_REQUIRE(need <= ULM_ADDR_BWD_NOALLOC_SCRATCH_BYTES,
+                "ulm_addr_bwd_noalloc: M=%d A=%d needs %zu bytes of scratch, past the %zu of the static array", M, A,
+                need, static_cast<size_t>(ULM_ADDR_BWD_NOALLOC_SCRATCH_BYTES));
+    void *buf = nullptr;
+    ULM_TRY(scratch_ptr(&buf));
+    return addr_bwd_run(pre, pre_dtype, bias, log_eps, r, denom, dr, dpre, dbias, dlog_eps, buf, M, A,
+                        static_cast<hipStream_t>(stream));
 }

@@ -35,6 +35,7 @@ SIGNATURES = {
     "ulm_addr_fwd": (I, [P, I, P, P, P, P, I, I, P]),
     "ulm_addr_bwd_workspace_bytes": (SZ, [I, I]),
     "ulm_addr_bwd": (I, [P, I, P, P, P, P, P, P, P, P, P, SZ, I, I, P]),
+    "ulm_addr_bwd_noalloc": (I, [P, I, P, P, P, P, P, P, P, P, I, I, P]),
     "ulm_norm_conv_fwd": (I, [P, I, P, P, I, F, P, I, P, I, P, I, I, I, P]),
     "ulm_norm_conv_bwd_workspace_bytes": (SZ, [I, I, I, I]),
     "ulm_norm_conv_bwd": (I, [P, I, P, P, P, I, P, I, P, I, P, P, P, P, P, SZ, I, I, I, P]),

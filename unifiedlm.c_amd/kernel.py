@@ -16,6 +16,8 @@ Besides the operator this module exposes the relu^2 slot address
 (model.py:70-72) as an autograd Function and the three per-token decode
 kernels used by UnifiedBlock.step.
 """
+from typing import Optional
+
 import torch
 
 import ulm_native as nat
@@ -49,59 +51,116 @@ def _check_fm(r, v, g, w):
     nat.require_device(r, v, g, w)
 
 
-class UnifiedMemory(torch.autograd.Function):
-    """Replaces kernel.py:199-233. Saves r, g, w and one opaque buffer that
-    the forward fills with what the backward needs (bf16 operand tiles of q, k
-    and v, score tiles and the per-chunk evidence checkpoints that stand in for
-    the full c tensor). v is passed in its own dtype; the library casts it to
-    bf16 for the products (kernel.py:205)."""
+# The operators below are registered torch ops (torch.library.custom_op) with
+# fake (meta) implementations and registered autograd, so torch.compile traces
+# models that use them without graph breaks: each op is one opaque node whose
+# output shapes the fake implementation gives. Their real implementations
+# launch the native kernels on the current stream. Outputs never alias inputs;
+# what a backward needs of an input's cast is recomputed from the input.
 
-    @staticmethod
-    def forward(ctx, r, v, g, w):
-        _check_fm(r, v, g, w)
-        B, T, A = r.shape
-        D = v.shape[-1]
-        r32 = r.float().contiguous()
-        vc = v.contiguous()
-        g1 = g.float().reshape(1).contiguous()
-        w32 = w.float().contiguous()
-        q = torch.empty_like(r32)
-        fast = torch.empty(B, T, D, device=r.device, dtype=v.dtype)
-        vdt = nat.dtype_code(v.dtype)
-        saved_bytes = nat.lib().ulm_fm_saved_bytes(B, T, A, D, vdt)
-        saved = torch.empty(saved_bytes, device=r.device, dtype=torch.uint8)
-        ws_bytes = nat.lib().ulm_fm_fwd_workspace_bytes(B, T, A, D, vdt)
-        ws = torch.empty(max(ws_bytes, 1), device=r.device, dtype=torch.uint8)
-        call("ulm_fm_fwd", ptr(r32), ptr(vc), vdt, ptr(g1), ptr(w32), ptr(q), ptr(fast), vdt, ptr(saved), saved_bytes,
-             ptr(ws), ws_bytes, B, T, A, D, nat.stream_of(r))
-        ctx.save_for_backward(r32, g1, w32, saved)
-        ctx.g_shape, ctx.D, ctx.vdt = g.shape, D, vdt
-        return q, fast
+Tensor = torch.Tensor
 
-    @staticmethod
-    def backward(ctx, dq_out, dfast):
-        r, g1, w, saved = ctx.saved_tensors
-        B, T, A = r.shape
-        D = ctx.D
-        if dfast is None:
-            dfast = torch.zeros(B, T, D, device=r.device, dtype=torch.float32)
-        ddt = nat.dtype_code(dfast.dtype)
-        dfast = dfast.contiguous()
-        dqo = dq_out.float().contiguous() if dq_out is not None else None
-        dr = torch.empty_like(r)
-        dv = torch.empty(B, T, D, device=r.device, dtype=dfast.dtype)
-        dg = torch.empty(1, device=r.device, dtype=torch.float32)
-        dw = torch.empty(A, device=r.device, dtype=torch.float32)
-        ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D, ddt)
-        ws = torch.empty(ws_bytes, device=r.device, dtype=torch.uint8)
-        call("ulm_fm_bwd", ptr(r), ptr(g1), ptr(w), ptr(saved), saved.numel(), ctx.vdt, ptr(dfast), ddt,
-             ptr(dqo), ptr(dr), ptr(dv), ddt, ptr(dg), ptr(dw), ptr(ws), ws_bytes, B, T, A, D, nat.stream_of(r))
-        return dr, dv, dg.reshape(ctx.g_shape), dw
+
+@torch.library.custom_op("ulm::fm_fwd", mutates_args=())
+def fm_fwd(r: Tensor, v: Tensor, g: Tensor, w: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """(q fp32, fast in v's dtype, saved uint8): ulm_fm_fwd."""
+    B, T, A = r.shape
+    D = v.shape[-1]
+    r32 = r.float().contiguous()
+    vc = v.contiguous()
+    g1 = g.float().reshape(1).contiguous()
+    w32 = w.float().contiguous()
+    q = torch.empty(B, T, A, device=r.device, dtype=torch.float32)
+    fast = torch.empty(B, T, D, device=r.device, dtype=v.dtype)
+    vdt = nat.dtype_code(v.dtype)
+    saved_bytes = nat.lib().ulm_fm_saved_bytes(B, T, A, D, vdt)
+    saved = torch.empty(saved_bytes, device=r.device, dtype=torch.uint8)
+    ws_bytes = nat.lib().ulm_fm_fwd_workspace_bytes(B, T, A, D, vdt)
+    ws = torch.empty(max(ws_bytes, 1), device=r.device, dtype=torch.uint8)
+    call("ulm_fm_fwd", ptr(r32), ptr(vc), vdt, ptr(g1), ptr(w32), ptr(q), ptr(fast), vdt, ptr(saved), saved_bytes,
+         ptr(ws), ws_bytes, B, T, A, D, nat.stream_of(r))
+    return q, fast, saved
+
+
+@fm_fwd.register_fake
+def _fm_fwd_fake(r, v, g, w):
+    B, T, A = r.shape
+    D = v.shape[-1]
+    saved_bytes = nat.lib().ulm_fm_saved_bytes(B, T, A, D, nat.dtype_code(v.dtype))
+    return (r.new_empty(B, T, A, dtype=torch.float32), v.new_empty(B, T, D),
+            r.new_empty(saved_bytes, dtype=torch.uint8))
+
+
+@torch.library.custom_op("ulm::fm_bwd", mutates_args=())
+def fm_bwd(r: Tensor, g: Tensor, w: Tensor, saved: Tensor, v_dtype: torch.dtype, dq_out: Optional[Tensor],
+           dfast: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(dr fp32, dv in dfast's dtype, dg (1,), dw (A,)): ulm_fm_bwd."""
+    B, T, A = r.shape
+    D = dfast.shape[-1]
+    r32 = r.float().contiguous()
+    g1 = g.float().reshape(1).contiguous()
+    w32 = w.float().contiguous()
+    ddt = nat.dtype_code(dfast.dtype)
+    dfast = dfast.contiguous()
+    dqo = dq_out.float().contiguous() if dq_out is not None else None
+    dr = torch.empty(B, T, A, device=r.device, dtype=torch.float32)
+    dv = torch.empty(B, T, D, device=r.device, dtype=dfast.dtype)
+    dg = torch.empty(1, device=r.device, dtype=torch.float32)
+    dw = torch.empty(A, device=r.device, dtype=torch.float32)
+    ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D, ddt)
+    ws = torch.empty(ws_bytes, device=r.device, dtype=torch.uint8)
+    call("ulm_fm_bwd", ptr(r32), ptr(g1), ptr(w32), ptr(saved), saved.numel(), nat.dtype_code(v_dtype), ptr(dfast),
+         ddt, ptr(dqo), ptr(dr), ptr(dv), ddt, ptr(dg), ptr(dw), ptr(ws), ws_bytes, B, T, A, D, nat.stream_of(r))
+    return dr, dv, dg, dw
+
+
+@fm_bwd.register_fake
+def _fm_bwd_fake(r, g, w, saved, v_dtype, dq_out, dfast):
+    B, T, A = r.shape
+    D = dfast.shape[-1]
+    return (r.new_empty(B, T, A, dtype=torch.float32), dfast.new_empty(B, T, D),
+            r.new_empty(1, dtype=torch.float32), r.new_empty(A, dtype=torch.float32))
+
+
+def _fm_setup(ctx, inputs, output):
+    r, v, g, w = inputs
+    _, _, saved = output
+    ctx.save_for_backward(r, g, w, saved)
+    ctx.v_dtype, ctx.D = v.dtype, v.shape[-1]
+    ctx.mark_non_differentiable(saved)
+
+
+def _fm_backward(ctx, dq_out, dfast, _dsaved):
+    r, g, w, saved = ctx.saved_tensors
+    if dfast is None:
+        dfast = r.new_zeros(*r.shape[:2], ctx.D, dtype=torch.float32)
+    dr, dv, dg, dw = fm_bwd(r, g, w, saved, ctx.v_dtype, dq_out, dfast)
+    return dr, dv, dg.reshape(g.shape), dw
+
+
+torch.library.register_autograd("ulm::fm_fwd", _fm_backward, setup_context=_fm_setup)
 
 
 def unified_memory(r, v, g, w):
-    """r: (B,T,M) read addresses, v: (B,T,D) values, g: scalar log decay, w: (M,) prior mass."""
-    return UnifiedMemory.apply(r, v, g, w)
+    """r: (B,T,M) read addresses, v: (B,T,D) values, g: scalar log decay, w: (M,) prior mass.
+    Returns (q fp32, fast in v's dtype) (kernel.py:236-238)."""
+    _check_fm(r, v, g, w)
+    q, fast, _ = fm_fwd(r, v, g, w)
+    return q, fast
+
+
+class UnifiedMemory:
+    """The reference's autograd Function (kernel.py:199-233) as a call
+    surface: apply(r, v, g, w) is unified_memory, whose backward is the
+    registered ulm::fm_bwd. The forward keeps one opaque buffer of what the
+    backward needs (bf16 operand tiles of q, k and v, score tiles and the
+    per-chunk evidence checkpoints that stand in for the full c tensor); v is
+    passed in its own dtype and cast to bf16 for the products inside
+    (kernel.py:205)."""
+
+    @staticmethod
+    def apply(r, v, g, w):
+        return unified_memory(r, v, g, w)
 
 
 def la(a, b, c, g, reverse=False, split=False):
@@ -126,52 +185,85 @@ def la(a, b, c, g, reverse=False, split=False):
 # ---------------------------------------------------------------------------
 # relu^2 slot address (model.py:70-72)
 
-class Relu2Address(torch.autograd.Function):
-    """r = z / (exp(clamp(log_eps,-10,10)) + sum_a z), z = relu(pre + bias)^2."""
+@torch.library.custom_op("ulm::addr_fwd", mutates_args=())
+def addr_fwd(pre: Tensor, bias: Optional[Tensor], log_eps: Tensor) -> tuple[Tensor, Tensor]:
+    """(r fp32 shaped like pre, denom (M,) fp32): ulm_addr_fwd."""
+    A = pre.shape[-1]
+    pre_c = pre.contiguous()
+    b32 = bias.float().contiguous() if bias is not None else None
+    le = log_eps.float().reshape(1).contiguous()
+    M = pre_c.numel() // A
+    r = torch.empty(pre.shape, device=pre.device, dtype=torch.float32)
+    denom = torch.empty(M, device=pre.device, dtype=torch.float32)
+    call("ulm_addr_fwd", ptr(pre_c), nat.dtype_code(pre.dtype), ptr(b32), ptr(le), ptr(r), ptr(denom), M, A,
+         nat.stream_of(pre))
+    return r, denom
 
-    @staticmethod
-    def forward(ctx, pre, bias, log_eps):
-        _check_float("pre", pre)
-        if pre.dim() < 1 or pre.numel() == 0:
-            raise ValueError(f"pre must be non-empty (..., A), got {tuple(pre.shape)}")
-        A = pre.shape[-1]
-        if bias is not None and bias.shape != (A,):
-            raise ValueError(f"bias must have shape ({A},), got {tuple(bias.shape)}")
-        if log_eps.numel() != 1:
-            raise ValueError("log_eps must hold one scalar")
-        nat.require_device(pre, bias, log_eps)
-        pdt = nat.dtype_code(pre.dtype)
-        pre_c = pre.contiguous()
-        b32 = bias.float().contiguous() if bias is not None else None
-        le = log_eps.float().reshape(1).contiguous()
-        M = pre_c.numel() // A
-        r = torch.empty(pre.shape, device=pre.device, dtype=torch.float32)
-        denom = torch.empty(M, device=pre.device, dtype=torch.float32)
-        call("ulm_addr_fwd", ptr(pre_c), pdt, ptr(b32), ptr(le), ptr(r), ptr(denom), M, A, nat.stream_of(pre))
-        ctx.save_for_backward(pre_c, b32, le, r, denom)
-        ctx.has_bias = bias is not None
-        ctx.le_shape = log_eps.shape
-        return r
 
-    @staticmethod
-    def backward(ctx, dr):
-        pre, b32, le, r, denom = ctx.saved_tensors
-        A = pre.shape[-1]
-        M = pre.numel() // A
-        dr = dr.float().contiguous()
-        dpre = torch.empty_like(pre)
-        dbias = torch.empty(A, device=pre.device, dtype=torch.float32) if ctx.has_bias else None
-        dle = torch.empty(1, device=pre.device, dtype=torch.float32)
-        ws_bytes = nat.lib().ulm_addr_bwd_workspace_bytes(M, A)
-        ws = torch.empty(ws_bytes, device=pre.device, dtype=torch.uint8)
-        call("ulm_addr_bwd", ptr(pre), nat.dtype_code(pre.dtype), ptr(b32), ptr(le), ptr(r), ptr(denom), ptr(dr),
-             ptr(dpre), ptr(dbias), ptr(dle), ptr(ws), ws_bytes, M, A, nat.stream_of(pre))
-        return dpre, dbias, dle.reshape(ctx.le_shape)
+@addr_fwd.register_fake
+def _addr_fwd_fake(pre, bias, log_eps):
+    return pre.new_empty(pre.shape, dtype=torch.float32), pre.new_empty(pre.numel() // pre.shape[-1],
+                                                                        dtype=torch.float32)
+
+
+@torch.library.custom_op("ulm::addr_bwd", mutates_args=())
+def addr_bwd(pre: Tensor, bias: Optional[Tensor], log_eps: Tensor, r: Tensor, denom: Tensor,
+             dr: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """(dpre in pre's dtype, dbias (A,) fp32 or (0,) without a bias, dlog_eps (1,)): ulm_addr_bwd."""
+    A = pre.shape[-1]
+    pre_c = pre.contiguous()
+    M = pre_c.numel() // A
+    b32 = bias.float().contiguous() if bias is not None else None
+    le = log_eps.float().reshape(1).contiguous()
+    dr = dr.float().contiguous()
+    dpre = torch.empty_like(pre_c)
+    dbias = torch.empty(A if bias is not None else 0, device=pre.device, dtype=torch.float32)
+    dle = torch.empty(1, device=pre.device, dtype=torch.float32)
+    ws_bytes = nat.lib().ulm_addr_bwd_workspace_bytes(M, A)
+    ws = torch.empty(ws_bytes, device=pre.device, dtype=torch.uint8)
+    call("ulm_addr_bwd", ptr(pre_c), nat.dtype_code(pre.dtype), ptr(b32), ptr(le), ptr(r.contiguous()),
+         ptr(denom), ptr(dr), ptr(dpre), ptr(dbias if bias is not None else None), ptr(dle), ptr(ws), ws_bytes,
+         M, A, nat.stream_of(pre))
+    return dpre, dbias, dle
+
+
+@addr_bwd.register_fake
+def _addr_bwd_fake(pre, bias, log_eps, r, denom, dr):
+    A = pre.shape[-1]
+    return (torch.empty_like(pre, memory_format=torch.contiguous_format),
+            pre.new_empty(A if bias is not None else 0, dtype=torch.float32), pre.new_empty(1, dtype=torch.float32))
+
+
+def _addr_setup(ctx, inputs, output):
+    pre, bias, log_eps = inputs
+    r, denom = output
+    ctx.save_for_backward(pre, bias, log_eps, r, denom)
+    ctx.mark_non_differentiable(denom)
+
+
+def _addr_backward(ctx, dr, _ddenom):
+    pre, bias, log_eps, r, denom = ctx.saved_tensors
+    dpre, dbias, dle = addr_bwd(pre, bias, log_eps, r, denom, dr)
+    return dpre, (dbias if bias is not None else None), dle.reshape(log_eps.shape)
+
+
+torch.library.register_autograd("ulm::addr_fwd", _addr_backward, setup_context=_addr_setup)
 
 
 def relu2_address(pre, bias, log_eps):
-    """The slot address of model.py:70-72 from pre = K u (bias added in fp32 inside)."""
-    return Relu2Address.apply(pre, bias, log_eps)
+    """The slot address of model.py:70-72 from pre = K u (the bias added in fp32
+    inside): r = z / (exp(clamp(log_eps,-10,10)) + sum_a z), z = relu(pre + bias)^2."""
+    _check_float("pre", pre)
+    if pre.dim() < 1 or pre.numel() == 0:
+        raise ValueError(f"pre must be non-empty (..., A), got {tuple(pre.shape)}")
+    A = pre.shape[-1]
+    if bias is not None and bias.shape != (A,):
+        raise ValueError(f"bias must have shape ({A},), got {tuple(bias.shape)}")
+    if log_eps.numel() != 1:
+        raise ValueError("log_eps must hold one scalar")
+    nat.dtype_code(pre.dtype)
+    nat.require_device(pre, bias, log_eps)
+    return addr_fwd(pre, bias, log_eps)[0]
 
 
 # ---------------------------------------------------------------------------
@@ -211,124 +303,194 @@ def _addmm_(c, a, b):
     return torch.addmm(c, a, b, out_dtype=c.dtype, out=c)
 
 
-class UnifiedBlockFn(torch.autograd.Function):
-    """out = x + mu(w q) + fast for one UnifiedBlock (model.py:77-85):
+# One UnifiedBlock (model.py:77-85) as two registered ops:
+#
+#     h, u   = RMSNorm(x), causal conv(h)               ulm_norm_conv_fwd
+#     pre, v = u K^T, h W_v^T                            GEMMs in cdt
+#     denom  = the relu^2 address's row sums of pre + b  ulm_addr_fwd (r not written)
+#     g, w   = -exp(log_rate), exp(clamp(log_w))         ulm_block_params
+#     wq, y  = w q, x + fast                             ulm_block_fm_fwd (r formed from pre)
+#     out    = y + wq mu^T                               GEMM accumulating into y
+#
+# cdt is the GEMM operand dtype: bf16 under bf16 autocast (the reference's
+# training configuration, train.py), fp32 otherwise. x is the fp32 residual
+# stream; every gradient is returned in fp32. The forward's extra outputs are
+# what the backward reads (the normalised input, the conv output, the key
+# GEMM's output, the address denominators, g and w, the fast memory's saved
+# buffer and w q).
 
-        h, u   = RMSNorm(x), causal conv(h)            ulm_norm_conv_fwd
-        pre, v = u K^T, h W_v^T                         GEMMs in cdt
-        denom  = the relu^2 address's row sums of pre + b  ulm_addr_fwd (r not written)
-        g, w   = -exp(log_rate), exp(clamp(log_w))      ulm_block_params
-        wq, y  = w q, x + fast                          ulm_block_fm_fwd (r formed from pre)
-        out    = y + wq mu^T                            GEMM accumulating into y
+_BLOCK_SAVED = 9   # outputs of block_fwd past `out`
 
-    cdt is the GEMM operand dtype: bf16 under bf16 autocast (the reference's
-    training configuration, train.py), fp32 otherwise. x is the fp32 residual
-    stream; every gradient is returned in fp32."""
 
-    @staticmethod
-    def forward(ctx, x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, norm_eps, cdt):
-        B, T, D = x.shape
-        A = key_w.shape[0]
-        Kc = conv_w.shape[-1]
-        M = B * T
-        dev = x.device
-        s = nat.stream_of(x)
-        cd = nat.dtype_code(cdt)
-        f32 = torch.float32
-        x32 = x.contiguous()
-        nw = norm_w.float().contiguous()
-        cw = conv_w.float().reshape(D, Kc).contiguous()
-        h = torch.empty(B, T, D, device=dev, dtype=cdt)
-        u = torch.empty(B, T, D, device=dev, dtype=cdt)
-        rstd = torch.empty(B, T, device=dev, dtype=f32)
-        call("ulm_norm_conv_fwd", ptr(x32), nat.ULM_F32, ptr(nw), ptr(cw), Kc, float(norm_eps), ptr(h), cd, ptr(u), cd,
-             ptr(rstd), B, T, D, s)
-        kw, vw, mw = (t.to(cdt).contiguous() for t in (key_w, val_w, mu_w))
-        pre = torch.mm(u.view(M, D), kw.t())
-        v = torch.mm(h.view(M, D), vw.t())
-        b32 = key_b.float().contiguous() if key_b is not None else None
-        le = log_eps.float().reshape(1).contiguous()
-        denom = torch.empty(M, device=dev, dtype=f32)
-        # r itself is never written: the fast memory forms it from pre, bias and denom
-        call("ulm_addr_fwd", ptr(pre), cd, ptr(b32), ptr(le), None, ptr(denom), M, A, s)
-        lr = log_rate.float().reshape(1).contiguous()
-        lw = log_w.float().contiguous()
-        g1 = torch.empty(1, device=dev, dtype=f32)
-        w32 = torch.empty(A, device=dev, dtype=f32)
-        call("ulm_block_params", ptr(lr), ptr(lw), LOG_W_MIN, LOG_W_MAX, A, ptr(g1), ptr(w32), s)
-        saved_bytes = nat.lib().ulm_fm_saved_bytes(B, T, A, D, cd)
-        saved = torch.empty(saved_bytes, device=dev, dtype=torch.uint8)
-        ws_bytes = nat.lib().ulm_block_fm_fwd_workspace_bytes(B, T, A, D)
-        ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
-        qw = torch.empty(M, A, device=dev, dtype=cdt)
-        y = torch.empty(M, D, device=dev, dtype=f32)
-        call("ulm_block_fm_fwd", ptr(pre), cd, ptr(b32), ptr(denom), ptr(v), cd, ptr(g1), ptr(w32), ptr(qw), cd,
-             ptr(x32), ptr(y), ptr(saved), saved_bytes, ptr(ws), ws_bytes, B, T, A, D, s)
-        del ws, v
-        out = _addmm_(y, qw, mw.t())
-        ctx.save_for_backward(x32, rstd, nw, cw, h, u, pre, b32, le, denom, lr, lw, g1, w32, saved, qw, kw, vw, mw)
-        ctx.meta = (B, T, A, D, Kc, cdt, conv_w.shape, log_eps.shape, log_rate.shape, key_b is not None)
-        return out.view(B, T, D)
+@torch.library.custom_op("ulm::block_fwd", mutates_args=())
+def block_fwd(x: Tensor, norm_w: Tensor, conv_w: Tensor, key_w: Tensor, key_b: Optional[Tensor], log_eps: Tensor,
+              val_w: Tensor, mu_w: Tensor, log_rate: Tensor, log_w: Tensor, norm_eps: float,
+              cdt: torch.dtype) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(out, rstd, h, u, pre, denom, g, w, saved, wq)."""
+    # the GEMM dtypes are explicit: autocast must not re-cast them
+    with torch.autocast("cuda", enabled=False):
+        return _block_fwd_impl(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, norm_eps, cdt)
 
-    @staticmethod
-    def backward(ctx, dout):
-        # the GEMM dtypes are explicit: no autocast re-casting in the backward
-        with torch.autocast("cuda", enabled=False):
-            return UnifiedBlockFn._backward(ctx, dout)
 
-    @staticmethod
-    def _backward(ctx, dout):
-        x32, rstd, nw, cw, h, u, pre, b32, le, denom, lr, lw, g1, w32, saved, qw, kw, vw, mw = ctx.saved_tensors
-        B, T, A, D, Kc, cdt, cw_shape, le_shape, lr_shape, has_bias = ctx.meta
-        M = B * T
-        dev = x32.device
-        s = nat.stream_of(x32)
-        cd = nat.dtype_code(cdt)
-        f32 = torch.float32
-        dout = dout.float().contiguous()
-        if cdt == f32:
-            d16 = dout
-        else:
-            d16 = torch.empty(B, T, D, device=dev, dtype=cdt)
-            call("ulm_cast", ptr(dout), nat.ULM_F32, ptr(d16), cd, M * D, s)
-        d2 = d16.view(M, D)
-        dqw = torch.mm(d2, mw)                       # d(w q) = dout mu
-        dmu = _wgrad(d2, qw)
-        dr = torch.empty(M, A, device=dev, dtype=f32)
-        dv = torch.empty(M, D, device=dev, dtype=cdt)
-        dg = torch.empty(1, device=dev, dtype=f32)
-        dw = torch.empty(A, device=dev, dtype=f32)
-        ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D, cd)
-        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
-        call("ulm_block_fm_bwd", ptr(pre), cd, ptr(b32), ptr(denom), ptr(g1), ptr(w32), ptr(saved), saved.numel(), cd,
-             ptr(d16), cd, ptr(dqw), cd, ptr(dr), ptr(dv), cd, ptr(dg), ptr(dw), ptr(ws), ws_bytes, B, T, A, D, s)
-        del ws, dqw
-        dlr = torch.empty(1, device=dev, dtype=f32)
-        dlw = torch.empty(A, device=dev, dtype=f32)
-        call("ulm_block_params_bwd", ptr(lr), ptr(lw), LOG_W_MIN, LOG_W_MAX, ptr(dg), ptr(dw), A, ptr(dlr), ptr(dlw), s)
-        dpre = torch.empty_like(pre)
-        dbias = torch.empty(A, device=dev, dtype=f32) if has_bias else None
-        dle = torch.empty(1, device=dev, dtype=f32)
-        ws_bytes = nat.lib().ulm_addr_bwd_workspace_bytes(M, A)
-        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
-        call("ulm_addr_bwd", ptr(pre), cd, ptr(b32), ptr(le), None, ptr(denom), ptr(dr), ptr(dpre), ptr(dbias),
-             ptr(dle), ptr(ws), ws_bytes, M, A, s)
-        del ws, dr
-        du = _mm(dpre, kw, f32)
-        dkey = _wgrad(dpre, u.view(M, D))
-        dhv = _mm(dv, vw, f32)
-        dval = _wgrad(dv, h.view(M, D))
-        dx = torch.empty(B, T, D, device=dev, dtype=f32)
-        dnw = torch.empty(D, device=dev, dtype=f32)
-        dcw = torch.empty(D, Kc, device=dev, dtype=f32)
-        ws_bytes = nat.lib().ulm_norm_conv_bwd_workspace_bytes(B, T, D, Kc)
-        if ws_bytes == 0:
-            raise ValueError(f"ulm_norm_conv_bwd: unsupported D={D}")
-        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
-        call("ulm_norm_conv_bwd", ptr(x32), nat.ULM_F32, ptr(rstd), ptr(nw), ptr(cw), Kc, ptr(du), nat.ULM_F32, ptr(dhv),
-             nat.ULM_F32, ptr(dout), ptr(dx), ptr(dnw), ptr(dcw), ptr(ws), ws_bytes, B, T, D, s)
-        return (dx, dnw, dcw.view(cw_shape), dkey, dbias, dle.reshape(le_shape), dval, dmu, dlr.reshape(lr_shape), dlw,
-                None, None)
+def _block_fwd_impl(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, norm_eps, cdt):
+    B, T, D = x.shape
+    A = key_w.shape[0]
+    Kc = conv_w.shape[-1]
+    M = B * T
+    dev = x.device
+    s = nat.stream_of(x)
+    cd = nat.dtype_code(cdt)
+    f32 = torch.float32
+    x32 = x.contiguous()
+    nw = norm_w.float().contiguous()
+    cw = conv_w.float().reshape(D, Kc).contiguous()
+    h = torch.empty(B, T, D, device=dev, dtype=cdt)
+    u = torch.empty(B, T, D, device=dev, dtype=cdt)
+    rstd = torch.empty(B, T, device=dev, dtype=f32)
+    call("ulm_norm_conv_fwd", ptr(x32), nat.ULM_F32, ptr(nw), ptr(cw), Kc, float(norm_eps), ptr(h), cd, ptr(u), cd,
+         ptr(rstd), B, T, D, s)
+    kw, vw, mw = (t.to(cdt).contiguous() for t in (key_w, val_w, mu_w))
+    pre = torch.mm(u.view(M, D), kw.t())
+    v = torch.mm(h.view(M, D), vw.t())
+    b32 = key_b.float().contiguous() if key_b is not None else None
+    le = log_eps.float().reshape(1).contiguous()
+    denom = torch.empty(M, device=dev, dtype=f32)
+    # r itself is never written: the fast memory forms it from pre, bias and denom
+    call("ulm_addr_fwd", ptr(pre), cd, ptr(b32), ptr(le), None, ptr(denom), M, A, s)
+    lr = log_rate.float().reshape(1).contiguous()
+    lw = log_w.float().contiguous()
+    g1 = torch.empty(1, device=dev, dtype=f32)
+    w32 = torch.empty(A, device=dev, dtype=f32)
+    call("ulm_block_params", ptr(lr), ptr(lw), LOG_W_MIN, LOG_W_MAX, A, ptr(g1), ptr(w32), s)
+    saved_bytes = nat.lib().ulm_fm_saved_bytes(B, T, A, D, cd)
+    saved = torch.empty(saved_bytes, device=dev, dtype=torch.uint8)
+    ws_bytes = nat.lib().ulm_block_fm_fwd_workspace_bytes(B, T, A, D)
+    ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    qw = torch.empty(M, A, device=dev, dtype=cdt)
+    y = torch.empty(M, D, device=dev, dtype=f32)
+    call("ulm_block_fm_fwd", ptr(pre), cd, ptr(b32), ptr(denom), ptr(v), cd, ptr(g1), ptr(w32), ptr(qw), cd,
+         ptr(x32), ptr(y), ptr(saved), saved_bytes, ptr(ws), ws_bytes, B, T, A, D, s)
+    del ws, v
+    out = _addmm_(y, qw, mw.t())
+    return out.view(B, T, D), rstd, h, u, pre, denom, g1, w32, saved, qw
+
+
+@block_fwd.register_fake
+def _block_fwd_fake(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, norm_eps, cdt):
+    B, T, D = x.shape
+    A = key_w.shape[0]
+    M = B * T
+    f32 = torch.float32
+    saved_bytes = nat.lib().ulm_fm_saved_bytes(B, T, A, D, nat.dtype_code(cdt))
+    e = x.new_empty
+    return (e(B, T, D, dtype=f32), e(B, T, dtype=f32), e(B, T, D, dtype=cdt), e(B, T, D, dtype=cdt),
+            e(M, A, dtype=cdt), e(M, dtype=f32), e(1, dtype=f32), e(A, dtype=f32), e(saved_bytes, dtype=torch.uint8),
+            e(M, A, dtype=cdt))
+
+
+@torch.library.custom_op("ulm::block_bwd", mutates_args=())
+def block_bwd(dout: Tensor, x: Tensor, norm_w: Tensor, conv_w: Tensor, key_w: Tensor, key_b: Optional[Tensor],
+              log_eps: Tensor, val_w: Tensor, mu_w: Tensor, log_rate: Tensor, log_w: Tensor, rstd: Tensor, h: Tensor,
+              u: Tensor, pre: Tensor, denom: Tensor, g1: Tensor, w32: Tensor, saved: Tensor, qw: Tensor,
+              cdt: torch.dtype) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+                                         Tensor]:
+    """(dx, dnorm_w, dconv_w, dkey_w, dkey_b ((0,) without a bias), dlog_eps,
+    dval_w, dmu_w, dlog_rate, dlog_w), all fp32."""
+    with torch.autocast("cuda", enabled=False):
+        return _block_bwd_impl(dout, x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, rstd, h,
+                               u, pre, denom, g1, w32, saved, qw, cdt)
+
+
+def _block_bwd_impl(dout, x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, rstd, h, u, pre,
+                    denom, g1, w32, saved, qw, cdt):
+    B, T, D = x.shape
+    A = key_w.shape[0]
+    Kc = conv_w.shape[-1]
+    M = B * T
+    dev = x.device
+    s = nat.stream_of(x)
+    cd = nat.dtype_code(cdt)
+    f32 = torch.float32
+    x32 = x.contiguous()
+    nw = norm_w.float().contiguous()
+    cw = conv_w.float().reshape(D, Kc).contiguous()
+    kw, vw, mw = (t.to(cdt).contiguous() for t in (key_w, val_w, mu_w))
+    b32 = key_b.float().contiguous() if key_b is not None else None
+    le = log_eps.float().reshape(1).contiguous()
+    lr = log_rate.float().reshape(1).contiguous()
+    lw = log_w.float().contiguous()
+    dout = dout.float().contiguous()
+    if cdt == f32:
+        d16 = dout
+    else:
+        d16 = torch.empty(B, T, D, device=dev, dtype=cdt)
+        call("ulm_cast", ptr(dout), nat.ULM_F32, ptr(d16), cd, M * D, s)
+    d2 = d16.view(M, D)
+    dqw = torch.mm(d2, mw)                       # d(w q) = dout mu
+    dmu = _wgrad(d2, qw)
+    dr = torch.empty(M, A, device=dev, dtype=f32)
+    dv = torch.empty(M, D, device=dev, dtype=cdt)
+    dg = torch.empty(1, device=dev, dtype=f32)
+    dw = torch.empty(A, device=dev, dtype=f32)
+    ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D, cd)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    call("ulm_block_fm_bwd", ptr(pre), cd, ptr(b32), ptr(denom), ptr(g1), ptr(w32), ptr(saved), saved.numel(), cd,
+         ptr(d16), cd, ptr(dqw), cd, ptr(dr), ptr(dv), cd, ptr(dg), ptr(dw), ptr(ws), ws_bytes, B, T, A, D, s)
+    del ws, dqw
+    dlr = torch.empty(1, device=dev, dtype=f32)
+    dlw = torch.empty(A, device=dev, dtype=f32)
+    call("ulm_block_params_bwd", ptr(lr), ptr(lw), LOG_W_MIN, LOG_W_MAX, ptr(dg), ptr(dw), A, ptr(dlr), ptr(dlw), s)
+    dpre = torch.empty_like(pre)
+    dbias = torch.empty(A if key_b is not None else 0, device=dev, dtype=f32)
+    dle = torch.empty(1, device=dev, dtype=f32)
+    ws_bytes = nat.lib().ulm_addr_bwd_workspace_bytes(M, A)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    call("ulm_addr_bwd", ptr(pre), cd, ptr(b32), ptr(le), None, ptr(denom), ptr(dr), ptr(dpre),
+         ptr(dbias if key_b is not None else None), ptr(dle), ptr(ws), ws_bytes, M, A, s)
+    del ws, dr
+    du = _mm(dpre, kw, f32)
+    dkey = _wgrad(dpre, u.view(M, D))
+    dhv = _mm(dv, vw, f32)
+    dval = _wgrad(dv, h.view(M, D))
+    dx = torch.empty(B, T, D, device=dev, dtype=f32)
+    dnw = torch.empty(D, device=dev, dtype=f32)
+    dcw = torch.empty(D, Kc, device=dev, dtype=f32)
+    ws_bytes = nat.lib().ulm_norm_conv_bwd_workspace_bytes(B, T, D, Kc)
+    if ws_bytes == 0:
+        raise ValueError(f"ulm_norm_conv_bwd: unsupported D={D}")
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    call("ulm_norm_conv_bwd", ptr(x32), nat.ULM_F32, ptr(rstd), ptr(nw), ptr(cw), Kc, ptr(du), nat.ULM_F32, ptr(dhv),
+         nat.ULM_F32, ptr(dout), ptr(dx), ptr(dnw), ptr(dcw), ptr(ws), ws_bytes, B, T, D, s)
+    return (dx, dnw, dcw.view(conv_w.shape), dkey, dbias, dle.reshape(log_eps.shape), dval, dmu,
+            dlr.reshape(log_rate.shape), dlw)
+
+
+@block_bwd.register_fake
+def _block_bwd_fake(dout, x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, rstd, h, u, pre,
+                    denom, g1, w32, saved, qw, cdt):
+    f32 = torch.float32
+    A = key_w.shape[0]
+    e = x.new_empty
+    return (e(x.shape, dtype=f32), e(norm_w.shape, dtype=f32), e(conv_w.shape, dtype=f32), e(key_w.shape, dtype=f32),
+            e(A if key_b is not None else 0, dtype=f32), e(log_eps.shape, dtype=f32), e(val_w.shape, dtype=f32),
+            e(mu_w.shape, dtype=f32), e(log_rate.shape, dtype=f32), e(log_w.shape, dtype=f32))
+
+
+def _block_setup(ctx, inputs, output):
+    x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, norm_eps, cdt = inputs
+    ctx.save_for_backward(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, *output[1:])
+    ctx.cdt = cdt
+    ctx.mark_non_differentiable(*output[1:])
+
+
+def _block_backward(ctx, dout, *_unused):
+    saved = ctx.saved_tensors
+    key_b = saved[4]
+    dx, dnw, dcw, dkey, dbias, dle, dval, dmu, dlr, dlw = block_bwd(dout, *saved, ctx.cdt)
+    return dx, dnw, dcw, dkey, (dbias if key_b is not None else None), dle, dval, dmu, dlr, dlw, None, None
+
+
+torch.library.register_autograd("ulm::block_fwd", _block_backward, setup_context=_block_setup)
 
 
 def unified_block(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, norm_eps,
@@ -353,18 +515,17 @@ def unified_block(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rat
     if cdt not in (torch.float32, torch.bfloat16, torch.float16):
         raise ValueError(f"unsupported GEMM dtype {cdt}")
     nat.require_device(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w)
-    return UnifiedBlockFn.apply(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, norm_eps, cdt)
+    return block_fwd(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, float(norm_eps), cdt)[0]
 
 
 # ---------------------------------------------------------------------------
 # per-token decode (model.py:96-111), N sequences at once, fp32
 
 @torch.no_grad()
-@torch.no_grad()
 def block_prefill(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, norm_eps,
                   cdt=torch.float32):
     """UnifiedBlock.forward over a prompt (no autograd), fused as in
-    UnifiedBlockFn, plus what decoding continues from: returns (out, S, c,
+    block_fwd, plus what decoding continues from: returns (out, S, c,
     r_prev, h) with S (B, D, A) and c (B, A) the fast-memory state after the
     last position (as fm_prefill), r_prev (B, A) fp32 the address at that
     position and h (B, T, D) the normalised input in cdt (its last positions

@@ -128,10 +128,14 @@ def _fm_setup(ctx, inputs, output):
     ctx.save_for_backward(r, g, w, saved)
     ctx.v_dtype, ctx.D = v.dtype, v.shape[-1]
     ctx.mark_non_differentiable(saved)
+    # no zero-filled stand-ins for absent gradients (the saved buffer's above all)
+    ctx.set_materialize_grads(False)
 
 
 def _fm_backward(ctx, dq_out, dfast, _dsaved):
     r, g, w, saved = ctx.saved_tensors
+    if dq_out is None and dfast is None:
+        return None, None, None, None
     if dfast is None:
         dfast = r.new_zeros(*r.shape[:2], ctx.D, dtype=torch.float32)
     dr, dv, dg, dw = fm_bwd(r, g, w, saved, ctx.v_dtype, dq_out, dfast)
@@ -239,9 +243,12 @@ def _addr_setup(ctx, inputs, output):
     r, denom = output
     ctx.save_for_backward(pre, bias, log_eps, r, denom)
     ctx.mark_non_differentiable(denom)
+    ctx.set_materialize_grads(False)
 
 
 def _addr_backward(ctx, dr, _ddenom):
+    if dr is None:
+        return None, None, None
     pre, bias, log_eps, r, denom = ctx.saved_tensors
     dpre, dbias, dle = addr_bwd(pre, bias, log_eps, r, denom, dr)
     return dpre, (dbias if bias is not None else None), dle.reshape(log_eps.shape)
@@ -481,9 +488,13 @@ def _block_setup(ctx, inputs, output):
     ctx.save_for_backward(x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w, log_rate, log_w, *output[1:])
     ctx.cdt = cdt
     ctx.mark_non_differentiable(*output[1:])
+    # the extra outputs never get gradients: no zero-filled stand-ins for them
+    ctx.set_materialize_grads(False)
 
 
 def _block_backward(ctx, dout, *_unused):
+    if dout is None:
+        return (None,) * 12
     saved = ctx.saved_tensors
     key_b = saved[4]
     dx, dnw, dcw, dkey, dbias, dle, dval, dmu, dlr, dlw = block_bwd(dout, *saved, ctx.cdt)

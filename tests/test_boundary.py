@@ -59,8 +59,10 @@ def test_workspace_sizes(monkeypatch):
     Tq = (T + 127) // 128 * 128
     for dt in (nat.ULM_BF16, nat.ULM_F32):
         assert lib.ulm_fm_saved_bytes(B, T, A, D, dt) >= B * T * (4 * A + 2 * D) + 3 * B * Tq * Tq * 2 + B * NT * A * 4
-    # backward: fp32 dq_f and dk_f, two tiled dfast copies, dS and its transpose
-    assert lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32) >= B * T * (8 * A + 4 * D) + 2 * B * Tq * Tq * 2
+    # backward: two tiled dfast copies, dS and its transpose, the per-tile statistics;
+    # dq_f and dk_f stay in the products' epilogues (no fp32 (B, T, A) copies)
+    nbw = lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32)
+    assert B * T * 4 * D + 2 * B * Tq * Tq * 2 <= nbw < B * T * 4 * D + 2 * B * Tq * Tq * 2 + B * T * 4 * A
     assert (lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32)
             == lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16))
     monkeypatch.setenv("ULM_FM_PATH", "chunked")

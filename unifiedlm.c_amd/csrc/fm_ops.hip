@@ -75,11 +75,12 @@ double pair_flops_per_token(int B, int T, int A, int D);
 int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *vQ, const float *g, uint16_t *P,
                         uint16_t *Pt, uint16_t *Plo, void *out, int out_dt, const float *resid, int B, int T, int A,
                         int D, hipStream_t s);
+size_t pair_stats_bytes(int B, int T, int A);
 int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t *doQ, const uint16_t *kQ,
                          const uint16_t *qQ, const uint16_t *P, const uint16_t *Pt, const uint16_t *Plo,
-                         const float *g, uint16_t *dS,
-                         uint16_t *dSt, double *dg_part, float *dqf, float *dkf, void *dv, int dv_dt, int B, int T,
-                         int A, int D, hipStream_t s);
+                         const float *g, uint16_t *dS, uint16_t *dSt, double *dg_part, const RSrc &r,
+                         const void *xq, int xq_kind, const float *nck, const float *w, float *dr, float *dw,
+                         float *dg, void *ws, void *dv, int dv_dt, int B, int T, int A, int D, hipStream_t s);
 
 namespace {
 
@@ -200,6 +201,7 @@ struct BwdWs {
     uint16_t *doR, *doRl, *doQ, *doQl, *Pdq, *Pdk;   // K-group path (pair: doR, doQ)
     uint16_t *dS, *dSt;                                      // pair path: the score gradients, transposed
     double *dgx;                                             // pair path: dg partials of the pair products
+    void *pstats;                                            // pair path: the fused statistics' arrays
     float *dqf, *dkf, *part;
     void *stats;
     size_t bytes;
@@ -210,8 +212,10 @@ BwdWs bwd_layout(void *base, int B, int T, int A, int D, int dfast_dtype, Path p
     const size_t td = B * NT * 64 * D;
     Carver c(base);
     BwdWs w{};
-    w.dqf = c.take<float>(na);
-    w.dkf = c.take<float>(na);
+    if (path != PATH_PAIR) {   // the pair path never materialises dq_f, dk_f
+        w.dqf = c.take<float>(na);
+        w.dkf = c.take<float>(na);
+    }
     if (path == PATH_PAIR) {
         const size_t tdp = B * NT * 64 * pad32(D);
         w.doR = c.take<uint16_t>(tdp);
@@ -219,6 +223,7 @@ BwdWs bwd_layout(void *base, int B, int T, int A, int D, int dfast_dtype, Path p
         w.dS = c.take<uint16_t>(pair_p_bytes(B, T) / 2);
         w.dSt = c.take<uint16_t>(pair_p_bytes(B, T) / 2);
         w.dgx = c.take<double>(pair_dscore_jobs(B, T));
+        w.pstats = c.take<char>(pair_stats_bytes(B, T, A));
     } else if (path == PATH_CHUNKED) {
         w.doR = c.take<uint16_t>(td);
         if (dfast_dtype != ULM_BF16) w.doRl = c.take<uint16_t>(td);
@@ -238,7 +243,7 @@ BwdWs bwd_layout(void *base, int B, int T, int A, int D, int dfast_dtype, Path p
                                    la_generic_parts(A) > 1 ? la_generic_parts(A) * nd : 0);
         if (gp) w.gpart = c.take<float>(gp);
     }
-    w.stats = c.take<char>(bwd_stats_partial_bytes(B, A));
+    if (path != PATH_PAIR) w.stats = c.take<char>(bwd_stats_partial_bytes(B, A));
     w.bytes = c.off;
     return w;
 }
@@ -448,10 +453,13 @@ int fm_backward(const RSrc &r, const float *g, const float *w, const void *saved
     const size_t nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
     if (path == PATH_PAIR) {
         ULM_TRY(launch_chunk_transpose(dfast, dfast_dtype, ws.doQ, nullptr, ws.doR, nullptr, B, T, D, s, pad32(D)));
-        ULM_TRY(launch_pair_backward(sv.vR, ws.doR, ws.doQ, sv.kQ, sv.qQ, sv.P, sv.Pt, sv.Plo, g, ws.dS, ws.dSt, ws.dgx, ws.dqf,
-                                     ws.dkf, dv, dv_dtype, B, T, A, D, s));
-        return launch_bwd_stats(ws.dqf, dq_out, r, sv.nck, w, g, ws.dkf, dr, dw, dg, ws.stats, B, T, A, s, dqw, dqw_dt,
-                                ws.dgx, pair_dscore_jobs(B, T));
+        // the statistics run in the dq_f and dk_f products' epilogues
+        const void *xq = dqw ? dqw : static_cast<const void *>(dq_out);
+        const int xq_kind = dqw ? 2 + dqw_dt : (dq_out ? 1 : 0);
+        if (dqw && dq_out) return fail(ULM_ERR_INVALID, "fm backward: dq_out and d(w q) are exclusive");
+        return launch_pair_backward(sv.vR, ws.doR, ws.doQ, sv.kQ, sv.qQ, sv.P, sv.Pt, sv.Plo, g, ws.dS, ws.dSt,
+                                    ws.dgx, r, xq, xq_kind, sv.nck, w, dr, dw, dg, ws.pstats, dv, dv_dtype, B, T, A,
+                                    D, s);
     }
     if (path == PATH_CHUNKED) {
         const int nkd = la_kgroup_groups(D), nka = la_kgroup_groups(A);

@@ -341,10 +341,14 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
         for (int i = kSeg - 1; i >= 0; --i) {
             // q = r / c, recomputed with the forward's operations (c is rebuilt
             // exactly from its checkpoint), so q is not read back from HBM
+            // q with the forward's exact division; the two gradient quotients
+            // by c take the hardware reciprocal (about 1 ulp), a third of the
+            // instructions of a correctly rounded division each
             const float qt = rv[i] / cv[i];
+            const float ic = __builtin_amdgcn_rcpf(cv[i]);
             const float dq = dqfv[i] + (XQ == 1 ? xv[i] : wa * xv[i]);
-            const float dc = -dq * qt / cv[i];
-            dqc[i] = dq / cv[i];
+            const float dc = -(dq * qt) * ic;
+            dqc[i] = dq * ic;
             racc = dc + lam * racc;
             rl[i] = racc;
             dw_acc += dc;

@@ -86,7 +86,10 @@ struct Mat {
     int nrt, nkt;
 };
 
-enum Epi { EPI_SCORES = 0, EPI_DSCORES = 1, EPI_ROWS = 2 };
+enum Epi { EPI_SCORES = 0, EPI_DSCORES = 1, EPI_ROWS = 2, EPI_DQSTATS = 3 };
+// EPI_ROWS output kinds: OUT % 3 = the ulm_dtype of the output, 3..5 the same
+// plus an fp32 residual, OUT_DRADD the backward's dr accumulation of dk_f
+constexpr int OUT_DRADD = 6;
 enum KRange { K_FULL = 0, K_CAUSAL = 1, K_ANTI = 2 };
 
 struct Args {
@@ -110,6 +113,19 @@ struct Args {
     void *out;
     int out_dt, F, nperm;    // nperm: B's rows are features in the order perm32 within 32-blocks
     const float *resid;      // fp32 (B, T, F) added, or null
+    // EPI_DQSTATS (dq_f with the backward statistics) and OUT_DRADD (dk_f into dr)
+    const float *r;          // r (B, T, A) fp32, or null: r = relu(pre + bias)^2 / denom
+    const void *pre;
+    int pre_dt;
+    const float *bias, *denom;
+    const void *xq;          // the extra gradient of q: xq_kind 0 none, 1 dq_out fp32, 2 + dtype d(w q)
+    int xq_kind;
+    const float *nck, *w;    // n at every 64-position chunk start (B, NT, A); the prior mass
+    int NT;
+    float *dr;               // (B, T, A)
+    float *tS, *tK, *tW;     // per (batch row, 128-position tile, slot) statistics, (B, MT, A)
+    const float *tC;         // OUT_DRADD: the carry of dkc into each tile
+    int MT;
 };
 
 // tile job -> (m-tile, n-tile) of one batch row
@@ -409,6 +425,178 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
             __syncthreads();
             if (threadIdx.x == 0) p.dg_part[logical] = (red[0] + red[1]) + (red[2] + red[3]);
         }
+    } else if constexpr (EPI == EPI_DQSTATS) {
+        // The per-slot statistics of the backward for this tile's 128 positions
+        // (t) and 128 slots (a), from dq_f in the accumulators (the recurrences
+        // of fm_stats.hip's backward, kernel.py:142-178):
+        //   c_t  = w + n_t, n from the chunk checkpoint as the forward forms it
+        //   dq   = dq_f + dq_out (or + w d(w q)),  dc = -dq q / c,  q = r / c
+        //   L_t  = sum_{t <= t' in this tile} lam^(t'-t) dc_t'   (dkc without
+        //          the carry from later tiles)
+        //   dr_t = dq_t / c_t + L_{t+1}        (dk_f and the carry are added by
+        //                                       the dk_f product, OUT_DRADD)
+        // and per (row, tile, slot) S = L at the tile start, K = sum_t (t - tau)
+        // k_t lam^(tile end - t) (the carry's share of the decay gradient), W =
+        // the tile's part of dw; the tile's own part of the decay gradient,
+        // sum_t (t - tau) (dc (c - w) - k L), goes to dg_part. The k L term is
+        // summed as sum_t' dc_t' V_t' with V_t' = sum_{t <= t'} (t - tau) k_t
+        // lam^(t' - t), a forward scan like n.
+        // Layout: four rounds of 32 slots; thread (segment j = tid / 32, slot
+        // column tid % 32) holds positions 16 j .. 16 j + 15 of the tile (chunk
+        // j / 4, that chunk's 16-position segment j % 4, as the forward
+        // statistics split it), so that c is formed with the forward's
+        // operations; segments meet through LDS.
+        static_assert(TM == 128 && TN == 128 && WAVES * 64 == 256, "statistics epilogue: 128 x 128 tiles");
+        constexpr int SEG = 16, NSEG = TM / SEG;
+        __shared__ float xa[NSEG][32], xb[NSEG][32];
+        __shared__ double xg[WAVES];
+        float *F = reinterpret_cast<float *>(lds);   // [128 t][128 a] fp32: the 64 KB of stage memory
+        __syncthreads();                             // every wave past its last operand read
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const int n = wn * (TN / 2) + 32 * j + lc;
+            const int fl = (n & ~31) + perm32(n & 31);   // the B operand's rows are slots in perm32 order
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) F[(wm * (TM / 2) + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * 128 + fl] = acc[i][j][r];
+        }
+        __syncthreads();
+        const int sj = threadIdx.x / 32, col = threadIdx.x % 32;
+        const int tl0 = SEG * sj, t0 = m0 + tl0;    // this thread's first position
+        const int cs = (sj / 4) * 4;                // the first segment of its chunk
+        const float g = p.g[0];
+        const float lam = __expf(g);
+        float lam16 = 1.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) lam16 *= lam;
+        const double tau = 0.5 * (p.T - 1);
+        const size_t brow = static_cast<size_t>(b) * p.T;
+        const bool xw = p.xq_kind >= 2;   // d(w q): dq gets w d(w q), dw gets q d(w q)
+        double dg_acc = 0.0;
+        for (int round = 0; round < 4; ++round) {
+            const int al = 32 * round + col;
+            const int a = n0 + al;
+            const bool va = a < p.F;
+            const uint32_t ac = va ? a : 0;
+            const float wa = va ? p.w[ac] : 1.f;
+            const float ba = (va && p.bias) ? p.bias[ac] : 0.f;
+            // r at positions t0 - 1 .. t0 + 15 (0 outside 0 <= t < T and past the
+            // slots), formed as the forward's statistics form it
+            float rv[SEG + 1];
+#pragma unroll
+            for (int i = 0; i <= SEG; ++i) {
+                const int t = t0 - 1 + i;
+                const bool ok = va && t >= 0 && t < p.T;
+                const size_t row = brow + (ok ? t : 0);
+                float v;
+                if (p.r) {
+                    v = p.r[row * p.F + ac];
+                } else {
+                    float x;
+                    if (p.pre_dt == ULM_BF16) x = bf16_to_f32(static_cast<const uint16_t *>(p.pre)[row * p.F + ac]);
+                    else if (p.pre_dt == ULM_F32) x = static_cast<const float *>(p.pre)[row * p.F + ac];
+                    else x = static_cast<float>(static_cast<const _Float16 *>(p.pre)[row * p.F + ac]);
+                    x += ba;
+                    x = x > 0.f ? x : 0.f;
+                    v = (x * x) * (1.f / p.denom[row]);
+                }
+                rv[i] = ok ? v : 0.f;
+            }
+            float xv[SEG];
+#pragma unroll
+            for (int i = 0; i < SEG; ++i) {
+                const int t = t0 + i;
+                const bool ok = va && t < p.T && p.xq_kind;
+                const size_t el = (brow + (ok ? t : 0)) * p.F + ac;
+                float v = 0.f;
+                if (p.xq_kind == 1 || p.xq_kind == 2 + ULM_F32) v = static_cast<const float *>(p.xq)[el];
+                else if (p.xq_kind == 2 + ULM_BF16) v = bf16_to_f32(static_cast<const uint16_t *>(p.xq)[el]);
+                else if (p.xq_kind == 2 + ULM_F16) v = static_cast<float>(static_cast<const _Float16 *>(p.xq)[el]);
+                xv[i] = ok ? v : 0.f;
+            }
+            // local scans of n (k_t = r_{t-1}) and of V from the segment start
+            float nl[SEG], vl[SEG];
+            float an = 0.f, av = 0.f;
+#pragma unroll
+            for (int i = 0; i < SEG; ++i) {
+                const float k = t0 + i < p.T ? rv[i] : 0.f;
+                an = lam * an + rv[i];
+                nl[i] = an;
+                av = lam * av + static_cast<float>(static_cast<double>(t0 + i) - tau) * k;
+                vl[i] = av;
+            }
+            xa[sj][col] = an;
+            xb[sj][col] = av;
+            __syncthreads();
+            // n at the segment start: the chunk checkpoint and the chunk's earlier
+            // segments; V at the segment start: the tile's earlier segments
+            float cj = va ? p.nck[(static_cast<size_t>(b) * p.NT + t0 / 64) * p.F + ac] : 0.f;
+            for (int m = cs; m < sj; ++m) cj = lam16 * cj + xa[m][col];
+            float vin = 0.f;
+            for (int m = 0; m < sj; ++m) vin = lam16 * vin + xb[m][col];
+            // c, q, dq, dc; dc back into F; the local parts of dw and dg
+            float dqc[SEG];
+            float dw_acc = 0.f, pw = lam, ecar = 0.f;
+#pragma unroll
+            for (int i = 0; i < SEG; ++i) {
+                const int tl = tl0 + i;
+                const float c = wa + (pw * cj + nl[i]);
+                const float q = rv[i + 1] / c;
+                const float ic = __builtin_amdgcn_rcpf(c);
+                const float dq = F[tl * 128 + al] + (xw ? wa * xv[i] : xv[i]);
+                const float dc = -(dq * q) * ic;
+                dqc[i] = dq * ic;
+                F[tl * 128 + al] = dc;
+                dw_acc += dc;
+                if (xw) dw_acc += q * xv[i];
+                ecar += pw * dc;   // sum_i lam^(i+1) dc_i: the earlier segments' V reach t0 + i as lam^(i+1) vin
+                dg_acc += (static_cast<double>(t0 + i) - tau) * static_cast<double>(dc * (c - wa)) -
+                          static_cast<double>(dc * vl[i]);
+                pw *= lam;
+            }
+            dg_acc -= static_cast<double>(vin) * static_cast<double>(ecar);
+            __syncthreads();   // xa, xb read
+            // reverse: the local scan of dc, the segments' totals through LDS
+            float rl[SEG];
+            float racc = 0.f;
+#pragma unroll
+            for (int i = SEG - 1; i >= 0; --i) {
+                racc = F[(tl0 + i) * 128 + al] + lam * racc;
+                rl[i] = racc;
+            }
+            xa[sj][col] = racc;
+            xb[sj][col] = dw_acc;
+            __syncthreads();
+            float rj = 0.f;   // L at the first position after this segment
+            for (int m = NSEG - 1; m > sj; --m) rj = xa[m][col] + lam16 * rj;
+            // dr_t = dq_t / c_t + L_{t+1}, L_{t+1} = rl[i+1] + lam^(15-i) rj
+            float pr = 1.f;
+#pragma unroll
+            for (int i = SEG - 1; i >= 0; --i) {
+                const float lnext = (i + 1 < SEG ? rl[i + 1] : 0.f) + pr * rj;
+                const int t = t0 + i;
+                if (va && t < p.T) p.dr[(brow + t) * p.F + a] = dqc[i] + lnext;
+                pr *= lam;
+            }
+            if (sj == NSEG - 1 && va) {
+                // K = sum_t (t - tau) k_t lam^(tile end - t) = lam V at the tile's last position
+                const size_t o = (static_cast<size_t>(b) * p.MT + m0 / TM) * p.F + a;
+                p.tK[o] = lam * (lam16 * vin + vl[SEG - 1]);
+            }
+            if (sj == 0 && va) {
+                float wsum = 0.f;
+                for (int m = 0; m < NSEG; ++m) wsum += xb[m][col];
+                const size_t o = (static_cast<size_t>(b) * p.MT + m0 / TM) * p.F + a;
+                p.tS[o] = rl[0] + lam16 * rj;
+                p.tW[o] = wsum;
+            }
+            __syncthreads();   // xa, xb and F's columns of this round done
+        }
+        const double wsum = wave_sum(dg_acc);
+        if (lane == 0) xg[wave] = wsum;
+        __syncthreads();
+        if (threadIdx.x == 0) p.dg_part[logical] = (xg[0] + xg[1]) + (xg[2] + xg[3]);
     } else {
         // rows = positions, columns = features of a (B, T, F) tensor, written
         // through a range-checked buffer of this batch row; invalid elements
@@ -418,13 +606,52 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
         const size_t row0 = static_cast<size_t>(b) * p.T * p.F;
         const uint32_t nbytes = static_cast<uint32_t>(p.T) * p.F * ES;
         const rsrc_t ro = rsrc(static_cast<char *>(p.out) + row0 * ES, nbytes);
-        const rsrc_t rr = rsrc(OUT >= 3 ? reinterpret_cast<const char *>(p.resid + row0) : static_cast<const char *>(p.out),
+        const rsrc_t rr = rsrc(OUT >= 3 && OUT < OUT_DRADD ? reinterpret_cast<const char *>(p.resid + row0)
+                                                           : static_cast<const char *>(p.out),
                                static_cast<uint32_t>(p.T) * p.F * 4);
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
             const int n = n0 + wn * (TN / 2) + 32 * j + lc;
             const int f = p.nperm ? (n & ~31) + perm32(n & 31) : n;
             const bool fok = f < p.F;
+            // OUT_DRADD: row pos of dk_f goes to dr at pos - 1 with the carry of dkc
+            // into this 128-position tile (and, on its first row, the tile's own
+            // local dkc, which the dq_f epilogue of the tile before left out)
+            float cC = 0.f, cS = 0.f;
+            if constexpr (OUT == OUT_DRADD) {
+                if (fok) {
+                    const size_t o = (static_cast<size_t>(b) * p.MT + m0 / TM) * p.F + f;
+                    cC = p.tC[o];
+                    cS = p.tS[o];
+                }
+            }
+            if constexpr (OUT == OUT_DRADD) {
+                // every load of dr first (the stores below may alias them), then the sums
+                float old[MI][16];
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int pos = m0 + wm * (TM / 2) + 32 * i + 8 * (r / 4) + 4 * h + r % 4;
+                        const uint32_t el = static_cast<uint32_t>(pos - 1) * p.F + f;
+                        const uint32_t bad = (fok && pos >= 1 && pos < p.T) ? 0u : OOB;
+                        old[i][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, (4u * el) | bad, 0, 0));
+                    }
+                const float g = p.g[0];
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int pl = wm * (TM / 2) + 32 * i + 8 * (r / 4) + 4 * h + r % 4;   // position in the tile
+                        const int pos = m0 + pl;
+                        const uint32_t el = static_cast<uint32_t>(pos - 1) * p.F + f;
+                        const uint32_t bad = (fok && pos >= 1 && pos < p.T) ? 0u : OOB;
+                        float v = old[i][r] + acc[i][j][r] + __expf(g * static_cast<float>(TM - pl)) * cC;
+                        if (pl == 0) v += cS;
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ro, (4u * el) | bad, 0, 0);
+                    }
+                continue;
+            }
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -443,6 +670,62 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
                     }
                 }
         }
+    }
+}
+
+// The carry of dkc between 128-position tiles, per batch row and slot:
+// D_m = S_m + lam^128 D_{m+1} (D past the last tile 0) is dkc at the start of
+// tile m, and C_m = D_{m+1} the carry into tile m's end. Also per batch row
+// and slot the sum of the tiles' dw parts, and per block the carry's share of
+// the decay gradient, -sum_m K_m C_m. Fixed-order sums.
+__global__ __launch_bounds__(256) void carry_kernel(const float *__restrict__ tS, const float *__restrict__ tK,
+                                                    const float *__restrict__ tW, const float *__restrict__ g,
+                                                    float *__restrict__ tC, float *__restrict__ dwb,
+                                                    double *__restrict__ dg_part, int MT, int A) {
+    __shared__ double red[4];
+    const int a = blockIdx.x * 256 + threadIdx.x;
+    const size_t b = blockIdx.y;
+    const float lam = __expf(g[0]);
+    float lam128 = lam;
+#pragma unroll
+    for (int e = 0; e < 7; ++e) lam128 *= lam128;
+    double corr = 0.0;
+    if (a < A) {
+        float D = 0.f, dw = 0.f;
+        for (int m = MT - 1; m >= 0; --m) {
+            const size_t o = (b * MT + m) * A + a;
+            tC[o] = D;
+            corr -= static_cast<double>(tK[o]) * D;
+            dw += tW[o];
+            D = tS[o] + lam128 * D;
+        }
+        dwb[b * A + a] = dw;
+    }
+    corr = wave_sum(corr);
+    if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = corr;
+    __syncthreads();
+    if (threadIdx.x == 0) dg_part[b * gridDim.x + blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// dw[a] = sum_b dwb[b, a]; dg = the sum of n1 + n2 partials, in a fixed order
+__global__ __launch_bounds__(256) void final_kernel(const float *__restrict__ dwb, const double *__restrict__ p1, int n1,
+                                                    const double *__restrict__ p2, int n2, float *__restrict__ dw,
+                                                    float *__restrict__ dg, int B, int A) {
+    __shared__ double red[4];
+    const int a = blockIdx.x * 256 + threadIdx.x;
+    if (a < A) {
+        float s = 0.f;
+        for (int b = 0; b < B; ++b) s += dwb[static_cast<size_t>(b) * A + a];
+        dw[a] = s;
+    }
+    if (blockIdx.x == 0) {
+        double s = 0.0;
+        for (int k = threadIdx.x; k < n1; k += 256) s += p1[k];
+        for (int k = threadIdx.x; k < n2; k += 256) s += p2[k];
+        s = wave_sum(s);
+        if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = s;
+        __syncthreads();
+        if (threadIdx.x == 0) dg[0] = static_cast<float>((red[0] + red[1]) + (red[2] + red[3]));
     }
 }
 
@@ -504,6 +787,7 @@ int launch(const Args &a, int G, int B, hipStream_t s) {
     if constexpr (EPI != EPI_ROWS) {
         return launch_o<TA, false, EPI, 0>(a, G, B, s);
     } else {
+        if (a.tC) return launch_o<TA, false, EPI, OUT_DRADD>(a, G, B, s);
         const int out = a.out_dt + (a.resid ? 3 : 0);
         switch (out) {
         case 0: return launch_o<TA, false, EPI, 0>(a, G, B, s);
@@ -587,26 +871,77 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *
     return launch<false, EPI_ROWS>(f, G, B, s);
 }
 
-// The backward products: dS = dscores(dfast, v) and its transpose dSt with the
-// pair part of the decay gradient into dg_part (pair_dscore_jobs doubles),
-// dq_f = dS k, dk_f = dS^T q (fp32 (B, T, A)), dv = P^T dfast in dv_dt (B, T, D).
-// vR, doR: R layout (D); kQ, qQ: Q layout (A); doQ: Q layout (D); P and Pt from
-// the forward (Plo: P's residual, for the decay gradient).
+// Bytes of the statistics workspace of launch_pair_backward: the per (batch
+// row, 128-position tile, slot) S, K, W and carry arrays, the per batch row dw
+// sums and the decay-gradient partials of the dq_f tiles and of the carry.
+namespace {
+struct PairStats {
+    float *tS, *tK, *tW, *tC, *dwb;
+    double *dgq, *dgc;
+    size_t bytes;
+};
+PairStats pair_stats_layout(void *base, int B, int T, int A) {
+    const int G = pair_block(B, T), MT = pair_tq(B, T) / G;
+    const size_t nst = static_cast<size_t>(B) * MT * A;
+    const size_t jobs_q = static_cast<size_t>(B) * MT * ((A + G - 1) / G), blocks_c = static_cast<size_t>(B) * ((A + 255) / 256);
+    Carver c(base);
+    PairStats w{};
+    w.tS = c.take<float>(nst);
+    w.tK = c.take<float>(nst);
+    w.tW = c.take<float>(nst);
+    w.tC = c.take<float>(nst);
+    w.dwb = c.take<float>(static_cast<size_t>(B) * A);
+    w.dgq = c.take<double>(jobs_q + blocks_c);   // the carry partials follow the tiles'
+    w.dgc = w.dgq + jobs_q;
+    w.bytes = c.off;
+    return w;
+}
+}  // namespace
+
+size_t pair_stats_bytes(int B, int T, int A) { return pair_stats_layout(nullptr, B, T, A).bytes; }
+
+// The backward: dv = P^T dfast in dv_dt (B, T, D); dS = dscores(dfast, v) and
+// its transpose dSt with the pair part of the decay gradient; dq_f = dS k with
+// the per-slot statistics in its epilogue (dr without dk_f and the carry; the
+// tile statistics); the carry of dkc between tiles; dk_f = dS^T q added into dr
+// with the carry; dw (A,) and dg (1,) reduced in a fixed order. vR, doR: R
+// layout (D); kQ, qQ: Q layout (A); doQ: Q layout (D); P, Pt, Plo from the
+// forward. r: the read addresses (or their address inputs); xq / xq_kind: the
+// extra gradient of q (0 none, 1 dq_out fp32, 2 + dtype d(w q)); nck: the
+// forward's chunk checkpoints; ws: pair_stats_bytes(B, T, A) bytes.
 int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t *doQ, const uint16_t *kQ,
                          const uint16_t *qQ, const uint16_t *P, const uint16_t *Pt, const uint16_t *Plo,
-                         const float *g, uint16_t *dS,
-                         uint16_t *dSt, double *dg_part, float *dqf, float *dkf, void *dv, int dv_dt, int B, int T,
-                         int A, int D, hipStream_t s) {
+                         const float *g, uint16_t *dS, uint16_t *dSt, double *dg_part, const RSrc &rsrc_in,
+                         const void *xq, int xq_kind, const float *nck, const float *w, float *dr, float *dw,
+                         float *dg, void *ws, void *dv, int dv_dt, int B, int T, int A, int D, hipStream_t s) {
     using namespace pair;
-    const int G = pair_block(B, T), Tq = pair_tq(B, T), NT = (T + 63) / 64;
+    const int G = pair_block(B, T), Tq = pair_tq(B, T), NT = (T + 63) / 64, MT = Tq / G;
     const int Ap = (A + 31) / 32 * 32, Dp = (D + 31) / 32 * 32;   // operand tile widths
+    const PairStats st = pair_stats_layout(ws, B, T, A);
     const Mat sm = p_mat(dS, Tq);
+    {
+        // dv = P^T dfast first, so that dq_f / dk_f meet their epilogues' inputs fresh
+        Args d{};
+        d.T = T;
+        d.g = g;
+        d.mt = MT;
+        d.nks = Tq / (16 * KT);
+        d.nperm = 1;
+        d.krange = K_ANTI;
+        d.a = p_mat(Pt, Tq);
+        d.b = q_mat(doQ, NT, Dp);
+        d.nt = (D + G - 1) / G;
+        d.out = dv;
+        d.out_dt = dv_dt;
+        d.F = D;
+        ULM_TRY((launch<false, EPI_ROWS>(d, G, B, s)));
+    }
     Args a{};
     a.T = T;
     a.g = g;
     a.a = r_mat(vR, NT, Dp);
     a.b = r_mat(doR, NT, Dp);
-    a.mt = a.nt = Tq / G;
+    a.mt = a.nt = MT;
     a.tri = 1;
     a.krange = K_FULL;
     a.nks = (Dp + 16 * KT - 1) / (16 * KT);
@@ -621,32 +956,47 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
     Args r{};
     r.T = T;
     r.g = g;
-    r.mt = Tq / G;
+    r.mt = MT;
     r.nks = Tq / (16 * KT);
     r.nperm = 1;
-    // dq_f = dS k
+    r.F = A;
+    r.r = rsrc_in.r;
+    r.pre = rsrc_in.pre;
+    r.pre_dt = rsrc_in.pre_dt;
+    r.bias = rsrc_in.bias;
+    r.denom = rsrc_in.denom;
+    r.xq = xq;
+    r.xq_kind = xq_kind;
+    r.nck = nck;
+    r.w = w;
+    r.NT = NT;
+    r.dr = dr;
+    r.tS = st.tS;
+    r.tK = st.tK;
+    r.tW = st.tW;
+    r.MT = MT;
+    // dq_f = dS k, and the statistics
     r.a = sm;
     r.b = q_mat(kQ, NT, Ap);
     r.nt = (A + G - 1) / G;
     r.krange = K_CAUSAL;
-    r.out = dqf;
-    r.out_dt = ULM_F32;
-    r.F = A;
-    ULM_TRY((launch<false, EPI_ROWS>(r, G, B, s)));
-    // dk_f = dS^T q: rows s of dSt, contraction t >= the start of s's block
+    r.dg_part = st.dgq;
+    ULM_TRY((launch<false, EPI_DQSTATS>(r, G, B, s)));
+    pair::carry_kernel<<<dim3((A + 255) / 256, B), 256, 0, s>>>(st.tS, st.tK, st.tW, g, st.tC, st.dwb, st.dgc, MT, A);
+    ULM_TRY(check_launch("carry_kernel"));
+    // dk_f = dS^T q (rows s of dSt, contraction t >= the start of s's block), into dr
     r.a = p_mat(dSt, Tq);
     r.b = q_mat(qQ, NT, Ap);
     r.krange = K_ANTI;
-    r.out = dkf;
+    r.out = dr;
+    r.out_dt = ULM_F32;
+    r.tC = st.tC;
+    r.dg_part = nullptr;
     ULM_TRY((launch<false, EPI_ROWS>(r, G, B, s)));
-    // dv = P^T dfast
-    r.a = p_mat(Pt, Tq);
-    r.b = q_mat(doQ, NT, Dp);
-    r.nt = (D + G - 1) / G;
-    r.out = dv;
-    r.out_dt = dv_dt;
-    r.F = D;
-    return launch<false, EPI_ROWS>(r, G, B, s);
+    const int jobs_q = B * MT * ((A + G - 1) / G), blocks_c = B * ((A + 255) / 256);
+    pair::final_kernel<<<(A + 255) / 256, 256, 0, s>>>(st.dwb, st.dgq, jobs_q + blocks_c, dg_part,
+                                                       pair_dscore_jobs(B, T), dw, dg, B, A);
+    return check_launch("final_kernel");
 }
 
 }  // namespace ulm

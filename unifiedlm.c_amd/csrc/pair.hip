@@ -165,7 +165,8 @@ __device__ __forceinline__ void wait_copies(int ksteps) {
 }
 
 // Output element types of the row epilogue: OUT % 3 = ulm_dtype of the
-// output, OUT >= 3 adds an fp32 residual.
+// output, OUT >= 3 adds an fp32 residual; the statistics epilogue uses OUT
+// for its input kinds.
 template <int TM, int TN, int KT, bool TA, bool TBt, int EPI, int OUT>
 __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Args p) {
     constexpr int MI = TM / 64, NI = TN / 64;          // 32-row / 32-column tiles per wave
@@ -450,6 +451,7 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
         constexpr int SEG = 16, NSEG = TM / SEG;
         __shared__ float xa[NSEG][32], xb[NSEG][32];
         __shared__ double xg[WAVES];
+        __shared__ float sidn[TM + 1];               // 1 / denom at positions m0 - 1 .. m0 + 127
         float *F = reinterpret_cast<float *>(lds);   // [128 t][128 a] fp32: the 64 KB of stage memory
         __syncthreads();                             // every wave past its last operand read
 #pragma unroll
@@ -460,6 +462,12 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) F[(wm * (TM / 2) + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * 128 + fl] = acc[i][j][r];
+        }
+        if constexpr (OUT / 2 != 0) {
+            if (threadIdx.x <= TM) {
+                const int t = m0 - 1 + static_cast<int>(threadIdx.x);
+                sidn[threadIdx.x] = (t >= 0 && t < p.T) ? 1.f / p.denom[static_cast<size_t>(b) * p.T + t] : 0.f;
+            }
         }
         __syncthreads();
         const int sj = threadIdx.x / 32, col = threadIdx.x % 32;
@@ -474,48 +482,91 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
         const size_t brow = static_cast<size_t>(b) * p.T;
         const bool xw = p.xq_kind >= 2;   // d(w q): dq gets w d(w q), dw gets q d(w q)
         double dg_acc = 0.0;
+        // this batch row of r (or pre and denom), of the extra gradient of q and
+        // of dr, through buffer loads and stores that return zeros and drop
+        // writes past the range: the loads of a round issue together, with no
+        // branch per element between them
+        // The input kinds are compile-time (OUT = 2 IN + X4): IN 0 reads r
+        // (fp32), 1 pre (fp32), 2 pre (bf16 or fp16) with denom; X4 reads the
+        // extra gradient of q in 4-byte elements (or there is none: a
+        // zero-length range on a valid base, whose loads return zeros without
+        // touching memory), else in 2-byte ones.
+        constexpr int IN = OUT / 2;
+        constexpr bool X4 = OUT % 2 == 1;
+        constexpr uint32_t pes = IN == 2 ? 2u : 4u, xes = X4 ? 4u : 2u;
+        const uint32_t rows = static_cast<uint32_t>(p.T) * p.F;
+        const rsrc_t rs_in = IN == 0 ? rsrc(p.r + brow * p.F, 4ull * rows)
+                                     : rsrc(static_cast<const char *>(p.pre) + brow * p.F * pes, static_cast<size_t>(pes) * rows);
+        const rsrc_t rs_xq = rsrc(p.xq_kind ? static_cast<const char *>(p.xq) + brow * p.F * xes : static_cast<const char *>(p.xq ? p.xq : p.dr),
+                                  p.xq_kind ? static_cast<size_t>(xes) * rows : 0);
+        const rsrc_t rs_dr = rsrc(p.dr + brow * p.F, 4ull * rows);
+        // The loads of round rd + 1 are issued while round rd computes: r (or
+        // pre), the extra gradient of q, n at the chunk start, w and the bias
+        // of this thread's slot, each through a range-checked buffer load (no
+        // branch between them).
+        const rsrc_t rs_nck = rsrc(p.nck + static_cast<size_t>(b) * p.NT * p.F, 4ull * p.NT * p.F);
+        const rsrc_t rs_w = rsrc(p.w, 4ull * p.F);
+        const rsrc_t rs_bias = rsrc(p.bias ? p.bias : p.w, p.bias ? 4ull * p.F : 0);
+        uint32_t rraw[SEG + 1], xraw[SEG], nraw, wraw, braw;
+        auto issue = [&](int rd) {
+            // Each range covers one batch row, so positions t < 0 (a negative
+            // offset wraps past 2^31) and t >= T read as zeros with no test;
+            // slots past A carry the out-of-range bit.
+            const int a = n0 + 32 * rd + col;
+            const uint32_t bad_a = static_cast<uint32_t>(a >= p.F) << 31;
+            const int ac = a < p.F ? a : 0;
+#pragma unroll
+            for (int i = 0; i <= SEG; ++i) {
+                const uint32_t off = (pes * static_cast<uint32_t>((t0 - 1 + i) * p.F + ac)) | bad_a;
+                rraw[i] = pes == 4u ? __builtin_amdgcn_raw_buffer_load_b32(rs_in, off, 0, 0)
+                                    : static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(rs_in, off, 0, 0));
+            }
+#pragma unroll
+            for (int i = 0; i < SEG; ++i) {
+                const uint32_t off = (xes * static_cast<uint32_t>((t0 + i) * p.F + ac)) | bad_a;
+                xraw[i] = X4 ? __builtin_amdgcn_raw_buffer_load_b32(rs_xq, off, 0, 0)
+                             : static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(rs_xq, off, 0, 0));
+            }
+            nraw = __builtin_amdgcn_raw_buffer_load_b32(rs_nck, (4u * static_cast<uint32_t>((t0 / 64) * p.F + ac)) | bad_a, 0, 0);
+            wraw = __builtin_amdgcn_raw_buffer_load_b32(rs_w, (4u * static_cast<uint32_t>(ac)) | bad_a, 0, 0);
+            braw = __builtin_amdgcn_raw_buffer_load_b32(rs_bias, (4u * static_cast<uint32_t>(ac)) | bad_a, 0, 0);
+        };
+        issue(0);
         for (int round = 0; round < 4; ++round) {
             const int al = 32 * round + col;
             const int a = n0 + al;
             const bool va = a < p.F;
-            const uint32_t ac = va ? a : 0;
-            const float wa = va ? p.w[ac] : 1.f;
-            const float ba = (va && p.bias) ? p.bias[ac] : 0.f;
+            const float wa = va ? __builtin_bit_cast(float, wraw) : 1.f;
+            const float ba = __builtin_bit_cast(float, braw);   // 0 past the slots and without a bias
+            const float nck0 = __builtin_bit_cast(float, nraw);
             // r at positions t0 - 1 .. t0 + 15 (0 outside 0 <= t < T and past the
             // slots), formed as the forward's statistics form it
             float rv[SEG + 1];
 #pragma unroll
             for (int i = 0; i <= SEG; ++i) {
-                const int t = t0 - 1 + i;
-                const bool ok = va && t >= 0 && t < p.T;
-                const size_t row = brow + (ok ? t : 0);
-                float v;
-                if (p.r) {
-                    v = p.r[row * p.F + ac];
-                } else {
-                    float x;
-                    if (p.pre_dt == ULM_BF16) x = bf16_to_f32(static_cast<const uint16_t *>(p.pre)[row * p.F + ac]);
-                    else if (p.pre_dt == ULM_F32) x = static_cast<const float *>(p.pre)[row * p.F + ac];
-                    else x = static_cast<float>(static_cast<const _Float16 *>(p.pre)[row * p.F + ac]);
+                const uint16_t h16 = static_cast<uint16_t>(rraw[i]);
+                float x = pes == 4u ? __builtin_bit_cast(float, rraw[i])
+                                    : (p.pre_dt == ULM_BF16 ? bf16_to_f32(h16) : static_cast<float>(__builtin_bit_cast(_Float16, h16)));
+                if constexpr (IN != 0) {
+                    // past the slots pre and the bias read as 0; sidn is 0 outside 0 <= t < T
                     x += ba;
                     x = x > 0.f ? x : 0.f;
-                    v = (x * x) * (1.f / p.denom[row]);
+                    x = (x * x) * sidn[tl0 + i];
                 }
-                rv[i] = ok ? v : 0.f;
+                rv[i] = x;
             }
+            // the extra gradient of q at t0 .. t0 + 15 (0 past T and the slots)
             float xv[SEG];
 #pragma unroll
             for (int i = 0; i < SEG; ++i) {
-                const int t = t0 + i;
-                const bool ok = va && t < p.T && p.xq_kind;
-                const size_t el = (brow + (ok ? t : 0)) * p.F + ac;
-                float v = 0.f;
-                if (p.xq_kind == 1 || p.xq_kind == 2 + ULM_F32) v = static_cast<const float *>(p.xq)[el];
-                else if (p.xq_kind == 2 + ULM_BF16) v = bf16_to_f32(static_cast<const uint16_t *>(p.xq)[el]);
-                else if (p.xq_kind == 2 + ULM_F16) v = static_cast<float>(static_cast<const _Float16 *>(p.xq)[el]);
-                xv[i] = ok ? v : 0.f;
+                const uint16_t h16 = static_cast<uint16_t>(xraw[i]);
+                xv[i] = X4 ? __builtin_bit_cast(float, xraw[i])
+                           : (p.xq_kind == 2 + ULM_BF16 ? bf16_to_f32(h16) : static_cast<float>(__builtin_bit_cast(_Float16, h16)));
             }
+            if (round < 3) issue(round + 1);
             // local scans of n (k_t = r_{t-1}) and of V from the segment start
+            // (t - tau is a multiple of 1/2 below 2^12 in magnitude: exact in fp32)
+            const float ft0 = static_cast<float>(static_cast<double>(t0) - tau);
             float nl[SEG], vl[SEG];
             float an = 0.f, av = 0.f;
 #pragma unroll
@@ -523,7 +574,7 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
                 const float k = t0 + i < p.T ? rv[i] : 0.f;
                 an = lam * an + rv[i];
                 nl[i] = an;
-                av = lam * av + static_cast<float>(static_cast<double>(t0 + i) - tau) * k;
+                av = lam * av + (ft0 + static_cast<float>(i)) * k;
                 vl[i] = av;
             }
             xa[sj][col] = an;
@@ -531,19 +582,22 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
             __syncthreads();
             // n at the segment start: the chunk checkpoint and the chunk's earlier
             // segments; V at the segment start: the tile's earlier segments
-            float cj = va ? p.nck[(static_cast<size_t>(b) * p.NT + t0 / 64) * p.F + ac] : 0.f;
+            float cj = nck0;
             for (int m = cs; m < sj; ++m) cj = lam16 * cj + xa[m][col];
             float vin = 0.f;
             for (int m = 0; m < sj; ++m) vin = lam16 * vin + xb[m][col];
-            // c, q, dq, dc; dc back into F; the local parts of dw and dg
+            // c, q, dq, dc; dc back into F; the local parts of dw and dg. The
+            // segment's share of the decay gradient, sum_i (t0 + i - tau) dc_i
+            // (c_i - w) - dc_i V_i, is summed in fp32 over the 16 positions as
+            // (t0 - tau) s0 + s1 - s2 and added to the double total once.
             float dqc[SEG];
-            float dw_acc = 0.f, pw = lam, ecar = 0.f;
+            float dw_acc = 0.f, pw = lam, ecar = 0.f, s0 = 0.f, s1 = 0.f, s2 = 0.f;
 #pragma unroll
             for (int i = 0; i < SEG; ++i) {
                 const int tl = tl0 + i;
                 const float c = wa + (pw * cj + nl[i]);
-                const float q = rv[i + 1] / c;
                 const float ic = __builtin_amdgcn_rcpf(c);
+                const float q = rv[i + 1] * ic;
                 const float dq = F[tl * 128 + al] + (xw ? wa * xv[i] : xv[i]);
                 const float dc = -(dq * q) * ic;
                 dqc[i] = dq * ic;
@@ -551,11 +605,14 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
                 dw_acc += dc;
                 if (xw) dw_acc += q * xv[i];
                 ecar += pw * dc;   // sum_i lam^(i+1) dc_i: the earlier segments' V reach t0 + i as lam^(i+1) vin
-                dg_acc += (static_cast<double>(t0 + i) - tau) * static_cast<double>(dc * (c - wa)) -
-                          static_cast<double>(dc * vl[i]);
+                const float e = dc * (c - wa);
+                s0 += e;
+                s1 += static_cast<float>(i) * e;
+                s2 += dc * vl[i];
                 pw *= lam;
             }
-            dg_acc -= static_cast<double>(vin) * static_cast<double>(ecar);
+            dg_acc += static_cast<double>(ft0) * static_cast<double>(s0) + static_cast<double>(s1) -
+                      static_cast<double>(s2) - static_cast<double>(vin) * static_cast<double>(ecar);
             __syncthreads();   // xa, xb read
             // reverse: the local scan of dc, the segments' totals through LDS
             float rl[SEG];
@@ -576,7 +633,9 @@ __global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Arg
             for (int i = SEG - 1; i >= 0; --i) {
                 const float lnext = (i + 1 < SEG ? rl[i + 1] : 0.f) + pr * rj;
                 const int t = t0 + i;
-                if (va && t < p.T) p.dr[(brow + t) * p.F + a] = dqc[i] + lnext;
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, dqc[i] + lnext), rs_dr,
+                                                      (4u * static_cast<uint32_t>(t * p.F + (va ? a : 0))) |
+                                                          (static_cast<uint32_t>(!va) << 31), 0, 0);
                 pr *= lam;
             }
             if (sj == NSEG - 1 && va) {
@@ -784,7 +843,19 @@ int launch_o(const Args &a, int G, int B, hipStream_t s) {
 // orientation its consumers contract over); TA is kept for the transposed read
 template <bool TA, int EPI>
 int launch(const Args &a, int G, int B, hipStream_t s) {
-    if constexpr (EPI != EPI_ROWS) {
+    if constexpr (EPI == EPI_DQSTATS) {
+        // OUT = 2 IN + X4 (the statistics epilogue's input kinds)
+        const int in = a.r ? 0 : (a.pre_dt == ULM_F32 ? 1 : 2);
+        const bool x4 = a.xq_kind == 0 || a.xq_kind == 1 || a.xq_kind == 2 + ULM_F32;
+        switch (2 * in + (x4 ? 1 : 0)) {
+        case 0: return launch_o<TA, false, EPI, 0>(a, G, B, s);
+        case 1: return launch_o<TA, false, EPI, 1>(a, G, B, s);
+        case 2: return launch_o<TA, false, EPI, 2>(a, G, B, s);
+        case 3: return launch_o<TA, false, EPI, 3>(a, G, B, s);
+        case 4: return launch_o<TA, false, EPI, 4>(a, G, B, s);
+        default: return launch_o<TA, false, EPI, 5>(a, G, B, s);
+        }
+    } else if constexpr (EPI != EPI_ROWS) {
         return launch_o<TA, false, EPI, 0>(a, G, B, s);
     } else {
         if (a.tC) return launch_o<TA, false, EPI, OUT_DRADD>(a, G, B, s);

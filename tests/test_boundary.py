@@ -61,6 +61,9 @@ def test_workspace_sizes(monkeypatch):
         assert lib.ulm_fm_saved_bytes(B, T, A, D, dt) >= B * T * (4 * A + 2 * D) + 3 * B * Tq * Tq * 2 + B * NT * A * 4
     # backward: two tiled dfast copies, dS and its transpose, the per-tile statistics;
     # dq_f and dk_f stay in the products' epilogues (no fp32 (B, T, A) copies)
+    # forward: q, k in the R layout for the scores, v in the Q layout for the apply
+    nfw = lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_F32)
+    assert nfw == 2 * B * NT * 64 * A * 2 + B * NT * 64 * D * 2
     nbw = lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32)
     assert B * T * 4 * D + 2 * B * Tq * Tq * 2 <= nbw < B * T * 4 * D + 2 * B * Tq * Tq * 2 + B * T * 4 * A
     assert (lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32)
@@ -184,11 +187,16 @@ def test_block_entry_points_reject_bad_arguments_without_touching_the_gpu():
     assert st == nat.ULM_ERR_INVALID and b"empty clamp range" in lib.ulm_last_error()
 
 
-def test_block_workspace_sizes():
+def test_block_workspace_sizes(monkeypatch):
     lib = nat.lib()
     B, T, A, D = 16, 1024, 3072, 768
-    # the forward with a residual always goes through fp32 partials of the 4 key groups
-    assert lib.ulm_block_fm_fwd_workspace_bytes(B, T, A, D) >= 4 * B * T * D * 4
+    # block-pair form: the products write the output (with its residual)
+    # directly; the workspace holds the forward's operand tiles only
+    assert lib.ulm_block_fm_fwd_workspace_bytes(B, T, A, D) == 2 * B * T * A * 2 + B * T * D * 2
+    # the state form with a residual goes through fp32 partials of the 4 key groups
+    with monkeypatch.context() as m:
+        m.setenv("ULM_FM_PATH", "chunked")
+        assert lib.ulm_block_fm_fwd_workspace_bytes(B, T, A, D) >= 4 * B * T * D * 4
     # one fp32 partial per split; one round of 256 workgroups of 256 x 256 tiles
     tiles = (768 // 256) * (3072 // 256)
     assert lib.ulm_wgrad_workspace_bytes(B * T, 768, 3072) == (256 // tiles) * 768 * 3072 * 4

@@ -57,9 +57,6 @@ namespace pair {
 
 constexpr uint32_t TB = 1024;           // bytes per operand tile
 constexpr uint32_t OOB = 0x80000000u;   // buffer offset past every range: loads return zeros
-// LDS stages of operand copies (NSTAGE - 1 k-steps in flight): all 160 KB of LDS
-// at 256 x 256 tiles (32 KB per stage), 64 KB at 128 x 128 (two workgroups per CU)
-template <int TM> constexpr int nstage() { return TM == 256 ? 5 : 4; }
 constexpr int WAVES = 4;
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
@@ -91,6 +88,16 @@ enum Epi { EPI_SCORES = 0, EPI_DSCORES = 1, EPI_ROWS = 2, EPI_DQSTATS = 3 };
 // plus an fp32 residual, OUT_DRADD the backward's dr accumulation of dk_f
 constexpr int OUT_DRADD = 6;
 enum KRange { K_FULL = 0, K_CAUSAL = 1, K_ANTI = 2 };
+
+// LDS stages of operand copies (NSTAGE - 1 k-steps in flight): all 160 KB of LDS
+// at 256 x 256 tiles (32 KB per stage); at 128 x 128, 64 KB (two workgroups
+// per CU) for the products whose jobs vary in length, and 48 KB (three per
+// CU) for the scores and dscores, whose equal jobs (B T^2 / 2 G^2 of them)
+// would otherwise leave a short second wave
+template <int TM, int EPI> constexpr int nstage() {
+    return TM == 256 ? 5 : (EPI == EPI_SCORES || EPI == EPI_DSCORES ? 3 : 4);
+}
+template <int TM, int EPI> constexpr int min_blocks() { return TM == 256 ? 1 : (nstage<TM, EPI>() == 3 ? 3 : 2); }
 
 struct Args {
     Mat a, b;
@@ -168,14 +175,14 @@ __device__ __forceinline__ void wait_copies(int ksteps) {
 // output, OUT >= 3 adds an fp32 residual; the statistics epilogue uses OUT
 // for its input kinds.
 template <int TM, int TN, int KT, bool TA, bool TBt, int EPI, int OUT>
-__global__ __launch_bounds__(WAVES * 64, TM == 256 ? 1 : 2) void pair_kernel(Args p) {
+__global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kernel(Args p) {
     constexpr int MI = TM / 64, NI = TN / 64;          // 32-row / 32-column tiles per wave
     constexpr int KS = 16 * KT;                        // contraction elements per k-step
     constexpr int A_TILES = TM / 32 * KT, B_TILES = TN / 32 * KT;   // tiles per k-step
     constexpr uint32_t STAGE = (A_TILES + B_TILES) * TB;
     constexpr int AC = A_TILES / WAVES, BC = B_TILES / WAVES;       // copies per wave per k-step
     constexpr int LPW = AC + BC;
-    constexpr int NSTAGE = nstage<TM>();
+    constexpr int NSTAGE = nstage<TM, EPI>();
     static_assert(KT % 2 == 0 && NSTAGE >= 2 && NSTAGE - 2 <= 4, "k-step and stage count");
     extern __shared__ __align__(16) char lds[];
 
@@ -778,9 +785,20 @@ __global__ __launch_bounds__(256) void final_kernel(const float *__restrict__ dw
         dw[a] = s;
     }
     if (blockIdx.x == 0) {
-        double s = 0.0;
-        for (int k = threadIdx.x; k < n1; k += 256) s += p1[k];
-        for (int k = threadIdx.x; k < n2; k += 256) s += p2[k];
+        // each thread's partials in index order; eight loads in flight at a time
+        auto sum = [](const double *__restrict__ p, int n, double s) {
+            int k = threadIdx.x;
+            for (; k + 7 * 256 < n; k += 8 * 256) {
+                double v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = p[k + 256 * u];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) s += v[u];
+            }
+            for (; k < n; k += 256) s += p[k];
+            return s;
+        };
+        double s = sum(p2, n2, sum(p1, n1, 0.0));
         s = wave_sum(s);
         if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = s;
         __syncthreads();
@@ -813,7 +831,7 @@ constexpr int KT = 2;   // contraction tiles per k-step (32 elements): four 32 K
 template <int G, bool TA, bool TBt, int EPI, int OUT>
 int launch_g(Args a, int B, hipStream_t s) {
     const void *fn = reinterpret_cast<const void *>(&pair_kernel<G, G, KT, TA, TBt, EPI, OUT>);
-    constexpr int lds = nstage<G>() * (G / 32 * KT) * 2 * TB;
+    constexpr int lds = nstage<G, EPI>() * (G / 32 * KT) * 2 * TB;
     static bool attr_done[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return check_launch("hipGetDevice");
@@ -835,6 +853,9 @@ int launch_g(Args a, int B, hipStream_t s) {
 
 template <bool TA, bool TBt, int EPI, int OUT>
 int launch_o(const Args &a, int G, int B, hipStream_t s) {
+    if constexpr (EPI == EPI_SCORES) {
+        if (G == 256) return launch_g<256, TA, TBt, EPI, OUT>(a, B, s);
+    }
     if (G != 128) return fail(ULM_ERR_UNSUPPORTED, "block-pair products: tile size %d", G);
     return launch_g<128, TA, TBt, EPI, OUT>(a, B, s);
 }
@@ -914,7 +935,10 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *
     a.g = g;
     a.a = r_mat(kR, NT, Ap);
     a.b = r_mat(qR, NT, Ap);
-    a.mt = a.nt = Tq / G;
+    // the scores in 256 x 256 tiles where they tile Tq: twice the flops per
+    // operand byte of 128 x 128 tiles, whose k-steps are bound by the copies
+    const int Gs = Tq % 256 == 0 ? 256 : G;
+    a.mt = a.nt = Tq / Gs;
     a.tri = 1;
     a.krange = K_FULL;
     a.nks = (Ap + 16 * KT - 1) / (16 * KT);
@@ -924,7 +948,7 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *
     a.pout_lo = Plo;
     a.p_bstride = pm.bstride;
     a.p_rt = pm.rt;
-    ULM_TRY((launch<false, EPI_SCORES>(a, G, B, s)));
+    ULM_TRY((launch<false, EPI_SCORES>(a, Gs, B, s)));
     Args f{};
     f.T = T;
     f.g = g;

@@ -12,8 +12,11 @@ are resident in HBM before the timed region. Prints one JSON line:
   roofline   the dominant kernel (pair_kernel, or la_kgroup_kernel on the
              chunked path): the algorithmic flops of every timed launch over
              their summed launch time, measured with HIP events on the stream
-             each launch uses, against the 2516.6 TFLOP/s dense bf16 peak;
-             traffic is the HBM bytes per launch recorded under profiles/
+             each launch uses, against the 2516.6 TFLOP/s dense bf16 peak.
+             The algorithmic flops are the chunked algorithm's 16AD + 8C(A + D)
+             per token and block (for the pair products, the work they carry
+             out; their own executed flops give executed_tflops); traffic is
+             the HBM bytes per launch recorded under profiles/
   path_tflops / chunked_equivalent_tflops
              the whole step (statistics kernels included) in the chosen
              evaluation's algorithmic flops, and in the chunked form's
@@ -126,13 +129,20 @@ def bench_training(torch, args, shape=None, steps=None, warmup=None):
         t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / steps
     launch_ms = timer.total_ms / max(timer.launches, 1)
+    executed = None
     if path == "pair":
         kname = "pair_kernel"
-        flops_launches = workloads.pair_flops(B, T, A, D) * L * steps   # all timed launches
+        # the work of all timed launches priced in the algorithm's flops per token
+        # and block, 16AD + 8C(A + D) (the four chunked products); the six
+        # block-pair products carry that work out with fewer flops of their own
+        flops_launches = workloads.chunked_flops_per_token(A, D) * B * T * L * steps
+        executed = workloads.pair_flops(B, T, A, D) * L * steps
         flops_step = workloads.pair_flops(B, T, A, D) * L
-        note = ("the six block-pair products (scores, apply, dscores, dq_f, dk_f, dv) of every block, "
-                "algorithmic flops 6 (A + D) per causal pair (t, s); the kernels execute whole 128 x 128 "
-                f"diagonal tiles, {workloads.pair_tile_flops(B, T, A, D) / workloads.pair_flops(B, T, A, D):.3f}x that")
+        note = ("the six block-pair products (scores, apply, dscores, dq_f with the backward statistics, "
+                "dk_f into dr, dv) of every block; achieved prices their work in the chunked algorithm's "
+                "16 A D + 8 C (A + D) flops per token and block; executed_tflops counts their own flops, "
+                "6 (A + D) per causal pair (t, s) (whole diagonal tiles execute "
+                f"{workloads.pair_tile_flops(B, T, A, D) / workloads.pair_flops(B, T, A, D):.3f}x that)")
     else:
         kname = "la_kgroup_kernel"
         # fwd and dv contract keys A into values D, dq and dk keys D into values A
@@ -140,6 +150,7 @@ def bench_training(torch, args, shape=None, steps=None, warmup=None):
         flops_step = 4 * workloads.la_flops(B, T, A, D) * L
         note = "the four chunked products of every block, 4 K V + 2 C V per token and product"
     achieved = flops_launches / (timer.total_ms * 1e-3) / 1e12 if timer.total_ms > 0 else 0.0
+    executed_tflops = executed / (timer.total_ms * 1e-3) / 1e12 if executed and timer.total_ms > 0 else None
     traffic = None
     tfile = TRAFFIC_FILES.get(kname)
     if tfile and os.path.exists(tfile) and shape == "110M":
@@ -153,7 +164,9 @@ def bench_training(torch, args, shape=None, steps=None, warmup=None):
                           "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                           "traffic_source": "recorded (profiles/)" if traffic else None,
                           "kernel": kname, "flops": note,
-                          "avg_launch_ms": round(launch_ms, 4), "launches_timed": timer.launches},
+                          "avg_launch_ms": round(launch_ms, 4), "launches_timed": timer.launches,
+                          **({"executed_tflops": round(executed_tflops, 2),
+                              "executed_frac": round(executed_tflops / PEAK_BF16_TFLOPS, 4)} if executed_tflops else {})},
                 path_tflops=path_tflops, chunked_equivalent_tflops=chunk_eq)
 
 

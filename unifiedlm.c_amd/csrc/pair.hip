@@ -589,10 +589,21 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
             __syncthreads();
             // n at the segment start: the chunk checkpoint and the chunk's earlier
             // segments; V at the segment start: the tile's earlier segments
-            float cj = nck0;
-            for (int m = cs; m < sj; ++m) cj = lam16 * cj + xa[m][col];
-            float vin = 0.f;
-            for (int m = 0; m < sj; ++m) vin = lam16 * vin + xb[m][col];
+            // (all eight segments' values read at once, then the same recurrences
+            // over the ones that apply, so that no step waits on its own read)
+            float ea[NSEG], eb[NSEG];
+#pragma unroll
+            for (int m = 0; m < NSEG; ++m) {
+                ea[m] = xa[m][col];
+                eb[m] = xb[m][col];
+            }
+            float cj = nck0, vin = 0.f;
+#pragma unroll
+            for (int m = 0; m < NSEG; ++m) {
+                const float c2 = lam16 * cj + ea[m], v2 = lam16 * vin + eb[m];
+                cj = (m >= cs && m < sj) ? c2 : cj;
+                vin = m < sj ? v2 : vin;
+            }
             // c, q, dq, dc; dc back into F; the local parts of dw and dg. The
             // segment's share of the decay gradient, sum_i (t0 + i - tau) dc_i
             // (c_i - w) - dc_i V_i, is summed in fp32 over the 16 positions as
@@ -632,8 +643,15 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
             xa[sj][col] = racc;
             xb[sj][col] = dw_acc;
             __syncthreads();
+            float ra[NSEG];
+#pragma unroll
+            for (int m = 0; m < NSEG; ++m) ra[m] = xa[m][col];
             float rj = 0.f;   // L at the first position after this segment
-            for (int m = NSEG - 1; m > sj; --m) rj = xa[m][col] + lam16 * rj;
+#pragma unroll
+            for (int m = NSEG - 1; m > 0; --m) {
+                const float r2 = ra[m] + lam16 * rj;
+                rj = m > sj ? r2 : rj;
+            }
             // dr_t = dq_t / c_t + L_{t+1}, L_{t+1} = rl[i+1] + lam^(15-i) rj
             float pr = 1.f;
 #pragma unroll
@@ -652,6 +670,7 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
             }
             if (sj == 0 && va) {
                 float wsum = 0.f;
+#pragma unroll
                 for (int m = 0; m < NSEG; ++m) wsum += xb[m][col];
                 const size_t o = (static_cast<size_t>(b) * p.MT + m0 / TM) * p.F + a;
                 p.tS[o] = rl[0] + lam16 * rj;

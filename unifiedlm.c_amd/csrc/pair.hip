@@ -63,6 +63,12 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 typedef __attribute__((address_space(3))) void lds_void;
 typedef uint32_t v2u32_t __attribute__((ext_vector_type(2)));
+// The 16-byte buffer builtins take and return a vector_size(16) type. Their
+// values go through float ext-vectors by bit cast: elements read one by one
+// from a uint ext-vector made from the load were shrunk to one dword and
+// splatted by this compiler.
+typedef float v4f32_t __attribute__((ext_vector_type(4)));
+typedef uint32_t gv4u32_t __attribute__((__vector_size__(16)));
 
 __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -682,6 +688,82 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
         if (lane == 0) xg[wave] = wsum;
         __syncthreads();
         if (threadIdx.x == 0) p.dg_part[logical] = (xg[0] + xg[1]) + (xg[2] + xg[3]);
+    } else if constexpr (EPI == EPI_ROWS && OUT == OUT_DRADD) {
+        // dk_f rows into dr at position - 1, with the carry of dkc into this
+        // 128-position tile (and, on its first row, the tile's own local dkc,
+        // which the dq_f epilogue of the tile before left out). The tile goes
+        // through LDS so that each half-wave reads, adds and writes one dr row
+        // in 16-byte runs (lane = 4 slots), every read issued before a store.
+        static_assert(TM == 128 && TN == 128 && WAVES == 4, "dr accumulation: 128 x 128 tiles");
+        constexpr int FS = TN + 4;                    // padded row stride in floats
+        float *Fk = reinterpret_cast<float *>(lds);   // [TM][FS] dk_f; then the carry C and S per slot
+        float *sC = Fk + TM * FS, *sS = sC + TN;
+        __syncthreads();                              // every wave past its last operand read
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const int n = wn * (TN / 2) + 32 * j + lc;
+            const int fl = p.nperm ? (n & ~31) + perm32(n & 31) : n;
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) Fk[(wm * (TM / 2) + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * FS + fl] = acc[i][j][r];
+        }
+        if (threadIdx.x < TN) {
+            const int f = n0 + static_cast<int>(threadIdx.x);
+            const size_t o = (static_cast<size_t>(b) * p.MT + m0 / TM) * p.F + (f < p.F ? f : 0);
+            sC[threadIdx.x] = f < p.F ? p.tC[o] : 0.f;
+            sS[threadIdx.x] = f < p.F ? p.tS[o] : 0.f;
+        }
+        __syncthreads();
+        const float g = p.g[0];
+        const int cl = lane % 32, half = lane / 32, c0 = 4 * cl;   // this lane's 4 slots of the tile
+        const int f0 = n0 + c0;
+        float cC[4], cS[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            cC[e] = sC[c0 + e];
+            cS[e] = sS[c0 + e];
+        }
+        const rsrc_t ro = rsrc(static_cast<float *>(p.out) + static_cast<size_t>(b) * p.T * p.F,
+                               static_cast<size_t>(p.T) * p.F * 4);
+        // rows 2 (wave + 4 k) + half, k = 0 .. 15: two rows per wave per step
+        auto row_of = [&](int k) { return 2 * (wave + WAVES * k) + half; };
+        auto off_of = [&](int k, int e) -> uint32_t {
+            const int pos = m0 + row_of(k);
+            const bool ok = pos >= 1 && pos < p.T && f0 + e < p.F;
+            return ok ? 4u * (static_cast<uint32_t>(pos - 1) * p.F + f0 + e) : OOB;
+        };
+        auto sum = [&](int k, int e, float old) {
+            const int rw = row_of(k);
+            float v = old + Fk[rw * FS + c0 + e] + __expf(g * static_cast<float>(TM - rw)) * cC[e];
+            if (rw == 0) v += cS[e];
+            return v;
+        };
+        if (p.F % 4 == 0) {
+            // 16-byte aligned runs, wholly in or out of the slots
+            v4f32_t old[TM / (2 * WAVES)];
+#pragma unroll
+            for (int k = 0; k < TM / (2 * WAVES); ++k)
+                old[k] = __builtin_bit_cast(v4f32_t, __builtin_amdgcn_raw_buffer_load_b128(ro, off_of(k, 0), 0, 0));
+#pragma unroll
+            for (int k = 0; k < TM / (2 * WAVES); ++k) {
+                v4f32_t v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = sum(k, e, old[k][e]);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(gv4u32_t, v), ro, off_of(k, 0), 0, 0);
+            }
+        } else {
+#pragma unroll 2
+            for (int k = 0; k < TM / (2 * WAVES); ++k) {
+                float old[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    old[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, off_of(k, e), 0, 0));
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum(k, e, old[e])), ro, off_of(k, e), 0, 0);
+            }
+        }
     } else {
         // rows = positions, columns = features of a (B, T, F) tensor, written
         // through a range-checked buffer of this batch row; invalid elements
@@ -691,52 +773,13 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
         const size_t row0 = static_cast<size_t>(b) * p.T * p.F;
         const uint32_t nbytes = static_cast<uint32_t>(p.T) * p.F * ES;
         const rsrc_t ro = rsrc(static_cast<char *>(p.out) + row0 * ES, nbytes);
-        const rsrc_t rr = rsrc(OUT >= 3 && OUT < OUT_DRADD ? reinterpret_cast<const char *>(p.resid + row0)
-                                                           : static_cast<const char *>(p.out),
+        const rsrc_t rr = rsrc(OUT >= 3 ? reinterpret_cast<const char *>(p.resid + row0) : static_cast<const char *>(p.out),
                                static_cast<uint32_t>(p.T) * p.F * 4);
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
             const int n = n0 + wn * (TN / 2) + 32 * j + lc;
             const int f = p.nperm ? (n & ~31) + perm32(n & 31) : n;
             const bool fok = f < p.F;
-            // OUT_DRADD: row pos of dk_f goes to dr at pos - 1 with the carry of dkc
-            // into this 128-position tile (and, on its first row, the tile's own
-            // local dkc, which the dq_f epilogue of the tile before left out)
-            float cC = 0.f, cS = 0.f;
-            if constexpr (OUT == OUT_DRADD) {
-                if (fok) {
-                    const size_t o = (static_cast<size_t>(b) * p.MT + m0 / TM) * p.F + f;
-                    cC = p.tC[o];
-                    cS = p.tS[o];
-                }
-            }
-            if constexpr (OUT == OUT_DRADD) {
-                // every load of dr first (the stores below may alias them), then the sums
-                float old[MI][16];
-#pragma unroll
-                for (int i = 0; i < MI; ++i)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int pos = m0 + wm * (TM / 2) + 32 * i + 8 * (r / 4) + 4 * h + r % 4;
-                        const uint32_t el = static_cast<uint32_t>(pos - 1) * p.F + f;
-                        const uint32_t bad = (fok && pos >= 1 && pos < p.T) ? 0u : OOB;
-                        old[i][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, (4u * el) | bad, 0, 0));
-                    }
-                const float g = p.g[0];
-#pragma unroll
-                for (int i = 0; i < MI; ++i)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int pl = wm * (TM / 2) + 32 * i + 8 * (r / 4) + 4 * h + r % 4;   // position in the tile
-                        const int pos = m0 + pl;
-                        const uint32_t el = static_cast<uint32_t>(pos - 1) * p.F + f;
-                        const uint32_t bad = (fok && pos >= 1 && pos < p.T) ? 0u : OOB;
-                        float v = old[i][r] + acc[i][j][r] + __expf(g * static_cast<float>(TM - pl)) * cC;
-                        if (pl == 0) v += cS;
-                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ro, (4u * el) | bad, 0, 0);
-                    }
-                continue;
-            }
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -850,7 +893,9 @@ constexpr int KT = 2;   // contraction tiles per k-step (32 elements): four 32 K
 template <int G, bool TA, bool TBt, int EPI, int OUT>
 int launch_g(Args a, int B, hipStream_t s) {
     const void *fn = reinterpret_cast<const void *>(&pair_kernel<G, G, KT, TA, TBt, EPI, OUT>);
-    constexpr int lds = nstage<G, EPI>() * (G / 32 * KT) * 2 * TB;
+    // the dr accumulation stages its 128 x 132 fp32 tile and two slot rows in LDS
+    constexpr int stages = nstage<G, EPI>() * (G / 32 * KT) * 2 * TB;
+    constexpr int lds = OUT == OUT_DRADD && stages < (G * (G + 4) + 2 * G) * 4 ? (G * (G + 4) + 2 * G) * 4 : stages;
     static bool attr_done[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return check_launch("hipGetDevice");

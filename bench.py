@@ -23,7 +23,10 @@ are resident in HBM before the timed region. Prints one JSON line:
              16AD + 8C(A + D) flops per token (the same work priced as the
              reference's algorithm)
   configs    one block of the 15M (B=32, T=256, D=288, A=1152) and 42M (B=16,
-             T=1024, D=512, A=2048) shapes
+             T=1024, D=512, A=2048) shapes, and of the two shapes the reference
+             publishes single-block times for (ref-15M: B=32, T=256, D=288,
+             A=712, 1.56 ms; ref-42M: B=8, T=1024, D=512, A=1280, 3.18 ms; on an
+             RTX 3090 Ti, docs/kernel.md:57-62)
   cpu_baseline  the oracle's chunked PyTorch form on the host cores (fp32,
              fwd+bwd of one block at B=1, T=1024), scaled to the 12-block step
   block      whole UnifiedBlocks (fused) fwd+bwd over the same shape under bf16
@@ -172,9 +175,12 @@ def bench_training(torch, args, shape=None, steps=None, warmup=None):
 
 def bench_configs(torch, args):
     """Single-block fast-memory fwd + bwd at the 15M (B=32, T=256, D=288,
-    A=1152) and 42M (B=16, T=1024, D=512, A=2048) shapes."""
+    A=1152) and 42M (B=16, T=1024, D=512, A=2048) shapes, and at the two
+    shapes the reference publishes single-block times for (D=288, A=712 and
+    D=512, A=1280; docs/kernel.md:57-62, on an RTX 3090 Ti: other hardware)."""
+    import workloads
     out = {}
-    for shape in ("15M", "42M"):
+    for shape in ("15M", "42M", "ref-15M", "ref-42M"):
         t = bench_training(torch, args, shape=shape, steps=max(args.steps, 10), warmup=max(args.warmup, 3))
         out[shape] = {"workload": f"fast-memory fwd+bwd, one block of the {shape} shape (B={t['B']}, T={t['T']}, "
                                   f"D={t['D']}, A={t['A']})",
@@ -183,6 +189,11 @@ def bench_configs(torch, args):
                       "frac_bf16_peak": round(t["path_tflops"] / PEAK_BF16_TFLOPS, 4),
                       "chunked_equivalent_tflops": round(t["chunked_equivalent_tflops"], 2),
                       "roofline": t["roofline"]}
+        ref_ms = workloads.SHAPES[shape].get("reference_ms")
+        if ref_ms:
+            out[shape]["reference_ms_per_block"] = ref_ms
+            out[shape]["reference_hardware"] = "RTX 3090 Ti, Triton (docs/kernel.md:57-62)"
+            out[shape]["speedup_vs_reference"] = round(ref_ms / t["ms_step"], 2)
     return out
 
 

@@ -16,6 +16,11 @@ SHAPES = {
     "15M": dict(B=32, T=256, D=288, A=1152, blocks=1),
     "42M": dict(B=16, T=1024, D=512, A=2048, blocks=1),
     "110M": dict(B=16, T=1024, D=768, A=3072, blocks=12),
+    # the reference's own published single-block timings (docs/kernel.md:57-62,
+    # RTX 3090 Ti): 1.56 ms at D=288, A=712, B=32, T=256 and 3.18 ms at D=512,
+    # A=1280, B=8, T=1024
+    "ref-15M": dict(B=32, T=256, D=288, A=712, blocks=1, reference_ms=1.56),
+    "ref-42M": dict(B=8, T=1024, D=512, A=1280, blocks=1, reference_ms=3.18),
 }
 DECODE_110M = dict(N=256, D=768, A=3072, blocks=12, vocab=32000, prefill=512, steps=256)
 

@@ -462,7 +462,10 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
         // operations; segments meet through LDS.
         static_assert(TM == 128 && TN == 128 && WAVES * 64 == 256, "statistics epilogue: 128 x 128 tiles");
         constexpr int SEG = 16, NSEG = TM / SEG;
-        __shared__ float xa[NSEG][32], xb[NSEG][32];
+        // segment totals: forward (xa, xb) and reverse (ya, yb), each in two
+        // copies used by alternate rounds, so that two barriers per round order
+        // every write after the reads it could overwrite
+        __shared__ float xa[2][NSEG][32], xb[2][NSEG][32], ya[2][NSEG][32], yb[2][NSEG][32];
         __shared__ double xg[WAVES];
         __shared__ float sidn[TM + 1];               // 1 / denom at positions m0 - 1 .. m0 + 127
         float *F = reinterpret_cast<float *>(lds);   // [128 t][128 a] fp32: the 64 KB of stage memory
@@ -590,8 +593,9 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
                 av = lam * av + (ft0 + static_cast<float>(i)) * k;
                 vl[i] = av;
             }
-            xa[sj][col] = an;
-            xb[sj][col] = av;
+            const int par = round & 1;
+            xa[par][sj][col] = an;
+            xb[par][sj][col] = av;
             __syncthreads();
             // n at the segment start: the chunk checkpoint and the chunk's earlier
             // segments; V at the segment start: the tile's earlier segments
@@ -600,8 +604,8 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
             float ea[NSEG], eb[NSEG];
 #pragma unroll
             for (int m = 0; m < NSEG; ++m) {
-                ea[m] = xa[m][col];
-                eb[m] = xb[m][col];
+                ea[m] = xa[par][m][col];
+                eb[m] = xb[par][m][col];
             }
             float cj = nck0, vin = 0.f;
 #pragma unroll
@@ -637,7 +641,6 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
             }
             dg_acc += static_cast<double>(ft0) * static_cast<double>(s0) + static_cast<double>(s1) -
                       static_cast<double>(s2) - static_cast<double>(vin) * static_cast<double>(ecar);
-            __syncthreads();   // xa, xb read
             // reverse: the local scan of dc, the segments' totals through LDS
             float rl[SEG];
             float racc = 0.f;
@@ -646,12 +649,12 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
                 racc = F[(tl0 + i) * 128 + al] + lam * racc;
                 rl[i] = racc;
             }
-            xa[sj][col] = racc;
-            xb[sj][col] = dw_acc;
+            ya[par][sj][col] = racc;
+            yb[par][sj][col] = dw_acc;
             __syncthreads();
             float ra[NSEG];
 #pragma unroll
-            for (int m = 0; m < NSEG; ++m) ra[m] = xa[m][col];
+            for (int m = 0; m < NSEG; ++m) ra[m] = ya[par][m][col];
             float rj = 0.f;   // L at the first position after this segment
 #pragma unroll
             for (int m = NSEG - 1; m > 0; --m) {
@@ -677,12 +680,11 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
             if (sj == 0 && va) {
                 float wsum = 0.f;
 #pragma unroll
-                for (int m = 0; m < NSEG; ++m) wsum += xb[m][col];
+                for (int m = 0; m < NSEG; ++m) wsum += yb[par][m][col];
                 const size_t o = (static_cast<size_t>(b) * p.MT + m0 / TM) * p.F + a;
                 p.tS[o] = rl[0] + lam16 * rj;
                 p.tW[o] = wsum;
             }
-            __syncthreads();   // xa, xb and F's columns of this round done
         }
         const double wsum = wave_sum(dg_acc);
         if (lane == 0) xg[wave] = wsum;

@@ -86,6 +86,10 @@ OP_CASES = [
     # padded with zero slots in the block-pair products
     (2, 256, 712, 288, torch.bfloat16),
     (1, 512, 1912, 768, torch.bfloat16),
+    # slot counts off the multiples of 4 (the dr accumulation's element-wise
+    # path) and odd widths, across two position tiles with a ragged end
+    (2, 200, 70, 48, torch.float32),
+    (2, 150, 33, 17, torch.bfloat16),
 ]
 
 

@@ -27,23 +27,27 @@
 //   apply    t  d  s   P                      v (Q)  s < end of t's block
 //   dscores  s  t  d   v (R)                  dO (R) all features; s-block <= t-block
 //   dq_f     t  a  s   dS                     k (Q)  s < end of t's block
-//   dk_f     s  a  t   dS read transposed     q (Q)  t >= start of s's block
-//   dv       s  d  t   P read transposed      dO (Q) t >= start of s's block
+//   dk_f     s  a  t   dS^T                   q (Q)  t >= start of s's block
+//   dv       s  d  t   P^T                    dO (Q) t >= start of s's block
 //
-// P and dS are stored per batch row as bf16 tiles with rows t and contraction
-// s (the "P layout", the R layout of a Tq x Tq matrix, Tq = T padded to the
-// block). The scores / dscores epilogue holds, in the MFMA accumulator, one t
-// per lane and four consecutive s per register group, so each lane writes 8
-// contiguous bytes of a P-layout tile. The transposed reads of the dk_f and dv
-// products use ds_read_b64_tr_b16 on the staged tiles.
+// P, dS and their transposes are stored per batch row as bf16 tiles with rows
+// t (s for the transposes) and contraction s (t) (the "P layout", the R layout
+// of a Tq x Tq matrix, Tq = T padded to 128). The scores / dscores epilogue
+// holds, in the MFMA accumulator, one t per lane and four consecutive s per
+// register group, so each lane writes 8 contiguous bytes of a P-layout tile
+// and 2-byte elements of the transpose; every product then reads its operands
+// plain.
 //
 // Workgroup: TM x TN output tile, 4 waves (2 x 2), one wave per SIMD holding a
-// (TM/2) x (TN/2) fp32 accumulator. Each 64-element k-step of A and B is
-// copied into LDS by buffer_load ... lds (no registers), two stages, so the
-// copy of step k+1 runs during the MFMAs of step k. All global loads are
+// (TM/2) x (TN/2) fp32 accumulator (in AGPRs at 256 x 256). Each 32-element
+// k-step of A and B is copied into LDS by buffer_load ... lds (no registers),
+// NSTAGE stages (3 to 5, nstage below), so the copies of the next NSTAGE - 1
+// k-steps run during the MFMAs of the current one. All global loads are
 // range-checked buffer loads (rows or contraction past a matrix read as zero)
-// and all global stores of the P-layout outputs are range-checked buffer
-// stores.
+// and all global stores are range-checked buffer stores. Epilogues: the
+// scores and dscores (P-layout outputs, the dg pair sum), rows of a (B, T, F)
+// output, the dq_f product's backward statistics (EPI_DQSTATS) and the dk_f
+// product's accumulation into dr (OUT_DRADD).
 #include "ulm_common.h"
 
 #include <type_traits>

@@ -65,8 +65,8 @@ int ulm_fm_path(int B, int T, int A, int D);
  *   r      (B,T,A) fp32          read addresses
  *   v      (B,T,D) v_dtype       values (the reference casts them to bf16 in
  *                                 Python, kernel.py:205; here the cast is
- *                                 inside, so the backward can also keep the
- *                                 bf16 remainder of an fp32 v)
+ *                                 inside, so the chunked form's backward can
+ *                                 also keep the bf16 remainder of an fp32 v)
  *   w      (A,)    fp32          prior mass
  *   q      (B,T,A) fp32   out    returned and saved
  *   fast   (B,T,D) fast_dtype out  (v.dtype in the reference, kernel.py:211)
@@ -101,8 +101,10 @@ int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const float *g, c
                    float *q, void *fast, int fast_dtype, float *S, float *c_last,
                    void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream);
 
-/* Replaces UnifiedMemory.backward (kernel.py:216-233): the three chunked
- * products dq, dk (reverse), dv (reverse) and the denominator chain rule.
+/* Replaces UnifiedMemory.backward (kernel.py:216-233): the products dq, dk
+ * (reverse) and dv (reverse), as chunked products or, on the block-pair form,
+ * as the dscores, dq_f, dk_f and dv tile GEMMs, and the denominator chain rule
+ * (on the block-pair form inside the dq_f and dk_f products' epilogues).
  *
  *   saved   the buffer ulm_fm_fwd filled for the same r, g, w (q is not
  *           needed: it is recomputed as r / c from the saved checkpoints)

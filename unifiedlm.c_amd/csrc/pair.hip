@@ -141,7 +141,7 @@ struct Args {
     int NT;
     float *dr;               // (B, T, A)
     float *tS, *tK, *tW;     // per (batch row, 128-position tile, slot) statistics, (B, MT, A)
-    const float *tC;         // OUT_DRADD: the carry of dkc into each tile
+    int drtile;              // OUT_DRADD: the dr accumulation (the carry formed from tS)
     int MT;
 };
 
@@ -324,10 +324,59 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
     // earlier (overwriting the set of MFMAs still queued waits for them to
     // read it), and the reads have the second half to land.
     bf16x8 af[2][MI], bf[2][NI];
+    // OUT_DRADD: the carry of dkc into this 128-position tile is C_m = D_{m+1},
+    // D_j = S_j + lam^128 D_{j+1} from the last tile down (D past it 0), with S
+    // the tiles' local dkc at their start. Its inputs are read ahead of the
+    // first copies (the loads complete in order, so the first wait below
+    // covers them; a load issued after the copies would wait for all of them)
+    // and the carry is formed while those copies land; thread f < TN keeps
+    // slot n0 + f's carry and S of this tile for the epilogue. Only the waves
+    // holding slots load, and only the tiles mt .. MT - 1 (branches on uniform
+    // values: a skipped load costs no address cycles).
+    constexpr int MAXMT = 32;   // T <= 4096 on this form
+    float sv[OUT == OUT_DRADD ? MAXMT : 1], carry = 0.f, s_own = 0.f, kown = 0.f, lgr = 0.f;
+    __shared__ double xr[WAVES];
+    if constexpr (OUT == OUT_DRADD) {
+        const int f = n0 + static_cast<int>(threadIdx.x), mt = m0 / TM;
+        const bool fok = threadIdx.x < TN && f < p.F;
+        const bool loads = wave < TN / 64;
+        const rsrc_t rs = rsrc(p.tS + static_cast<size_t>(b) * p.MT * p.F, 4ull * p.MT * p.F);
+        const rsrc_t rk = rsrc(p.tK + static_cast<size_t>(b) * p.MT * p.F, 4ull * p.MT * p.F);
+        const rsrc_t rg = rsrc(p.g, 4);
+        lgr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, 0u, 0, 0));
+        if (loads)
+            kown = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                 rk, fok ? 4u * static_cast<uint32_t>(mt * p.F + f) : OOB, 0, 0));
+#pragma unroll
+        for (int j = 0; j < MAXMT; ++j) {
+            sv[j] = 0.f;
+            if (loads && j >= mt && j < p.MT)
+                sv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                      rs, fok ? 4u * static_cast<uint32_t>(j * p.F + f) : OOB, 0, 0));
+        }
+    }
 #pragma unroll
     for (int d = 0; d < NSTAGE - 1; ++d) issue(kb + d, d);
     __builtin_amdgcn_s_waitcnt(waitcnt_vm((NSTAGE - 2) * LPW));
     __builtin_amdgcn_s_barrier();
+    if constexpr (OUT == OUT_DRADD) {
+        // this job's share of the decay gradient, -K_m C_m summed over its slots
+        const int mt = m0 / TM;
+        const float lam = __expf(lgr);
+        float lam128 = lam;
+#pragma unroll
+        for (int e = 0; e < 7; ++e) lam128 *= lam128;
+        lam128 = fminf(lam128, 3.0e38f);   // finite, so that 0 carried past the last tile stays 0
+#pragma unroll
+        for (int j = MAXMT - 1; j >= 0; --j) {
+            const float d2 = sv[j] + lam128 * carry;
+            carry = j > mt ? d2 : carry;   // S past the last tile reads 0
+        }
+        s_own = sv[mt < MAXMT ? mt : 0];
+        double corr = -static_cast<double>(kown) * static_cast<double>(carry);   // 0 past the slots
+        corr = wave_sum(corr);
+        if (lane == 0) xr[wave] = corr;
+    }
     issue(kb + NSTAGE - 1, NSTAGE - 1);
     frags(0, 0, af[0], bf[0]);
     // half h of a substep's MFMAs: A tiles [h MI / 2, (h + 1) MI / 2)
@@ -696,10 +745,11 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
         if (threadIdx.x == 0) p.dg_part[logical] = (xg[0] + xg[1]) + (xg[2] + xg[3]);
     } else if constexpr (EPI == EPI_ROWS && OUT == OUT_DRADD) {
         // dk_f rows into dr at position - 1, with the carry of dkc into this
-        // 128-position tile (and, on its first row, the tile's own local dkc,
-        // which the dq_f epilogue of the tile before left out). The tile goes
-        // through LDS so that each half-wave reads, adds and writes one dr row
-        // in 16-byte runs (lane = 4 slots), every read issued before a store.
+        // 128-position tile formed before the k-loop (and, on its first row, the
+        // tile's own local dkc, which the dq_f epilogue of the tile before left
+        // out). The tile goes through LDS so that each half-wave reads, adds and
+        // writes one dr row in 16-byte runs (lane = 4 slots), every read issued
+        // before a store.
         static_assert(TM == 128 && TN == 128 && WAVES == 4, "dr accumulation: 128 x 128 tiles");
         constexpr int FS = TN + 4;                    // padded row stride in floats
         float *Fk = reinterpret_cast<float *>(lds);   // [TM][FS] dk_f; then the carry C and S per slot
@@ -715,13 +765,12 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
                 for (int r = 0; r < 16; ++r) Fk[(wm * (TM / 2) + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * FS + fl] = acc[i][j][r];
         }
         if (threadIdx.x < TN) {
-            const int f = n0 + static_cast<int>(threadIdx.x);
-            const size_t o = (static_cast<size_t>(b) * p.MT + m0 / TM) * p.F + (f < p.F ? f : 0);
-            sC[threadIdx.x] = f < p.F ? p.tC[o] : 0.f;
-            sS[threadIdx.x] = f < p.F ? p.tS[o] : 0.f;
+            sC[threadIdx.x] = carry;   // 0 past the slots: every S read there is 0
+            sS[threadIdx.x] = s_own;
         }
         __syncthreads();
-        const float g = p.g[0];
+        if (threadIdx.x == 0) p.dg_part[logical] = (xr[0] + xr[1]) + (xr[2] + xr[3]);
+        const float g = lgr;
         const int cl = lane % 32, half = lane / 32, c0 = 4 * cl;   // this lane's 4 slots of the tile
         const int f0 = n0 + c0;
         float cC[4], cS[4];
@@ -807,52 +856,44 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
     }
 }
 
-// The carry of dkc between 128-position tiles, per batch row and slot:
-// D_m = S_m + lam^128 D_{m+1} (D past the last tile 0) is dkc at the start of
-// tile m, and C_m = D_{m+1} the carry into tile m's end. Also per batch row
-// and slot the sum of the tiles' dw parts, and per block the carry's share of
-// the decay gradient, -sum_m K_m C_m. Fixed-order sums.
-__global__ __launch_bounds__(256) void carry_kernel(const float *__restrict__ tS, const float *__restrict__ tK,
-                                                    const float *__restrict__ tW, const float *__restrict__ g,
-                                                    float *__restrict__ tC, float *__restrict__ dwb,
-                                                    double *__restrict__ dg_part, int MT, int A) {
+// dw[a] = sum over batch rows of sum over tiles (last first) of the tiles'
+// dw parts, in that fixed order: blocks of 16 slots x 16 batch rows, the rows
+// summed through LDS. The last block sums the n1 + n2 decay-gradient partials
+// into dg in a fixed order.
+constexpr int kFinalSlots = 16;
+__global__ __launch_bounds__(256) void final_kernel(const float *__restrict__ tW, int MT, const double *__restrict__ p1,
+                                                    int n1, const double *__restrict__ p2, int n2,
+                                                    float *__restrict__ dw, float *__restrict__ dg, int B, int A) {
     __shared__ double red[4];
-    const int a = blockIdx.x * 256 + threadIdx.x;
-    const size_t b = blockIdx.y;
-    const float lam = __expf(g[0]);
-    float lam128 = lam;
-#pragma unroll
-    for (int e = 0; e < 7; ++e) lam128 *= lam128;
-    double corr = 0.0;
-    if (a < A) {
-        float D = 0.f, dw = 0.f;
-        for (int m = MT - 1; m >= 0; --m) {
-            const size_t o = (b * MT + m) * A + a;
-            tC[o] = D;
-            corr -= static_cast<double>(tK[o]) * D;
-            dw += tW[o];
-            D = tS[o] + lam128 * D;
-        }
-        dwb[b * A + a] = dw;
-    }
-    corr = wave_sum(corr);
-    if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = corr;
-    __syncthreads();
-    if (threadIdx.x == 0) dg_part[b * gridDim.x + blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
-}
-
-// dw[a] = sum_b dwb[b, a]; dg = the sum of n1 + n2 partials, in a fixed order
-__global__ __launch_bounds__(256) void final_kernel(const float *__restrict__ dwb, const double *__restrict__ p1, int n1,
-                                                    const double *__restrict__ p2, int n2, float *__restrict__ dw,
-                                                    float *__restrict__ dg, int B, int A) {
-    __shared__ double red[4];
-    const int a = blockIdx.x * 256 + threadIdx.x;
-    if (a < A) {
+    __shared__ float rows[16][kFinalSlots];
+    if (blockIdx.x + 1 < gridDim.x) {
+        const int al = threadIdx.x % kFinalSlots, bl = threadIdx.x / kFinalSlots;
+        const int a = blockIdx.x * kFinalSlots + al;
         float s = 0.f;
-        for (int b = 0; b < B; ++b) s += dwb[static_cast<size_t>(b) * A + a];
-        dw[a] = s;
+        for (int b0 = 0; b0 < B; b0 += 16) {
+            const int b = b0 + bl;
+            float row = 0.f;
+            if (a < A && b < B) {
+                float v[8];
+                int m = MT - 1;
+                for (; m >= 7; m -= 8) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) v[u] = tW[(static_cast<size_t>(b) * MT + m - u) * A + a];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) row += v[u];
+                }
+                for (; m >= 0; --m) row += tW[(static_cast<size_t>(b) * MT + m) * A + a];
+            }
+            rows[bl][al] = row;
+            __syncthreads();
+            if (bl == 0)
+                for (int k = 0; k < 16 && b0 + k < B; ++k) s += rows[k][al];
+            __syncthreads();
+        }
+        if (bl == 0 && a < A) dw[a] = s;
+        return;
     }
-    if (blockIdx.x == 0) {
+    {
         // each thread's partials in index order; eight loads in flight at a time
         auto sum = [](const double *__restrict__ p, int n, double s) {
             int k = threadIdx.x;
@@ -949,7 +990,7 @@ int launch(const Args &a, int G, int B, hipStream_t s) {
     } else if constexpr (EPI != EPI_ROWS) {
         return launch_o<TA, false, EPI, 0>(a, G, B, s);
     } else {
-        if (a.tC) return launch_o<TA, false, EPI, OUT_DRADD>(a, G, B, s);
+        if (a.drtile) return launch_o<TA, false, EPI, OUT_DRADD>(a, G, B, s);
         const int out = a.out_dt + (a.resid ? 3 : 0);
         switch (out) {
         case 0: return launch_o<TA, false, EPI, 0>(a, G, B, s);
@@ -1041,23 +1082,21 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *
 // sums and the decay-gradient partials of the dq_f tiles and of the carry.
 namespace {
 struct PairStats {
-    float *tS, *tK, *tW, *tC, *dwb;
-    double *dgq, *dgc;
+    float *tS, *tK, *tW;
+    double *dgq, *dgk;
     size_t bytes;
 };
 PairStats pair_stats_layout(void *base, int B, int T, int A) {
     const int G = pair_block(B, T), MT = pair_tq(B, T) / G;
     const size_t nst = static_cast<size_t>(B) * MT * A;
-    const size_t jobs_q = static_cast<size_t>(B) * MT * ((A + G - 1) / G), blocks_c = static_cast<size_t>(B) * ((A + 255) / 256);
+    const size_t jobs = static_cast<size_t>(B) * MT * ((A + G - 1) / G);
     Carver c(base);
     PairStats w{};
     w.tS = c.take<float>(nst);
     w.tK = c.take<float>(nst);
     w.tW = c.take<float>(nst);
-    w.tC = c.take<float>(nst);
-    w.dwb = c.take<float>(static_cast<size_t>(B) * A);
-    w.dgq = c.take<double>(jobs_q + blocks_c);   // the carry partials follow the tiles'
-    w.dgc = w.dgq + jobs_q;
+    w.dgq = c.take<double>(2 * jobs);   // the dq_f jobs' partials, then the dk_f jobs'
+    w.dgk = w.dgq + jobs;
     w.bytes = c.off;
     return w;
 }
@@ -1083,6 +1122,7 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
     const int G = pair_block(B, T), Tq = pair_tq(B, T), NT = (T + 63) / 64, MT = Tq / G;
     const int Ap = (A + 31) / 32 * 32, Dp = (D + 31) / 32 * 32;   // operand tile widths
     const PairStats st = pair_stats_layout(ws, B, T, A);
+    if (MT > 32) return fail(ULM_ERR_UNSUPPORTED, "block-pair backward: %d position tiles (at most 32)", MT);
     const Mat sm = p_mat(dS, Tq);
     {
         // dv = P^T dfast first, so that dq_f / dk_f meet their epilogues' inputs fresh
@@ -1147,20 +1187,19 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
     r.krange = K_CAUSAL;
     r.dg_part = st.dgq;
     ULM_TRY((launch<false, EPI_DQSTATS>(r, G, B, s)));
-    pair::carry_kernel<<<dim3((A + 255) / 256, B), 256, 0, s>>>(st.tS, st.tK, st.tW, g, st.tC, st.dwb, st.dgc, MT, A);
-    ULM_TRY(check_launch("carry_kernel"));
     // dk_f = dS^T q (rows s of dSt, contraction t >= the start of s's block), into dr
+    // with the carry between tiles, which its epilogue forms from the tiles' S
     r.a = p_mat(dSt, Tq);
     r.b = q_mat(qQ, NT, Ap);
     r.krange = K_ANTI;
     r.out = dr;
     r.out_dt = ULM_F32;
-    r.tC = st.tC;
-    r.dg_part = nullptr;
+    r.drtile = 1;
+    r.dg_part = st.dgk;
     ULM_TRY((launch<false, EPI_ROWS>(r, G, B, s)));
-    const int jobs_q = B * MT * ((A + G - 1) / G), blocks_c = B * ((A + 255) / 256);
-    pair::final_kernel<<<(A + 255) / 256, 256, 0, s>>>(st.dwb, st.dgq, jobs_q + blocks_c, dg_part,
-                                                       pair_dscore_jobs(B, T), dw, dg, B, A);
+    const int jobs = B * MT * ((A + G - 1) / G);
+    pair::final_kernel<<<(A + pair::kFinalSlots - 1) / pair::kFinalSlots + 1, 256, 0, s>>>(
+        st.tW, MT, st.dgq, 2 * jobs, dg_part, pair_dscore_jobs(B, T), dw, dg, B, A);
     return check_launch("final_kernel");
 }
 

@@ -152,26 +152,27 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
     const float wa = va ? w[a] : 1.f;
     const float rb = va ? rs.slot_const(a) : 0.f;   // the slot's key bias when r is formed here
     float carry = 0.f;   // n at the position before the chunk
-    // the stored elements of the next chunk's positions t0 .. t0+15 and t0 - 1,
-    // and their denominators, loaded one chunk ahead
-    typename RS::raw_t pv[kSeg + 1];
-    float pd;
-    auto fetch = [&](int n) {
+    // the stored elements of a chunk's positions t0 .. t0+15 and t0 - 1, and
+    // their denominators, loaded two chunks ahead into alternating buffers
+    typename RS::raw_t pv[2][kSeg + 1];
+    float pd[2];
+    auto fetch = [&](int n, int u) {
         const int t0 = n * ULM_CHUNK + j * kSeg;
-        pd = seg_row_raw(rs, bs * T + t0, t0, T, s);
+        pd[u] = seg_row_raw(rs, bs * T + t0, t0, T, s);
 #pragma unroll
-        for (int i = 0; i < kSeg; ++i) pv[i] = rs.raw(urow(bs, t0 + i, T), ac, A);
-        pv[kSeg] = rs.raw(urow(bs, t0 - 1, T), ac, A);
+        for (int i = 0; i < kSeg; ++i) pv[u][i] = rs.raw(urow(bs, t0 + i, T), ac, A);
+        pv[u][kSeg] = rs.raw(urow(bs, t0 - 1, T), ac, A);
     };
-    fetch(0);
-    for (int n = 0; n < NT; ++n) {
+    fetch(0, 0);
+    if (NT > 1) fetch(1, 1);
+    auto chunk = [&](int n, int u) {
         const int t0 = n * ULM_CHUNK + j * kSeg;
-        const float seg_c = seg_inv<RS>(pd);
+        const float seg_c = seg_inv<RS>(pd[u]);
         float rv[kSeg], kv[kSeg], nl[kSeg];
 #pragma unroll
-        for (int i = 0; i < kSeg; ++i) rv[i] = rs.make(pv[i], rb, lane_value(seg_c, i), va && t0 + i < T);
-        kv[0] = rs.make(pv[kSeg], rb, lane_value(seg_c, kSeg), va && t0 >= 1 && t0 - 1 < T);
-        if (n + 1 < NT) fetch(n + 1);
+        for (int i = 0; i < kSeg; ++i) rv[i] = rs.make(pv[u][i], rb, lane_value(seg_c, i), va && t0 + i < T);
+        kv[0] = rs.make(pv[u][kSeg], rb, lane_value(seg_c, kSeg), va && t0 >= 1 && t0 - 1 < T);
+        if (n + 2 < NT) fetch(n + 2, u);
 #pragma unroll
         for (int i = 1; i < kSeg; ++i) kv[i] = rv[i - 1];
         float acc = 0.f;
@@ -246,6 +247,10 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
             }
         }
         __syncthreads();   // sq, sk read before the next chunk writes them
+    };
+    for (int n = 0; n < NT; n += 2) {
+        chunk(n, 0);
+        if (n + 1 < NT) chunk(n + 1, 1);
     }
 }
 

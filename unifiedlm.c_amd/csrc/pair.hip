@@ -50,6 +50,7 @@
 // product's accumulation into dr (OUT_DRADD).
 #include "ulm_common.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace ulm {
@@ -1032,6 +1033,30 @@ double pair_flops_per_token(int B, int T, int A, int D) {
     return nb * (nb + 1) * G * G * 3.0 * (A + D) / T;
 }
 
+namespace {
+// A second stream per device (default priority) and its fork / join events:
+// the backward's dv product runs on it beside the dscores product, which
+// leaves a quarter of the CUs' workgroup slots free
+struct SideStream {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+int side_stream(SideStream *&out) {
+    static SideStream sides[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return check_launch("hipGetDevice");
+    SideStream &sd = sides[dev];
+    if (!sd.s) {
+        if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess)
+            return check_launch("side stream");
+    }
+    out = &sd;
+    return ULM_OK;
+}
+}  // namespace
+
 // P = scores(q, k) in the P layout (Tq x Tq per batch row), its transpose
 // Pt and its bf16 residual Plo (P layout), then out = P v (+ resid) in out_dt
 // (B, T, D). qR, kR: R layout (A); vQ: Q layout (D).
@@ -1104,11 +1129,17 @@ PairStats pair_stats_layout(void *base, int B, int T, int A) {
 
 size_t pair_stats_bytes(int B, int T, int A) { return pair_stats_layout(nullptr, B, T, A).bytes; }
 
-// The backward: dv = P^T dfast in dv_dt (B, T, D); dS = dscores(dfast, v) and
-// its transpose dSt with the pair part of the decay gradient; dq_f = dS k with
-// the per-slot statistics in its epilogue (dr without dk_f and the carry; the
-// tile statistics); the carry of dkc between tiles; dk_f = dS^T q added into dr
-// with the carry; dw (A,) and dg (1,) reduced in a fixed order. vR, doR: R
+
+
+// The backward: dv = P^T dfast in dv_dt (B, T, D), on the device's second
+// stream (forked from s and joined back into s before the return, so that work
+// later on s is ordered after it); dS = dscores(dfast, v) and its transpose dSt
+// with the pair part of the decay gradient; dq_f = dS k with the per-slot
+// statistics in its epilogue (dr without dk_f and the carry; the tile
+// statistics); dk_f = dS^T q added into dr with the carry of dkc between
+// tiles, formed in that product; dw (A,) and dg (1,) reduced in a fixed order.
+// Calls from several host threads enqueue one at a time: the fork and join
+// events are shared. vR, doR: R
 // layout (D); kQ, qQ: Q layout (A); doQ: Q layout (D); P, Pt, Plo from the
 // forward. r: the read addresses (or their address inputs); xq / xq_kind: the
 // extra gradient of q (0 none, 1 dq_out fp32, 2 + dtype d(w q)); nck: the
@@ -1124,8 +1155,14 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
     const PairStats st = pair_stats_layout(ws, B, T, A);
     if (MT > 32) return fail(ULM_ERR_UNSUPPORTED, "block-pair backward: %d position tiles (at most 32)", MT);
     const Mat sm = p_mat(dS, Tq);
+    // dv = P^T dfast on the second stream, beside dscores (joined at the end)
+    static std::mutex side_mu;
+    const std::lock_guard<std::mutex> lock(side_mu);
+    SideStream *sd = nullptr;
+    ULM_TRY(side_stream(sd));
+    if (hipEventRecord(sd->fork, s) != hipSuccess || hipStreamWaitEvent(sd->s, sd->fork, 0) != hipSuccess)
+        return check_launch("side stream fork");
     {
-        // dv = P^T dfast first, so that dq_f / dk_f meet their epilogues' inputs fresh
         Args d{};
         d.T = T;
         d.g = g;
@@ -1139,7 +1176,8 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
         d.out = dv;
         d.out_dt = dv_dt;
         d.F = D;
-        ULM_TRY((launch<false, EPI_ROWS>(d, G, B, s)));
+        ULM_TRY((launch<false, EPI_ROWS>(d, G, B, sd->s)));
+        if (hipEventRecord(sd->join, sd->s) != hipSuccess) return check_launch("side stream join");
     }
     Args a{};
     a.T = T;
@@ -1200,7 +1238,9 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
     const int jobs = B * MT * ((A + G - 1) / G);
     pair::final_kernel<<<(A + pair::kFinalSlots - 1) / pair::kFinalSlots + 1, 256, 0, s>>>(
         st.tW, MT, st.dgq, 2 * jobs, dg_part, pair_dscore_jobs(B, T), dw, dg, B, A);
-    return check_launch("final_kernel");
+    ULM_TRY(check_launch("final_kernel"));
+    if (hipStreamWaitEvent(s, sd->join, 0) != hipSuccess) return check_launch("side stream wait");
+    return ULM_OK;
 }
 
 }  // namespace ulm

@@ -424,6 +424,12 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
                                                     : reinterpret_cast<const char *>(p.pout_lo) + b * p.p_bstride,
                                  p.p_bstride);
         float dg = 0.f;
+        // the transpose goes through the stage memory as bf16 [s][t] (rows
+        // padded to XS elements), then out in 16-byte runs of t
+        constexpr int XS = TN + 8;
+        static_assert(TM * XS * 2 <= nstage<TM, EPI>() * (TM / 32 * KT + TN / 32 * KT) * TB, "transpose staging");
+        uint16_t *Xt = reinterpret_cast<uint16_t *>(lds);
+        __syncthreads();   // every wave past its last operand read
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
             const int t = n0 + wn * (TN / 2) + 32 * j + lc;
@@ -473,15 +479,20 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
                         vl[1] = static_cast<uint32_t>(lb[2]) | (static_cast<uint32_t>(lb[3]) << 16);
                         __builtin_amdgcn_raw_buffer_store_b64(vl, rplo, off, 0, 0);
                     }
-                    // the transpose: element (row s, contraction t), one 2-byte store
-                    // each (the lanes of one s write 16-byte runs of t)
-                    const uint32_t off_t = (t / 16) * TB + 16u * 32 * ((t % 16) / 8) + 2u * (t % 8);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int s = s0 + e;
-                        __builtin_amdgcn_raw_buffer_store_b16(xb[e], rpt, off_t + (s / 32) * p.p_rt + 16u * (s % 32), 0, 0);
-                    }
+                    for (int e = 0; e < 4; ++e) Xt[(s0 - m0 + e) * XS + (t - n0)] = xb[e];
                 }
+        }
+        __syncthreads();
+        // the transpose: rows s, contraction t, 16 bytes (8 t) of one s per lane;
+        // 32 consecutive lanes take the 32 rows s of one P-layout tile
+#pragma unroll 4
+        for (int c = threadIdx.x; c < TM * TN / 8; c += WAVES * 64) {
+            const int sl = 32 * (c / (32 * (TN / 8))) + c % 32, t8 = (c / 32) % (TN / 8);
+            const int s = m0 + sl, t = n0 + 8 * t8;
+            const gv4u32_t v = *reinterpret_cast<const gv4u32_t *>(Xt + sl * XS + 8 * t8);
+            __builtin_amdgcn_raw_buffer_store_b128(v, rpt, (t / 16) * TB + 16u * 32 * ((t % 16) / 8) + (s / 32) * p.p_rt + 16u * (s % 32),
+                                                   0, 0);
         }
         if constexpr (EPI == EPI_DSCORES) {
             // the wave sums meet in the stage memory, once every wave is past

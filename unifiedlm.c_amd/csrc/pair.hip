@@ -62,7 +62,6 @@ namespace pair {
 
 constexpr uint32_t TB = 1024;           // bytes per operand tile
 constexpr uint32_t OOB = 0x80000000u;   // buffer offset past every range: loads return zeros
-constexpr int WAVES = 4;
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
@@ -109,6 +108,9 @@ template <int TM, int EPI> constexpr int nstage() {
     return TM == 256 ? 5 : (EPI == EPI_SCORES || EPI == EPI_DSCORES ? 3 : 4);
 }
 template <int TM, int EPI> constexpr int min_blocks() { return TM == 256 ? 1 : (nstage<TM, EPI>() == 3 ? 3 : 2); }
+// Waves per workgroup, in a (waves / 2) x 2 layout: eight for the 256 x 256
+// scores (two per SIMD, one workgroup per CU), else four
+template <int TM, int EPI> constexpr int waves_of() { return TM == 256 && EPI == EPI_SCORES ? 8 : 4; }
 
 struct Args {
     Mat a, b;
@@ -186,12 +188,14 @@ __device__ __forceinline__ void wait_copies(int ksteps) {
 // output, OUT >= 3 adds an fp32 residual; the statistics epilogue uses OUT
 // for its input kinds.
 template <int TM, int TN, int KT, bool TA, bool TBt, int EPI, int OUT>
-__global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kernel(Args p) {
-    constexpr int MI = TM / 64, NI = TN / 64;          // 32-row / 32-column tiles per wave
+__global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI>())) void pair_kernel(Args p) {
+    constexpr int WV = waves_of<TM, EPI>(), WM = WV / 2;   // waves, and waves along m
+    constexpr int MI = TM / (32 * WM), NI = TN / 64;       // 32-row / 32-column tiles per wave
     constexpr int KS = 16 * KT;                        // contraction elements per k-step
     constexpr int A_TILES = TM / 32 * KT, B_TILES = TN / 32 * KT;   // tiles per k-step
     constexpr uint32_t STAGE = (A_TILES + B_TILES) * TB;
-    constexpr int AC = A_TILES / WAVES, BC = B_TILES / WAVES;       // copies per wave per k-step
+    constexpr int AC = A_TILES / WV, BC = B_TILES / WV;             // copies per wave per k-step
+    static_assert(A_TILES % WV == 0 && B_TILES % WV == 0 && MI % 2 == 0, "copies per wave and MFMA halves");
     constexpr int LPW = AC + BC;
     constexpr int NSTAGE = nstage<TM, EPI>();
     static_assert(KT % 2 == 0 && NSTAGE >= 2 && NSTAGE - 2 <= 4, "k-step and stage count");
@@ -242,7 +246,7 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
     // per-copy part of copy c's offset (OOB bit set when never valid) and the
     // k-steps kk < lim for which it is valid; independent of kk, so hoisted
     auto copy_off = [&](const Mat &m, bool trans, int tile0, int TX, uint32_t lane_off, int c, int &lim) -> uint32_t {
-        const int q = wave + WAVES * c;
+        const int q = wave + WV * c;
         if (!trans) {
             const int rt = tile0 / 32 + q / KT;
             lim = m.nkt / KT;                            // nkt is even: kt = 2 kk + q % 2 < nkt
@@ -260,14 +264,14 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
         for (int c = 0; c < AC; ++c) {
             int lim;
             const uint32_t off = copy_off(p.a, TA, m0, TM, TA ? lane_tr : lane16, c, lim);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(base + (wave + WAVES * c) * TB), 16,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(base + (wave + WV * c) * TB), 16,
                                                      (off + ka) | (kk < lim ? past : OOB), 0, 0, 0);
         }
 #pragma unroll
         for (int c = 0; c < BC; ++c) {
             int lim;
             const uint32_t off = copy_off(p.b, TBt, n0, TN, TBt ? lane_tr : lane16, c, lim);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void *)(base + (A_TILES + wave + WAVES * c) * TB), 16,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void *)(base + (A_TILES + wave + WV * c) * TB), 16,
                                                      (off + kb2) | (kk < lim ? past : OOB), 0, 0, 0);
         }
     };
@@ -336,7 +340,7 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
     // values: a skipped load costs no address cycles).
     constexpr int MAXMT = 32;   // T <= 4096 on this form
     float sv[OUT == OUT_DRADD ? MAXMT : 1], carry = 0.f, s_own = 0.f, kown = 0.f, lgr = 0.f;
-    __shared__ double xr[WAVES];
+    __shared__ double xr[WV];
     if constexpr (OUT == OUT_DRADD) {
         const int f = n0 + static_cast<int>(threadIdx.x), mt = m0 / TM;
         const bool fok = threadIdx.x < TN && f < p.F;
@@ -437,7 +441,7 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int r4 = 0; r4 < 4; ++r4) {
-                    const int s0 = m0 + wm * (TM / 2) + 32 * i + 8 * r4 + 4 * h;
+                    const int s0 = m0 + wm * (TM / WM) + 32 * i + 8 * r4 + 4 * h;
                     const uint32_t off = (t / 32) * p.p_rt + (s0 / 16) * TB + 16u * (t % 32 + 32 * ((s0 % 16) / 8)) +
                                          2u * (s0 % 8);
                     float x[4];
@@ -487,7 +491,7 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
         // the transpose: rows s, contraction t, 16 bytes (8 t) of one s per lane;
         // 32 consecutive lanes take the 32 rows s of one P-layout tile
 #pragma unroll 4
-        for (int c = threadIdx.x; c < TM * TN / 8; c += WAVES * 64) {
+        for (int c = threadIdx.x; c < TM * TN / 8; c += WV * 64) {
             const int sl = 32 * (c / (32 * (TN / 8))) + c % 32, t8 = (c / 32) % (TN / 8);
             const int s = m0 + sl, t = n0 + 8 * t8;
             const gv4u32_t v = *reinterpret_cast<const gv4u32_t *>(Xt + sl * XS + 8 * t8);
@@ -525,13 +529,13 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
         // j / 4, that chunk's 16-position segment j % 4, as the forward
         // statistics split it), so that c is formed with the forward's
         // operations; segments meet through LDS.
-        static_assert(TM == 128 && TN == 128 && WAVES * 64 == 256, "statistics epilogue: 128 x 128 tiles");
+        static_assert(TM == 128 && TN == 128 && WV * 64 == 256, "statistics epilogue: 128 x 128 tiles");
         constexpr int SEG = 16, NSEG = TM / SEG;
         // segment totals: forward (xa, xb) and reverse (ya, yb), each in two
         // copies used by alternate rounds, so that two barriers per round order
         // every write after the reads it could overwrite
         __shared__ float xa[2][NSEG][32], xb[2][NSEG][32], ya[2][NSEG][32], yb[2][NSEG][32];
-        __shared__ double xg[WAVES];
+        __shared__ double xg[WV];
         __shared__ float sidn[TM + 1];               // 1 / denom at positions m0 - 1 .. m0 + 127
         float *F = reinterpret_cast<float *>(lds);   // [128 t][128 a] fp32: the 64 KB of stage memory
         __syncthreads();                             // every wave past its last operand read
@@ -542,7 +546,7 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) F[(wm * (TM / 2) + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * 128 + fl] = acc[i][j][r];
+                for (int r = 0; r < 16; ++r) F[(wm * (TM / WM) + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * 128 + fl] = acc[i][j][r];
         }
         if constexpr (OUT / 2 != 0) {
             if (threadIdx.x <= TM) {
@@ -762,7 +766,7 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
         // out). The tile goes through LDS so that each half-wave reads, adds and
         // writes one dr row in 16-byte runs (lane = 4 slots), every read issued
         // before a store.
-        static_assert(TM == 128 && TN == 128 && WAVES == 4, "dr accumulation: 128 x 128 tiles");
+        static_assert(TM == 128 && TN == 128 && WV == 4, "dr accumulation: 128 x 128 tiles");
         constexpr int FS = TN + 4;                    // padded row stride in floats
         float *Fk = reinterpret_cast<float *>(lds);   // [TM][FS] dk_f; then the carry C and S per slot
         float *sC = Fk + TM * FS, *sS = sC + TN;
@@ -774,7 +778,7 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) Fk[(wm * (TM / 2) + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * FS + fl] = acc[i][j][r];
+                for (int r = 0; r < 16; ++r) Fk[(wm * (TM / WM) + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * FS + fl] = acc[i][j][r];
         }
         if (threadIdx.x < TN) {
             sC[threadIdx.x] = carry;   // 0 past the slots: every S read there is 0
@@ -794,7 +798,7 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
         const rsrc_t ro = rsrc(static_cast<float *>(p.out) + static_cast<size_t>(b) * p.T * p.F,
                                static_cast<size_t>(p.T) * p.F * 4);
         // rows 2 (wave + 4 k) + half, k = 0 .. 15: two rows per wave per step
-        auto row_of = [&](int k) { return 2 * (wave + WAVES * k) + half; };
+        auto row_of = [&](int k) { return 2 * (wave + WV * k) + half; };
         auto off_of = [&](int k, int e) -> uint32_t {
             const int pos = m0 + row_of(k);
             const bool ok = pos >= 1 && pos < p.T && f0 + e < p.F;
@@ -808,12 +812,12 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
         };
         if (p.F % 4 == 0) {
             // 16-byte aligned runs, wholly in or out of the slots
-            v4f32_t old[TM / (2 * WAVES)];
+            v4f32_t old[TM / (2 * WV)];
 #pragma unroll
-            for (int k = 0; k < TM / (2 * WAVES); ++k)
+            for (int k = 0; k < TM / (2 * WV); ++k)
                 old[k] = __builtin_bit_cast(v4f32_t, __builtin_amdgcn_raw_buffer_load_b128(ro, off_of(k, 0), 0, 0));
 #pragma unroll
-            for (int k = 0; k < TM / (2 * WAVES); ++k) {
+            for (int k = 0; k < TM / (2 * WV); ++k) {
                 v4f32_t v;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = sum(k, e, old[k][e]);
@@ -821,7 +825,7 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
             }
         } else {
 #pragma unroll 2
-            for (int k = 0; k < TM / (2 * WAVES); ++k) {
+            for (int k = 0; k < TM / (2 * WV); ++k) {
                 float old[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
@@ -851,7 +855,7 @@ __global__ __launch_bounds__(WAVES * 64, (min_blocks<TM, EPI>())) void pair_kern
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int pos = m0 + wm * (TM / 2) + 32 * i + 8 * (r / 4) + 4 * h + r % 4;
+                    const int pos = m0 + wm * (TM / WM) + 32 * i + 8 * (r / 4) + 4 * h + r % 4;
                     const uint32_t el = static_cast<uint32_t>(pos) * p.F + f;
                     const uint32_t bad = (fok && pos < p.T) ? 0u : OOB;
                     float v = acc[i][j][r];
@@ -968,7 +972,7 @@ int launch_g(Args a, int B, hipStream_t s) {
     a.jobs = B * a.jobs_per_row;
     int st = la_timer_begin(s);
     if (st) return st;
-    pair_kernel<G, G, KT, TA, TBt, EPI, OUT><<<dim3(static_cast<unsigned>(a.jobs)), WAVES * 64, lds, s>>>(a);
+    pair_kernel<G, G, KT, TA, TBt, EPI, OUT><<<dim3(static_cast<unsigned>(a.jobs)), waves_of<G, EPI>() * 64, lds, s>>>(a);
     st = check_launch("pair_kernel");
     if (st) return st;
     return la_timer_end(s);

@@ -62,6 +62,7 @@ namespace pair {
 
 constexpr uint32_t TB = 1024;           // bytes per operand tile
 constexpr uint32_t OOB = 0x80000000u;   // buffer offset past every range: loads return zeros
+constexpr int kNT = 2;                  // buffer cache policy: non-temporal (streamed, evicted first)
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
@@ -588,7 +589,9 @@ __global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI>())
         // The loads of round rd + 1 are issued while round rd computes: r (or
         // pre), the extra gradient of q, n at the chunk start, w and the bias
         // of this thread's slot, each through a range-checked buffer load (no
-        // branch between them).
+        // branch between them). r and the extra gradient are read once and dr
+        // written once: their loads and stores carry the non-temporal hint
+        // (kNT), so that they do not push the operand tiles out of the caches.
         const rsrc_t rs_nck = rsrc(p.nck + static_cast<size_t>(b) * p.NT * p.F, 4ull * p.NT * p.F);
         const rsrc_t rs_w = rsrc(p.w, 4ull * p.F);
         const rsrc_t rs_bias = rsrc(p.bias ? p.bias : p.w, p.bias ? 4ull * p.F : 0);
@@ -603,14 +606,14 @@ __global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI>())
 #pragma unroll
             for (int i = 0; i <= SEG; ++i) {
                 const uint32_t off = (pes * static_cast<uint32_t>((t0 - 1 + i) * p.F + ac)) | bad_a;
-                rraw[i] = pes == 4u ? __builtin_amdgcn_raw_buffer_load_b32(rs_in, off, 0, 0)
-                                    : static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(rs_in, off, 0, 0));
+                rraw[i] = pes == 4u ? __builtin_amdgcn_raw_buffer_load_b32(rs_in, off, 0, kNT)
+                                    : static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(rs_in, off, 0, kNT));
             }
 #pragma unroll
             for (int i = 0; i < SEG; ++i) {
                 const uint32_t off = (xes * static_cast<uint32_t>((t0 + i) * p.F + ac)) | bad_a;
-                xraw[i] = X4 ? __builtin_amdgcn_raw_buffer_load_b32(rs_xq, off, 0, 0)
-                             : static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(rs_xq, off, 0, 0));
+                xraw[i] = X4 ? __builtin_amdgcn_raw_buffer_load_b32(rs_xq, off, 0, kNT)
+                             : static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(rs_xq, off, 0, kNT));
             }
             nraw = __builtin_amdgcn_raw_buffer_load_b32(rs_nck, (4u * static_cast<uint32_t>((t0 / 64) * p.F + ac)) | bad_a, 0, 0);
             wraw = __builtin_amdgcn_raw_buffer_load_b32(rs_w, (4u * static_cast<uint32_t>(ac)) | bad_a, 0, 0);
@@ -738,7 +741,7 @@ __global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI>())
                 const int t = t0 + i;
                 __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, dqc[i] + lnext), rs_dr,
                                                       (4u * static_cast<uint32_t>(t * p.F + (va ? a : 0))) |
-                                                          (static_cast<uint32_t>(!va) << 31), 0, 0);
+                                                          (static_cast<uint32_t>(!va) << 31), 0, kNT);
                 pr *= lam;
             }
             if (sj == NSEG - 1 && va) {
@@ -815,13 +818,13 @@ __global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI>())
             v4f32_t old[TM / (2 * WV)];
 #pragma unroll
             for (int k = 0; k < TM / (2 * WV); ++k)
-                old[k] = __builtin_bit_cast(v4f32_t, __builtin_amdgcn_raw_buffer_load_b128(ro, off_of(k, 0), 0, 0));
+                old[k] = __builtin_bit_cast(v4f32_t, __builtin_amdgcn_raw_buffer_load_b128(ro, off_of(k, 0), 0, kNT));
 #pragma unroll
             for (int k = 0; k < TM / (2 * WV); ++k) {
                 v4f32_t v;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = sum(k, e, old[k][e]);
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(gv4u32_t, v), ro, off_of(k, 0), 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(gv4u32_t, v), ro, off_of(k, 0), 0, kNT);
             }
         } else {
 #pragma unroll 2

@@ -1173,13 +1173,17 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
     const PairStats st = pair_stats_layout(ws, B, T, A);
     if (MT > 32) return fail(ULM_ERR_UNSUPPORTED, "block-pair backward: %d position tiles (at most 32)", MT);
     const Mat sm = p_mat(dS, Tq);
-    // dv = P^T dfast on the second stream, beside dscores (joined at the end)
+    // dv = P^T dfast on the second stream, beside dscores (joined at the end),
+    // where its work outweighs the fork and join: each event between two
+    // dependent kernels costs several microseconds of gap
     static std::mutex side_mu;
     const std::lock_guard<std::mutex> lock(side_mu);
     SideStream *sd = nullptr;
-    ULM_TRY(side_stream(sd));
-    if (hipEventRecord(sd->fork, s) != hipSuccess || hipStreamWaitEvent(sd->s, sd->fork, 0) != hipSuccess)
-        return check_launch("side stream fork");
+    if (static_cast<double>(B) * Tq * Tq * D >= 2e9) {
+        ULM_TRY(side_stream(sd));
+        if (hipEventRecord(sd->fork, s) != hipSuccess || hipStreamWaitEvent(sd->s, sd->fork, 0) != hipSuccess)
+            return check_launch("side stream fork");
+    }
     {
         Args d{};
         d.T = T;
@@ -1194,8 +1198,8 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
         d.out = dv;
         d.out_dt = dv_dt;
         d.F = D;
-        ULM_TRY((launch<false, EPI_ROWS>(d, G, B, sd->s)));
-        if (hipEventRecord(sd->join, sd->s) != hipSuccess) return check_launch("side stream join");
+        ULM_TRY((launch<false, EPI_ROWS>(d, G, B, sd ? sd->s : s)));
+        if (sd && hipEventRecord(sd->join, sd->s) != hipSuccess) return check_launch("side stream join");
     }
     Args a{};
     a.T = T;
@@ -1257,7 +1261,7 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
     pair::final_kernel<<<(A + pair::kFinalSlots - 1) / pair::kFinalSlots + 1, 256, 0, s>>>(
         st.tW, MT, st.dgq, 2 * jobs, dg_part, pair_dscore_jobs(B, T), dw, dg, B, A);
     ULM_TRY(check_launch("final_kernel"));
-    if (hipStreamWaitEvent(s, sd->join, 0) != hipSuccess) return check_launch("side stream wait");
+    if (sd && hipStreamWaitEvent(s, sd->join, 0) != hipSuccess) return check_launch("side stream wait");
     return ULM_OK;
 }
 

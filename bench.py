@@ -73,8 +73,8 @@ def log(msg):
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=5)
-    p.add_argument("--warmup", type=int, default=2)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--shape", default="110M")
     p.add_argument("--decode-steps", type=int, default=256)
     p.add_argument("--prefill", type=int, default=512)

@@ -105,10 +105,12 @@ enum KRange { K_FULL = 0, K_CAUSAL = 1, K_ANTI = 2 };
 // per CU) for the products whose jobs vary in length, and 48 KB (three per
 // CU) for the scores and dscores, whose equal jobs (B T^2 / 2 G^2 of them)
 // would otherwise leave a short second wave
-template <int TM, int EPI> constexpr int nstage() {
-    return TM == 256 ? 5 : (EPI == EPI_SCORES || EPI == EPI_DSCORES ? 3 : 4);
+template <int TM, int EPI, int OUT = 0> constexpr int nstage() {
+    return TM == 256 ? 5 : (EPI == EPI_SCORES || EPI == EPI_DSCORES || OUT == OUT_DRADD ? 3 : 4);
 }
-template <int TM, int EPI> constexpr int min_blocks() { return TM == 256 ? 1 : (nstage<TM, EPI>() == 3 ? 3 : 2); }
+template <int TM, int EPI, int OUT = 0> constexpr int min_blocks() {
+    return TM == 256 ? 1 : (nstage<TM, EPI, OUT>() == 3 ? 3 : 2);
+}
 // Waves per workgroup, in a (waves / 2) x 2 layout: eight for the 256 x 256
 // scores (two per SIMD, one workgroup per CU), else four
 template <int TM, int EPI> constexpr int waves_of() { return TM == 256 && EPI == EPI_SCORES ? 8 : 4; }
@@ -189,7 +191,7 @@ __device__ __forceinline__ void wait_copies(int ksteps) {
 // output, OUT >= 3 adds an fp32 residual; the statistics epilogue uses OUT
 // for its input kinds.
 template <int TM, int TN, int KT, bool TA, bool TBt, int EPI, int OUT>
-__global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI>())) void pair_kernel(Args p) {
+__global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI, OUT>())) void pair_kernel(Args p) {
     constexpr int WV = waves_of<TM, EPI>(), WM = WV / 2;   // waves, and waves along m
     constexpr int MI = TM / (32 * WM), NI = TN / 64;       // 32-row / 32-column tiles per wave
     constexpr int KS = 16 * KT;                        // contraction elements per k-step
@@ -198,7 +200,7 @@ __global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI>())
     constexpr int AC = A_TILES / WV, BC = B_TILES / WV;             // copies per wave per k-step
     static_assert(A_TILES % WV == 0 && B_TILES % WV == 0 && MI % 2 == 0, "copies per wave and MFMA halves");
     constexpr int LPW = AC + BC;
-    constexpr int NSTAGE = nstage<TM, EPI>();
+    constexpr int NSTAGE = nstage<TM, EPI, OUT>();
     static_assert(KT % 2 == 0 && NSTAGE >= 2 && NSTAGE - 2 <= 4, "k-step and stage count");
     extern __shared__ __align__(16) char lds[];
 
@@ -766,77 +768,90 @@ __global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI>())
         // dk_f rows into dr at position - 1, with the carry of dkc into this
         // 128-position tile formed before the k-loop (and, on its first row, the
         // tile's own local dkc, which the dq_f epilogue of the tile before left
-        // out). The tile goes through LDS so that each half-wave reads, adds and
-        // writes one dr row in 16-byte runs (lane = 4 slots), every read issued
-        // before a store.
+        // out). The tile goes through LDS in two halves of 64 rows (the halves
+        // of the waves wm = 0 and 1), so that each half-wave reads, adds and
+        // writes one dr row in 16-byte runs (lane = 4 slots); every dr read of the
+        // tile is issued before the first store. Half a tile of LDS (34 KB)
+        // stays within the three 16 KB stages: three workgroups per CU.
         static_assert(TM == 128 && TN == 128 && WV == 4, "dr accumulation: 128 x 128 tiles");
         constexpr int FS = TN + 4;                    // padded row stride in floats
-        float *Fk = reinterpret_cast<float *>(lds);   // [TM][FS] dk_f; then the carry C and S per slot
-        float *sC = Fk + TM * FS, *sS = sC + TN;
+        constexpr int HR = TM / 2;                    // rows per half
+        float *Fk = reinterpret_cast<float *>(lds);   // [HR][FS] dk_f; then the carry C and S per slot
+        float *sC = Fk + HR * FS, *sS = sC + TN;
         __syncthreads();                              // every wave past its last operand read
-#pragma unroll
-        for (int j = 0; j < NI; ++j) {
-            const int n = wn * (TN / 2) + 32 * j + lc;
-            const int fl = p.nperm ? (n & ~31) + perm32(n & 31) : n;
-#pragma unroll
-            for (int i = 0; i < MI; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) Fk[(wm * (TM / WM) + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * FS + fl] = acc[i][j][r];
-        }
-        if (threadIdx.x < TN) {
-            sC[threadIdx.x] = carry;   // 0 past the slots: every S read there is 0
-            sS[threadIdx.x] = s_own;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) p.dg_part[logical] = (xr[0] + xr[1]) + (xr[2] + xr[3]);
         const float g = lgr;
         const int cl = lane % 32, half = lane / 32, c0 = 4 * cl;   // this lane's 4 slots of the tile
         const int f0 = n0 + c0;
-        float cC[4], cS[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            cC[e] = sC[c0 + e];
-            cS[e] = sS[c0 + e];
-        }
         const rsrc_t ro = rsrc(static_cast<float *>(p.out) + static_cast<size_t>(b) * p.T * p.F,
                                static_cast<size_t>(p.T) * p.F * 4);
-        // rows 2 (wave + 4 k) + half, k = 0 .. 15: two rows per wave per step
+        // rows 2 (wave + 4 k) + half, k = 0 .. 15: two rows per wave per step;
+        // k < 8 in the first half, k >= 8 in the second
         auto row_of = [&](int k) { return 2 * (wave + WV * k) + half; };
         auto off_of = [&](int k, int e) -> uint32_t {
             const int pos = m0 + row_of(k);
             const bool ok = pos >= 1 && pos < p.T && f0 + e < p.F;
             return ok ? 4u * (static_cast<uint32_t>(pos - 1) * p.F + f0 + e) : OOB;
         };
-        auto sum = [&](int k, int e, float old) {
-            const int rw = row_of(k);
-            float v = old + Fk[rw * FS + c0 + e] + __expf(g * static_cast<float>(TM - rw)) * cC[e];
-            if (rw == 0) v += cS[e];
-            return v;
-        };
-        if (p.F % 4 == 0) {
-            // 16-byte aligned runs, wholly in or out of the slots
-            v4f32_t old[TM / (2 * WV)];
+        constexpr int KR = TM / (2 * WV);             // rows per half-wave
+        const bool vec = p.F % 4 == 0;                // 16-byte aligned runs, wholly in or out of the slots
+        v4f32_t old[KR];
+        if (vec) {
 #pragma unroll
-            for (int k = 0; k < TM / (2 * WV); ++k)
+            for (int k = 0; k < KR; ++k)
                 old[k] = __builtin_bit_cast(v4f32_t, __builtin_amdgcn_raw_buffer_load_b128(ro, off_of(k, 0), 0, kNT));
+        }
+        if (threadIdx.x < TN) {
+            sC[threadIdx.x] = carry;   // 0 past the slots: every S read there is 0
+            sS[threadIdx.x] = s_own;
+        }
 #pragma unroll
-            for (int k = 0; k < TM / (2 * WV); ++k) {
-                v4f32_t v;
+        for (int hh = 0; hh < 2; ++hh) {
+            if (wm == hh) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = sum(k, e, old[k][e]);
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(gv4u32_t, v), ro, off_of(k, 0), 0, kNT);
+                for (int j = 0; j < NI; ++j) {
+                    const int n = wn * (TN / 2) + 32 * j + lc;
+                    const int fl = p.nperm ? (n & ~31) + perm32(n & 31) : n;
+#pragma unroll
+                    for (int i = 0; i < MI; ++i)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) Fk[(32 * i + 8 * (r / 4) + 4 * h + r % 4) * FS + fl] = acc[i][j][r];
+                }
             }
-        } else {
+            __syncthreads();
+            if (hh == 0 && threadIdx.x == 0) p.dg_part[logical] = (xr[0] + xr[1]) + (xr[2] + xr[3]);
+            float cC[4], cS[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                cC[e] = sC[c0 + e];
+                cS[e] = sS[c0 + e];
+            }
+            auto sum = [&](int k, int e, float o) {
+                const int rw = row_of(k);
+                float v = o + Fk[(rw - HR * hh) * FS + c0 + e] + __expf(g * static_cast<float>(TM - rw)) * cC[e];
+                if (rw == 0) v += cS[e];
+                return v;
+            };
+            if (vec) {
+#pragma unroll
+                for (int k = KR / 2 * hh; k < KR / 2 * (hh + 1); ++k) {
+                    v4f32_t v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = sum(k, e, old[k][e]);
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(gv4u32_t, v), ro, off_of(k, 0), 0, kNT);
+                }
+            } else {
 #pragma unroll 2
-            for (int k = 0; k < TM / (2 * WV); ++k) {
-                float old[4];
+                for (int k = KR / 2 * hh; k < KR / 2 * (hh + 1); ++k) {
+                    float o4[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    old[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, off_of(k, e), 0, 0));
+                    for (int e = 0; e < 4; ++e)
+                        o4[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, off_of(k, e), 0, 0));
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum(k, e, old[e])), ro, off_of(k, e), 0, 0);
+                    for (int e = 0; e < 4; ++e)
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum(k, e, o4[e])), ro, off_of(k, e), 0, 0);
+                }
             }
+            if (hh == 0) __syncthreads();   // the first half's rows read before the second's overwrite them
         }
     } else {
         // rows = positions, columns = features of a (B, T, F) tensor, written
@@ -959,9 +974,9 @@ constexpr int KT = 2;   // contraction tiles per k-step (32 elements): four 32 K
 template <int G, bool TA, bool TBt, int EPI, int OUT>
 int launch_g(Args a, int B, hipStream_t s) {
     const void *fn = reinterpret_cast<const void *>(&pair_kernel<G, G, KT, TA, TBt, EPI, OUT>);
-    // the dr accumulation stages its 128 x 132 fp32 tile and two slot rows in LDS
-    constexpr int stages = nstage<G, EPI>() * (G / 32 * KT) * 2 * TB;
-    constexpr int lds = OUT == OUT_DRADD && stages < (G * (G + 4) + 2 * G) * 4 ? (G * (G + 4) + 2 * G) * 4 : stages;
+    // the dr accumulation stages half its tile (64 x 132 fp32) and two slot rows in LDS
+    constexpr int stages = nstage<G, EPI, OUT>() * (G / 32 * KT) * 2 * TB;
+    constexpr int lds = OUT == OUT_DRADD && stages < (G / 2 * (G + 4) + 2 * G) * 4 ? (G / 2 * (G + 4) + 2 * G) * 4 : stages;
     static bool attr_done[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return check_launch("hipGetDevice");

@@ -428,7 +428,9 @@ extern "C" int ulm_la_timer_start(int max_launches) {
         hipEvent_t *ev = new hipEvent_t[2 * max_launches];
         for (int i = 0; i < 2 * g_la_timer.cap; ++i) ev[i] = g_la_timer.ev[i];
         for (int i = 2 * g_la_timer.cap; i < 2 * max_launches; ++i)
-            if (hipEventCreate(&ev[i]) != hipSuccess) {
+            // timing only: no system-scope fence, which would write the caches back
+            // and invalidate them between the timed kernels
+            if (hipEventCreateWithFlags(&ev[i], hipEventDisableSystemFence) != hipSuccess) {
                 delete[] ev;
                 return check_launch("hipEventCreate");
             }

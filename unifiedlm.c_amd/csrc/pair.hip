@@ -1070,6 +1070,10 @@ namespace {
 // A second stream per device (default priority) and its fork / join events:
 // the backward's dv product runs on it beside the dscores product, which
 // leaves a quarter of the CUs' workgroup slots free
+// The fork and join order work between two streams of one device: no timing,
+// and no system-scope fence (a cache write-back and invalidate that only the
+// host or another device would need)
+constexpr unsigned kSideEventFlags = hipEventDisableTiming | hipEventDisableSystemFence;
 struct SideStream {
     hipStream_t s = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
@@ -1081,8 +1085,8 @@ int side_stream(SideStream *&out) {
     SideStream &sd = sides[dev];
     if (!sd.s) {
         if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess ||
-            hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
-            hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess)
+            hipEventCreateWithFlags(&sd.fork, kSideEventFlags) != hipSuccess ||
+            hipEventCreateWithFlags(&sd.join, kSideEventFlags) != hipSuccess)
             return check_launch("side stream");
     }
     out = &sd;

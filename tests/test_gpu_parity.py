@@ -133,6 +133,8 @@ PATH_CASES = [
       for path in ("chunked", "pair", "generic")],
     # widths off the 32 grid: the block-pair form on padded tiles, or the generic kernel
     *[(*shape, path) for shape in [(2, 200, 140, 64), (2, 100, 100, 36)] for path in ("pair", "generic")],
+    # B T^2 D >= 2e9: the block-pair backward runs dv on the device's second stream
+    (3, 1024, 128, 768, "pair"),
 ]
 
 

@@ -134,58 +134,13 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__
 }
 
 // The bf16 case of transpose_kernel with X % 64 == 0 and the layouts X wide:
-// grid (ceil(X / 256), NT, B), 256 threads, 64 positions x 256 features per
-// workgroup (fewer, longer workgroups: every load of the workgroup is issued
-// before the first store). The R layout is a re-tiling of the rows, written
-// from registers; the Q layout goes through LDS, where thread (feature pair
-// p, position group g) reads positions 8 g .. 8 g + 7 of features 2 p, 2 p + 1
-// as 8 words and writes two 16-byte Q chunks. The LDS row stride of 36 words
-// puts the two position groups of a wave on disjoint banks.
+// grid (ceil(X / 256), NT, B), 256 threads, one tile_copy_bf16 job (64
+// positions x 256 features) per workgroup.
 __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t *__restrict__ src, uint16_t *__restrict__ raw,
                                                              uint16_t *__restrict__ xr, int T, int X, int NT) {
-    constexpr int NB = 4, RS = 36;   // 64-feature blocks per workgroup; LDS row stride in words
-    __shared__ __align__(16) uint32_t tile[NB][C][RS];
-    const int xw = blockIdx.x * NB * C, n = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, i = tid / 4, c = tid % 4, t = n * C + i;
-    uint4 v[NB][2];
-#pragma unroll
-    for (int k = 0; k < NB; ++k) {
-        const int x0 = xw + k * C;
-        const bool ok = t < T && x0 < X;
-        const uint4 *p = reinterpret_cast<const uint4 *>(src + (static_cast<size_t>(b) * T + (ok ? t : 0)) * X + (ok ? x0 : 0) + 16 * c);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) v[k][h] = ok ? p[h] : make_uint4(0u, 0u, 0u, 0u);
-    }
-#pragma unroll
-    for (int k = 0; k < NB; ++k) {
-        const int x0 = xw + k * C;
-        if (x0 >= X) break;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if (xr) *reinterpret_cast<uint4 *>(xr + r_index(b, t, x0 + 16 * c + 8 * h, NT, X)) = v[k][h];
-            if (raw) *reinterpret_cast<uint4 *>(&tile[k][i][8 * c + 4 * h]) = v[k][h];
-        }
-    }
-    if (!raw) return;
-    __syncthreads();
-    const int fp = tid % 32, g = tid / 32;
-#pragma unroll
-    for (int k = 0; k < NB; ++k) {
-        const int x0 = xw + k * C;
-        if (x0 >= X) break;
-        uint32_t w[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) w[j] = tile[k][8 * g + j][fp];
-        uint32_t e0[4], e1[4];   // features 2 fp and 2 fp + 1, positions in pairs
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            e0[e] = (w[2 * e] & 0xffffu) | (w[2 * e + 1] << 16);
-            e1[e] = (w[2 * e] >> 16) | (w[2 * e + 1] & 0xffff0000u);
-        }
-        const int t0 = n * C + 8 * g;
-        *reinterpret_cast<uint4 *>(raw + q_index(b, t0, x0 + 2 * fp, NT, X)) = make_uint4(e0[0], e0[1], e0[2], e0[3]);
-        *reinterpret_cast<uint4 *>(raw + q_index(b, t0, x0 + 2 * fp + 1, NT, X)) = make_uint4(e1[0], e1[1], e1[2], e1[3]);
-    }
+    __shared__ __align__(16) copy_tile_t tile[kCopyBlocks];
+    tile_copy_bf16(src, raw, xr, T, X, NT, blockIdx.x * kCopyBlocks * C, blockIdx.y, blockIdx.z, threadIdx.x, true,
+                   tile);
 }
 
 __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {

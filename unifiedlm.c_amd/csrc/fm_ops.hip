@@ -72,9 +72,9 @@ int pair_tq(int B, int T);
 size_t pair_p_bytes(int B, int T);
 int pair_dscore_jobs(int B, int T);
 double pair_flops_per_token(int B, int T, int A, int D);
-int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *vQ, const float *g, uint16_t *P,
+int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, uint16_t *vQ, const float *g, uint16_t *P,
                         uint16_t *Pt, uint16_t *Plo, void *out, int out_dt, const float *resid, int B, int T, int A,
-                        int D, hipStream_t s);
+                        int D, hipStream_t s, const uint16_t *v, uint16_t *vR);
 size_t pair_stats_bytes(int B, int T, int A);
 int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t *doQ, const uint16_t *kQ,
                          const uint16_t *qQ, const uint16_t *P, const uint16_t *Pt, const uint16_t *Plo,
@@ -342,11 +342,14 @@ int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const 
         if (state || c_last) return fail(ULM_ERR_INVALID, "prefill state: not on the block-pair path");
         // q, k: R layout for the scores (this pass only), Q layout for the
         // backward's dk_f, dq_f; v: Q layout for the apply, R layout for the
-        // backward's dscores
+        // backward's dscores. bf16 v with D % 64 == 0 is tiled by the scores
+        // launch, on the CUs its tiles leave idle; other v by a launch of its own.
         ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, ws.qR, ws.kR, sv.qQ, sv.kQ, sv.nck, nullptr, B, T, A, s,
                                  qw, qw_dt, pad32(A)));
-        ULM_TRY(launch_chunk_transpose(v, v_dtype, ws.vQ, nullptr, sv.vR, nullptr, B, T, D, s, pad32(D)));
-        return launch_pair_forward(ws.qR, ws.kR, ws.vQ, g, sv.P, sv.Pt, sv.Plo, fast, fast_dtype, resid, B, T, A, D, s);
+        const bool ride = v_dtype == ULM_BF16 && D % 64 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0;
+        if (!ride) ULM_TRY(launch_chunk_transpose(v, v_dtype, ws.vQ, nullptr, sv.vR, nullptr, B, T, D, s, pad32(D)));
+        return launch_pair_forward(ws.qR, ws.kR, ws.vQ, g, sv.P, sv.Pt, sv.Plo, fast, fast_dtype, resid, B, T, A, D, s,
+                                   ride ? static_cast<const uint16_t *>(v) : nullptr, ride ? sv.vR : nullptr);
     }
     if (path == PATH_CHUNKED) {
         // widths off the 32 grid (a prefill only) run on zero-padded tiles; the

@@ -149,6 +149,12 @@ struct Args {
     float *tS, *tK, *tW;     // per (batch row, 128-position tile, slot) statistics, (B, MT, A)
     int drtile;              // OUT_DRADD: the dr accumulation (the carry formed from tS)
     int MT;
+    // EPI_SCORES: bf16 tile copies of a (B, T, cp_X) tensor done by workgroups
+    // past the tile jobs (cp_jobs tile_copy_bf16 jobs, cp_gx per chunk), into
+    // the Q layout (cp_q) and the R layout (cp_r, or null)
+    const uint16_t *cp_src;
+    uint16_t *cp_q, *cp_r;
+    int cp_X, cp_gx, cp_jobs;
 };
 
 // tile job -> (m-tile, n-tile) of one batch row
@@ -203,6 +209,24 @@ __global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI, OU
     constexpr int NSTAGE = nstage<TM, EPI, OUT>();
     static_assert(KT % 2 == 0 && NSTAGE >= 2 && NSTAGE - 2 <= 4, "k-step and stage count");
     extern __shared__ __align__(16) char lds[];
+
+    if constexpr (EPI == EPI_SCORES) {
+        // the tile copies ride on the workgroups past the tile jobs: the
+        // scores' tiles leave CUs idle, and copies need no MFMA. Each group of
+        // 4 waves takes one job with its own part of the stage memory.
+        if (static_cast<int>(blockIdx.x) >= p.jobs) {
+            constexpr int WV = waves_of<TM, EPI>();
+            const int grp = threadIdx.x / 256;
+            const int job = (static_cast<int>(blockIdx.x) - p.jobs) * (WV / 4) + grp;
+            const int per_b = p.cp_gx * p.NT;
+            const bool live = job < p.cp_jobs;
+            const int jj = live ? job : 0;
+            tile_copy_bf16(p.cp_src, p.cp_q, p.cp_r, p.T, p.cp_X, p.NT, (jj % p.cp_gx) * kCopyBlocks * ULM_CHUNK,
+                           (jj % per_b) / p.cp_gx, jj / per_b, threadIdx.x % 256, live,
+                           reinterpret_cast<copy_tile_t *>(lds + grp * kCopyLds));
+            return;
+        }
+    }
 
     const int wave = uniform(threadIdx.x / 64);
     const int lane = threadIdx.x % 64;
@@ -988,9 +1012,16 @@ int launch_g(Args a, int B, hipStream_t s) {
     a.mt = a.mt ? a.mt : 1;
     a.jobs_per_row = a.tri ? a.mt * (a.mt + 1) / 2 : a.mt * a.nt;
     a.jobs = B * a.jobs_per_row;
+    int grid = a.jobs;
+    if constexpr (EPI == EPI_SCORES) {
+        // tile copies: WV / 4 jobs per extra workgroup, each in its own kCopyLds of the stages
+        constexpr int per_wg = waves_of<G, EPI>() / 4;
+        static_assert(per_wg * kCopyLds <= lds, "tile copies fit in the stage memory");
+        if (a.cp_jobs > 0) grid += (a.cp_jobs + per_wg - 1) / per_wg;
+    }
     int st = la_timer_begin(s);
     if (st) return st;
-    pair_kernel<G, G, KT, TA, TBt, EPI, OUT><<<dim3(static_cast<unsigned>(a.jobs)), waves_of<G, EPI>() * 64, lds, s>>>(a);
+    pair_kernel<G, G, KT, TA, TBt, EPI, OUT><<<dim3(static_cast<unsigned>(grid)), waves_of<G, EPI>() * 64, lds, s>>>(a);
     st = check_launch("pair_kernel");
     if (st) return st;
     return la_timer_end(s);
@@ -1096,10 +1127,12 @@ int side_stream(SideStream *&out) {
 
 // P = scores(q, k) in the P layout (Tq x Tq per batch row), its transpose
 // Pt and its bf16 residual Plo (P layout), then out = P v (+ resid) in out_dt
-// (B, T, D). qR, kR: R layout (A); vQ: Q layout (D).
-int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *vQ, const float *g, uint16_t *P,
+// (B, T, D). qR, kR: R layout (A); vQ: Q layout (D). With v (bf16 (B, T, D),
+// D % 64 == 0, 16-byte aligned) the scores launch also writes vQ and vR (the R
+// layout, or null) from it; else vQ is an input.
+int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, uint16_t *vQ, const float *g, uint16_t *P,
                         uint16_t *Pt, uint16_t *Plo, void *out, int out_dt, const float *resid, int B, int T, int A,
-                        int D, hipStream_t s) {
+                        int D, hipStream_t s, const uint16_t *v, uint16_t *vR) {
     using namespace pair;
     const int G = pair_block(B, T), Tq = pair_tq(B, T), NT = (T + 63) / 64;
     const int Ap = (A + 31) / 32 * 32, Dp = (D + 31) / 32 * 32;   // operand tile widths
@@ -1121,6 +1154,17 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, const uint16_t *
     a.pout_lo = Plo;
     a.p_bstride = pm.bstride;
     a.p_rt = pm.rt;
+    if (v) {
+        if (D % 64 || reinterpret_cast<uintptr_t>(v) % 16)
+            return fail(ULM_ERR_INVALID, "pair forward: v tile copies need D %% 64 == 0 and 16-byte rows (D=%d)", D);
+        a.NT = NT;
+        a.cp_src = v;
+        a.cp_q = vQ;
+        a.cp_r = vR;
+        a.cp_X = D;
+        a.cp_gx = (D + kCopyBlocks * ULM_CHUNK - 1) / (kCopyBlocks * ULM_CHUNK);
+        a.cp_jobs = a.cp_gx * NT * B;
+    }
     ULM_TRY((launch<false, EPI_SCORES>(a, Gs, B, s)));
     Args f{};
     f.T = T;

@@ -209,6 +209,72 @@ struct Carver {
     }
 };
 
+// ---- the bf16 tile copies of a (B, T, X) tensor, X % 64 == 0
+//
+// One job: the 64 positions of chunk n x 256 features from xw, on 256 threads
+// (tid), into the Q layout (raw) and the R layout (xr), either null; the
+// layouts are X wide. Every load of the job is issued before its first store.
+// The R layout is a re-tiling of the rows, written from registers; the Q
+// layout goes through tile (4 x 64 x 36 words of LDS), where thread (feature
+// pair fp, position group g) reads positions 8 g .. 8 g + 7 of features 2 fp,
+// 2 fp + 1 as 8 words and writes two 16-byte Q chunks. The row stride of 36
+// words puts the two position groups of a wave on disjoint banks.
+// With raw, the job takes one workgroup barrier (raw is uniform over the
+// workgroup); a job with live false takes it too and touches no memory, so
+// several jobs can share a workgroup.
+constexpr int kCopyBlocks = 4, kCopyStride = 36;
+constexpr uint32_t kCopyLds = kCopyBlocks * ULM_CHUNK * kCopyStride * 4;   // bytes of tile per job
+using copy_tile_t = uint32_t[ULM_CHUNK][kCopyStride];
+
+__device__ __forceinline__ void tile_copy_bf16(const uint16_t *__restrict__ src, uint16_t *__restrict__ raw,
+                                               uint16_t *__restrict__ xr, int T, int X, int NT, int xw, int n,
+                                               int b, int tid, bool live, copy_tile_t *tile) {
+    constexpr int C = ULM_CHUNK, NB = kCopyBlocks;
+    const int i = tid / 4, c = tid % 4, t = n * C + i;
+    uint4 v[NB][2];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+        const int x0 = xw + k * C;
+        const bool ok = live && t < T && x0 < X;
+        const uint4 *p = reinterpret_cast<const uint4 *>(src + (static_cast<size_t>(b) * T + (ok ? t : 0)) * X +
+                                                         (ok ? x0 : 0) + 16 * c);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) v[k][h] = ok ? p[h] : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+        const int x0 = xw + k * C;
+        if (!live || x0 >= X) break;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (xr) *reinterpret_cast<uint4 *>(xr + r_index(b, t, x0 + 16 * c + 8 * h, NT, X)) = v[k][h];
+            if (raw) *reinterpret_cast<uint4 *>(&tile[k][i][8 * c + 4 * h]) = v[k][h];
+        }
+    }
+    if (!raw) return;
+    __syncthreads();
+    if (!live) return;
+    const int fp = tid % 32, g = tid / 32;
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+        const int x0 = xw + k * C;
+        if (x0 >= X) break;
+        uint32_t w[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[j] = tile[k][8 * g + j][fp];
+        uint32_t e0[4], e1[4];   // features 2 fp and 2 fp + 1, positions in pairs
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            e0[e] = (w[2 * e] & 0xffffu) | (w[2 * e + 1] << 16);
+            e1[e] = (w[2 * e] >> 16) | (w[2 * e + 1] & 0xffff0000u);
+        }
+        const int t0 = n * C + 8 * g;
+        *reinterpret_cast<uint4 *>(raw + q_index(b, t0, x0 + 2 * fp, NT, X)) = make_uint4(e0[0], e0[1], e0[2], e0[3]);
+        *reinterpret_cast<uint4 *>(raw + q_index(b, t0, x0 + 2 * fp + 1, NT, X)) =
+            make_uint4(e1[0], e1[1], e1[2], e1[3]);
+    }
+}
+
 }  // namespace ulm
 
 // return a nonzero status from the enclosing function

@@ -1,16 +1,18 @@
-"""The block-pair fast memory at the full 110M benchmark shape (B=16, T=1024,
-A=3072, D=768, v and fast in bf16; needs an MI355X), through a property that
+"""The block-pair fast memory at the full benchmark shapes (110M: B=16,
+T=1024, A=3072, D=768; 42M: B=16, T=1024, A=2048, D=512; 15M: B=32, T=256,
+A=1152, D=288; v and fast in bf16; needs an MI355X), through a property that
 holds at any size: batch rows are independent. Every per-row output and
-gradient of the B=16 call (q, fast, dr, dv) equals, bit for bit, that of a
-B=1 call on the same row: a tile's arithmetic does not depend on which
+gradient of the full-batch call (q, fast, dr, dv) equals, bit for bit, that
+of a B=1 call on the same row: a tile's arithmetic does not depend on which
 workgroup runs it or what runs beside it. dg and dw are sums over the rows;
-they match the sums of the 16 row calls' within fp32 rounding. The B=1 call
-of the same product form and shape is held to the float64 oracle in
+they match the sums of the row calls' within fp32 rounding. The B=1 call of
+the same product form and shape is held to the float64 oracle in
 test_gpu_parity (PATH_CASES).
 
-Only the full shape runs 16 rows of jobs in the XCD-local order, dv on the
-device's second stream (B T^2 D >= 2e9) and the scores' tile copies of v on
-the CUs the 160 score tiles leave idle, so those are what this test adds.
+Only the full shapes run all rows of jobs in the XCD-local order, dv on the
+device's second stream (B T^2 D >= 2e9: the 110M and 42M shapes) and, at the
+110M shape, the scores' tile copies of v on the CUs the 160 score tiles leave
+idle, so those are what this test adds.
 """
 import pytest
 import torch
@@ -23,12 +25,15 @@ import kernel  # noqa: E402
 import ulm_native as nat  # noqa: E402
 
 
-def test_full_shape_rows_match_single_row_calls(monkeypatch):
-    B, T, A, D = 16, 1024, 3072, 768
+SHAPES = [(16, 1024, 3072, 768), (16, 1024, 2048, 512), (32, 256, 1152, 288)]
+
+
+@pytest.mark.parametrize("B,T,A,D", SHAPES)
+def test_full_shape_rows_match_single_row_calls(B, T, A, D, monkeypatch):
     say(f"full-shape row independence: block-pair form, B={B} T={T} A={A} D={D}, v bf16")
     monkeypatch.setenv("ULM_FM_PATH", "pair")
     assert nat.lib().ulm_fm_path(B, T, A, D) == 2
-    r, v, g, w = fm_inputs(B, T, A, D, seed=16, device="cuda")
+    r, v, g, w = fm_inputs(B, T, A, D, seed=B + T + A, device="cuda")
     r, g, w = r.float(), g.float(), w.float()
     v = v.to(torch.bfloat16)
     gen = torch.Generator(device="cuda").manual_seed(16)

@@ -135,9 +135,11 @@ PATH_CASES = [
     *[(*shape, path) for shape in [(2, 200, 140, 64), (2, 100, 100, 36)] for path in ("pair", "generic")],
     # B T^2 D >= 2e9: the block-pair backward runs dv on the device's second stream
     (3, 1024, 128, 768, "pair"),
-    # the 110M shape's row (T=1024, A=3072, D=768): the single-row calls that
-    # test_gpu_fullsize compares the full B=16 call with
+    # one row of the 110M, 42M and 15M benchmark shapes: the single-row calls that
+    # test_gpu_fullsize compares the full-batch calls with
     (1, 1024, 3072, 768, "pair"),
+    (1, 1024, 2048, 512, "pair"),
+    (1, 256, 1152, 288, "pair"),
     # the v tile copies done by the scores launch: an odd number of copy jobs (the
     # last workgroup's second group idle) and a last 256-feature block cut at D
     (1, 190, 96, 576, "pair"),

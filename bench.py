@@ -16,15 +16,24 @@ are resident in HBM before the timed region. Prints one JSON line:
              The events run in a second pass of the same timed steps: an event
              record between two dependent kernels lengthens the gap between
              them, so the pass that gives value carries none.
-             The algorithmic flops are the chunked algorithm's 16AD + 8C(A + D)
-             per token and block (for the pair products, the work they carry
-             out; their own executed flops give executed_tflops); traffic is
-             the HBM bytes per launch recorded under profiles/
+             The algorithmic flops are those of the evaluation that runs: for
+             the six block-pair products 6 (A + D) per causal pair (t, s) of a
+             batch row (mfma_executed_tflops counts their whole 128 x 128 tiles,
+             masked halves of the diagonal ones included); for the chunked
+             products 4 K V + 2 C V per token and product.
+             chunked_equivalent_tflops prices the same work in the chunked
+             algorithm's 16AD + 8C(A + D) flops per token and block (a
+             comparison with the reference's algorithm, not a utilisation);
+             traffic is the HBM bytes per launch recorded under profiles/
   path_tflops / chunked_equivalent_tflops
              the whole step (statistics kernels included) in the chosen
              evaluation's algorithmic flops, and in the chunked form's
              16AD + 8C(A + D) flops per token (the same work priced as the
              reference's algorithm)
+  chunked    the chunked state form (the reference's algorithm, `_la`) on
+             the same 110M shape (forced by ULM_FM_PATH=chunked) and on
+             B=2, T=8192 sequences of the same widths, which the library
+             sends to it by itself; each with its la_kgroup_kernel roofline
   configs    one block of the 15M (B=32, T=256, D=288, A=1152) and 42M (B=16,
              T=1024, D=512, A=2048) shapes, and of the two shapes the reference
              publishes single-block times for (ref-15M: B=32, T=256, D=288,
@@ -40,8 +49,11 @@ are resident in HBM before the timed region. Prints one JSON line:
   decode     batched recurrent decode at the 110M shape: 256 sequences, 12
              blocks, fp32 state (29 GB); the 512-position prompt in one
              chunked pass (UnifiedLM.prefill), then greedy steps; GB/s of the
-             algorithmic bytes per step against 8 TB/s, with the oracle's
-             forward_recurrent on the host cores as its cpu_baseline
+             algorithmic bytes per step against 8 TB/s. Its cpu_baseline is
+             the reference's own C decoder (run.c, built with its runomp
+             flags by oracle/Makefile) on the host cores, one sequence, in the
+             same algorithmic bytes per position; the oracle's
+             forward_recurrent is reported beside it
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--decode-steps N]
 """
@@ -84,6 +96,7 @@ def parse():
     p.add_argument("--no-block", action="store_true")
     p.add_argument("--no-step", action="store_true")
     p.add_argument("--no-configs", action="store_true")
+    p.add_argument("--no-chunked", action="store_true")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                    help="first run one plain fp32 copy kernel over MB megabytes (a known-size reference for "
                         "hardware byte counters)")
@@ -145,48 +158,83 @@ def bench_training(torch, args, shape=None, steps=None, warmup=None):
         t3 = time.perf_counter()
     ms_step_events = (t3 - t2) * 1e3 / steps
     launch_ms = timer.total_ms / max(timer.launches, 1)
-    executed = None
     if path == "pair":
         kname = "pair_kernel"
-        # the work of all timed launches priced in the algorithm's flops per token
-        # and block, 16AD + 8C(A + D) (the four chunked products); the six
-        # block-pair products carry that work out with fewer flops of their own
-        flops_launches = workloads.chunked_flops_per_token(A, D) * B * T * L * steps
-        executed = workloads.pair_flops(B, T, A, D) * L * steps
+        # the six block-pair products' own algorithmic flops, 6 (A + D) per
+        # causal pair (t, s), over their summed launch time
+        flops_launches = workloads.pair_flops(B, T, A, D) * L * steps
+        tile_flops = workloads.pair_tile_flops(B, T, A, D) * L * steps
         flops_step = workloads.pair_flops(B, T, A, D) * L
-        note = ("the six block-pair products (scores, apply, dscores, dq_f with the backward statistics, "
-                "dk_f into dr, dv) of every block; achieved prices their work in the chunked algorithm's "
-                "16 A D + 8 C (A + D) flops per token and block; executed_tflops counts their own flops, "
-                "6 (A + D) per causal pair (t, s) (whole diagonal tiles execute "
-                f"{workloads.pair_tile_flops(B, T, A, D) / workloads.pair_flops(B, T, A, D):.3f}x that)")
+        note = ("the six block-pair products (scores, apply, dscores, dq_f with the backward statistics, dk_f into dr, "
+                "dv) of every block, 6 (A + D) flops per causal pair (t, s); mfma_executed_tflops counts their whole "
+                "128 x 128 tiles (the diagonal ones computed in full and masked), "
+                f"{workloads.pair_tile_flops(B, T, A, D) / workloads.pair_flops(B, T, A, D):.3f}x that")
     else:
         kname = "la_kgroup_kernel"
         # fwd and dv contract keys A into values D, dq and dk keys D into values A
         flops_launches = (workloads.la_kernel_flops(B, T, A, D) + workloads.la_kernel_flops(B, T, D, A)) / 2 * timer.launches
+        tile_flops = None
         flops_step = 4 * workloads.la_flops(B, T, A, D) * L
         note = "the four chunked products of every block, 4 K V + 2 C V per token and product"
-    achieved = flops_launches / (timer.total_ms * 1e-3) / 1e12 if timer.total_ms > 0 else 0.0
-    executed_tflops = executed / (timer.total_ms * 1e-3) / 1e12 if executed and timer.total_ms > 0 else None
+    secs = timer.total_ms * 1e-3
+    achieved = flops_launches / secs / 1e12 if secs > 0 else 0.0
+    # the same launches' work priced in the chunked algorithm's 16AD + 8C(A + D) per token and block
+    chunked_eq_launch = (workloads.chunked_flops_per_token(A, D) * B * T * L * steps / secs / 1e12
+                         if secs > 0 and path == "pair" else None)
     traffic = None
     tfile = TRAFFIC_FILES.get(kname)
     if tfile and os.path.exists(tfile) and shape == "110M":
         with open(tfile) as f:
-            traffic = json.load(f).get("bytes_per_launch")
+            rec = json.load(f)
+        if rec.get("path", path) == path:
+            traffic = rec.get("bytes_per_launch")
     path_tflops = flops_step / (ms_step * 1e-3) / 1e12
     chunk_eq = workloads.chunked_flops_per_token(A, D) * L * B * T / (ms_step * 1e-3) / 1e12
     log(f"step {ms_step:.2f} ms ({ms_step_events:.2f} ms with the launch events), {kname} {launch_ms:.3f} ms x "
         f"{timer.launches} launches, {achieved:.1f} TFLOP/s")
+    roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+            "traffic_source": "recorded (profiles/)" if traffic else None, "kernel": kname, "flops": note,
+            "avg_launch_ms": round(launch_ms, 4), "launches_timed": timer.launches,
+            "launch_events": "a second pass of the timed steps with a HIP event pair around every product launch on "
+                             f"its stream ({ms_step_events:.3f} ms per step with them)"}
+    if tile_flops and secs > 0:
+        roof["mfma_executed_tflops"] = round(tile_flops / secs / 1e12, 2)
+        roof["mfma_executed_frac"] = round(tile_flops / secs / 1e12 / PEAK_BF16_TFLOPS, 4)
+    if chunked_eq_launch:
+        roof["chunked_equivalent_tflops"] = round(chunked_eq_launch, 2)
+        roof["chunked_equivalent_frac"] = round(chunked_eq_launch / PEAK_BF16_TFLOPS, 4)
     return dict(B=B, T=T, D=D, A=A, L=L, path=path, ms_step=ms_step, value=B * T / (ms_step * 1e-3) / 1e6,
-                roofline={"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-                          "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
-                          "traffic_source": "recorded (profiles/)" if traffic else None,
-                          "kernel": kname, "flops": note,
-                          "avg_launch_ms": round(launch_ms, 4), "launches_timed": timer.launches,
-                          "launch_events": "a second pass of the timed steps with a HIP event pair around every "
-                                           f"product launch on its stream ({ms_step_events:.3f} ms per step with them)",
-                          **({"executed_tflops": round(executed_tflops, 2),
-                              "executed_frac": round(executed_tflops / PEAK_BF16_TFLOPS, 4)} if executed_tflops else {})},
-                path_tflops=path_tflops, chunked_equivalent_tflops=chunk_eq)
+                roofline=roof, path_tflops=path_tflops, chunked_equivalent_tflops=chunk_eq)
+
+
+def bench_chunked(torch, args):
+    """The chunked state form (`_la`, kernel.py:183-196; the K-group kernel) at
+    the 110M widths: the training shape with the form forced, and sequences of
+    8192 positions (B=2, the same 16384 tokens per step), which the library
+    sends to it by itself."""
+    out = {}
+    saved = os.environ.get("ULM_FM_PATH")
+    try:
+        os.environ["ULM_FM_PATH"] = "chunked"
+        t = bench_training(torch, args, shape="110M", steps=max(args.steps // 2, 5), warmup=2)
+    finally:
+        if saved is None:
+            os.environ.pop("ULM_FM_PATH", None)
+        else:
+            os.environ["ULM_FM_PATH"] = saved
+    legs = [("110M (forced)", t)]
+    if saved is None:
+        legs.append(("110M-T8192", bench_training(torch, args, shape="110M-T8192", steps=max(args.steps // 2, 5),
+                                                  warmup=2)))
+    for name, t in legs:
+        out[name] = {"workload": f"fast-memory fwd+bwd, {t['L']} blocks, B={t['B']} T={t['T']} D={t['D']} "
+                                 f"A={t['A']}, chunked state form",
+                     "path": t["path"], "ms_per_step": round(t["ms_step"], 3), "Mtok_per_s": round(t["value"], 4),
+                     "tflops": round(t["path_tflops"], 2),
+                     "frac_bf16_peak": round(t["path_tflops"] / PEAK_BF16_TFLOPS, 4),
+                     "roofline": t["roofline"]}
+    return out
 
 
 def bench_configs(torch, args):
@@ -396,7 +444,10 @@ def bench_decode(torch, args):
     if os.path.exists(tfile) and N == 256:
         with open(tfile) as f:
             traffic = json.load(f).get("bytes_per_launch")
-    cpu = None if args.no_cpu else bench_decode_cpu(torch, model, c)
+    cpu = cpu_port = None
+    if not args.no_cpu:
+        cpu_port = bench_decode_cpu(torch, model, c)
+        cpu = bench_decode_runc(torch, model, c)
     return {"metric": "decode GB/s", "value": round(gbps, 1), "unit": "GB/s", "ms_per_step": round(step_ms, 3),
             "tok_per_s": round(N / (step_ms * 1e-3), 1),
             "prefill": "chunked (UnifiedLM.prefill, fused blocks, GEMMs bf16 under autocast)",
@@ -407,7 +458,8 @@ def bench_decode(torch, args):
                          "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": traffic,
                          "traffic_kernel": "decode_state_kernel (S read + write and read-out, per block-step)",
                          "traffic_source": "recorded (profiles/)" if traffic else None},
-            "cpu_baseline": cpu,
+            "cpu_baseline": cpu or cpu_port,
+            "cpu_baseline_port": cpu_port if cpu else None,
             "config": {"N": N, "D": D, "A": A, "blocks": L, "vocab": V, "prefill": args.prefill,
                        "steps": args.decode_steps}}
 
@@ -439,6 +491,45 @@ def bench_decode_cpu(torch, model, c, n_seq=8, n_pos=12):
                       f"prior state ({dt:.2f} s), algorithmic bytes per position at N={n_seq}"}
 
 
+def bench_decode_runc(torch, model, c, n_pos=2048):
+    """The reference's own C decoder (run.c:193-265, built unmodified from its
+    source with its runomp flags by oracle/Makefile) on the host cores: the
+    110M decode model exported to its ULMe v1 format, one sequence, n_pos
+    positions from the prior state after 2 of warm-up, in GB/s of the
+    algorithmic bytes per decode position at N=1. None where that build is
+    absent."""
+    import tempfile
+    from oracle import runc
+    import ulme
+    import workloads
+    if not runc.available(omp=True):
+        log("decode cpu baseline: oracle/_ref/librunc_ref_omp.so not built, skipped")
+        return None
+    threads = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+    gen = torch.Generator().manual_seed(12)
+    tokens = torch.randint(0, c["vocab"], (n_pos + 2,), generator=gen).tolist()
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "decode_110M.bin")
+        ulme.export_ulme(model, path)
+        ref = runc.RuncReference(path, omp=True)
+    ref.reset()
+    for tok in tokens[:2]:
+        ref.forward(tok)
+    t0 = time.perf_counter()
+    for tok in tokens[2:]:
+        ref.forward(tok)
+    dt = time.perf_counter() - t0
+    step_s = dt / n_pos
+    bytes_step = workloads.decode_bytes_per_step(1, c["blocks"], c["A"], c["D"], c["vocab"])
+    log(f"decode cpu baseline (run.c, OpenMP): {step_s * 1e3:.1f} ms per position, {threads} threads")
+    return {"value": round(bytes_step / step_s / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "reference",
+            "tok_per_s": round(1 / step_s, 2),
+            "sample": f"run.c forward() (built with -Ofast -fopenmp, its runomp target) on the 110M decode model "
+                      f"exported to ULMe v1 (D={c['D']}, A={c['A']}, {c['blocks']} blocks, vocab {c['vocab']}), one "
+                      f"sequence x {n_pos} positions from the prior state after 2 of warm-up ({dt:.2f} s), "
+                      "algorithmic bytes per position at N=1"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -460,6 +551,7 @@ def main():
         del x, y
     train = bench_training(torch, args)
     configs = None if args.no_configs else bench_configs(torch, args)
+    chunked = None if args.no_chunked else bench_chunked(torch, args)
     cpu = None if args.no_cpu else bench_cpu_baseline(torch, train)
     block = None if args.no_block else bench_block(torch, args)
     train_step = None if args.no_step else bench_train_step(torch, args)
@@ -479,7 +571,9 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"fast-memory fwd+bwd, {train['L']} blocks of the {args.shape} shape",
                    "global_batch": train["B"], "seq_len": train["T"], "dim": train["D"], "slots": train["A"],
-                   "blocks": train["L"], "chunk": 64, "parallelism": "single GPU"},
+                   "blocks": train["L"],
+                   **({"position_block": 128} if train["path"] == "pair" else {"chunk": 64}),
+                   "parallelism": "single GPU"},
         "products": train["path"],
         "path_tflops": round(train["path_tflops"], 2),
         "path_frac_bf16_peak": round(train["path_tflops"] / PEAK_BF16_TFLOPS, 4),
@@ -487,6 +581,7 @@ def main():
         "chunked_equivalent_frac_bf16_peak": round(train["chunked_equivalent_tflops"] / PEAK_BF16_TFLOPS, 4),
         "roofline": train["roofline"],
         "configs": configs,
+        "chunked": chunked,
         "cpu_baseline": cpu,
         "block": block,
         "train_step": train_step,

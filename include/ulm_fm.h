@@ -50,10 +50,13 @@ const char *ulm_last_error(void);
  * sums over pairs of 128-position blocks, six tile GEMMs; T <= 4096, any A and
  * D on zero-padded tiles), whichever needs fewer flops where both apply: about
  * 4 A D per token and product for the first, T (A + D) / 2 for the second;
- * 0 the generic kernel (widths off the 32 grid past 4096 positions). The
+ * 0 the generic kernel (widths off the 32 grid past 2048 positions where the
+ * pair form would need more than twice the state form's flops, or past 4096
+ * positions). The
  * environment variable ULM_FM_PATH=chunked, =pair or =generic forces one of
- * them where it applies; it must not change between a forward and its
- * backward. -1 for invalid sizes. No counterpart in the reference (one
+ * them where it applies. The choice is made when the saved buffer is sized
+ * (ulm_fm_saved_bytes) and travels with it: a forward and its backward always
+ * use one form. -1 for invalid sizes. No counterpart in the reference (one
  * algorithm, kernel.py:183-196). */
 int ulm_fm_path(int B, int T, int A, int D);
 
@@ -77,8 +80,18 @@ int ulm_fm_path(int B, int T, int A, int D);
  *          ulm_fm_path chooses, the bf16 scores P (with their transpose and
  *          bf16 residual) of the block-pair form or the dv product's score
  *          tiles of the chunked form). Opaque; pass it unchanged to ulm_fm_bwd.
+ *          saved_bytes must be exactly the value ulm_fm_saved_bytes returned:
+ *          that size names the form (ulm_fm_path at the time of the call)
+ *          that the forward evaluates and the backward reads the buffer in.
+ *          A size that names no form at this shape is rejected
+ *          (ULM_ERR_INVALID).
  */
 size_t ulm_fm_saved_bytes(int B, int T, int A, int D, int v_dtype);
+
+/* The form (as ulm_fm_path numbers them) a saved buffer of saved_bytes bytes
+ * holds at this shape and v_dtype, or -1 if no form has that size. No
+ * counterpart in the reference. */
+int ulm_fm_saved_path(size_t saved_bytes, int B, int T, int A, int D, int v_dtype);
 size_t ulm_fm_fwd_workspace_bytes(int B, int T, int A, int D, int fast_dtype);
 int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const float *g, const float *w,
                float *q, void *fast, int fast_dtype, void *saved, size_t saved_bytes,
@@ -117,8 +130,12 @@ int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const float *g, c
  *   dg      (1,)    fp32  out    d loss / d g
  *   dw      (A,)    fp32  out
  * Every output is reduced in a fixed order (no atomics): repeated calls agree
- * bit for bit. */
-size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D, int dfast_dtype);
+ * bit for bit. The workspace is ulm_fm_bwd_workspace_bytes(..., saved_bytes,
+ * v_dtype) bytes: the need of the form the saved buffer holds (saved_bytes = 0:
+ * of the form ulm_fm_path picks now; 0 is returned for a size that names no
+ * form). */
+size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D, int dfast_dtype, size_t saved_bytes,
+                                  int v_dtype);
 int ulm_fm_bwd(const float *r, const float *g, const float *w,
                const void *saved, size_t saved_bytes, int v_dtype,
                const void *dfast, int dfast_dtype, const float *dq_out,
@@ -230,7 +247,8 @@ int ulm_block_fm_fwd(const void *pre, int pre_dtype, const float *bias, const fl
 /* ulm_fm_bwd inside the block: r given by the address inputs as for
  * ulm_block_fm_fwd; dqw (B,T,A) dqw_dtype is d loss / d(w q), the q gradient
  * is w dqw and dw also gets sum_t q dqw. Workspace of
- * ulm_fm_bwd_workspace_bytes() bytes; other arguments as for ulm_fm_bwd. */
+ * ulm_fm_bwd_workspace_bytes(..., saved_bytes, v_dtype) bytes; other
+ * arguments as for ulm_fm_bwd. */
 int ulm_block_fm_bwd(const void *pre, int pre_dtype, const float *bias, const float *denom,
                      const float *g, const float *w, const void *saved, size_t saved_bytes,
                      int v_dtype, const void *dfast, int dfast_dtype, const void *dqw, int dqw_dtype,

@@ -30,6 +30,9 @@ How each function is pinned (tests/test_oracle.py):
   dg_bf16_floor         with rounding off equals autograd's dg (the identity
                         with the kernel's tau); rounding its operands to bf16
                         is the only difference.
+  pair_form_grads       with no roundings equals float64 autograd of the dense
+                        form (every output and gradient); each rounding moves
+                        only the outputs that read its operand.
   block_forward         autocast=False is the reference block; with autocast=True
                         its forward and its scalar/bias gradients match torch's
                         CPU bf16 autocast of the block's products (30x closer
@@ -308,6 +311,87 @@ def lm_forward(p, tokens, targets=None, norm_eps=1e-5, form="chunked", chunk=64,
     if targets is not None:
         loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), targets.reshape(-1), ignore_index=-1)
     return logits, loss
+
+
+# ---------------------------------------------------------------------------
+# the block-pair evaluation's bf16 roundings, in otherwise exact arithmetic
+
+PAIR_ROUNDINGS = frozenset({"qk", "P", "v", "dfast", "dS", "qk_bwd"})
+
+
+def _rb(x, on):
+    return x.to(torch.bfloat16).to(x.dtype) if on else x
+
+
+def pair_form_grads(r, v, g, w, dq_out, dfast, roundings=PAIR_ROUNDINGS):
+    """(q, fast, dr, dv, dg, dw) of <q, dq_out> + <fast, dfast> as the block-pair
+    products evaluate them, each operand the products read in bf16 rounded to
+    bf16 (the ones named in ``roundings``) and every other step exact:
+
+      "qk"      q and k in the scores P = lam^(t-s) (q_t . k_s)
+      "P"       P in the apply and dv products; the decay gradient's pair sum
+                weights with P + bf16(P - bf16(P)) (16 significant bits)
+      "v"       v in the apply and dscores products
+      "dfast"   dfast in the dscores and dv products
+      "dS"      dS = lam^(t-s) (dfast_t . v_s) in the dq_f and dk_f products
+      "qk_bwd"  k and q in the dq_f and dk_f products
+
+    The gradients are the closed forms of the definition (kernel.py:139-180,
+    summed directly over pairs for the decay): dq_f = dS k, dk_f = dS^T q,
+    dv = P^T dfast, dc = -dq q / c, dk_c = M^T dc, dr_t = dq_t / c_t +
+    (dk_f + dk_c)_{t+1}, dw = sum dc, dg = sum (t-s) P[t][s] (dfast_t . v_s) +
+    sum dc (sum_s (t-s) lam^(t-s) k_s). With no roundings they equal float64
+    autograd of dense_fast_memory (tests/test_oracle.py)."""
+    r, v, g, w, dfast = (x.detach().double() for x in (r, v, g, w, dfast))
+    R = set(roundings)
+    lam = torch.exp(g)
+    T = r.shape[1]
+    k = shift_keys(r)
+    M = decay_mask(T, lam).to(r.device)
+    t = torch.arange(T, dtype=torch.float64, device=r.device)
+    lagM = (t[:, None] - t[None, :]).clamp(min=0) * M
+    c = w + M @ k
+    q = r / c
+    P = (_rb(q, "qk" in R) @ _rb(k, "qk" in R).transpose(1, 2)) * M
+    P_hi = _rb(P, "P" in R)
+    P_dg = P_hi + _rb(P - P_hi, "P" in R) if "P" in R else P
+    V, DO = _rb(v, "v" in R), _rb(dfast, "dfast" in R)
+    fast = P_hi @ V
+    dots = DO @ V.transpose(1, 2)                    # dfast_t . v_s
+    dS = _rb(dots * M, "dS" in R)
+    dq_f = dS @ _rb(k, "qk_bwd" in R)
+    dk_f = dS.transpose(1, 2) @ _rb(q, "qk_bwd" in R)
+    dv = P_hi.transpose(1, 2) @ DO
+    dq = dq_f + (dq_out.detach().double() if dq_out is not None else 0.0)
+    dc = -dq * q / c
+    dk = dk_f + M.transpose(0, 1) @ dc
+    dr = dq / c
+    dr[:, :-1] += dk[:, 1:]
+    dg = ((t[:, None] - t[None, :]) * P_dg * dots).sum() + (dc * (lagM @ k)).sum()
+    return q, fast, dr, dv, dg, dc.sum((0, 1))
+
+
+class _PairForm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, r, v, g, w, roundings):
+        ctx.save_for_backward(r, v, g, w)
+        ctx.roundings = roundings
+        q, fast = pair_form_grads(r, v, g, w, None, torch.zeros_like(v), roundings)[:2]
+        return q.to(r.dtype), fast.to(r.dtype)
+
+    @staticmethod
+    def backward(ctx, dq, dfast):
+        r, v, g, w = ctx.saved_tensors
+        if dfast is None:
+            dfast = torch.zeros_like(v)
+        _, _, dr, dv, dg, dw = pair_form_grads(r, v, g, w, dq, dfast, ctx.roundings)
+        return dr.to(r.dtype), dv.to(v.dtype), dg.to(g.dtype).reshape(g.shape), dw.to(w.dtype), None
+
+
+def pair_form(r, v, g, w, roundings=PAIR_ROUNDINGS):
+    """unified_memory(r, v, g, w) -> (q, fast) as the block-pair products
+    evaluate it (pair_form_grads), differentiable in r, v, g, w."""
+    return _PairForm.apply(r, v, g, w, frozenset(roundings))
 
 
 # ---------------------------------------------------------------------------

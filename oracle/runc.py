@@ -13,6 +13,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "_ref", "librunc_ref.so")
+LIB_OMP = os.path.join(HERE, "_ref", "librunc_ref_omp.so")   # the reference's runomp flags
 REFERENCE = "/root/reference"
 
 
@@ -22,15 +23,16 @@ def build():
         subprocess.run(["make", "-s", "-C", HERE, f"REF={REFERENCE}"], check=True)
 
 
-def available():
-    return os.path.exists(LIB)
+def available(omp=False):
+    return os.path.exists(LIB_OMP if omp else LIB)
 
 
 class RuncReference:
-    """The reference decoder: load(path), reset(), forward(token) -> logits."""
+    """The reference decoder: load(path), reset(), forward(token) -> logits.
+    omp=True loads the OpenMP build (its threads from OMP_NUM_THREADS)."""
 
-    def __init__(self, checkpoint):
-        self._lib = ctypes.CDLL(LIB)
+    def __init__(self, checkpoint, omp=False):
+        self._lib = ctypes.CDLL(LIB_OMP if omp else LIB)
         self._lib.runc_ref_load.argtypes = [ctypes.c_char_p]
         self._lib.runc_ref_forward.argtypes = [ctypes.c_int]
         self._lib.runc_ref_forward.restype = ctypes.POINTER(ctypes.c_float)

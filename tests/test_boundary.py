@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert sorted(nat.SIGNATURES) == declared
-    assert lib.ulm_abi_version() == 2
+    assert lib.ulm_abi_version() == 3
 
 
 def test_c_side_rejects_bad_sizes_without_touching_the_gpu():
@@ -52,8 +52,13 @@ def test_workspace_sizes(monkeypatch):
     # at the 110M shape the block-pair form needs fewer flops than the chunked state form
     assert lib.ulm_fm_path(B, T, A, D) == 2
     assert lib.ulm_fm_path(B, 8192, A, D) == 1            # past 4096 positions: the state form
-    assert lib.ulm_fm_path(2, 70, 12, 8) == 2             # widths off the 32 grid: padded pair tiles
+    assert lib.ulm_fm_path(2, 200, 140, 64) == 2          # widths off the 32 grid: padded pair tiles
     assert lib.ulm_fm_path(2, 5000, 12, 8) == 0           # ... past 4096 positions: the generic kernel
+    # ... and where the pair form would need more than twice the state form's
+    # flops: at the reference's 15M widths from about 2400 positions on
+    assert lib.ulm_fm_path(32, 2048, 712, 288) == 2
+    assert lib.ulm_fm_path(32, 2560, 712, 288) == 0
+    assert lib.ulm_fm_path(32, 4096, 712, 288) == 0
     # pair form, saved: bf16 q, k (Q layout), v (R layout), the scores P, their
     # transpose and their bf16 residual (Tq x Tq per row), n checkpoints
     Tq = (T + 127) // 128 * 128
@@ -64,23 +69,23 @@ def test_workspace_sizes(monkeypatch):
     # forward: q, k in the R layout for the scores, v in the Q layout for the apply
     nfw = lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_F32)
     assert nfw == 2 * B * NT * 64 * A * 2 + B * NT * 64 * D * 2
-    nbw = lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32)
+    nbw = lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32, 0, 0)
     assert B * T * 4 * D + 2 * B * Tq * Tq * 2 <= nbw < B * T * 4 * D + 2 * B * Tq * Tq * 2 + B * T * 4 * A
-    assert (lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32)
-            == lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16))
+    assert (lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32, 0, 0)
+            == lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16, 0, 0))
     monkeypatch.setenv("ULM_FM_PATH", "chunked")
     assert lib.ulm_fm_path(B, T, A, D) == 1
     # 4 key groups of 768 slots: fp32 partial outputs, plus the forward score tiles
     assert lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_F32) >= 4 * B * T * D * 4 + B * NT * 64 * 64 * 2
     assert lib.ulm_fm_fwd_workspace_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * D * 4
-    assert lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * (2 * A * 4 + D * 4)
+    assert lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16, 0, 0) >= B * T * (2 * A * 4 + D * 4)
     # an fp32 dfast adds the bf16 remainder tiles of its two tiled copies
-    assert (lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32)
-            - lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16)) == 2 * B * T * D * 2
+    assert (lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_F32, 0, 0)
+            - lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16, 0, 0)) == 2 * B * T * D * 2
     # saved: bf16 q, k in both tiled layouts, two v copies, n checkpoints
     assert lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_BF16) >= B * T * (8 * A + 4 * D) + B * NT * A * 4
     assert (lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_F32)
-            - lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_BF16)) == 2 * B * T * D * 2
+            - lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_BF16)) == 2 * B * T * D * 2   # both multiples of 4 KB
     # the generic kernel keeps natural bf16 copies of q, k, v and the checkpoints
     assert lib.ulm_fm_saved_bytes(2, 5000, 12, 8, nat.ULM_F32) >= 2 * 5000 * (12 * 4 + 8 * 2) + 2 * 79 * 12 * 4
     # its bare product needs partial planes only past one 128-key tile
@@ -88,7 +93,52 @@ def test_workspace_sizes(monkeypatch):
     assert lib.ulm_la_workspace_bytes(2, 70, 300, 8) == 3 * 2 * 70 * 8 * 4
     assert lib.ulm_la_workspace_bytes(B, T, A, D) >= 3 * B * NT * A * 64 * 2 + 4 * B * T * D * 4
     assert lib.ulm_addr_bwd_workspace_bytes(B * T, A) >= A * 4
-    assert lib.ulm_fm_bwd_workspace_bytes(0, T, A, D, nat.ULM_F32) == 0
+    assert lib.ulm_fm_bwd_workspace_bytes(0, T, A, D, nat.ULM_F32, 0, 0) == 0
+
+
+def test_saved_buffer_names_its_form(monkeypatch):
+    """The saved buffer's size records the form that filled it: ulm_fm_bwd and
+    its workspace sizer follow that form whatever ULM_FM_PATH says later, and a
+    size that names no form is rejected before any HIP call."""
+    lib = nat.lib()
+    B, T, A, D = 16, 1024, 3072, 768
+    sizes = {}
+    for name, code in (("pair", 2), ("chunked", 1), ("generic", 0)):
+        monkeypatch.setenv("ULM_FM_PATH", name)
+        n = lib.ulm_fm_saved_bytes(B, T, A, D, nat.ULM_BF16)
+        assert lib.ulm_fm_saved_path(n, B, T, A, D, nat.ULM_BF16) == code
+        # the size also pins the shape and the dtype of v
+        assert lib.ulm_fm_saved_path(n, B, T + 64, A, D, nat.ULM_BF16) == -1
+        assert lib.ulm_fm_saved_path(n, B, T, A, D, nat.ULM_F32) in (-1, code) and n % 4096 == 256 * (code + 1)
+        assert lib.ulm_fm_saved_path(n + 4096, B, T, A, D, nat.ULM_BF16) == -1
+        sizes[name] = (n, lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16, 0, 0))
+    assert len({n for n, _ in sizes.values()}) == 3
+    # under another setting, the workspace sizer still answers for the saved form
+    monkeypatch.setenv("ULM_FM_PATH", "pair")
+    for name, (n, ws) in sizes.items():
+        assert lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16, n, nat.ULM_BF16) == ws, name
+    assert lib.ulm_fm_bwd_workspace_bytes(B, T, A, D, nat.ULM_BF16, 12345, nat.ULM_BF16) == 0
+    # a form the shape does not allow: the chunked form needs A, D multiples of 32
+    monkeypatch.setenv("ULM_FM_PATH", "chunked")
+    n_unaligned = lib.ulm_fm_saved_bytes(2, 200, 140, 64, nat.ULM_BF16)
+    assert lib.ulm_fm_saved_path(n_unaligned, 2, 200, 140, 64, nat.ULM_BF16) == 2
+    # the entry points reject a saved size that names no form, or a workspace
+    # sized for another form, before touching the GPU
+    x = ctypes.c_void_p(256)
+    n_pair, ws_pair = sizes["pair"]
+    n_chunked, ws_chunked = sizes["chunked"]
+    assert ws_chunked > ws_pair
+    st = lib.ulm_fm_bwd(x, x, x, x, n_pair + 1, nat.ULM_BF16, x, nat.ULM_BF16, None, x, x, nat.ULM_BF16, x, x, x,
+                        1 << 40, B, T, A, D, None)
+    assert st == nat.ULM_ERR_INVALID and b"names no form" in lib.ulm_last_error()
+    st = lib.ulm_fm_bwd(x, x, x, x, n_chunked, nat.ULM_BF16, x, nat.ULM_BF16, None, x, x, nat.ULM_BF16, x, x, x,
+                        ws_pair, B, T, A, D, None)
+    assert st == nat.ULM_ERR_INVALID and b"workspace" in lib.ulm_last_error()
+    st = lib.ulm_fm_fwd(x, x, nat.ULM_BF16, x, x, x, x, nat.ULM_BF16, x, n_pair - 256, x, 1 << 40, B, T, A, D, None)
+    assert st == nat.ULM_ERR_INVALID and b"names no form" in lib.ulm_last_error()
+    st = lib.ulm_block_fm_bwd(x, nat.ULM_BF16, None, x, x, x, x, n_pair + 4096, nat.ULM_BF16, x, nat.ULM_BF16, x,
+                              nat.ULM_BF16, x, x, nat.ULM_BF16, x, x, x, 1 << 40, B, T, A, D, None)
+    assert st == nat.ULM_ERR_INVALID and b"names no form" in lib.ulm_last_error()
 
 
 def _fm_args(B=2, T=70, A=12, D=8, dtype=torch.float32):
@@ -146,8 +196,41 @@ def test_model_parameters_match_reference_layout():
                                                "key.weight", "key.bias", "mu.weight", "val.weight")]
     expect += ["norm.weight"]
     assert names == expect
+    # the state dict lists the same tensors in the same order (the tied output matrix last)
+    assert list(m.state_dict()) == expect + ["output.weight"]
+    # registration order inside a block (model.py:59-68): norm, conv, key, mu,
+    # log_eps, val, log_rate, log_w, dropout
+    blk = m.layers[0]
+    assert list(blk._modules) == ["norm", "conv", "key", "mu", "val", "dropout"]
+    assert list(blk._parameters) == ["log_eps", "log_rate", "log_w"]
     assert m.output.weight is m.tok_embeddings.weight
     assert torch.all(m.layers[0].val.weight == 0) and torch.all(m.layers[0].conv.weight[:, 0, -1] == 1)
+
+
+def test_training_helpers_of_the_reference_interface():
+    """configure_optimizers and estimate_mfu, called as train.py:172 and :295 call them."""
+    from model import ModelArgs, UnifiedLM
+    args = ModelArgs(dim=16, n_layers=2, hidden_dim=24, vocab_size=50, max_seq_len=32)
+    m = UnifiedLM(args)
+    opt = m.configure_optimizers(0.1, 3e-4, (0.9, 0.95), "cpu")
+    assert isinstance(opt, torch.optim.AdamW)
+    decay, nodecay = opt.param_groups
+    assert decay["weight_decay"] == 0.1 and nodecay["weight_decay"] == 0.0
+    assert opt.defaults["lr"] == 3e-4 and opt.defaults["betas"] == (0.9, 0.95)
+    named = dict(m.named_parameters())
+    ids = lambda group: [id(p) for p in group["params"]]
+    # matrices decay (the tied embedding once), vectors and scalars do not, in parameters() order
+    assert ids(decay) == [id(p) for n, p in named.items() if p.dim() >= 2]
+    assert ids(nodecay) == [id(p) for n, p in named.items() if p.dim() < 2]
+    assert {n for n, p in named.items() if p.dim() < 2} == {
+        f"layers.{i}.{n}" for i in range(2) for n in ("log_eps", "log_rate", "log_w", "norm.weight", "key.bias")
+    } | {"norm.weight"}
+    # the MFU of an iteration that runs at exactly the peak rate is 1
+    n_params = sum(p.numel() for p in m.parameters())
+    mixing = min(64, 32) * (2 * 24 + 16) + 2 * 24 * 16
+    flops = (6 * n_params + 6 * 2 * mixing) * 32 * 8
+    assert abs(m.estimate_mfu(8, flops / 2516.6e12) - 1.0) < 1e-12
+    assert abs(m.estimate_mfu(8, flops / 312e12, peak_flops=312e12) - 1.0) < 1e-12
 
 
 def test_block_entry_points_reject_bad_arguments_without_touching_the_gpu():

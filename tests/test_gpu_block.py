@@ -129,9 +129,7 @@ BLOCK_CASES = [
     (2, 130, 100, 1600, False),
     (2, 130, 100, 1600, True),
     (2, 256, 288, 712, True),     # the reference's 15M model widths (docs/models.md:11), A off the 32 grid
-    # A off the multiples of 4: the dr accumulation's element-wise path. (At D=40
-    # the same seed draws a block whose decay gradient bf16 q and k alone move by
-    # 9e-3 in exact arithmetic: tests/test_conditioning.py.)
+    # A off the multiples of 4: the dr accumulation's element-wise path
     (2, 150, 64, 70, False),
     (2, 150, 64, 70, True),
 ]
@@ -179,6 +177,74 @@ def test_block_matches_oracle(B, T, D, A, autocast):
     say(f"  worst {max(errs.values()):.3e}: {errs}")
     # test_all.py:157-166 holds loss and every gradient to 1e-2
     assert all(e < 1e-2 for e in errs.values()), errs
+
+
+_XFAIL_PAIR = "log_rate gradient {} of float64 on the block-pair form: the bf16 operand floor of this draw exceeds 1e-2"
+
+
+@pytest.mark.parametrize("autocast,path", [
+    pytest.param(False, "pair", marks=pytest.mark.xfail(strict=True, reason=_XFAIL_PAIR.format("2.1e-2"))),
+    pytest.param(True, "pair", marks=pytest.mark.xfail(strict=True, reason=_XFAIL_PAIR.format("5.6e-2"))),
+    (True, "generic"),
+])
+def test_ill_conditioned_block_draw(autocast, path, monkeypatch):
+    """The D=40, A=70, T=150 draw, whose decay gradient bf16 operands alone move
+    past 1e-2 (tests/test_conditioning.py), held to the parity bound. The
+    block-pair form (the library's choice at this shape) misses it by as much
+    as its roundings predict (test_ill_conditioned_draw_matches_its_rounding_floor):
+    kept as strict expected failures. Under autocast the generic kernel, whose
+    rounding profile differs, meets it."""
+    monkeypatch.setenv("ULM_FM_PATH", path)
+    test_block_matches_oracle(2, 150, 40, 70, autocast)
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+def test_ill_conditioned_draw_matches_its_rounding_floor(autocast, monkeypatch):
+    """The D=40, A=70, T=150 draw on the block-pair form: every gradient but log_rate within 1e-2 of
+    float64, and log_rate as far from it as the block-pair products' own bf16
+    roundings put it in otherwise exact arithmetic (oracle.fastmem.pair_form,
+    within 15% of that distance, and on the same side of the exact value): the
+    kernel's fp32 accumulations add nothing that matters beyond its operands'
+    roundings."""
+    B, T, D, A = 2, 150, 40, 70
+    monkeypatch.setenv("ULM_FM_PATH", "pair")
+    say(f"ill-conditioned block draw B={B} T={T} D={D} A={A} autocast={autocast}, block-pair form")
+    model = tiny_model(seed=T + A, dim=D, hidden_dim=A, n_layers=1, vocab_size=97, max_seq_len=max(T, 64))
+    blk = model.layers[0]
+    gen = torch.Generator().manual_seed(A)
+    with torch.no_grad():
+        blk.norm.weight.copy_(1.0 + 0.2 * torch.randn(D, generator=gen))
+    blk = blk.cuda().train()
+    x = torch.randn(B, T, D, generator=gen)
+    head = torch.randn(97, D, generator=gen, dtype=torch.float64) / D ** 0.5
+    targets = torch.randint(0, 97, (B, T), generator=gen)
+    xg = x.cuda().requires_grad_()
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        out = blk(xg)
+    _head_loss(out, head.float().cuda(), targets.cuda()).backward()
+    torch.cuda.synchronize()
+
+    def oracle_grads(fast_memory):
+        p = {n: t.detach().double().cpu().requires_grad_() for n, t in blk.named_parameters()}
+        orig = fm.fast_memory
+        fm.fast_memory = fast_memory
+        try:
+            ref = fm.block_forward(p, "", x.double(), norm_eps=blk.norm.eps, autocast=autocast)
+        finally:
+            fm.fast_memory = orig
+        _head_loss(ref, head, targets).backward()
+        return {n: t.grad for n, t in p.items()}
+
+    exact = oracle_grads(fm.fast_memory)
+    floor = oracle_grads(lambda r, v, g, w, form="chunked", chunk=64: fm.pair_form(r, v, g, w))
+    errs = {n: rel(t.grad, exact[n]) for n, t in blk.named_parameters()}
+    want = rel(floor["log_rate"], exact["log_rate"])
+    say(f"  kernel log_rate {errs['log_rate']:.3e}, bf16 rounding floor {want:.3e}; others {errs}")
+    assert all(e < 1e-2 for n, e in errs.items() if n != "log_rate"), errs
+    assert abs(errs["log_rate"] - want) < 0.15 * want
+    got_dev = (blk.log_rate.grad.double().cpu() - exact["log_rate"]).item()
+    want_dev = (floor["log_rate"] - exact["log_rate"]).item()
+    assert got_dev * want_dev > 0
 
 
 WGRAD_CASES = [

@@ -70,3 +70,41 @@ def test_training_step_at_110m_shape_matches_oracle(autocast):
     worst = max(errs, key=errs.get)
     say(f"  loss {loss.item():.6f}; worst {worst} {errs[worst]:.3e}")
     assert max(errs.values()) < 1e-2, {k: e for k, e in errs.items() if e >= 1e-3}
+
+
+def test_decode_at_its_benchmark_batch():
+    """The decode workload at its own batch: N=256 sequences of a 512-token
+    prompt through the chunked prefill (UnifiedLM.prefill, fp32 GEMMs), then 4
+    decode steps (model.py:96-111, 164-175), the 29 GB of fp32 state resident.
+    Rows 0, 137 and 255 must equal (within 1e-5) the same prompts run alone at
+    N=1, every row stays finite, and row 0's logits after the last step are
+    within 1e-2 of the oracle's forward_recurrent over the same 516 tokens in
+    float64 (the prefill's products take bf16 operands)."""
+    N, T, steps = 256, 512, 4
+    say(f"decode at the benchmark batch: N={N}, prefill {T} positions, {steps} steps, 12 blocks D=768 A=3072")
+    model = _model(13, 1024).eval()
+    gen = torch.Generator().manual_seed(13)
+    prompt = torch.randint(0, WIDTH["vocab_size"], (N, T), generator=gen)
+    nxt = torch.randint(0, WIDTH["vocab_size"], (steps, N), generator=gen)
+
+    def run(rows):
+        logits, states = model.prefill(prompt[rows].cuda())
+        outs = [logits]
+        for i in range(steps):
+            outs.append(model.step(nxt[i, rows].cuda(), states))
+        torch.cuda.synchronize()
+        return torch.stack(outs, 1)          # (n, steps + 1, V)
+
+    with torch.no_grad():
+        full = run(slice(None))
+        assert torch.isfinite(full).all()
+        for row in (0, 137, 255):
+            alone = run(slice(row, row + 1))
+            err = rel(full[row], alone[0])
+            say(f"  row {row}: N={N} vs N=1 rel {err:.3e}")
+            assert err < 1e-5
+        tokens = torch.cat([prompt[:1], nxt[:, :1].t()], 1).cuda()
+        ref = fm.forward_recurrent(oracle_params(model, device="cuda"), tokens)[0, T - 1:]
+    err = rel(full[0], ref)
+    say(f"  row 0 vs the oracle's forward_recurrent: rel {err:.3e}")
+    assert err < 1e-2

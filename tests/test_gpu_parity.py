@@ -143,6 +143,9 @@ PATH_CASES = [
     # the v tile copies done by the scores launch: an odd number of copy jobs (the
     # last workgroup's second group idle) and a last 256-feature block cut at D
     (1, 190, 96, 576, "pair"),
+    # slot counts off the multiples of 4 and odd widths on the pair form (the
+    # automatic choice there is the generic kernel, which the operator cases run)
+    (2, 150, 33, 17, "pair"),
 ]
 
 
@@ -154,6 +157,85 @@ def test_unified_memory_paths(B, T, A, D, path, monkeypatch):
     code = {"generic": 0, "chunked": 1, "pair": 2}[path]
     assert nat.lib().ulm_fm_path(B, T, A, D) == code
     test_unified_memory_matches_oracle(B, T, A, D, torch.bfloat16)
+
+
+AUTO_LONG_CASES = [
+    # B, T, A, D, the form the library picks by itself
+    (1, 2048, 3072, 768, 2),   # 110M widths: the pair form still needs fewer flops
+    (1, 3072, 3072, 768, 1),   # ... and past it the chunked state form
+    (1, 4160, 256, 768, 1),    # past 4096 positions the pair form does not apply
+    (1, 4160, 768, 256, 1),
+    (1, 2600, 712, 288, 0),    # the reference's 15M widths: the generic kernel past twice the state flops
+]
+
+
+@pytest.mark.parametrize("B,T,A,D,code", AUTO_LONG_CASES)
+def test_unified_memory_long_sequences_pick_their_form(B, T, A, D, code):
+    """Sequences past the lengths of the benchmark shapes, each on the form the
+    library chooses by itself (ulm_fm_path, no ULM_FM_PATH), against the oracle."""
+    assert nat.lib().ulm_fm_path(B, T, A, D) == code
+    test_unified_memory_matches_oracle(B, T, A, D, torch.bfloat16)
+
+
+def test_backward_follows_the_forward_form(monkeypatch):
+    """The form is fixed when the forward sizes its saved buffer: switching
+    ULM_FM_PATH between the forward and the backward changes nothing, the
+    backward reads the buffer in the forward's form (bitwise the same
+    gradients as without the switch)."""
+    B, T, A, D = 2, 200, 128, 64
+    say(f"form switched between forward and backward B={B} T={T} A={A} D={D}")
+    r, v, g, w = fm_inputs(B, T, A, D, seed=5, device="cpu")
+    qr, fr = fm.fast_memory(r, v, g, w, "chunked")
+
+    def run(fwd_form, bwd_form):
+        monkeypatch.setenv("ULM_FM_PATH", fwd_form)
+        leaves = [t.float().cuda().requires_grad_(True) for t in (r, v, g, w)]
+        q, fast = kernel.unified_memory(*leaves)
+        monkeypatch.setenv("ULM_FM_PATH", bwd_form)
+        ((q * (0.1 * qr).float().cuda()).sum() + (fast * fr.float().cuda()).sum()).backward()
+        torch.cuda.synchronize()
+        return [t.grad.cpu() for t in leaves]
+
+    for fwd_form, bwd_form in (("chunked", "pair"), ("pair", "chunked"), ("pair", "generic")):
+        same = run(fwd_form, fwd_form)
+        switched = run(fwd_form, bwd_form)
+        assert all(torch.equal(a, b) for a, b in zip(same, switched)), (fwd_form, bwd_form)
+        ref = fm.fast_memory_grads(r, v, g, w, 0.1 * qr, fr)
+        assert max(rel(a, b) for a, b in zip(switched, ref)) < 1e-2
+
+
+@pytest.mark.parametrize("B,T,A,D,path", [(2, 200, 128, 64, "pair"), (2, 200, 128, 64, "chunked"),
+                                          (1, 1024, 3072, 768, "pair"), (2, 200, 140, 64, "generic")])
+def test_decay_gradient_under_white_noise(B, T, A, D, path, monkeypatch):
+    """White-noise upstream gradients, whose random signs make the decay
+    gradient a sum with heavy cancellation: dr, dv, dw within 1e-2, and dg
+    within 1e-2 plus twice the distance the bf16 operands of the form put it
+    from the exact value in otherwise exact arithmetic (the block-pair form's
+    roundings, oracle.fastmem.pair_form_grads; the chunked forms' positional
+    identity, oracle.fastmem.dg_bf16_floor)."""
+    monkeypatch.setenv("ULM_FM_PATH", path)
+    say(f"white-noise upstream gradients B={B} T={T} A={A} D={D} {path}")
+    r, v, g, w = fm_inputs(B, T, A, D, seed=T + A + 1, device="cpu")
+    v = v.to(torch.bfloat16).double()
+    gen = torch.Generator().manual_seed(17)
+    dq = torch.randn(B, T, A, generator=gen, dtype=torch.float64) * 0.01
+    df = torch.randn(B, T, D, generator=gen, dtype=torch.float64).to(torch.bfloat16).double()
+    leaves = [r.float().cuda(), v.to(torch.bfloat16).cuda(), g.float().cuda(), w.float().cuda()]
+    leaves = [t.requires_grad_(True) for t in leaves]
+    q, fast = kernel.unified_memory(*leaves)
+    torch.autograd.backward((q, fast), (dq.float().cuda(), df.to(torch.bfloat16).cuda()))
+    torch.cuda.synchronize()
+    dr, dv, dg, dw = fm.fast_memory_grads(r, v, g, w, dq, df)
+    if path == "pair":
+        floor = fm.pair_form_grads(r, v, g, w, dq, df)[4]
+    else:
+        floor = fm.dg_bf16_floor(r, v, g, w, dq, df)
+    dg_floor = abs(floor.item() - dg.item()) / abs(dg.item())
+    errs = {"dr": rel(leaves[0].grad, dr), "dv": rel(leaves[1].grad, dv), "dw": rel(leaves[3].grad, dw)}
+    dg_err = abs(leaves[2].grad.item() - dg.item()) / abs(dg.item())
+    say(f"  rel errors {errs}, dg {dg_err:.3e} (bf16 floor {dg_floor:.3e})")
+    assert max(errs.values()) < 1e-2, errs
+    assert dg_err < 1e-2 + 2 * dg_floor, (dg_err, dg_floor)
 
 
 @pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])

@@ -246,6 +246,51 @@ def test_dg_bf16_floor_without_rounding_is_the_exact_dg():
     assert 0 < abs(rounded.item() - dg.item()) < 0.1 * abs(dg.item())
 
 
+def test_pair_form_without_rounding_is_autograd():
+    """pair_form_grads' closed-form gradients (summed over pairs for the decay)
+    equal float64 autograd of the dense form, with and without dq_out, and
+    pair_form's autograd wrapper returns the same."""
+    r, v, g, w = _inputs(B=2, T=70, A=6, D=4)
+    gen = torch.Generator().manual_seed(12)
+    dq = torch.randn(r.shape, generator=gen, dtype=torch.float64)
+    df = torch.randn(v.shape, generator=gen, dtype=torch.float64)
+    for dq_out in (dq, None):
+        q, fast, dr, dv, dg, dw = fm.pair_form_grads(r, v, g, w, dq_out, df, roundings=())
+        qe, fe = fm.fast_memory(r, v, g, w, "dense")
+        ref = fm.fast_memory_grads(r, v, g, w, dq_out, df, "dense")
+        for got, exp in zip((q, fast, dr, dv, dg, dw), (qe, fe) + tuple(ref)):
+            assert (got - exp).abs().max() < 1e-12 * max(1.0, exp.abs().max().item())
+    leaves = [t.clone().requires_grad_() for t in (r, v, g, w)]
+    q, fast = fm.pair_form(*leaves, roundings=())
+    ((q * dq).sum() + (fast * df).sum()).backward()
+    for t, exp in zip(leaves, fm.fast_memory_grads(r, v, g, w, dq, df, "dense")):
+        assert (t.grad - exp).abs().max() < 1e-12 * max(1.0, exp.abs().max().item())
+
+
+@pytest.mark.parametrize("rounding,moves,keeps", [
+    ("qk", {"fast", "dv", "dg"}, {"q", "dr", "dw"}),   # P, hence fast, dv and the pair sum
+    ("P", {"fast", "dv", "dg"}, {"q", "dr", "dw"}),
+    ("v", {"fast", "dr", "dg", "dw"}, {"q", "dv"}),
+    ("dfast", {"dr", "dv", "dg", "dw"}, {"q", "fast"}),
+    ("dS", {"dr", "dg", "dw"}, {"q", "fast", "dv"}),
+    ("qk_bwd", {"dr", "dg", "dw"}, {"q", "fast", "dv"}),
+])
+def test_each_pair_rounding_moves_only_what_reads_it(rounding, moves, keeps):
+    """A planted bf16 rounding of one operand changes exactly the outputs that
+    read that operand (a rounding applied at the wrong place fails this)."""
+    r, v, g, w = _inputs(B=2, T=70, A=6, D=4)
+    gen = torch.Generator().manual_seed(13)
+    dq = torch.randn(r.shape, generator=gen, dtype=torch.float64)
+    df = torch.randn(v.shape, generator=gen, dtype=torch.float64)
+    names = ("q", "fast", "dr", "dv", "dg", "dw")
+    exact = dict(zip(names, fm.pair_form_grads(r, v, g, w, dq, df, roundings=())))
+    got = dict(zip(names, fm.pair_form_grads(r, v, g, w, dq, df, roundings=(rounding,))))
+    for n in moves:
+        assert (got[n] - exact[n]).abs().max() > 0, n
+    for n in keeps:
+        assert torch.equal(got[n], exact[n]), n
+
+
 # ----- model level (test_all.py:100-137)
 
 def _tokens(B=3, T=40, V=97, seed=0):

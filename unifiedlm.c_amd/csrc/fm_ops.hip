@@ -105,16 +105,36 @@ int pad32(int x) { return (x + 31) / 32 * 32; }
 // change between a forward and its backward).
 enum Path { PATH_GENERIC = 0, PATH_CHUNKED = 1, PATH_PAIR = 2 };
 
+bool pair_supported(int B, int T, int A, int D) { return T <= 4096 && fm_aligned(B, T, pad32(A), pad32(D)); }
+
+// Whether a form can evaluate this shape at all.
+bool path_supported(Path p, int B, int T, int A, int D) {
+    return p == PATH_GENERIC || (p == PATH_PAIR && pair_supported(B, T, A, D)) ||
+           (p == PATH_CHUNKED && fm_aligned(B, T, A, D));
+}
+
 Path train_path(int B, int T, int A, int D) {
     const char *env = getenv("ULM_FM_PATH");
     if (env && env[0] == 'g') return PATH_GENERIC;
-    const bool pair_ok = T <= 4096 && fm_aligned(B, T, pad32(A), pad32(D));
-    if (!fm_aligned(B, T, A, D)) return pair_ok ? PATH_PAIR : PATH_GENERIC;
+    const bool pair_ok = pair_supported(B, T, A, D);
+    // the pair form's flops and its saved scores (6 B Tq^2 bytes) grow with T.
+    // Off the 32 grid the alternative is the generic kernel (natural bf16
+    // copies, no scores saved), which runs its flops at a fraction of the pair
+    // products' rate and whose decay gradient goes through the positional
+    // identity (bf16 operands move it further): it serves sequences past 2048
+    // positions where the pair form needs twice the state form's flops (at
+    // the reference's 15M widths, A = 712 and D = 288, from about 2400
+    // positions on)
+    const double chunked = 16.0 * A * D + 8.0 * ULM_CHUNK * (A + D);
+    const double pair = pair_flops_per_token(B, T, A, D);
+    if (!fm_aligned(B, T, A, D)) {
+        if (env && env[0] == 'p' && pair_ok) return PATH_PAIR;
+        return pair_ok && (T <= 2048 || pair < 2.0 * chunked) ? PATH_PAIR : PATH_GENERIC;
+    }
     if (env && env[0] == 'c') return PATH_CHUNKED;
     if (!pair_ok) return PATH_CHUNKED;
     if (env && env[0] == 'p') return PATH_PAIR;
-    const double chunked = 16.0 * A * D + 8.0 * ULM_CHUNK * (A + D);
-    return pair_flops_per_token(B, T, A, D) < 0.8 * chunked ? PATH_PAIR : PATH_CHUNKED;
+    return pair < 0.8 * chunked ? PATH_PAIR : PATH_CHUNKED;
 }
 
 struct Saved {
@@ -248,6 +268,27 @@ BwdWs bwd_layout(void *base, int B, int T, int A, int D, int dfast_dtype, Path p
     return w;
 }
 
+// The saved buffer's size names the form that filled it: the layout rounded
+// up to 4 KB plus 256 (form + 1) bytes. ulm_fm_saved_bytes returns that size,
+// ulm_fm_fwd evaluates the form it names and ulm_fm_bwd reads the buffer in
+// the same form, so the forward and the backward of one call agree whatever
+// ULM_FM_PATH says in between. Returns -1 for a size no form produces at this
+// shape.
+constexpr size_t kTagQuantum = 4096, kTagStep = 256;
+
+size_t saved_tagged_bytes(int B, int T, int A, int D, int v_dtype, Path p) {
+    return align_up(saved_layout(nullptr, B, T, A, D, v_dtype, p).bytes, kTagQuantum) +
+           kTagStep * (static_cast<size_t>(p) + 1);
+}
+
+int saved_path(size_t bytes, int B, int T, int A, int D, int v_dtype) {
+    const size_t tag = bytes % kTagQuantum / kTagStep;
+    if (tag < 1 || tag > 3) return -1;
+    const Path p = static_cast<Path>(tag - 1);
+    if (!path_supported(p, B, T, A, D) || saved_tagged_bytes(B, T, A, D, v_dtype, p) != bytes) return -1;
+    return static_cast<int>(p);
+}
+
 }  // namespace
 
 }  // namespace ulm
@@ -318,7 +359,12 @@ extern "C" int ulm_fm_path(int B, int T, int A, int D) {
 
 extern "C" size_t ulm_fm_saved_bytes(int B, int T, int A, int D, int v_dtype) {
     if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(v_dtype)) return 0;
-    return saved_layout(nullptr, B, T, A, D, v_dtype, train_path(B, T, A, D)).bytes;
+    return saved_tagged_bytes(B, T, A, D, v_dtype, train_path(B, T, A, D));
+}
+
+extern "C" int ulm_fm_saved_path(size_t saved_bytes, int B, int T, int A, int D, int v_dtype) {
+    if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(v_dtype)) return -1;
+    return saved_path(saved_bytes, B, T, A, D, v_dtype);
 }
 
 extern "C" size_t ulm_fm_fwd_workspace_bytes(int B, int T, int A, int D, int fast_dtype) {
@@ -397,15 +443,16 @@ extern "C" int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const floa
     ULM_REQUIRE(B > 0 && T > 0 && A > 0 && D > 0, "ulm_fm_fwd: bad sizes B=%d T=%d A=%d D=%d", B, T, A, D);
     ULM_REQUIRE(valid_dtype(v_dtype) && valid_dtype(fast_dtype), "ulm_fm_fwd: bad dtype %d/%d", v_dtype, fast_dtype);
     ULM_REQUIRE(r && v && g && w && q && fast && saved, "ulm_fm_fwd: null pointer");
-    const size_t need_s = ulm_fm_saved_bytes(B, T, A, D, v_dtype);
-    ULM_REQUIRE(saved_bytes >= need_s, "ulm_fm_fwd: saved buffer of %zu bytes, need %zu", saved_bytes, need_s);
-    const size_t need = ulm_fm_fwd_workspace_bytes(B, T, A, D, fast_dtype);
+    const int path = saved_path(saved_bytes, B, T, A, D, v_dtype);
+    ULM_REQUIRE(path >= 0, "ulm_fm_fwd: a saved buffer of %zu bytes names no form at B=%d T=%d A=%d D=%d (pass "
+                "the size ulm_fm_saved_bytes returned)", saved_bytes, B, T, A, D);
+    const size_t need = fwd_layout(nullptr, B, T, A, D, fast_dtype, static_cast<Path>(path)).bytes;
     ULM_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), "ulm_fm_fwd: workspace of %zu bytes, need %zu",
                 workspace_bytes, need);
     RSrc rs;
     rs.r = r;
     return fm_forward(rs, v, v_dtype, g, w, q, nullptr, ULM_F32, nullptr, fast, fast_dtype, saved, workspace, nullptr,
-                      nullptr, B, T, A, D, train_path(B, T, A, D), static_cast<hipStream_t>(stream));
+                      nullptr, B, T, A, D, static_cast<Path>(path), static_cast<hipStream_t>(stream));
 }
 
 // ---------------------------------------------------------------------------
@@ -438,9 +485,13 @@ extern "C" int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const 
                       A, D, PATH_CHUNKED, static_cast<hipStream_t>(stream));
 }
 
-extern "C" size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D, int dfast_dtype) {
+extern "C" size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D, int dfast_dtype, size_t saved_bytes,
+                                             int v_dtype) {
     if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(dfast_dtype)) return 0;
-    return bwd_layout(nullptr, B, T, A, D, dfast_dtype, train_path(B, T, A, D)).bytes;
+    if (saved_bytes == 0) return bwd_layout(nullptr, B, T, A, D, dfast_dtype, train_path(B, T, A, D)).bytes;
+    if (!valid_dtype(v_dtype)) return 0;
+    const int path = saved_path(saved_bytes, B, T, A, D, v_dtype);
+    return path < 0 ? 0 : bwd_layout(nullptr, B, T, A, D, dfast_dtype, static_cast<Path>(path)).bytes;
 }
 
 namespace {
@@ -449,8 +500,7 @@ namespace {
 // (d(w q) in dqw_dt, may be null) adds w dqw to dq_out and sum_t q dqw to dw.
 int fm_backward(const RSrc &r, const float *g, const float *w, const void *saved, int v_dtype, const void *dfast,
                 int dfast_dtype, const float *dq_out, const void *dqw, int dqw_dt, float *dr, void *dv, int dv_dtype,
-                float *dg, float *dw, void *workspace, int B, int T, int A, int D, hipStream_t s) {
-    const Path path = train_path(B, T, A, D);
+                float *dg, float *dw, void *workspace, int B, int T, int A, int D, Path path, hipStream_t s) {
     const Saved sv = saved_layout(const_cast<void *>(saved), B, T, A, D, v_dtype, path);
     const BwdWs ws = bwd_layout(workspace, B, T, A, D, dfast_dtype, path);
     const size_t nd = static_cast<size_t>(B) * T * D, na = static_cast<size_t>(B) * T * A;
@@ -512,15 +562,16 @@ extern "C" int ulm_fm_bwd(const float *r, const float *g, const float *w, const 
     ULM_REQUIRE(valid_dtype(v_dtype) && valid_dtype(dfast_dtype) && valid_dtype(dv_dtype),
                 "ulm_fm_bwd: bad dtype %d/%d/%d", v_dtype, dfast_dtype, dv_dtype);
     ULM_REQUIRE(r && g && w && saved && dfast && dr && dv && dg && dw, "ulm_fm_bwd: null pointer");
-    const size_t need_s = ulm_fm_saved_bytes(B, T, A, D, v_dtype);
-    ULM_REQUIRE(saved_bytes >= need_s, "ulm_fm_bwd: saved buffer of %zu bytes, need %zu", saved_bytes, need_s);
-    const size_t need = ulm_fm_bwd_workspace_bytes(B, T, A, D, dfast_dtype);
+    const int path = saved_path(saved_bytes, B, T, A, D, v_dtype);
+    ULM_REQUIRE(path >= 0, "ulm_fm_bwd: a saved buffer of %zu bytes names no form at B=%d T=%d A=%d D=%d", saved_bytes,
+                B, T, A, D);
+    const size_t need = bwd_layout(nullptr, B, T, A, D, dfast_dtype, static_cast<Path>(path)).bytes;
     ULM_REQUIRE(workspace && workspace_bytes >= need, "ulm_fm_bwd: workspace of %zu bytes, need %zu",
                 workspace_bytes, need);
     RSrc rs;
     rs.r = r;
     return fm_backward(rs, g, w, saved, v_dtype, dfast, dfast_dtype, dq_out, nullptr, ULM_BF16, dr, dv, dv_dtype, dg,
-                       dw, workspace, B, T, A, D, static_cast<hipStream_t>(stream));
+                       dw, workspace, B, T, A, D, static_cast<Path>(path), static_cast<hipStream_t>(stream));
 }
 
 // ---------------------------------------------------------------------------
@@ -541,9 +592,10 @@ extern "C" int ulm_block_fm_fwd(const void *pre, int pre_dtype, const float *bia
                 "ulm_block_fm_fwd: bad dtype %d/%d/%d", pre_dtype, v_dtype, qw_dtype);
     ULM_REQUIRE(pre && denom && v && g && w && qw && x && y && saved && workspace, "ulm_block_fm_fwd: null pointer");
     ULM_REQUIRE(static_cast<const void *>(x) != static_cast<const void *>(y), "ulm_block_fm_fwd: y must not alias x");
-    const size_t need_s = ulm_fm_saved_bytes(B, T, A, D, v_dtype);
-    ULM_REQUIRE(saved_bytes >= need_s, "ulm_block_fm_fwd: saved buffer of %zu bytes, need %zu", saved_bytes, need_s);
-    const size_t need = ulm_block_fm_fwd_workspace_bytes(B, T, A, D);
+    const int path = saved_path(saved_bytes, B, T, A, D, v_dtype);
+    ULM_REQUIRE(path >= 0, "ulm_block_fm_fwd: a saved buffer of %zu bytes names no form at B=%d T=%d A=%d D=%d",
+                saved_bytes, B, T, A, D);
+    const size_t need = fwd_layout(nullptr, B, T, A, D, ULM_F32, static_cast<Path>(path), true).bytes;
     ULM_REQUIRE(workspace_bytes >= need, "ulm_block_fm_fwd: workspace of %zu bytes, need %zu", workspace_bytes, need);
     RSrc rs;
     rs.pre = pre;
@@ -551,7 +603,7 @@ extern "C" int ulm_block_fm_fwd(const void *pre, int pre_dtype, const float *bia
     rs.bias = bias;
     rs.denom = denom;
     return fm_forward(rs, v, v_dtype, g, w, nullptr, qw, qw_dtype, x, y, ULM_F32, saved, workspace, nullptr, nullptr, B,
-                      T, A, D, train_path(B, T, A, D), static_cast<hipStream_t>(stream));
+                      T, A, D, static_cast<Path>(path), static_cast<hipStream_t>(stream));
 }
 
 extern "C" int ulm_block_fm_bwd(const void *pre, int pre_dtype, const float *bias, const float *denom, const float *g,
@@ -565,9 +617,10 @@ extern "C" int ulm_block_fm_bwd(const void *pre, int pre_dtype, const float *bia
                 "ulm_block_fm_bwd: bad dtype %d/%d/%d/%d/%d", pre_dtype, v_dtype, dfast_dtype, dv_dtype, dqw_dtype);
     ULM_REQUIRE(pre && denom && g && w && saved && dfast && dqw && dr && dv && dg && dw,
                 "ulm_block_fm_bwd: null pointer");
-    const size_t need_s = ulm_fm_saved_bytes(B, T, A, D, v_dtype);
-    ULM_REQUIRE(saved_bytes >= need_s, "ulm_block_fm_bwd: saved buffer of %zu bytes, need %zu", saved_bytes, need_s);
-    const size_t need = ulm_fm_bwd_workspace_bytes(B, T, A, D, dfast_dtype);
+    const int path = saved_path(saved_bytes, B, T, A, D, v_dtype);
+    ULM_REQUIRE(path >= 0, "ulm_block_fm_bwd: a saved buffer of %zu bytes names no form at B=%d T=%d A=%d D=%d",
+                saved_bytes, B, T, A, D);
+    const size_t need = bwd_layout(nullptr, B, T, A, D, dfast_dtype, static_cast<Path>(path)).bytes;
     ULM_REQUIRE(workspace && workspace_bytes >= need, "ulm_block_fm_bwd: workspace of %zu bytes, need %zu",
                 workspace_bytes, need);
     RSrc rs;
@@ -576,7 +629,7 @@ extern "C" int ulm_block_fm_bwd(const void *pre, int pre_dtype, const float *bia
     rs.bias = bias;
     rs.denom = denom;
     return fm_backward(rs, g, w, saved, v_dtype, dfast, dfast_dtype, nullptr, dqw, dqw_dtype, dr, dv, dv_dtype, dg, dw,
-                       workspace, B, T, A, D, static_cast<hipStream_t>(stream));
+                       workspace, B, T, A, D, static_cast<Path>(path), static_cast<hipStream_t>(stream));
 }
 
 // the block's chunked prefill: ulm_block_fm_fwd plus the decode state after T-1

@@ -1212,41 +1212,20 @@ size_t pair_stats_bytes(int B, int T, int A) { return pair_stats_layout(nullptr,
 
 
 
-// The backward: dv = P^T dfast in dv_dt (B, T, D), on the device's second
-// stream (forked from s and joined back into s before the return, so that work
-// later on s is ordered after it); dS = dscores(dfast, v) and its transpose dSt
-// with the pair part of the decay gradient; dq_f = dS k with the per-slot
-// statistics in its epilogue (dr without dk_f and the carry; the tile
-// statistics); dk_f = dS^T q added into dr with the carry of dkc between
-// tiles, formed in that product; dw (A,) and dg (1,) reduced in a fixed order.
-// Calls from several host threads enqueue one at a time: the fork and join
-// events are shared. vR, doR: R
-// layout (D); kQ, qQ: Q layout (A); doQ: Q layout (D); P, Pt, Plo from the
-// forward. r: the read addresses (or their address inputs); xq / xq_kind: the
-// extra gradient of q (0 none, 1 dq_out fp32, 2 + dtype d(w q)); nck: the
-// forward's chunk checkpoints; ws: pair_stats_bytes(B, T, A) bytes.
-int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t *doQ, const uint16_t *kQ,
-                         const uint16_t *qQ, const uint16_t *P, const uint16_t *Pt, const uint16_t *Plo,
-                         const float *g, uint16_t *dS, uint16_t *dSt, double *dg_part, const RSrc &rsrc_in,
-                         const void *xq, int xq_kind, const float *nck, const float *w, float *dr, float *dw,
-                         float *dg, void *ws, void *dv, int dv_dt, int B, int T, int A, int D, hipStream_t s) {
+namespace {
+// The launches of launch_pair_backward after the fork: dv on the second stream
+// (sd, or s when null), then dscores, dq_f with the statistics, dk_f into dr and
+// the final sums on s.
+int pair_backward_products(const SideStream *sd, const uint16_t *vR, const uint16_t *doR, const uint16_t *doQ,
+                           const uint16_t *kQ, const uint16_t *qQ, const uint16_t *P, const uint16_t *Pt,
+                           const uint16_t *Plo, const float *g, uint16_t *dS, uint16_t *dSt, double *dg_part,
+                           const RSrc &rsrc_in, const void *xq, int xq_kind, const float *nck, const float *w,
+                           float *dr, float *dw, float *dg, const PairStats &st, void *dv, int dv_dt, int B, int T,
+                           int A, int D, hipStream_t s) {
     using namespace pair;
     const int G = pair_block(B, T), Tq = pair_tq(B, T), NT = (T + 63) / 64, MT = Tq / G;
     const int Ap = (A + 31) / 32 * 32, Dp = (D + 31) / 32 * 32;   // operand tile widths
-    const PairStats st = pair_stats_layout(ws, B, T, A);
-    if (MT > 32) return fail(ULM_ERR_UNSUPPORTED, "block-pair backward: %d position tiles (at most 32)", MT);
     const Mat sm = p_mat(dS, Tq);
-    // dv = P^T dfast on the second stream, beside dscores (joined at the end),
-    // where its work outweighs the fork and join: each event between two
-    // dependent kernels costs several microseconds of gap
-    static std::mutex side_mu;
-    const std::lock_guard<std::mutex> lock(side_mu);
-    SideStream *sd = nullptr;
-    if (static_cast<double>(B) * Tq * Tq * D >= 2e9) {
-        ULM_TRY(side_stream(sd));
-        if (hipEventRecord(sd->fork, s) != hipSuccess || hipStreamWaitEvent(sd->s, sd->fork, 0) != hipSuccess)
-            return check_launch("side stream fork");
-    }
     {
         Args d{};
         d.T = T;
@@ -1262,7 +1241,6 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
         d.out_dt = dv_dt;
         d.F = D;
         ULM_TRY((launch<false, EPI_ROWS>(d, G, B, sd ? sd->s : s)));
-        if (sd && hipEventRecord(sd->join, sd->s) != hipSuccess) return check_launch("side stream join");
     }
     Args a{};
     a.T = T;
@@ -1323,9 +1301,52 @@ int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t
     const int jobs = B * MT * ((A + G - 1) / G);
     pair::final_kernel<<<(A + pair::kFinalSlots - 1) / pair::kFinalSlots + 1, 256, 0, s>>>(
         st.tW, MT, st.dgq, 2 * jobs, dg_part, pair_dscore_jobs(B, T), dw, dg, B, A);
-    ULM_TRY(check_launch("final_kernel"));
-    if (sd && hipStreamWaitEvent(s, sd->join, 0) != hipSuccess) return check_launch("side stream wait");
-    return ULM_OK;
+    return check_launch("final_kernel");
+}
+}  // namespace
+
+// The backward: dv = P^T dfast in dv_dt (B, T, D), on the device's second
+// stream (forked from s and joined back into s before the return, so that work
+// later on s is ordered after it); dS = dscores(dfast, v) and its transpose dSt
+// with the pair part of the decay gradient; dq_f = dS k with the per-slot
+// statistics in its epilogue (dr without dk_f and the carry; the tile
+// statistics); dk_f = dS^T q added into dr with the carry of dkc between
+// tiles, formed in that product; dw (A,) and dg (1,) reduced in a fixed order.
+// Calls from several host threads enqueue one at a time: the fork and join
+// events are shared. vR, doR: R
+// layout (D); kQ, qQ: Q layout (A); doQ: Q layout (D); P, Pt, Plo from the
+// forward. r: the read addresses (or their address inputs); xq / xq_kind: the
+// extra gradient of q (0 none, 1 dq_out fp32, 2 + dtype d(w q)); nck: the
+// forward's chunk checkpoints; ws: pair_stats_bytes(B, T, A) bytes.
+int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t *doQ, const uint16_t *kQ,
+                         const uint16_t *qQ, const uint16_t *P, const uint16_t *Pt, const uint16_t *Plo,
+                         const float *g, uint16_t *dS, uint16_t *dSt, double *dg_part, const RSrc &rsrc_in,
+                         const void *xq, int xq_kind, const float *nck, const float *w, float *dr, float *dw,
+                         float *dg, void *ws, void *dv, int dv_dt, int B, int T, int A, int D, hipStream_t s) {
+    const int Tq = pair_tq(B, T), MT = Tq / pair_block(B, T);
+    const PairStats st = pair_stats_layout(ws, B, T, A);
+    if (MT > 32) return fail(ULM_ERR_UNSUPPORTED, "block-pair backward: %d position tiles (at most 32)", MT);
+    // dv = P^T dfast on the second stream, beside dscores (joined at the end),
+    // where its work outweighs the fork and join: each event between two
+    // dependent kernels costs several microseconds of gap
+    static std::mutex side_mu;
+    const std::lock_guard<std::mutex> lock(side_mu);
+    SideStream *sd = nullptr;
+    if (static_cast<double>(B) * Tq * Tq * D >= 2e9) {
+        ULM_TRY(side_stream(sd));
+        if (hipEventRecord(sd->fork, s) != hipSuccess || hipStreamWaitEvent(sd->s, sd->fork, 0) != hipSuccess)
+            return check_launch("side stream fork");
+    }
+    // From the fork on, every return joins the second stream back into s, the
+    // error returns included: the caller frees the workspace (and may reuse dv)
+    // in stream order on s once this returns, so s must not run ahead of dv.
+    const int rc = pair_backward_products(sd, vR, doR, doQ, kQ, qQ, P, Pt, Plo, g, dS, dSt, dg_part, rsrc_in, xq,
+                                          xq_kind, nck, w, dr, dw, dg, st, dv, dv_dt, B, T, A, D, s);
+    if (sd && (hipEventRecord(sd->join, sd->s) != hipSuccess || hipStreamWaitEvent(s, sd->join, 0) != hipSuccess)) {
+        const int jrc = check_launch("side stream join");
+        return rc != ULM_OK ? rc : jrc;
+    }
+    return rc;
 }
 
 }  // namespace ulm

@@ -24,6 +24,6 @@ int check_launch(const char *what) {
 
 }  // namespace ulm
 
-extern "C" int ulm_abi_version(void) { return 2; }
+extern "C" int ulm_abi_version(void) { return 3; }
 
 extern "C" const char *ulm_last_error(void) { return ulm::g_last_error; }

@@ -107,8 +107,9 @@ def fm_bwd(r: Tensor, g: Tensor, w: Tensor, saved: Tensor, v_dtype: torch.dtype,
     dv = torch.empty(B, T, D, device=r.device, dtype=dfast.dtype)
     dg = torch.empty(1, device=r.device, dtype=torch.float32)
     dw = torch.empty(A, device=r.device, dtype=torch.float32)
-    ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D, ddt)
-    ws = torch.empty(ws_bytes, device=r.device, dtype=torch.uint8)
+    # the saved buffer's size names the form its forward used; the backward follows it
+    ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D, ddt, saved.numel(), nat.dtype_code(v_dtype))
+    ws = torch.empty(max(ws_bytes, 1), device=r.device, dtype=torch.uint8)
     call("ulm_fm_bwd", ptr(r32), ptr(g1), ptr(w32), ptr(saved), saved.numel(), nat.dtype_code(v_dtype), ptr(dfast),
          ddt, ptr(dqo), ptr(dr), ptr(dv), ddt, ptr(dg), ptr(dw), ptr(ws), ws_bytes, B, T, A, D, nat.stream_of(r))
     return dr, dv, dg, dw
@@ -439,8 +440,8 @@ def _block_bwd_impl(dout, x, norm_w, conv_w, key_w, key_b, log_eps, val_w, mu_w,
     dv = torch.empty(M, D, device=dev, dtype=cdt)
     dg = torch.empty(1, device=dev, dtype=f32)
     dw = torch.empty(A, device=dev, dtype=f32)
-    ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D, cd)
-    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    ws_bytes = nat.lib().ulm_fm_bwd_workspace_bytes(B, T, A, D, cd, saved.numel(), cd)
+    ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
     call("ulm_block_fm_bwd", ptr(pre), cd, ptr(b32), ptr(denom), ptr(g1), ptr(w32), ptr(saved), saved.numel(), cd,
          ptr(d16), cd, ptr(dqw), cd, ptr(dr), ptr(dv), cd, ptr(dg), ptr(dw), ptr(ws), ws_bytes, B, T, A, D, s)
     del ws, dqw

@@ -15,9 +15,11 @@ weights). Every body here is this package's own:
     address and the conv window;
   * prefill runs a prompt in one chunked pass and leaves the decode state.
 
-Training-loop and sampling helpers of the reference (optimizer groups, MFU
-estimate, sampling loop) are outside the fast-memory path and not provided.
+The reference's training-loop and sampling helpers keep their signatures
+(configure_optimizers, estimate_mfu, generate: train.py:172, 295, sample.py:61)
+with bodies of this package's own; generate samples on the decode kernels.
 """
+import inspect
 import math
 from dataclasses import dataclass
 from typing import Optional
@@ -26,7 +28,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from kernel import (LOG_W_MAX, LOG_W_MIN, block_prefill, decode_addr, decode_pre, decode_state, fm_prefill,
+from kernel import (CHUNK, LOG_W_MAX, LOG_W_MIN, block_prefill, decode_addr, decode_pre, decode_state, fm_prefill,
                     relu2_address, unified_block, unified_memory)
 
 
@@ -78,18 +80,21 @@ class UnifiedBlock(nn.Module):
     def __init__(self, args: ModelArgs):
         super().__init__()
         width, slots, taps = args.dim, args.hidden_dim, args.conv_size
-        # the memory's scalar and per-slot parameters: the implicit null slot
-        # (log eps), the forgetting rate (1 / (4 max_seq_len)), the prior mass
-        self.log_eps = nn.Parameter(torch.zeros(()))
-        self.log_rate = nn.Parameter(torch.tensor(-math.log(4.0 * args.max_seq_len)))
-        self.log_w = nn.Parameter(torch.full((slots,), math.log(args.prior)))
-        # submodules in the reference's registration order (their default
-        # initialisations draw from the RNG in this order)
+        # registered in the reference's order (model.py:59-68): the submodules'
+        # default initialisations draw from the RNG in this order, and
+        # parameters() / state_dict() list the same names in the same order
+        # (a module's own parameters before its submodules'), so optimizer
+        # states keyed by position carry over. The memory's own parameters are
+        # the implicit null slot (log eps), the forgetting rate
+        # (1 / (4 max_seq_len)) and the prior mass.
         self.norm = RMSNorm(width, eps=args.norm_eps)
         self.conv = nn.Conv1d(width, width, taps, padding=taps - 1, groups=width, bias=False)
         self.key = nn.Linear(width, slots)
         self.mu = nn.Linear(slots, width, bias=False)
+        self.log_eps = nn.Parameter(torch.zeros(()))
         self.val = nn.Linear(width, width, bias=False)
+        self.log_rate = nn.Parameter(torch.tensor(-math.log(4.0 * args.max_seq_len)))
+        self.log_w = nn.Parameter(torch.full((slots,), math.log(args.prior)))
         self.dropout = nn.Dropout(args.dropout)
 
     def code(self, u):
@@ -305,3 +310,69 @@ class UnifiedLM(nn.Module):
         constant-size state per block: what run.c computes (model.py:164-175)."""
         states = self.init_states(tokens.shape[0], tokens.device)
         return torch.stack([self.step(tokens[:, t], states) for t in range(tokens.shape[1])], dim=1)
+
+    # ---- the training loop's and the sampler's helpers (train.py:172, 295; sample.py:61)
+
+    def configure_optimizers(self, weight_decay, learning_rate, betas, device_type):
+        """AdamW over two groups: weight decay on the matrices (every parameter
+        of two or more dimensions: embedding, key, mu, value and conv weights),
+        none on the vectors and scalars (norm weights, key biases, log_eps,
+        log_rate, log_w), in parameters() order (model.py:177-194). The fused
+        AdamW kernel is used on a GPU when this torch provides it."""
+        params = [p for p in self.parameters() if p.requires_grad]
+        matrices = [p for p in params if p.dim() >= 2]
+        vectors = [p for p in params if p.dim() < 2]
+        print(f"num decayed parameter tensors: {len(matrices)}, with {sum(p.numel() for p in matrices):,} "
+              "parameters")
+        print(f"num non-decayed parameter tensors: {len(vectors)}, with {sum(p.numel() for p in vectors):,} "
+              "parameters")
+        fused = device_type == "cuda" and "fused" in inspect.signature(torch.optim.AdamW).parameters
+        groups = [{"params": matrices, "weight_decay": weight_decay}, {"params": vectors, "weight_decay": 0.0}]
+        optimizer = torch.optim.AdamW(groups, lr=learning_rate, betas=betas, **({"fused": True} if fused else {}))
+        print(f"using fused AdamW: {fused}")
+        return optimizer
+
+    def estimate_mfu(self, fwdbwd_per_iter, dt, peak_flops=2516.6e12):
+        """Model flops utilisation of one iteration of fwdbwd_per_iter sequences
+        of max_seq_len tokens taking dt seconds. The model flops per token are
+        the reference's count (model.py:196-203): 6 per parameter, plus per
+        block 6 (min(CHUNK, T) (2 A + D) + 2 A D) for the chunk-local mixing
+        and the carried state. The reference divides by the A100's bf16 peak
+        (312 TFLOP/s); here the default is the MI355X's dense bf16 peak."""
+        n_params = sum(p.numel() for p in self.parameters())
+        cfg = self.params
+        T, A, D = cfg.max_seq_len, cfg.hidden_dim, cfg.dim
+        mixing = min(CHUNK, T) * (2 * A + D) + 2 * A * D
+        per_token = 6 * n_params + 6 * cfg.n_layers * mixing
+        return per_token * T * fwdbwd_per_iter / dt / peak_flops
+
+    @torch.inference_mode()
+    def generate(self, idx, max_new_tokens, temperature=1.0, top_k=None):
+        """Appends max_new_tokens sampled tokens to idx (B, T0) (model.py:205-222):
+        each is drawn from the last position's logits over at most max_seq_len
+        preceding tokens, divided by temperature and cut to the top_k largest
+        (temperature 0: the argmax). While the context fits max_seq_len the
+        sequences are decoded recurrently (one chunked prefill, then one
+        decode step per token), which gives the logits of a full forward over
+        the same context; once it slides, each token re-reads the window of
+        the last max_seq_len tokens in one chunked pass."""
+        window = self.params.max_seq_len
+        states = None
+        for _ in range(max_new_tokens):
+            if states is None or idx.size(1) > window:
+                logits, states = self.prefill(idx[:, -window:])
+            nxt = self._sample(logits.float(), temperature, top_k)
+            idx = torch.cat((idx, nxt), dim=1)
+            if idx.size(1) <= window:
+                logits = self.step(nxt[:, 0], states)
+        return idx
+
+    @staticmethod
+    def _sample(logits, temperature, top_k):
+        if temperature == 0.0:
+            return logits.argmax(-1, keepdim=True)
+        logits = logits / temperature
+        if top_k is not None:
+            kth = torch.topk(logits, min(top_k, logits.size(-1))).values[:, -1:]
+            logits = logits.masked_fill(logits < kth, -float("inf"))
+        return torch.multinomial(torch.softmax(logits, dim=-1), num_samples=1)

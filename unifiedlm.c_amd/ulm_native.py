@@ -24,11 +24,12 @@ SIGNATURES = {
     "ulm_last_error": (ctypes.c_char_p, []),
     "ulm_fm_path": (I, [I, I, I, I]),
     "ulm_fm_saved_bytes": (SZ, [I, I, I, I, I]),
+    "ulm_fm_saved_path": (I, [SZ, I, I, I, I, I]),
     "ulm_fm_fwd_workspace_bytes": (SZ, [I, I, I, I, I]),
     "ulm_fm_fwd": (I, [P, P, I, P, P, P, P, I, P, SZ, P, SZ, I, I, I, I, P]),
     "ulm_fm_prefill_workspace_bytes": (SZ, [I, I, I, I, I, I]),
     "ulm_fm_prefill": (I, [P, P, I, P, P, P, P, I, P, P, P, SZ, I, I, I, I, P]),
-    "ulm_fm_bwd_workspace_bytes": (SZ, [I, I, I, I, I]),
+    "ulm_fm_bwd_workspace_bytes": (SZ, [I, I, I, I, I, SZ, I]),
     "ulm_fm_bwd": (I, [P, P, P, P, SZ, I, P, I, P, P, P, I, P, P, P, SZ, I, I, I, I, P]),
     "ulm_la_workspace_bytes": (SZ, [I, I, I, I]),
     "ulm_la": (I, [P, P, P, P, P, I, I, I, I, I, I, P, SZ, P]),

@@ -16,6 +16,8 @@ SHAPES = {
     "15M": dict(B=32, T=256, D=288, A=1152, blocks=1),
     "42M": dict(B=16, T=1024, D=512, A=2048, blocks=1),
     "110M": dict(B=16, T=1024, D=768, A=3072, blocks=12),
+    # the same widths and tokens per step in sequences of 8192 positions (the chunked state form's range)
+    "110M-T8192": dict(B=2, T=8192, D=768, A=3072, blocks=12),
     # the reference's own published single-block timings (docs/kernel.md:57-62,
     # RTX 3090 Ti): 1.56 ms at D=288, A=712, B=32, T=256 and 3.18 ms at D=512,
     # A=1280, B=8, T=1024

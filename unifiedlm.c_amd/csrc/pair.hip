@@ -1141,9 +1141,13 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, uint16_t *vQ, co
     a.g = g;
     a.a = r_mat(kR, NT, Ap);
     a.b = r_mat(qR, NT, Ap);
-    // the scores in 256 x 256 tiles where they tile Tq: twice the flops per
-    // operand byte of 128 x 128 tiles, whose k-steps are bound by the copies
-    const int Gs = Tq % 256 == 0 ? 256 : G;
+    // the scores in 256 x 256 tiles where they tile Tq and their jobs fill at
+    // least half the CUs: twice the flops per operand byte of 128 x 128 tiles,
+    // whose k-steps are bound by the copies (at B = 32, T = 256 one 256 tile per
+    // batch row would leave 224 of the 256 CUs idle: 34.5 us, against about
+    // 12 us in three 128 tiles per row)
+    const int n256 = Tq / 256;
+    const int Gs = Tq % 256 == 0 && B * n256 * (n256 + 1) / 2 >= 128 ? 256 : G;
     a.mt = a.nt = Tq / Gs;
     a.tri = 1;
     a.krange = K_FULL;

@@ -81,12 +81,14 @@ __global__ __launch_bounds__(256) void decode_addr_kernel(const float *__restric
     }
 }
 
-constexpr int kStateRows = 16;   // rows (features) per block, 4 per wave
+constexpr int kStateRows = 4;    // rows (features) per block, one per wave
+constexpr int kRowChunk = 12;    // 16-byte loads per lane in flight per row: 3072 slots in one pass
 
 // S[n, d, :] <- lam S + v[n, d] r_prev[n, :];  out[n, d] = x + S[n, d, :] . q[n, :] + ymu.
 // q and r_prev of the block's sequence are staged once in LDS; each wave
-// streams whole rows with 16-byte accesses and reduces its dot product with
-// cross-lane shuffles.
+// streams one whole row with 16-byte accesses, all of a pass's loads issued
+// before any of its stores (kRowChunk per lane: at A = 3072 the row's 12 KB
+// in flight at once), and reduces its dot product with cross-lane shuffles.
 template <bool VEC4>
 __global__ __launch_bounds__(256) void decode_state_kernel(float *__restrict__ S, const float *__restrict__ v,
                                                            const float *__restrict__ r_prev, const float *__restrict__ q,
@@ -104,37 +106,91 @@ __global__ __launch_bounds__(256) void decode_state_kernel(float *__restrict__ S
     __syncthreads();
     const float lam = __expf(g[0]);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int d0 = blockIdx.y * kStateRows;
-    for (int i = wave; i < kStateRows; i += 4) {
-        const int d = d0 + i;
-        if (d >= D) break;
-        float *Sr = S + (n * D + d) * static_cast<size_t>(A);
-        const float vd = v[n * D + d];
-        float acc = 0.f;
-        if (VEC4) {
-            // S is touched once per token: non-temporal 16-byte loads and stores
-            // keep it from evicting the staged and reused data in the caches
-            const int A4 = A / 4;
-            f32x4 *S4 = reinterpret_cast<f32x4 *>(Sr);
-            const f32x4 *q4 = reinterpret_cast<const f32x4 *>(sq);
-            const f32x4 *p4 = reinterpret_cast<const f32x4 *>(srp);
-#pragma unroll 4
-            for (int j = lane; j < A4; j += kWave) {
-                f32x4 s = __builtin_nontemporal_load(S4 + j);
-                const f32x4 rp = p4[j], qq = q4[j];
-                s = lam * s + vd * rp;
-                __builtin_nontemporal_store(s, S4 + j);
-                acc += s[0] * qq[0] + s[1] * qq[1] + s[2] * qq[2] + s[3] * qq[3];
+    const int d = blockIdx.y * kStateRows + wave;
+    if (d >= D) return;
+    float *Sr = S + (n * D + d) * static_cast<size_t>(A);
+    const float vd = v[n * D + d];
+    float acc = 0.f;
+    if (VEC4) {
+        // S is touched once per token: non-temporal 16-byte loads and stores
+        // keep it from evicting the staged and reused data in the caches
+        const int A4 = A / 4;
+        f32x4 *S4 = reinterpret_cast<f32x4 *>(Sr);
+        const f32x4 *q4 = reinterpret_cast<const f32x4 *>(sq);
+        const f32x4 *p4 = reinterpret_cast<const f32x4 *>(srp);
+        for (int base = 0; base < A4; base += kWave * kRowChunk) {
+            f32x4 sv[kRowChunk];
+#pragma unroll
+            for (int k = 0; k < kRowChunk; ++k) {
+                const int j = base + lane + kWave * k;
+                sv[k] = j < A4 ? __builtin_nontemporal_load(S4 + j) : f32x4{0.f, 0.f, 0.f, 0.f};
             }
-        } else {
-            for (int a = lane; a < A; a += kWave) {
-                const float s = lam * Sr[a] + vd * srp[a];
-                Sr[a] = s;
-                acc += s * sq[a];
+#pragma unroll
+            for (int k = 0; k < kRowChunk; ++k) {
+                const int j = base + lane + kWave * k;
+                if (j < A4) {
+                    const f32x4 rp = p4[j], qq = q4[j];
+                    const f32x4 s = lam * sv[k] + vd * rp;
+                    __builtin_nontemporal_store(s, S4 + j);
+                    acc += s[0] * qq[0] + s[1] * qq[1] + s[2] * qq[2] + s[3] * qq[3];
+                }
             }
         }
-        acc = wave_sum(acc);
-        if (lane == 0) out[n * D + d] = x[n * D + d] + acc + ymu[n * D + d];
+    } else {
+        for (int a = lane; a < A; a += kWave) {
+            const float s = lam * Sr[a] + vd * srp[a];
+            Sr[a] = s;
+            acc += s * sq[a];
+        }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) out[n * D + d] = x[n * D + d] + acc + ymu[n * D + d];
+}
+
+// decode_addr with 16-byte accesses, A % 4 == 0 and A <= 1024 R4: pre (+ bias)
+// is read once and its relu^2 kept in registers across the row sum
+template <int R4>
+__global__ __launch_bounds__(256) void decode_addr_vec_kernel(const float *__restrict__ pre, const float *__restrict__ bias,
+                                                              const float *__restrict__ log_eps, const float *__restrict__ w,
+                                                              const float *__restrict__ g, const float *__restrict__ r_prev,
+                                                              float *__restrict__ c, float *__restrict__ r,
+                                                              float *__restrict__ q, float *__restrict__ wq, int A) {
+    __shared__ float red[4];
+    const size_t row = static_cast<size_t>(blockIdx.x) * A;
+    const int A4 = A / 4;
+    const f32x4 *p4 = reinterpret_cast<const f32x4 *>(pre + row);
+    const f32x4 *b4 = reinterpret_cast<const f32x4 *>(bias);
+    f32x4 z[R4];
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < R4; ++k) {
+        const int j = threadIdx.x + 256 * k;
+        f32x4 p = j < A4 ? p4[j] : f32x4{0.f, 0.f, 0.f, 0.f};
+        if (bias && j < A4) p += b4[j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p[e] = p[e] > 0.f ? p[e] * p[e] : 0.f;
+        z[k] = p;
+        s += (p[0] + p[1]) + (p[2] + p[3]);
+    }
+    s = block_sum_256(s, red);
+    const float idn = 1.f / (__expf(fminf(fmaxf(log_eps[0], -10.f), 10.f)) + s);
+    const float lam = __expf(g[0]);
+    const f32x4 *w4 = reinterpret_cast<const f32x4 *>(w);
+    const f32x4 *rp4 = reinterpret_cast<const f32x4 *>(r_prev + row);
+    f32x4 *c4 = reinterpret_cast<f32x4 *>(c + row);
+#pragma unroll
+    for (int k = 0; k < R4; ++k) {
+        const int j = threadIdx.x + 256 * k;
+        if (j >= A4) break;
+        const f32x4 wa = w4[j], cn = lam * c4[j] + (1.f - lam) * wa + rp4[j];
+        const f32x4 ra = z[k] * idn;
+        f32x4 qa;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qa[e] = ra[e] / cn[e];
+        c4[j] = cn;
+        reinterpret_cast<f32x4 *>(r + row)[j] = ra;
+        reinterpret_cast<f32x4 *>(q + row)[j] = qa;
+        reinterpret_cast<f32x4 *>(wq + row)[j] = wa * qa;
     }
 }
 
@@ -156,8 +212,23 @@ extern "C" int ulm_decode_addr(const float *pre, const float *bias, const float 
                                int A, void *stream) {
     ULM_REQUIRE(N > 0 && A > 0, "ulm_decode_addr: bad sizes N=%d A=%d", N, A);
     ULM_REQUIRE(pre && log_eps && w && g && r_prev && c && r && q && wq, "ulm_decode_addr: null pointer");
-    decode_addr_kernel<<<dim3(N), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(pre, bias, log_eps, w, g, r_prev,
-                                                                                    c, r, q, wq, A);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    bool aligned = A % 4 == 0;
+    for (const void *t : {static_cast<const void *>(pre), static_cast<const void *>(bias), static_cast<const void *>(w),
+                          static_cast<const void *>(r_prev), static_cast<const void *>(c), static_cast<const void *>(r),
+                          static_cast<const void *>(q), static_cast<const void *>(wq)})
+        aligned = aligned && reinterpret_cast<uintptr_t>(t) % 16 == 0;
+    const int r4 = (A / 4 + 255) / 256;
+    if (aligned && r4 <= 4) {
+        switch (r4) {
+        case 1: decode_addr_vec_kernel<1><<<dim3(N), dim3(256), 0, s>>>(pre, bias, log_eps, w, g, r_prev, c, r, q, wq, A); break;
+        case 2: decode_addr_vec_kernel<2><<<dim3(N), dim3(256), 0, s>>>(pre, bias, log_eps, w, g, r_prev, c, r, q, wq, A); break;
+        case 3: decode_addr_vec_kernel<3><<<dim3(N), dim3(256), 0, s>>>(pre, bias, log_eps, w, g, r_prev, c, r, q, wq, A); break;
+        default: decode_addr_vec_kernel<4><<<dim3(N), dim3(256), 0, s>>>(pre, bias, log_eps, w, g, r_prev, c, r, q, wq, A); break;
+        }
+        return check_launch("decode_addr_vec_kernel");
+    }
+    decode_addr_kernel<<<dim3(N), dim3(256), 0, s>>>(pre, bias, log_eps, w, g, r_prev, c, r, q, wq, A);
     return check_launch("decode_addr_kernel");
 }
 

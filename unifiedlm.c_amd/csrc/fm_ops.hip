@@ -61,8 +61,10 @@ int launch_unpad_sum(const float *part, int nK, int B, int R, int Rp, int F, int
 // fm_stats.hip
 int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
                      uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, float *c_last, int B, int T,
-                     int A, hipStream_t s, void *qw = nullptr, int qw_dt = ULM_BF16, int AL = 0);
-size_t bwd_stats_partial_bytes(int B, int A);
+                     int A, hipStream_t s, void *qw = nullptr, int qw_dt = ULM_BF16, int AL = 0,
+                     float *segtot = nullptr);
+size_t fwd_stats_segtot_bytes(int B, int T, int A);
+size_t bwd_stats_partial_bytes(int B, int T, int A);
 int launch_bwd_stats(const float *dqf, const float *dqo, const RSrc &src, const float *nck,
                      const float *w, const float *g, const float *dkf, float *dr, float *dw, float *dg, void *part,
                      int B, int T, int A, hipStream_t s, const void *dqw = nullptr, int dqw_dt = ULM_BF16,
@@ -185,6 +187,7 @@ struct FwdWs {
     uint16_t *qR, *kR, *vQ;   // pair path: the forward's operand tiles
     float *part;   // fp32 output or partials
     float *state;  // chunked prefill at widths off the 32 grid: the padded state
+    float *segtot; // the statistics scan's segment totals (sequences past one segment)
     size_t bytes;
 };
 
@@ -211,6 +214,8 @@ FwdWs fwd_layout(void *base, int B, int T, int A, int D, int fast_dtype, Path pa
         if (fast_dtype != ULM_F32 || resid) w.part = c.take<float>(nd);
         if (la_generic_parts(A) > 1) w.gpart = c.take<float>(la_generic_parts(A) * nd);
     }
+    const size_t stb = fwd_stats_segtot_bytes(B, T, A);
+    if (stb) w.segtot = reinterpret_cast<float *>(c.take<char>(stb));
     w.bytes = c.off;
     return w;
 }
@@ -263,7 +268,7 @@ BwdWs bwd_layout(void *base, int B, int T, int A, int D, int dfast_dtype, Path p
                                    la_generic_parts(A) > 1 ? la_generic_parts(A) * nd : 0);
         if (gp) w.gpart = c.take<float>(gp);
     }
-    if (path != PATH_PAIR) w.stats = c.take<char>(bwd_stats_partial_bytes(B, A));
+    if (path != PATH_PAIR) w.stats = c.take<char>(bwd_stats_partial_bytes(B, T, A));
     w.bytes = c.off;
     return w;
 }
@@ -391,7 +396,7 @@ int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const 
         // backward's dscores. bf16 v with D % 64 == 0 is tiled by the scores
         // launch, on the CUs its tiles leave idle; other v by a launch of its own.
         ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, ws.qR, ws.kR, sv.qQ, sv.kQ, sv.nck, nullptr, B, T, A, s,
-                                 qw, qw_dt, pad32(A)));
+                                 qw, qw_dt, pad32(A), ws.segtot));
         const bool ride = v_dtype == ULM_BF16 && D % 64 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0;
         if (!ride) ULM_TRY(launch_chunk_transpose(v, v_dtype, ws.vQ, nullptr, sv.vR, nullptr, B, T, D, s, pad32(D)));
         return launch_pair_forward(ws.qR, ws.kR, ws.vQ, g, sv.P, sv.Pt, sv.Plo, fast, fast_dtype, resid, B, T, A, D, s,
@@ -407,7 +412,7 @@ int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const 
         // a prefill (state wanted) has no backward, the only reader of q in the Q
         // layout and of v in the R layout: those tiles are not written then
         ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, sv.qR, sv.kR, state ? nullptr : sv.qQ, sv.kQ, sv.nck,
-                                 c_last, B, T, A, s, qw, qw_dt, Ap));
+                                 c_last, B, T, A, s, qw, qw_dt, Ap, ws.segtot));
         ULM_TRY(launch_chunk_transpose(v, v_dtype, sv.vQ, sv.vQl, state ? nullptr : sv.vR, state ? nullptr : sv.vRl, B,
                                        T, D, s, Dp));
         ULM_TRY(launch_chunk_scores(sv.qR, nullptr, sv.kR, nullptr, g, ws.Pf, sv.Pdv, B, T, Ap, true, s));
@@ -427,7 +432,7 @@ int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const 
     }
     if (state || c_last) return fail(ULM_ERR_UNSUPPORTED, "prefill state: not on the generic path");
     ULM_TRY(launch_fwd_stats(r, w, g, q, sv.q16n, sv.k16n, nullptr, nullptr, nullptr, nullptr, sv.nck, nullptr, B, T, A,
-                             s, qw, qw_dt));
+                             s, qw, qw_dt, 0, ws.segtot));
     ULM_TRY(launch_convert(v, v_dtype, sv.v16n, ULM_BF16, nf, s));
     float *acc = ws.part ? ws.part : static_cast<float *>(fast);
     ULM_TRY(launch_la_generic(sv.q16n, sv.k16n, sv.v16n, g, acc, ws.gpart, B, T, A, D, false, s));

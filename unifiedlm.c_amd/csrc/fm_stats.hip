@@ -20,17 +20,39 @@
 // (carry_j = lam^16 carry_{j-1} + total_{j-1}). Instead of the full c tensor
 // the forward saves n at every chunk start (B x ceil(T/64) x A); the backward
 // rebuilds c inside each chunk from it.
+//
+// Sequence segments: a workgroup scans the chunks of one segment of
+// kSegChunks chunks (1024 positions), so that a long sequence over few batch
+// rows still spreads over the CUs. The values carried into a segment come
+// from a totals pass over the segments that precede it (forward) or follow it
+// (backward), folded by each workgroup in a fixed order. The segment length
+// is fixed, so a row's arithmetic does not depend on the batch size; a
+// sequence of one segment has no totals pass and nothing carried in.
 #include "ulm_common.h"
+
+#include <type_traits>
 
 namespace ulm {
 
 constexpr int kSeg = 16;      // positions per thread segment
 constexpr int kSlots = 64;    // slots per block
+constexpr int kSegChunks = 16;                   // chunks per sequence segment
+constexpr int kSegLen = kSegChunks * ULM_CHUNK;  // positions per sequence segment
+
+int stat_segments(int T) {
+    const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
+    return (NT + kSegChunks - 1) / kSegChunks;
+}
 
 __device__ __forceinline__ float pow_int(float x, int e) {
     float r = 1.f;
     for (int i = 0; i < e; ++i) r *= x;
     return r;
+}
+// x^(2^k) by k squarings
+__device__ __forceinline__ float pow_2k(float x, int k) {
+    for (int i = 0; i < k; ++i) x *= x;
+    return x;
 }
 
 // Sources of r for the kernels below (RSrc). raw(row, ac, A) loads the stored
@@ -122,6 +144,49 @@ int with_rsrc(const RSrc &src, F &&f) {
     return fail(ULM_ERR_INVALID, "stats: bad pre dtype %d", src.pre_dt);
 }
 
+// The forward's segment totals: tot[b][j][a], for the segments j < S - 1, is n
+// at the last position of segment j with n = 0 before the segment
+// (n_t = lam n_{t-1} + k_t). A workgroup of 16 waves takes 64 slots of one
+// segment, wave w its chunk w: each lane walks the chunk's 64 positions in
+// order, 16 loads in flight, and the chunks join as
+// (((p_0 lam^64 + p_1) lam^64 + p_2) ...) lam^64 + p_15.
+template <class RS>
+__global__ __launch_bounds__(1024) void fwd_segtot_kernel(RS rs, const float *__restrict__ g,
+                                                          float *__restrict__ tot, int T, int A, int S) {
+    __shared__ float part[kSegChunks][kSlots];
+    const int s = threadIdx.x % kSlots;
+    const int u = __builtin_amdgcn_readfirstlane(threadIdx.x / kSlots);   // the wave's chunk in the segment
+    const int a = blockIdx.x * kSlots + s;
+    const bool va = a < A;
+    const uint32_t ac = va ? a : 0;
+    const size_t b = blockIdx.y;
+    const int j = blockIdx.z;
+    const float lam = __expf(g[0]);
+    const float rb = va ? rs.slot_const(a) : 0.f;
+    const int t0 = j * kSegLen + u * ULM_CHUNK;
+    float n = 0.f;
+    for (int i0 = 0; i0 < ULM_CHUNK; i0 += kSeg) {
+        float kv[kSeg];
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) {
+            const int t = t0 + i0 + i - 1;   // k at position t + 1 is r at t
+            const bool tok = t >= 0 && t < T;
+            const float inv = seg_inv<RS>(rs.row_raw(urow(b, t, T), tok));
+            kv[i] = rs.at(urow(b, t, T), ac, A, rb, inv, va && tok);
+        }
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) n = lam * n + kv[i];
+    }
+    part[u][s] = n;
+    __syncthreads();
+    if (u == 0 && va) {
+        const float l64 = pow_2k(lam, 6);   // lam^64
+        float acc = part[0][s];
+        for (int m = 1; m < kSegChunks; ++m) acc = l64 * acc + part[m][s];
+        tot[(b * S + j) * A + a] = acc;
+    }
+}
+
 // Outputs besides n_ckpt (each may be null): q (fp32); qw = w q in qw_dt; q16n, k16n natural bf16
 // copies; qR, kR in the R layout and qQ, kQ in the Q layout (the products'
 // operand tiles, AL slots wide: AL % 32 == 0, A <= AL <= the grid's slots);
@@ -136,7 +201,8 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
                                                         uint16_t *__restrict__ qR, uint16_t *__restrict__ kR,
                                                         uint16_t *__restrict__ qQ, uint16_t *__restrict__ kQ,
                                                         float *__restrict__ nck, float *__restrict__ c_last, int T,
-                                                        int A, int AL, int NT) {
+                                                        int A, int AL, int NT, const float *__restrict__ segtot,
+                                                        int S) {
     __shared__ float tot[4][kSlots];
     __shared__ __align__(16) uint16_t sq[ULM_CHUNK][kSlots + 8], sk[ULM_CHUNK][kSlots + 8];   // [position][slot]
     const int s = threadIdx.x % kSlots;
@@ -151,7 +217,15 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
     const float lam16 = pow_int(lam, kSeg);
     const float wa = va ? w[a] : 1.f;
     const float rb = va ? rs.slot_const(a) : 0.f;   // the slot's key bias when r is formed here
+    // this workgroup's sequence segment: chunks n0 .. n1 - 1, n carried in from
+    // the totals of the segments before it
+    const int seg = blockIdx.z;
+    const int n0 = seg * kSegChunks, n1 = min(NT, n0 + kSegChunks);
     float carry = 0.f;   // n at the position before the chunk
+    if (seg > 0) {
+        const float lamL = pow_2k(lam, 10);   // lam^1024, across one segment
+        for (int i = 0; i < seg; ++i) carry = lamL * carry + (va ? segtot[(bs * S + i) * A + a] : 0.f);
+    }
     // the stored elements of a chunk's positions t0 .. t0+15 and t0 - 1, and
     // their denominators, loaded two chunks ahead into alternating buffers
     typename RS::raw_t pv[2][kSeg + 1];
@@ -163,8 +237,8 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
         for (int i = 0; i < kSeg; ++i) pv[u][i] = rs.raw(urow(bs, t0 + i, T), ac, A);
         pv[u][kSeg] = rs.raw(urow(bs, t0 - 1, T), ac, A);
     };
-    fetch(0, 0);
-    if (NT > 1) fetch(1, 1);
+    fetch(n0, 0);
+    if (n0 + 1 < n1) fetch(n0 + 1, 1);
     auto chunk = [&](int n, int u) {
         const int t0 = n * ULM_CHUNK + j * kSeg;
         const float seg_c = seg_inv<RS>(pd[u]);
@@ -172,7 +246,7 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) rv[i] = rs.make(pv[u][i], rb, lane_value(seg_c, i), va && t0 + i < T);
         kv[0] = rs.make(pv[u][kSeg], rb, lane_value(seg_c, kSeg), va && t0 >= 1 && t0 - 1 < T);
-        if (n + 2 < NT) fetch(n + 2, u);
+        if (n + 2 < n1) fetch(n + 2, u);
 #pragma unroll
         for (int i = 1; i < kSeg; ++i) kv[i] = rv[i - 1];
         float acc = 0.f;
@@ -248,9 +322,9 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
         }
         __syncthreads();   // sq, sk read before the next chunk writes them
     };
-    for (int n = 0; n < NT; n += 2) {
+    for (int n = n0; n < n1; n += 2) {
         chunk(n, 0);
-        if (n + 1 < NT) chunk(n + 1, 1);
+        if (n + 1 < n1) chunk(n + 1, 1);
     }
 }
 
@@ -264,6 +338,87 @@ __device__ __forceinline__ float load_xq(const void *p, size_t ro, uint32_t ac) 
     else return 0.f;
 }
 
+// The backward's segment totals: tot[b][j][a], for the segments j >= 1, is
+// the sum over the segment's positions t of lam^(t - t_j) dc_t (t_j its first
+// position): dkc at t_j with nothing carried in from later positions. A
+// workgroup of 16 waves takes 64 slots of one segment, wave w its chunk w:
+// each lane rebuilds n from the chunk's checkpoint and walks the chunk's 64
+// positions in order with the operations of bwd_stats_kernel for c, q and dc;
+// the chunks join as p_0 + lam^64 (p_1 + lam^64 (p_2 + ... + lam^64 p_15)).
+template <int XQ, class RS>
+__global__ __launch_bounds__(1024) void bwd_segtot_kernel(const float *__restrict__ dqf, const void *__restrict__ xq,
+                                                          RS rs, const float *__restrict__ nck,
+                                                          const float *__restrict__ w, const float *__restrict__ g,
+                                                          float *__restrict__ tot, int T, int A, int NT, int S) {
+    __shared__ float part[kSegChunks][kSlots];
+    const int s = threadIdx.x % kSlots;
+    const int u = __builtin_amdgcn_readfirstlane(threadIdx.x / kSlots);   // the wave's chunk in the segment
+    const int a = blockIdx.x * kSlots + s;
+    const bool va = a < A;
+    const uint32_t ac = va ? a : 0;
+    const size_t b = blockIdx.y;
+    const int j = blockIdx.z + 1;
+    const float lam = __expf(g[0]);
+    const float wa = va ? w[a] : 1.f;
+    const float rb = va ? rs.slot_const(a) : 0.f;
+    float R = 0.f, pw = 1.f;   // pw = lam^(t - the chunk's first position)
+    // the wave's chunk, none past the sequence (written as a loop: this
+    // compiler rejects the uniform row addresses below under an if)
+    const int c0 = j * kSegChunks + u;
+    for (int c = c0; c < min(NT, c0 + 1); ++c) {
+        float n = va ? nck[(b * NT + c) * A + a] : 0.f;
+        for (int i0 = 0; i0 < ULM_CHUNK; i0 += kSeg) {
+            const int tb = c * ULM_CHUNK + i0;
+            // every load of the 16 positions is issued before any arithmetic
+            // (the barrier keeps the scheduler from interleaving them, which
+            // left one load in flight at a time)
+            typename RS::raw_t pv[kSeg + 1];
+            float pd[kSeg + 1], fv[kSeg], xv[kSeg];
+#pragma unroll
+            for (int i = 0; i <= kSeg; ++i) {
+                const int t = tb + i - 1;   // pv[i]: position tb + i - 1
+                pd[i] = rs.row_raw(urow(b, t, T), t >= 0 && t < T);
+                pv[i] = rs.raw(urow(b, t, T), ac, A);
+            }
+#pragma unroll
+            for (int i = 0; i < kSeg; ++i) {
+                const size_t ro = urow(b, tb + i, T) * A;
+                fv[i] = ld_row(dqf + ro, 4u * ac);
+                xv[i] = XQ != 0 ? load_xq<XQ>(xq, ro, ac) : 0.f;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            float rv[kSeg + 1], dqv[kSeg];
+#pragma unroll
+            for (int i = 0; i <= kSeg; ++i) {
+                const int t = tb + i - 1;
+                rv[i] = rs.make(pv[i], rb, seg_inv<RS>(pd[i]), va && t >= 0 && t < T);
+            }
+#pragma unroll
+            for (int i = 0; i < kSeg; ++i) {
+                const float dq = fv[i] + (XQ == 1 ? xv[i] : wa * xv[i]);
+                dqv[i] = va && tb + i < T ? dq : 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < kSeg; ++i) {
+                n = lam * n + rv[i];
+                const float ct = wa + n;
+                const float qt = rv[i + 1] / ct;
+                const float dc = -(dqv[i] * qt) * __builtin_amdgcn_rcpf(ct);
+                R += pw * dc;
+                pw *= lam;
+            }
+        }
+    }
+    part[u][s] = R;
+    __syncthreads();
+    if (u == 0 && va) {
+        const float l64 = pow_2k(lam, 6);   // lam^64
+        float acc = part[kSegChunks - 1][s];
+        for (int m = kSegChunks - 2; m >= 0; --m) acc = part[m][s] + l64 * acc;
+        tot[(b * S + j) * A + a] = acc;
+    }
+}
+
 template <int XQ, class RS>
 __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict__ dqf, const void *__restrict__ xq,
                                                         RS rs,
@@ -271,7 +426,7 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
                                                         const float *__restrict__ g, const float *__restrict__ dkf,
                                                         float *__restrict__ dr, float *__restrict__ dw_part,
                                                         double *__restrict__ dg_part, int T, int A, int NT,
-                                                        int fast_dg) {
+                                                        int fast_dg, const float *__restrict__ segtot, int S) {
     __shared__ float tot[4][kSlots];
     __shared__ float first_dkt[4][kSlots];
     __shared__ float dw_sh[4][kSlots];
@@ -287,11 +442,23 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
     const float wa = va ? w[a] : 1.f;
     const float rb = va ? rs.slot_const(a) : 0.f;   // the slot's key bias when r is formed here
     const double tau = 0.5 * (T - 1);
+    // this workgroup's sequence segment: chunks n1 - 1 down to n0, dkc carried
+    // in from the totals of the segments after it
+    const int seg = blockIdx.z;
+    const int n0 = seg * kSegChunks, n1 = min(NT, n0 + kSegChunks);
     float dkc_next = 0.f;   // dkc at the first position after the chunk
     float dkt_next = 0.f;   // dkt at the first position after the chunk
+    if (seg + 1 < S) {
+        const float lamL = pow_2k(lam, 10);   // lam^1024, across one segment
+        float d = 0.f;
+        for (int i = S - 1; i > seg; --i) d = (va ? segtot[(b * S + i) * A + a] : 0.f) + lamL * d;
+        dkc_next = d;
+        // the next segment's first position is inside the sequence
+        dkt_next = va ? ld_row(dkf + (b * T + n1 * ULM_CHUNK) * A, 4u * ac) + d : 0.f;
+    }
     float dw_acc = 0.f;
     double dg_acc = 0.0;
-    for (int n = NT - 1; n >= 0; --n) {
+    for (int n = n1 - 1; n >= n0; --n) {
         const int t0 = n * ULM_CHUNK + j * kSeg;
         const float seg_c = seg_inv<RS>(seg_row_raw(rs, b * T + t0, t0, T, s));
         // xv: the extra gradient of q (dq_out or d(w q), by XQ); dq is formed
@@ -404,14 +571,15 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(const float *__restrict_
     dg_acc = wave_sum(dg_acc);
     if (threadIdx.x % kWave == 0) dg_sh[threadIdx.x / kWave] = dg_acc;
     __syncthreads();
-    if (j == 0 && va) dw_part[b * A + a] = dw_sh[0][s] + dw_sh[1][s] + dw_sh[2][s] + dw_sh[3][s];
-    if (threadIdx.x == 0) dg_part[b * gridDim.x + blockIdx.x] = dg_sh[0] + dg_sh[1] + dg_sh[2] + dg_sh[3];
+    const size_t pr = static_cast<size_t>(seg) * gridDim.y + b;   // partial row (segment, batch row)
+    if (j == 0 && va) dw_part[pr * A + a] = dw_sh[0][s] + dw_sh[1][s] + dw_sh[2][s] + dw_sh[3][s];
+    if (threadIdx.x == 0) dg_part[pr * gridDim.x + blockIdx.x] = dg_sh[0] + dg_sh[1] + dg_sh[2] + dg_sh[3];
 }
 
-// dw[a] = sum_b dw_part[b, a]; dg = sum of all dg partials (those of the
-// statistics and, when given, nextra more). Every sum runs in a fixed order
-// (thread-strided partial sums, then a fixed shuffle tree), so the result does
-// not depend on scheduling.
+// dw[a] = sum over the B partial rows (segment, batch row) of dw_part[row][a];
+// dg = the sum of all dg partials (those of the statistics and, when given,
+// nextra more). Every sum runs in a fixed order (thread-strided partial sums,
+// then a fixed shuffle tree), so the result does not depend on scheduling.
 __global__ __launch_bounds__(256) void stats_reduce_kernel(const float *__restrict__ dw_part,
                                                            const double *__restrict__ dg_part,
                                                            const double *__restrict__ dg_extra, float *__restrict__ dw,
@@ -438,9 +606,11 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(const float *__restri
 // copies AL slots wide (0: AL = A; AL % 32 == 0, the slots past A zero).
 int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
                      uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, float *c_last, int B, int T,
-                     int A, hipStream_t s, void *qw, int qw_dt, int AL) {
+                     int A, hipStream_t s, void *qw, int qw_dt, int AL, float *segtot) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
+    const int S = stat_segments(T);
     if ((q16n == nullptr) != (k16n == nullptr)) return fail(ULM_ERR_INVALID, "fwd stats: q16n and k16n go together");
+    if (S > 1 && !segtot) return fail(ULM_ERR_INVALID, "fwd stats: %d sequence segments need their totals array", S);
     // the tiled copies: kQ always, qR and kR together (the chunked products'
     // R layout), qQ when a backward follows
     const bool tiled = qR || kR || qQ || kQ;
@@ -453,10 +623,14 @@ int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, 
     const int qwk = qw ? qw_dt : -1;
     return with_rsrc(src, [&](auto rs) {
         using RS = decltype(rs);
-        const dim3 grid((A + kSlots - 1) / kSlots, B);
+        if (S > 1) {
+            fwd_segtot_kernel<RS><<<dim3((A + kSlots - 1) / kSlots, B, S - 1), 1024, 0, s>>>(rs, g, segtot, T, A, S);
+            ULM_TRY(check_launch("fwd_segtot_kernel"));
+        }
+        const dim3 grid((A + kSlots - 1) / kSlots, B, S);
 #define ULM_FWD_STATS(QWK, HQ)                                                                                    \
     fwd_stats_kernel<RS, QWK, HQ><<<grid, 256, 0, s>>>(rs, w, g, q, qw, qw_dt, q16n, k16n, qR, kR, qQ, kQ, nck,   \
-                                                       c_last, T, A, AL, NT)
+                                                       c_last, T, A, AL, NT, segtot, S)
         if (q) {
             switch (qwk) {
             case ULM_F32: ULM_FWD_STATS(ULM_F32, true); break;
@@ -477,9 +651,18 @@ int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, 
     });
 }
 
-size_t bwd_stats_partial_bytes(int B, int A) {
-    const size_t nb = (A + kSlots - 1) / kSlots;
-    return align_up(static_cast<size_t>(B) * A * sizeof(float), 256) + align_up(B * nb * sizeof(double), 256);
+// The forward's segment totals (none for a sequence of one segment).
+size_t fwd_stats_segtot_bytes(int B, int T, int A) {
+    const int S = stat_segments(T);
+    return S > 1 ? align_up(static_cast<size_t>(B) * S * A * sizeof(float), 256) : 0;
+}
+
+// The backward's partial sums: dw per (segment, batch row, slot), dg per
+// (segment, batch row, slot block), then the segment totals.
+size_t bwd_stats_partial_bytes(int B, int T, int A) {
+    const size_t nb = (A + kSlots - 1) / kSlots, rows = static_cast<size_t>(B) * stat_segments(T);
+    return align_up(rows * A * sizeof(float), 256) + align_up(rows * nb * sizeof(double), 256) +
+           fwd_stats_segtot_bytes(B, T, A);
 }
 
 // dg_extra: nextra more partials of dg (the block-pair products' fast-read
@@ -490,10 +673,12 @@ int launch_bwd_stats(const float *dqf, const float *dqo, const RSrc &src, const 
                      int B, int T, int A, hipStream_t s, const void *dqw, int dqw_dt, const double *dg_extra,
                      int nextra) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
-    const int nb = (A + kSlots - 1) / kSlots;
+    const int nb = (A + kSlots - 1) / kSlots, S = stat_segments(T);
+    const size_t rows = static_cast<size_t>(B) * S;   // partial rows: (segment, batch row)
     float *dw_part = static_cast<float *>(part);
-    double *dg_part = reinterpret_cast<double *>(static_cast<char *>(part) +
-                                                 align_up(static_cast<size_t>(B) * A * sizeof(float), 256));
+    double *dg_part = reinterpret_cast<double *>(static_cast<char *>(part) + align_up(rows * A * sizeof(float), 256));
+    float *segtot = reinterpret_cast<float *>(reinterpret_cast<char *>(dg_part) +
+                                              align_up(rows * nb * sizeof(double), 256));
     const int xq = dqw ? 2 + dqw_dt : (dqo ? 1 : 0);   // ULM_F32, ULM_BF16, ULM_F16 = 0, 1, 2
     const void *xp = dqw ? dqw : static_cast<const void *>(dqo);
     if (dqw && dqo) return fail(ULM_ERR_INVALID, "bwd stats: dq_out and d(w q) are exclusive");
@@ -501,20 +686,27 @@ int launch_bwd_stats(const float *dqf, const float *dqo, const RSrc &src, const 
     const int fast_dg = dg_extra ? 0 : 1;
     ULM_TRY(with_rsrc(src, [&](auto rs) {
         using RS = decltype(rs);
-        const dim3 grid(nb, B);
+        const dim3 tgrid(nb, B, S - 1), grid(nb, B, S);
+        auto run = [&](auto xk) {
+            constexpr int XQ = decltype(xk)::value;
+            if (S > 1) {
+                bwd_segtot_kernel<XQ, RS><<<tgrid, 1024, 0, s>>>(dqf, xp, rs, nck, w, g, segtot, T, A, NT, S);
+                ULM_TRY(check_launch("bwd_segtot_kernel"));
+            }
+            bwd_stats_kernel<XQ, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT,
+                                                          fast_dg, segtot, S);
+            return check_launch("bwd_stats_kernel");
+        };
         switch (xq) {
-        case 0: bwd_stats_kernel<0, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT, fast_dg); break;
-        case 1: bwd_stats_kernel<1, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT, fast_dg); break;
-        case 2: bwd_stats_kernel<2, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT, fast_dg); break;
-        case 3: bwd_stats_kernel<3, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT, fast_dg); break;
-        default: bwd_stats_kernel<4, RS><<<grid, 256, 0, s>>>(dqf, xp, rs, nck, w, g, dkf, dr, dw_part, dg_part, T, A, NT, fast_dg); break;
+        case 0: return run(std::integral_constant<int, 0>{});
+        case 1: return run(std::integral_constant<int, 1>{});
+        case 2: return run(std::integral_constant<int, 2>{});
+        case 3: return run(std::integral_constant<int, 3>{});
+        default: return run(std::integral_constant<int, 4>{});
         }
-        return ULM_OK;
     }));
-    int st = check_launch("bwd_stats_kernel");
-    if (st) return st;
-    stats_reduce_kernel<<<(A + 255) / 256, 256, 0, s>>>(dw_part, dg_part, dg_extra, dw, dg, B, A, B * nb,
-                                                        dg_extra ? nextra : 0);
+    stats_reduce_kernel<<<(A + 255) / 256, 256, 0, s>>>(dw_part, dg_part, dg_extra, dw, dg, static_cast<int>(rows), A,
+                                                        static_cast<int>(rows) * nb, dg_extra ? nextra : 0);
     return check_launch("stats_reduce_kernel");
 }
 

@@ -97,6 +97,9 @@ def parse():
     p.add_argument("--no-step", action="store_true")
     p.add_argument("--no-configs", action="store_true")
     p.add_argument("--no-chunked", action="store_true")
+    p.add_argument("--only", choices=("block", "step"),
+                   help="profiling: run one leg alone (the fused block leg without its op-by-op pass, or the "
+                        "training step) and print its record instead of the benchmark line")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                    help="first run one plain fp32 copy kernel over MB megabytes (a known-size reference for "
                         "hardware byte counters)")
@@ -261,7 +264,7 @@ def bench_configs(torch, args):
     return out
 
 
-def bench_block(torch, args):
+def bench_block(torch, args, composed=True):
     """Whole UnifiedBlocks (model.py:77-85) forward + backward over the training
     workload's shape under bf16 autocast: the fused block and the op-by-op
     path (forward_composed) on the same weights and input."""
@@ -299,16 +302,19 @@ def bench_block(torch, args):
         return (time.perf_counter() - t0) * 1e3 / args.steps
 
     ms = timed(True)
-    ms_c = timed(False)
     import ulm_native
     path = fm_path_name(ulm_native.lib().ulm_fm_path(B, T, A, D))
     ftok = workloads.block_flops_per_token(T, A, D, path=path) * L
+    rec = {"workload": f"UnifiedBlock fwd+bwd, {L} blocks of the {args.shape} shape, bf16 autocast",
+           "ms_per_step": round(ms, 3), "Mtok_per_s": round(B * T / (ms * 1e-3) / 1e6, 4),
+           "tflops": round(ftok * B * T / (ms * 1e-3) / 1e12, 2)}
+    if not composed:
+        log(f"block step {ms:.2f} ms fused")
+        return rec
+    ms_c = timed(False)
     log(f"block step {ms:.2f} ms fused, {ms_c:.2f} ms op by op")
-    return {"workload": f"UnifiedBlock fwd+bwd, {L} blocks of the {args.shape} shape, bf16 autocast",
-            "ms_per_step": round(ms, 3), "Mtok_per_s": round(B * T / (ms * 1e-3) / 1e6, 4),
-            "tflops": round(ftok * B * T / (ms * 1e-3) / 1e12, 2),
-            "composed_ms_per_step": round(ms_c, 3), "composed_Mtok_per_s": round(B * T / (ms_c * 1e-3) / 1e6, 4),
-            "speedup_vs_composed": round(ms_c / ms, 3)}
+    return {**rec, "composed_ms_per_step": round(ms_c, 3),
+            "composed_Mtok_per_s": round(B * T / (ms_c * 1e-3) / 1e6, 4), "speedup_vs_composed": round(ms_c / ms, 3)}
 
 
 def bench_train_step(torch, args):
@@ -549,6 +555,10 @@ def main():
         torch.cuda.synchronize()
         log(f"copy probe: {4 * n} bytes read, {4 * n} bytes written")
         del x, y
+    if args.only:
+        rec = bench_block(torch, args, composed=False) if args.only == "block" else bench_train_step(torch, args)
+        print(json.dumps({"leg": args.only, "steps": args.steps, "warmup": args.warmup, **rec}), flush=True)
+        return
     train = bench_training(torch, args)
     configs = None if args.no_configs else bench_configs(torch, args)
     chunked = None if args.no_chunked else bench_chunked(torch, args)

@@ -888,20 +888,41 @@ __global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI, OU
         const rsrc_t ro = rsrc(static_cast<char *>(p.out) + row0 * ES, nbytes);
         const rsrc_t rr = rsrc(OUT >= 3 ? reinterpret_cast<const char *>(p.resid + row0) : static_cast<const char *>(p.out),
                                static_cast<uint32_t>(p.T) * p.F * 4);
-#pragma unroll
-        for (int j = 0; j < NI; ++j) {
+        // element (i, j, r) of this lane, and OOB in bad when it lies outside the tensor
+        auto elem = [&](int i, int j, int r, uint32_t &bad) -> uint32_t {
             const int n = n0 + wn * (TN / 2) + 32 * j + lc;
             const int f = p.nperm ? (n & ~31) + perm32(n & 31) : n;
-            const bool fok = f < p.F;
+            const int pos = m0 + wm * (TM / WM) + 32 * i + 8 * (r / 4) + 4 * h + r % 4;
+            bad = (f < p.F && pos < p.T) ? 0u : OOB;
+            return static_cast<uint32_t>(pos) * p.F + f;
+        };
+        // Every residual load is issued before the first store: as far as the
+        // compiler knows a store may alias the residual, so interleaved, each
+        // load would wait for the store before it to complete.
+        float res[OUT >= 3 ? MI : 1][NI][16];
+        if constexpr (OUT >= 3) {
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        uint32_t bad;
+                        const uint32_t el = elem(i, j, r, bad);
+                        res[i][j][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                     rr, (4u * el) | bad, 0, 0));
+                    }
+        }
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int pos = m0 + wm * (TM / WM) + 32 * i + 8 * (r / 4) + 4 * h + r % 4;
-                    const uint32_t el = static_cast<uint32_t>(pos) * p.F + f;
-                    const uint32_t bad = (fok && pos < p.T) ? 0u : OOB;
+                    uint32_t bad;
+                    const uint32_t el = elem(i, j, r, bad);
                     float v = acc[i][j][r];
-                    if constexpr (OUT >= 3) v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, (4u * el) | bad, 0, 0));
+                    if constexpr (OUT >= 3) v += res[i][j][r];
                     if constexpr (DT == ULM_F32) {
                         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ro, (4u * el) | bad, 0, 0);
                     } else {

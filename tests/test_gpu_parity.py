@@ -271,6 +271,44 @@ def test_address_matches_oracle(pdt, log_eps):
         assert l64.grad.item() != 0.0 and rel(lg.grad, l64.grad) < 1e-5
 
 
+@pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("A", [1800, 3072, 4000, 4400, 702])
+@pytest.mark.parametrize("with_r", [True, False])
+def test_address_backward_widths(pdt, A, with_r):
+    """ulm_addr_bwd over row widths that take each of its forms: rows of up to
+    8, 12 and 16 steps of 256 slots kept in registers between its two passes
+    (1800, 3072, 4000), a row read twice (4400), and the scalar form (702, not
+    a multiple of 4); with r given, and with r formed from pre, bias and the
+    denominators as the block's backward calls it. Against the oracle's
+    address in float64."""
+    say(f"address backward A={A} {pdt} r {'given' if with_r else 'formed'}")
+    gen = torch.Generator().manual_seed(A)
+    M = 96
+    pre = torch.randn(M, A, generator=gen).to(pdt)
+    bias = torch.randn(A, generator=gen) * 0.5
+    le = torch.tensor([0.3])
+    dr = torch.randn(M, A, generator=gen)
+    pc, bc, lc, drc = pre.cuda(), bias.cuda(), le.cuda(), dr.cuda()
+    r, denom = kernel.addr_fwd(pc, bc, lc)
+    dpre = torch.empty_like(pc)
+    dbias = torch.empty(A, device="cuda")
+    dle = torch.empty(1, device="cuda")
+    wsb = nat.lib().ulm_addr_bwd_workspace_bytes(M, A)
+    ws = torch.empty(wsb, device="cuda", dtype=torch.uint8)
+    nat.call("ulm_addr_bwd", pc.data_ptr(), nat.dtype_code(pdt), bc.data_ptr(), lc.data_ptr(),
+                r.data_ptr() if with_r else None, denom.data_ptr(), drc.data_ptr(), dpre.data_ptr(),
+                dbias.data_ptr(), dle.data_ptr(), ws.data_ptr(), wsb, M, A, nat.stream_of(pc))
+    torch.cuda.synchronize()
+    p64 = pre.double().requires_grad_(True)
+    b64 = bias.double().requires_grad_(True)
+    l64 = le.double().reshape(()).requires_grad_(True)
+    (fm.address(p64 + b64, l64) * dr.double()).sum().backward()
+    tol = 1e-5 if pdt == torch.float32 else 1e-2
+    assert rel(dpre.double().cpu(), p64.grad) < tol
+    assert rel(dbias.cpu(), b64.grad) < 1e-5
+    assert rel(dle.cpu().reshape(()), l64.grad) < 1e-5
+
+
 def _decode_model(seed=0, **kw):
     return tiny_model(seed, **kw).cuda()
 

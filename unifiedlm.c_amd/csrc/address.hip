@@ -128,8 +128,11 @@ __global__ __launch_bounds__(kAddrWaves * 64) void addr_fwd_kernel(const T *__re
 // One wave per row: rho = sum_a dr r by a wave reduction, then dpre. Each wave
 // keeps its dbias column partials in its own LDS row; the block writes their
 // sum as one partial row, and the dlog_eps partial. Without HAS_R, r is formed
-// from pre, bias and denom with the forward's operations.
-template <typename T, int W, bool HAS_R>
+// from pre, bias and denom with the forward's operations. With NS > 0 (rows of
+// at most NS W 64 slots) the row's relu(pre + b) and dr stay in registers
+// between the two passes, so each is read from memory once; with NS = 0 the
+// second pass reads them again.
+template <typename T, int W, bool HAS_R, int NS = 0>
 __global__ __launch_bounds__(kAddrWaves * 64) void addr_bwd_kernel(const T *__restrict__ pre,
                                                                    const float *__restrict__ bias,
                                                                    const float *__restrict__ log_eps,
@@ -151,6 +154,58 @@ __global__ __launch_bounds__(kAddrWaves * 64) void addr_bwd_kernel(const T *__re
         const float dn = denom[row];
         const float inv = 1.f / dn;
         float rho = 0.f;
+        if constexpr (NS > 0) {
+            // every load of the row first, unconditional at a clamped slot (a
+            // load in a branch is waited for before the branch ends), the
+            // slots past A masked to zero after
+            float ps[NS][W], xs[NS][W];
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+                const int a = W * lane + k * W * kWave, ac = a < A ? a : 0;
+                relu_row<T, W>(pre, bias, base, ac, ps[k]);
+                Vec<float, W>::ld(dr, base + ac, xs[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < NS; ++k)
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    const bool ok = W * lane + k * W * kWave < A;
+                    ps[k][e] = ok ? ps[k][e] : 0.f;
+                    xs[k][e] = ok ? xs[k][e] : 0.f;
+                }
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+                float y[W];
+                const int a = W * lane + k * W * kWave;
+                if constexpr (HAS_R) {
+                    if (a < A) Vec<float, W>::ld(r, base + a, y);
+                    else for (int e = 0; e < W; ++e) y[e] = 0.f;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < W; ++e) y[e] = (ps[k][e] * ps[k][e]) * inv;   // as the fast memory's statistics form it
+                }
+#pragma unroll
+                for (int e = 0; e < W; ++e) rho += xs[k][e] * y[e];
+            }
+            rho = wave_sum(rho);
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+                const int a = W * lane + k * W * kWave;
+                if (a < A) {
+                    float acc[W];
+                    Vec<float, W>::ld(mine, a, acc);
+#pragma unroll
+                    for (int e = 0; e < W; ++e) {
+                        ps[k][e] = 2.f * ps[k][e] * (xs[k][e] - rho) * inv;
+                        acc[e] += ps[k][e];
+                    }
+                    Vec<T, W>::st(dpre, base + a, ps[k]);
+                    Vec<float, W>::st(mine, a, acc);
+                }
+            }
+            dle -= rho * inv;
+            continue;
+        }
 #pragma unroll 4
         for (int a = W * lane; a < A; a += W * kWave) {
             float x[W], y[W];
@@ -226,17 +281,41 @@ int launch_addr_fwd(const void *pre, const float *bias, const float *log_eps, fl
     return check_launch("addr_fwd_kernel");
 }
 
+template <typename T, int W, bool HAS_R, int NS>
+int launch_addr_bwd_ns(const T *pre, const float *bias, const float *log_eps, const float *r, const float *denom,
+                       const float *dr, T *dpre, float *dbias_part, float *dle_part, int M, int A, int nblk,
+                       size_t lds, hipStream_t s) {
+    if (lds > 65536 &&
+        hipFuncSetAttribute(reinterpret_cast<const void *>(&addr_bwd_kernel<T, W, HAS_R, NS>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
+        return check_launch("addr_bwd_kernel attribute");
+    addr_bwd_kernel<T, W, HAS_R, NS><<<nblk, kAddrWaves * 64, lds, s>>>(pre, bias, log_eps, r, denom, dr, dpre,
+                                                                        dbias_part, dle_part, M, A);
+    return check_launch("addr_bwd_kernel");
+}
+
+// rows of up to 16 x 256 slots (W = 4) are kept in registers between the passes
 template <typename T, int W, bool HAS_R>
 int launch_addr_bwd_kernel(const T *pre, const float *bias, const float *log_eps, const float *r, const float *denom,
                            const float *dr, T *dpre, float *dbias_part, float *dle_part, int M, int A, int nblk,
                            size_t lds, hipStream_t s) {
-    if (lds > 65536 &&
-        hipFuncSetAttribute(reinterpret_cast<const void *>(&addr_bwd_kernel<T, W, HAS_R>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
-        return check_launch("addr_bwd_kernel attribute");
-    addr_bwd_kernel<T, W, HAS_R><<<nblk, kAddrWaves * 64, lds, s>>>(pre, bias, log_eps, r, denom, dr, dpre, dbias_part,
-                                                                    dle_part, M, A);
-    return check_launch("addr_bwd_kernel");
+    if constexpr (W == 4) {
+        const int steps = (A + W * kWave - 1) / (W * kWave);
+        if (steps <= 4)
+            return launch_addr_bwd_ns<T, W, HAS_R, 4>(pre, bias, log_eps, r, denom, dr, dpre, dbias_part, dle_part, M, A,
+                                                      nblk, lds, s);
+        if (steps <= 8)
+            return launch_addr_bwd_ns<T, W, HAS_R, 8>(pre, bias, log_eps, r, denom, dr, dpre, dbias_part, dle_part, M, A,
+                                                      nblk, lds, s);
+        if (steps <= 12)
+            return launch_addr_bwd_ns<T, W, HAS_R, 12>(pre, bias, log_eps, r, denom, dr, dpre, dbias_part, dle_part, M,
+                                                       A, nblk, lds, s);
+        if (steps <= 16)
+            return launch_addr_bwd_ns<T, W, HAS_R, 16>(pre, bias, log_eps, r, denom, dr, dpre, dbias_part, dle_part, M,
+                                                       A, nblk, lds, s);
+    }
+    return launch_addr_bwd_ns<T, W, HAS_R, 0>(pre, bias, log_eps, r, denom, dr, dpre, dbias_part, dle_part, M, A, nblk,
+                                              lds, s);
 }
 
 template <typename T>

@@ -30,8 +30,28 @@ __global__ void convert_kernel(const void *src, int sdt, void *dst, int ddt, siz
     for (size_t k = i; k < n; k += stride) store_from_f32(dst, k, ddt, load_as_f32(src, k, sdt));
 }
 
+// fp32 -> bf16, four elements per thread and step (16-byte loads, 8-byte stores)
+__global__ void convert_f32_bf16x4_kernel(const float4 *__restrict__ src, uint2 *__restrict__ dst, size_t n4) {
+    size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t k = i; k < n4; k += stride) {
+        const float4 v = src[k];
+        dst[k] = make_uint2(f32_to_bf16_bits(v.x) | (static_cast<uint32_t>(f32_to_bf16_bits(v.y)) << 16),
+                            f32_to_bf16_bits(v.z) | (static_cast<uint32_t>(f32_to_bf16_bits(v.w)) << 16));
+    }
+}
+
 int launch_convert(const void *src, int src_dt, void *dst, int dst_dt, size_t n, hipStream_t s) {
     if (n == 0) return ULM_OK;
+    if (src_dt == ULM_F32 && dst_dt == ULM_BF16 && n % 4 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(dst) % 8 == 0) {
+        const size_t n4 = n / 4;
+        size_t blocks = (n4 + 255) / 256;
+        if (blocks > 16384) blocks = 16384;
+        convert_f32_bf16x4_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(
+            static_cast<const float4 *>(src), static_cast<uint2 *>(dst), n4);
+        return check_launch("convert_f32_bf16x4_kernel");
+    }
     size_t blocks = (n + 255) / 256;
     if (blocks > 16384) blocks = 16384;
     convert_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(src, src_dt, dst, dst_dt, n);
@@ -48,8 +68,18 @@ __global__ __launch_bounds__(256) void column_sum_kernel(const float *__restrict
     if (c >= ncol) return;
     const size_t per = (nrow + gridDim.y - 1) / gridDim.y;
     const size_t r0 = blockIdx.y * per, r1 = min(nrow, r0 + per);
+    // rows added one after another in row order; their loads issued eight at a
+    // time, so that the sum does not wait for one load at a time
     float s = 0.f;
-    for (size_t r = r0; r < r1; ++r) s += in[r * ncol + c];
+    size_t r = r0;
+    for (; r + 8 <= r1; r += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = in[(r + k) * ncol + c];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s += v[k];
+    }
+    for (; r < r1; ++r) s += in[r * ncol + c];
     if (out2 && c >= ncol1) out2[c - ncol1] = s;
     else out[blockIdx.y * ncol + c] = s;
 }

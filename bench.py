@@ -75,7 +75,7 @@ PEAK_BF16_TFLOPS = 2516.6
 PEAK_HBM_GBPS = 8000.0
 TRAFFIC_FILES = {"la_kgroup_kernel": os.path.join(ROOT, "profiles", "la_kgroup_kernel_traffic.txt"),
                  "pair_kernel": os.path.join(ROOT, "profiles", "pair_kernel_traffic.txt"),
-                 "decode_state_kernel": os.path.join(ROOT, "profiles", "decode_state_kernel_traffic.txt")}
+                 "decode_read_kernel": os.path.join(ROOT, "profiles", "decode_read_kernel_traffic.txt")}
 
 
 def log(msg):
@@ -97,9 +97,10 @@ def parse():
     p.add_argument("--no-step", action="store_true")
     p.add_argument("--no-configs", action="store_true")
     p.add_argument("--no-chunked", action="store_true")
-    p.add_argument("--only", choices=("block", "step"),
-                   help="profiling: run one leg alone (the fused block leg without its op-by-op pass, or the "
-                        "training step) and print its record instead of the benchmark line")
+    p.add_argument("--only", choices=("block", "step", "decode"),
+                   help="profiling: run one leg alone (the fused block leg without its op-by-op pass, the "
+                        "training step, or the decode leg without its CPU baselines) and print its record "
+                        "instead of the benchmark line")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                    help="first run one plain fp32 copy kernel over MB megabytes (a known-size reference for "
                         "hardware byte counters)")
@@ -439,14 +440,45 @@ def bench_decode(torch, args):
             log(f"  decode {i + 1}/{args.decode_steps}")
     torch.cuda.synchronize()
     t2 = time.perf_counter()
-    bytes_step = workloads.decode_bytes_per_step(N, L, A, D, V)
+    import model as model_mod
+    deferred = A % 4 == 0 and A <= 4096
+    J = model_mod.DECODE_PENDING if deferred else 1
+    bytes_step = workloads.decode_bytes_per_step(N, L, A, D, V, pending=J)
+    bytes_each = workloads.decode_bytes_per_step(N, L, A, D, V, pending=1)
     step_ms = (t2 - t1) * 1e3 / max(args.decode_steps, 1)
     pre_ms = (t_pre - t0) * 1e3
     gbps = bytes_step / (step_ms * 1e-3) / 1e9
-    log(f"decode {step_ms:.2f} ms/step, {gbps:.0f} GB/s; chunked prefill {pre_ms:.1f} ms "
-        f"({N * args.prefill / (pre_ms * 1e-3) / 1e6:.2f} Mtok/s)")
+    log(f"decode {step_ms:.2f} ms/step, {gbps:.0f} GB/s ({J} positions per state write-back; "
+        f"{bytes_each / (step_ms * 1e-3) / 1e9:.0f} GB/s in the bytes of a write at every position); "
+        f"chunked prefill {pre_ms:.1f} ms ({N * args.prefill / (pre_ms * 1e-3) / 1e6:.2f} Mtok/s)")
+    # a second pass of 2 J positions with a HIP event pair around every state
+    # launch, on the stream it runs on (torch's current stream)
+    kernel_ms = {"decode_read_kernel": [], "decode_flush_kernel": []}
+    if deferred:
+        real = model_mod.decode_deferred
+
+        def timed(S, pv, pr, m, flush, *rest, **kw):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            out = real(S, pv, pr, m, flush, *rest, **kw)
+            e1.record()
+            kernel_ms["decode_flush_kernel" if flush else "decode_read_kernel"].append((e0, e1))
+            return out
+
+        model_mod.decode_deferred = timed
+        try:
+            for _ in range(2 * J):
+                logits = model.step(nxt, states)
+                nxt = logits.argmax(-1)
+            torch.cuda.synchronize()
+        finally:
+            model_mod.decode_deferred = real
+    launch = {k: (sum(a.elapsed_time(b) for a, b in v) / len(v) if v else None) for k, v in kernel_ms.items()}
+    # algorithmic bytes per launch: S read (and for the write-back, written), q, and the m pending terms
+    read_bytes = N * D * A * 4 + N * A * 4 + N * (J + 1) // 2 * (D + 1) * 4
+    flush_bytes = 2 * N * D * A * 4 + N * A * 4 + N * J * (A + D) * 4
     traffic = None
-    tfile = TRAFFIC_FILES["decode_state_kernel"]
+    tfile = TRAFFIC_FILES["decode_read_kernel"]
     if os.path.exists(tfile) and N == 256:
         with open(tfile) as f:
             traffic = json.load(f).get("bytes_per_launch")
@@ -454,16 +486,33 @@ def bench_decode(torch, args):
     if not args.no_cpu:
         cpu_port = bench_decode_cpu(torch, model, c)
         cpu = bench_decode_runc(torch, model, c)
+    read_gbps = read_bytes / (launch["decode_read_kernel"] * 1e-3) / 1e9 if launch["decode_read_kernel"] else None
+    flush_gbps = flush_bytes / (launch["decode_flush_kernel"] * 1e-3) / 1e9 if launch["decode_flush_kernel"] else None
+    if read_gbps:
+        log(f"  decode_read_kernel {launch['decode_read_kernel']:.3f} ms ({read_gbps:.0f} GB/s), "
+            f"decode_flush_kernel {launch['decode_flush_kernel']:.3f} ms ({flush_gbps:.0f} GB/s)")
+    roofline = {"bound": "hbm", "achieved": round(read_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                "frac": round(read_gbps / PEAK_HBM_GBPS, 4), "traffic": traffic,
+                "kernel": "decode_read_kernel",
+                "bytes": "S read (N D A fp32), q, the pending terms' values and weights, per block and position",
+                "avg_launch_ms": round(launch["decode_read_kernel"], 4),
+                "launches_timed": len(kernel_ms["decode_read_kernel"]),
+                "launch_events": "a second pass of 2 J positions with a HIP event pair around every state launch",
+                "flush_kernel": "decode_flush_kernel", "flush_avg_launch_ms": round(launch["decode_flush_kernel"], 4),
+                "flush_achieved": round(flush_gbps, 1), "flush_frac": round(flush_gbps / PEAK_HBM_GBPS, 4),
+                "traffic_source": "recorded (profiles/)" if traffic else None} if read_gbps else \
+        {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+         "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None, "kernel": "decode_state_kernel (whole step)"}
     return {"metric": "decode GB/s", "value": round(gbps, 1), "unit": "GB/s", "ms_per_step": round(step_ms, 3),
             "tok_per_s": round(N / (step_ms * 1e-3), 1),
+            "state_write_back_every": J,
+            "frac_hbm_peak": round(gbps / PEAK_HBM_GBPS, 4),
+            "write_each_position_equivalent_GBps": round(bytes_each / (step_ms * 1e-3) / 1e9, 1),
             "prefill": "chunked (UnifiedLM.prefill, fused blocks, GEMMs bf16 under autocast)",
             "prefill_ms": round(pre_ms, 2), "prefill_ms_per_position": round(pre_ms / max(args.prefill, 1), 4),
             "prefill_Mtok_per_s": round(N * args.prefill / (pre_ms * 1e-3) / 1e6, 3), "bytes_per_step": bytes_step,
             "state_GB": round(N * L * D * A * 4 / 1e9, 2),
-            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                         "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": traffic,
-                         "traffic_kernel": "decode_state_kernel (S read + write and read-out, per block-step)",
-                         "traffic_source": "recorded (profiles/)" if traffic else None},
+            "roofline": roofline,
             "cpu_baseline": cpu or cpu_port,
             "cpu_baseline_port": cpu_port if cpu else None,
             "config": {"N": N, "D": D, "A": A, "blocks": L, "vocab": V, "prefill": args.prefill,
@@ -556,7 +605,11 @@ def main():
         log(f"copy probe: {4 * n} bytes read, {4 * n} bytes written")
         del x, y
     if args.only:
-        rec = bench_block(torch, args, composed=False) if args.only == "block" else bench_train_step(torch, args)
+        if args.only == "decode":
+            args.no_cpu = True
+        legs = {"block": lambda: bench_block(torch, args, composed=False),
+                "step": lambda: bench_train_step(torch, args), "decode": lambda: bench_decode(torch, args)}
+        rec = legs[args.only]()
         print(json.dumps({"leg": args.only, "steps": args.steps, "warmup": args.warmup, **rec}), flush=True)
         return
     train = bench_training(torch, args)

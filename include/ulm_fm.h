@@ -319,6 +319,37 @@ int ulm_decode_state(float *S, const float *v, const float *r_prev, const float 
                      const float *g, const float *x, const float *ymu, float *out,
                      int N, int D, int A, void *stream);
 
+/* Deferred write-back of the decode state (the same position-by-position
+ * maths as ulm_decode_state, model.py:107-109 / run.c:244-255, in another
+ * order). The state is S_base (N,D,A) plus the m most recent write terms,
+ * j = 0 (oldest) .. m-1: pv (m,N,D) their values v_j and pr (m,N,A) their
+ * keys r_prev_j, so that
+ *   S_t = lam^m S_base + sum_j lam^(m-1-j) v_j r_prev_j^T.
+ * A position appends its term (v, r_prev) as term m-1 and then either reads
+ * (ulm_decode_read, S_base unchanged) or, once the terms reach the capacity
+ * its caller chose (at most ulm_decode_max_pending()), writes S_t back as the
+ * new S_base (ulm_decode_flush) and starts over with no terms. Over J
+ * positions S then moves J reads and one write instead of J reads and J
+ * writes. A % 4 == 0, A <= 4096, S, q and pr 16-byte aligned; 1 <= m.
+ *
+ * ulm_decode_dots: cj (m,N) = pr_j[n,:] . q[n,:], the terms' read-out weights.
+ * ulm_decode_read: out = x + lam^m S_base q + sum_j lam^(m-1-j) v_j cj_j + ymu.
+ * ulm_decode_flush: S_base <- S_t (in place); out = x + S_t q + ymu. */
+int ulm_decode_max_pending(void);
+/* ulm_decode_addr_deferred: ulm_decode_addr for a deferred state, which also
+ *   appends r_prev as the pending key of term `slot` (pr (slot+1,N,A) at least)
+ *   and, with cj given, writes cj (slot+1,N) = pr_j[n,:] . q[n,:] for
+ *   j = 0 .. slot (what ulm_decode_dots forms, from the q it has just made).
+ *   A % 4 == 0, A <= 4096, every vector 16-byte aligned. */
+int ulm_decode_addr_deferred(const float *pre, const float *bias, const float *log_eps, const float *w,
+                             const float *g, const float *r_prev, float *c, float *r, float *q, float *wq,
+                             float *pr, int slot, float *cj, int N, int A, void *stream);
+int ulm_decode_dots(const float *pr, const float *q, float *cj, int m, int N, int A, void *stream);
+int ulm_decode_read(const float *S, const float *pv, const float *cj, int m, const float *q, const float *g,
+                    const float *x, const float *ymu, float *out, int N, int D, int A, void *stream);
+int ulm_decode_flush(float *S, const float *pv, const float *pr, int m, const float *q, const float *g,
+                     const float *x, const float *ymu, float *out, int N, int D, int A, void *stream);
+
 /* ------------------------------------------------------------------------
  * Diagnostics: HIP-event timing of every chunked-kernel launch (ulm_la and
  * the launches inside ulm_fm_fwd / ulm_fm_bwd) between start and stop, on

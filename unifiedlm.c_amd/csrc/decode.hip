@@ -82,6 +82,7 @@ __global__ __launch_bounds__(256) void decode_addr_kernel(const float *__restric
 }
 
 constexpr int kStateRows = 4;    // rows (features) per block, one per wave
+constexpr int kMaxPending = 8;   // write terms a deferred state holds at most
 constexpr int kRowChunk = 12;    // 16-byte loads per lane in flight per row: 3072 slots in one pass
 
 // S[n, d, :] <- lam S + v[n, d] r_prev[n, :];  out[n, d] = x + S[n, d, :] . q[n, :] + ymu.
@@ -148,13 +149,18 @@ __global__ __launch_bounds__(256) void decode_state_kernel(float *__restrict__ S
 }
 
 // decode_addr with 16-byte accesses, A % 4 == 0 and A <= 1024 R4: pre (+ bias)
-// is read once and its relu^2 kept in registers across the row sum
+// is read once and its relu^2 kept in registers across the row sum. With pr
+// (a deferred state's pending keys, (mslot + 1, N, A) at least), r_prev is also
+// appended as term mslot, and with cj the terms' read-out weights
+// cj[j][n] = pr_j[n, :] . q[n, :], j = 0 .. mslot, are formed from the q in registers.
 template <int R4>
 __global__ __launch_bounds__(256) void decode_addr_vec_kernel(const float *__restrict__ pre, const float *__restrict__ bias,
                                                               const float *__restrict__ log_eps, const float *__restrict__ w,
                                                               const float *__restrict__ g, const float *__restrict__ r_prev,
                                                               float *__restrict__ c, float *__restrict__ r,
-                                                              float *__restrict__ q, float *__restrict__ wq, int A) {
+                                                              float *__restrict__ q, float *__restrict__ wq, int A,
+                                                              float *__restrict__ pr = nullptr, int mslot = 0,
+                                                              float *__restrict__ cj = nullptr, int N = 0) {
     __shared__ float red[4];
     const size_t row = static_cast<size_t>(blockIdx.x) * A;
     const int A4 = A / 4;
@@ -178,11 +184,13 @@ __global__ __launch_bounds__(256) void decode_addr_vec_kernel(const float *__res
     const f32x4 *w4 = reinterpret_cast<const f32x4 *>(w);
     const f32x4 *rp4 = reinterpret_cast<const f32x4 *>(r_prev + row);
     f32x4 *c4 = reinterpret_cast<f32x4 *>(c + row);
+    f32x4 qk[R4];
 #pragma unroll
     for (int k = 0; k < R4; ++k) {
         const int j = threadIdx.x + 256 * k;
-        if (j >= A4) break;
-        const f32x4 wa = w4[j], cn = lam * c4[j] + (1.f - lam) * wa + rp4[j];
+        qk[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (j >= A4) continue;
+        const f32x4 wa = w4[j], rp = rp4[j], cn = lam * c4[j] + (1.f - lam) * wa + rp;
         const f32x4 ra = z[k] * idn;
         f32x4 qa;
 #pragma unroll
@@ -191,6 +199,196 @@ __global__ __launch_bounds__(256) void decode_addr_vec_kernel(const float *__res
         reinterpret_cast<f32x4 *>(r + row)[j] = ra;
         reinterpret_cast<f32x4 *>(q + row)[j] = qa;
         reinterpret_cast<f32x4 *>(wq + row)[j] = wa * qa;
+        if (pr) reinterpret_cast<f32x4 *>(pr + static_cast<size_t>(mslot) * N * A + row)[j] = rp;
+        qk[k] = qa;
+    }
+    if (!cj) return;
+    // the pending terms' weights; the term just appended is read back from the
+    // store above by the same lanes, so the sum needs no barrier before it
+    const size_t n = blockIdx.x;
+    for (int t = 0; t <= mslot; ++t) {
+        const f32x4 *p4 = reinterpret_cast<const f32x4 *>(pr + static_cast<size_t>(t) * N * A + row);
+        f32x4 pk[R4];
+#pragma unroll
+        for (int k = 0; k < R4; ++k) {
+            const int j = threadIdx.x + 256 * k;
+            pk[k] = p4[j < A4 ? j : 0];   // clamped load; selected away past A below
+        }
+        float d = 0.f;
+#pragma unroll
+        for (int k = 0; k < R4; ++k) {
+            const bool ok = threadIdx.x + 256 * k < A4;
+            const f32x4 u = pk[k] * qk[k];
+            d += ok ? (u[0] + u[1]) + (u[2] + u[3]) : 0.f;
+        }
+        d = block_sum_256(d, red);
+        if (threadIdx.x == 0) cj[static_cast<size_t>(t) * N + n] = d;
+    }
+}
+
+// ---- Deferred state write-back. The state is kept as S_base plus the m most
+// recent write terms (v_j, rp_j), j = 0 (oldest) .. m - 1, of m <= J pending
+// positions:
+//   S_t = lam^m S_base + sum_j lam^(m-1-j) v_j rp_j^T,
+//   y_t = S_t q = lam^m (S_base q) + sum_j lam^(m-1-j) v_j (rp_j . q).
+// A position with m < J only reads S_base (decode_read_kernel); the position
+// that fills the J-th term writes S_t back as the new S_base (decode_flush_kernel).
+// Per J positions the state moves J reads and one write instead of J of each.
+
+// cj[j][n] = rp_j[n, :] . q[n, :] for the m pending terms; one block per sequence
+__global__ __launch_bounds__(256) void decode_dots_kernel(const float *__restrict__ pr, const float *__restrict__ q,
+                                                          float *__restrict__ cj, int m, int N, int A) {
+    __shared__ float red[4];
+    const size_t n = blockIdx.x;
+    for (int j = 0; j < m; ++j) {
+        const float *p = pr + (static_cast<size_t>(j) * N + n) * A;
+        float s = 0.f;
+        for (int a = threadIdx.x; a < A; a += 256) s += p[a] * q[n * A + a];
+        s = block_sum_256(s, red);
+        if (threadIdx.x == 0) cj[static_cast<size_t>(j) * N + n] = s;
+    }
+}
+
+constexpr int kReadRowsPerWave = 4;
+
+// Read-only position: out[n, d] = x + lam^m (S_base[n, d, :] . q) + sum_j lam^(m-1-j)
+// pv_j[n, d] cj[j][n] + ymu. Each lane keeps its CH 16-byte slices of q in
+// registers for all of its wave's rows and streams each row with all of the
+// row's loads in flight (A % 4 == 0, A <= 256 CH).
+template <int CH>
+__global__ __launch_bounds__(256) void decode_read_kernel(const float *__restrict__ S, const float *__restrict__ pv,
+                                                          const float *__restrict__ cj, int m,
+                                                          const float *__restrict__ q, const float *__restrict__ g,
+                                                          const float *__restrict__ x, const float *__restrict__ ymu,
+                                                          float *__restrict__ out, int N, int D, int A) {
+    const size_t n = blockIdx.x;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int A4 = A / 4;
+    const f32x4 *q4 = reinterpret_cast<const f32x4 *>(q + n * A);
+    f32x4 qv[CH];
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+        const int j = lane + kWave * k;
+        qv[k] = j < A4 ? q4[j] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const float lam = __expf(g[0]);
+    float lm = 1.f;
+    for (int j = 0; j < m; ++j) lm *= lam;
+    const int d0 = (blockIdx.y * 4 + wave) * kReadRowsPerWave;
+    for (int r = 0; r < kReadRowsPerWave; ++r) {
+        const int d = d0 + r;
+        if (d >= D) break;
+        const f32x4 *S4 = reinterpret_cast<const f32x4 *>(S + (n * D + d) * static_cast<size_t>(A));
+        f32x4 sv[CH];
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const int j = lane + kWave * k;
+            sv[k] = __builtin_nontemporal_load(S4 + (j < A4 ? j : 0));
+        }
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const f32x4 t = sv[k] * qv[k];   // q is zero past A
+            acc += (t[0] + t[1]) + (t[2] + t[3]);
+        }
+        acc = wave_sum(acc);
+        // the pending terms: every load issued at once (clamped to term 0, masked after)
+        float pvv[kMaxPending], cjv[kMaxPending];
+#pragma unroll
+        for (int j = 0; j < kMaxPending; ++j) {
+            const size_t jj = j < m ? j : 0;
+            pvv[j] = pv[(jj * N + n) * D + d];
+            cjv[j] = cj[jj * N + n];
+        }
+        float y = lm * acc, pw = 1.f;
+#pragma unroll
+        for (int j = kMaxPending - 1; j >= 0; --j) {   // the newest term first, weight lam^0
+            if (j < m) {
+                y += pw * pvv[j] * cjv[j];
+                pw *= lam;
+            }
+        }
+        if (lane == 0) out[n * D + d] = x[n * D + d] + y + ymu[n * D + d];
+    }
+}
+
+constexpr int kFlushRows = 32;   // rows (features) per workgroup
+#ifndef ULM_FLUSH_BATCH
+#define ULM_FLUSH_BATCH 8
+#endif
+constexpr int kFlushBatch = ULM_FLUSH_BATCH;   // rows whose loads a lane has in flight at once
+
+// Flush position: S_base[n, d, :] <- lam^m S_base + sum_j lam^(m-1-j) pv_j[n, d] rp_j[n, :],
+// out[n, d] = x + S_base . q + ymu. Column-strip layout: wave w of the
+// workgroup owns slots 256 w .. 256 w + 255 (one 16-byte slice per lane) of
+// kFlushRows rows of one sequence, and keeps its slices of the m pending keys
+// and of q in registers for all of them; the per-row coefficients
+// lam^(m-1-j) pv_j[n, d] are uniform over the wave. Each lane streams its
+// slice of kFlushBatch rows at a time (loads first), and the rows' dot
+// products are summed over the waves through LDS in a fixed order.
+// A <= 4096 (at most 16 waves), A % 4 == 0.
+__global__ __launch_bounds__(1024) void decode_flush_kernel(float *__restrict__ S, const float *__restrict__ pv,
+                                                            const float *__restrict__ pr, int m,
+                                                            const float *__restrict__ q, const float *__restrict__ g,
+                                                            const float *__restrict__ x, const float *__restrict__ ymu,
+                                                            float *__restrict__ out, int N, int D, int A) {
+    __shared__ float part[16][kFlushRows];
+    __shared__ float spv[kMaxPending][kFlushRows];   // the block's rows' pending values
+    const size_t n = blockIdx.x;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, nw = blockDim.x / kWave;
+    const int d0 = blockIdx.y * kFlushRows;
+    for (int k = threadIdx.x; k < kMaxPending * kFlushRows; k += blockDim.x) {
+        const int j = k / kFlushRows, d = min(d0 + k % kFlushRows, D - 1);
+        spv[j][k % kFlushRows] = j < m ? pv[(static_cast<size_t>(j) * N + n) * D + d] : 0.f;
+    }
+    const int A4 = A / 4, i = wave * kWave + lane;   // this lane's 16-byte slice of every row
+    const bool ok = i < A4;
+    const int ic = ok ? i : 0;
+    f32x4 rp[kMaxPending];
+#pragma unroll
+    for (int j = 0; j < kMaxPending; ++j)
+        rp[j] = reinterpret_cast<const f32x4 *>(pr + (static_cast<size_t>(j < m ? j : 0) * N + n) * A)[ic];
+    const f32x4 qv = reinterpret_cast<const f32x4 *>(q + n * A)[ic];
+    const float lam = __expf(g[0]);
+    float lm = 1.f;
+    for (int j = 0; j < m; ++j) lm *= lam;
+    __syncthreads();
+    for (int b = 0; b < kFlushRows; b += kFlushBatch) {
+        f32x4 sv[kFlushBatch];
+#pragma unroll
+        for (int u = 0; u < kFlushBatch; ++u) {
+            const int d = min(d0 + b + u, D - 1);   // rows past D: a clamped load, nothing stored
+            sv[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(S + (n * D + d) * static_cast<size_t>(A)) + ic);
+        }
+#pragma unroll
+        for (int u = 0; u < kFlushBatch; ++u) {
+            const int d = d0 + b + u;
+            float cf[kMaxPending];
+            float pw = 1.f;
+#pragma unroll
+            for (int j = kMaxPending - 1; j >= 0; --j) {
+                cf[j] = j < m ? pw * spv[j][b + u] : 0.f;
+                if (j < m) pw *= lam;
+            }
+            f32x4 t = lm * sv[u];
+#pragma unroll
+            for (int j = 0; j < kMaxPending; ++j) t += cf[j] * rp[j];
+            if (ok && d < D)
+                __builtin_nontemporal_store(t, reinterpret_cast<f32x4 *>(S + (n * D + d) * static_cast<size_t>(A)) + i);
+            const f32x4 pq = t * qv;
+            float acc = ok ? (pq[0] + pq[1]) + (pq[2] + pq[3]) : 0.f;
+            acc = wave_sum(acc);
+            if (lane == 0) part[wave][b + u] = acc;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < kFlushRows) {
+        const int d = d0 + threadIdx.x;
+        if (d < D) {
+            float y = 0.f;
+            for (int w2 = 0; w2 < nw; ++w2) y += part[w2][threadIdx.x];
+            out[n * D + d] = x[n * D + d] + y + ymu[n * D + d];
+        }
     }
 }
 
@@ -246,4 +444,80 @@ extern "C" int ulm_decode_state(float *S, const float *v, const float *r_prev, c
     else
         decode_state_kernel<false><<<grid, dim3(256), lds, s>>>(S, v, r_prev, q, g, x, ymu, out, D, A);
     return check_launch("decode_state_kernel");
+}
+
+namespace {
+// the per-lane 16-byte slice count of a row of A slots: 4, 8, 12 or 16 (A <= 4096), else 0
+int deferred_chunks(int A) {
+    const int ch = (A / 4 + kWave - 1) / kWave;
+    return ch <= 4 ? 4 : ch <= 8 ? 8 : ch <= 12 ? 12 : ch <= 16 ? 16 : 0;
+}
+bool aligned16(std::initializer_list<const void *> ps) {
+    for (const void *p : ps)
+        if (reinterpret_cast<uintptr_t>(p) % 16) return false;
+    return true;
+}
+}  // namespace
+
+extern "C" int ulm_decode_max_pending(void) { return kMaxPending; }
+
+extern "C" int ulm_decode_dots(const float *pr, const float *q, float *cj, int m, int N, int A, void *stream) {
+    ULM_REQUIRE(N > 0 && A > 0 && m >= 1 && m <= kMaxPending, "ulm_decode_dots: bad sizes N=%d A=%d m=%d", N, A, m);
+    ULM_REQUIRE(pr && q && cj, "ulm_decode_dots: null pointer");
+    decode_dots_kernel<<<dim3(N), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(pr, q, cj, m, N, A);
+    return check_launch("decode_dots_kernel");
+}
+
+extern "C" int ulm_decode_read(const float *S, const float *pv, const float *cj, int m, const float *q, const float *g,
+                               const float *x, const float *ymu, float *out, int N, int D, int A, void *stream) {
+    ULM_REQUIRE(N > 0 && D > 0 && A > 0 && m >= 1 && m <= kMaxPending, "ulm_decode_read: bad sizes N=%d D=%d A=%d m=%d",
+                N, D, A, m);
+    ULM_REQUIRE(A % 4 == 0 && deferred_chunks(A) > 0, "ulm_decode_read: A=%d must be a multiple of 4 and at most 4096",
+                A);
+    ULM_REQUIRE(S && pv && cj && q && g && x && ymu && out, "ulm_decode_read: null pointer");
+    ULM_REQUIRE(aligned16({S, q}), "ulm_decode_read: S and q must be 16-byte aligned");
+    const dim3 grid(N, (D + 4 * kReadRowsPerWave - 1) / (4 * kReadRowsPerWave));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (deferred_chunks(A)) {
+    case 4: decode_read_kernel<4><<<grid, dim3(256), 0, s>>>(S, pv, cj, m, q, g, x, ymu, out, N, D, A); break;
+    case 8: decode_read_kernel<8><<<grid, dim3(256), 0, s>>>(S, pv, cj, m, q, g, x, ymu, out, N, D, A); break;
+    case 12: decode_read_kernel<12><<<grid, dim3(256), 0, s>>>(S, pv, cj, m, q, g, x, ymu, out, N, D, A); break;
+    default: decode_read_kernel<16><<<grid, dim3(256), 0, s>>>(S, pv, cj, m, q, g, x, ymu, out, N, D, A); break;
+    }
+    return check_launch("decode_read_kernel");
+}
+
+extern "C" int ulm_decode_flush(float *S, const float *pv, const float *pr, int m, const float *q, const float *g,
+                                const float *x, const float *ymu, float *out, int N, int D, int A, void *stream) {
+    ULM_REQUIRE(N > 0 && D > 0 && A > 0 && m >= 1 && m <= kMaxPending,
+                "ulm_decode_flush: bad sizes N=%d D=%d A=%d m=%d", N, D, A, m);
+    ULM_REQUIRE(A % 4 == 0 && deferred_chunks(A) > 0, "ulm_decode_flush: A=%d must be a multiple of 4 and at most 4096",
+                A);
+    ULM_REQUIRE(S && pv && pr && q && g && x && ymu && out, "ulm_decode_flush: null pointer");
+    ULM_REQUIRE(aligned16({S, q, pr}), "ulm_decode_flush: S, q and the pending keys must be 16-byte aligned");
+    const int waves = (A / 4 + kWave - 1) / kWave;   // one 256-slot strip per wave
+    const dim3 grid(N, (D + kFlushRows - 1) / kFlushRows);
+    decode_flush_kernel<<<grid, dim3(waves * kWave), 0, static_cast<hipStream_t>(stream)>>>(S, pv, pr, m, q, g, x, ymu,
+                                                                                           out, N, D, A);
+    return check_launch("decode_flush_kernel");
+}
+
+extern "C" int ulm_decode_addr_deferred(const float *pre, const float *bias, const float *log_eps, const float *w,
+                                        const float *g, const float *r_prev, float *c, float *r, float *q, float *wq,
+                                        float *pr, int mslot, float *cj, int N, int A, void *stream) {
+    ULM_REQUIRE(N > 0 && A > 0 && mslot >= 0 && mslot < kMaxPending,
+                "ulm_decode_addr_deferred: bad sizes N=%d A=%d slot=%d", N, A, mslot);
+    ULM_REQUIRE(pre && log_eps && w && g && r_prev && c && r && q && wq && pr, "ulm_decode_addr_deferred: null pointer");
+    const int r4 = (A / 4 + 255) / 256;
+    ULM_REQUIRE(A % 4 == 0 && r4 <= 4, "ulm_decode_addr_deferred: A=%d must be a multiple of 4 and at most 4096", A);
+    ULM_REQUIRE(aligned16({pre, bias, w, r_prev, c, r, q, wq, pr}),
+                "ulm_decode_addr_deferred: every vector must be 16-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (r4) {
+    case 1: decode_addr_vec_kernel<1><<<dim3(N), dim3(256), 0, s>>>(pre, bias, log_eps, w, g, r_prev, c, r, q, wq, A, pr, mslot, cj, N); break;
+    case 2: decode_addr_vec_kernel<2><<<dim3(N), dim3(256), 0, s>>>(pre, bias, log_eps, w, g, r_prev, c, r, q, wq, A, pr, mslot, cj, N); break;
+    case 3: decode_addr_vec_kernel<3><<<dim3(N), dim3(256), 0, s>>>(pre, bias, log_eps, w, g, r_prev, c, r, q, wq, A, pr, mslot, cj, N); break;
+    default: decode_addr_vec_kernel<4><<<dim3(N), dim3(256), 0, s>>>(pre, bias, log_eps, w, g, r_prev, c, r, q, wq, A, pr, mslot, cj, N); break;
+    }
+    return check_launch("decode_addr_vec_kernel");
 }

@@ -663,6 +663,44 @@ def decode_state(S, v, r_prev, q, g, x, ymu, out=None):
     return out
 
 
+def decode_addr_deferred(pre, bias, log_eps, w, g, r_prev, c, pr, slot, dots):
+    """decode_addr for a deferred state: also appends r_prev as pending key
+    `slot` of pr (J,N,A) and, with dots, returns the read-out weights
+    cj (slot+1, N) of the terms 0 .. slot. Returns (r, q, w*q, cj or None)."""
+    N, A = pre.shape
+    nat.require_device(pre, bias, log_eps, w, g, r_prev, c, pr)
+    r = torch.empty_like(pre)
+    q = torch.empty_like(pre)
+    wq = torch.empty_like(pre)
+    cj = torch.empty(slot + 1, N, device=pre.device, dtype=torch.float32) if dots else None
+    call("ulm_decode_addr_deferred", ptr(_f32c(pre)), ptr(None if bias is None else _f32c(bias)), ptr(_f32c(log_eps)),
+         ptr(_f32c(w)), ptr(_f32c(g)), ptr(_f32c(r_prev)), ptr(_f32c(c)), ptr(r), ptr(q), ptr(wq), ptr(_f32c(pr)),
+         slot, ptr(cj), N, A, nat.stream_of(pre))
+    return r, q, wq, cj
+
+
+def decode_deferred(S, pv, pr, m, flush, q, g, x, ymu, cj=None):
+    """One position on a deferred state (S_base, the first m of the pending
+    write terms pv (J,N,D), pr (J,N,A), the newest term already appended):
+    with flush, S_base <- S_t in place; else S_base is only read, with the
+    terms' read-out weights cj (m,N) (formed here by ulm_decode_dots when not
+    given). Returns x + S_t q + ymu."""
+    N, D, A = S.shape
+    nat.require_device(S, pv, pr, q, g, x, ymu)
+    out = torch.empty_like(x)
+    st = nat.stream_of(S)
+    if flush:
+        call("ulm_decode_flush", ptr(_f32c(S)), ptr(_f32c(pv)), ptr(_f32c(pr)), m, ptr(_f32c(q)), ptr(_f32c(g)),
+             ptr(_f32c(x)), ptr(_f32c(ymu)), ptr(out), N, D, A, st)
+    else:
+        if cj is None:
+            cj = torch.empty(m, N, device=S.device, dtype=torch.float32)
+            call("ulm_decode_dots", ptr(_f32c(pr)), ptr(_f32c(q)), ptr(cj), m, N, A, st)
+        call("ulm_decode_read", ptr(_f32c(S)), ptr(_f32c(pv)), ptr(_f32c(cj)), m, ptr(_f32c(q)), ptr(_f32c(g)),
+             ptr(_f32c(x)), ptr(_f32c(ymu)), ptr(out), N, D, A, st)
+    return out
+
+
 def probe_mfma(a, b):
     """D = A B (A 32x16, B 16x32, bf16) through the kernels' MFMA operand layout."""
     a16 = a.to(torch.bfloat16).contiguous()

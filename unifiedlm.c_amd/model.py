@@ -28,7 +28,9 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from kernel import (CHUNK, LOG_W_MAX, LOG_W_MIN, block_prefill, decode_addr, decode_pre, decode_state, fm_prefill,
+from kernel import (CHUNK, LOG_W_MAX, LOG_W_MIN, block_prefill, decode_addr, decode_addr_deferred, decode_deferred,
+                    decode_pre, decode_state,
+                    fm_prefill,
                     relu2_address, unified_block, unified_memory)
 
 
@@ -67,6 +69,11 @@ class RMSNorm(nn.Module):
         x32 = x.float()
         scaled = x32 * torch.rsqrt(x32.square().mean(dim=-1, keepdim=True) + self.eps)
         return scaled.to(x.dtype) * self.weight
+
+
+# write terms a decode state holds before it writes S back (at most
+# ulm_decode_max_pending(), 8)
+DECODE_PENDING = 8
 
 
 class UnifiedBlock(nn.Module):
@@ -196,12 +203,35 @@ class UnifiedBlock(nn.Module):
     @torch.no_grad()
     def step(self, x, s):
         """One position x (B, d) for a batch of sequences: write (key r_{t-1},
-        value v_t), then read with the new address."""
+        value v_t), then read with the new address.
+
+        With slots a multiple of 4 (at most 4096) the write is deferred: the
+        state holds S (its last written value) and up to DECODE_PENDING
+        pending write terms (s["pv"], s["pr"], s["np"] of them); a position
+        appends its term and reads S with the terms added, and the position
+        that fills the last term writes S back with all of them. The maths of
+        model.py:107-109 in another order: S moves one write per
+        DECODE_PENDING positions instead of one per position."""
         p = s["params"]
         x32 = x.float().contiguous()
         h, u = decode_pre(x32, p["norm_w"], p["conv_w"], s["buf"], self.norm.eps)
-        r, q, wq = decode_addr(u @ p["key_wt"], p["key_b"], p["log_eps"], p["w"], p["g"], s["r_prev"], s["c"])
-        out = decode_state(s["S"], h @ p["val_wt"], s["r_prev"], q, p["g"], x32, wq @ p["mu_wt"])
+        N, width, slots = s["S"].shape
+        if slots % 4 or slots > 4096:
+            r, q, wq = decode_addr(u @ p["key_wt"], p["key_b"], p["log_eps"], p["w"], p["g"], s["r_prev"], s["c"])
+            out = decode_state(s["S"], h @ p["val_wt"], s["r_prev"], q, p["g"], x32, wq @ p["mu_wt"])
+        else:
+            if "pv" not in s:
+                s["pv"] = torch.empty(DECODE_PENDING, N, width, device=x.device, dtype=torch.float32)
+                s["pr"] = torch.empty(DECODE_PENDING, N, slots, device=x.device, dtype=torch.float32)
+                s["np"] = 0
+            m = s["np"]
+            flush = m + 1 == DECODE_PENDING
+            # appends r_prev as pending key m (and the terms' read-out weights unless this position writes back)
+            r, q, wq, cj = decode_addr_deferred(u @ p["key_wt"], p["key_b"], p["log_eps"], p["w"], p["g"],
+                                                s["r_prev"], s["c"], s["pr"], m, not flush)
+            torch.mm(h, p["val_wt"], out=s["pv"][m])
+            out = decode_deferred(s["S"], s["pv"], s["pr"], m + 1, flush, q, p["g"], x32, wq @ p["mu_wt"], cj)
+            s["np"] = 0 if flush else m + 1
         s["r_prev"] = r
         return out.to(x.dtype)
 

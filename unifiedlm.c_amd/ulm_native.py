@@ -53,6 +53,11 @@ SIGNATURES = {
     "ulm_decode_pre": (I, [P, P, P, P, P, P, I, I, I, F, P]),
     "ulm_decode_addr": (I, [P, P, P, P, P, P, P, P, P, P, I, I, P]),
     "ulm_decode_state": (I, [P, P, P, P, P, P, P, P, I, I, I, P]),
+    "ulm_decode_max_pending": (I, []),
+    "ulm_decode_addr_deferred": (I, [P, P, P, P, P, P, P, P, P, P, P, I, P, I, I, P]),
+    "ulm_decode_dots": (I, [P, P, P, I, I, I, P]),
+    "ulm_decode_read": (I, [P, P, P, I, P, P, P, P, P, I, I, I, P]),
+    "ulm_decode_flush": (I, [P, P, P, I, P, P, P, P, P, I, I, I, P]),
     "ulm_la_timer_start": (I, [I]),
     "ulm_la_timer_stop": (I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]),
     "ulm_probe_mfma": (I, [P, P, P, P]),

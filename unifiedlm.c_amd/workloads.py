@@ -70,12 +70,19 @@ def init_decode_model(model, seed):
     return model
 
 
-def decode_bytes_per_step(N, L, A, D, V, conv_size=4):
+def decode_bytes_per_step(N, L, A, D, V, conv_size=4, pending=1):
     """Algorithmic HBM bytes of one decode position for N sequences and L blocks, fp32:
-    S read+write, c and r_prev read+write, the conv window read+write, every block's
-    weights once and the tied classifier."""
+    the state S, c and r_prev read+write, the conv window read+write, every block's
+    weights once and the tied classifier. pending = 1: S read and written at
+    every position. pending = J > 1 (the deferred write-back): S read at every
+    position and written at one in J, the appended term (v and r_prev) written
+    once, and the pending terms read, (J + 1) / 2 of them on average."""
     kw = conv_size - 1
-    per_seq_block = 8 * A * D + 16 * A + 8 * kw * D
+    if pending <= 1:
+        per_seq_block = 8 * A * D + 16 * A + 8 * kw * D
+    else:
+        per_seq_block = (4 * A * D * (pending + 1)) // pending + 16 * A + 8 * kw * D + 4 * (A + D) \
+            + 2 * (A + D) * (pending + 1)
     # norm D, conv D*Kc, key A*D + bias A, mu D*A, val D*D, w A, lam, eps
     weights = 4 * (2 * A * D + D * D + 2 * A + (1 + conv_size) * D + 2)
     return N * L * per_seq_block + L * weights + 4 * V * D

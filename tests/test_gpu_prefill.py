@@ -83,6 +83,35 @@ def test_model_prefill_then_step_matches_recurrent(dim, hidden):
         assert max(errs.values()) < 1e-2, errs
 
 
+def test_flushed_states_after_steps_match_oracle():
+    """UnifiedLM.flush_states after 5 steps past a prefill (5 write terms
+    pending in every block): each block's S, c and r_prev are the oracle's
+    state after the same 55 tokens (S = U - mu w) within 1e-2 (S from bf16
+    products in the prefill), and stepping on from the flushed states gives the
+    oracle's logits."""
+    say("UnifiedLM.flush_states after a prefill of 50 positions and 5 steps vs the oracle's states")
+    kw = dict(dim=32, n_layers=2, hidden_dim=64, vocab_size=97, max_seq_len=80)
+    model = tiny_model(**kw).cuda()
+    x = torch.randint(0, 97, (3, 60), generator=torch.Generator().manual_seed(5))
+    _, states = model.prefill(x[:, :50].cuda())
+    for t in range(50, 55):
+        model.step(x[:, t].cuda(), states)
+    assert all(s["np"] == 5 for s in states)
+    model.flush_states(states)
+    p = oracle_params(model)
+    so = _oracle_states(p, x[:, :55], kw["n_layers"])
+    for i, (a, o) in enumerate(zip(states, so)):
+        assert a["np"] == 0
+        w = fm.prior_mass(p[f"layers.{i}.log_w"])
+        errs = {"S": rel(a["S"], o["U"] - p[f"layers.{i}.mu.weight"] * w), "c": rel(a["c"], o["c"]),
+                "r_prev": rel(a["r_prev"], o["r_prev"])}
+        say(f"  block {i} rel errors {errs}")
+        assert max(errs.values()) < 1e-2, errs
+    cont = torch.stack([model.step(x[:, t].cuda(), states) for t in range(55, 60)], 1)
+    ref = fm.forward_recurrent(p, x)
+    assert rel(cont, ref[:, 55:]) < 1e-2
+
+
 def test_model_prefill_short_prompt():
     """A prompt shorter than the conv window (T = 2 < 3): the window keeps its zeros."""
     say("UnifiedLM.prefill of 2 positions vs forward_recurrent")

@@ -235,6 +235,22 @@ class UnifiedBlock(nn.Module):
         s["r_prev"] = r
         return out.to(x.dtype)
 
+    @torch.no_grad()
+    def flush_state(self, s):
+        """Writes a deferred decode state's pending terms into s["S"] (S <- S_t,
+        no pending terms left), so that s["S"] is the state after the last
+        position `step` took; a no-op when nothing is pending."""
+        m = s.get("np", 0)
+        if not m:
+            return s
+        p = s["params"]
+        N, width, slots = s["S"].shape
+        zeros = torch.zeros(N, slots, device=s["S"].device, dtype=torch.float32)
+        x0 = torch.zeros(N, width, device=s["S"].device, dtype=torch.float32)
+        decode_deferred(s["S"], s["pv"], s["pr"], m, True, zeros, p["g"], x0, x0)   # the read-out is discarded
+        s["np"] = 0
+        return s
+
 
 class UnifiedLM(nn.Module):
     """Token embedding, `n_layers` UnifiedBlocks, a final RMSNorm and a
@@ -288,6 +304,12 @@ class UnifiedLM(nn.Module):
 
     def init_states(self, batch: int, device):
         return [layer.init_state(batch, device) for layer in self.layers]
+
+    def flush_states(self, states):
+        """Every block's decode state written back (UnifiedBlock.flush_state)."""
+        for layer, s in zip(self.layers, states):
+            layer.flush_state(s)
+        return states
 
     @torch.no_grad()
     def prefill(self, tokens: torch.Tensor):

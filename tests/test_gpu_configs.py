@@ -74,14 +74,14 @@ def test_training_step_at_110m_shape_matches_oracle(autocast):
 
 def test_decode_at_its_benchmark_batch():
     """The decode workload at its own batch: N=256 sequences of a 512-token
-    prompt through the chunked prefill (UnifiedLM.prefill, fp32 GEMMs), then 12
+    prompt through the chunked prefill (UnifiedLM.prefill, fp32 GEMMs), then 20
     decode steps (model.py:96-111, 164-175; one write-back of the deferred
-    state at the 8th), the 29 GB of fp32 state resident. Rows 0, 137 and 255
+    state at the 16th), the 29 GB of fp32 state resident. Rows 0, 137 and 255
     must equal (within 1e-5) the same prompts run alone at N=1, every row
     stays finite, and row 0's logits after the last step are within 1e-2 of
-    the oracle's forward_recurrent over the same 524 tokens in float64 (the
+    the oracle's forward_recurrent over the same 532 tokens in float64 (the
     prefill's products take bf16 operands)."""
-    N, T, steps = 256, 512, 12
+    N, T, steps = 256, 512, 20
     say(f"decode at the benchmark batch: N={N}, prefill {T} positions, {steps} steps, 12 blocks D=768 A=3072")
     model = _model(13, 1024).eval()
     gen = torch.Generator().manual_seed(13)

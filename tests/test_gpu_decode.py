@@ -2,7 +2,7 @@
 ulm_decode_flush) against ulm_decode_state position by position (needs an
 MI355X): the same write S <- lam S + v r_prev^T and read-out x + S q + ymu
 (model.py:107-109, run.c:244-255), the writes held as pending terms and
-written back every 8 positions. Outputs and, after each write-back, the state
+written back every 16 positions. Outputs and, after each write-back, the state
 itself agree within fp32 rounding (1e-6). Widths: 3072 slots (12 16-byte
 slices per lane), 712 and 1000 (a row cut inside a lane's last slice), 4096
 (the largest), 256; feature counts off the 16 rows of a workgroup."""
@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 import kernel  # noqa: E402
 import ulm_native as nat  # noqa: E402
 
-J = 8
+J = 16
 
 
 @pytest.mark.parametrize("N,D,A", [(3, 40, 3072), (2, 17, 712), (1, 8, 4096), (4, 24, 256), (2, 9, 1000)])

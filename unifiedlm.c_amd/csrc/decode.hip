@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void decode_addr_kernel(const float *__restric
 }
 
 constexpr int kStateRows = 4;    // rows (features) per block, one per wave
-constexpr int kMaxPending = 8;   // write terms a deferred state holds at most
+constexpr int kMaxPending = 16;  // write terms a deferred state holds at most
 constexpr int kRowChunk = 12;    // 16-byte loads per lane in flight per row: 3072 slots in one pass
 
 // S[n, d, :] <- lam S + v[n, d] r_prev[n, :];  out[n, d] = x + S[n, d, :] . q[n, :] + ymu.
@@ -203,27 +203,37 @@ __global__ __launch_bounds__(256) void decode_addr_vec_kernel(const float *__res
         qk[k] = qa;
     }
     if (!cj) return;
-    // the pending terms' weights; the term just appended is read back from the
-    // store above by the same lanes, so the sum needs no barrier before it
+    // the pending terms' weights pr_t . q, t = 0 .. mslot: each thread's partial
+    // dots of every term, then one exchange for all of them. The term just
+    // appended is read back from the store above by the same lanes, so it
+    // needs no barrier.
+    __shared__ float part[4][kMaxPending];
     const size_t n = blockIdx.x;
-    for (int t = 0; t <= mslot; ++t) {
+    float dt[kMaxPending];
+#pragma unroll
+    for (int t = 0; t < kMaxPending; ++t) {
+        dt[t] = 0.f;
+        if (t > mslot) continue;
         const f32x4 *p4 = reinterpret_cast<const f32x4 *>(pr + static_cast<size_t>(t) * N * A + row);
-        f32x4 pk[R4];
 #pragma unroll
         for (int k = 0; k < R4; ++k) {
             const int j = threadIdx.x + 256 * k;
-            pk[k] = p4[j < A4 ? j : 0];   // clamped load; selected away past A below
+            const f32x4 pk = p4[j < A4 ? j : 0];   // clamped load; selected away past A
+            const f32x4 u = pk * qk[k];
+            dt[t] += j < A4 ? (u[0] + u[1]) + (u[2] + u[3]) : 0.f;
         }
-        float d = 0.f;
-#pragma unroll
-        for (int k = 0; k < R4; ++k) {
-            const bool ok = threadIdx.x + 256 * k < A4;
-            const f32x4 u = pk[k] * qk[k];
-            d += ok ? (u[0] + u[1]) + (u[2] + u[3]) : 0.f;
-        }
-        d = block_sum_256(d, red);
-        if (threadIdx.x == 0) cj[static_cast<size_t>(t) * N + n] = d;
     }
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+#pragma unroll
+    for (int t = 0; t < kMaxPending; ++t) {
+        if (t > mslot) break;
+        const float v = wave_sum(dt[t]);
+        if (lane == 0) part[wave][t] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x <= mslot)
+        cj[static_cast<size_t>(threadIdx.x) * N + n] =
+            (part[0][threadIdx.x] + part[1][threadIdx.x]) + (part[2][threadIdx.x] + part[3][threadIdx.x]);
 }
 
 // ---- Deferred state write-back. The state is kept as S_base plus the m most
@@ -274,6 +284,12 @@ __global__ __launch_bounds__(256) void decode_read_kernel(const float *__restric
     const float lam = __expf(g[0]);
     float lm = 1.f;
     for (int j = 0; j < m; ++j) lm *= lam;
+    // lane j < m carries term j: its weight lam^(m-1-j) cj[j][n]; the term's
+    // v_j[n, d] joins the row's wave sum
+    const int jt = lane < m ? lane : 0;
+    float cw = cj[static_cast<size_t>(jt) * N + n];
+    for (int e = jt + 1; e < m; ++e) cw *= lam;
+    cw = lane < m ? cw : 0.f;
     const int d0 = (blockIdx.y * 4 + wave) * kReadRowsPerWave;
     for (int r = 0; r < kReadRowsPerWave; ++r) {
         const int d = d0 + r;
@@ -285,38 +301,25 @@ __global__ __launch_bounds__(256) void decode_read_kernel(const float *__restric
             const int j = lane + kWave * k;
             sv[k] = __builtin_nontemporal_load(S4 + (j < A4 ? j : 0));
         }
+        const float pvl = pv[(static_cast<size_t>(jt) * N + n) * D + d];
+        // the row's loads all go out before its arithmetic (interleaved by the
+        // scheduler, each load waited for the one before it)
+        __builtin_amdgcn_sched_barrier(0);
         float acc = 0.f;
 #pragma unroll
         for (int k = 0; k < CH; ++k) {
             const f32x4 t = sv[k] * qv[k];   // q is zero past A
             acc += (t[0] + t[1]) + (t[2] + t[3]);
         }
-        acc = wave_sum(acc);
-        // the pending terms: every load issued at once (clamped to term 0, masked after)
-        float pvv[kMaxPending], cjv[kMaxPending];
-#pragma unroll
-        for (int j = 0; j < kMaxPending; ++j) {
-            const size_t jj = j < m ? j : 0;
-            pvv[j] = pv[(jj * N + n) * D + d];
-            cjv[j] = cj[jj * N + n];
-        }
-        float y = lm * acc, pw = 1.f;
-#pragma unroll
-        for (int j = kMaxPending - 1; j >= 0; --j) {   // the newest term first, weight lam^0
-            if (j < m) {
-                y += pw * pvv[j] * cjv[j];
-                pw *= lam;
-            }
-        }
-        if (lane == 0) out[n * D + d] = x[n * D + d] + y + ymu[n * D + d];
+        acc = wave_sum(lm * acc + cw * pvl);
+        if (lane == 0) out[n * D + d] = x[n * D + d] + acc + ymu[n * D + d];
     }
 }
 
 constexpr int kFlushRows = 32;   // rows (features) per workgroup
-#ifndef ULM_FLUSH_BATCH
-#define ULM_FLUSH_BATCH 8
-#endif
-constexpr int kFlushBatch = ULM_FLUSH_BATCH;   // rows whose loads a lane has in flight at once
+// rows whose loads a lane has in flight at once: 8 where the registers allow
+// (12 waves, 168 VGPRs), else 4
+template <int MAXW> constexpr int flush_batch() { return MAXW <= 12 ? 8 : 4; }
 
 // Flush position: S_base[n, d, :] <- lam^m S_base + sum_j lam^(m-1-j) pv_j[n, d] rp_j[n, :],
 // out[n, d] = x + S_base . q + ymu. Column-strip layout: wave w of the
@@ -324,10 +327,12 @@ constexpr int kFlushBatch = ULM_FLUSH_BATCH;   // rows whose loads a lane has in
 // kFlushRows rows of one sequence, and keeps its slices of the m pending keys
 // and of q in registers for all of them; the per-row coefficients
 // lam^(m-1-j) pv_j[n, d] are uniform over the wave. Each lane streams its
-// slice of kFlushBatch rows at a time (loads first), and the rows' dot
+// slice of a batch of rows at a time (loads first), and the rows' dot
 // products are summed over the waves through LDS in a fixed order.
-// A <= 4096 (at most 16 waves), A % 4 == 0.
-__global__ __launch_bounds__(1024) void decode_flush_kernel(float *__restrict__ S, const float *__restrict__ pv,
+// A <= 64 MAXW (MAXW waves at most), A % 4 == 0; MAXW = 12 (A <= 3072) allows
+// 168 VGPRs per lane, where the 16 key slices fit without spills.
+template <int MAXW>
+__global__ __launch_bounds__(MAXW * 64) void decode_flush_kernel(float *__restrict__ S, const float *__restrict__ pv,
                                                             const float *__restrict__ pr, int m,
                                                             const float *__restrict__ q, const float *__restrict__ g,
                                                             const float *__restrict__ x, const float *__restrict__ ymu,
@@ -353,15 +358,16 @@ __global__ __launch_bounds__(1024) void decode_flush_kernel(float *__restrict__ 
     float lm = 1.f;
     for (int j = 0; j < m; ++j) lm *= lam;
     __syncthreads();
-    for (int b = 0; b < kFlushRows; b += kFlushBatch) {
-        f32x4 sv[kFlushBatch];
+    for (int b = 0; b < kFlushRows; b += flush_batch<MAXW>()) {
+        f32x4 sv[flush_batch<MAXW>()];
 #pragma unroll
-        for (int u = 0; u < kFlushBatch; ++u) {
+        for (int u = 0; u < flush_batch<MAXW>(); ++u) {
             const int d = min(d0 + b + u, D - 1);   // rows past D: a clamped load, nothing stored
             sv[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(S + (n * D + d) * static_cast<size_t>(A)) + ic);
         }
+        __builtin_amdgcn_sched_barrier(0);   // the batch's loads before its arithmetic
 #pragma unroll
-        for (int u = 0; u < kFlushBatch; ++u) {
+        for (int u = 0; u < flush_batch<MAXW>(); ++u) {
             const int d = d0 + b + u;
             float cf[kMaxPending];
             float pw = 1.f;
@@ -497,8 +503,11 @@ extern "C" int ulm_decode_flush(float *S, const float *pv, const float *pr, int 
     ULM_REQUIRE(aligned16({S, q, pr}), "ulm_decode_flush: S, q and the pending keys must be 16-byte aligned");
     const int waves = (A / 4 + kWave - 1) / kWave;   // one 256-slot strip per wave
     const dim3 grid(N, (D + kFlushRows - 1) / kFlushRows);
-    decode_flush_kernel<<<grid, dim3(waves * kWave), 0, static_cast<hipStream_t>(stream)>>>(S, pv, pr, m, q, g, x, ymu,
-                                                                                           out, N, D, A);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (waves <= 12)
+        decode_flush_kernel<12><<<grid, dim3(waves * kWave), 0, s>>>(S, pv, pr, m, q, g, x, ymu, out, N, D, A);
+    else
+        decode_flush_kernel<16><<<grid, dim3(waves * kWave), 0, s>>>(S, pv, pr, m, q, g, x, ymu, out, N, D, A);
     return check_launch("decode_flush_kernel");
 }
 

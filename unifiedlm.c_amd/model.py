@@ -72,8 +72,8 @@ class RMSNorm(nn.Module):
 
 
 # write terms a decode state holds before it writes S back (at most
-# ulm_decode_max_pending(), 8)
-DECODE_PENDING = 8
+# ulm_decode_max_pending(), 16)
+DECODE_PENDING = 16
 
 
 class UnifiedBlock(nn.Module):

@@ -48,7 +48,7 @@ are resident in HBM before the timed region. Prints one JSON line:
              autocast, token ids uniform
   decode     batched recurrent decode at the 110M shape: 256 sequences, 12
              blocks, fp32 state (29 GB); the 512-position prompt in one
-             chunked pass (UnifiedLM.prefill), then greedy steps; GB/s of the
+             parallel pass (UnifiedLM.prefill), then greedy steps; GB/s of the
              algorithmic bytes per step against 8 TB/s. Its cpu_baseline is
              the reference's own C decoder (run.c, built with its runomp
              flags by oracle/Makefile) on the host cores, one sequence, in the
@@ -414,7 +414,7 @@ def bench_decode(torch, args):
     model = model.to(dev).eval()
     gen = torch.Generator(device=dev).manual_seed(3)
     prompt = torch.randint(0, V, (N, args.prefill), device=dev, generator=gen)
-    # the prompt in one chunked pass (UnifiedLM.prefill), which leaves the same
+    # the prompt in one parallel pass (UnifiedLM.prefill), which leaves the same
     # decode states as stepping through it position by position; its GEMMs take
     # bf16 operands under autocast, as the training step's do
     with torch.autocast("cuda", dtype=torch.bfloat16):
@@ -425,7 +425,10 @@ def bench_decode(torch, args):
         logits, states = model.prefill(prompt)
         torch.cuda.synchronize()
     t_pre = time.perf_counter()
-    log(f"  prefill {args.prefill} positions x {N} sequences in one chunked pass: {(t_pre - t0) * 1e3:.1f} ms")
+    import ulm_native
+    pre_form = {1: "chunked state form", 2: "block-pair products, the state as one product over positions"}.get(
+        ulm_native.lib().ulm_fm_prefill_path(N, args.prefill, A, D), "unsupported")
+    log(f"  prefill {args.prefill} positions x {N} sequences in one pass ({pre_form}): {(t_pre - t0) * 1e3:.1f} ms")
     nxt = logits.argmax(-1)
     for _ in range(2):   # untimed: first launches of the decode kernels
         logits = model.step(nxt, states)
@@ -450,7 +453,7 @@ def bench_decode(torch, args):
     gbps = bytes_step / (step_ms * 1e-3) / 1e9
     log(f"decode {step_ms:.2f} ms/step, {gbps:.0f} GB/s ({J} positions per state write-back; "
         f"{bytes_each / (step_ms * 1e-3) / 1e9:.0f} GB/s in the bytes of a write at every position); "
-        f"chunked prefill {pre_ms:.1f} ms ({N * args.prefill / (pre_ms * 1e-3) / 1e6:.2f} Mtok/s)")
+        f"prefill {pre_ms:.1f} ms ({N * args.prefill / (pre_ms * 1e-3) / 1e6:.2f} Mtok/s)")
     # a second pass of 2 J positions with a HIP event pair around every state
     # launch, on the stream it runs on (torch's current stream)
     kernel_ms = {"decode_read_kernel": [], "decode_flush_kernel": []}
@@ -508,7 +511,7 @@ def bench_decode(torch, args):
             "state_write_back_every": J,
             "frac_hbm_peak": round(gbps / PEAK_HBM_GBPS, 4),
             "write_each_position_equivalent_GBps": round(bytes_each / (step_ms * 1e-3) / 1e9, 1),
-            "prefill": "chunked (UnifiedLM.prefill, fused blocks, GEMMs bf16 under autocast)",
+            "prefill": f"one pass of the prompt (UnifiedLM.prefill, fused blocks, GEMMs bf16 under autocast; {pre_form})",
             "prefill_ms": round(pre_ms, 2), "prefill_ms_per_position": round(pre_ms / max(args.prefill, 1), 4),
             "prefill_Mtok_per_s": round(N * args.prefill / (pre_ms * 1e-3) / 1e6, 3), "bytes_per_step": bytes_step,
             "state_GB": round(N * L * D * A * 4 / 1e9, 2),

@@ -97,7 +97,7 @@ int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const float *g, const
                float *q, void *fast, int fast_dtype, void *saved, size_t saved_bytes,
                void *workspace, size_t workspace_bytes, int B, int T, int A, int D, void *stream);
 
-/* Chunked prefill: the forward of ulm_fm_fwd (no autograd state kept) plus the
+/* Prefill: the forward of ulm_fm_fwd (no autograd state kept) plus the
  * decode state after position T-1, so decoding can continue from a prompt
  * processed in one parallel pass instead of the token-by-token loop of
  * UnifiedLM.forward_recurrent (model.py:164-175; the state of
@@ -108,7 +108,13 @@ int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const float *g, const
  *   c_last (B,A)   fp32 out: w + sum_{s<T} lam^(T-1-s) k_s, the decode c
  *   r, v, g, w, q, fast as for ulm_fm_fwd; workspace of
  *   ulm_fm_prefill_workspace_bytes() bytes (0: unsupported shape).
- * Any A and D (widths off the 32 grid run on zero-padded tiles). */
+ * Any A and D (widths off the 32 grid run on zero-padded tiles).
+ * ulm_fm_prefill_path reports the form: 1 the chunked state form (S is the end
+ * of its walk), 2 the block-pair products for fast plus S as one product of v
+ * with the keys decayed to T-1, where those need fewer flops (at the 110M
+ * widths up to about 768 positions); ULM_FM_PATH=chunked|pair forces one.
+ * -1: unsupported shape. */
+int ulm_fm_prefill_path(int B, int T, int A, int D);
 size_t ulm_fm_prefill_workspace_bytes(int B, int T, int A, int D, int v_dtype, int fast_dtype);
 int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const float *g, const float *w,
                    float *q, void *fast, int fast_dtype, float *S, float *c_last,

@@ -1,5 +1,7 @@
-"""Chunked prefill (needs an MI355X): the forward of the fast memory plus the
-decode state after the last position, against the float64 oracle.
+"""Prefill (needs an MI355X): the forward of the fast memory plus the decode
+state after the last position, against the float64 oracle, in both of its
+forms: the chunked state form, and the block-pair products with the state as
+one product over positions (ulm_fm_prefill_path; ULM_FM_PATH forces one).
 
 Tolerances: q and c are fp32 scans (1e-5); fast and the state S come from bf16
 MFMA products with fp32 accumulation, the training path's 1e-2 (test_all.py:166).
@@ -14,6 +16,7 @@ from oracle import fastmem as fm
 pytestmark = pytest.mark.gpu
 
 import kernel  # noqa: E402
+import ulm_native as nat  # noqa: E402
 
 PREFILL_CASES = [
     # B, T, A, D, lam, dtype of v
@@ -30,9 +33,12 @@ PREFILL_CASES = [
 ]
 
 
+@pytest.mark.parametrize("path", ["chunked", "pair"])
 @pytest.mark.parametrize("B,T,A,D,lam,vdt", PREFILL_CASES)
-def test_fm_prefill_matches_oracle_state(B, T, A, D, lam, vdt):
-    say(f"fm_prefill B={B} T={T} A={A} D={D} lam={lam} v={vdt}")
+def test_fm_prefill_matches_oracle_state(B, T, A, D, lam, vdt, path, monkeypatch):
+    monkeypatch.setenv("ULM_FM_PATH", path)
+    assert nat.lib().ulm_fm_prefill_path(B, T, A, D) == {"chunked": 1, "pair": 2}[path]
+    say(f"fm_prefill B={B} T={T} A={A} D={D} lam={lam} v={vdt}, {path} form")
     r, v, g, w = fm_inputs(B, T, A, D, seed=T + A, device="cpu", lam=lam)
     q, fast, S, c = kernel.fm_prefill(r.float().cuda(), v.to(vdt).cuda(), g.float().cuda(), w.float().cuda())
     torch.cuda.synchronize()
@@ -57,9 +63,12 @@ def _oracle_states(p, tokens, n_layers):
     return states
 
 
+@pytest.mark.parametrize("path", ["chunked", "pair"])
 @pytest.mark.parametrize("dim,hidden", [(32, 64), (64, 140)])
-def test_model_prefill_then_step_matches_recurrent(dim, hidden):
-    say(f"UnifiedLM.prefill of 50 positions, then 20 steps, vs the oracle's forward_recurrent, dim={dim} A={hidden}")
+def test_model_prefill_then_step_matches_recurrent(dim, hidden, path, monkeypatch):
+    monkeypatch.setenv("ULM_FM_PATH", path)
+    say(f"UnifiedLM.prefill of 50 positions, then 20 steps, vs the oracle's forward_recurrent, dim={dim} A={hidden}, "
+        f"{path} form")
     kw = dict(dim=dim, n_layers=3, hidden_dim=hidden, vocab_size=97, max_seq_len=80)
     model = tiny_model(**kw).cuda()
     x = torch.randint(0, 97, (3, 70), generator=torch.Generator().manual_seed(2))
@@ -124,10 +133,13 @@ def test_model_prefill_short_prompt():
     assert rel(cont, ref[:, 2:]) < 1e-2
 
 
-def test_model_prefill_under_autocast():
-    """The fused prefill with bf16 GEMM operands (the bench's configuration):
-    logits and the decode states after the prompt against the oracle, 1e-2."""
-    say("UnifiedLM.prefill under bf16 autocast, 100 positions, vs the oracle's states and forward_recurrent")
+@pytest.mark.parametrize("path", ["chunked", "pair"])
+def test_model_prefill_under_autocast(path, monkeypatch):
+    """The fused prefill with bf16 GEMM operands (the bench's configuration)
+    in both forms: logits and the decode states after the prompt against the
+    oracle, 1e-2."""
+    monkeypatch.setenv("ULM_FM_PATH", path)
+    say(f"UnifiedLM.prefill under bf16 autocast, 100 positions, {path} form, vs the oracle's states and forward_recurrent")
     kw = dict(dim=64, n_layers=2, hidden_dim=128, vocab_size=97, max_seq_len=160)
     model = tiny_model(**kw).cuda()
     x = torch.randint(0, 97, (2, 120), generator=torch.Generator().manual_seed(6))

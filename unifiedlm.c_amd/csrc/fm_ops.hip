@@ -62,7 +62,7 @@ int launch_unpad_sum(const float *part, int nK, int B, int R, int Rp, int F, int
 int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
                      uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, float *c_last, int B, int T,
                      int A, hipStream_t s, void *qw = nullptr, int qw_dt = ULM_BF16, int AL = 0,
-                     float *segtot = nullptr);
+                     float *segtot = nullptr, int kq_decay = 0);
 size_t fwd_stats_segtot_bytes(int B, int T, int A);
 size_t bwd_stats_partial_bytes(int B, int T, int A);
 int launch_bwd_stats(const float *dqf, const float *dqo, const RSrc &src, const float *nck,
@@ -78,6 +78,7 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, uint16_t *vQ, co
                         uint16_t *Pt, uint16_t *Plo, void *out, int out_dt, const float *resid, int B, int T, int A,
                         int D, hipStream_t s, const uint16_t *v, uint16_t *vR);
 size_t pair_stats_bytes(int B, int T, int A);
+int launch_pair_state(const uint16_t *vQ, const uint16_t *kdQ, float *S, int B, int T, int A, int D, hipStream_t s);
 int launch_pair_backward(const uint16_t *vR, const uint16_t *doR, const uint16_t *doQ, const uint16_t *kQ,
                          const uint16_t *qQ, const uint16_t *P, const uint16_t *Pt, const uint16_t *Plo,
                          const float *g, uint16_t *dS, uint16_t *dSt, double *dg_part, const RSrc &r,
@@ -136,6 +137,24 @@ Path train_path(int B, int T, int A, int D) {
     if (env && env[0] == 'c') return PATH_CHUNKED;
     if (!pair_ok) return PATH_CHUNKED;
     if (env && env[0] == 'p') return PATH_PAIR;
+    return pair < 0.8 * chunked ? PATH_PAIR : PATH_CHUNKED;
+}
+
+// The form of a prefill, a forward that also emits the decode state after
+// position T-1: the chunked state form (the state is its walk's end), or the
+// block-pair products for the output plus the state as one product over
+// positions (the keys decayed to T-1), where those need fewer flops per token:
+// the scores and the apply (a third of the pair form's six products) plus
+// 2 A D for the state, against 4 A D + 2 C (A + D) for the state form's
+// forward. At the 110M widths that is up to about 768 positions.
+Path prefill_path(int B, int T, int A, int D) {
+    const char *env = getenv("ULM_FM_PATH");
+    const bool pair_ok = pair_supported(B, T, A, D);
+    if (env && env[0] == 'c') return PATH_CHUNKED;
+    if (!pair_ok) return PATH_CHUNKED;
+    if (env && env[0] == 'p') return PATH_PAIR;
+    const double pair = pair_flops_per_token(B, T, A, D) / 3.0 + 2.0 * A * D;
+    const double chunked = 4.0 * A * D + 2.0 * ULM_CHUNK * (A + D);
     return pair < 0.8 * chunked ? PATH_PAIR : PATH_CHUNKED;
 }
 
@@ -380,8 +399,8 @@ extern "C" size_t ulm_fm_fwd_workspace_bytes(int B, int T, int A, int D, int fas
 namespace {
 
 // The forward composite of ulm_fm_fwd; with state (B, D, A) and c_last (B, A)
-// (aligned shapes, the chunked path) it also emits the decode state after
-// position T-1. q (fp32) and qw (w q in qw_dt) are each optional; with resid
+// (a prefill: the chunked or the block-pair form) it also emits the decode
+// state after position T-1. q (fp32) and qw (w q in qw_dt) are each optional; with resid
 // (fp32 (B,T,D)) the output is resid + fast.
 int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const float *w, float *q, void *qw,
                int qw_dt, const float *resid, void *fast, int fast_dtype, void *saved, void *workspace, float *state,
@@ -390,17 +409,25 @@ int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const 
     const FwdWs ws = fwd_layout(workspace, B, T, A, D, fast_dtype, path, resid != nullptr, state != nullptr);
     const size_t nf = static_cast<size_t>(B) * T * D;
     if (path == PATH_PAIR) {
-        if (state || c_last) return fail(ULM_ERR_INVALID, "prefill state: not on the block-pair path");
         // q, k: R layout for the scores (this pass only), Q layout for the
         // backward's dk_f, dq_f; v: Q layout for the apply, R layout for the
         // backward's dscores. bf16 v with D % 64 == 0 is tiled by the scores
         // launch, on the CUs its tiles leave idle; other v by a launch of its own.
-        ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, ws.qR, ws.kR, sv.qQ, sv.kQ, sv.nck, nullptr, B, T, A, s,
-                                 qw, qw_dt, pad32(A), ws.segtot));
+        // A prefill (state wanted) has no backward: no qQ, vR, P^T or P residual;
+        // kQ holds the keys decayed to T-1, and the state is one product of them
+        // with v over the positions.
+        const bool prefill = state != nullptr;
+        if (prefill != (c_last != nullptr)) return fail(ULM_ERR_INVALID, "prefill: state and c_last go together");
+        ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, ws.qR, ws.kR, prefill ? nullptr : sv.qQ, sv.kQ, sv.nck,
+                                 c_last, B, T, A, s, qw, qw_dt, pad32(A), ws.segtot, prefill ? 1 : 0));
         const bool ride = v_dtype == ULM_BF16 && D % 64 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0;
-        if (!ride) ULM_TRY(launch_chunk_transpose(v, v_dtype, ws.vQ, nullptr, sv.vR, nullptr, B, T, D, s, pad32(D)));
-        return launch_pair_forward(ws.qR, ws.kR, ws.vQ, g, sv.P, sv.Pt, sv.Plo, fast, fast_dtype, resid, B, T, A, D, s,
-                                   ride ? static_cast<const uint16_t *>(v) : nullptr, ride ? sv.vR : nullptr);
+        uint16_t *vR = prefill ? nullptr : sv.vR;
+        if (!ride) ULM_TRY(launch_chunk_transpose(v, v_dtype, ws.vQ, nullptr, vR, nullptr, B, T, D, s, pad32(D)));
+        ULM_TRY(launch_pair_forward(ws.qR, ws.kR, ws.vQ, g, sv.P, prefill ? nullptr : sv.Pt, prefill ? nullptr : sv.Plo,
+                                    fast, fast_dtype, resid, B, T, A, D, s,
+                                    ride ? static_cast<const uint16_t *>(v) : nullptr, ride ? vR : nullptr));
+        if (prefill) ULM_TRY(launch_pair_state(ws.vQ, sv.kQ, state, B, T, A, D, s));
+        return ULM_OK;
     }
     if (path == PATH_CHUNKED) {
         // widths off the 32 grid (a prefill only) run on zero-padded tiles; the
@@ -461,13 +488,20 @@ extern "C" int ulm_fm_fwd(const float *r, const void *v, int v_dtype, const floa
 }
 
 // ---------------------------------------------------------------------------
-// chunked prefill: the forward plus the decode state after position T-1
+// prefill: the forward plus the decode state after position T-1, in the form
+// prefill_path picks
+
+extern "C" int ulm_fm_prefill_path(int B, int T, int A, int D) {
+    if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !fm_aligned(B, T, pad32(A), pad32(D))) return -1;
+    return static_cast<int>(prefill_path(B, T, A, D));
+}
 
 extern "C" size_t ulm_fm_prefill_workspace_bytes(int B, int T, int A, int D, int v_dtype, int fast_dtype) {
     if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(v_dtype) || !valid_dtype(fast_dtype)) return 0;
     if (!fm_aligned(B, T, pad32(A), pad32(D))) return 0;
-    return align_up(saved_layout(nullptr, B, T, A, D, v_dtype, PATH_CHUNKED).bytes, 256) +
-           fwd_layout(nullptr, B, T, A, D, fast_dtype, PATH_CHUNKED, false, true).bytes;
+    const Path path = prefill_path(B, T, A, D);
+    return align_up(saved_layout(nullptr, B, T, A, D, v_dtype, path).bytes, 256) +
+           fwd_layout(nullptr, B, T, A, D, fast_dtype, path, false, true).bytes;
 }
 
 extern "C" int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const float *g, const float *w, float *q,
@@ -482,12 +516,13 @@ extern "C" int ulm_fm_prefill(const float *r, const void *v, int v_dtype, const 
     ULM_REQUIRE(reinterpret_cast<uintptr_t>(S) % 16 == 0, "ulm_fm_prefill: S must be 16-byte aligned");
     const size_t need = ulm_fm_prefill_workspace_bytes(B, T, A, D, v_dtype, fast_dtype);
     ULM_REQUIRE(workspace_bytes >= need, "ulm_fm_prefill: workspace of %zu bytes, need %zu", workspace_bytes, need);
+    const Path path = prefill_path(B, T, A, D);
     char *saved = static_cast<char *>(workspace);
-    char *ws = saved + align_up(saved_layout(nullptr, B, T, A, D, v_dtype, PATH_CHUNKED).bytes, 256);
+    char *ws = saved + align_up(saved_layout(nullptr, B, T, A, D, v_dtype, path).bytes, 256);
     RSrc rs;
     rs.r = r;
     return fm_forward(rs, v, v_dtype, g, w, q, nullptr, ULM_F32, nullptr, fast, fast_dtype, saved, ws, S, c_last, B, T,
-                      A, D, PATH_CHUNKED, static_cast<hipStream_t>(stream));
+                      A, D, path, static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t ulm_fm_bwd_workspace_bytes(int B, int T, int A, int D, int dfast_dtype, size_t saved_bytes,
@@ -637,13 +672,14 @@ extern "C" int ulm_block_fm_bwd(const void *pre, int pre_dtype, const float *bia
                        workspace, B, T, A, D, static_cast<Path>(path), static_cast<hipStream_t>(stream));
 }
 
-// the block's chunked prefill: ulm_block_fm_fwd plus the decode state after T-1
+// the block's prefill: ulm_block_fm_fwd plus the decode state after T-1
 
 extern "C" size_t ulm_block_fm_prefill_workspace_bytes(int B, int T, int A, int D, int v_dtype) {
     if (B <= 0 || T <= 0 || A <= 0 || D <= 0 || !valid_dtype(v_dtype)) return 0;
     if (!fm_aligned(B, T, pad32(A), pad32(D))) return 0;
-    return align_up(saved_layout(nullptr, B, T, A, D, v_dtype, PATH_CHUNKED).bytes, 256) +
-           fwd_layout(nullptr, B, T, A, D, ULM_F32, PATH_CHUNKED, true, true).bytes;
+    const Path path = prefill_path(B, T, A, D);
+    return align_up(saved_layout(nullptr, B, T, A, D, v_dtype, path).bytes, 256) +
+           fwd_layout(nullptr, B, T, A, D, ULM_F32, path, true, true).bytes;
 }
 
 extern "C" int ulm_block_fm_prefill(const void *pre, int pre_dtype, const float *bias, const float *denom,
@@ -662,13 +698,14 @@ extern "C" int ulm_block_fm_prefill(const void *pre, int pre_dtype, const float 
     const size_t need = ulm_block_fm_prefill_workspace_bytes(B, T, A, D, v_dtype);
     ULM_REQUIRE(workspace_bytes >= need, "ulm_block_fm_prefill: workspace of %zu bytes, need %zu", workspace_bytes,
                 need);
+    const Path path = prefill_path(B, T, A, D);
     char *saved = static_cast<char *>(workspace);
-    char *ws = saved + align_up(saved_layout(nullptr, B, T, A, D, v_dtype, PATH_CHUNKED).bytes, 256);
+    char *ws = saved + align_up(saved_layout(nullptr, B, T, A, D, v_dtype, path).bytes, 256);
     RSrc rs;
     rs.pre = pre;
     rs.pre_dt = pre_dtype;
     rs.bias = bias;
     rs.denom = denom;
     return fm_forward(rs, v, v_dtype, g, w, nullptr, qw, qw_dtype, x, y, ULM_F32, saved, ws, S, c_last, B, T, A, D,
-                      PATH_CHUNKED, static_cast<hipStream_t>(stream));
+                      path, static_cast<hipStream_t>(stream));
 }

@@ -191,7 +191,10 @@ __global__ __launch_bounds__(1024) void fwd_segtot_kernel(RS rs, const float *__
 // copies; qR, kR in the R layout and qQ, kQ in the Q layout (the products'
 // operand tiles, AL slots wide: AL % 32 == 0, A <= AL <= the grid's slots);
 // c_last = c at position T-1 (B, A), the decode state after the sequence.
-// Positions past T and slots past A are zero in R and Q.
+// Positions past T and slots past A are zero in R and Q. With kq_decay, kQ
+// holds the keys decayed to position T-1, k_t lam^(T-1-t) (the operand of the
+// decode state as one product over positions).
+// segtot: the segment totals of sequences past one segment (see above).
 // QW: the dtype of the w q output (-1 none, else a ulm_dtype); HAS_Q: the fp32 q output.
 template <class RS, int QW, bool HAS_Q>
 __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__restrict__ w,
@@ -202,7 +205,7 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
                                                         uint16_t *__restrict__ qQ, uint16_t *__restrict__ kQ,
                                                         float *__restrict__ nck, float *__restrict__ c_last, int T,
                                                         int A, int AL, int NT, const float *__restrict__ segtot,
-                                                        int S) {
+                                                        int S, int kq_decay) {
     __shared__ float tot[4][kSlots];
     __shared__ __align__(16) uint16_t sq[ULM_CHUNK][kSlots + 8], sk[ULM_CHUNK][kSlots + 8];   // [position][slot]
     const int s = threadIdx.x % kSlots;
@@ -213,7 +216,8 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
     const uint32_t ac = va ? a : 0;   // the lane's slot, clamped for loads
     const int b = blockIdx.y;
     const size_t bs = blockIdx.y;
-    const float lam = __expf(g[0]);
+    const float lg = g[0];
+    const float lam = __expf(lg);
     const float lam16 = pow_int(lam, kSeg);
     const float wa = va ? w[a] : 1.f;
     const float rb = va ? rs.slot_const(a) : 0.f;   // the slot's key bias when r is formed here
@@ -266,13 +270,15 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
             const int t = t0 + i;
             const float ct = wa + (pw * cj + nl[i]);
             pw *= lam;
-            uint16_t qb = 0, kb = 0;   // positions past T are zero in the tiled copies
+            uint16_t qb = 0, kb = 0, kqb = 0;   // positions past T are zero in the tiled copies
             if (va && t < T) {
                 const size_t ro = (bs * T + t) * A;   // wave-uniform row offset
                 const float qt = rv[i] / ct;
                 if (c_last && t == T - 1) c_last[bs * A + a] = ct;
                 qb = f32_to_bf16_bits(qt);
                 kb = f32_to_bf16_bits(kv[i]);
+                // kq_decay: the Q-layout keys decayed to T - 1, k_t lam^(T-1-t)
+                kqb = kq_decay ? f32_to_bf16_bits(kv[i] * __expf(lg * static_cast<float>(T - 1 - t))) : kb;
                 if constexpr (HAS_Q) st_row(q + ro, 4u * ac, qt);
                 if constexpr (QW == ULM_F32) st_row(static_cast<float *>(qw) + ro, 4u * ac, qt * wa);
                 if constexpr (QW == ULM_BF16) st_row(static_cast<uint16_t *>(qw) + ro, 2u * ac, f32_to_bf16_bits(qt * wa));
@@ -286,10 +292,10 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(RS rs, const float *__re
             sk[j * kSeg + i][s] = kb;
             if (i % 2 == 0) {
                 qpk[i / 2] = qb;
-                kpk[i / 2] = kb;
+                kpk[i / 2] = kqb;
             } else {
                 qpk[i / 2] |= static_cast<uint32_t>(qb) << 16;
-                kpk[i / 2] |= static_cast<uint32_t>(kb) << 16;
+                kpk[i / 2] |= static_cast<uint32_t>(kqb) << 16;
             }
         }
         if ((qQ || kQ) && a < AL) {
@@ -606,7 +612,7 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(const float *__restri
 // copies AL slots wide (0: AL = A; AL % 32 == 0, the slots past A zero).
 int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, uint16_t *q16n, uint16_t *k16n,
                      uint16_t *qR, uint16_t *kR, uint16_t *qQ, uint16_t *kQ, float *nck, float *c_last, int B, int T,
-                     int A, hipStream_t s, void *qw, int qw_dt, int AL, float *segtot) {
+                     int A, hipStream_t s, void *qw, int qw_dt, int AL, float *segtot, int kq_decay) {
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
     const int S = stat_segments(T);
     if ((q16n == nullptr) != (k16n == nullptr)) return fail(ULM_ERR_INVALID, "fwd stats: q16n and k16n go together");
@@ -630,7 +636,7 @@ int launch_fwd_stats(const RSrc &src, const float *w, const float *g, float *q, 
         const dim3 grid((A + kSlots - 1) / kSlots, B, S);
 #define ULM_FWD_STATS(QWK, HQ)                                                                                    \
     fwd_stats_kernel<RS, QWK, HQ><<<grid, 256, 0, s>>>(rs, w, g, q, qw, qw_dt, q16n, k16n, qR, kR, qQ, kQ, nck,   \
-                                                       c_last, T, A, AL, NT, segtot, S)
+                                                       c_last, T, A, AL, NT, segtot, S, kq_decay)
         if (q) {
             switch (qwk) {
             case ULM_F32: ULM_FWD_STATS(ULM_F32, true); break;

@@ -135,6 +135,7 @@ struct Args {
     // EPI_ROWS: (B, T, F) row-major output, rows = positions, columns = features
     void *out;
     int out_dt, F, nperm;    // nperm: B's rows are features in the order perm32 within 32-blocks
+    int mperm;               // EPI_ROWS: A's rows too (an output row index in perm32 order)
     const float *resid;      // fp32 (B, T, F) added, or null
     // EPI_DQSTATS (dq_f with the backward statistics) and OUT_DRADD (dk_f into dr)
     const float *r;          // r (B, T, A) fp32, or null: r = relu(pre + bias)^2 / denom
@@ -446,14 +447,19 @@ __global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI, OU
     const int h = lane / 32, lc = lane % 32;
     if constexpr (EPI == EPI_SCORES || EPI == EPI_DSCORES) {
         const float g = p.g[0];
+        // the transpose and the residual are optional (a prefill has no backward
+        // to read them): without them their buffers have no range, and the
+        // stores to them are dropped
         const rsrc_t rp = rsrc(reinterpret_cast<char *>(p.pout) + b * p.p_bstride, p.p_bstride);
-        const rsrc_t rpt = rsrc(reinterpret_cast<char *>(p.pout_t) + b * p.p_bstride, p.p_bstride);
+        const bool want_t = p.pout_t != nullptr;
+        const rsrc_t rpt = rsrc(want_t ? reinterpret_cast<char *>(p.pout_t) + b * p.p_bstride : nullptr,
+                                want_t ? p.p_bstride : 0);
         // DSCORES reads P and its residual; SCORES writes the residual
         const rsrc_t rpin = rsrc(EPI == EPI_DSCORES ? reinterpret_cast<const char *>(p.pin) + b * p.p_bstride
                                                     : reinterpret_cast<const char *>(p.pout), p.p_bstride);
-        const rsrc_t rplo = rsrc(EPI == EPI_DSCORES ? reinterpret_cast<const char *>(p.pin_lo) + b * p.p_bstride
-                                                    : reinterpret_cast<const char *>(p.pout_lo) + b * p.p_bstride,
-                                 p.p_bstride);
+        const char *lo = EPI == EPI_DSCORES ? reinterpret_cast<const char *>(p.pin_lo)
+                                            : reinterpret_cast<const char *>(p.pout_lo);
+        const rsrc_t rplo = rsrc(lo ? lo + b * p.p_bstride : nullptr, lo ? p.p_bstride : 0);
         float dg = 0.f;
         // the transpose goes through the stage memory as bf16 [s][t] (rows
         // padded to XS elements), then out in 16-byte runs of t
@@ -518,7 +524,7 @@ __global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI, OU
         // the transpose: rows s, contraction t, 16 bytes (8 t) of one s per lane;
         // 32 consecutive lanes take the 32 rows s of one P-layout tile
 #pragma unroll 4
-        for (int c = threadIdx.x; c < TM * TN / 8; c += WV * 64) {
+        for (int c = threadIdx.x; want_t && c < TM * TN / 8; c += WV * 64) {
             const int sl = 32 * (c / (32 * (TN / 8))) + c % 32, t8 = (c / 32) % (TN / 8);
             const int s = m0 + sl, t = n0 + 8 * t8;
             const gv4u32_t v = *reinterpret_cast<const gv4u32_t *>(Xt + sl * XS + 8 * t8);
@@ -892,7 +898,8 @@ __global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI, OU
         auto elem = [&](int i, int j, int r, uint32_t &bad) -> uint32_t {
             const int n = n0 + wn * (TN / 2) + 32 * j + lc;
             const int f = p.nperm ? (n & ~31) + perm32(n & 31) : n;
-            const int pos = m0 + wm * (TM / WM) + 32 * i + 8 * (r / 4) + 4 * h + r % 4;
+            const int mr = m0 + wm * (TM / WM) + 32 * i + 8 * (r / 4) + 4 * h + r % 4;
+            const int pos = p.mperm ? (mr & ~31) + perm32(mr & 31) : mr;
             bad = (f < p.F && pos < p.T) ? 0u : OOB;
             return static_cast<uint32_t>(pos) * p.F + f;
         };
@@ -1206,6 +1213,31 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, uint16_t *vQ, co
     f.nperm = 1;
     f.resid = resid;
     return launch<false, EPI_ROWS>(f, G, B, s);
+}
+
+// The decode state after position T-1 of every batch row, as one product over
+// positions: S[b][d][a] = sum_s v[b][s][d] kd[b][s][a], with kd the keys
+// decayed to T-1 (k_s lam^(T-1-s), fwd_stats' decayed Q-layout copy) and v in the
+// Q layout (Dp features). Rows of both operands are features in the perm32
+// order, so the row epilogue un-permutes both. S (B, D, A) fp32, overwritten.
+int launch_pair_state(const uint16_t *vQ, const uint16_t *kdQ, float *S, int B, int T, int A, int D, hipStream_t s) {
+    using namespace pair;
+    const int G = 128, NT = (T + 63) / 64;
+    const int Ap = (A + 31) / 32 * 32, Dp = (D + 31) / 32 * 32;
+    Args a{};
+    a.T = D;             // output rows: features d
+    a.a = q_mat(vQ, NT, Dp);
+    a.b = q_mat(kdQ, NT, Ap);
+    a.mt = (D + G - 1) / G;
+    a.nt = (A + G - 1) / G;
+    a.krange = K_FULL;
+    a.nks = 2 * NT;      // every position (those past T are zero in both operands)
+    a.out = S;
+    a.out_dt = ULM_F32;
+    a.F = A;
+    a.nperm = 1;
+    a.mperm = 1;
+    return launch<false, EPI_ROWS>(a, G, B, s);
 }
 
 // Bytes of the statistics workspace of launch_pair_backward: the per (batch

@@ -27,6 +27,7 @@ SIGNATURES = {
     "ulm_fm_saved_path": (I, [SZ, I, I, I, I, I]),
     "ulm_fm_fwd_workspace_bytes": (SZ, [I, I, I, I, I]),
     "ulm_fm_fwd": (I, [P, P, I, P, P, P, P, I, P, SZ, P, SZ, I, I, I, I, P]),
+    "ulm_fm_prefill_path": (I, [I, I, I, I]),
     "ulm_fm_prefill_workspace_bytes": (SZ, [I, I, I, I, I, I]),
     "ulm_fm_prefill": (I, [P, P, I, P, P, P, P, I, P, P, P, SZ, I, I, I, I, P]),
     "ulm_fm_bwd_workspace_bytes": (SZ, [I, I, I, I, I, SZ, I]),

@@ -166,15 +166,23 @@ __global__ __launch_bounds__(256) void decode_addr_vec_kernel(const float *__res
     const int A4 = A / 4;
     const f32x4 *p4 = reinterpret_cast<const f32x4 *>(pre + row);
     const f32x4 *b4 = reinterpret_cast<const f32x4 *>(bias);
-    f32x4 z[R4];
+    // every load unconditional at a clamped index and selected after, so that
+    // a loop's loads are in flight together (a load under a condition is
+    // waited for before the condition ends)
+    f32x4 z[R4], bz[R4];
+#pragma unroll
+    for (int k = 0; k < R4; ++k) {
+        const int j = threadIdx.x + 256 * k, jc = j < A4 ? j : 0;
+        z[k] = p4[jc];
+        bz[k] = bias ? b4[jc] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < R4; ++k) {
-        const int j = threadIdx.x + 256 * k;
-        f32x4 p = j < A4 ? p4[j] : f32x4{0.f, 0.f, 0.f, 0.f};
-        if (bias && j < A4) p += b4[j];
+        const bool ok = threadIdx.x + 256 * k < A4;
+        f32x4 p = z[k] + bz[k];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) p[e] = p[e] > 0.f ? p[e] * p[e] : 0.f;
+        for (int e = 0; e < 4; ++e) p[e] = ok && p[e] > 0.f ? p[e] * p[e] : 0.f;
         z[k] = p;
         s += (p[0] + p[1]) + (p[2] + p[3]);
     }
@@ -184,13 +192,20 @@ __global__ __launch_bounds__(256) void decode_addr_vec_kernel(const float *__res
     const f32x4 *w4 = reinterpret_cast<const f32x4 *>(w);
     const f32x4 *rp4 = reinterpret_cast<const f32x4 *>(r_prev + row);
     f32x4 *c4 = reinterpret_cast<f32x4 *>(c + row);
-    f32x4 qk[R4];
+    f32x4 qk[R4], wv[R4], rpv[R4], cv[R4];
+#pragma unroll
+    for (int k = 0; k < R4; ++k) {
+        const int j = threadIdx.x + 256 * k, jc = j < A4 ? j : 0;
+        wv[k] = w4[jc];
+        rpv[k] = rp4[jc];
+        cv[k] = c4[jc];
+    }
 #pragma unroll
     for (int k = 0; k < R4; ++k) {
         const int j = threadIdx.x + 256 * k;
         qk[k] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (j >= A4) continue;
-        const f32x4 wa = w4[j], rp = rp4[j], cn = lam * c4[j] + (1.f - lam) * wa + rp;
+        const f32x4 wa = wv[k], rp = rpv[k], cn = lam * cv[k] + (1.f - lam) * wa + rp;
         const f32x4 ra = z[k] * idn;
         f32x4 qa;
 #pragma unroll
@@ -211,17 +226,32 @@ __global__ __launch_bounds__(256) void decode_addr_vec_kernel(const float *__res
     const size_t n = blockIdx.x;
     float dt[kMaxPending];
 #pragma unroll
-    for (int t = 0; t < kMaxPending; ++t) {
-        dt[t] = 0.f;
-        if (t > mslot) continue;
-        const f32x4 *p4 = reinterpret_cast<const f32x4 *>(pr + static_cast<size_t>(t) * N * A + row);
+    for (int t = 0; t < kMaxPending; ++t) dt[t] = 0.f;
+    // terms in groups of 4, each group's loads unconditional (terms past the
+    // slot clamped to it and selected away), so a group's loads are in flight
+    // together; the groups past the slot are skipped
 #pragma unroll
-        for (int k = 0; k < R4; ++k) {
-            const int j = threadIdx.x + 256 * k;
-            const f32x4 pk = p4[j < A4 ? j : 0];   // clamped load; selected away past A
-            const f32x4 u = pk * qk[k];
-            dt[t] += j < A4 ? (u[0] + u[1]) + (u[2] + u[3]) : 0.f;
+    for (int t0 = 0; t0 < kMaxPending; t0 += 4) {
+        if (t0 > mslot) break;
+        f32x4 pk[4][R4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int t = min(t0 + u, mslot);
+            const f32x4 *p4 = reinterpret_cast<const f32x4 *>(pr + static_cast<size_t>(t) * N * A + row);
+#pragma unroll
+            for (int k = 0; k < R4; ++k) {
+                const int j = threadIdx.x + 256 * k;
+                pk[u][k] = p4[j < A4 ? j : 0];   // clamped load; selected away past A
+            }
         }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int k = 0; k < R4; ++k) {
+                const f32x4 v = pk[u][k] * qk[k];
+                const bool ok = threadIdx.x + 256 * k < A4 && t0 + u <= mslot;
+                dt[t0 + u] += ok ? (v[0] + v[1]) + (v[2] + v[3]) : 0.f;
+            }
     }
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
 #pragma unroll

@@ -346,7 +346,7 @@ __global__ __launch_bounds__(256) void decode_read_kernel(const float *__restric
     }
 }
 
-constexpr int kFlushRows = 32;   // rows (features) per workgroup
+constexpr int kFlushRows = 64;   // rows (features) per workgroup
 // rows whose loads a lane has in flight at once: 8 where the registers allow
 // (12 waves, 168 VGPRs), else 4
 template <int MAXW> constexpr int flush_batch() { return MAXW <= 12 ? 8 : 4; }

@@ -74,3 +74,30 @@ def test_compiled_model_matches_eager(autocast):
     errs.update({n: rel(p.grad, g_e[n]) for n, p in model.named_parameters()})
     say(f"  worst {max(errs.values()):.3e}")
     assert max(errs.values()) < 1e-5, errs
+
+
+@pytest.mark.gpu
+def test_eager_function_matches_registered_op():
+    """unified_memory on plain tensors calls the native kernels through a plain
+    autograd Function; the registered op pair (what torch.compile traces) must
+    give the same outputs and gradients bit for bit."""
+    from helpers import say
+    import workloads
+    B, T, D, A = 2, 200, 64, 140
+    say(f"eager Function vs registered op, B={B} T={T} D={D} A={A}")
+    r, v, g, w = workloads.block_inputs(B, T, D, A, seed=7, device=torch.device("cuda"), v_dtype=torch.bfloat16)
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    dq = torch.randn(B, T, A, device="cuda", generator=gen) * 0.01
+    df = torch.randn(B, T, D, device="cuda", generator=gen).to(torch.bfloat16)
+    res = []
+    for eager in (True, False):
+        leaves = [t.detach().clone().requires_grad_(True) for t in (r, v, g, w)]
+        if eager:
+            assert kernel._plain_eager(*leaves)
+            q, fast = kernel.unified_memory(*leaves)
+        else:
+            q, fast, _ = kernel.fm_fwd(*leaves)
+        grads = torch.autograd.grad((q, fast), leaves, (dq, df))
+        res.append([q, fast, *grads])
+    for a, b in zip(*res):
+        assert a.dtype == b.dtype and torch.equal(a, b)

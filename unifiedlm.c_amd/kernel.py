@@ -61,8 +61,7 @@ def _check_fm(r, v, g, w):
 Tensor = torch.Tensor
 
 
-@torch.library.custom_op("ulm::fm_fwd", mutates_args=())
-def fm_fwd(r: Tensor, v: Tensor, g: Tensor, w: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+def _fm_fwd_impl(r: Tensor, v: Tensor, g: Tensor, w: Tensor) -> tuple[Tensor, Tensor, Tensor]:
     """(q fp32, fast in v's dtype, saved uint8): ulm_fm_fwd."""
     B, T, A = r.shape
     D = v.shape[-1]
@@ -82,6 +81,9 @@ def fm_fwd(r: Tensor, v: Tensor, g: Tensor, w: Tensor) -> tuple[Tensor, Tensor, 
     return q, fast, saved
 
 
+fm_fwd = torch.library.custom_op("ulm::fm_fwd", mutates_args=())(_fm_fwd_impl)
+
+
 @fm_fwd.register_fake
 def _fm_fwd_fake(r, v, g, w):
     B, T, A = r.shape
@@ -91,9 +93,8 @@ def _fm_fwd_fake(r, v, g, w):
             r.new_empty(saved_bytes, dtype=torch.uint8))
 
 
-@torch.library.custom_op("ulm::fm_bwd", mutates_args=())
-def fm_bwd(r: Tensor, g: Tensor, w: Tensor, saved: Tensor, v_dtype: torch.dtype, dq_out: Optional[Tensor],
-           dfast: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+def _fm_bwd_impl(r: Tensor, g: Tensor, w: Tensor, saved: Tensor, v_dtype: torch.dtype, dq_out: Optional[Tensor],
+                 dfast: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """(dr fp32, dv in dfast's dtype, dg (1,), dw (A,)): ulm_fm_bwd."""
     B, T, A = r.shape
     D = dfast.shape[-1]
@@ -115,6 +116,9 @@ def fm_bwd(r: Tensor, g: Tensor, w: Tensor, saved: Tensor, v_dtype: torch.dtype,
     return dr, dv, dg, dw
 
 
+fm_bwd = torch.library.custom_op("ulm::fm_bwd", mutates_args=())(_fm_bwd_impl)
+
+
 @fm_bwd.register_fake
 def _fm_bwd_fake(r, g, w, saved, v_dtype, dq_out, dfast):
     B, T, A = r.shape
@@ -133,24 +137,58 @@ def _fm_setup(ctx, inputs, output):
     ctx.set_materialize_grads(False)
 
 
-def _fm_backward(ctx, dq_out, dfast, _dsaved):
+def _fm_backward_with(bwd, ctx, dq_out, dfast):
     r, g, w, saved = ctx.saved_tensors
     if dq_out is None and dfast is None:
         return None, None, None, None
     if dfast is None:
         dfast = r.new_zeros(*r.shape[:2], ctx.D, dtype=torch.float32)
-    dr, dv, dg, dw = fm_bwd(r, g, w, saved, ctx.v_dtype, dq_out, dfast)
+    dr, dv, dg, dw = bwd(r, g, w, saved, ctx.v_dtype, dq_out, dfast)
     return dr, dv, dg.reshape(g.shape), dw
 
 
+def _fm_backward(ctx, dq_out, dfast, _dsaved):
+    return _fm_backward_with(fm_bwd, ctx, dq_out, dfast)
+
+
 torch.library.register_autograd("ulm::fm_fwd", _fm_backward, setup_context=_fm_setup)
+
+
+def _plain_eager(*tensors):
+    """True when the call runs eagerly on plain tensors: no torch.compile
+    trace, no dispatch mode (fake tensors, functionalization) and no tensor
+    subclass, so the native kernels can be called without the registered
+    op's dispatch."""
+    if torch.compiler.is_compiling() or torch._C._len_torch_dispatch_stack() > 0:
+        return False
+    return all(type(t) is torch.Tensor for t in tensors)
+
+
+class _FMEager(torch.autograd.Function):
+    """The registered op pair ulm::fm_fwd / ulm::fm_bwd as a plain autograd
+    Function over the same implementations: the eager path, without the
+    registered ops' dispatch (about 20 us of host time per call, which
+    small shapes feel). torch.compile traces the registered ops instead."""
+
+    @staticmethod
+    def forward(ctx, r, v, g, w):
+        out = _fm_fwd_impl(r, v, g, w)
+        _fm_setup(ctx, (r, v, g, w), out)
+        return out
+
+    @staticmethod
+    def backward(ctx, dq_out, dfast, _dsaved):
+        return _fm_backward_with(_fm_bwd_impl, ctx, dq_out, dfast)
 
 
 def unified_memory(r, v, g, w):
     """r: (B,T,M) read addresses, v: (B,T,D) values, g: scalar log decay, w: (M,) prior mass.
     Returns (q fp32, fast in v's dtype) (kernel.py:236-238)."""
     _check_fm(r, v, g, w)
-    q, fast, _ = fm_fwd(r, v, g, w)
+    if _plain_eager(r, v, g, w):
+        q, fast, _ = _FMEager.apply(r, v, g, w)
+    else:
+        q, fast, _ = fm_fwd(r, v, g, w)
     return q, fast
 
 

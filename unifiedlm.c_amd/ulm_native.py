@@ -118,7 +118,8 @@ def ptr(t):
 
 
 def stream_of(t):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    """The current stream of t's device, as the hipStream_t the entry points take."""
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(t.get_device()))
 
 
 def require_device(*tensors):

@@ -99,6 +99,10 @@ enum Epi { EPI_SCORES = 0, EPI_DSCORES = 1, EPI_ROWS = 2, EPI_DQSTATS = 3 };
 // plus an fp32 residual, OUT_DRADD the backward's dr accumulation of dk_f
 constexpr int OUT_DRADD = 6;
 enum KRange { K_FULL = 0, K_CAUSAL = 1, K_ANTI = 2 };
+// EPI_SCORES with fewer 128 x 128 tile jobs than CUs: one workgroup per CU
+// holds them all, so its stages go to depth instead (96 KB: five k-steps of
+// copies in flight instead of two, against the latency of each k-step's reads)
+constexpr int kScoresDeep = 1;
 
 // LDS stages of operand copies (NSTAGE - 1 k-steps in flight): all 160 KB of LDS
 // at 256 x 256 tiles (32 KB per stage); at 128 x 128, 64 KB (two workgroups
@@ -106,6 +110,7 @@ enum KRange { K_FULL = 0, K_CAUSAL = 1, K_ANTI = 2 };
 // CU) for the scores and dscores, whose equal jobs (B T^2 / 2 G^2 of them)
 // would otherwise leave a short second wave
 template <int TM, int EPI, int OUT = 0> constexpr int nstage() {
+    if (TM == 128 && EPI == EPI_SCORES && OUT == kScoresDeep) return 6;
     return TM == 256 ? 5 : (EPI == EPI_SCORES || EPI == EPI_DSCORES || OUT == OUT_DRADD ? 3 : 4);
 }
 template <int TM, int EPI, int OUT = 0> constexpr int min_blocks() {
@@ -1080,6 +1085,10 @@ int launch(const Args &a, int G, int B, hipStream_t s) {
         case 4: return launch_o<TA, false, EPI, 4>(a, G, B, s);
         default: return launch_o<TA, false, EPI, 5>(a, G, B, s);
         }
+    } else if constexpr (EPI == EPI_SCORES) {
+        const int tiles = B * (a.tri ? a.mt * (a.mt + 1) / 2 : a.mt * a.nt);
+        if (G == 128 && tiles < 256) return launch_g<128, TA, false, EPI, kScoresDeep>(a, B, s);
+        return launch_o<TA, false, EPI, 0>(a, G, B, s);
     } else if constexpr (EPI != EPI_ROWS) {
         return launch_o<TA, false, EPI, 0>(a, G, B, s);
     } else {

@@ -366,22 +366,6 @@ int ulm_decode_flush(float *S, const float *pv, const float *pr, int m, const fl
 int ulm_la_timer_start(int max_launches);
 int ulm_la_timer_stop(double *total_ms, int *launches);
 
-/* Writes, for lane l of one wave, the operand/result layout of
- * one v_mfma_f32_32x32x16_bf16 on A = a (32x16 row-major), B = b (16x32
- * row-major): d (32x32 row-major) = A B computed through the kernels' own
- * operand-loading helpers. No counterpart in the reference. */
-int ulm_probe_mfma(const uint16_t *a, const uint16_t *b, float *d, void *stream);
-
-/* LDS transpose read: lane L of one wave addresses elements 4L..4L+3 of the
- * 256 16-bit values in src (staged in LDS) with ds_read_b64_tr_b16 and writes
- * the 4 values it receives to dst[4L..4L+3]. */
-int ulm_probe_lds_tr(const uint16_t *src, uint16_t *dst, void *stream);
-
-/* Buffer-to-LDS DMA: lane L loads 16 bytes at byte offset offsets[L] of src
- * (n floats; offsets past the end read as zero) with buffer_load_dwordx4
- * ... lds; the 256-float LDS image is copied to dst. */
-int ulm_probe_lds_dma(const float *src, int n, const int *offsets, float *dst, void *stream);
-
 #ifdef __cplusplus
 }
 #endif

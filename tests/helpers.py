@@ -1,5 +1,7 @@
 """Shared fixtures of the GPU parity tests."""
+import ctypes
 import math
+import os
 import sys
 
 import torch
@@ -57,3 +59,37 @@ def fm_inputs(B, T, A, D, seed=0, device="cuda", lam=None, zero_frac=0.5):
         lam = torch.sigmoid(3.0 + 0.5 * torch.randn((), generator=gen, dtype=torch.float64))
     g = torch.log(torch.as_tensor(lam, dtype=torch.float64))
     return [t.to(device) for t in (r, v, g, w)]
+
+
+# ---- the test-only probe library (libulm_probe.so, include/ulm_probe.h)
+_probe = None
+PROBE_SIGNATURES = {
+    "ulm_probe_mfma": (ctypes.c_int, [ctypes.c_void_p] * 4),
+    "ulm_probe_lds_tr": (ctypes.c_int, [ctypes.c_void_p] * 3),
+    "ulm_probe_lds_dma": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                         ctypes.c_void_p]),
+    "ulm_last_error": (ctypes.c_char_p, []),
+}
+
+
+def probe_lib():
+    """The layout-probe library built beside libulm_fm.so; raises if missing."""
+    global _probe
+    if _probe is None:
+        import ulm_native as nat
+        path = os.path.join(os.path.dirname(nat.LIB_PATH), "libulm_probe.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: build it with `python unifiedlm.c_amd/build.py`")
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in PROBE_SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = res, args
+        _probe = lib
+    return _probe
+
+
+def probe_call(name, *args):
+    """Calls a probe and raises RuntimeError on a nonzero status."""
+    st = getattr(probe_lib(), name)(*args)
+    if st != 0:
+        raise RuntimeError(f"{name} failed with status {st}: {probe_lib().ulm_last_error().decode(errors='replace')}")

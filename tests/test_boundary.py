@@ -13,8 +13,8 @@ HEADER = os.path.join(ROOT, "include", "ulm_fm.h")
 import ulm_native as nat  # noqa: E402
 
 
-def header_functions():
-    text = open(HEADER).read()
+def header_functions(header=HEADER):
+    text = open(header).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(ulm_\w+)\s*\(", text)))
 
@@ -27,6 +27,21 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert sorted(nat.SIGNATURES) == declared
     assert lib.ulm_abi_version() == 3
+
+
+def test_probes_live_in_the_test_library_only():
+    """The layout probes (include/ulm_probe.h) are exported by the test-only
+    libulm_probe.so and not by the product library."""
+    from helpers import PROBE_SIGNATURES, probe_lib
+    declared = header_functions(os.path.join(ROOT, "include", "ulm_probe.h"))
+    assert declared == sorted(n for n in PROBE_SIGNATURES if n.startswith("ulm_probe_"))
+    plib = probe_lib()
+    lib = nat.lib()
+    for name in declared:
+        assert hasattr(plib, name), name
+        assert not hasattr(lib, name), name
+    st = plib.ulm_probe_mfma(None, None, None, None)
+    assert st == nat.ULM_ERR_INVALID and b"null pointer" in plib.ulm_last_error()
 
 
 def test_c_side_rejects_bad_sizes_without_touching_the_gpu():

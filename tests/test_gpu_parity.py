@@ -9,7 +9,7 @@ import math
 import pytest
 import torch
 
-from helpers import fm_inputs, oracle_params, rel, say, tiny_model
+from helpers import fm_inputs, oracle_params, probe_call, rel, say, tiny_model
 from oracle import fastmem as fm
 
 pytestmark = pytest.mark.gpu
@@ -23,7 +23,10 @@ def test_mfma_operand_layout():
     gen = torch.Generator().manual_seed(0)
     a = torch.randn(32, 16, generator=gen).to(torch.bfloat16)
     b = torch.randn(16, 32, generator=gen).to(torch.bfloat16)
-    d = kernel.probe_mfma(a.cuda(), b.cuda()).cpu()
+    a16, b16 = a.cuda(), b.cuda()
+    d = torch.empty(32, 32, device="cuda")
+    probe_call("ulm_probe_mfma", nat.ptr(a16), nat.ptr(b16), nat.ptr(d), nat.stream_of(a16))
+    d = d.cpu()
     ref = a.double() @ b.double()
     assert (d.double() - ref).abs().max() < 1e-4
 
@@ -383,7 +386,7 @@ def test_lds_transpose_read_layout():
     say("probe ds_read_b64_tr_b16")
     src = torch.arange(256, dtype=torch.int32).to(torch.int16).cuda()
     dst = torch.zeros(256, dtype=torch.int16, device="cuda")
-    nat.call("ulm_probe_lds_tr", nat.ptr(src), nat.ptr(dst), nat.stream_of(src))
+    probe_call("ulm_probe_lds_tr", nat.ptr(src), nat.ptr(dst), nat.stream_of(src))
     got = dst.cpu().view(64, 4).long()
     L = torch.arange(64)[:, None]
     e = torch.arange(4)[None, :]
@@ -400,7 +403,7 @@ def test_buffer_lds_dma_layout():
     offs = [16 * (63 - L) for L in range(60)] + [4 * n + 1000] * 4
     offsets = torch.tensor(offs, dtype=torch.int32).cuda()
     dst = torch.zeros(256, device="cuda")
-    nat.call("ulm_probe_lds_dma", nat.ptr(src), n, nat.ptr(offsets), nat.ptr(dst), nat.stream_of(src))
+    probe_call("ulm_probe_lds_dma", nat.ptr(src), n, nat.ptr(offsets), nat.ptr(dst), nat.stream_of(src))
     got = dst.cpu().view(64, 4)
     exp = torch.zeros(64, 4)
     for L in range(60):

@@ -402,22 +402,6 @@ int launch_la_generic(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
     return launch_partial_reduce(part, nK, plane, out, ULM_F32, s, nullptr);
 }
 
-// ---- layout probe: one wave, D (32x32) = A (32x16) B (16x32) through the
-// operand conventions above.
-__global__ void probe_mfma_kernel(const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, float *__restrict__ d) {
-    const int lane = threadIdx.x, lr = lane % 32, lh = lane / 32;
-    bf16x8 x, y;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        x[e] = __builtin_bit_cast(bf16, a[lr * 16 + 8 * lh + e]);
-        y[e] = __builtin_bit_cast(bf16, b[(8 * lh + e) * 32 + lr]);
-    }
-    f32x16 acc = {};
-    acc = mfma(x, y, acc);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) d[(8 * (r / 4) + 4 * lh + (r % 4)) * 32 + lr] = acc[r];
-}
-
 }  // namespace ulm
 
 using namespace ulm;
@@ -458,10 +442,4 @@ extern "C" int ulm_la_timer_stop(double *total_ms, int *launches) {
     *launches = g_la_timer.used;
     g_la_timer.used = 0;
     return ULM_OK;
-}
-
-extern "C" int ulm_probe_mfma(const uint16_t *a, const uint16_t *b, float *d, void *stream) {
-    ULM_REQUIRE(a && b && d, "ulm_probe_mfma: null pointer");
-    probe_mfma_kernel<<<1, 64, 0, static_cast<hipStream_t>(stream)>>>(a, b, d);
-    return check_launch("probe_mfma_kernel");
 }

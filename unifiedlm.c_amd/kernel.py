@@ -737,12 +737,3 @@ def decode_deferred(S, pv, pr, m, flush, q, g, x, ymu, cj=None):
         call("ulm_decode_read", ptr(_f32c(S)), ptr(_f32c(pv)), ptr(_f32c(cj)), m, ptr(_f32c(q)), ptr(_f32c(g)),
              ptr(_f32c(x)), ptr(_f32c(ymu)), ptr(out), N, D, A, st)
     return out
-
-
-def probe_mfma(a, b):
-    """D = A B (A 32x16, B 16x32, bf16) through the kernels' MFMA operand layout."""
-    a16 = a.to(torch.bfloat16).contiguous()
-    b16 = b.to(torch.bfloat16).contiguous()
-    d = torch.empty(32, 32, device=a.device, dtype=torch.float32)
-    call("ulm_probe_mfma", ptr(a16), ptr(b16), ptr(d), nat.stream_of(a))
-    return d

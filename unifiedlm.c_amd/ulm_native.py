@@ -61,9 +61,6 @@ SIGNATURES = {
     "ulm_decode_flush": (I, [P, P, P, I, P, P, P, P, P, I, I, I, P]),
     "ulm_la_timer_start": (I, [I]),
     "ulm_la_timer_stop": (I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]),
-    "ulm_probe_mfma": (I, [P, P, P, P]),
-    "ulm_probe_lds_tr": (I, [P, P, P]),
-    "ulm_probe_lds_dma": (I, [P, I, P, P, P]),
 }
 
 

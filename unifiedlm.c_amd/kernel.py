@@ -154,12 +154,16 @@ def _fm_backward(ctx, dq_out, dfast, _dsaved):
 torch.library.register_autograd("ulm::fm_fwd", _fm_backward, setup_context=_fm_setup)
 
 
+# the number of active torch dispatch modes (one assumed where torch does not say)
+_dispatch_modes = getattr(torch._C, "_len_torch_dispatch_stack", lambda: 1)
+
+
 def _plain_eager(*tensors):
     """True when the call runs eagerly on plain tensors: no torch.compile
     trace, no dispatch mode (fake tensors, functionalization) and no tensor
     subclass, so the native kernels can be called without the registered
     op's dispatch."""
-    if torch.compiler.is_compiling() or torch._C._len_torch_dispatch_stack() > 0:
+    if torch.compiler.is_compiling() or _dispatch_modes() > 0:
         return False
     return all(type(t) is torch.Tensor for t in tensors)
 

@@ -114,9 +114,15 @@ def ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t):
-    """The current stream of t's device, as the hipStream_t the entry points take."""
-    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(t.get_device()))
+    """The current stream of t's device, as the hipStream_t the entry points take
+    (read without building a Python stream object where torch offers that)."""
+    if _raw_stream is not None:
+        return ctypes.c_void_p(_raw_stream(t.get_device()))
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
 def require_device(*tensors):

@@ -249,7 +249,7 @@ def bench_configs(torch, args):
     import workloads
     out = {}
     for shape in ("15M", "42M", "ref-15M", "ref-42M"):
-        t = bench_training(torch, args, shape=shape, steps=max(args.steps, 10), warmup=max(args.warmup, 3))
+        t = bench_training(torch, args, shape=shape, steps=max(args.steps, 50), warmup=max(args.warmup, 5))
         out[shape] = {"workload": f"fast-memory fwd+bwd, one block of the {shape} shape (B={t['B']}, T={t['T']}, "
                                   f"D={t['D']}, A={t['A']})",
                       "path": t["path"], "ms_per_block": round(t["ms_step"], 4), "Mtok_per_s": round(t["value"], 4),

@@ -133,7 +133,7 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *__restrict__
     }
 }
 
-// The bf16 case of transpose_kernel with X % 64 == 0 and the layouts X wide:
+// The bf16 case of transpose_kernel with X % 32 == 0 and the layouts X wide:
 // grid (ceil(X / 256), NT, B), 256 threads, one tile_copy_bf16 job (64
 // positions x 256 features) per workgroup.
 __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t *__restrict__ src, uint16_t *__restrict__ raw,
@@ -326,7 +326,7 @@ int launch_chunk_transpose(const void *src, int src_dt, uint16_t *raw, uint16_t 
     if (raw_lo && !raw) return fail(ULM_ERR_INVALID, "chunk transpose: raw_lo needs raw");
     if (xr_lo && !xr) return fail(ULM_ERR_INVALID, "chunk transpose: xr_lo needs xr");
     const int NT = (T + ULM_CHUNK - 1) / ULM_CHUNK;
-    if (src_dt == ULM_BF16 && X % 64 == 0 && XL == X && !raw_lo && !xr_lo && reinterpret_cast<uintptr_t>(src) % 16 == 0) {
+    if (src_dt == ULM_BF16 && X % 32 == 0 && XL == X && !raw_lo && !xr_lo && reinterpret_cast<uintptr_t>(src) % 16 == 0) {
         const dim3 grid((X + 4 * ULM_CHUNK - 1) / (4 * ULM_CHUNK), NT, B);
         chunks::transpose_bf16_kernel<<<grid, 256, 0, s>>>(static_cast<const uint16_t *>(src), raw, xr, T, X, NT);
         return check_launch("chunk transpose_bf16_kernel");

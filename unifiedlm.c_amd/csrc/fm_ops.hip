@@ -411,7 +411,7 @@ int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const 
     if (path == PATH_PAIR) {
         // q, k: R layout for the scores (this pass only), Q layout for the
         // backward's dk_f, dq_f; v: Q layout for the apply, R layout for the
-        // backward's dscores. bf16 v with D % 64 == 0 is tiled by the scores
+        // backward's dscores. bf16 v with D % 32 == 0 is tiled by the scores
         // launch, on the CUs its tiles leave idle; other v by a launch of its own.
         // A prefill (state wanted) has no backward: no qQ, vR, P^T or P residual;
         // kQ holds the keys decayed to T-1, and the state is one product of them
@@ -420,7 +420,7 @@ int fm_forward(const RSrc &r, const void *v, int v_dtype, const float *g, const 
         if (prefill != (c_last != nullptr)) return fail(ULM_ERR_INVALID, "prefill: state and c_last go together");
         ULM_TRY(launch_fwd_stats(r, w, g, q, nullptr, nullptr, ws.qR, ws.kR, prefill ? nullptr : sv.qQ, sv.kQ, sv.nck,
                                  c_last, B, T, A, s, qw, qw_dt, pad32(A), ws.segtot, prefill ? 1 : 0));
-        const bool ride = v_dtype == ULM_BF16 && D % 64 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0;
+        const bool ride = v_dtype == ULM_BF16 && D % 32 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0;
         uint16_t *vR = prefill ? nullptr : sv.vR;
         if (!ride) ULM_TRY(launch_chunk_transpose(v, v_dtype, ws.vQ, nullptr, vR, nullptr, B, T, D, s, pad32(D)));
         ULM_TRY(launch_pair_forward(ws.qR, ws.kR, ws.vQ, g, sv.P, prefill ? nullptr : sv.Pt, prefill ? nullptr : sv.Plo,

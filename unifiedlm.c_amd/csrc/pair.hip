@@ -1165,7 +1165,7 @@ int side_stream(SideStream *&out) {
 // P = scores(q, k) in the P layout (Tq x Tq per batch row), its transpose
 // Pt and its bf16 residual Plo (P layout), then out = P v (+ resid) in out_dt
 // (B, T, D). qR, kR: R layout (A); vQ: Q layout (D). With v (bf16 (B, T, D),
-// D % 64 == 0, 16-byte aligned) the scores launch also writes vQ and vR (the R
+// D % 32 == 0, 16-byte aligned) the scores launch also writes vQ and vR (the R
 // layout, or null) from it; else vQ is an input.
 int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, uint16_t *vQ, const float *g, uint16_t *P,
                         uint16_t *Pt, uint16_t *Plo, void *out, int out_dt, const float *resid, int B, int T, int A,
@@ -1196,8 +1196,8 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, uint16_t *vQ, co
     a.p_bstride = pm.bstride;
     a.p_rt = pm.rt;
     if (v) {
-        if (D % 64 || reinterpret_cast<uintptr_t>(v) % 16)
-            return fail(ULM_ERR_INVALID, "pair forward: v tile copies need D %% 64 == 0 and 16-byte rows (D=%d)", D);
+        if (D % 32 || reinterpret_cast<uintptr_t>(v) % 16)
+            return fail(ULM_ERR_INVALID, "pair forward: v tile copies need D %% 32 == 0 and 16-byte rows (D=%d)", D);
         a.NT = NT;
         a.cp_src = v;
         a.cp_q = vQ;

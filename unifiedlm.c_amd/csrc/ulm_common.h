@@ -209,7 +209,7 @@ struct Carver {
     }
 };
 
-// ---- the bf16 tile copies of a (B, T, X) tensor, X % 64 == 0
+// ---- the bf16 tile copies of a (B, T, X) tensor, X % 32 == 0
 //
 // One job: the 64 positions of chunk n x 256 features from xw, on 256 threads
 // (tid), into the Q layout (raw) and the R layout (xr), either null; the
@@ -235,7 +235,8 @@ __device__ __forceinline__ void tile_copy_bf16(const uint16_t *__restrict__ src,
 #pragma unroll
     for (int k = 0; k < NB; ++k) {
         const int x0 = xw + k * C;
-        const bool ok = live && t < T && x0 < X;
+        // 16 features per thread: with X % 32 == 0 the block's second half may lie past X
+        const bool ok = live && t < T && x0 + 16 * c < X;
         const uint4 *p = reinterpret_cast<const uint4 *>(src + (static_cast<size_t>(b) * T + (ok ? t : 0)) * X +
                                                          (ok ? x0 : 0) + 16 * c);
 #pragma unroll
@@ -247,7 +248,7 @@ __device__ __forceinline__ void tile_copy_bf16(const uint16_t *__restrict__ src,
         if (!live || x0 >= X) break;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            if (xr) *reinterpret_cast<uint4 *>(xr + r_index(b, t, x0 + 16 * c + 8 * h, NT, X)) = v[k][h];
+            if (xr && x0 + 16 * c < X) *reinterpret_cast<uint4 *>(xr + r_index(b, t, x0 + 16 * c + 8 * h, NT, X)) = v[k][h];
             if (raw) *reinterpret_cast<uint4 *>(&tile[k][i][8 * c + 4 * h]) = v[k][h];
         }
     }
@@ -269,6 +270,7 @@ __device__ __forceinline__ void tile_copy_bf16(const uint16_t *__restrict__ src,
             e1[e] = (w[2 * e] >> 16) | (w[2 * e + 1] & 0xffff0000u);
         }
         const int t0 = n * C + 8 * g;
+        if (x0 + 2 * fp >= X) continue;   // the block's second half past X (X % 64 == 32)
         *reinterpret_cast<uint4 *>(raw + q_index(b, t0, x0 + 2 * fp, NT, X)) = make_uint4(e0[0], e0[1], e0[2], e0[3]);
         *reinterpret_cast<uint4 *>(raw + q_index(b, t0, x0 + 2 * fp + 1, NT, X)) =
             make_uint4(e1[0], e1[1], e1[2], e1[3]);

@@ -475,13 +475,29 @@ __global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI, OU
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
             const int t = n0 + wn * (TN / 2) + 32 * j + lc;
+            auto off_of = [&](int i, int r4) -> uint32_t {
+                const int s0 = m0 + wm * (TM / WM) + 32 * i + 8 * r4 + 4 * h;
+                return (t / 32) * p.p_rt + (s0 / 16) * TB + 16u * (t % 32 + 32 * ((s0 % 16) / 8)) + 2u * (s0 % 8);
+            };
+            // DSCORES: this column's P and residual loads all issued before its
+            // first store: as far as the compiler knows a store may alias them, so
+            // interleaved, each load pair waited for the stores before it
+            v2u32_t pvs[MI][4], pls[MI][4];
+            if constexpr (EPI == EPI_DSCORES) {
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4) {
+                        pvs[i][r4] = __builtin_amdgcn_raw_buffer_load_b64(rpin, off_of(i, r4), 0, 0);
+                        pls[i][r4] = __builtin_amdgcn_raw_buffer_load_b64(rplo, off_of(i, r4), 0, 0);
+                    }
+            }
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int r4 = 0; r4 < 4; ++r4) {
                     const int s0 = m0 + wm * (TM / WM) + 32 * i + 8 * r4 + 4 * h;
-                    const uint32_t off = (t / 32) * p.p_rt + (s0 / 16) * TB + 16u * (t % 32 + 32 * ((s0 % 16) / 8)) +
-                                         2u * (s0 % 8);
+                    const uint32_t off = off_of(i, r4);
                     float x[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
@@ -493,8 +509,7 @@ __global__ __launch_bounds__((waves_of<TM, EPI>() * 64), (min_blocks<TM, EPI, OU
                         // P to about 16 significant bits (bf16 value + bf16 residual):
                         // the lag-weighted sum cancels heavily, and one bf16 rounding
                         // of P alone moves it by about 1e-2
-                        const v2u32_t pv = __builtin_amdgcn_raw_buffer_load_b64(rpin, off, 0, 0);
-                        const v2u32_t pl = __builtin_amdgcn_raw_buffer_load_b64(rplo, off, 0, 0);
+                        const v2u32_t pv = pvs[i][r4], pl = pls[i][r4];
                         const float pe[4] = {bf16_to_f32(pv[0] & 0xffffu) + bf16_to_f32(pl[0] & 0xffffu),
                                              bf16_to_f32(pv[0] >> 16) + bf16_to_f32(pl[0] >> 16),
                                              bf16_to_f32(pv[1] & 0xffffu) + bf16_to_f32(pl[1] & 0xffffu),

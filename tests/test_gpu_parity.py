@@ -5,6 +5,7 @@ gradient (test_all.py:166); fp32 decode 1e-5 relative to forward_recurrent.
 Every case prints its name before touching the GPU.
 """
 import math
+import random
 
 import pytest
 import torch
@@ -128,6 +129,26 @@ def test_unified_memory_matches_oracle(B, T, A, D, vdt):
     errs = {"dr": rel(rg.grad, dr), "dv": rel(vg.grad, dv), "dg": rel(gg.grad, dgr), "dw": rel(wg.grad, dw)}
     say(f"  rel errors {errs}")
     assert max(errs.values()) < 1e-2, errs
+
+
+def _random_op_cases(n, seed):
+    """Seeded random shapes over the operator's edge cases: ragged chunks and
+    position tiles, widths on and off the 32 and 64 grids, few and many tile
+    jobs, fp32 and bf16 values."""
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(n):
+        cases.append((rng.choice([1, 2, 3, 4]), rng.choice([1, 17, 64, 65, 127, 128, 129, 200, 256, 300, 511, 640, 1100]),
+                      rng.choice([32, 64, 96, 100, 128, 140, 192, 288, 448, 712, 768]),
+                      rng.choice([16, 32, 48, 64, 96, 160, 224, 288, 320]),
+                      rng.choice([torch.float32, torch.bfloat16])))
+    return cases
+
+
+@pytest.mark.parametrize("B,T,A,D,vdt", _random_op_cases(24, 2026))
+def test_unified_memory_random_shapes(B, T, A, D, vdt):
+    """The checks of test_unified_memory_matches_oracle over seeded random shapes."""
+    test_unified_memory_matches_oracle(B, T, A, D, vdt)
 
 
 PATH_CASES = [

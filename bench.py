@@ -208,8 +208,48 @@ def bench_training(torch, args, shape=None, steps=None, warmup=None):
     if chunked_eq_launch:
         roof["chunked_equivalent_tflops"] = round(chunked_eq_launch, 2)
         roof["chunked_equivalent_frac"] = round(chunked_eq_launch / PEAK_BF16_TFLOPS, 4)
+    if path == "pair" and timer.products:
+        roof["products"] = pair_product_rooflines(timer.products, B, T, A, D,
+                                                  tfile if traffic is not None else None)
+        log("  per product: " + ", ".join(f"{k} {v['avg_us']} us" + (f" {v['frac_hbm_peak']:.2f} HBM" if "GBps" in v
+                                                                       else f" {v['frac_bf16_peak']:.2f} MFMA")
+                                          for k, v in roof["products"].items()))
     return dict(B=B, T=T, D=D, A=A, L=L, path=path, ms_step=ms_step, value=B * T / (ms_step * 1e-3) / 1e6,
                 roofline=roof, path_tflops=path_tflops, chunked_equivalent_tflops=chunk_eq)
+
+
+def pair_product_rooflines(products, B, T, A, D, traffic_file):
+    """Each block-pair product on its own: average launch time (the HIP events
+    of the timed pass, on the stream it ran on), its own algorithmic flops
+    (2A or 2D per causal pair) against the bf16 MFMA peak and, where the
+    recorded counters of this shape are at hand, its HBM bytes per launch
+    against the 8 TB/s peak. dv runs beside dscores on the second stream, so
+    both times include their sharing of the CUs."""
+    pairs = B * T * (T + 1) / 2
+    width = {"scores": A, "apply": D, "dscores": D, "dv": D, "dq_f": A, "dk_f": A, "state": A}
+    recorded = {}
+    if traffic_file:
+        with open(traffic_file) as f:
+            for key, rec in json.load(f).get("products", {}).items():
+                for name in ("dscores", "dq_f", "dk_f"):
+                    if key.startswith(name):
+                        recorded[name] = rec["bytes"]
+                if key.startswith("scores ("):
+                    recorded["scores"] = rec["bytes"]
+                if key.startswith("apply and dv"):
+                    recorded["apply"] = recorded["dv"] = rec["bytes"]
+    out = {}
+    for name, (ms, n) in products.items():
+        secs = ms * 1e-3 / n
+        tflops = 2 * width[name] * pairs / secs / 1e12
+        row = {"avg_us": round(secs * 1e6, 1), "launches": n, "tflops": round(tflops, 1),
+               "frac_bf16_peak": round(tflops / PEAK_BF16_TFLOPS, 4)}
+        if name in recorded:
+            gbps = recorded[name] / secs / 1e9
+            row.update(hbm_MB=round(recorded[name] / 1e6, 1), GBps=round(gbps, 1),
+                       frac_hbm_peak=round(gbps / PEAK_HBM_GBPS, 4))
+        out[name] = row
+    return out
 
 
 def bench_chunked(torch, args):

@@ -365,6 +365,19 @@ int ulm_decode_flush(float *S, const float *pv, const float *pr, int m, const fl
  * (its timings come from external scripts, docs/kernel.md:55-70). */
 int ulm_la_timer_start(int max_launches);
 int ulm_la_timer_stop(double *total_ms, int *launches);
+/* The share of the last stop()'s launches that one block-pair product made
+ * (tag one of ULM_PRODUCT_*; the chunked products carry no tag): their summed
+ * kernel time and their number. */
+enum {
+    ULM_PRODUCT_SCORES = 1,  /* P = lam^(t-s) q.k, with the v tile copies */
+    ULM_PRODUCT_APPLY = 2,   /* fast = P v */
+    ULM_PRODUCT_DSCORES = 3, /* dS = lam^(t-s) dfast.v, the decay gradient's pair sum */
+    ULM_PRODUCT_DV = 4,      /* dv = P^T dfast */
+    ULM_PRODUCT_DQSTATS = 5, /* dq_f = dS k with the backward statistics (writes dr) */
+    ULM_PRODUCT_DKDR = 6,    /* dk_f = dS^T q added into dr with the carry */
+    ULM_PRODUCT_STATE = 7    /* a prefill's decode state, one product over positions */
+};
+int ulm_la_timer_product(int tag, double *total_ms, int *launches);
 
 #ifdef __cplusplus
 }

@@ -325,19 +325,24 @@ __global__ __launch_bounds__(kThreads, 1) void la_kernel(const uint16_t *__restr
 // launch while enabled, so a benchmark can read the kernel's own average
 // duration on the stream it runs on. Process-wide and not thread-safe.
 namespace {
+constexpr int kTimerTags = 8;   // 0: untagged, else a ULM_PRODUCT_* value
 struct LaTimer {
     bool on = false;
     int cap = 0, used = 0;
     hipEvent_t *ev = nullptr;
+    int *tag = nullptr;
+    double tag_ms[kTimerTags] = {};   // the last stop()'s sums per tag
+    int tag_n[kTimerTags] = {};
 };
 LaTimer g_la_timer;
 bool g_la_timer_open = false;   // a begin without its end
 }  // namespace
 
-int la_timer_begin(hipStream_t s) {
+int la_timer_begin(hipStream_t s, int tag) {
     g_la_timer_open = g_la_timer.on && g_la_timer.used < g_la_timer.cap;
-    if (g_la_timer_open && hipEventRecord(g_la_timer.ev[2 * g_la_timer.used], s) != hipSuccess)
-        return check_launch("timer");
+    if (!g_la_timer_open) return ULM_OK;
+    g_la_timer.tag[g_la_timer.used] = tag >= 0 && tag < kTimerTags ? tag : 0;
+    if (hipEventRecord(g_la_timer.ev[2 * g_la_timer.used], s) != hipSuccess) return check_launch("timer");
     return ULM_OK;
 }
 
@@ -386,7 +391,7 @@ int launch_la_generic(const uint16_t *a, const uint16_t *b, const uint16_t *c, c
     }
     const dim3 grid(static_cast<unsigned>(total));
     const int tot = static_cast<int>(total);
-    int st = la_timer_begin(s);
+    int st = la_timer_begin(s, 0);
     if (st) return st;
     if (reverse) {
         if (vec) la_kernel<true, true><<<grid, kThreads, lds, s>>>(a, b, c, g, dst, plane, T, K, V, NT, nK, nV, tot);
@@ -409,6 +414,9 @@ using namespace ulm;
 extern "C" int ulm_la_timer_start(int max_launches) {
     ULM_REQUIRE(max_launches > 0 && max_launches <= 1 << 16, "ulm_la_timer_start: bad capacity %d", max_launches);
     if (g_la_timer.cap < max_launches) {
+        int *tag = new int[max_launches];
+        delete[] g_la_timer.tag;
+        g_la_timer.tag = tag;
         hipEvent_t *ev = new hipEvent_t[2 * max_launches];
         for (int i = 0; i < 2 * g_la_timer.cap; ++i) ev[i] = g_la_timer.ev[i];
         for (int i = 2 * g_la_timer.cap; i < 2 * max_launches; ++i)
@@ -431,15 +439,29 @@ extern "C" int ulm_la_timer_stop(double *total_ms, int *launches) {
     ULM_REQUIRE(total_ms && launches, "ulm_la_timer_stop: null pointer");
     g_la_timer.on = false;
     double tot = 0.0;
+    for (int t = 0; t < kTimerTags; ++t) {
+        g_la_timer.tag_ms[t] = 0.0;
+        g_la_timer.tag_n[t] = 0;
+    }
     for (int i = 0; i < g_la_timer.used; ++i) {
         if (hipEventSynchronize(g_la_timer.ev[2 * i + 1]) != hipSuccess) return check_launch("hipEventSynchronize");
         float ms = 0.f;
         if (hipEventElapsedTime(&ms, g_la_timer.ev[2 * i], g_la_timer.ev[2 * i + 1]) != hipSuccess)
             return check_launch("hipEventElapsedTime");
         tot += ms;
+        g_la_timer.tag_ms[g_la_timer.tag[i]] += ms;
+        ++g_la_timer.tag_n[g_la_timer.tag[i]];
     }
     *total_ms = tot;
     *launches = g_la_timer.used;
     g_la_timer.used = 0;
+    return ULM_OK;
+}
+
+extern "C" int ulm_la_timer_product(int tag, double *total_ms, int *launches) {
+    ULM_REQUIRE(total_ms && launches, "ulm_la_timer_product: null pointer");
+    ULM_REQUIRE(tag > 0 && tag < kTimerTags, "ulm_la_timer_product: bad product tag %d", tag);
+    *total_ms = g_la_timer.tag_ms[tag];
+    *launches = g_la_timer.tag_n[tag];
     return ULM_OK;
 }

@@ -72,7 +72,7 @@
 namespace ulm {
 
 // launch timer of fm_chunk.hip
-int la_timer_begin(hipStream_t s);
+int la_timer_begin(hipStream_t s, int tag);
 int la_timer_end(hipStream_t s);
 
 namespace kgrp {
@@ -573,7 +573,7 @@ int launch(const uint16_t *a, const uint16_t *alo, const uint16_t *ua, const uin
             return check_launch("la_kgroup_kernel attribute");
         attr_done[dev] = true;
     }
-    int st = la_timer_begin(s);
+    int st = la_timer_begin(s, 0);
     if (st) return st;
     la_kgroup_kernel<MH, REV, UBSPLIT, FULL><<<dim3(static_cast<unsigned>(total)), WAVES * kWave, LDS_BYTES, s>>>(
         a, alo, ua, ualo, c, clo, P, pscaled ? 1 : 0, g, out, state, B, T, K, V, NT, nKG, bpg, nVT, static_cast<int>(total));

@@ -55,7 +55,7 @@
 
 namespace ulm {
 
-int la_timer_begin(hipStream_t s);
+int la_timer_begin(hipStream_t s, int tag);
 int la_timer_end(hipStream_t s);
 
 namespace pair {
@@ -161,6 +161,7 @@ struct Args {
     const uint16_t *cp_src;
     uint16_t *cp_q, *cp_r;
     int cp_X, cp_gx, cp_jobs;
+    int tag;                 // the launch timer's product tag (ULM_PRODUCT_*)
 };
 
 // tile job -> (m-tile, n-tile) of one batch row
@@ -1067,7 +1068,7 @@ int launch_g(Args a, int B, hipStream_t s) {
         static_assert(per_wg * kCopyLds <= lds, "tile copies fit in the stage memory");
         if (a.cp_jobs > 0) grid += (a.cp_jobs + per_wg - 1) / per_wg;
     }
-    int st = la_timer_begin(s);
+    int st = la_timer_begin(s, a.tag);
     if (st) return st;
     pair_kernel<G, G, KT, TA, TBt, EPI, OUT><<<dim3(static_cast<unsigned>(grid)), waves_of<G, EPI>() * 64, lds, s>>>(a);
     st = check_launch("pair_kernel");
@@ -1221,6 +1222,7 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, uint16_t *vQ, co
         a.cp_gx = (D + kCopyBlocks * ULM_CHUNK - 1) / (kCopyBlocks * ULM_CHUNK);
         a.cp_jobs = a.cp_gx * NT * B;
     }
+    a.tag = ULM_PRODUCT_SCORES;
     ULM_TRY((launch<false, EPI_SCORES>(a, Gs, B, s)));
     Args f{};
     f.T = T;
@@ -1236,6 +1238,7 @@ int launch_pair_forward(const uint16_t *qR, const uint16_t *kR, uint16_t *vQ, co
     f.F = D;
     f.nperm = 1;
     f.resid = resid;
+    f.tag = ULM_PRODUCT_APPLY;
     return launch<false, EPI_ROWS>(f, G, B, s);
 }
 
@@ -1261,6 +1264,7 @@ int launch_pair_state(const uint16_t *vQ, const uint16_t *kdQ, float *S, int B, 
     a.F = A;
     a.nperm = 1;
     a.mperm = 1;
+    a.tag = ULM_PRODUCT_STATE;
     return launch<false, EPI_ROWS>(a, G, B, s);
 }
 
@@ -1321,6 +1325,7 @@ int pair_backward_products(const SideStream *sd, const uint16_t *vR, const uint1
         d.out = dv;
         d.out_dt = dv_dt;
         d.F = D;
+        d.tag = ULM_PRODUCT_DV;
         ULM_TRY((launch<false, EPI_ROWS>(d, G, B, sd ? sd->s : s)));
     }
     Args a{};
@@ -1339,6 +1344,7 @@ int pair_backward_products(const SideStream *sd, const uint16_t *vR, const uint1
     a.pin = P;
     a.pin_lo = Plo;
     a.dg_part = dg_part;
+    a.tag = ULM_PRODUCT_DSCORES;
     ULM_TRY((launch<false, EPI_DSCORES>(a, G, B, s)));
     Args r{};
     r.T = T;
@@ -1368,6 +1374,7 @@ int pair_backward_products(const SideStream *sd, const uint16_t *vR, const uint1
     r.nt = (A + G - 1) / G;
     r.krange = K_CAUSAL;
     r.dg_part = st.dgq;
+    r.tag = ULM_PRODUCT_DQSTATS;
     ULM_TRY((launch<false, EPI_DQSTATS>(r, G, B, s)));
     // dk_f = dS^T q (rows s of dSt, contraction t >= the start of s's block), into dr
     // with the carry between tiles, which its epilogue forms from the tiles' S
@@ -1378,6 +1385,7 @@ int pair_backward_products(const SideStream *sd, const uint16_t *vR, const uint1
     r.out_dt = ULM_F32;
     r.drtile = 1;
     r.dg_part = st.dgk;
+    r.tag = ULM_PRODUCT_DKDR;
     ULM_TRY((launch<false, EPI_ROWS>(r, G, B, s)));
     const int jobs = B * MT * ((A + G - 1) / G);
     pair::final_kernel<<<(A + pair::kFinalSlots - 1) / pair::kFinalSlots + 1, 256, 0, s>>>(

@@ -61,16 +61,22 @@ SIGNATURES = {
     "ulm_decode_flush": (I, [P, P, P, I, P, P, P, P, P, I, I, I, P]),
     "ulm_la_timer_start": (I, [I]),
     "ulm_la_timer_stop": (I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]),
+    "ulm_la_timer_product": (I, [I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]),
 }
+
+# the launch timer's block-pair product tags (ULM_PRODUCT_* of ulm_fm.h)
+PRODUCTS = {"scores": 1, "apply": 2, "dscores": 3, "dv": 4, "dq_f": 5, "dk_f": 6, "state": 7}
 
 
 class LaTimer:
     """Context manager: HIP-event time of every chunked-kernel launch inside it.
-    After exit, ``total_ms`` and ``launches`` hold the sums."""
+    After exit, ``total_ms`` and ``launches`` hold the sums, and ``products``
+    maps each block-pair product that ran (PRODUCTS) to its (ms, launches)."""
 
     def __init__(self, max_launches=4096):
         self.max_launches = max_launches
         self.total_ms, self.launches = 0.0, 0
+        self.products = {}
 
     def __enter__(self):
         call("ulm_la_timer_start", self.max_launches)
@@ -80,6 +86,10 @@ class LaTimer:
         ms, n = ctypes.c_double(), ctypes.c_int()
         call("ulm_la_timer_stop", ctypes.byref(ms), ctypes.byref(n))
         self.total_ms, self.launches = ms.value, n.value
+        for name, tag in PRODUCTS.items():
+            call("ulm_la_timer_product", tag, ctypes.byref(ms), ctypes.byref(n))
+            if n.value:
+                self.products[name] = (ms.value, n.value)
         return False
 
 _lib = None

@@ -55,6 +55,23 @@ def test_c_side_rejects_bad_sizes_without_touching_the_gpu():
     assert st == nat.ULM_ERR_INVALID and b"LDS" in lib.ulm_last_error()
 
 
+def test_timer_product_query_checks_its_tag():
+    """ulm_la_timer_product: tags outside ULM_PRODUCT_* and null outputs are
+    rejected (no HIP call); the Python tag table equals the header's enum."""
+    lib = nat.lib()
+    ms, n = ctypes.c_double(), ctypes.c_int()
+    for tag in (0, -1, 8):
+        assert lib.ulm_la_timer_product(tag, ctypes.byref(ms), ctypes.byref(n)) == nat.ULM_ERR_INVALID
+        assert b"bad product tag" in lib.ulm_last_error()
+    assert lib.ulm_la_timer_product(1, None, ctypes.byref(n)) == nat.ULM_ERR_INVALID
+    assert lib.ulm_la_timer_product(nat.PRODUCTS["scores"], ctypes.byref(ms), ctypes.byref(n)) == nat.ULM_OK
+    assert n.value >= 0 and ms.value >= 0.0
+    enum = {k.lower(): int(v) for k, v in re.findall(r"ULM_PRODUCT_(\w+) = (\d+)", open(HEADER).read())}
+    names = {"scores": "scores", "apply": "apply", "dscores": "dscores", "dv": "dv", "dqstats": "dq_f",
+             "dkdr": "dk_f", "state": "state"}
+    assert {names[k]: v for k, v in enum.items()} == nat.PRODUCTS
+
+
 def test_nonzero_status_surfaces_as_runtime_error():
     with pytest.raises(RuntimeError, match="status 1"):
         nat.call("ulm_la", None, None, None, None, None, 1, 0, 8, 8, 0, 0, None, 0, None)

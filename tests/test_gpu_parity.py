@@ -193,6 +193,26 @@ AUTO_LONG_CASES = [
 ]
 
 
+def test_launch_timer_splits_the_block_pair_products(monkeypatch):
+    """One fwd+bwd on the block-pair form under the launch timer: each of the
+    six products is timed once under its own tag, and their times add up to
+    the total."""
+    monkeypatch.setenv("ULM_FM_PATH", "pair")
+    say("launch timer over one block-pair fwd+bwd B=2 T=256 A=256 D=128")
+    r, v, g, w = fm_inputs(2, 256, 256, 128, seed=11, device="cuda")
+    r, v, g, w = (t.requires_grad_(True) for t in (r.float(), v.to(torch.bfloat16), g.float(), w.float()))
+    q, fast = kernel.unified_memory(r, v, g, w)
+    torch.cuda.synchronize()
+    with nat.LaTimer(max_launches=64) as timer:
+        q, fast = kernel.unified_memory(r, v, g, w)
+        torch.autograd.grad((q, fast), (r, v, g, w), (0.1 * q, fast))
+        torch.cuda.synchronize()
+    assert set(timer.products) == {"scores", "apply", "dscores", "dv", "dq_f", "dk_f"}, timer.products
+    assert all(n == 1 for _, n in timer.products.values()), timer.products
+    assert timer.launches == 6
+    assert abs(sum(ms for ms, _ in timer.products.values()) - timer.total_ms) <= 1e-9 * max(timer.total_ms, 1.0)
+
+
 @pytest.mark.parametrize("B,T,A,D,code", AUTO_LONG_CASES)
 def test_unified_memory_long_sequences_pick_their_form(B, T, A, D, code):
     """Sequences past the lengths of the benchmark shapes, each on the form the

@@ -7,6 +7,8 @@ Tolerances: q and c are fp32 scans (1e-5); fast and the state S come from bf16
 MFMA products with fp32 accumulation, the training path's 1e-2 (test_all.py:166).
 Every case prints its name before touching the GPU.
 """
+import random
+
 import pytest
 import torch
 
@@ -50,6 +52,23 @@ def test_fm_prefill_matches_oracle_state(B, T, A, D, lam, vdt, path, monkeypatch
     assert S.shape == (B, D, A) and c.shape == (B, A)
     assert errs["q"] < 1e-5 and errs["c"] < 1e-5
     assert errs["fast"] < 1e-2 and errs["S"] < 1e-2
+
+
+def _random_prefill_cases(n, seed):
+    """Seeded (B, T, A, D, lam, dtype of v) draws: ragged and whole chunks,
+    widths on and off the 32 grid, lam from fast to slow decay."""
+    rng = random.Random(seed)
+    return [(rng.choice([1, 2, 3]), rng.choice([1, 5, 63, 64, 65, 129, 256, 300, 517]),
+             rng.choice([32, 64, 100, 140, 256, 320, 712, 1024]), rng.choice([16, 32, 36, 64, 96, 160, 288]),
+             rng.choice([0.5, 0.8, 0.93, 0.99, None]), rng.choice([torch.float32, torch.bfloat16]))
+            for _ in range(n)]
+
+
+@pytest.mark.parametrize("path", ["chunked", "pair"])
+@pytest.mark.parametrize("B,T,A,D,lam,vdt", _random_prefill_cases(12, 7))
+def test_fm_prefill_random_shapes(B, T, A, D, lam, vdt, path, monkeypatch):
+    """The checks of test_fm_prefill_matches_oracle_state over seeded random draws."""
+    test_fm_prefill_matches_oracle_state(B, T, A, D, lam, vdt, path, monkeypatch)
 
 
 def _oracle_states(p, tokens, n_layers):

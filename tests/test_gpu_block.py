@@ -116,6 +116,21 @@ def test_norm_conv_bwd_matches_autograd(B, T, D, Kc):
     assert max(errs2.values()) < 1e-5, errs2
 
 
+def _random_nc_cases(n, seed):
+    """Seeded (B, T, D, Kc) draws: single and ragged position tiles, widths
+    from one channel to 2100, every tap count up to the largest."""
+    rng = random.Random(seed)
+    return [(rng.choice([1, 2, 3]), rng.choice([1, 2, 5, 17, 64, 100, 257]),
+             rng.choice([1, 5, 64, 100, 288, 768, 1024, 2100]), rng.choice([1, 2, 3, 4, 8])) for _ in range(n)]
+
+
+@pytest.mark.parametrize("B,T,D,Kc", _random_nc_cases(10, 13))
+def test_norm_conv_random_shapes(B, T, D, Kc):
+    """The forward and backward checks above over seeded random draws."""
+    test_norm_conv_fwd_matches_oracle(B, T, D, Kc)
+    test_norm_conv_bwd_matches_autograd(B, T, D, Kc)
+
+
 BLOCK_CASES = [
     # B, T, D, A, autocast
     (2, 200, 64, 140, False),     # the reference test's shape (test_all.py:140-154)
@@ -377,6 +392,20 @@ def test_wgrad_matches_fp32_product(K, N1, N2):
     err = rel(c, ref)
     say(f"  rel error {err:.2e}")
     assert err < 1e-5
+
+
+def _random_wgrad_cases(n, seed):
+    """Seeded (K, N1, N2) draws: contractions from one row to ragged
+    thousands, widths multiples of 8 from 8 to 3200."""
+    rng = random.Random(seed)
+    return [(rng.choice([1, 7, 64, 100, 1000, 4096, 5000]), 8 * rng.randint(1, 400), 8 * rng.randint(1, 400))
+            for _ in range(n)]
+
+
+@pytest.mark.parametrize("K,N1,N2", _random_wgrad_cases(10, 17))
+def test_wgrad_random_shapes(K, N1, N2):
+    """The check of test_wgrad_matches_fp32_product over seeded random draws."""
+    test_wgrad_matches_fp32_product(K, N1, N2)
 
 
 @pytest.mark.parametrize("autocast", [False, True])

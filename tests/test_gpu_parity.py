@@ -315,19 +315,11 @@ def test_address_matches_oracle(pdt, log_eps):
         assert l64.grad.item() != 0.0 and rel(lg.grad, l64.grad) < 1e-5
 
 
-@pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("A", [1800, 3072, 4000, 4400, 702])
-@pytest.mark.parametrize("with_r", [True, False])
-def test_address_backward_widths(pdt, A, with_r):
-    """ulm_addr_bwd over row widths that take each of its forms: rows of up to
-    8, 12 and 16 steps of 256 slots kept in registers between its two passes
-    (1800, 3072, 4000), a row read twice (4400), and the scalar form (702, not
-    a multiple of 4); with r given, and with r formed from pre, bias and the
-    denominators as the block's backward calls it. Against the oracle's
-    address in float64."""
-    say(f"address backward A={A} {pdt} r {'given' if with_r else 'formed'}")
-    gen = torch.Generator().manual_seed(A)
-    M = 96
+def _address_case(M, A, pdt, with_r, seed):
+    """ulm_addr_fwd and ulm_addr_bwd on one (M, A) against the oracle's
+    address in float64: r and the denominators to 1e-5, and the gradients of
+    pre (1e-5 in fp32, 1e-2 for bf16 pre), of the bias and of log_eps (1e-5)."""
+    gen = torch.Generator().manual_seed(seed)
     pre = torch.randn(M, A, generator=gen).to(pdt)
     bias = torch.randn(A, generator=gen) * 0.5
     le = torch.tensor([0.3])
@@ -346,11 +338,43 @@ def test_address_backward_widths(pdt, A, with_r):
     p64 = pre.double().requires_grad_(True)
     b64 = bias.double().requires_grad_(True)
     l64 = le.double().reshape(()).requires_grad_(True)
-    (fm.address(p64 + b64, l64) * dr.double()).sum().backward()
+    rr = fm.address(p64 + b64, l64)
+    (rr * dr.double()).sum().backward()
+    assert rel(r, rr) < 1e-5
     tol = 1e-5 if pdt == torch.float32 else 1e-2
     assert rel(dpre.double().cpu(), p64.grad) < tol
     assert rel(dbias.cpu(), b64.grad) < 1e-5
     assert rel(dle.cpu().reshape(()), l64.grad) < 1e-5
+
+
+@pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("A", [1800, 3072, 4000, 4400, 702])
+@pytest.mark.parametrize("with_r", [True, False])
+def test_address_backward_widths(pdt, A, with_r):
+    """ulm_addr_bwd over row widths that take each of its forms: rows of up to
+    8, 12 and 16 steps of 256 slots kept in registers between its two passes
+    (1800, 3072, 4000), a row read twice (4400), and the scalar form (702, not
+    a multiple of 4); with r given, and with r formed from pre, bias and the
+    denominators as the block's backward calls it. Against the oracle's
+    address in float64."""
+    say(f"address backward A={A} {pdt} r {'given' if with_r else 'formed'}")
+    _address_case(96, A, pdt, with_r, A)
+
+
+def _random_address_cases(n, seed):
+    """Seeded (M, A, dtype of pre, r given) draws: one to a few hundred rows,
+    widths from 1 slot to past 4096, multiples of 4 and not."""
+    rng = random.Random(seed)
+    return [(rng.choice([1, 3, 17, 96, 257]), rng.choice([1, 3, 4, 64, 255, 256, 700, 1024, 1800, 3000, 3072, 4096,
+                                                          4100, 5000]),
+             rng.choice([torch.float32, torch.bfloat16]), rng.choice([True, False])) for _ in range(n)]
+
+
+@pytest.mark.parametrize("M,A,pdt,with_r", _random_address_cases(16, 11))
+def test_address_random_shapes(M, A, pdt, with_r):
+    """The checks of test_address_backward_widths over seeded random draws."""
+    say(f"address M={M} A={A} {pdt} r {'given' if with_r else 'formed'}")
+    _address_case(M, A, pdt, with_r, M * 10007 + A)
 
 
 def _decode_model(seed=0, **kw):

@@ -74,6 +74,26 @@ def test_la_matches_dense(B, T, K, V, reverse, lam, split):
     assert err < 1e-2
 
 
+def _random_la_cases(n, seed):
+    """Seeded (B, T, K, V, reverse, lam, split) draws over both kernels: widths
+    on and off the 32 grid, ragged and single chunks, fast and slow decay."""
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(n):
+        K = rng.choice([16, 32, 48, 64, 100, 128, 140, 256, 300, 768, 1600])
+        V = rng.choice([8, 32, 64, 70, 96, 128, 192, 256, 520])
+        split = rng.choice([False, True]) and K % 32 == 0 and V % 32 == 0
+        cases.append((rng.choice([1, 2, 3]), rng.choice([1, 33, 64, 65, 130, 200, 300, 600]), K, V,
+                      rng.choice([False, True]), rng.choice([0.5, 0.9, 0.93, 0.99]), split))
+    return cases
+
+
+@pytest.mark.parametrize("B,T,K,V,reverse,lam,split", _random_la_cases(16, 29))
+def test_la_random_shapes(B, T, K, V, reverse, lam, split):
+    """The check of test_la_matches_dense over seeded random draws."""
+    test_la_matches_dense(B, T, K, V, reverse, lam, split)
+
+
 OP_CASES = [
     # B, T, A, D, dtype of v
     (2, 200, 140, 64, torch.float32),

@@ -82,33 +82,67 @@ def _oracle_states(p, tokens, n_layers):
     return states
 
 
+def _prefill_then_step(dim, hidden, n_layers, B, T0, T, seed):
+    """UnifiedLM.prefill of T0 positions, then steps to T, against the
+    oracle's forward_recurrent (logits within 1e-2), and the states right
+    after the prompt against the oracle's (S = U - mu w, c, r_prev, the conv
+    window; 1e-2)."""
+    kw = dict(dim=dim, n_layers=n_layers, hidden_dim=hidden, vocab_size=97, max_seq_len=max(T, 64))
+    model = tiny_model(seed=seed, **kw).cuda()
+    x = torch.randint(0, 97, (B, T), generator=torch.Generator().manual_seed(seed + 2))
+    logits0, states = model.prefill(x[:, :T0].cuda())
+    cont = [model.step(x[:, t].cuda(), states) for t in range(T0, T)]
+    torch.cuda.synchronize()
+    p = oracle_params(model)
+    ref = fm.forward_recurrent(p, x)
+    assert rel(logits0, ref[:, T0 - 1]) < 1e-2
+    if cont:
+        assert rel(torch.stack(cont, 1), ref[:, T0:]) < 1e-2
+    model2 = tiny_model(seed=seed, **kw).cuda()
+    _, st = model2.prefill(x[:, :T0].cuda())
+    so = _oracle_states(p, x[:, :T0], n_layers)
+    for i, (a, o) in enumerate(zip(st, so)):
+        w = fm.prior_mass(p[f"layers.{i}.log_w"])
+        errs = {"S": rel(a["S"], o["U"] - p[f"layers.{i}.mu.weight"] * w), "c": rel(a["c"], o["c"]),
+                "r_prev": rel(a["r_prev"], o["r_prev"]), "buf": rel(a["buf"], o["buf"])}
+        if T0 == 1:
+            # one position: its key r_{-1} is zero, so the state holds nothing:
+            # S is exactly 0 (the oracle's U - mu w is float64 rounding of it)
+            assert a["S"].abs().max().item() == 0.0
+            errs["S"] = 0.0
+        say(f"  block {i} rel errors {errs}")
+        assert max(errs.values()) < 1e-2, errs
+
+
 @pytest.mark.parametrize("path", ["chunked", "pair"])
 @pytest.mark.parametrize("dim,hidden", [(32, 64), (64, 140)])
 def test_model_prefill_then_step_matches_recurrent(dim, hidden, path, monkeypatch):
     monkeypatch.setenv("ULM_FM_PATH", path)
     say(f"UnifiedLM.prefill of 50 positions, then 20 steps, vs the oracle's forward_recurrent, dim={dim} A={hidden}, "
         f"{path} form")
-    kw = dict(dim=dim, n_layers=3, hidden_dim=hidden, vocab_size=97, max_seq_len=80)
-    model = tiny_model(**kw).cuda()
-    x = torch.randint(0, 97, (3, 70), generator=torch.Generator().manual_seed(2))
-    T0 = 50
-    logits0, states = model.prefill(x[:, :T0].cuda())
-    cont = torch.stack([model.step(x[:, t].cuda(), states) for t in range(T0, 70)], 1)
-    torch.cuda.synchronize()
-    p = oracle_params(model)
-    ref = fm.forward_recurrent(p, x)
-    assert rel(logits0, ref[:, T0 - 1]) < 1e-2
-    assert rel(cont, ref[:, T0:]) < 1e-2
-    # the states right after the prompt (S = U - mu w)
-    model2 = tiny_model(**kw).cuda()
-    _, st = model2.prefill(x[:, :T0].cuda())
-    so = _oracle_states(p, x[:, :T0], kw["n_layers"])
-    for i, (a, o) in enumerate(zip(st, so)):
-        w = fm.prior_mass(p[f"layers.{i}.log_w"])
-        errs = {"S": rel(a["S"], o["U"] - p[f"layers.{i}.mu.weight"] * w), "c": rel(a["c"], o["c"]),
-                "r_prev": rel(a["r_prev"], o["r_prev"]), "buf": rel(a["buf"], o["buf"])}
-        say(f"  block {i} rel errors {errs}")
-        assert max(errs.values()) < 1e-2, errs
+    _prefill_then_step(dim, hidden, 3, 3, 50, 70, 0)
+
+
+def _random_model_cases(n, seed):
+    """Seeded (dim, hidden, n_layers, B, T0, T, form) draws: prompts of one to
+    a hundred positions, 0 to 33 steps after them (two write-backs of the
+    deferred state), slot counts that take the deferred state and one
+    (A % 4 != 0) that takes the per-position kernel."""
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(n):
+        T0 = rng.choice([1, 7, 50, 64, 100])
+        cases.append((rng.choice([16, 32, 48, 64, 96]), rng.choice([24, 64, 70, 100, 140, 256]), rng.choice([1, 2, 3]),
+                      rng.choice([1, 2, 4]), T0, T0 + rng.choice([0, 1, 17, 33]), rng.choice(["chunked", "pair"])))
+    return cases
+
+
+@pytest.mark.parametrize("dim,hidden,n_layers,B,T0,T,path", _random_model_cases(10, 23))
+def test_model_prefill_then_step_random(dim, hidden, n_layers, B, T0, T, path, monkeypatch):
+    monkeypatch.setenv("ULM_FM_PATH", path)
+    say(f"UnifiedLM.prefill of {T0} positions, then {T - T0} steps, B={B} dim={dim} A={hidden} {n_layers} blocks, "
+        f"{path} form")
+    _prefill_then_step(dim, hidden, n_layers, B, T0, T, dim * 31 + hidden + T0)
 
 
 def test_flushed_states_after_steps_match_oracle():

@@ -29,6 +29,14 @@ def test_library_exports_every_declared_symbol():
     assert lib.ulm_abi_version() == 3
 
 
+def test_integration_notes_name_every_entry_point():
+    """Every function include/ulm_fm.h declares has its row in INTEGRATION.md's
+    table of entry points."""
+    notes = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    missing = [name for name in header_functions() if f"`{name}`" not in notes]
+    assert not missing, missing
+
+
 def test_probes_live_in_the_test_library_only():
     """The layout probes (include/ulm_probe.h) are exported by the test-only
     libulm_probe.so and not by the product library."""

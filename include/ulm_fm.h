@@ -300,7 +300,7 @@ int ulm_block_params_bwd(const float *log_rate, const float *log_w, float log_w_
  * Batched recurrent decode, N sequences, one block, one position. Together
  * these replace UnifiedBlock.step (model.py:96-111) / run.c:193-265. The
  * slot contents are held as S = U - mu*w, so the stored state is exactly the
- * north-star S_t = lam S_{t-1} + v_t r_{t-1}^T and y = S q + mu (w*q).
+ * recurrence S_t = lam S_{t-1} + v_t r_{t-1}^T and y = S q + mu (w*q).
  *
  * ulm_decode_pre: h = RMSNorm(x) (model.py:31-42), u = causal depthwise conv
  *   over [conv_buf, h] (model.py:100-102), conv_buf shifted in place.

@@ -1,6 +1,6 @@
 """CPU oracle for the UnifiedLM fast-memory path (test infrastructure).
 
-This package is the checker, never the product: only ``tests/``,
+This package checks the product and is never part of it: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it. The HIP library under ``unifiedlm.c_amd/`` never calls into it.
 

@@ -1,7 +1,7 @@
 """Float64 CPU restatement of the UnifiedLM fast-memory path (ORACLE, test infrastructure).
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this
-module, as the checker. Nothing in the product imports it.
+module, to check the product against. Nothing in the product imports it.
 
 Every function works on plain tensors (or a dict of parameters named like the
 reference's ``UnifiedLM.state_dict()``), so the oracle does not depend on the

@@ -631,7 +631,7 @@ def bench_decode_runc(torch, model, c, n_pos=2048):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+        print(f"bench.py runs on one GPU: the library has no multi-GPU path (asked for --gpus {args.gpus}); "
               "the fast-memory path shards by sequence with no communication for decode and a DDP "
               "all-reduce for training, which is not built here.", file=sys.stderr)
         sys.exit(2)

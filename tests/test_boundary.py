@@ -30,8 +30,8 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_integration_notes_name_every_entry_point():
-    """Every function include/ulm_fm.h declares has its row in INTEGRATION.md's
-    table of entry points."""
+    """Every function include/ulm_fm.h declares has its row in the
+    integration notes' table of entry points."""
     notes = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     missing = [name for name in header_functions() if f"`{name}`" not in notes]
     assert not missing, missing

@@ -97,6 +97,7 @@ def parse():
     p.add_argument("--no-step", action="store_true")
     p.add_argument("--no-configs", action="store_true")
     p.add_argument("--no-chunked", action="store_true")
+    p.add_argument("--no-address", action="store_true")
     p.add_argument("--only", choices=("block", "step", "decode"),
                    help="profiling: run one leg alone (the fused block leg without its op-by-op pass, the "
                         "training step, or the decode leg without its CPU baselines) and print its record "
@@ -249,6 +250,59 @@ def pair_product_rooflines(products, B, T, A, D, traffic_file):
             row.update(hbm_MB=round(recorded[name] / 1e6, 1), GBps=round(gbps, 1),
                        frac_hbm_peak=round(gbps / PEAK_HBM_GBPS, 4))
         out[name] = row
+    return out
+
+
+def bench_address(torch, args):
+    """The relu^2 slot address (model.py:70-72; ulm_addr_fwd / ulm_addr_bwd) on
+    its own at the 110M training rows: M = B T = 16384 rows of A = 3072 slots,
+    pre in bf16 as the block's key GEMM leaves it under autocast. HIP events
+    around K launches each, on the stream they run on. Priced in the
+    algorithmic bytes per element: forward 2 (pre in) + 4 (r out), backward
+    4 (dr) + 4 (r) + 2 (pre) in and 2 (dpre) out."""
+    import kernel
+    import ulm_native as nat
+    M, A = 16 * 1024, 3072
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(9)
+    pre = torch.randn(M, A, device=dev, generator=gen).to(torch.bfloat16)
+    bias = torch.randn(A, device=dev, generator=gen) * 0.5
+    le = torch.tensor([0.3], device=dev)
+    dr = torch.randn(M, A, device=dev, generator=gen)
+    r = torch.empty(M, A, device=dev)
+    denom = torch.empty(M, device=dev)
+    dpre = torch.empty_like(pre)
+    dbias = torch.empty(A, device=dev)
+    dle = torch.empty(1, device=dev)
+    wsb = nat.lib().ulm_addr_bwd_workspace_bytes(M, A)
+    ws = torch.empty(max(wsb, 1), device=dev, dtype=torch.uint8)
+    st = nat.stream_of(pre)
+    pdt = nat.dtype_code(pre.dtype)
+
+    def fwd():
+        nat.call("ulm_addr_fwd", nat.ptr(pre), pdt, nat.ptr(bias), nat.ptr(le), nat.ptr(r), nat.ptr(denom), M, A, st)
+
+    def bwd():
+        nat.call("ulm_addr_bwd", nat.ptr(pre), pdt, nat.ptr(bias), nat.ptr(le), nat.ptr(r), nat.ptr(denom),
+                 nat.ptr(dr), nat.ptr(dpre), nat.ptr(dbias), nat.ptr(dle), nat.ptr(ws), wsb, M, A, st)
+
+    out = {"workload": f"relu^2 address of M={M} rows x A={A} slots (the 110M training rows), bf16 pre"}
+    k = max(args.steps, 20)
+    for name, fn, nbytes in (("forward", fwd, M * A * (2 + 4)), ("backward", bwd, M * A * (4 + 4 + 2 + 2))):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(k):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / k
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"avg_launch_ms": round(ms, 4), "bytes": nbytes, "GBps": round(gbps, 1),
+                     "frac_hbm_peak": round(gbps / PEAK_HBM_GBPS, 4), "launches_timed": k}
+        log(f"address {name}: {ms * 1e3:.1f} us per call, {gbps:.0f} GB/s ({gbps / PEAK_HBM_GBPS:.2f} of HBM peak)")
     return out
 
 
@@ -658,6 +712,7 @@ def main():
     train = bench_training(torch, args)
     configs = None if args.no_configs else bench_configs(torch, args)
     chunked = None if args.no_chunked else bench_chunked(torch, args)
+    address = None if args.no_address else bench_address(torch, args)
     cpu = None if args.no_cpu else bench_cpu_baseline(torch, train)
     block = None if args.no_block else bench_block(torch, args)
     train_step = None if args.no_step else bench_train_step(torch, args)
@@ -688,6 +743,7 @@ def main():
         "roofline": train["roofline"],
         "configs": configs,
         "chunked": chunked,
+        "address": address,
         "cpu_baseline": cpu,
         "block": block,
         "train_step": train_step,

@@ -98,10 +98,10 @@ def parse():
     p.add_argument("--no-configs", action="store_true")
     p.add_argument("--no-chunked", action="store_true")
     p.add_argument("--no-address", action="store_true")
-    p.add_argument("--only", choices=("block", "step", "decode"),
+    p.add_argument("--only", choices=("block", "step", "decode", "address"),
                    help="profiling: run one leg alone (the fused block leg without its op-by-op pass, the "
-                        "training step, or the decode leg without its CPU baselines) and print its record "
-                        "instead of the benchmark line")
+                        "training step, the decode leg without its CPU baselines, or the relu^2 address) and "
+                        "print its record instead of the benchmark line")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                    help="first run one plain fp32 copy kernel over MB megabytes (a known-size reference for "
                         "hardware byte counters)")
@@ -705,7 +705,8 @@ def main():
         if args.only == "decode":
             args.no_cpu = True
         legs = {"block": lambda: bench_block(torch, args, composed=False),
-                "step": lambda: bench_train_step(torch, args), "decode": lambda: bench_decode(torch, args)}
+                "step": lambda: bench_train_step(torch, args), "decode": lambda: bench_decode(torch, args),
+                "address": lambda: bench_address(torch, args)}
         rec = legs[args.only]()
         print(json.dumps({"leg": args.only, "steps": args.steps, "warmup": args.warmup, **rec}), flush=True)
         return

@@ -19,7 +19,7 @@
 
 namespace ulm {
 
-constexpr int kFwdRowsPerWave = 2;
+constexpr int kFwdRowsPerWave = 1;   // 66.7 us at the 110M rows against 74.0 (2), 77.3 (4), 97.0 (8)
 constexpr int kBwdRowsPerWave = 8;   // amortises the per-block dbias partial row
 constexpr int kAddrWaves = 4;
 constexpr int kAddrSplit = 32;       // first-level row ranges of the dbias column sum
